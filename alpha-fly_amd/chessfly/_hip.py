@@ -1,0 +1,123 @@
+"""ctypes binding of libflyeval.so, the gfx950 HIP library behind the evaluator (include/flyeval.h).
+
+Loading fails loudly: there is no CPU or PyTorch fallback for anything the library computes.  Device
+pointers are passed as integers (torch `data_ptr()`), the stream is torch's current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflyeval.so")
+
+MODE_DEVIATION_F16 = 0
+MODE_F32 = 1
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+_pp = ctypes.POINTER(ctypes.c_void_p)
+
+
+class HeadDesc(ctypes.Structure):
+    """fly_head_desc: RunningNorm statistics and the four read-out maps (device pointers)."""
+    _fields_ = [("n_out", _i64), ("n_moves", _i64), ("norm_mean", _p), ("norm_var", _p), ("norm_eps", _f32),
+                ("norm_clip", _f32), ("policy_w", _p), ("policy_b", _p), ("from_w", _p), ("from_b", _p),
+                ("to_w", _p), ("to_b", _p), ("value_w", _p), ("value_b", _p), ("move_from", _p), ("move_to", _p)]
+
+
+# name -> (restype, argtypes); every function declared in include/flyeval.h
+SIGNATURES = {
+    "fly_abi_version": (_i32, []),
+    "fly_last_error": (ctypes.c_char_p, []),
+    "fly_cone_create": (_i32, [_i64, _i64, _p, _p, _p, _i64, _p, _i64, _i32, _p, _pp]),
+    "fly_cone_destroy": (_i32, [_p]),
+    "fly_cone_sizes": (_i32, [_p, _p, _p, _p]),
+    "fly_cone_rows": (_i32, [_p, _i32, _p, _p]),
+    "fly_cone_step": (_i32, [_p, _i32, _p, _p, _p, _p, _p, _p]),
+    "fly_cone_outputs": (_i32, [_p, _p, _p]),
+    "fly_edge_weights": (_i32, [_p, _p, _p, _i64, _p, _p]),
+    "fly_plan_create": (_i32, [_p, _p, _p, _p, _p, _p, _f32, _i32, _p, _pp]),
+    "fly_plan_create_full": (_i32, [_i64, _i64, _p, _p, _p, _p, _f32, _p, _pp]),
+    "fly_plan_destroy": (_i32, [_p]),
+    "fly_plan_resting": (_i32, [_p, _p, _p]),
+    "fly_forward_io_workspace": (_sz, [_p, _i64]),
+    "fly_forward_io": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
+    "fly_forward_literal_workspace": (_sz, [_p, _i64]),
+    "fly_forward_literal": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
+    "fly_encoder": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _f32, _p, _i64, _i32, _p]),
+    "fly_head_workspace": (_sz, [ctypes.POINTER(HeadDesc), _i64]),
+    "fly_head": (_i32, [ctypes.POINTER(HeadDesc), _p, _i64, _i64, _p, _p, _p, _sz, _p]),
+    "fly_model_workspace": (_sz, [_p, ctypes.POINTER(HeadDesc), _i64]),
+    "fly_model_forward": (_i32, [_p, ctypes.POINTER(HeadDesc), _p, _i64, _i64, _i64, _p, _i64, _p, _f32, _p, _p, _p,
+                                 _sz, _p]),
+    "fly_profile_enable": (_i32, [_i32]),
+    "fly_profile_read": (_i32, [_p, _p]),
+    "fly_set_tuning": (_i32, [ctypes.c_char_p, _i64]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library, with argument types set.  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C alpha-fly_amd/csrc` "
+                               "(or __graft_entry__.build()); the evaluator has no fallback")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        if lib.fly_abi_version() != 1:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {lib.fly_abi_version()}, expected 1")
+        _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed ({status}): {load().fly_last_error().decode(errors='replace')}")
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what}: the evaluator runs on a HIP device (ROCm GPU); got a {t.device} tensor")
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Scratch bytes from torch's caching allocator (256-byte aligned by construction)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+KERNEL_CLASSES = ("state_step", "encoder", "head", "other")
+
+
+def profile_enable(on: bool) -> None:
+    check(load().fly_profile_enable(1 if on else 0), "fly_profile_enable")
+
+
+def profile_read() -> dict:
+    """{kernel class: (milliseconds, launches)} recorded since profiling was enabled."""
+    ms = (ctypes.c_double * 4)()
+    n = (ctypes.c_int64 * 4)()
+    check(load().fly_profile_read(ms, n), "fly_profile_read")
+    return {name: (float(ms[i]), int(n[i])) for i, name in enumerate(KERNEL_CLASSES)}
+
+
+def set_tuning(key: str, value: int) -> None:
+    check(load().fly_set_tuning(key.encode(), int(value)), "fly_set_tuning")

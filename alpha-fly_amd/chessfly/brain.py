@@ -1,0 +1,360 @@
+"""Connectome-constrained rate RNN, evaluated by gfx950 HIP kernels.
+
+    h[t+1] = (1 - alpha) * h[t] + alpha * clamp(W h[t] + b + u, 0, h_max)
+
+Drop-in for chessfly/brain.py of the reference: same classes, constructor arguments, parameters, buffers
+and method signatures (ConnectomeRNN.forward / forward_io / light_cone / edge_weights, LightCone and its
+attributes).  What runs underneath is libflyeval.so:
+
+* `forward` (chessfly/brain.py:211-223): the literal recurrence over the whole matrix, one fused kernel per
+  step (SpMM + bias + input + clamp + lerp), float32.
+* `forward_io` (brain.py:282-329): the light cone.  float16 input selects the deviation-from-rest path
+  (brain.py:254-280): the resting trajectory and per-row constants are float32 and built once per weight
+  version; only the position-dependent deviation is stored, in float16, and accumulated in float32.
+  float32 input selects the float32 light-cone path.  Either way one fused kernel per step.
+* `light_cone` (brain.py:126-173, 232-236): reach masks, row compaction and sub-matrix extraction on the
+  device, integer and bit-exact with the reference's definition.
+
+Inference only: with autograd enabled (training, brain.py:66-99, 289-294) the forward methods raise.  The
+tensors must live on a HIP device; nothing here falls back to the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import nn
+
+from . import _hip
+from .connectome import Connectome
+
+
+def _crow(sorted_rows: torch.Tensor, n: int) -> torch.Tensor:
+    """CSR row pointer of a row-sorted edge list (brain.py:28-31)."""
+    crow = torch.zeros(n + 1, dtype=torch.long, device=sorted_rows.device)
+    crow[1:] = torch.bincount(sorted_rows, minlength=n).cumsum(0)
+    return crow
+
+
+def _no_grad_only(what: str) -> None:
+    if torch.is_grad_enabled():
+        raise NotImplementedError(f"{what}: this evaluator is inference-only; run it under torch.no_grad() "
+                                  "(the training backward is not part of the HIP forward evaluator)")
+
+
+class _SubMatrix:
+    """Rows x columns of W as its own CSR (brain.py:102-123), read back from the device cone on first use:
+    `edges` (global edge ids in W's order), `post` / `pre` (local row / column), `crow`, `shape`."""
+
+    def __init__(self, cone: "LightCone", t: int, n_rows: int, n_cols: int, nnz: int):
+        self._cone, self._t, self._nnz = cone, t, nnz
+        self.shape = (n_rows, n_cols)
+        self._data = None
+
+    def _load(self):
+        if self._data is None:
+            dev = self._cone.device
+            crow = torch.empty(self.shape[0] + 1, dtype=torch.int32, device=dev)
+            col = torch.empty(self._nnz, dtype=torch.int32, device=dev)
+            edge = torch.empty(self._nnz, dtype=torch.int32, device=dev)
+            self._cone._step_export(self._t, crow=crow, col=col, edge=edge)
+            crow = crow.long()
+            rows = torch.repeat_interleave(torch.arange(self.shape[0], device=dev), crow[1:] - crow[:-1])
+            self._data = (edge.long(), rows, col.long(), crow)
+        return self._data
+
+    @property
+    def edges(self) -> torch.Tensor:
+        return self._load()[0]
+
+    @property
+    def post(self) -> torch.Tensor:
+        return self._load()[1]
+
+    @property
+    def pre(self) -> torch.Tensor:
+        return self._load()[2]
+
+    @property
+    def crow(self) -> torch.Tensor:
+        return self._load()[3]
+
+    def csr(self, w: torch.Tensor) -> torch.Tensor:
+        return torch.sparse_csr_tensor(self.crow, self.pre, w, self.shape, check_invariants=False)
+
+
+class LightCone:
+    """Which rows of the state each step computes (brain.py:126-173), built on the device.
+
+    V_1 = inputs and V_t = V_{t-1} plus the postsynaptic partners of V_{t-1} (within t-1 synapses of an
+    input); D_T = outputs and D_t = D_{t+1} plus the presynaptic partners of D_{t+1} (within T-t synapses of
+    an output); R_t = sorted(V_t & D_t), R_0 empty.  Attributes match the reference: steps, rows, ops,
+    keep_next, keep_prev, carried, prev_row, u_pos, u_src, out_pos, out_src, out_idx, edge_visits (int64
+    tensors on the device; `carried` is a (|R_t|, 1) bool column).  The per-step index lists are read back
+    from the device cone the first time they are used.
+    """
+
+    def __init__(self, rnn: "ConnectomeRNN", in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int):
+        _hip.require_device(rnn.pre, "LightCone")
+        lib = _hip.load()
+        self.device = rnn.pre.device
+        self.steps = int(steps)
+        self.out_idx = out_idx
+        in32 = in_idx.to(device=self.device, dtype=torch.int32).contiguous()
+        out32 = out_idx.to(device=self.device, dtype=torch.int32).contiguous()
+        handle = ctypes.c_void_p()
+        _hip.check(lib.fly_cone_create(rnn.n, rnn.n_edges, rnn.crow32.data_ptr(), rnn.pre32.data_ptr(),
+                                       in32.data_ptr(), in32.numel(), out32.data_ptr(), out32.numel(), self.steps,
+                                       _hip.stream(self.device), ctypes.byref(handle)), "fly_cone_create")
+        self._handle = handle
+        T = self.steps
+        rows = (ctypes.c_int64 * (T + 1))()
+        nnz = (ctypes.c_int64 * (T + 1))()
+        has_op = (ctypes.c_int32 * (T + 1))()
+        _hip.check(lib.fly_cone_sizes(handle, rows, nnz, has_op), "fly_cone_sizes")
+        self.row_counts = [int(r) for r in rows]
+        self.nnz = [int(x) for x in nnz]
+        self.has_op = [bool(x) for x in has_op]
+        self.edge_visits = sum(self.nnz)
+        self.n_out = int(out32.numel())
+        self._rows = None
+        self._steps_idx = None
+        self._outs = None
+        self.ops = [None] + [_SubMatrix(self, t, self.row_counts[t], self.row_counts[t - 1], self.nnz[t])
+                             if self.has_op[t] else None for t in range(1, T + 1)]
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._handle
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value:
+            try:
+                _hip.load().fly_cone_destroy(h)
+            except Exception:
+                pass
+            self._handle = None
+
+    def _step_export(self, t: int, crow=None, col=None, edge=None, prev=None, usrc=None) -> None:
+        lib = _hip.load()
+        _hip.check(lib.fly_cone_step(self._handle, t, _hip.ptr(crow), _hip.ptr(col), _hip.ptr(edge), _hip.ptr(prev),
+                                     _hip.ptr(usrc), _hip.stream(self.device)), "fly_cone_step")
+
+    @property
+    def rows(self) -> list:
+        if self._rows is None:
+            lib = _hip.load()
+            out = []
+            for t in range(self.steps + 1):
+                r = torch.empty(self.row_counts[t], dtype=torch.int32, device=self.device)
+                _hip.check(lib.fly_cone_rows(self._handle, t, r.data_ptr(), _hip.stream(self.device)), "fly_cone_rows")
+                out.append(r.long())
+            self._rows = out
+        return self._rows
+
+    def _per_step(self):
+        if self._steps_idx is None:
+            keep_next, keep_prev, carried, prev_row, u_pos, u_src = ([None] for _ in range(6))
+            for t in range(1, self.steps + 1):
+                nr = self.row_counts[t]
+                prev = torch.empty(nr, dtype=torch.int32, device=self.device)
+                usrc = torch.empty(nr, dtype=torch.int32, device=self.device)
+                self._step_export(t, prev=prev, usrc=usrc)
+                prev, usrc = prev.long(), usrc.long()
+                is_carried = prev >= 0
+                keep_next.append(torch.nonzero(is_carried).squeeze(1))
+                keep_prev.append(prev[is_carried])
+                carried.append(is_carried.unsqueeze(1))
+                prev_row.append(prev.clamp_min(0))
+                fed = usrc >= 0
+                u_pos.append(torch.nonzero(fed).squeeze(1))
+                u_src.append(usrc[fed])
+            self._steps_idx = (keep_next, keep_prev, carried, prev_row, u_pos, u_src)
+        return self._steps_idx
+
+    keep_next = property(lambda self: self._per_step()[0])
+    keep_prev = property(lambda self: self._per_step()[1])
+    carried = property(lambda self: self._per_step()[2])
+    prev_row = property(lambda self: self._per_step()[3])
+    u_pos = property(lambda self: self._per_step()[4])
+    u_src = property(lambda self: self._per_step()[5])
+
+    def _outputs(self):
+        if self._outs is None:
+            src = torch.empty(self.n_out, dtype=torch.int32, device=self.device)
+            if self.n_out:
+                _hip.check(_hip.load().fly_cone_outputs(self._handle, src.data_ptr(), _hip.stream(self.device)),
+                           "fly_cone_outputs")
+            src = src.long()
+            hit = src >= 0
+            self._outs = (torch.nonzero(hit).squeeze(1), src[hit])
+        return self._outs
+
+    out_pos = property(lambda self: self._outputs()[0])
+    out_src = property(lambda self: self._outputs()[1])
+
+
+class _Plan:
+    """Owner of a device weight-set plan (fly_plan)."""
+
+    def __init__(self, handle: ctypes.c_void_p, key):
+        self.handle, self.key = handle, key
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            try:
+                _hip.load().fly_plan_destroy(h)
+            except Exception:
+                pass
+            self.handle = None
+
+
+class ConnectomeRNN(nn.Module):
+    def __init__(self, conn: Connectome, alpha_init: float = 0.5, bias_init: float = 0.0,
+                 global_scale: float = 1.0, h_max: float | None = 10.0):
+        """global_scale multiplies the normalised connectome weights; activity is clamped to [0, h_max]
+        (brain.py:176-199).  The wiring is rebuilt from the connectome, never stored in checkpoints."""
+        super().__init__()
+        if h_max is None:
+            raise ValueError("the evaluator clamps activity to [0, h_max]; h_max=None is not supported")
+        self.n = conn.n_neurons
+        self.n_edges = conn.n_edges
+        self.h_max = float(h_max)
+        self.register_buffer("pre", conn.pre, persistent=False)      # (post, pre) order = CSR order of W
+        self.register_buffer("post", conn.post, persistent=False)
+        self.register_buffer("sign", conn.sign, persistent=False)
+        self.register_buffer("w0", conn.weight * global_scale, persistent=False)
+        self.register_buffer("crow", _crow(conn.post, self.n), persistent=False)
+        # int32 copies of the CSR structure for the device library
+        self.register_buffer("crow32", self.crow.to(torch.int32), persistent=False)
+        self.register_buffer("pre32", conn.pre.to(torch.int32), persistent=False)
+        self.log_gain = nn.Parameter(torch.zeros(conn.n_edges))
+        self.bias = nn.Parameter(torch.full((self.n,), float(bias_init)))
+        a = torch.full((self.n,), float(alpha_init))
+        self.alpha_logit = nn.Parameter(torch.log(a / (1 - a)))
+        self._cone = None
+        self._plans: dict = {}
+
+    # ---- weights -----------------------------------------------------------------------------------
+    def _param_key(self):
+        return tuple((p._version, p.data_ptr()) for p in (self.log_gain, self.bias, self.alpha_logit))
+
+    def _check_params(self, what: str) -> None:
+        for name in ("log_gain", "bias", "alpha_logit", "sign", "w0"):
+            t = getattr(self, name)
+            _hip.require_device(t, what)
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise RuntimeError(f"{what}: {name} must be a contiguous float32 tensor, got {t.dtype}")
+
+    def edge_weights(self) -> torch.Tensor:
+        """sign * w0 * exp(log_gain) per edge, in CSR order (brain.py:201-202)."""
+        self._check_params("edge_weights")
+        w = torch.empty_like(self.w0)
+        dev = self.w0.device
+        _hip.check(_hip.load().fly_edge_weights(self.sign.data_ptr(), self.w0.data_ptr(), self.log_gain.data_ptr(),
+                                                self.n_edges, w.data_ptr(), _hip.stream(dev)), "fly_edge_weights")
+        return w
+
+    def csr(self, w: torch.Tensor) -> torch.Tensor:
+        return torch.sparse_csr_tensor(self.crow, self.pre, w, (self.n, self.n), check_invariants=False)
+
+    # ---- plans (everything that depends on the weights only; rebuilt when a parameter changes) -------
+    def _plan(self, key_extra, build):
+        key = self._param_key() + (key_extra,)
+        plan = self._plans.get(key_extra)
+        if plan is None or plan.key != key:
+            self._plans.pop(key_extra, None)          # free the stale plan before building the new one
+            handle = ctypes.c_void_p()
+            with torch.no_grad():
+                build(handle)
+            plan = _Plan(handle, key)
+            self._plans[key_extra] = plan
+        return plan
+
+    def _full_plan(self) -> _Plan:
+        def build(handle):
+            w = self.edge_weights()
+            _hip.check(_hip.load().fly_plan_create_full(self.n, self.n_edges, self.crow32.data_ptr(),
+                                                        self.pre32.data_ptr(), w.data_ptr(),
+                                                        self.alpha_logit.data_ptr(), self.h_max,
+                                                        _hip.stream(w.device), ctypes.byref(handle)),
+                       "fly_plan_create_full")
+        return self._plan(("full",), build)
+
+    def _cone_plan(self, cone: LightCone, mode: int) -> _Plan:
+        def build(handle):
+            w = self.edge_weights()
+            _hip.check(_hip.load().fly_plan_create(cone.handle, self.crow32.data_ptr(), self.pre32.data_ptr(),
+                                                   w.data_ptr(), self.bias.data_ptr(), self.alpha_logit.data_ptr(),
+                                                   self.h_max, mode, _hip.stream(w.device), ctypes.byref(handle)),
+                       "fly_plan_create")
+        return self._plan(("cone", mode, id(cone)), build)
+
+    # ---- the literal recurrence ----------------------------------------------------------------------
+    def forward(self, u: torch.Tensor, steps: int) -> torch.Tensor:
+        """u: (N, B) contiguous constant external drive.  Returns the state after `steps` updates, (N, B).
+        As in the reference's inference path, u is updated in place to u + bias (brain.py:218)."""
+        assert u.is_contiguous()
+        _no_grad_only("ConnectomeRNN.forward")
+        _hip.require_device(u, "ConnectomeRNN.forward")
+        self._check_params("ConnectomeRNN.forward")
+        if u.dtype != torch.float32 or u.dim() != 2 or u.shape[0] != self.n:
+            raise RuntimeError(f"ConnectomeRNN.forward: u must be float32 ({self.n}, B), got {u.dtype} {tuple(u.shape)}")
+        lib = _hip.load()
+        plan = self._full_plan()
+        batch = u.shape[1]
+        h = torch.empty_like(u)
+        ws = _hip.workspace(lib.fly_forward_literal_workspace(plan.handle, batch), u.device)
+        _hip.check(lib.fly_forward_literal(plan.handle, u.data_ptr(), batch, self.bias.data_ptr(), batch, int(steps),
+                                           h.data_ptr(), batch, ws.data_ptr(), ws.numel(), _hip.stream(u.device)),
+                   "fly_forward_literal")
+        return h
+
+    # ---- the same function through the light cone ------------------------------------------------
+    def light_cone(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> LightCone:
+        key = (steps, in_idx.data_ptr(), out_idx.data_ptr(), str(self.pre.device))
+        if self._cone is None or self._cone[0] != key:
+            self._cone = None                         # release the old cone (and its plans) first
+            self._plans = {k: v for k, v in self._plans.items() if k[0] == "full"}
+            self._cone = (key, LightCone(self, in_idx, out_idx, steps))
+        return self._cone[1]
+
+    def forward_io(self, u_in: torch.Tensor, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> torch.Tensor:
+        """u_in: (len(in_idx), B) drive of the input neurons.  Returns the output neurons after `steps`
+        updates, (len(out_idx), B): forward(u, steps)[out_idx] with u zero outside in_idx.  float16 u_in
+        takes the deviation path and returns float32; float32 u_in takes the float32 path."""
+        _no_grad_only("ConnectomeRNN.forward_io")
+        _hip.require_device(u_in, "ConnectomeRNN.forward_io")
+        self._check_params("ConnectomeRNN.forward_io")
+        if u_in.dtype == torch.float16:
+            mode = _hip.MODE_DEVIATION_F16
+        elif u_in.dtype == torch.float32:
+            mode = _hip.MODE_F32
+        else:
+            raise RuntimeError(f"forward_io: u_in must be float16 or float32, got {u_in.dtype}")
+        if u_in.dim() != 2 or u_in.shape[0] != len(in_idx):
+            raise RuntimeError(f"forward_io: u_in must be (len(in_idx), B), got {tuple(u_in.shape)}")
+        cone = self.light_cone(in_idx, out_idx, steps)
+        plan = self._cone_plan(cone, mode)
+        batch = u_in.shape[1]
+        if u_in.stride(1) != 1 or (batch > 1 and u_in.stride(0) < batch):
+            u_in = u_in.contiguous()
+        out = torch.empty(len(out_idx), batch, dtype=torch.float32, device=u_in.device)
+        lib = _hip.load()
+        ws = _hip.workspace(lib.fly_forward_io_workspace(plan.handle, batch), u_in.device)
+        ldu = u_in.stride(0) if u_in.shape[0] > 1 else batch
+        _hip.check(lib.fly_forward_io(plan.handle, u_in.data_ptr(), ldu, batch, out.data_ptr(), batch, ws.data_ptr(),
+                                      ws.numel(), _hip.stream(u_in.device)), "fly_forward_io")
+        return out
+
+    def resting_outputs(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> torch.Tensor:
+        """c_T[out_idx]: the outputs of a network that sees no position (float32)."""
+        cone = self.light_cone(in_idx, out_idx, steps)
+        plan = self._cone_plan(cone, _hip.MODE_DEVIATION_F16)
+        out = torch.empty(len(out_idx), dtype=torch.float32, device=self.pre.device)
+        _hip.check(_hip.load().fly_plan_resting(plan.handle, out.data_ptr(), _hip.stream(out.device)),
+                   "fly_plan_resting")
+        return out

@@ -1,0 +1,188 @@
+"""Policy/value network whose only hidden computation is the fly connectome, evaluated on gfx950.
+
+    board features --linear--> sensory neurons --`steps` recurrent updates--> output neurons
+                   --RunningNorm--> move logits (+ from/to-square terms), WDL logits
+
+Drop-in for chessfly/model.py of the reference (ModelConfig, RunningNorm, FlyChessNet, Evaluator,
+load_weights): same constructor, parameters, state_dict keys and forward signature.  FlyChessNet.forward
+runs as one call into libflyeval.so (fly_model_forward): the encoder GEMM on the matrix cores, the light-cone
+recurrence (float16 deviation path when `infer_dtype` is float16, float32 otherwise), and the head GEMMs whose
+operand loader gathers the output neurons and applies the eval-mode normaliser in place.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import torch
+from torch import nn
+
+from . import _hip
+from .brain import ConnectomeRNN, _no_grad_only
+from .connectome import Connectome
+from .encoding import N_BASE, N_FEATURES, N_MOVES, move_squares
+
+READOUT_SUPERCLASSES = ("descending_neuron",)   # plus every efferent neuron (model.py:23)
+
+
+@dataclasses.dataclass
+class ModelConfig:
+    """chessfly/model.py:26-34."""
+    steps: int = 4
+    min_syn: int = 3
+    shuffled: bool = False       # control: degree-preserving rewired connectome
+    attack_planes: bool = False  # feed the attack-plane features (columns N_BASE..N_FEATURES)
+    input_gain: float = 5.0
+    weight_scale: float = 2.0
+    bias_init: float = 0.1
+
+
+class RunningNorm(nn.Module):
+    """Per-neuron standardisation with running statistics (chessfly/model.py:37-58).  In eval mode it is
+    clamp((r - mean) / sqrt(var + eps), -clip, clip); FlyChessNet.forward applies it inside the head kernel.
+    Calling the module directly keeps the reference's behaviour, statistics update in training mode included."""
+
+    def __init__(self, n: int, momentum: float = 0.05, eps: float = 1e-8, clip: float = 8.0):
+        super().__init__()
+        self.momentum, self.eps, self.clip = momentum, eps, clip
+        self.register_buffer("mean", torch.zeros(n))
+        self.register_buffer("var", torch.ones(n))
+        self.register_buffer("initialised", torch.tensor(False))
+
+    def forward(self, r: torch.Tensor) -> torch.Tensor:
+        if self.training and r.shape[0] > 1:
+            with torch.no_grad():
+                m = 1.0 if not self.initialised else self.momentum
+                self.mean.lerp_(r.mean(0), m)
+                self.var.lerp_(r.var(0), m)
+                self.initialised.fill_(True)
+        return ((r - self.mean) / (self.var + self.eps).sqrt()).clamp(-self.clip, self.clip)
+
+
+class FlyChessNet(nn.Module):
+    def __init__(self, conn: Connectome, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        # float16 selects the deviation-from-rest path (the only float16 inference the reference trusts,
+        # chessfly/model.py:65-72); float32 selects the float32 light cone.
+        self.infer_dtype = torch.float16
+        if cfg.shuffled:
+            conn = conn.shuffled()
+        self.brain = ConnectomeRNN(conn, bias_init=cfg.bias_init, global_scale=cfg.weight_scale)
+        self.register_buffer("in_idx", conn.nodes("afferent"), persistent=False)
+        out = torch.cat([conn.nodes("efferent"), conn.nodes_of_superclass(*READOUT_SUPERCLASSES)]).unique()
+        self.register_buffer("out_idx", out, persistent=False)
+        self.encoder = nn.Linear(N_FEATURES, len(self.in_idx))
+        self.norm = RunningNorm(len(out))
+        self.policy = nn.Linear(len(out), N_MOVES)
+        self.value = nn.Linear(len(out), 3)
+        self.policy_from, self.policy_to = nn.Linear(len(out), 64), nn.Linear(len(out), 64)
+        frm, to = move_squares()
+        self.register_buffer("move_from", torch.as_tensor(frm), persistent=False)
+        self.register_buffer("move_to", torch.as_tensor(to), persistent=False)
+        self.register_buffer("move_from32", torch.as_tensor(frm.astype(np.int32)), persistent=False)
+        self.register_buffer("move_to32", torch.as_tensor(to.astype(np.int32)), persistent=False)
+        for layer in (self.policy_from, self.policy_to):
+            nn.init.zeros_(layer.weight)
+            nn.init.zeros_(layer.bias)
+        nn.init.zeros_(self.policy.weight)
+        nn.init.zeros_(self.value.weight)
+
+    def _head_desc(self) -> _hip.HeadDesc:
+        tensors = (self.norm.mean, self.norm.var, self.policy.weight, self.policy.bias, self.policy_from.weight,
+                   self.policy_from.bias, self.policy_to.weight, self.policy_to.bias, self.value.weight,
+                   self.value.bias)
+        for t in tensors:
+            _hip.require_device(t, "FlyChessNet.forward")
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise RuntimeError("FlyChessNet.forward: head parameters must be contiguous float32")
+        return _hip.HeadDesc(len(self.out_idx), N_MOVES, *[t.data_ptr() for t in tensors[:2]], float(self.norm.eps),
+                             float(self.norm.clip), *[t.data_ptr() for t in tensors[2:]],
+                             self.move_from32.data_ptr(), self.move_to32.data_ptr())
+
+    def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """x: (B, >= N_BASE) -> policy logits (B, N_MOVES), WDL logits (B, 3), both float32."""
+        _no_grad_only("FlyChessNet.forward")
+        _hip.require_device(x, "FlyChessNet.forward")
+        if self.training:
+            raise NotImplementedError("FlyChessNet.forward: the evaluator runs the eval-mode normaliser; call .eval()")
+        dtype = self.infer_dtype
+        if dtype not in (torch.float16, torch.float32):
+            raise RuntimeError(f"infer_dtype must be float16 or float32, got {dtype}")
+        k = N_FEATURES if self.cfg.attack_planes else N_BASE
+        if x.dim() != 2 or x.shape[1] < k:
+            raise RuntimeError(f"FlyChessNet.forward: x must be (B, >= {k}), got {tuple(x.shape)}")
+        if x.dtype != torch.float32:
+            x = x.float()
+        if x.stride(1) != 1:
+            x = x.contiguous()
+        enc_w, enc_b = self.encoder.weight, self.encoder.bias
+        if enc_w.dtype != torch.float32 or not enc_w.is_contiguous():
+            raise RuntimeError("FlyChessNet.forward: encoder weight must be contiguous float32")
+        brain = self.brain
+        brain._check_params("FlyChessNet.forward")
+        cone = brain.light_cone(self.in_idx, self.out_idx, self.cfg.steps)
+        mode = _hip.MODE_DEVIATION_F16 if dtype == torch.float16 else _hip.MODE_F32
+        plan = brain._cone_plan(cone, mode)
+        head = self._head_desc()
+        batch = x.shape[0]
+        logits = torch.empty(batch, N_MOVES, dtype=torch.float32, device=x.device)
+        wdl = torch.empty(batch, 3, dtype=torch.float32, device=x.device)
+        lib = _hip.load()
+        ws = _hip.workspace(lib.fly_model_workspace(plan.handle, head, batch), x.device)
+        ldx = x.stride(0) if batch > 1 else x.shape[1]
+        _hip.check(lib.fly_model_forward(plan.handle, head, x.data_ptr(), ldx, batch, k, enc_w.data_ptr(),
+                                         enc_w.stride(0), enc_b.data_ptr(), float(self.cfg.input_gain),
+                                         logits.data_ptr(), wdl.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _hip.stream(x.device)), "fly_model_forward")
+        return logits, wdl
+
+    @staticmethod
+    def expected_value(wdl_logits: torch.Tensor) -> torch.Tensor:
+        """P(win) - P(loss) under the softmax of the WDL logits (model.py:107-110)."""
+        p = wdl_logits.softmax(-1)
+        return p[..., 0] - p[..., 2]
+
+
+class Evaluator:
+    """The `evaluate` callable of the search: numpy in, numpy out (chessfly/model.py:113-135).  `submit`
+    launches the evaluation and returns before the GPU finishes; `result` waits for it.  Legal-move logits
+    are gathered on the device, so only the requested entries cross back to the host."""
+
+    def __init__(self, net: FlyChessNet, device):
+        self.net, self.device = net, device
+
+    @torch.no_grad()
+    def submit(self, x, rows, cols):
+        self.net.eval()
+        logits, wdl = self.net(torch.from_numpy(x).to(self.device, non_blocking=True).float())
+        if rows is None:                      # lazy search: the whole policy vector, half precision
+            return logits.half(), self.net.expected_value(wdl.float())
+        legal = logits[torch.from_numpy(rows).to(self.device, non_blocking=True),
+                       torch.from_numpy(cols).to(self.device, non_blocking=True)]
+        return legal.float(), self.net.expected_value(wdl.float())
+
+    @staticmethod
+    def result(handle):
+        return handle[0].cpu().numpy(), handle[1].float().cpu().numpy()
+
+    def __call__(self, x, rows, cols):
+        return self.result(self.submit(x, rows, cols))
+
+
+NEW_HEADS = ("policy_from.", "policy_to.")
+
+
+def load_weights(net: FlyChessNet, state: dict) -> None:
+    """Load a state dict (chessfly/model.py:141-151): an encoder saved before the attack planes is padded
+    with zero columns, and the zero-initialised from/to heads may be missing; nothing else may be."""
+    state = dict(state)
+    w = state.get("encoder.weight")
+    if w is not None and w.shape[1] < net.encoder.weight.shape[1]:
+        pad = w.new_zeros(w.shape[0], net.encoder.weight.shape[1] - w.shape[1])
+        state["encoder.weight"] = torch.cat([w, pad], dim=1)
+    missing, unexpected = net.load_state_dict(state, strict=False)
+    bad = [k for k in missing if not k.startswith(NEW_HEADS)] + list(unexpected)
+    if bad:
+        raise RuntimeError(f"checkpoint does not match the network: {bad}")

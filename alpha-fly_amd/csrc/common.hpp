@@ -1,0 +1,165 @@
+// Shared infrastructure of the flyeval library: error capture at the C boundary, device buffers,
+// small launch helpers and the per-row constant record of the state step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "flyeval.h"
+
+namespace fly {
+
+struct Error {
+  int code;
+  std::string msg;
+};
+
+void set_error(const std::string &msg);
+
+#define FLY_HIP(call)                                                                              \
+  do {                                                                                             \
+    hipError_t e_ = (call);                                                                        \
+    if (e_ != hipSuccess)                                                                          \
+      throw ::fly::Error{FLY_ERR_HIP, std::string(#call) + ": " + hipGetErrorString(e_)};         \
+  } while (0)
+
+#define FLY_REQUIRE(cond, msg)                                                                     \
+  do {                                                                                             \
+    if (!(cond)) throw ::fly::Error{FLY_ERR_INVALID, std::string(msg)};                            \
+  } while (0)
+
+// Run `f` and turn any exception into a status code plus a thread-local message.
+template <typename F>
+int guard(F &&f) {
+  try {
+    f();
+    return FLY_OK;
+  } catch (const Error &e) {
+    set_error(e.msg);
+    return e.code;
+  } catch (const std::exception &e) {
+    set_error(e.what());
+    return FLY_ERR_INTERNAL;
+  } catch (...) {
+    set_error("unknown exception");
+    return FLY_ERR_INTERNAL;
+  }
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline void check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) throw Error{FLY_ERR_HIP, std::string(what) + " launch: " + hipGetErrorString(e)};
+}
+
+inline int current_device() {
+  int d = -1;
+  FLY_HIP(hipGetDevice(&d));
+  return d;
+}
+
+// Device allocation owned by a library object.
+template <typename T>
+struct DevArray {
+  T *p = nullptr;
+  size_t n = 0;
+  DevArray() = default;
+  explicit DevArray(size_t count) { alloc(count); }
+  DevArray(const DevArray &) = delete;
+  DevArray &operator=(const DevArray &) = delete;
+  DevArray(DevArray &&o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+  DevArray &operator=(DevArray &&o) noexcept {
+    if (this != &o) { release(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+    return *this;
+  }
+  ~DevArray() { release(); }
+  void alloc(size_t count) {
+    release();
+    n = count;
+    if (count) FLY_HIP(hipMalloc(reinterpret_cast<void **>(&p), count * sizeof(T)));
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
+inline unsigned blocks_for(int64_t work, int per_block) {
+  return static_cast<unsigned>((work + per_block - 1) / per_block);
+}
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+inline bool aligned(const void *p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+// Constants of one row of a state step (32 bytes, read once per row by a wave):
+//   x   = clamp(s + u + k, lo, hi) + e         s = row of A_t times the previous state, u = input drive
+//   p   = prev >= 0 ? state_{t-1}[prev] : pdef
+//   out = lerp(p, x, a)
+// Deviation mode: k = 0, lo = -k_t, hi = H - k_t, e = k_t - clamp(k_t, 0, H), pdef = 0.
+// Float32 mode:   k = k_t, lo = 0, hi = H, e = 0, pdef = c_{t-1}.
+struct __attribute__((aligned(16))) RowParam {
+  float k, lo, hi, e, a, pdef;
+  int32_t prev, usrc;
+};
+static_assert(sizeof(RowParam) == 32, "RowParam is 32 bytes");
+
+// Launch timing for measurement (fly_profile_enable / fly_profile_read): a scope records a HIP event on
+// the stream before and after the launches it covers, when profiling is on.
+class LaunchTimer {
+ public:
+  LaunchTimer(int kernel_class, hipStream_t st);
+  ~LaunchTimer();
+  LaunchTimer(const LaunchTimer &) = delete;
+  LaunchTimer &operator=(const LaunchTimer &) = delete;
+
+ private:
+  int cls_;
+  hipStream_t st_;
+  hipEvent_t start_ = nullptr;
+};
+
+// Tuning knobs set through fly_set_tuning.
+struct Tuning {
+  int vec = 0;    // elements per lane of the step kernel, 0 = automatic
+  int tiles = 0;  // batch tiles swept row-major, 0 = automatic
+};
+Tuning &tuning();
+
+}  // namespace fly
+
+// Opaque objects of the C ABI.
+struct fly_cone {
+  int device = -1;
+  int64_t n = 0, n_edges = 0, n_in = 0, n_out = 0;
+  int32_t steps = 0;
+  std::vector<int64_t> rows_n;  // |R_t|, t = 0..T
+  std::vector<int64_t> nnz;     // non-zeros of A_t
+  std::vector<int32_t> has_op;  // A_t exists (R_{t-1} non-empty)
+  std::vector<fly::DevArray<int32_t>> rows, rowptr, col, edge, prev, usrc;
+  fly::DevArray<int32_t> out_src;
+  fly::DevArray<int32_t> out_idx;
+};
+
+struct fly_plan {
+  int device = -1;
+  int32_t mode = FLY_MODE_F32;
+  int32_t steps = 0;
+  float h_max = 10.f;
+  bool full = false;  // literal recurrence plan (every row carried, u added to every row)
+  int64_t n = 0, n_in = 0, n_out = 0, max_rows = 0;
+  std::vector<int64_t> rows_n, nnz;
+  std::vector<fly::DevArray<int32_t>> rowptr;
+  std::vector<fly::DevArray<int2>> colval;  // {local column, float bits of the weight}
+  std::vector<fly::DevArray<fly::RowParam>> params;
+  fly::DevArray<int32_t> out_src;  // position of out_idx[j] in R_T or -1
+  fly::DevArray<float> cbase;      // value added to the carried state at the outputs
+  fly::DevArray<float> c_out;      // c_T[out_idx]
+};

@@ -1,0 +1,286 @@
+// Weight-set plan: everything forward_io needs that depends only on the weights, built once per
+// weight version on the device.
+//   resting trajectory  c_0 = 0, k_full_t = (t > 1 ? W c_{t-1} : 0) + b, c_t = lerp(c_{t-1}, clamp(k_full_t, 0, H), alpha)
+//   deviation mode      lo = -k, hi = H - k, e = k - clamp(k, 0, H), a = alpha, k = k_full_t[R_t]   (brain.py:257-270)
+//   float32 mode        k_t = k_full_t[R_t] - A_t c_{t-1}[R_{t-1}], p_default = c_{t-1}[R_t]      (brain.py:238-252, 303-304)
+//   sub-matrices        {local column, float32 weight} pairs in W's edge order
+#include "common.hpp"
+
+#include <memory>
+
+namespace fly {
+void validate_graph(int64_t n, int64_t n_edges, const int32_t *crow, const int32_t *pre, hipStream_t st);
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// torch.lerp(start, end, weight) in its CPU vector form: weight < 0.5 in magnitude interpolates from the
+// start, otherwise from the end, as one fused multiply-add.
+__device__ __forceinline__ float lerp_torch(float start, float end, float weight) {
+  const bool small = fabsf(weight) < 0.5f;
+  return fmaf(small ? weight : weight - 1.0f, end - start, small ? start : end);
+}
+
+__device__ __forceinline__ float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
+
+__global__ void k_edge_weights(const float *__restrict__ sign, const float *__restrict__ w0,
+                               const float *__restrict__ lg, int64_t n_edges, float *__restrict__ w) {
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (e < n_edges) w[e] = (sign[e] * w0[e]) * expf(lg[e]);
+}
+
+__global__ void k_sigmoid(const float *__restrict__ x, int64_t n, float *__restrict__ y) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) y[i] = 1.0f / (1.0f + expf(-x[i]));
+}
+
+// k_full[r] = (c ? sum_e w_e c[pre_e] : 0) + bias[r], edges summed in CSR order
+__global__ void k_drive(const int32_t *__restrict__ crow, const int32_t *__restrict__ pre, const float *__restrict__ w,
+                        const float *__restrict__ c, const float *__restrict__ bias, int64_t n, float *__restrict__ k_full) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  float s = 0.0f;
+  if (c) {
+    const int32_t end = crow[r + 1];
+    for (int32_t e = crow[r]; e < end; ++e) s = fmaf(w[e], c[pre[e]], s);
+  }
+  k_full[r] = s + bias[r];
+}
+
+__global__ void k_rest_update(const float *__restrict__ c, const float *__restrict__ k_full,
+                              const float *__restrict__ alpha, float h_max, int64_t n, float *__restrict__ c_next) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r < n) c_next[r] = lerp_torch(c ? c[r] : 0.0f, clampf(k_full[r], 0.0f, h_max), alpha[r]);
+}
+
+__global__ void k_params_deviation(const int32_t *__restrict__ rows, int64_t nr, const float *__restrict__ k_full,
+                                   const float *__restrict__ alpha, float h_max, const int32_t *__restrict__ prev,
+                                   const int32_t *__restrict__ usrc, RowParam *__restrict__ rp) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= nr) return;
+  const int32_t r = rows[i];
+  const float k = k_full[r];
+  RowParam p;
+  p.k = 0.0f;
+  p.lo = -k;
+  p.hi = h_max - k;
+  p.e = k - clampf(k, 0.0f, h_max);
+  p.a = alpha[r];
+  p.pdef = 0.0f;
+  p.prev = prev[i];
+  p.usrc = usrc[i];
+  rp[i] = p;
+}
+
+// k_t = k_full[R_t[i]] - sum over the kept edges of w_e c_{t-1}[pre_e]
+__global__ void k_params_f32(const int32_t *__restrict__ rows, int64_t nr, const float *__restrict__ k_full,
+                             const float *__restrict__ alpha, float h_max, const float *__restrict__ c_prev,
+                             const int32_t *__restrict__ rowptr, const int32_t *__restrict__ edge,
+                             const int32_t *__restrict__ pre, const float *__restrict__ w,
+                             const int32_t *__restrict__ prev, const int32_t *__restrict__ usrc,
+                             RowParam *__restrict__ rp) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= nr) return;
+  const int32_t r = rows[i];
+  float sub = 0.0f;
+  if (rowptr) {
+    const int32_t end = rowptr[i + 1];
+    for (int32_t q = rowptr[i]; q < end; ++q) {
+      const int32_t e = edge[q];
+      sub = fmaf(w[e], c_prev[pre[e]], sub);
+    }
+  }
+  RowParam p;
+  p.k = k_full[r] - sub;
+  p.lo = 0.0f;
+  p.hi = h_max;
+  p.e = 0.0f;
+  p.a = alpha[r];
+  p.pdef = c_prev ? c_prev[r] : 0.0f;
+  p.prev = prev[i];
+  p.usrc = usrc[i];
+  rp[i] = p;
+}
+
+__global__ void k_params_full(const float *__restrict__ alpha, float h_max, int64_t n, RowParam *__restrict__ rp) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  RowParam p;
+  p.k = 0.0f;
+  p.lo = 0.0f;
+  p.hi = h_max;
+  p.e = 0.0f;
+  p.a = alpha[r];
+  p.pdef = 0.0f;
+  p.prev = (int32_t)r;
+  p.usrc = (int32_t)r;
+  rp[r] = p;
+}
+
+__global__ void k_pack(const int32_t *__restrict__ col, const int32_t *__restrict__ edge, const float *__restrict__ w,
+                       int64_t nnz, int2 *__restrict__ cv) {
+  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q >= nnz) return;
+  const int32_t e = edge ? edge[q] : (int32_t)q;
+  cv[q] = make_int2(col[q], __float_as_int(w[e]));
+}
+
+// c_out[j] = c_T[out_idx[j]]; cbase is what the head adds to the carried state at output j: the resting
+// value in deviation mode, and in float32 mode the resting value only where the output is not carried.
+__global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *__restrict__ out_src,
+                           const float *__restrict__ c_last, int64_t n_out, int32_t mode, float *__restrict__ c_out,
+                           float *__restrict__ cbase) {
+  const int64_t j = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (j >= n_out) return;
+  const float c = c_last ? c_last[out_idx[j]] : 0.0f;
+  c_out[j] = c;
+  cbase[j] = (mode == FLY_MODE_F32 && out_src[j] >= 0) ? 0.0f : c;
+}
+
+}  // namespace
+}  // namespace fly
+
+using namespace fly;
+
+extern "C" int fly_edge_weights(const float *sign, const float *w0, const float *log_gain, int64_t n_edges, float *w,
+                                void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(n_edges >= 0, "negative n_edges");
+    if (!n_edges) return;
+    FLY_REQUIRE(sign && w0 && log_gain && w, "null argument");
+    hipLaunchKernelGGL(k_edge_weights, dim3(blocks_for(n_edges, kThreads)), dim3(kThreads), 0, as_stream(stream), sign,
+                       w0, log_gain, n_edges, w);
+    check_launch("edge weights");
+  });
+}
+
+extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const int32_t *pre, const float *w,
+                               const float *bias, const float *alpha_logit, float h_max, int32_t mode, void *stream,
+                               fly_plan **out) {
+  return guard([&] {
+    FLY_REQUIRE(out != nullptr, "out is null");
+    *out = nullptr;
+    FLY_REQUIRE(cone != nullptr, "cone is null");
+    FLY_REQUIRE(mode == FLY_MODE_DEVIATION_F16 || mode == FLY_MODE_F32, "unknown mode");
+    FLY_REQUIRE(crow && bias && alpha_logit && (cone->n_edges == 0 || (pre && w)), "null argument");
+    FLY_REQUIRE(current_device() == cone->device, "the cone lives on another device");
+    hipStream_t st = as_stream(stream);
+    const int64_t n = cone->n;
+    const int T = cone->steps;
+    const unsigned nb = blocks_for(n, kThreads);
+    validate_graph(n, cone->n_edges, crow, pre, st);
+
+    auto plan = std::make_unique<fly_plan>();
+    plan->device = cone->device;
+    plan->mode = mode;
+    plan->steps = T;
+    plan->h_max = h_max;
+    plan->n = n;
+    plan->n_in = cone->n_in;
+    plan->n_out = cone->n_out;
+    plan->rows_n = cone->rows_n;
+    plan->nnz = cone->nnz;
+    plan->max_rows = 0;
+    for (int t = 1; t <= T; ++t) plan->max_rows = std::max(plan->max_rows, cone->rows_n[t]);
+    plan->rowptr.resize(T + 1);
+    plan->colval.resize(T + 1);
+    plan->params.resize(T + 1);
+
+    DevArray<float> alpha(n), k_full(n), c_a(n), c_b(n);
+    hipLaunchKernelGGL(k_sigmoid, dim3(nb), dim3(kThreads), 0, st, alpha_logit, n, alpha.p);
+    float *c_prev = nullptr;  // c_0 = 0
+    float *c_next = c_a.p;
+    for (int t = 1; t <= T; ++t) {
+      hipLaunchKernelGGL(k_drive, dim3(nb), dim3(kThreads), 0, st, crow, pre, w, t > 1 ? c_prev : nullptr, bias, n,
+                         k_full.p);
+      const int64_t nr = cone->rows_n[t];
+      plan->params[t].alloc(nr);
+      if (cone->has_op[t]) {
+        plan->rowptr[t].alloc(nr + 1);
+        FLY_HIP(hipMemcpyAsync(plan->rowptr[t].p, cone->rowptr[t].p, sizeof(int32_t) * (nr + 1), hipMemcpyDeviceToDevice, st));
+        plan->colval[t].alloc(cone->nnz[t]);
+        if (cone->nnz[t])
+          hipLaunchKernelGGL(k_pack, dim3(blocks_for(cone->nnz[t], kThreads)), dim3(kThreads), 0, st, cone->col[t].p,
+                             cone->edge[t].p, w, cone->nnz[t], plan->colval[t].p);
+      }
+      if (nr) {
+        if (mode == FLY_MODE_DEVIATION_F16)
+          hipLaunchKernelGGL(k_params_deviation, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, cone->rows[t].p,
+                             nr, k_full.p, alpha.p, h_max, cone->prev[t].p, cone->usrc[t].p, plan->params[t].p);
+        else
+          hipLaunchKernelGGL(k_params_f32, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, cone->rows[t].p, nr,
+                             k_full.p, alpha.p, h_max, c_prev, cone->has_op[t] && c_prev ? cone->rowptr[t].p : nullptr,
+                             cone->edge[t].p, pre, w, cone->prev[t].p, cone->usrc[t].p, plan->params[t].p);
+      }
+      hipLaunchKernelGGL(k_rest_update, dim3(nb), dim3(kThreads), 0, st, c_prev, k_full.p, alpha.p, h_max, n, c_next);
+      c_prev = c_next;
+      c_next = (c_next == c_a.p) ? c_b.p : c_a.p;
+    }
+    plan->out_src.alloc(cone->n_out);
+    plan->cbase.alloc(cone->n_out);
+    plan->c_out.alloc(cone->n_out);
+    if (cone->n_out) {
+      FLY_HIP(hipMemcpyAsync(plan->out_src.p, cone->out_src.p, sizeof(int32_t) * cone->n_out, hipMemcpyDeviceToDevice, st));
+      hipLaunchKernelGGL(k_out_base, dim3(blocks_for(cone->n_out, kThreads)), dim3(kThreads), 0, st, cone->out_idx.p,
+                         cone->out_src.p, c_prev, cone->n_out, mode, plan->c_out.p, plan->cbase.p);
+    }
+    check_launch("plan");
+    FLY_HIP(hipStreamSynchronize(st));
+    *out = plan.release();
+  });
+}
+
+extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *crow, const int32_t *pre, const float *w,
+                                    const float *alpha_logit, float h_max, void *stream, fly_plan **out) {
+  return guard([&] {
+    FLY_REQUIRE(out != nullptr, "out is null");
+    *out = nullptr;
+    FLY_REQUIRE(n > 0 && n < (int64_t)INT32_MAX && n_edges >= 0 && n_edges < (int64_t)INT32_MAX, "size out of range");
+    FLY_REQUIRE(crow && alpha_logit && (n_edges == 0 || (pre && w)), "null argument");
+    hipStream_t st = as_stream(stream);
+    validate_graph(n, n_edges, crow, pre, st);
+    auto plan = std::make_unique<fly_plan>();
+    plan->device = current_device();
+    plan->mode = FLY_MODE_F32;
+    plan->full = true;
+    plan->steps = 0;
+    plan->h_max = h_max;
+    plan->n = n;
+    plan->n_in = n;
+    plan->n_out = n;
+    plan->max_rows = n;
+    plan->rows_n = {n};
+    plan->nnz = {n_edges};
+    plan->rowptr.resize(1);
+    plan->colval.resize(1);
+    plan->params.resize(1);
+    plan->rowptr[0].alloc(n + 1);
+    FLY_HIP(hipMemcpyAsync(plan->rowptr[0].p, crow, sizeof(int32_t) * (n + 1), hipMemcpyDeviceToDevice, st));
+    plan->colval[0].alloc(n_edges);
+    if (n_edges)
+      hipLaunchKernelGGL(k_pack, dim3(blocks_for(n_edges, kThreads)), dim3(kThreads), 0, st, pre, nullptr, w, n_edges,
+                         plan->colval[0].p);
+    DevArray<float> alpha(n);
+    hipLaunchKernelGGL(k_sigmoid, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, alpha_logit, n, alpha.p);
+    plan->params[0].alloc(n);
+    hipLaunchKernelGGL(k_params_full, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, alpha.p, h_max, n,
+                       plan->params[0].p);
+    check_launch("full plan");
+    FLY_HIP(hipStreamSynchronize(st));
+    *out = plan.release();
+  });
+}
+
+extern "C" int fly_plan_destroy(fly_plan *plan) {
+  return guard([&] { delete plan; });
+}
+
+extern "C" int fly_plan_resting(const fly_plan *plan, float *c_out, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(plan && c_out, "null argument");
+    FLY_REQUIRE(!plan->full, "the literal-recurrence plan has no resting outputs");
+    if (plan->n_out)
+      FLY_HIP(hipMemcpyAsync(c_out, plan->c_out.p, sizeof(float) * plan->n_out, hipMemcpyDeviceToDevice, as_stream(stream)));
+  });
+}

@@ -1,0 +1,383 @@
+// The recurrent state step, the hot kernel of the evaluator, and the forward_io / literal drivers.
+//
+// One step computes, for every row i of R_t and every board b,
+//     s   = sum_e A_t[i, e] * X_{t-1}[col_e, b]                  (float32 accumulation, CSR edge order)
+//     x   = clamp(s + U[usrc_i, b] + k_i, lo_i, hi_i) + e_i        (input drive only on input rows)
+//     p   = prev_i >= 0 ? X_{t-1}[prev_i, b] : pdef_i
+//     X_t[i, b] = lerp(p, x, a_i)
+// with the state X stored (rows, ld) batch-fastest, in __half (deviation mode) or float.  This fuses the
+// reference's SpMM, index_add_, gather and jiterator update (chessfly/brain.py:273-277, 310-313, 217-223)
+// into one pass.
+//
+// Mapping: one wave64 per (row, chunk of 64*V batch columns); each lane owns V consecutive columns and
+// reads them with one V*sizeof(S)-byte load per non-zero.  The row's {column, weight} pairs and its
+// constants are wave-uniform and come through the scalar cache.  Non-zeros are unrolled by 8 so every lane
+// keeps 8 independent gathers in flight.  Lanes past the batch re-read lane 0's address (same cache line)
+// instead of branching, and only the store is masked.  Waves are numbered (tile, row, chunk-in-tile): a
+// tile of batch columns is swept over all rows before the next, so the previous state's working set of one
+// sweep is the tile's columns only (sized to stay in the 256 MB Infinity Cache at large batches).
+#include "common.hpp"
+
+namespace fly {
+
+Tuning &tuning() {
+  static Tuning t;
+  return t;
+}
+
+namespace {
+
+__device__ __forceinline__ float lerp_torch(float start, float end, float weight) {
+  const bool small = fabsf(weight) < 0.5f;
+  return fmaf(small ? weight : weight - 1.0f, end - start, small ? start : end);
+}
+
+// V elements of S as one vector access.
+template <typename S, int V>
+struct Lanes {
+  typedef S vec __attribute__((ext_vector_type(V)));
+  static __device__ __forceinline__ void load(const S *p, float (&f)[V]) {
+    const vec v = *reinterpret_cast<const vec *>(p);
+#pragma unroll
+    for (int i = 0; i < V; ++i) f[i] = static_cast<float>(v[i]);
+  }
+  static __device__ __forceinline__ void store(S *p, const float (&f)[V]) {
+    vec v;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = static_cast<S>(f[i]);
+    *reinterpret_cast<vec *>(p) = v;
+  }
+};
+
+template <typename S>
+struct Lanes<S, 1> {
+  static __device__ __forceinline__ void load(const S *p, float (&f)[1]) { f[0] = static_cast<float>(*p); }
+  static __device__ __forceinline__ void store(S *p, const float (&f)[1]) { *p = static_cast<S>(f[0]); }
+};
+
+template <typename S>
+struct StepArgs {
+  const int32_t *rowptr;   // |R_t| + 1, or null: no matrix term
+  const int2 *colval;      // {column in X_{t-1}, float bits of the weight}
+  const RowParam *params;  // |R_t|
+  const S *xprev;          // X_{t-1} (rows, ldx), or null: previous state absent (zero, nothing carried)
+  int64_t ldx;
+  const S *u;              // input drive (n_in, ldu), or null
+  int64_t ldu;
+  S *xout;                 // X_t (|R_t|, ldo)
+  int64_t ldo;
+  int32_t nrows, batch, wpt, ntiles;
+  int32_t u_vec;           // the drive can be read with V-wide loads
+};
+
+template <typename S, int V, bool TORCH_LERP>
+__global__ __launch_bounds__(256) void k_state_step(const StepArgs<S> a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t per_tile = (uint32_t)a.nrows * (uint32_t)a.wpt;
+  const uint32_t tile = wave / per_tile;
+  if (tile >= (uint32_t)a.ntiles) return;
+  const uint32_t in_tile = wave - tile * per_tile;
+  const uint32_t row = in_tile / (uint32_t)a.wpt;
+  const uint32_t chunk = tile * (uint32_t)a.wpt + (in_tile - row * (uint32_t)a.wpt);
+  const int64_t cbeg = (int64_t)chunk * (64 * V);
+  const int64_t col = cbeg + (int64_t)lane * V;
+  const bool active = col < a.batch;
+  const int64_t lcol = active ? col : cbeg;
+
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+  if (a.xprev != nullptr && a.rowptr != nullptr) {
+    const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
+    const S *base = a.xprev + lcol;
+    int32_t e = beg;
+    for (; e + 8 <= end; e += 8) {
+      int2 cv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cv[j] = a.colval[e + j];
+      float xv[8][V];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float w = __int_as_float(cv[j].y);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(w, xv[j][i], acc[i]);
+      }
+    }
+    for (; e < end; ++e) {
+      const int2 cv = a.colval[e];
+      float xv[V];
+      Lanes<S, V>::load(base + (int64_t)cv.x * a.ldx, xv);
+      const float w = __int_as_float(cv.y);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = fmaf(w, xv[i], acc[i]);
+    }
+  }
+  if (!active) return;
+
+  const RowParam p = a.params[row];
+  float u[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) u[i] = 0.0f;
+  if (a.u != nullptr && p.usrc >= 0) {
+    const S *src = a.u + (int64_t)p.usrc * a.ldu + col;
+    if (a.u_vec) {
+      Lanes<S, V>::load(src, u);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) u[i] = (col + i < a.batch) ? static_cast<float>(src[i]) : 0.0f;
+    }
+  }
+  float pv[V];
+  if (a.xprev != nullptr && p.prev >= 0) {
+    Lanes<S, V>::load(a.xprev + (int64_t)p.prev * a.ldx + col, pv);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) pv[i] = p.pdef;
+  }
+  float out[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const float x = fminf(fmaxf((acc[i] + u[i]) + p.k, p.lo), p.hi) + p.e;
+    out[i] = TORCH_LERP ? lerp_torch(pv[i], x, p.a) : fmaf(p.a, x - pv[i], pv[i]);
+  }
+  Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out);
+}
+
+template <typename S, int V>
+void launch_v(const StepArgs<S> &a, bool torch_lerp, hipStream_t st) {
+  const int64_t waves = (int64_t)a.nrows * a.wpt * a.ntiles;
+  FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
+  const dim3 grid(blocks_for(waves, 4)), block(256);
+  LaunchTimer timer(FLY_K_STATE_STEP, st);
+  if (torch_lerp)
+    hipLaunchKernelGGL((k_state_step<S, V, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((k_state_step<S, V, false>), grid, block, 0, st, a);
+}
+
+template <typename S>
+constexpr int max_vec() { return 16 / (int)sizeof(S); }
+
+// Largest V (elements per lane) that every V-wide access of the step allows, or the tuned value.
+template <typename S>
+int pick_vec(const StepArgs<S> &a) {
+  auto ok = [&](int v) {
+    const size_t bytes = (size_t)v * sizeof(S);
+    if (a.ldo % v || !aligned(a.xout, bytes)) return false;
+    if (a.xprev && (a.ldx % v || !aligned(a.xprev, bytes))) return false;
+    return true;
+  };
+  const int want = tuning().vec;
+  if (want > 0 && want <= max_vec<S>() && (want & (want - 1)) == 0 && ok(want)) return want;
+  for (int v = max_vec<S>(); v > 1; v >>= 1)
+    if (ok(v)) return v;
+  return 1;
+}
+
+template <typename S>
+void state_step(StepArgs<S> a, bool torch_lerp, hipStream_t st) {
+  if (a.nrows == 0 || a.batch == 0) return;
+  const int v = pick_vec(a);
+  a.u_vec = (a.u != nullptr && a.ldu % v == 0 && aligned(a.u, (size_t)v * sizeof(S))) ? 1 : 0;
+  const int chunks = (int)((a.batch + 64 * v - 1) / (64 * v));
+  int tiles = tuning().tiles > 0 ? (int)tuning().tiles : chunks;
+  if (tiles > chunks || chunks % tiles) tiles = chunks;
+  a.ntiles = tiles;
+  a.wpt = chunks / tiles;
+  switch (v) {
+    case 1: launch_v<S, 1>(a, torch_lerp, st); break;
+    case 2: launch_v<S, 2>(a, torch_lerp, st); break;
+    case 4: launch_v<S, 4>(a, torch_lerp, st); break;
+    default:
+      if constexpr (sizeof(S) == 2) launch_v<S, 8>(a, torch_lerp, st);
+      break;
+  }
+  check_launch("state step");
+}
+
+// Row-looped 2-D launches: blockIdx.x covers the batch, blockIdx.y strides over the rows.
+inline dim3 rows_grid(int64_t rows, int64_t batch) {
+  return dim3(blocks_for(batch, 256), (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, 65535)));
+}
+
+template <typename S>
+__global__ void k_outputs(const S *__restrict__ state, int64_t lds, const int32_t *__restrict__ out_src,
+                          const float *__restrict__ cbase, int64_t n_out, int64_t batch, float *__restrict__ out,
+                          int64_t ldo) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  for (int64_t j = blockIdx.y; j < n_out; j += gridDim.y) {
+    const int32_t src = out_src[j];
+    const float d = (state != nullptr && src >= 0) ? static_cast<float>(state[(int64_t)src * lds + b]) : 0.0f;
+    out[j * ldo + b] = cbase[j] + d;
+  }
+}
+
+__global__ void k_add_bias(float *__restrict__ u, int64_t ldu, const float *__restrict__ bias, int64_t n, int64_t batch) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) u[r * ldu + b] += bias[r];
+}
+
+__global__ void k_zero_rows(float *__restrict__ h, int64_t ld, int64_t n, int64_t batch) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) h[r * ld + b] = 0.0f;
+}
+
+}  // namespace
+
+int64_t state_ld(int64_t batch) { return round_up(batch, 64); }
+
+size_t io_workspace(const fly_plan &plan, int64_t batch) {
+  const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? 2 : 4;
+  return 2 * (size_t)plan.max_rows * (size_t)state_ld(batch) * es + 256;
+}
+
+// Runs steps 1..T of a light-cone plan.  Returns the final state (null if R_T is empty) in one of the two
+// workspace buffers, whose row stride is state_ld(batch).
+template <typename S>
+const S *run_cone_steps(const fly_plan &plan, const S *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st) {
+  const int64_t lds = state_ld(batch);
+  S *buf[2] = {reinterpret_cast<S *>(ws), reinterpret_cast<S *>(ws) + (size_t)plan.max_rows * lds};
+  const S *prev = nullptr;
+  int cur = 0;
+  const bool torch_lerp = plan.mode == FLY_MODE_F32;
+  for (int t = 1; t <= plan.steps; ++t) {
+    const int64_t nr = plan.rows_n[t];
+    if (nr == 0) {
+      prev = nullptr;
+      continue;
+    }
+    StepArgs<S> a{};
+    a.rowptr = plan.rowptr[t].p;  // null where A_t does not exist
+    a.colval = plan.colval[t].p;
+    a.params = plan.params[t].p;
+    a.xprev = prev;
+    a.ldx = lds;
+    a.u = u;
+    a.ldu = ldu;
+    a.xout = buf[cur];
+    a.ldo = lds;
+    a.nrows = (int32_t)nr;
+    a.batch = (int32_t)batch;
+    state_step(a, torch_lerp, st);
+    prev = buf[cur];
+    cur ^= 1;
+  }
+  return prev;
+}
+
+template <typename S>
+void write_outputs(const fly_plan &plan, const S *state, int64_t batch, float *out, int64_t ldo, hipStream_t st) {
+  if (!plan.n_out || !batch) return;
+  LaunchTimer timer(FLY_K_OTHER, st);
+  hipLaunchKernelGGL(k_outputs<S>, rows_grid(plan.n_out, batch), dim3(256), 0, st, state, state_ld(batch), plan.out_src.p, plan.cbase.p,
+                     plan.n_out, batch, out, ldo);
+  check_launch("outputs");
+}
+
+template const _Float16 *run_cone_steps<_Float16>(const fly_plan &, const _Float16 *, int64_t, int64_t, void *, hipStream_t);
+template const float *run_cone_steps<float>(const fly_plan &, const float *, int64_t, int64_t, void *, hipStream_t);
+
+void check_plan_device(const fly_plan *plan) {
+  FLY_REQUIRE(plan != nullptr, "plan is null");
+  FLY_REQUIRE(current_device() == plan->device, "the plan lives on another device");
+}
+
+}  // namespace fly
+
+using namespace fly;
+
+extern "C" size_t fly_forward_io_workspace(const fly_plan *plan, int64_t batch) {
+  return plan ? io_workspace(*plan, batch) : 0;
+}
+
+extern "C" int fly_forward_io(const fly_plan *plan, const void *u_in, int64_t ldu, int64_t batch, float *out,
+                              int64_t ldo, void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] {
+    check_plan_device(plan);
+    FLY_REQUIRE(!plan->full, "forward_io needs a light-cone plan");
+    FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+    if (batch == 0) return;
+    FLY_REQUIRE(out && ldo >= batch, "bad output");
+    FLY_REQUIRE(plan->n_in == 0 || (u_in && ldu >= batch), "bad input drive");
+    FLY_REQUIRE(ws && ws_bytes >= io_workspace(*plan, batch), "workspace too small");
+    FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
+    hipStream_t st = as_stream(stream);
+    if (plan->mode == FLY_MODE_DEVIATION_F16) {
+      const _Float16 *fin = run_cone_steps<_Float16>(*plan, static_cast<const _Float16 *>(u_in), ldu, batch, ws, st);
+      write_outputs<_Float16>(*plan, fin, batch, out, ldo, st);
+    } else {
+      const float *fin = run_cone_steps<float>(*plan, static_cast<const float *>(u_in), ldu, batch, ws, st);
+      write_outputs<float>(*plan, fin, batch, out, ldo, st);
+    }
+  });
+}
+
+extern "C" size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch) {
+  return plan ? 2 * (size_t)plan->n * (size_t)state_ld(batch) * sizeof(float) + 256 : 0;
+}
+
+extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, const float *bias, int64_t batch,
+                                   int32_t steps, float *h, int64_t ldh, void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] {
+    check_plan_device(plan);
+    FLY_REQUIRE(plan->full, "the literal recurrence needs a plan from fly_plan_create_full");
+    FLY_REQUIRE(steps >= 0, "negative steps");
+    FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+    if (batch == 0) return;
+    FLY_REQUIRE(u && bias && h && ldu >= batch && ldh >= batch, "bad argument");
+    const int64_t n = plan->n;
+    hipStream_t st = as_stream(stream);
+    {
+      LaunchTimer timer(FLY_K_OTHER, st);
+      hipLaunchKernelGGL(k_add_bias, rows_grid(n, batch), dim3(256), 0, st, u, ldu, bias, n, batch);
+    }
+    check_launch("bias add");
+    if (steps == 0) {
+      LaunchTimer timer(FLY_K_OTHER, st);
+      hipLaunchKernelGGL(k_zero_rows, rows_grid(n, batch), dim3(256), 0, st, h, ldh, n, batch);
+      check_launch("zero state");
+      return;
+    }
+    FLY_REQUIRE(ws && ws_bytes >= fly_forward_literal_workspace(plan, batch), "workspace too small");
+    FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
+    const int64_t lds = state_ld(batch);
+    float *buf[2] = {static_cast<float *>(ws), static_cast<float *>(ws) + (size_t)n * lds};
+    const float *prev = nullptr;
+    int cur = 0;
+    for (int t = 1; t <= steps; ++t) {
+      const bool last = t == steps;
+      StepArgs<float> a{};
+      a.rowptr = plan->rowptr[0].p;
+      a.colval = plan->colval[0].p;
+      a.params = plan->params[0].p;
+      a.xprev = prev;
+      a.ldx = lds;
+      a.u = u;
+      a.ldu = ldu;
+      a.xout = last ? h : buf[cur];
+      a.ldo = last ? ldh : lds;
+      a.nrows = (int32_t)n;
+      a.batch = (int32_t)batch;
+      state_step(a, true, st);
+      prev = buf[cur];
+      cur ^= 1;
+    }
+  });
+}
+
+extern "C" int fly_set_tuning(const char *key, int64_t value) {
+  return guard([&] {
+    FLY_REQUIRE(key != nullptr, "key is null");
+    const std::string k(key);
+    if (k == "vec") tuning().vec = (int)value;
+    else if (k == "tiles") tuning().tiles = (int)value;
+    else FLY_REQUIRE(false, "unknown tuning key " + k);
+  });
+}

@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Board-evals/s of the connectome network's forward evaluator on one MI355X.
+
+Workload (default): the full-scale synthetic connectome (166,700 neurons, ~10.5M synapses), B = 1120 boards
+(one leaf per concurrent self-play game), 6 recurrent steps through the light cone, float16 deviation from
+the float32 resting trajectory, with the 838 -> 17,937 encoder and the 2,333 -> 4,168 policy / 3 WDL heads:
+FlyChessNet.forward exactly as the search's Evaluator calls it, with the boards already on the device.
+
+One "step" of this benchmark is one forward of the whole batch.  Prints one JSON line on stdout:
+value = B * steps / wall time; `roofline` rates the fused state-step kernel by its compulsory HBM bytes
+(CSR columns and values, per-row constants, previous/new state and input rows, read or written once) over
+its launch time measured with HIP events on its stream; `cpu_baseline` times the reference's CPU path
+(restated in oracle/, the float32 light cone with cached constants) on a bounded sample of the same boards.
+
+    python bench.py [--steps K] [--warmup W] [--batch B] [--dtype f16|f32] [--graph synthetic|shuffled]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for p in (REPO, os.path.join(REPO, "alpha-fly_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "board evals/sec, 6-step forward at B=1120; SpMM HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(cone, batch: int, state_bytes: int) -> list[int]:
+    """Compulsory bytes of each state-step launch t = 1..T: the CSR column (4 B) and value of every
+    non-zero, the row pointer (4 B) and per-row constants (5 values) of every row, and the previous state,
+    the new state and the input rows, each read or written once."""
+    out = []
+    for t in range(1, cone.steps + 1):
+        nnz, rows, prev = cone.nnz[t], cone.row_counts[t], cone.row_counts[t - 1]
+        fed = len(cone.u_pos[t])
+        out.append(nnz * (4 + state_bytes) + (rows + 1) * 4 + rows * 5 * state_bytes
+                   + batch * state_bytes * (prev + rows + fed))
+    return out
+
+
+def cpu_baseline(net, conn, x_cpu, threads: int, seconds: float = 12.0):
+    """The reference's CPU forward (float32 light cone, constants cached per weight version, as
+    chessfly/brain.py:295-306 does) on the host cores; returns (evals/s, per-forward seconds, logits, wdl)."""
+    import warnings
+
+    import numpy as np
+    import torch
+
+    warnings.filterwarnings("ignore", message="Sparse CSR tensor support is in beta")
+    from chessfly.encoding import N_BASE, move_squares
+    from chessfly.synthetic import synthetic_maps, synthetic_params
+    from oracle import forward as F
+    from oracle.lightcone import light_cone
+
+    torch.set_num_threads(threads)
+    p = synthetic_params(conn, seed=0)
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.float32))
+    w0 = F.normalised_weight(conn.n_neurons, conn.post, conn.syn_count) * p.global_scale
+    ba = F.BrainArrays(conn.n_neurons, conn.pre, conn.post, conn.sign, w0, t(p.log_gain), t(p.bias), t(p.alpha_logit))
+    in_idx, out_idx = conn.nodes("afferent").numpy(), conn.nodes("efferent").numpy()
+    maps = synthetic_maps(len(in_idx), len(out_idx), 0)
+    frm, to = move_squares()
+    hp = F.HeadArrays(t(maps.encoder_w), t(maps.encoder_b), 5.0, N_BASE, t(maps.policy_w), t(maps.policy_b),
+                      t(maps.from_w), t(maps.from_b), t(maps.to_w), t(maps.to_b), t(maps.value_w), t(maps.value_b),
+                      torch.as_tensor(frm), torch.as_tensor(to), torch.zeros(len(out_idx)), torch.ones(len(out_idx)))
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), in_idx, out_idx, net.cfg.steps)
+    prep = F.prepare_f32(ba, cone)
+    x = torch.as_tensor(x_cpu)
+    logits, wdl = F.model_forward(ba, hp, cone, x, "f32", prep=prep)          # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < seconds and len(times) < 20):
+        t0 = time.perf_counter()
+        logits, wdl = F.model_forward(ba, hp, cone, x, "f32", prep=prep)
+        times.append(time.perf_counter() - t0)
+    per = statistics.median(times)
+    return x.shape[0] / per, per, logits, wdl, len(times)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30, help="timed forwards")
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=1120)
+    ap.add_argument("--recurrent-steps", type=int, default=6)
+    ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
+    ap.add_argument("--graph", choices=["synthetic", "shuffled"], default="synthetic")
+    ap.add_argument("--ones", default="40", help="ones per board: N or LO-HI")
+    ap.add_argument("--cpu-boards", type=int, default=256, help="boards in the CPU baseline sample (0: skip)")
+    ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        msg = (f"bench.py measures one GPU: the evaluator shards by board across GPUs with no collective on the "
+               f"critical path, and this build runs on a single MI355X only (asked for --gpus {args.gpus}, "
+               f"WORLD_SIZE {world})")
+        print(msg, file=sys.stderr)
+        print(msg)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from chessfly import _hip
+    from chessfly.synthetic import synthetic_boards, synthetic_net
+
+    dev = torch.device("cuda:0")
+    for kv in args.tune:
+        k, v = kv.split("=")
+        _hip.set_tuning(k, int(v))
+    t0 = time.perf_counter()
+    net, conn = synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev)
+    net.infer_dtype = torch.float16 if args.dtype == "f16" else torch.float32
+    ones = tuple(int(v) for v in args.ones.split("-")) if "-" in args.ones else int(args.ones)
+    x_np = synthetic_boards(args.batch, seed=1, ones=ones)
+    x = torch.as_tensor(x_np, device=dev)
+    torch.cuda.synchronize()
+    log(f"graph {conn.n_neurons:,} neurons, {conn.n_edges:,} edges; net on {dev} in {time.perf_counter() - t0:.1f}s")
+
+    brain = net.brain
+    t0 = time.perf_counter()
+    cone = brain.light_cone(net.in_idx, net.out_idx, args.recurrent_steps)
+    torch.cuda.synchronize()
+    t_cone = time.perf_counter() - t0
+    mode = _hip.MODE_DEVIATION_F16 if args.dtype == "f16" else _hip.MODE_F32
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        brain._cone_plan(cone, mode)
+    torch.cuda.synchronize()
+    t_plan = time.perf_counter() - t0
+    log(f"light cone {t_cone * 1e3:.1f} ms, weight-set plan {t_plan * 1e3:.1f} ms; rows {cone.row_counts}, "
+        f"nnz {cone.nnz} ({cone.edge_visits:,} visits)")
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            net(x)
+        torch.cuda.synchronize()
+        _hip.profile_enable(True)
+        stream = torch.cuda.current_stream(dev)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(args.steps):
+            logits, wdl = net(x)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - w0
+        prof = _hip.profile_read()
+        _hip.profile_enable(False)
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = wall / args.steps * 1e3
+    value = args.batch * args.steps / wall
+    log(f"{args.steps} forwards: wall {wall * 1e3:.1f} ms, events {gpu_ms:.1f} ms -> {value:,.0f} evals/s; "
+        f"kernel classes {prof}")
+
+    state_bytes = 2 if args.dtype == "f16" else 4
+    per_launch = algorithmic_bytes(cone, args.batch, state_bytes)
+    step_ms, step_launches = prof["state_step"]
+    launches_per_fwd = sum(1 for t in range(1, cone.steps + 1) if cone.row_counts[t] > 0)
+    avg_launch_ms = step_ms / max(step_launches, 1)
+    avg_bytes = sum(per_launch) / max(launches_per_fwd, 1)
+    achieved = avg_bytes / (avg_launch_ms * 1e-3) / 1e9
+    gather = sum(cone.nnz) * args.batch * state_bytes
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_state_step (fused CSR SpMM + input + clamp + leaky update)",
+                "algorithmic_bytes_per_launch": int(avg_bytes), "launches_per_forward": launches_per_fwd,
+                "avg_launch_ms": round(avg_launch_ms, 4),
+                "gather_bytes_per_forward": int(gather),
+                "gather_GBps": round(gather / (step_ms / max(step_launches, 1) * launches_per_fwd * 1e-3) / 1e9, 1)}
+    shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
+
+    cpu = None
+    parity = None
+    if args.cpu_boards > 0:
+        nb = min(args.cpu_boards, args.batch)
+        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+        log(f"CPU baseline: {nb} boards on {threads} threads ...")
+        rate, per, ref_logits, ref_wdl, reps = cpu_baseline(net, conn, x_np[:nb], threads)
+        cpu = {"value": round(rate, 1), "unit": "board-evals/s", "cores": threads, "kind": "port",
+               "sample": f"{nb} of the {args.batch} boards, full graph, float32 light cone with cached constants "
+                         f"(reference CPU path, chessfly/brain.py:295-329), median of {reps} forwards "
+                         f"({per:.2f} s each)"}
+        dl = float((logits[:nb].float().cpu() - ref_logits).abs().max())
+        dw = float((wdl[:nb].float().cpu() - ref_wdl).abs().max())
+        agree = float((logits[:nb].argmax(1).cpu() == ref_logits.argmax(1)).float().mean())
+        parity = {"boards": nb, "max_abs_logit": dl, "max_abs_wdl": dw, "argmax_agreement": agree,
+                  "reference": "oracle float32 path"}
+        log(f"CPU {rate:,.1f} evals/s; parity on {nb} boards: logits {dl:.2e}, wdl {dw:.2e}, argmax {agree:.4f}")
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "board-evals/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": (f"FlyChessNet.forward, {args.graph} connectome {conn.n_neurons} neurons / "
+                                f"{conn.n_edges} synapses, B={args.batch}, {args.recurrent_steps} steps, light cone, "
+                                + ("fp16 deviation state, fp32 math" if args.dtype == "f16" else "fp32 state")),
+                   "batch": args.batch, "recurrent_steps": args.recurrent_steps, "graph": args.graph,
+                   "state": "fp16 deviation from fp32 resting trajectory" if args.dtype == "f16" else "fp32",
+                   "edge_visits": cone.edge_visits, "rows": cone.row_counts[1:], "ones_per_board": args.ones},
+        "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
+        "kernel_ms_per_forward": shares, "gpu_event_ms_per_step": round(gpu_ms / args.steps, 4),
+        "one_off_ms": {"light_cone": round(t_cone * 1e3, 1), "plan": round(t_plan * 1e3, 1)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,175 @@
+/*
+ * flyeval.h - C ABI of the MI355X (gfx950) forward evaluator of the connectome chess network.
+ *
+ * Every entry point returns an int status (FLY_OK = 0) and never throws; on failure
+ * fly_last_error() returns a message for the calling thread.  Pointers named *_dev are device
+ * pointers owned by the caller (torch tensors on the Python side); the library never frees them.
+ * The library owns only what its create functions return (cones and plans) and frees it in the
+ * matching destroy.  `stream` is a hipStream_t passed as void* (torch's current stream); every
+ * launch goes on it.  Only the create functions synchronise (they read sizes back to the host);
+ * the forward entry points are asynchronous.  Index arrays are int32, the graph is CSR of
+ * W[post, pre] (row = postsynaptic neuron).  Objects are not thread-safe.
+ *
+ * Reference interfaces replaced (paths relative to the alpha-fly repository):
+ *   fly_cone_*            chessfly/brain.py:126-173 LightCone, :102-123 _SubMatrix, :232-236 light_cone
+ *   fly_edge_weights      chessfly/brain.py:201-202 ConnectomeRNN.edge_weights
+ *   fly_plan_create       chessfly/brain.py:257-270 (_forward_io_half cache) and :295-306 (float32 cache),
+ *                         :238-252 _constants
+ *   fly_plan_create_full  chessfly/brain.py:215-216 (per-call weights of the literal recurrence)
+ *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280)
+ *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch)
+ *   fly_encoder           chessfly/model.py:99-102 (encoder linear map, input gain, cast, transpose)
+ *   fly_head              chessfly/model.py:103-105 and :51-58 (RunningNorm eval, policy/from/to/value)
+ *   fly_model_forward     chessfly/model.py:95-105 FlyChessNet.forward (no-grad, device inputs)
+ */
+#ifndef FLYEVAL_H
+#define FLYEVAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLY_ABI_VERSION 1
+
+enum fly_status {
+    FLY_OK = 0,
+    FLY_ERR_INVALID = 1,   /* bad argument: null pointer, size, alignment, index out of range */
+    FLY_ERR_HIP = 2,       /* a HIP runtime call failed */
+    FLY_ERR_INTERNAL = 3
+};
+
+/* State arithmetic of a plan. */
+enum fly_mode {
+    FLY_MODE_DEVIATION_F16 = 0,  /* fp16 deviation from the float32 resting trajectory (brain.py:254-280) */
+    FLY_MODE_F32 = 1             /* float32 light-cone state (brain.py:295-329) */
+};
+
+typedef struct fly_cone fly_cone;
+typedef struct fly_plan fly_plan;
+
+int fly_abi_version(void);
+const char *fly_last_error(void);
+
+/* ---- light cone (integer, bit-exact with chessfly/brain.py:126-173) ------------------------------
+ * crow_dev (n+1), pre_dev (n_edges): CSR of W; in_idx_dev (n_in), out_idx_dev (n_out): neuron ids.
+ * Validates every index on the device first (FLY_ERR_INVALID if any is out of range). */
+int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow_dev, const int32_t *pre_dev,
+                    const int32_t *in_idx_dev, int64_t n_in, const int32_t *out_idx_dev, int64_t n_out,
+                    int32_t steps, void *stream, fly_cone **out);
+int fly_cone_destroy(fly_cone *cone);
+/* rows[t] = |R_t| for t = 0..steps; nnz[t] = non-zeros of A_t (0 where A_t is None); has_op[t] = 1 where
+ * A_t exists (R_{t-1} non-empty).  Arrays have steps+1 entries; any may be NULL. */
+int fly_cone_sizes(const fly_cone *cone, int64_t *rows, int64_t *nnz, int32_t *has_op);
+/* R_t, sorted neuron ids (|R_t| entries). */
+int fly_cone_rows(const fly_cone *cone, int32_t t, int32_t *rows_dev, void *stream);
+/* Step t >= 1: crow (|R_t|+1), local column (nnz_t), global edge id (nnz_t) of A_t (NULL skips an array;
+ * all three are skipped when A_t is None), prev (|R_t|: position in R_{t-1}, -1 if not carried) and usrc
+ * (|R_t|: position in in_idx, -1 if the row is not an input). */
+int fly_cone_step(const fly_cone *cone, int32_t t, int32_t *crow_dev, int32_t *col_dev, int32_t *edge_dev,
+                  int32_t *prev_dev, int32_t *usrc_dev, void *stream);
+/* out_src (n_out): position of out_idx[j] in R_T, -1 if absent. */
+int fly_cone_outputs(const fly_cone *cone, int32_t *out_src_dev, void *stream);
+
+/* ---- weights ----------------------------------------------------------------------------------- */
+/* w = sign * w0 * exp(log_gain), n_edges entries. */
+int fly_edge_weights(const float *sign_dev, const float *w0_dev, const float *log_gain_dev, int64_t n_edges,
+                     float *w_dev, void *stream);
+
+/* Weight-set plan for forward_io: per-step sub-matrices with float32 values, per-row constants and the
+ * resting trajectory, from the cone and the graph (crow/pre as given to fly_cone_create), edge weights w
+ * (n_edges), bias and alpha_logit (n).  The plan is self-contained: the inputs may be freed afterwards. */
+int fly_plan_create(const fly_cone *cone, const int32_t *crow_dev, const int32_t *pre_dev, const float *w_dev,
+                    const float *bias_dev, const float *alpha_logit_dev, float h_max, int32_t mode,
+                    void *stream, fly_plan **out);
+/* Plan for the literal recurrence over the whole matrix (mode FLY_MODE_F32, every row carried). */
+int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *crow_dev, const int32_t *pre_dev,
+                         const float *w_dev, const float *alpha_logit_dev, float h_max, void *stream,
+                         fly_plan **out);
+int fly_plan_destroy(fly_plan *plan);
+/* c_T[out_idx] (n_out floats): the outputs of a network that sees no position. */
+int fly_plan_resting(const fly_plan *plan, float *c_out_dev, void *stream);
+
+/* ---- forward ----------------------------------------------------------------------------------- */
+/* Bytes of scratch the forward entry points need for `batch` columns (pass at least this many). */
+size_t fly_forward_io_workspace(const fly_plan *plan, int64_t batch);
+/* u_in (n_in, ldu): __half for FLY_MODE_DEVIATION_F16, float for FLY_MODE_F32.
+ * out (n_out, ldo) float32 = forward_io(u_in)[out rows]. */
+int fly_forward_io(const fly_plan *plan, const void *u_in_dev, int64_t ldu, int64_t batch, float *out_dev,
+                   int64_t ldo, void *workspace_dev, size_t workspace_bytes, void *stream);
+/* Literal recurrence (plan from fly_plan_create_full): u (n, ldu) float32 is updated in place to u + bias
+ * (as the reference's no-grad path does), then h_steps (n, ldh) = steps updates from h = 0. */
+size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch);
+int fly_forward_literal(const fly_plan *plan, float *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
+                        int32_t steps, float *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
+                        void *stream);
+
+/* ---- dense maps -------------------------------------------------------------------------------- */
+/* u (n_in, ldu) = cast((x[:, :k] W[:, :k]^T + b) * gain): x (batch, ldx) float32, W (n_in, ldw) float32.
+ * out_f16 != 0 stores __half, else float. */
+int fly_encoder(const float *x_dev, int64_t ldx, int64_t batch, int64_t k, const float *w_dev, int64_t ldw,
+                const float *b_dev, int64_t n_in, float gain, void *u_dev, int64_t ldu, int32_t out_f16,
+                void *stream);
+
+/* Weights of the read-out: RunningNorm statistics and the four linear maps over the n_out outputs. */
+typedef struct fly_head_desc {
+    int64_t n_out;              /* 2,333 */
+    int64_t n_moves;            /* 4,168 */
+    const float *norm_mean;     /* (n_out) */
+    const float *norm_var;      /* (n_out) */
+    float norm_eps;
+    float norm_clip;
+    const float *policy_w;      /* (n_moves, n_out) row-major */
+    const float *policy_b;      /* (n_moves) */
+    const float *from_w;        /* (64, n_out) */
+    const float *from_b;
+    const float *to_w;          /* (64, n_out) */
+    const float *to_b;
+    const float *value_w;       /* (3, n_out) */
+    const float *value_b;
+    const int32_t *move_from;   /* (n_moves) squares 0..63 */
+    const int32_t *move_to;
+} fly_head_desc;
+
+/* logits (batch, n_moves) and wdl (batch, 3), float32 row-major, from the output activity
+ * r (n_out, ldr) float32 (column b = board b). */
+size_t fly_head_workspace(const fly_head_desc *head, int64_t batch);
+int fly_head(const fly_head_desc *head, const float *r_dev, int64_t ldr, int64_t batch, float *logits_dev,
+             float *wdl_dev, void *workspace_dev, size_t workspace_bytes, void *stream);
+
+/* FlyChessNet.forward: x (batch, ldx) float32 -> logits (batch, n_moves), wdl (batch, 3).  The encoder is
+ * (n_in, ldw) over the first k feature columns; the plan's mode selects the state arithmetic. */
+size_t fly_model_workspace(const fly_plan *plan, const fly_head_desc *head, int64_t batch);
+int fly_model_forward(const fly_plan *plan, const fly_head_desc *head, const float *x_dev, int64_t ldx,
+                      int64_t batch, int64_t k, const float *enc_w_dev, int64_t ldw, const float *enc_b_dev,
+                      float input_gain, float *logits_dev, float *wdl_dev, void *workspace_dev,
+                      size_t workspace_bytes, void *stream);
+
+/* ---- measurement ------------------------------------------------------------------------------- */
+/* Kernel classes timed by the profiler. */
+enum fly_kernel_class {
+    FLY_K_STATE_STEP = 0,   /* the fused SpMM + update step */
+    FLY_K_ENCODER = 1,      /* encoder GEMM */
+    FLY_K_HEAD = 2,         /* head GEMMs and logit assembly */
+    FLY_K_OTHER = 3,        /* output gather, bias add, zero fill */
+    FLY_K_CLASSES = 4
+};
+/* While enabled, every launch of the forward entry points is bracketed by HIP events on its stream (no
+ * synchronisation is added).  Enabling (on = 1) clears the counters; on = 0 stops recording. */
+int fly_profile_enable(int32_t on);
+/* Waits for the recorded events and returns, per kernel class, the summed milliseconds and the number of
+ * launches (arrays of FLY_K_CLASSES entries; either may be NULL). */
+int fly_profile_read(double *ms, int64_t *launches);
+
+/* ---- tuning (for sweeps; defaults are the measured best) --------------------------------------- */
+/* key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept
+ * row-major (0 = automatic, 1 = all column chunks of a row back to back). */
+int fly_set_tuning(const char *key, int64_t value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLYEVAL_H */

@@ -1,0 +1,69 @@
+"""CPU tests of the C ABI: the library loads, exports every function include/flyeval.h declares, and its
+host-side argument checks answer without a GPU.  No compute call is made here."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from helpers import REPO, tiny_connectome
+
+HEADER = os.path.join(REPO, "include", "flyeval.h")
+
+
+def _declared() -> set[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(fly_[a-z0-9_]+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from chessfly import _hip
+    if not os.path.exists(_hip.LIB_PATH):
+        subprocess.run(["make", "-C", os.path.join(REPO, "alpha-fly_amd", "csrc"), "-j8"], check=True)
+    return _hip.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    names = _declared()
+    assert {"fly_cone_create", "fly_plan_create", "fly_forward_io", "fly_forward_literal", "fly_model_forward",
+            "fly_encoder", "fly_head", "fly_last_error", "fly_abi_version"} <= names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [name for name in sorted(_declared()) if not hasattr(lib, name)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header_exactly():
+    from chessfly import _hip
+    assert set(_hip.SIGNATURES) == _declared()
+
+
+def test_version_and_error_reporting_on_host(lib):
+    assert lib.fly_abi_version() == 1
+    assert lib.fly_set_tuning(b"no-such-knob", 1) == 1          # FLY_ERR_INVALID
+    assert b"no-such-knob" in lib.fly_last_error()
+    out = ctypes.c_void_p()
+    assert lib.fly_cone_create(0, 0, None, None, None, 0, None, 0, 1, None, ctypes.byref(out)) == 1
+    assert out.value is None
+    assert lib.fly_forward_io_workspace(None, 64) == 0
+
+
+def test_product_refuses_cpu_tensors():
+    """No CPU fallback: the drop-in classes raise instead of computing on the host."""
+    from chessfly.brain import ConnectomeRNN
+    rnn = ConnectomeRNN(tiny_connectome(), global_scale=3.0)
+    with torch.no_grad():
+        with pytest.raises(RuntimeError, match="HIP device"):
+            rnn(torch.zeros(30, 4), 3)
+        with pytest.raises(RuntimeError, match="HIP device"):
+            rnn.forward_io(torch.zeros(5, 4), torch.arange(5), torch.arange(25, 30), 3)
+    with pytest.raises(NotImplementedError):
+        rnn(torch.zeros(30, 4), 3)                              # grad mode: training is not part of the evaluator

@@ -1,0 +1,344 @@
+"""GPU parity: the HIP evaluator (through the C ABI) against the CPU oracle on the same seeded inputs.
+
+Integer work (light cones, sub-matrices, index tables) must be bit-exact; float32 paths within float32
+round-off of the fp64 oracle; the float16 deviation path within the reference's own float16 tolerance and,
+for the full model, within 1e-3 max-abs of the float32 path with >= 99.9% policy-argmax agreement."""
+
+from __future__ import annotations
+
+import json
+import os
+import warnings
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import REPO, brain_arrays, random_params, tiny_connectome
+
+from oracle import lightcone as L, forward as F
+
+warnings.filterwarnings("ignore", message="Sparse CSR tensor support is in beta")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+GOLDEN = os.path.join(REPO, "tests", "golden", "fullscale_cone.json")
+
+
+def product_rnn(conn, scale, lg, b, al, h_max=10.0):
+    from chessfly.brain import ConnectomeRNN
+    rnn = ConnectomeRNN(conn, global_scale=scale, h_max=h_max)
+    with torch.no_grad():
+        rnn.log_gain.copy_(torch.as_tensor(lg))
+        rnn.bias.copy_(torch.as_tensor(b))
+        rnn.alpha_logit.copy_(torch.as_tensor(al))
+    return rnn.to(DEV)
+
+
+def oracle_cone(conn, in_idx, out_idx, steps):
+    return L.light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), np.asarray(in_idx), np.asarray(out_idx),
+                        steps)
+
+
+def assert_cone_equal(cone, ref):
+    """Every LightCone attribute of the device cone equals the oracle's, element for element."""
+    cpu = lambda t: t.detach().cpu().numpy()
+    assert cone.steps == ref.steps
+    for t in range(ref.steps + 1):
+        np.testing.assert_array_equal(cpu(cone.rows[t]), ref.rows[t])
+    for t in range(1, ref.steps + 1):
+        if ref.ops[t] is None:
+            assert cone.ops[t] is None
+        else:
+            op, rop = cone.ops[t], ref.ops[t]
+            assert op.shape == rop.shape
+            for name in ("edges", "post", "pre", "crow"):
+                np.testing.assert_array_equal(cpu(getattr(op, name)), getattr(rop, name), err_msg=f"{name} t={t}")
+        for name in ("keep_next", "keep_prev", "prev_row", "u_pos", "u_src"):
+            np.testing.assert_array_equal(cpu(getattr(cone, name)[t]), getattr(ref, name)[t], err_msg=f"{name} t={t}")
+        np.testing.assert_array_equal(cpu(cone.carried[t]).reshape(-1), ref.carried[t])
+    np.testing.assert_array_equal(cpu(cone.out_pos), ref.out_pos)
+    np.testing.assert_array_equal(cpu(cone.out_src), ref.out_src)
+    assert cone.edge_visits == ref.edge_visits
+
+
+TINY = [(120, 700, 3, np.arange(0, 9), np.arange(100, 120)),
+        (30, 200, 0, np.arange(0, 5), np.arange(25, 30)),
+        (60, 600, 1, np.array([3, 7, 11, 40]), np.array([0, 7, 59]))]
+
+
+@pytest.mark.parametrize("n,e,seed,in_idx,out_idx", TINY)
+@pytest.mark.parametrize("steps", [0, 1, 2, 4, 6])
+def test_light_cone_bit_exact_tiny(n, e, seed, in_idx, out_idx, steps):
+    conn = tiny_connectome(n, e, seed)
+    rnn = product_rnn(conn, 3.0, *random_params(conn, 1))
+    cone = rnn.light_cone(torch.as_tensor(in_idx, device=DEV), torch.as_tensor(out_idx, device=DEV), steps)
+    assert_cone_equal(cone, oracle_cone(conn, in_idx, out_idx, steps))
+
+
+def test_light_cone_bit_exact_on_shuffled_control_with_repeats():
+    conn = tiny_connectome(80, 2000, 4).shuffled(3)
+    rnn = product_rnn(conn, 2.0, *random_params(conn, 2))
+    in_idx, out_idx = np.arange(0, 10), np.arange(60, 80)
+    for steps in (3, 6):
+        cone = rnn.light_cone(torch.as_tensor(in_idx, device=DEV), torch.as_tensor(out_idx, device=DEV), steps)
+        assert_cone_equal(cone, oracle_cone(conn, in_idx, out_idx, steps))
+
+
+def _medium(seed=0):
+    from chessfly.synthetic import GraphSpec, synthetic_connectome
+    spec = GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=80, seed=seed)
+    return synthetic_connectome(spec)
+
+
+@pytest.mark.parametrize("batch", [1, 5, 64, 200])
+def test_literal_recurrence_matches_oracle(batch):
+    conn = _medium()
+    lg, b, al = random_params(conn, 5, gain_sd=0.1)
+    rnn = product_rnn(conn, 4.0, lg, b, al)
+    ba = brain_arrays(conn, 4.0, lg, b, al, dtype=torch.float64)
+    g = torch.Generator().manual_seed(batch)
+    u = torch.randn(conn.n_neurons, batch, generator=g) * 0.5
+    for steps in (0, 1, 3, 6):
+        u_dev = u.to(DEV)
+        with torch.no_grad():
+            h = rnn(u_dev, steps)
+        torch.cuda.synchronize()
+        ref = F.literal(ba, u.double(), steps)
+        np.testing.assert_allclose(h.cpu().numpy(), ref.numpy(), rtol=2e-5, atol=2e-5)
+        # the reference's inference path leaves u + bias in u
+        np.testing.assert_allclose(u_dev.cpu().numpy(), (u + torch.as_tensor(b)[:, None]).numpy(), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("batch", [1, 7, 64, 130])
+@pytest.mark.parametrize("steps", [1, 2, 4, 6])
+def test_cone_forward_f32_matches_oracle_and_literal(batch, steps):
+    conn = _medium(1)
+    lg, b, al = random_params(conn, 6, gain_sd=0.1)
+    rnn = product_rnn(conn, 4.0, lg, b, al)
+    ba = brain_arrays(conn, 4.0, lg, b, al, dtype=torch.float64)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    u_in = torch.randn(len(in_idx), batch, generator=torch.Generator().manual_seed(steps)) * 0.5
+    with torch.no_grad():
+        out = rnn.forward_io(u_in.to(DEV), in_idx.to(DEV), out_idx.to(DEV), steps)
+        u = torch.zeros(conn.n_neurons, batch, device=DEV).index_add_(0, in_idx.to(DEV), u_in.to(DEV))
+        lit = rnn(u, steps)[out_idx.to(DEV)]
+    cone = oracle_cone(conn, in_idx, out_idx, steps)
+    ref = F.cone_f32(ba, cone, u_in.double(), steps)
+    assert out.dtype == torch.float32 and out.shape == (len(out_idx), batch)
+    np.testing.assert_allclose(out.cpu().numpy(), ref.numpy(), rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(out.cpu().numpy(), lit.cpu().numpy(), rtol=2e-5, atol=2e-5)
+
+
+def test_half_precision_inference_matches_float32():
+    """tests/test_core.py:491-511 on the device: a small signal on a large resting state, rows clamped below
+    zero and above h_max; the float16 deviation path must stay within 0.02 * signal + 1e-4 of float32."""
+    conn = tiny_connectome(400, 9000, seed=5)
+    g = torch.Generator().manual_seed(0)
+    lg = (torch.randn(conn.n_edges, generator=g) * 0.8).numpy()
+    b = (0.6 + torch.randn(conn.n_neurons, generator=g) * 0.7).numpy()
+    b[::17] += 12.0
+    al = torch.randn(conn.n_neurons, generator=g).numpy()
+    rnn = product_rnn(conn, 2.0, lg, b, al)
+    in_idx, out_idx = torch.arange(0, 40, device=DEV), torch.arange(300, 400, device=DEV)
+    u = (torch.randn(40, 64, generator=g) * 0.05).to(DEV)
+    ba = brain_arrays(conn, 2.0, lg, b, al, dtype=torch.float64)
+    with torch.no_grad():
+        for steps in (1, 3, 6):
+            ref = rnn.forward_io(u, in_idx, out_idx, steps)
+            half = rnn.forward_io(u.half(), in_idx, out_idx, steps)
+            assert half.dtype == torch.float32
+            signal = (ref - ref.mean(1, keepdim=True)).abs().mean()
+            assert float((half - ref).abs().max()) < 0.02 * float(signal) + 1e-4
+            # and at least as close to the exact function as the reference's float16 emulation
+            cone = oracle_cone(conn, in_idx.cpu(), out_idx.cpu(), steps)
+            exact = F.cone_f32(ba, cone, u.cpu().double(), steps).numpy()
+            ours = np.abs(half.cpu().numpy() - exact).max()
+            emulated = np.abs(F.cone_half(brain_arrays(conn, 2.0, lg, b, al), cone, u.cpu(), steps).numpy() - exact).max()
+            assert ours <= emulated + 1e-6, (steps, ours, emulated)
+
+
+@pytest.mark.parametrize("batch", [1, 3, 64, 100])
+def test_deviation_path_matches_exact_function(batch):
+    conn = _medium(2)
+    lg, b, al = random_params(conn, 8, gain_sd=0.1)
+    rnn = product_rnn(conn, 4.0, lg, b, al)
+    ba = brain_arrays(conn, 4.0, lg, b, al, dtype=torch.float64)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    u_in = torch.randn(len(in_idx), batch, generator=torch.Generator().manual_seed(batch))
+    steps = 6
+    with torch.no_grad():
+        out = rnn.forward_io(u_in.half().to(DEV), in_idx.to(DEV), out_idx.to(DEV), steps)
+    cone = oracle_cone(conn, in_idx, out_idx, steps)
+    exact = F.cone_f32(ba, cone, u_in.half().double(), steps).numpy()
+    err = np.abs(out.cpu().numpy() - exact).max()
+    dev_scale = np.abs(exact - F.cone_f32(ba, cone, torch.zeros_like(u_in).double(), steps).numpy()).max()
+    assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
+
+
+def test_encoder_and_head_gemms_match_fp64():
+    import ctypes
+    from chessfly import _hip
+    lib = _hip.load()
+    rng = np.random.default_rng(0)
+    for batch, n_in, k, ld in ((5, 70, 30, 33), (130, 300, 838, 967)):
+        x = torch.as_tensor(rng.random((batch, ld)) < 0.1, dtype=torch.float32)
+        x[:, 0] = 0.37
+        w = torch.as_tensor(rng.normal(0, 0.05, (n_in, ld)), dtype=torch.float32)
+        bias = torch.as_tensor(rng.normal(0, 0.05, n_in), dtype=torch.float32)
+        ref = ((x[:, :k].double() @ w[:, :k].double().T + bias.double()) * 5.0).T
+        for f16 in (0, 1):
+            ldu = batch + 3
+            u = torch.zeros(n_in, ldu, dtype=torch.float16 if f16 else torch.float32, device=DEV)
+            xd, wd, bd = x.to(DEV), w.to(DEV), bias.to(DEV)
+            _hip.check(lib.fly_encoder(xd.data_ptr(), ld, batch, k, wd.data_ptr(), ld, bd.data_ptr(), n_in, 5.0,
+                                       u.data_ptr(), ldu, f16, _hip.stream(torch.device(DEV))), "fly_encoder")
+            got = u[:, :batch].double().cpu()
+            tol = ref.abs() * (2 ** -10) + 1e-6 if f16 else 1e-5
+            assert bool(((got - ref).abs() <= tol).all())
+    # head
+    n_out, moves, batch = 150, 4168, 37
+    from chessfly.encoding import move_squares
+    frm, to = move_squares()
+    T = lambda a: torch.as_tensor(np.asarray(a, dtype=np.float32))
+    P = dict(policy_w=rng.normal(0, 0.1, (moves, n_out)), policy_b=rng.normal(0, 0.1, moves),
+             from_w=rng.normal(0, 0.1, (64, n_out)), from_b=rng.normal(0, 0.1, 64),
+             to_w=rng.normal(0, 0.1, (64, n_out)), to_b=rng.normal(0, 0.1, 64),
+             value_w=rng.normal(0, 0.1, (3, n_out)), value_b=rng.normal(0, 0.1, 3),
+             mean=rng.normal(0, 1, n_out), var=rng.uniform(0.01, 2, n_out))
+    dev = {k: T(v).to(DEV).contiguous() for k, v in P.items()}
+    mf, mt = torch.as_tensor(frm.astype(np.int32), device=DEV), torch.as_tensor(to.astype(np.int32), device=DEV)
+    desc = _hip.HeadDesc(n_out, moves, dev["mean"].data_ptr(), dev["var"].data_ptr(), 1e-8, 8.0,
+                         dev["policy_w"].data_ptr(), dev["policy_b"].data_ptr(), dev["from_w"].data_ptr(),
+                         dev["from_b"].data_ptr(), dev["to_w"].data_ptr(), dev["to_b"].data_ptr(),
+                         dev["value_w"].data_ptr(), dev["value_b"].data_ptr(), mf.data_ptr(), mt.data_ptr())
+    r = torch.as_tensor(rng.normal(0, 3, (n_out, batch)), dtype=torch.float32)
+    logits = torch.empty(batch, moves, device=DEV)
+    wdl = torch.empty(batch, 3, device=DEV)
+    ws = _hip.workspace(lib.fly_head_workspace(ctypes.byref(desc), batch), torch.device(DEV))
+    rd = r.to(DEV)
+    _hip.check(lib.fly_head(ctypes.byref(desc), rd.data_ptr(), batch, batch, logits.data_ptr(), wdl.data_ptr(),
+                            ws.data_ptr(), ws.numel(), _hip.stream(torch.device(DEV))), "fly_head")
+    from oracle.forward import HeadArrays
+    d = lambda k: T(P[k]).double()
+    hp = HeadArrays(None, None, 5.0, 0, d("policy_w"), d("policy_b"), d("from_w"), d("from_b"), d("to_w"), d("to_b"),
+                    d("value_w"), d("value_b"), torch.as_tensor(frm), torch.as_tensor(to), d("mean"), d("var"))
+    ref_l, ref_w = F.heads(hp, F.norm(hp, r.double().T))
+    np.testing.assert_allclose(logits.cpu().numpy(), ref_l.numpy(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(wdl.cpu().numpy(), ref_w.numpy(), rtol=1e-5, atol=1e-5)
+
+
+# ---- full scale (166,700 neurons, 10.5M synapses) ------------------------------------------------------------
+
+def _record_from_device(cone, in_idx):
+    """The golden-record digests of a device cone (same fields as tests/golden/make_golden.py)."""
+    from golden.make_golden import digest
+    steps = []
+    for t in range(cone.steps + 1):
+        rec = {"rows": int(cone.row_counts[t]), "rows_sha": digest(cone.rows[t].cpu().numpy())}
+        if t >= 1:
+            nr = cone.row_counts[t]
+            prev = torch.empty(nr, dtype=torch.int32, device=DEV)
+            usrc = torch.empty(nr, dtype=torch.int32, device=DEV)
+            cone._step_export(t, prev=prev, usrc=usrc)
+            rec.update(prev_sha=digest(prev.cpu().numpy()), usrc_sha=digest(usrc.cpu().numpy()),
+                       carried=int((prev >= 0).sum()), fed=int((usrc >= 0).sum()))
+            if cone.ops[t] is None:
+                rec.update(op=False, nnz=0)
+            else:
+                op = cone.ops[t]
+                rec.update(op=True, nnz=int(cone.nnz[t]), crow_sha=digest(op.crow.cpu().numpy()),
+                           col_sha=digest(op.pre.cpu().numpy()), edge_sha=digest(op.edges.cpu().numpy()))
+        steps.append(rec)
+    src = torch.full((cone.n_out,), -1, dtype=torch.long, device=DEV)
+    src[cone.out_pos] = cone.out_src
+    return {"steps": steps, "edge_visits": int(cone.edge_visits), "out_src_sha": digest(src.cpu().numpy()),
+            "out_hit": int(len(cone.out_pos))}
+
+
+@pytest.mark.parametrize("graph", ["synthetic", "shuffled"])
+def test_full_scale_light_cone_bit_exact(graph, full_net):
+    with open(GOLDEN) as f:
+        gold = json.load(f)["graphs"][graph]
+    net, conn = full_net
+    if graph == "shuffled":
+        from chessfly.brain import ConnectomeRNN
+        conn = conn.shuffled(0)
+        rnn = ConnectomeRNN(conn).to(DEV)
+    else:
+        rnn = net.brain
+    in_idx, out_idx = conn.nodes("afferent").to(DEV), conn.nodes("efferent").to(DEV)
+    for steps in ("6", "4"):
+        cone = rnn.light_cone(in_idx, out_idx, int(steps))
+        assert _record_from_device(cone, in_idx) == gold["cones"][steps], (graph, steps)
+
+
+def _oracle_full(conn):
+    from chessfly.synthetic import synthetic_maps, synthetic_params
+    from chessfly.encoding import N_BASE, move_squares
+    from helpers import head_arrays
+    p = synthetic_params(conn, seed=0)
+    ba = brain_arrays(conn, p.global_scale, p.log_gain, p.bias, p.alpha_logit)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    frm, to = move_squares()
+    hp = head_arrays(synthetic_maps(len(in_idx), len(out_idx), 0), 5.0, N_BASE, frm, to, len(out_idx))
+    cone = oracle_cone(conn, in_idx, out_idx, 6)
+    return ba, hp, cone
+
+
+def test_full_scale_model_matches_oracle(full_net):
+    """FlyChessNet.forward at full scale, float32 and float16-deviation paths, against the oracle's float32
+    forward on 24 boards: policy logits and WDL within 1e-3 max-abs, argmax equal."""
+    from chessfly.synthetic import synthetic_boards
+    net, conn = full_net
+    ba, hp, cone = _oracle_full(conn)
+    x = torch.as_tensor(synthetic_boards(24, seed=11))
+    ref_logits, ref_wdl = F.model_forward(ba, hp, cone, x, "f32")
+    for dtype in (torch.float32, torch.float16):
+        net.infer_dtype = dtype
+        with torch.no_grad():
+            logits, wdl = net(x.to(DEV))
+        torch.cuda.synchronize()
+        dl = float((logits.cpu() - ref_logits).abs().max())
+        dw = float((wdl.cpu() - ref_wdl).abs().max())
+        print(f"{dtype}: max |logit diff| {dl:.3e}  max |wdl diff| {dw:.3e}", flush=True)
+        assert dl < 1e-3 and dw < 1e-3, (dtype, dl, dw)
+        assert torch.equal(logits.cpu().argmax(1), ref_logits.argmax(1))
+    net.infer_dtype = torch.float16
+
+
+def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
+    """The bench configuration: B = 1120 boards, float16 deviation vs float32 on the device."""
+    from chessfly.synthetic import synthetic_boards
+    net, _ = full_net
+    x = torch.as_tensor(synthetic_boards(1120, seed=5)).to(DEV)
+    out = {}
+    for dtype in (torch.float32, torch.float16):
+        net.infer_dtype = dtype
+        with torch.no_grad():
+            out[dtype] = net(x)
+    net.infer_dtype = torch.float16
+    (l32, w32), (l16, w16) = out[torch.float32], out[torch.float16]
+    dl, dw = float((l16 - l32).abs().max()), float((w16 - w32).abs().max())
+    agree = float((l16.argmax(1) == l32.argmax(1)).float().mean())
+    print(f"B=1120: max |logit diff| {dl:.3e}, max |wdl diff| {dw:.3e}, argmax agreement {agree:.4%}", flush=True)
+    assert dl < 1e-3 and dw < 1e-3 and agree >= 0.999
+
+
+def test_evaluator_protocol(full_net):
+    """Evaluator.submit/result (chessfly/model.py:113-135): lazy fp16 policy vectors, eager legal gathers."""
+    from chessfly.model import Evaluator
+    from chessfly.synthetic import synthetic_boards
+    from chessfly.encoding import N_MOVES
+    net, _ = full_net
+    ev = Evaluator(net, torch.device(DEV))
+    x = synthetic_boards(9, seed=2).astype(np.float16)
+    lazy_logits, values = ev(x, None, None)
+    assert lazy_logits.shape == (9, N_MOVES) and lazy_logits.dtype == np.float16 and values.shape == (9,)
+    rows = np.repeat(np.arange(9), 5)
+    cols = np.random.default_rng(0).integers(0, N_MOVES, size=45)
+    legal, values2 = ev(x, rows, cols)
+    assert legal.dtype == np.float32 and legal.shape == (45,)
+    np.testing.assert_allclose(legal, lazy_logits[rows, cols].astype(np.float32), rtol=2e-3, atol=2e-3)
+    np.testing.assert_allclose(values, values2, rtol=1e-6)
+    assert np.all(np.abs(values) <= 1)
