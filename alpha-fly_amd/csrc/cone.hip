@@ -337,8 +337,10 @@ extern "C" int fly_cone_sizes(const fly_cone *cone, int64_t *rows, int64_t *nnz,
 
 extern "C" int fly_cone_rows(const fly_cone *cone, int32_t t, int32_t *rows, void *stream) {
   return guard([&] {
-    FLY_REQUIRE(cone && rows, "null argument");
+    FLY_REQUIRE(cone, "cone is null");
     FLY_REQUIRE(t >= 0 && t <= cone->steps, "step out of range");
+    if (cone->rows_n[t] == 0) return;
+    FLY_REQUIRE(rows, "rows is null");
     copy_d2d(rows, cone->rows[t].p, sizeof(int32_t) * cone->rows_n[t], as_stream(stream));
   });
 }
@@ -362,7 +364,9 @@ extern "C" int fly_cone_step(const fly_cone *cone, int32_t t, int32_t *crow, int
 
 extern "C" int fly_cone_outputs(const fly_cone *cone, int32_t *out_src, void *stream) {
   return guard([&] {
-    FLY_REQUIRE(cone && out_src, "null argument");
+    FLY_REQUIRE(cone, "cone is null");
+    if (cone->n_out == 0) return;
+    FLY_REQUIRE(out_src, "out_src is null");
     copy_d2d(out_src, cone->out_src.p, sizeof(int32_t) * cone->n_out, as_stream(stream));
   });
 }

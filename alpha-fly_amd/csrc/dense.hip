@@ -15,8 +15,8 @@ namespace fly {
 
 int64_t state_ld(int64_t batch);
 size_t io_workspace(const fly_plan &plan, int64_t batch);
-template <typename S>
-const S *run_cone_steps(const fly_plan &plan, const S *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st);
+template <typename S, typename U>
+const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st);
 void check_plan_device(const fly_plan *plan);
 
 namespace {
@@ -252,8 +252,7 @@ extern "C" int fly_head(const fly_head_desc *head, const float *r, int64_t ldr, 
 
 extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_head_desc *head, int64_t batch) {
   if (!plan || !head) return 0;
-  const size_t es = plan->mode == FLY_MODE_DEVIATION_F16 ? 2 : 4;
-  return align256((size_t)plan->n_in * state_ld(batch) * es) + align256(io_workspace(*plan, batch)) +
+  return align256((size_t)plan->n_in * state_ld(batch) * sizeof(float)) + align256(io_workspace(*plan, batch)) +
          align256(head_ws(*head, batch));
 }
 
@@ -276,20 +275,20 @@ extern "C" int fly_model_forward(const fly_plan *plan, const fly_head_desc *head
     const bool dev = plan->mode == FLY_MODE_DEVIATION_F16;
     char *base = static_cast<char *>(ws);
     void *u = base;
-    base += align256((size_t)plan->n_in * ldu * (dev ? 2 : 4));
+    base += align256((size_t)plan->n_in * ldu * sizeof(float));
     void *states = base;
     base += align256(io_workspace(*plan, batch));
     float *ct = reinterpret_cast<float *>(base);
     const int64_t lds = state_ld(batch);
+    // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
+    run_encoder<float>(x, ldx, batch, k, enc_w, ldw, enc_b, plan->n_in, input_gain, static_cast<float *>(u), ldu, st);
     if (dev) {
-      run_encoder<_Float16>(x, ldx, batch, k, enc_w, ldw, enc_b, plan->n_in, input_gain, static_cast<_Float16 *>(u), ldu, st);
-      const _Float16 *fin = run_cone_steps<_Float16>(*plan, static_cast<_Float16 *>(u), ldu, batch, states, st);
+      const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, static_cast<float *>(u), ldu, batch, states, st);
       NormalisedOutputsB<_Float16> B{fin, lds, plan->out_src.p, plan->cbase.p, head->norm_mean, head->norm_var,
                                      head->norm_eps, head->norm_clip};
       run_head<_Float16>(*head, B, batch, ct, logits, wdl, st);
     } else {
-      run_encoder<float>(x, ldx, batch, k, enc_w, ldw, enc_b, plan->n_in, input_gain, static_cast<float *>(u), ldu, st);
-      const float *fin = run_cone_steps<float>(*plan, static_cast<float *>(u), ldu, batch, states, st);
+      const float *fin = run_cone_steps<float, float>(*plan, static_cast<float *>(u), ldu, batch, states, st);
       NormalisedOutputsB<float> B{fin, lds, plan->out_src.p, plan->cbase.p, head->norm_mean, head->norm_var,
                                   head->norm_eps, head->norm_clip};
       run_head<float>(*head, B, batch, ct, logits, wdl, st);

@@ -55,14 +55,14 @@ struct Lanes<S, 1> {
   static __device__ __forceinline__ void store(S *p, const float (&f)[1]) { *p = static_cast<S>(f[0]); }
 };
 
-template <typename S>
+template <typename S, typename U>
 struct StepArgs {
   const int32_t *rowptr;   // |R_t| + 1, or null: no matrix term
   const int2 *colval;      // {column in X_{t-1}, float bits of the weight}
   const RowParam *params;  // |R_t|
   const S *xprev;          // X_{t-1} (rows, ldx), or null: previous state absent (zero, nothing carried)
   int64_t ldx;
-  const S *u;              // input drive (n_in, ldu), or null
+  const U *u;              // input drive (n_in, ldu), or null
   int64_t ldu;
   S *xout;                 // X_t (|R_t|, ldo)
   int64_t ldo;
@@ -70,8 +70,8 @@ struct StepArgs {
   int32_t u_vec;           // the drive can be read with V-wide loads
 };
 
-template <typename S, int V, bool TORCH_LERP>
-__global__ __launch_bounds__(256) void k_state_step(const StepArgs<S> a) {
+template <typename S, typename U, int V, bool TORCH_LERP>
+__global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   const int lane = threadIdx.x & 63;
   const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t per_tile = (uint32_t)a.nrows * (uint32_t)a.wpt;
@@ -123,9 +123,9 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S> a) {
 #pragma unroll
   for (int i = 0; i < V; ++i) u[i] = 0.0f;
   if (a.u != nullptr && p.usrc >= 0) {
-    const S *src = a.u + (int64_t)p.usrc * a.ldu + col;
+    const U *src = a.u + (int64_t)p.usrc * a.ldu + col;
     if (a.u_vec) {
-      Lanes<S, V>::load(src, u);
+      Lanes<U, V>::load(src, u);
     } else {
 #pragma unroll
       for (int i = 0; i < V; ++i) u[i] = (col + i < a.batch) ? static_cast<float>(src[i]) : 0.0f;
@@ -147,24 +147,24 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S> a) {
   Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out);
 }
 
-template <typename S, int V>
-void launch_v(const StepArgs<S> &a, bool torch_lerp, hipStream_t st) {
+// Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
+// with torch.lerp's formula, like the reference's CPU path.
+template <typename S, typename U, int V>
+void launch_v(const StepArgs<S, U> &a, hipStream_t st) {
   const int64_t waves = (int64_t)a.nrows * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
-  if (torch_lerp)
-    hipLaunchKernelGGL((k_state_step<S, V, true>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((k_state_step<S, V, false>), grid, block, 0, st, a);
+  constexpr bool kTorchLerp = sizeof(S) == 4;
+  hipLaunchKernelGGL((k_state_step<S, U, V, kTorchLerp>), grid, block, 0, st, a);
 }
 
 template <typename S>
 constexpr int max_vec() { return 16 / (int)sizeof(S); }
 
 // Largest V (elements per lane) that every V-wide access of the step allows, or the tuned value.
-template <typename S>
-int pick_vec(const StepArgs<S> &a) {
+template <typename S, typename U>
+int pick_vec(const StepArgs<S, U> &a) {
   auto ok = [&](int v) {
     const size_t bytes = (size_t)v * sizeof(S);
     if (a.ldo % v || !aligned(a.xout, bytes)) return false;
@@ -178,22 +178,22 @@ int pick_vec(const StepArgs<S> &a) {
   return 1;
 }
 
-template <typename S>
-void state_step(StepArgs<S> a, bool torch_lerp, hipStream_t st) {
+template <typename S, typename U>
+void state_step(StepArgs<S, U> a, hipStream_t st) {
   if (a.nrows == 0 || a.batch == 0) return;
   const int v = pick_vec(a);
-  a.u_vec = (a.u != nullptr && a.ldu % v == 0 && aligned(a.u, (size_t)v * sizeof(S))) ? 1 : 0;
+  a.u_vec = (a.u != nullptr && a.ldu % v == 0 && aligned(a.u, (size_t)v * sizeof(U))) ? 1 : 0;
   const int chunks = (int)((a.batch + 64 * v - 1) / (64 * v));
   int tiles = tuning().tiles > 0 ? (int)tuning().tiles : chunks;
   if (tiles > chunks || chunks % tiles) tiles = chunks;
   a.ntiles = tiles;
   a.wpt = chunks / tiles;
   switch (v) {
-    case 1: launch_v<S, 1>(a, torch_lerp, st); break;
-    case 2: launch_v<S, 2>(a, torch_lerp, st); break;
-    case 4: launch_v<S, 4>(a, torch_lerp, st); break;
+    case 1: launch_v<S, U, 1>(a, st); break;
+    case 2: launch_v<S, U, 2>(a, st); break;
+    case 4: launch_v<S, U, 4>(a, st); break;
     default:
-      if constexpr (sizeof(S) == 2) launch_v<S, 8>(a, torch_lerp, st);
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, st);
       break;
   }
   check_launch("state step");
@@ -240,20 +240,19 @@ size_t io_workspace(const fly_plan &plan, int64_t batch) {
 
 // Runs steps 1..T of a light-cone plan.  Returns the final state (null if R_T is empty) in one of the two
 // workspace buffers, whose row stride is state_ld(batch).
-template <typename S>
-const S *run_cone_steps(const fly_plan &plan, const S *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st) {
+template <typename S, typename U>
+const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st) {
   const int64_t lds = state_ld(batch);
   S *buf[2] = {reinterpret_cast<S *>(ws), reinterpret_cast<S *>(ws) + (size_t)plan.max_rows * lds};
   const S *prev = nullptr;
   int cur = 0;
-  const bool torch_lerp = plan.mode == FLY_MODE_F32;
   for (int t = 1; t <= plan.steps; ++t) {
     const int64_t nr = plan.rows_n[t];
     if (nr == 0) {
       prev = nullptr;
       continue;
     }
-    StepArgs<S> a{};
+    StepArgs<S, U> a{};
     a.rowptr = plan.rowptr[t].p;  // null where A_t does not exist
     a.colval = plan.colval[t].p;
     a.params = plan.params[t].p;
@@ -265,7 +264,7 @@ const S *run_cone_steps(const fly_plan &plan, const S *u, int64_t ldu, int64_t b
     a.ldo = lds;
     a.nrows = (int32_t)nr;
     a.batch = (int32_t)batch;
-    state_step(a, torch_lerp, st);
+    state_step(a, st);
     prev = buf[cur];
     cur ^= 1;
   }
@@ -281,8 +280,11 @@ void write_outputs(const fly_plan &plan, const S *state, int64_t batch, float *o
   check_launch("outputs");
 }
 
-template const _Float16 *run_cone_steps<_Float16>(const fly_plan &, const _Float16 *, int64_t, int64_t, void *, hipStream_t);
-template const float *run_cone_steps<float>(const fly_plan &, const float *, int64_t, int64_t, void *, hipStream_t);
+template const _Float16 *run_cone_steps<_Float16, _Float16>(const fly_plan &, const _Float16 *, int64_t, int64_t, void *,
+                                                            hipStream_t);
+template const _Float16 *run_cone_steps<_Float16, float>(const fly_plan &, const float *, int64_t, int64_t, void *,
+                                                         hipStream_t);
+template const float *run_cone_steps<float, float>(const fly_plan &, const float *, int64_t, int64_t, void *, hipStream_t);
 
 void check_plan_device(const fly_plan *plan) {
   FLY_REQUIRE(plan != nullptr, "plan is null");
@@ -310,10 +312,11 @@ extern "C" int fly_forward_io(const fly_plan *plan, const void *u_in, int64_t ld
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     hipStream_t st = as_stream(stream);
     if (plan->mode == FLY_MODE_DEVIATION_F16) {
-      const _Float16 *fin = run_cone_steps<_Float16>(*plan, static_cast<const _Float16 *>(u_in), ldu, batch, ws, st);
+      const _Float16 *fin =
+          run_cone_steps<_Float16, _Float16>(*plan, static_cast<const _Float16 *>(u_in), ldu, batch, ws, st);
       write_outputs<_Float16>(*plan, fin, batch, out, ldo, st);
     } else {
-      const float *fin = run_cone_steps<float>(*plan, static_cast<const float *>(u_in), ldu, batch, ws, st);
+      const float *fin = run_cone_steps<float, float>(*plan, static_cast<const float *>(u_in), ldu, batch, ws, st);
       write_outputs<float>(*plan, fin, batch, out, ldo, st);
     }
   });
@@ -353,7 +356,7 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
     int cur = 0;
     for (int t = 1; t <= steps; ++t) {
       const bool last = t == steps;
-      StepArgs<float> a{};
+      StepArgs<float, float> a{};
       a.rowptr = plan->rowptr[0].p;
       a.colval = plan->colval[0].p;
       a.params = plan->params[0].p;
@@ -365,7 +368,7 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
       a.ldo = last ? ldh : lds;
       a.nrows = (int32_t)n;
       a.batch = (int32_t)batch;
-      state_step(a, true, st);
+      state_step(a, st);
       prev = buf[cur];
       cur ^= 1;
     }
