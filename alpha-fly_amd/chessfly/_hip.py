@@ -50,12 +50,14 @@ SIGNATURES = {
     "fly_forward_io": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_forward_literal_workspace": (_sz, [_p, _i64]),
     "fly_forward_literal": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
-    "fly_encoder": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _f32, _p, _i64, _i32, _p]),
-    "fly_head_workspace": (_sz, [ctypes.POINTER(HeadDesc), _i64]),
-    "fly_head": (_i32, [ctypes.POINTER(HeadDesc), _p, _i64, _i64, _p, _p, _p, _sz, _p]),
-    "fly_model_workspace": (_sz, [_p, ctypes.POINTER(HeadDesc), _i64]),
-    "fly_model_forward": (_i32, [_p, ctypes.POINTER(HeadDesc), _p, _i64, _i64, _i64, _p, _i64, _p, _f32, _p, _p, _p,
-                                 _sz, _p]),
+    "fly_dense_create": (_i32, [ctypes.POINTER(HeadDesc), _p, _i64, _i64, _p, _i64, _p, _pp]),
+    "fly_dense_destroy": (_i32, [_p]),
+    "fly_encoder_workspace": (_sz, [_p, _i64]),
+    "fly_encoder": (_i32, [_p, _p, _i64, _i64, _f32, _p, _i64, _i32, _p, _sz, _p]),
+    "fly_head_workspace": (_sz, [_p, _i64]),
+    "fly_head": (_i32, [_p, _p, _i64, _i64, _p, _p, _p, _sz, _p]),
+    "fly_model_workspace": (_sz, [_p, _p, _i64]),
+    "fly_model_forward": (_i32, [_p, _p, _p, _i64, _i64, _f32, _p, _p, _p, _sz, _p]),
     "fly_profile_enable": (_i32, [_i32]),
     "fly_profile_read": (_i32, [_p, _p]),
     "fly_set_tuning": (_i32, [ctypes.c_char_p, _i64]),
@@ -117,6 +119,22 @@ def profile_read() -> dict:
     n = (ctypes.c_int64 * 4)()
     check(load().fly_profile_read(ms, n), "fly_profile_read")
     return {name: (float(ms[i]), int(n[i])) for i, name in enumerate(KERNEL_CLASSES)}
+
+
+class Handle:
+    """Owner of a library object (cone, plan or dense plan): destroyed with the matching C call."""
+
+    def __init__(self, handle: ctypes.c_void_p, destroy: str, key=None):
+        self.handle, self._destroy, self.key = handle, destroy, key
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            try:
+                getattr(load(), self._destroy)(h)
+            except Exception:
+                pass
+            self.handle = None
 
 
 def set_tuning(key: str, value: int) -> None:

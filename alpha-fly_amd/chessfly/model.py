@@ -12,6 +12,7 @@ operand loader gathers the output neurons and applies the eval-mode normaliser i
 
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 
 import numpy as np
@@ -89,17 +90,33 @@ class FlyChessNet(nn.Module):
         nn.init.zeros_(self.policy.weight)
         nn.init.zeros_(self.value.weight)
 
-    def _head_desc(self) -> _hip.HeadDesc:
-        tensors = (self.norm.mean, self.norm.var, self.policy.weight, self.policy.bias, self.policy_from.weight,
-                   self.policy_from.bias, self.policy_to.weight, self.policy_to.bias, self.value.weight,
-                   self.value.bias)
+    def _dense_tensors(self):
+        return (self.encoder.weight, self.encoder.bias, self.norm.mean, self.norm.var, self.policy.weight,
+                self.policy.bias, self.policy_from.weight, self.policy_from.bias, self.policy_to.weight,
+                self.policy_to.bias, self.value.weight, self.value.bias)
+
+    def _dense(self, k: int) -> _hip.Handle:
+        """The encoder and head weights split for the matrix cores, rebuilt when any of them changes."""
+        tensors = self._dense_tensors()
+        key = (k,) + tuple((t._version, t.data_ptr()) for t in tensors)
+        cached = getattr(self, "_dense_cache", None)
+        if cached is not None and cached.key == key:
+            return cached
+        self._dense_cache = None
         for t in tensors:
             _hip.require_device(t, "FlyChessNet.forward")
             if t.dtype != torch.float32 or not t.is_contiguous():
-                raise RuntimeError("FlyChessNet.forward: head parameters must be contiguous float32")
-        return _hip.HeadDesc(len(self.out_idx), N_MOVES, *[t.data_ptr() for t in tensors[:2]], float(self.norm.eps),
-                             float(self.norm.clip), *[t.data_ptr() for t in tensors[2:]],
+                raise RuntimeError("FlyChessNet.forward: encoder, head and normaliser tensors must be contiguous float32")
+        enc_w, enc_b = tensors[0], tensors[1]
+        head = _hip.HeadDesc(len(self.out_idx), N_MOVES, self.norm.mean.data_ptr(), self.norm.var.data_ptr(),
+                             float(self.norm.eps), float(self.norm.clip), *[t.data_ptr() for t in tensors[4:]],
                              self.move_from32.data_ptr(), self.move_to32.data_ptr())
+        handle = ctypes.c_void_p()
+        _hip.check(_hip.load().fly_dense_create(ctypes.byref(head), enc_w.data_ptr(), enc_w.stride(0), k,
+                                                enc_b.data_ptr(), enc_w.shape[0], _hip.stream(enc_w.device),
+                                                ctypes.byref(handle)), "fly_dense_create")
+        self._dense_cache = _hip.Handle(handle, "fly_dense_destroy", key)
+        return self._dense_cache
 
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """x: (B, >= N_BASE) -> policy logits (B, N_MOVES), WDL logits (B, 3), both float32."""
@@ -117,25 +134,21 @@ class FlyChessNet(nn.Module):
             x = x.float()
         if x.stride(1) != 1:
             x = x.contiguous()
-        enc_w, enc_b = self.encoder.weight, self.encoder.bias
-        if enc_w.dtype != torch.float32 or not enc_w.is_contiguous():
-            raise RuntimeError("FlyChessNet.forward: encoder weight must be contiguous float32")
         brain = self.brain
         brain._check_params("FlyChessNet.forward")
         cone = brain.light_cone(self.in_idx, self.out_idx, self.cfg.steps)
         mode = _hip.MODE_DEVIATION_F16 if dtype == torch.float16 else _hip.MODE_F32
         plan = brain._cone_plan(cone, mode)
-        head = self._head_desc()
+        dense = self._dense(k)
         batch = x.shape[0]
         logits = torch.empty(batch, N_MOVES, dtype=torch.float32, device=x.device)
         wdl = torch.empty(batch, 3, dtype=torch.float32, device=x.device)
         lib = _hip.load()
-        ws = _hip.workspace(lib.fly_model_workspace(plan.handle, head, batch), x.device)
+        ws = _hip.workspace(lib.fly_model_workspace(plan.handle, dense.handle, batch), x.device)
         ldx = x.stride(0) if batch > 1 else x.shape[1]
-        _hip.check(lib.fly_model_forward(plan.handle, head, x.data_ptr(), ldx, batch, k, enc_w.data_ptr(),
-                                         enc_w.stride(0), enc_b.data_ptr(), float(self.cfg.input_gain),
-                                         logits.data_ptr(), wdl.data_ptr(), ws.data_ptr(), ws.numel(),
-                                         _hip.stream(x.device)), "fly_model_forward")
+        _hip.check(lib.fly_model_forward(plan.handle, dense.handle, x.data_ptr(), ldx, batch,
+                                         float(self.cfg.input_gain), logits.data_ptr(), wdl.data_ptr(), ws.data_ptr(),
+                                         ws.numel(), _hip.stream(x.device)), "fly_model_forward")
         return logits, wdl
 
     @staticmethod

@@ -130,6 +130,7 @@ class LaunchTimer {
 struct Tuning {
   int vec = 0;    // elements per lane of the step kernel, 0 = automatic
   int tiles = 0;  // batch tiles swept row-major, 0 = automatic
+  int unroll = 0; // non-zeros gathered per wave per iteration (8, 16, 32), 0 = automatic
 };
 Tuning &tuning();
 

@@ -1,15 +1,24 @@
 // Dense maps of the network on the matrix cores, and the whole-model forward.
 //
-//   encoder  u[m, b] = cast((sum_k W[m, k] x[b, k] + bias[m]) * gain)        chessfly/model.py:99-102
+//   encoder  u[m, b] = (sum_k W[m, k] x[b, k] + bias[m]) * gain              chessfly/model.py:99-102
 //   head     r[b, j] = clamp((c_base[j] + X_T[src_j, b] - mean_j) / sqrt(var_j + eps), -clip, clip)
 //            logits[b, i] = (P r + bp)[i] + (F r + bf)[from_i] + (T r + bt)[to_i],  wdl = V r + bv
 //                                                                            chessfly/model.py:51-58, 103-105
-// The GEMM is C = A B^T with A row-major (the weight) and B produced by a loader functor, on 64x64
-// output tiles of 4 waves (2x2 waves of 32x32, each 2x2 v_mfma_f32_16x16x4f32 tiles), K staged 16 at a
-// time through LDS.  float32 matrix cores keep the dense maps float32-exact in their products.  The head's
-// B loader reads the final recurrent state in place, so the output gather, the transpose to (B, n_out) and
-// the normaliser never touch HBM as separate passes.
+// float32 accuracy on fp16 matrix cores: every operand is split into hi = fp16(v) and lo = fp16(v - hi) (22
+// significant bits together) and C = A_hi B_hi + A_hi B_lo + A_lo B_hi is accumulated in float32 with
+// v_mfma_f32_16x16x32_f16 (the dropped A_lo B_lo term is below float32 round-off).  Weights are scaled by a
+// power of two before the split so their low parts stay clear of fp16 subnormals; the scale is undone
+// exactly on the accumulator.  The weights are split once per weight version into a dense plan (fly_dense);
+// the boards and the normalised outputs are split per forward by small prologue kernels, the latter reading
+// the final recurrent state in place (output gather, normaliser and transpose in one pass).
+//
+// GEMM tiling: C = A B^T with both operands K-contiguous (K padded to 32 with zeros), 64x64 output tiles per
+// workgroup of 4 waves (2x2 waves of 32x32, each 2x2 MFMA 16x16 tiles), K staged 32 at a time through LDS
+// as hi/lo halves, 16-byte global loads and 16-byte LDS fragment reads.
 #include "common.hpp"
+
+#include <cmath>
+#include <cstring>
 
 namespace fly {
 
@@ -19,125 +28,146 @@ template <typename S, typename U>
 const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st);
 void check_plan_device(const fly_plan *plan);
 
+}  // namespace fly
+
+struct fly_dense {
+  int device = -1;
+  int64_t n_in = 0, k = 0, kp_enc = 0;            // encoder: n_in rows over k feature columns (padded to kp_enc)
+  int64_t n_out = 0, n_moves = 0, kp_head = 0;    // head: n_moves + 131 rows over n_out outputs
+  fly::DevArray<_Float16> enc_hi, enc_lo, head_hi, head_lo;
+  fly::DevArray<float> enc_b, head_b, norm_mean, norm_var;
+  fly::DevArray<int32_t> move_from, move_to;
+  float enc_unscale = 1.f, head_unscale = 1.f, eps = 1e-8f, clip = 8.f;
+  int64_t head_rows() const { return n_moves + 131; }
+};
+
+namespace fly {
 namespace {
 
-typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 64, BN = 64, BK = 16, PAD = 4;
-typedef float TileA[BK][BM + PAD];
-typedef float TileB[BK][BN + PAD];
+constexpr int GBM = 64, GBN = 64, GBK = 32, LDK = GBK + 8;  // LDS rows padded to 80 bytes
 
-// A: row-major weight (M, ld), columns [0, K) used.
-struct RowMajorA {
-  const float *w;
-  int64_t ld;
-  __device__ __forceinline__ void tile(TileA &s, int64_t m0, int64_t k0, int64_t M, int64_t K, int tid) const {
-    const int m = tid >> 2, kq = (tid & 3) * 4;
-    const int64_t gm = m0 + m;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t k = k0 + kq + i;
-      s[kq + i][m] = (gm < M && k < K) ? w[gm * ld + k] : 0.0f;
-    }
-  }
-};
+int64_t pad_k(int64_t k) { return round_up(std::max<int64_t>(k, 1), GBK); }
 
-// B for the encoder: boards x (N, ld), B[n, k] = x[n, k].
-struct BoardsB {
-  const float *x;
-  int64_t ld;
-  __device__ __forceinline__ void tile(TileB &s, int64_t n0, int64_t k0, int64_t N, int64_t K, int tid) const {
-    const int n = tid >> 2, kq = (tid & 3) * 4;
-    const int64_t gn = n0 + n;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t k = k0 + kq + i;
-      s[kq + i][n] = (gn < N && k < K) ? x[gn * ld + k] : 0.0f;
-    }
-  }
-};
+// hi = fp16(v * scale), lo = fp16(v * scale - hi), rows x kp, zero beyond k.
+__global__ void k_split_rows(const float *__restrict__ src, int64_t ld, int64_t rows, int64_t k, float scale,
+                             _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, int64_t kp) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= rows * kp) return;
+  const int64_t r = i / kp, c = i - r * kp;
+  const float v = c < k ? src[r * ld + c] * scale : 0.0f;
+  const _Float16 h = static_cast<_Float16>(v);
+  hi[i] = h;
+  lo[i] = static_cast<_Float16>(v - static_cast<float>(h));
+}
 
-// B for the head: the normalised output activity r[n, k] read from the state (rows, lds) in place.
+// Normalised outputs r[n, k] split into (N x kp) hi/lo rows, read from the state (rows, lds) where output k
+// sits at row src[k] (-1: not carried; src null: row k), plus cbase[k] (null: 0).  A 64x64 tile goes through
+// LDS so both the state reads (n fastest) and the split writes (k fastest) are contiguous.
 template <typename S>
-struct NormalisedOutputsB {
-  const S *state;        // null: no carried state
-  int64_t lds;
-  const int32_t *src;    // row of output k in the state (-1: none); null: row k
-  const float *cbase;    // added to the state value; null: 0
-  const float *mean, *var;
-  float eps, clip;
-  __device__ __forceinline__ void tile(TileB &s, int64_t n0, int64_t k0, int64_t N, int64_t K, int tid) const {
-    const int k = tid >> 4, nq = (tid & 15) * 4;
-    const int64_t gk = k0 + k;
-    if (gk >= K) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[k][nq + i] = 0.0f;
-      return;
+__global__ __launch_bounds__(256) void k_norm_split(const S *__restrict__ state, int64_t lds, const int32_t *__restrict__ src,
+                                                    const float *__restrict__ cbase, const float *__restrict__ mean,
+                                                    const float *__restrict__ var, float eps, float clip, int64_t K,
+                                                    int64_t N, _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                                                    int64_t kp) {
+  __shared__ float tile[64][65];
+  const int64_t k0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int kk = ty; kk < 64; kk += 4) {
+    const int64_t k = k0 + kk, n = n0 + tx;
+    float v = 0.0f;
+    if (k < K && n < N) {
+      const int32_t row = src ? src[k] : (int32_t)k;
+      const float r = (cbase ? cbase[k] : 0.0f) +
+                      ((state != nullptr && row >= 0) ? static_cast<float>(state[(int64_t)row * lds + n]) : 0.0f);
+      v = fminf(fmaxf((r - mean[k]) / sqrtf(var[k] + eps), -clip), clip);
     }
-    const int32_t row = src ? src[gk] : (int32_t)gk;
-    const float base = cbase ? cbase[gk] : 0.0f;
-    const float mu = mean[gk];
-    const float sd = sqrtf(var[gk] + eps);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t n = n0 + nq + i;
-      float v = 0.0f;
-      if (n < N) {
-        const float r = base + ((state != nullptr && row >= 0) ? static_cast<float>(state[(int64_t)row * lds + n]) : 0.0f);
-        v = fminf(fmaxf((r - mu) / sd, -clip), clip);
-      }
-      s[k][nq + i] = v;
+    tile[kk][tx] = v;
+  }
+  __syncthreads();
+  for (int nn = ty; nn < 64; nn += 4) {
+    const int64_t n = n0 + nn, k = k0 + tx;
+    if (n < N && k < kp) {
+      const float v = tile[tx][nn];
+      const _Float16 h = static_cast<_Float16>(v);
+      hi[n * kp + k] = h;
+      lo[n * kp + k] = static_cast<_Float16>(v - static_cast<float>(h));
     }
   }
+}
+
+struct Split {
+  const _Float16 *hi, *lo;
+  int64_t rows;  // leading dimension is the padded K
 };
 
-template <typename S>
 struct EncoderEpilogue {
   const float *bias;
   float gain;
-  S *u;
+  float *u;
+  _Float16 *u16;
   int64_t ldu;
   __device__ __forceinline__ void operator()(int64_t m, int64_t n, float v) const {
-    u[m * ldu + n] = static_cast<S>((v + bias[m]) * gain);
+    const float x = (v + bias[m]) * gain;
+    if (u16) u16[m * ldu + n] = static_cast<_Float16>(x);
+    else u[m * ldu + n] = x;
   }
 };
 
-// C^T rows: ct[n, moff + m] = C[m, n] (one row of all head outputs per board).
+// ct[n, m] = C[m, n]: one row of all head outputs per board.
 struct HeadEpilogue {
   float *ct;
-  int64_t ldc, moff;
-  __device__ __forceinline__ void operator()(int64_t m, int64_t n, float v) const { ct[n * ldc + moff + m] = v; }
+  int64_t ldc;
+  __device__ __forceinline__ void operator()(int64_t m, int64_t n, float v) const { ct[n * ldc + m] = v; }
 };
 
-template <class AL, class BL, class EP>
-__global__ __launch_bounds__(256) void k_gemm(int64_t M, int64_t N, int64_t K, const AL A, const BL B, const EP ep) {
-  __shared__ TileA As;
-  __shared__ TileB Bs;
+__device__ __forceinline__ half8 load8(const _Float16 *p) { return *reinterpret_cast<const half8 *>(p); }
+
+template <class EP>
+__global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B, int64_t kp, float unscale, const EP ep) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][GBM][LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][GBN][LDK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-  v4f acc[2][2];
+  const int64_t m0 = (int64_t)blockIdx.y * GBM, n0 = (int64_t)blockIdx.x * GBN;
+  const int lr = tid >> 2, lk = (tid & 3) * 8;  // this thread's 16-byte piece of a 64x32 tile
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  floatx4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int64_t k0 = 0; k0 < K; k0 += BK) {
-    A.tile(As, m0, k0, M, K, tid);
-    B.tile(Bs, n0, k0, N, K, tid);
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const bool a_ok = m0 + lr < A.rows, b_ok = n0 + lr < B.rows;
+  const int64_t arow = a_ok ? m0 + lr : 0, brow = b_ok ? n0 + lr : 0;
+  const _Float16 *ah = A.hi + arow * kp + lk, *al = A.lo + arow * kp + lk;
+  const _Float16 *bh = B.hi + brow * kp + lk, *bl = B.lo + brow * kp + lk;
+  for (int64_t k0 = 0; k0 < kp; k0 += GBK) {
+    const half8 vah = a_ok ? load8(ah + k0) : zero, val = a_ok ? load8(al + k0) : zero;
+    const half8 vbh = b_ok ? load8(bh + k0) : zero, vbl = b_ok ? load8(bl + k0) : zero;
+    *reinterpret_cast<half8 *>(&As[0][lr][lk]) = vah;
+    *reinterpret_cast<half8 *>(&As[1][lr][lk]) = val;
+    *reinterpret_cast<half8 *>(&Bs[0][lr][lk]) = vbh;
+    *reinterpret_cast<half8 *>(&Bs[1][lr][lk]) = vbl;
     __syncthreads();
+    const int fk = 8 * (lane >> 4), fr = lane & 15;
+    half8 a_hi[2], a_lo[2], b_hi[2], b_lo[2];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 4) {
-      const int kr = kk + (lane >> 4);
-      float a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = As[kr][wm * 32 + i * 16 + (lane & 15)];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = Bs[kr][wn * 32 + j * 16 + (lane & 15)];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+      a_hi[i] = *reinterpret_cast<const half8 *>(&As[0][wm * 32 + i * 16 + fr][fk]);
+      a_lo[i] = *reinterpret_cast<const half8 *>(&As[1][wm * 32 + i * 16 + fr][fk]);
+      b_hi[i] = *reinterpret_cast<const half8 *>(&Bs[0][wn * 32 + i * 16 + fr][fk]);
+      b_lo[i] = *reinterpret_cast<const half8 *>(&Bs[1][wn * 32 + i * 16 + fr][fk]);
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[i], b_hi[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[i], b_lo[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[i], b_hi[j], acc[i][j], 0, 0, 0);
+      }
     __syncthreads();
   }
 #pragma unroll
@@ -148,150 +178,277 @@ __global__ __launch_bounds__(256) void k_gemm(int64_t M, int64_t N, int64_t K, c
       for (int r = 0; r < 4; ++r) {
         const int64_t m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
         const int64_t n = n0 + wn * 32 + j * 16 + (lane & 15);
-        if (m < M && n < N) ep(m, n, acc[i][j][r]);
+        if (m < A.rows && n < B.rows) ep(m, n, acc[i][j][r] * unscale);
       }
 }
 
-template <class AL, class BL, class EP>
-void gemm(int64_t M, int64_t N, int64_t K, const AL &A, const BL &B, const EP &ep, hipStream_t st) {
-  if (M == 0 || N == 0) return;
-  const int64_t gy = (M + BM - 1) / BM, gx = (N + BN - 1) / BN;
+template <class EP>
+void gemm_split(const Split &A, const Split &B, int64_t kp, float unscale, const EP &ep, hipStream_t st) {
+  if (A.rows == 0 || B.rows == 0) return;
+  const int64_t gy = (A.rows + GBM - 1) / GBM, gx = (B.rows + GBN - 1) / GBN;
   FLY_REQUIRE(gy < 65536 && gx < INT32_MAX, "GEMM grid too large");
-  hipLaunchKernelGGL((k_gemm<AL, BL, EP>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, st, M, N, K, A, B, ep);
-  check_launch("gemm");
+  hipLaunchKernelGGL((k_gemm_split<EP>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, st, A, B, kp, unscale, ep);
+  check_launch("split gemm");
 }
 
-// logits[n, i] = (ct[n, i] + bp[i]) + (ct[n, M + f] + bf[f]) + (ct[n, M + 64 + t] + bt[t]); wdl from the last 3.
-__global__ void k_assemble(const float *__restrict__ ct, int64_t ldc, int64_t n_moves, const float *__restrict__ bp,
-                           const float *__restrict__ bf, const float *__restrict__ bt, const float *__restrict__ bv,
+// logits[n, i] = (ct[n, i] + b[i]) + (ct[n, M + f] + b[M + f]) + (ct[n, M + 64 + t] + b[M + 64 + t]),
+// wdl[n, j] = ct[n, M + 128 + j] + b[M + 128 + j], with M = n_moves and (f, t) the move's squares.
+__global__ void k_assemble(const float *__restrict__ ct, int64_t ldc, int64_t n_moves, const float *__restrict__ b,
                            const int32_t *__restrict__ mfrom, const int32_t *__restrict__ mto, int64_t batch,
                            float *__restrict__ logits, float *__restrict__ wdl) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   for (int64_t n = blockIdx.y; n < batch; n += gridDim.y) {
     const float *row = ct + n * ldc;
     if (i < n_moves) {
-      const int32_t f = min(max(mfrom[i], 0), 63), t = min(max(mto[i], 0), 63);  // squares are 0..63
-      logits[n * n_moves + i] = ((row[i] + bp[i]) + (row[n_moves + f] + bf[f])) + (row[n_moves + 64 + t] + bt[t]);
+      const int64_t f = n_moves + mfrom[i], t = n_moves + 64 + mto[i];
+      logits[n * n_moves + i] = ((row[i] + b[i]) + (row[f] + b[f])) + (row[t] + b[t]);
     }
-    if (i < 3) wdl[n * 3 + i] = row[n_moves + 128 + i] + bv[i];
+    if (i < 3) wdl[n * 3 + i] = row[n_moves + 128 + i] + b[n_moves + 128 + i];
   }
 }
 
-int64_t head_ld(const fly_head_desc &h) { return round_up(h.n_moves + 131, 4); }
-
-size_t head_ws(const fly_head_desc &h, int64_t batch) { return (size_t)batch * head_ld(h) * sizeof(float) + 256; }
-
-void check_head(const fly_head_desc *h) {
-  FLY_REQUIRE(h != nullptr, "head is null");
-  FLY_REQUIRE(h->n_out > 0 && h->n_moves > 0, "empty head");
-  FLY_REQUIRE(h->norm_mean && h->norm_var && h->policy_w && h->policy_b && h->from_w && h->from_b && h->to_w &&
-                  h->to_b && h->value_w && h->value_b && h->move_from && h->move_to,
-              "head has a null pointer");
+__global__ void k_max_abs(const float *__restrict__ w, int64_t ld, int64_t rows, int64_t k, unsigned *__restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= rows * k) return;
+  const int64_t r = i / k, c = i - r * k;
+  const float a = fabsf(w[r * ld + c]);
+  if (a > 0.0f) atomicMax(out, __float_as_uint(a));   // non-negative floats order like their bit patterns
 }
 
-template <typename S>
-void run_head(const fly_head_desc &h, const NormalisedOutputsB<S> &B, int64_t batch, float *ct, float *logits,
-              float *wdl, hipStream_t st) {
-  const int64_t ldc = head_ld(h), K = h.n_out;
-  LaunchTimer timer(FLY_K_HEAD, st);
-  gemm(h.n_moves, batch, K, RowMajorA{h.policy_w, K}, B, HeadEpilogue{ct, ldc, 0}, st);
-  gemm(64, batch, K, RowMajorA{h.from_w, K}, B, HeadEpilogue{ct, ldc, h.n_moves}, st);
-  gemm(64, batch, K, RowMajorA{h.to_w, K}, B, HeadEpilogue{ct, ldc, h.n_moves + 64}, st);
-  gemm(3, batch, K, RowMajorA{h.value_w, K}, B, HeadEpilogue{ct, ldc, h.n_moves + 128}, st);
-  const dim3 grid(blocks_for(h.n_moves, 256), (unsigned)std::min<int64_t>(batch, 65535));
-  hipLaunchKernelGGL(k_assemble, grid, dim3(256), 0, st, ct, ldc, h.n_moves, h.policy_b, h.from_b, h.to_b, h.value_b,
-                     h.move_from, h.move_to, batch, logits, wdl);
-  check_launch("head assembly");
+__global__ void k_check_squares(const int32_t *__restrict__ sq, int64_t n, int32_t *__restrict__ bad) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n && (sq[i] < 0 || sq[i] > 63)) atomicOr(bad, 1);
 }
 
-template <typename S>
-void run_encoder(const float *x, int64_t ldx, int64_t batch, int64_t k, const float *w, int64_t ldw, const float *b,
-                 int64_t n_in, float gain, S *u, int64_t ldu, hipStream_t st) {
-  LaunchTimer timer(FLY_K_ENCODER, st);
-  gemm(n_in, batch, k, RowMajorA{w, ldw}, BoardsB{x, ldx}, EncoderEpilogue<S>{b, gain, u, ldu}, st);
+__global__ void k_zero_u32(unsigned *__restrict__ p) { *p = 0u; }
+
+constexpr int kThreads = 256;
+
+// Power-of-two scale that puts the largest |w| at 2^14 (low halves stay normal fp16 for every weight that
+// matters); 1 for an all-zero matrix.
+float weight_scale(const float *w, int64_t ld, int64_t rows, int64_t k, hipStream_t st) {
+  if (rows * k == 0) return 1.0f;
+  DevArray<unsigned> mx(1);
+  hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(1), 0, st, mx.p);
+  hipLaunchKernelGGL(k_max_abs, dim3(blocks_for(rows * k, kThreads)), dim3(kThreads), 0, st, w, ld, rows, k, mx.p);
+  check_launch("max abs");
+  unsigned bits = 0;
+  FLY_HIP(hipMemcpyAsync(&bits, mx.p, sizeof(bits), hipMemcpyDeviceToHost, st));
+  FLY_HIP(hipStreamSynchronize(st));
+  float m;
+  memcpy(&m, &bits, sizeof(m));
+  FLY_REQUIRE(std::isfinite(m), "dense weights hold a non-finite value");
+  if (m == 0.0f) return 1.0f;
+  const int e = std::max(-24, std::min(24, 14 - (int)std::ceil(std::log2(m))));
+  return std::ldexp(1.0f, e);
+}
+
+void split_into(const float *w, int64_t ld, int64_t rows, int64_t k, float scale, _Float16 *hi, _Float16 *lo,
+                int64_t kp, hipStream_t st) {
+  if (rows == 0) return;
+  hipLaunchKernelGGL(k_split_rows, dim3(blocks_for(rows * kp, kThreads)), dim3(kThreads), 0, st, w, ld, rows, k, scale,
+                     hi, lo, kp);
+  check_launch("split");
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+int64_t head_ld(const fly_dense &d) { return round_up(d.head_rows(), 4); }
+
+size_t split_bytes(int64_t rows, int64_t kp) { return align256((size_t)rows * kp * sizeof(_Float16)); }
+
+size_t encoder_ws(const fly_dense &d, int64_t batch) { return 2 * split_bytes(batch, d.kp_enc); }
+
+size_t head_ws(const fly_dense &d, int64_t batch) {
+  return 2 * split_bytes(batch, d.kp_head) + align256((size_t)batch * head_ld(d) * sizeof(float));
+}
+
+void run_encoder(const fly_dense &d, const float *x, int64_t ldx, int64_t batch, float gain, float *u, _Float16 *u16,
+                 int64_t ldu, void *ws, hipStream_t st) {
+  LaunchTimer timer(FLY_K_ENCODER, st);
+  _Float16 *xh = static_cast<_Float16 *>(ws);
+  _Float16 *xl = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + split_bytes(batch, d.kp_enc));
+  split_into(x, ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st);
+  gemm_split(Split{d.enc_hi.p, d.enc_lo.p, d.n_in}, Split{xh, xl, batch}, d.kp_enc, d.enc_unscale,
+             EncoderEpilogue{d.enc_b.p, gain, u, u16, ldu}, st);
+}
+
+template <typename S>
+void run_head(const fly_dense &d, const S *state, int64_t lds, const int32_t *src, const float *cbase, int64_t batch,
+              float *logits, float *wdl, void *ws, hipStream_t st) {
+  LaunchTimer timer(FLY_K_HEAD, st);
+  char *base = static_cast<char *>(ws);
+  _Float16 *rh = reinterpret_cast<_Float16 *>(base);
+  _Float16 *rl = reinterpret_cast<_Float16 *>(base + split_bytes(batch, d.kp_head));
+  float *ct = reinterpret_cast<float *>(base + 2 * split_bytes(batch, d.kp_head));
+  const dim3 grid(blocks_for(batch, 64), (unsigned)((d.kp_head + 63) / 64));
+  hipLaunchKernelGGL(k_norm_split<S>, grid, dim3(256), 0, st, state, lds, src, cbase, d.norm_mean.p, d.norm_var.p, d.eps,
+                     d.clip, d.n_out, batch, rh, rl, d.kp_head);
+  check_launch("normalised outputs");
+  const int64_t ldc = head_ld(d);
+  gemm_split(Split{d.head_hi.p, d.head_lo.p, d.head_rows()}, Split{rh, rl, batch}, d.kp_head, d.head_unscale,
+             HeadEpilogue{ct, ldc}, st);
+  const dim3 agrid(blocks_for(d.n_moves, 256), (unsigned)std::min<int64_t>(batch, 65535));
+  hipLaunchKernelGGL(k_assemble, agrid, dim3(256), 0, st, ct, ldc, d.n_moves, d.head_b.p, d.move_from.p, d.move_to.p,
+                     batch, logits, wdl);
+  check_launch("head assembly");
+}
+
+void check_dense(const fly_dense *d) {
+  FLY_REQUIRE(d != nullptr, "dense plan is null");
+  FLY_REQUIRE(current_device() == d->device, "the dense plan lives on another device");
+}
 
 }  // namespace
 }  // namespace fly
 
 using namespace fly;
 
-extern "C" int fly_encoder(const float *x, int64_t ldx, int64_t batch, int64_t k, const float *w, int64_t ldw,
-                           const float *b, int64_t n_in, float gain, void *u, int64_t ldu, int32_t out_f16,
-                           void *stream) {
+extern "C" int fly_dense_create(const fly_head_desc *h, const float *enc_w, int64_t ldw, int64_t k,
+                                const float *enc_b, int64_t n_in, void *stream, fly_dense **out) {
   return guard([&] {
-    FLY_REQUIRE(batch >= 0 && n_in >= 0 && k >= 0, "negative size");
-    if (!batch || !n_in) return;
-    FLY_REQUIRE(x && w && b && u, "null argument");
-    FLY_REQUIRE(ldx >= k && ldw >= k && ldu >= batch, "leading dimension too small");
-    if (out_f16)
-      run_encoder<_Float16>(x, ldx, batch, k, w, ldw, b, n_in, gain, static_cast<_Float16 *>(u), ldu, as_stream(stream));
-    else
-      run_encoder<float>(x, ldx, batch, k, w, ldw, b, n_in, gain, static_cast<float *>(u), ldu, as_stream(stream));
+    FLY_REQUIRE(out != nullptr, "out is null");
+    *out = nullptr;
+    FLY_REQUIRE(h != nullptr, "head is null");
+    FLY_REQUIRE(h->n_out > 0 && h->n_moves > 0 && n_in >= 0 && k >= 0 && ldw >= k, "bad size");
+    FLY_REQUIRE(h->norm_mean && h->norm_var && h->policy_w && h->policy_b && h->from_w && h->from_b && h->to_w &&
+                    h->to_b && h->value_w && h->value_b && h->move_from && h->move_to,
+                "head has a null pointer");
+    FLY_REQUIRE(n_in == 0 || (enc_w && enc_b), "encoder has a null pointer");
+    hipStream_t st = as_stream(stream);
+    auto d = std::make_unique<fly_dense>();
+    d->device = current_device();
+    d->n_in = n_in;
+    d->k = k;
+    d->kp_enc = pad_k(k);
+    d->n_out = h->n_out;
+    d->n_moves = h->n_moves;
+    d->kp_head = pad_k(h->n_out);
+    d->eps = h->norm_eps;
+    d->clip = h->norm_clip;
+    {  // move squares must index the 64 from/to rows
+      DevArray<int32_t> bad(1);
+      hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(1), 0, st, reinterpret_cast<unsigned *>(bad.p));
+      hipLaunchKernelGGL(k_check_squares, dim3(blocks_for(h->n_moves, kThreads)), dim3(kThreads), 0, st, h->move_from,
+                         h->n_moves, bad.p);
+      hipLaunchKernelGGL(k_check_squares, dim3(blocks_for(h->n_moves, kThreads)), dim3(kThreads), 0, st, h->move_to,
+                         h->n_moves, bad.p);
+      check_launch("square check");
+      int32_t hb = 0;
+      FLY_HIP(hipMemcpyAsync(&hb, bad.p, sizeof(hb), hipMemcpyDeviceToHost, st));
+      FLY_HIP(hipStreamSynchronize(st));
+      FLY_REQUIRE(hb == 0, "move_from / move_to hold a square outside 0..63");
+    }
+    // encoder
+    const float es = weight_scale(enc_w, ldw, n_in, k, st);
+    d->enc_unscale = 1.0f / es;
+    d->enc_hi.alloc(n_in * d->kp_enc);
+    d->enc_lo.alloc(n_in * d->kp_enc);
+    split_into(enc_w, ldw, n_in, k, es, d->enc_hi.p, d->enc_lo.p, d->kp_enc, st);
+    d->enc_b.alloc(n_in);
+    if (n_in) FLY_HIP(hipMemcpyAsync(d->enc_b.p, enc_b, sizeof(float) * n_in, hipMemcpyDeviceToDevice, st));
+    // head: policy, from, to and value rows stacked under one scale
+    const int64_t K = h->n_out, M = h->n_moves;
+    struct Part {
+      const float *w, *b;
+      int64_t rows, off;
+    } parts[4] = {{h->policy_w, h->policy_b, M, 0}, {h->from_w, h->from_b, 64, M}, {h->to_w, h->to_b, 64, M + 64},
+                  {h->value_w, h->value_b, 3, M + 128}};
+    float hs = 0.0f;
+    for (const Part &p : parts) {
+      const float s = weight_scale(p.w, K, p.rows, K, st);
+      hs = (hs == 0.0f) ? s : std::min(hs, s);
+    }
+    d->head_unscale = 1.0f / hs;
+    d->head_hi.alloc(d->head_rows() * d->kp_head);
+    d->head_lo.alloc(d->head_rows() * d->kp_head);
+    d->head_b.alloc(d->head_rows());
+    for (const Part &p : parts) {
+      split_into(p.w, K, p.rows, K, hs, d->head_hi.p + p.off * d->kp_head, d->head_lo.p + p.off * d->kp_head,
+                 d->kp_head, st);
+      FLY_HIP(hipMemcpyAsync(d->head_b.p + p.off, p.b, sizeof(float) * p.rows, hipMemcpyDeviceToDevice, st));
+    }
+    d->move_from.alloc(M);
+    d->move_to.alloc(M);
+    FLY_HIP(hipMemcpyAsync(d->move_from.p, h->move_from, sizeof(int32_t) * M, hipMemcpyDeviceToDevice, st));
+    FLY_HIP(hipMemcpyAsync(d->move_to.p, h->move_to, sizeof(int32_t) * M, hipMemcpyDeviceToDevice, st));
+    d->norm_mean.alloc(K);
+    d->norm_var.alloc(K);
+    FLY_HIP(hipMemcpyAsync(d->norm_mean.p, h->norm_mean, sizeof(float) * K, hipMemcpyDeviceToDevice, st));
+    FLY_HIP(hipMemcpyAsync(d->norm_var.p, h->norm_var, sizeof(float) * K, hipMemcpyDeviceToDevice, st));
+    FLY_HIP(hipStreamSynchronize(st));
+    *out = d.release();
   });
 }
 
-extern "C" size_t fly_head_workspace(const fly_head_desc *head, int64_t batch) {
-  return head ? head_ws(*head, batch) : 0;
+extern "C" int fly_dense_destroy(fly_dense *d) {
+  return guard([&] { delete d; });
 }
 
-extern "C" int fly_head(const fly_head_desc *head, const float *r, int64_t ldr, int64_t batch, float *logits,
-                        float *wdl, void *ws, size_t ws_bytes, void *stream) {
+extern "C" size_t fly_encoder_workspace(const fly_dense *d, int64_t batch) { return d ? encoder_ws(*d, batch) : 0; }
+
+extern "C" int fly_encoder(const fly_dense *d, const float *x, int64_t ldx, int64_t batch, float gain, void *u,
+                           int64_t ldu, int32_t out_f16, void *ws, size_t ws_bytes, void *stream) {
   return guard([&] {
-    check_head(head);
+    check_dense(d);
+    FLY_REQUIRE(batch >= 0, "negative batch");
+    if (!batch || !d->n_in) return;
+    FLY_REQUIRE(x && u && ldx >= d->k && ldu >= batch, "bad argument");
+    FLY_REQUIRE(ws && ws_bytes >= encoder_ws(*d, batch) && aligned(ws, 256), "workspace too small or misaligned");
+    run_encoder(*d, x, ldx, batch, gain, out_f16 ? nullptr : static_cast<float *>(u),
+                out_f16 ? static_cast<_Float16 *>(u) : nullptr, ldu, ws, as_stream(stream));
+  });
+}
+
+extern "C" size_t fly_head_workspace(const fly_dense *d, int64_t batch) { return d ? head_ws(*d, batch) : 0; }
+
+extern "C" int fly_head(const fly_dense *d, const float *r, int64_t ldr, int64_t batch, float *logits, float *wdl,
+                        void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] {
+    check_dense(d);
     FLY_REQUIRE(batch >= 0, "negative batch");
     if (!batch) return;
     FLY_REQUIRE(r && ldr >= batch && logits && wdl, "bad argument");
-    FLY_REQUIRE(ws && ws_bytes >= head_ws(*head, batch), "workspace too small");
-    NormalisedOutputsB<float> B{r, ldr, nullptr, nullptr, head->norm_mean, head->norm_var, head->norm_eps, head->norm_clip};
-    run_head<float>(*head, B, batch, static_cast<float *>(ws), logits, wdl, as_stream(stream));
+    FLY_REQUIRE(ws && ws_bytes >= head_ws(*d, batch) && aligned(ws, 256), "workspace too small or misaligned");
+    run_head<float>(*d, r, ldr, nullptr, nullptr, batch, logits, wdl, ws, as_stream(stream));
   });
 }
 
-extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_head_desc *head, int64_t batch) {
-  if (!plan || !head) return 0;
+extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_dense *d, int64_t batch) {
+  if (!plan || !d) return 0;
   return align256((size_t)plan->n_in * state_ld(batch) * sizeof(float)) + align256(io_workspace(*plan, batch)) +
-         align256(head_ws(*head, batch));
+         std::max(encoder_ws(*d, batch), head_ws(*d, batch));
 }
 
-extern "C" int fly_model_forward(const fly_plan *plan, const fly_head_desc *head, const float *x, int64_t ldx,
-                                 int64_t batch, int64_t k, const float *enc_w, int64_t ldw, const float *enc_b,
+extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const float *x, int64_t ldx, int64_t batch,
                                  float input_gain, float *logits, float *wdl, void *ws, size_t ws_bytes, void *stream) {
   return guard([&] {
     check_plan_device(plan);
-    check_head(head);
+    check_dense(d);
     FLY_REQUIRE(!plan->full, "the model forward needs a light-cone plan");
-    FLY_REQUIRE(head->n_out == plan->n_out, "head and plan disagree on the number of outputs");
+    FLY_REQUIRE(d->n_out == plan->n_out && d->n_in == plan->n_in, "dense maps and plan disagree on sizes");
     FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
     if (!batch) return;
-    FLY_REQUIRE(x && ldx >= k && logits && wdl, "bad argument");
-    FLY_REQUIRE(plan->n_in == 0 || (enc_w && enc_b && ldw >= k), "bad encoder");
-    FLY_REQUIRE(ws && ws_bytes >= fly_model_workspace(plan, head, batch), "workspace too small");
+    FLY_REQUIRE(x && ldx >= d->k && logits && wdl, "bad argument");
+    FLY_REQUIRE(ws && ws_bytes >= fly_model_workspace(plan, d, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     hipStream_t st = as_stream(stream);
     const int64_t ldu = state_ld(batch);
-    const bool dev = plan->mode == FLY_MODE_DEVIATION_F16;
     char *base = static_cast<char *>(ws);
-    void *u = base;
+    float *u = reinterpret_cast<float *>(base);
     base += align256((size_t)plan->n_in * ldu * sizeof(float));
     void *states = base;
     base += align256(io_workspace(*plan, batch));
-    float *ct = reinterpret_cast<float *>(base);
+    void *scratch = base;  // the encoder's operand split, then the head's
     const int64_t lds = state_ld(batch);
     // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
-    run_encoder<float>(x, ldx, batch, k, enc_w, ldw, enc_b, plan->n_in, input_gain, static_cast<float *>(u), ldu, st);
-    if (dev) {
-      const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, static_cast<float *>(u), ldu, batch, states, st);
-      NormalisedOutputsB<_Float16> B{fin, lds, plan->out_src.p, plan->cbase.p, head->norm_mean, head->norm_var,
-                                     head->norm_eps, head->norm_clip};
-      run_head<_Float16>(*head, B, batch, ct, logits, wdl, st);
+    run_encoder(*d, x, ldx, batch, input_gain, u, nullptr, ldu, scratch, st);
+    if (plan->mode == FLY_MODE_DEVIATION_F16) {
+      const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, batch, states, st);
+      run_head<_Float16>(*d, fin, lds, plan->out_src.p, plan->cbase.p, batch, logits, wdl, scratch, st);
     } else {
-      const float *fin = run_cone_steps<float, float>(*plan, static_cast<float *>(u), ldu, batch, states, st);
-      NormalisedOutputsB<float> B{fin, lds, plan->out_src.p, plan->cbase.p, head->norm_mean, head->norm_var,
-                                  head->norm_eps, head->norm_clip};
-      run_head<float>(*head, B, batch, ct, logits, wdl, st);
+      const float *fin = run_cone_steps<float, float>(*plan, u, ldu, batch, states, st);
+      run_head<float>(*d, fin, lds, plan->out_src.p, plan->cbase.p, batch, logits, wdl, scratch, st);
     }
   });
 }

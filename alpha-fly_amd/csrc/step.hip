@@ -70,7 +70,7 @@ struct StepArgs {
   int32_t u_vec;           // the drive can be read with V-wide loads
 };
 
-template <typename S, typename U, int V, bool TORCH_LERP>
+template <typename S, typename U, int V, int UNROLL, bool TORCH_LERP>
 __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   const int lane = threadIdx.x & 63;
   const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -93,15 +93,15 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
     const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
     const S *base = a.xprev + lcol;
     int32_t e = beg;
-    for (; e + 8 <= end; e += 8) {
-      int2 cv[8];
+    for (; e + UNROLL <= end; e += UNROLL) {
+      int2 cv[UNROLL];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cv[j] = a.colval[e + j];
-      float xv[8][V];
+      for (int j = 0; j < UNROLL; ++j) cv[j] = a.colval[e + j];
+      float xv[UNROLL][V];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
+      for (int j = 0; j < UNROLL; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < UNROLL; ++j) {
         const float w = __int_as_float(cv[j].y);
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = fmaf(w, xv[j][i], acc[i]);
@@ -150,13 +150,18 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
 // Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
 // with torch.lerp's formula, like the reference's CPU path.
 template <typename S, typename U, int V>
-void launch_v(const StepArgs<S, U> &a, hipStream_t st) {
+void launch_v(const StepArgs<S, U> &a, int unroll, hipStream_t st) {
   const int64_t waves = (int64_t)a.nrows * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
   constexpr bool kTorchLerp = sizeof(S) == 4;
-  hipLaunchKernelGGL((k_state_step<S, U, V, kTorchLerp>), grid, block, 0, st, a);
+  if (unroll >= 32)
+    hipLaunchKernelGGL((k_state_step<S, U, V, 32, kTorchLerp>), grid, block, 0, st, a);
+  else if (unroll >= 16)
+    hipLaunchKernelGGL((k_state_step<S, U, V, 16, kTorchLerp>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTorchLerp>), grid, block, 0, st, a);
 }
 
 template <typename S>
@@ -173,7 +178,10 @@ int pick_vec(const StepArgs<S, U> &a) {
   };
   const int want = tuning().vec;
   if (want > 0 && want <= max_vec<S>() && (want & (want - 1)) == 0 && ok(want)) return want;
-  for (int v = max_vec<S>(); v > 1; v >>= 1)
+  // Measured on MI355X: 4-byte lanes (128-column chunks of fp16) below 2048 boards, 8-byte lanes above;
+  // narrower chunks keep each sweep's gather working set inside the Infinity Cache.
+  const int best = std::max(1, std::min(max_vec<S>(), (a.batch < 2048 ? 4 : 8) / (int)sizeof(S)));
+  for (int v = best; v > 1; v >>= 1)
     if (ok(v)) return v;
   return 1;
 }
@@ -188,12 +196,13 @@ void state_step(StepArgs<S, U> a, hipStream_t st) {
   if (tiles > chunks || chunks % tiles) tiles = chunks;
   a.ntiles = tiles;
   a.wpt = chunks / tiles;
+  const int unroll = tuning().unroll > 0 ? tuning().unroll : 8;
   switch (v) {
-    case 1: launch_v<S, U, 1>(a, st); break;
-    case 2: launch_v<S, U, 2>(a, st); break;
-    case 4: launch_v<S, U, 4>(a, st); break;
+    case 1: launch_v<S, U, 1>(a, unroll, st); break;
+    case 2: launch_v<S, U, 2>(a, unroll, st); break;
+    case 4: launch_v<S, U, 4>(a, unroll, st); break;
     default:
-      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, st);
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, unroll, st);
       break;
   }
   check_launch("state step");
@@ -380,6 +389,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     FLY_REQUIRE(key != nullptr, "key is null");
     const std::string k(key);
     if (k == "vec") tuning().vec = (int)value;
+    else if (k == "unroll") tuning().unroll = (int)value;
     else if (k == "tiles") tuning().tiles = (int)value;
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });

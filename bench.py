@@ -101,6 +101,9 @@ def main() -> int:
     ap.add_argument("--ones", default="40", help="ones per board: N or LO-HI")
     ap.add_argument("--cpu-boards", type=int, default=256, help="boards in the CPU baseline sample (0: skip)")
     ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="after the timed loop, run a plain float32 streaming copy of MIB MiB three times (a kernel "
+                         "of known HBM traffic, to scale rocprof FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -162,6 +165,13 @@ def main() -> int:
         wall = time.perf_counter() - w0
         prof = _hip.profile_read()
         _hip.profile_enable(False)
+    if args.calibrate_copy > 0:
+        src = torch.ones(args.calibrate_copy * 2**18, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 3 x {args.calibrate_copy} MiB read + {args.calibrate_copy} MiB written")
     gpu_ms = ev0.elapsed_time(ev1)
     ms_per_step = wall / args.steps * 1e3
     value = args.batch * args.steps / wall

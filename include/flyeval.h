@@ -18,6 +18,7 @@
  *   fly_plan_create_full  chessfly/brain.py:215-216 (per-call weights of the literal recurrence)
  *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280)
  *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch)
+ *   fly_dense_create      chessfly/model.py:79-93 (the encoder and head weights, as the matrix cores read them)
  *   fly_encoder           chessfly/model.py:99-102 (encoder linear map, input gain, cast, transpose)
  *   fly_head              chessfly/model.py:103-105 and :51-58 (RunningNorm eval, policy/from/to/value)
  *   fly_model_forward     chessfly/model.py:95-105 FlyChessNet.forward (no-grad, device inputs)
@@ -107,12 +108,6 @@ int fly_forward_literal(const fly_plan *plan, float *u_dev, int64_t ldu, const f
                         void *stream);
 
 /* ---- dense maps -------------------------------------------------------------------------------- */
-/* u (n_in, ldu) = cast((x[:, :k] W[:, :k]^T + b) * gain): x (batch, ldx) float32, W (n_in, ldw) float32.
- * out_f16 != 0 stores __half, else float. */
-int fly_encoder(const float *x_dev, int64_t ldx, int64_t batch, int64_t k, const float *w_dev, int64_t ldw,
-                const float *b_dev, int64_t n_in, float gain, void *u_dev, int64_t ldu, int32_t out_f16,
-                void *stream);
-
 /* Weights of the read-out: RunningNorm statistics and the four linear maps over the n_out outputs. */
 typedef struct fly_head_desc {
     int64_t n_out;              /* 2,333 */
@@ -133,17 +128,31 @@ typedef struct fly_head_desc {
     const int32_t *move_to;
 } fly_head_desc;
 
+typedef struct fly_dense fly_dense;
+
+/* Dense plan: the encoder (n_in, ldw) over its first k feature columns, its bias, and the head, copied and
+ * split into fp16 hi/lo pairs for the matrix cores (rebuild it when any of these weights changes).
+ * Validates the move squares (FLY_ERR_INVALID outside 0..63). */
+int fly_dense_create(const fly_head_desc *head, const float *enc_w_dev, int64_t ldw, int64_t k,
+                     const float *enc_b_dev, int64_t n_in, void *stream, fly_dense **out);
+int fly_dense_destroy(fly_dense *dense);
+
+/* u (n_in, ldu) = cast((x[:, :k] W[:, :k]^T + b) * gain): x (batch, ldx) float32; out_f16 != 0 stores
+ * __half, else float. */
+size_t fly_encoder_workspace(const fly_dense *dense, int64_t batch);
+int fly_encoder(const fly_dense *dense, const float *x_dev, int64_t ldx, int64_t batch, float gain, void *u_dev,
+                int64_t ldu, int32_t out_f16, void *workspace_dev, size_t workspace_bytes, void *stream);
+
 /* logits (batch, n_moves) and wdl (batch, 3), float32 row-major, from the output activity
- * r (n_out, ldr) float32 (column b = board b). */
-size_t fly_head_workspace(const fly_head_desc *head, int64_t batch);
-int fly_head(const fly_head_desc *head, const float *r_dev, int64_t ldr, int64_t batch, float *logits_dev,
+ * r (n_out, ldr) float32 (column b = board b), through the eval-mode normaliser. */
+size_t fly_head_workspace(const fly_dense *dense, int64_t batch);
+int fly_head(const fly_dense *dense, const float *r_dev, int64_t ldr, int64_t batch, float *logits_dev,
              float *wdl_dev, void *workspace_dev, size_t workspace_bytes, void *stream);
 
-/* FlyChessNet.forward: x (batch, ldx) float32 -> logits (batch, n_moves), wdl (batch, 3).  The encoder is
- * (n_in, ldw) over the first k feature columns; the plan's mode selects the state arithmetic. */
-size_t fly_model_workspace(const fly_plan *plan, const fly_head_desc *head, int64_t batch);
-int fly_model_forward(const fly_plan *plan, const fly_head_desc *head, const float *x_dev, int64_t ldx,
-                      int64_t batch, int64_t k, const float *enc_w_dev, int64_t ldw, const float *enc_b_dev,
+/* FlyChessNet.forward: x (batch, ldx) float32 -> logits (batch, n_moves), wdl (batch, 3).  The plan's mode
+ * selects the state arithmetic; the encoder output (times input_gain) is kept in float32 in both modes. */
+size_t fly_model_workspace(const fly_plan *plan, const fly_dense *dense, int64_t batch);
+int fly_model_forward(const fly_plan *plan, const fly_dense *dense, const float *x_dev, int64_t ldx, int64_t batch,
                       float input_gain, float *logits_dev, float *wdl_dev, void *workspace_dev,
                       size_t workspace_bytes, void *stream);
 
@@ -165,7 +174,8 @@ int fly_profile_read(double *ms, int64_t *launches);
 
 /* ---- tuning (for sweeps; defaults are the measured best) --------------------------------------- */
 /* key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept
- * row-major (0 = automatic, 1 = all column chunks of a row back to back). */
+ * row-major (0 = automatic, 1 = all column chunks of a row back to back); "unroll": non-zeros each wave
+ * gathers per iteration (8, 16 or 32; 0 = automatic). */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus
