@@ -131,6 +131,8 @@ struct Tuning {
   int vec = 0;    // elements per lane of the step kernel, 0 = automatic
   int tiles = 0;  // batch tiles swept row-major, 0 = automatic
   int unroll = 0; // non-zeros gathered per wave per iteration (8, 16, 32), 0 = automatic
+  int nt_store = 0;  // non-temporal stores of the new state
+  int groups = 0;    // lane groups of the step (1, 2, 4, 8), each gathering its own non-zero; 0 = automatic
 };
 Tuning &tuning();
 

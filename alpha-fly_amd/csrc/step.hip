@@ -41,18 +41,26 @@ struct Lanes {
 #pragma unroll
     for (int i = 0; i < V; ++i) f[i] = static_cast<float>(v[i]);
   }
-  static __device__ __forceinline__ void store(S *p, const float (&f)[V]) {
+  static __device__ __forceinline__ void store(S *p, const float (&f)[V], bool nt = false) {
     vec v;
 #pragma unroll
     for (int i = 0; i < V; ++i) v[i] = static_cast<S>(f[i]);
-    *reinterpret_cast<vec *>(p) = v;
+    if (nt)
+      __builtin_nontemporal_store(v, reinterpret_cast<vec *>(p));
+    else
+      *reinterpret_cast<vec *>(p) = v;
   }
 };
 
 template <typename S>
 struct Lanes<S, 1> {
   static __device__ __forceinline__ void load(const S *p, float (&f)[1]) { f[0] = static_cast<float>(*p); }
-  static __device__ __forceinline__ void store(S *p, const float (&f)[1]) { *p = static_cast<S>(f[0]); }
+  static __device__ __forceinline__ void store(S *p, const float (&f)[1], bool nt = false) {
+    if (nt)
+      __builtin_nontemporal_store(static_cast<S>(f[0]), p);
+    else
+      *p = static_cast<S>(f[0]);
+  }
 };
 
 template <typename S, typename U>
@@ -68,56 +76,29 @@ struct StepArgs {
   int64_t ldo;
   int32_t nrows, batch, wpt, ntiles;
   int32_t u_vec;           // the drive can be read with V-wide loads
+  int32_t nt_store;        // write the new state with non-temporal stores
 };
 
-template <typename S, typename U, int V, int UNROLL, bool TORCH_LERP>
-__global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
-  const int lane = threadIdx.x & 63;
+// Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
+// chunks is swept over every row before the next tile starts.
+struct WaveSlot {
+  uint32_t row, chunk;
+  bool valid;
+};
+
+template <typename S, typename U>
+__device__ __forceinline__ WaveSlot wave_slot(const StepArgs<S, U> &a) {
   const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t per_tile = (uint32_t)a.nrows * (uint32_t)a.wpt;
   const uint32_t tile = wave / per_tile;
-  if (tile >= (uint32_t)a.ntiles) return;
   const uint32_t in_tile = wave - tile * per_tile;
   const uint32_t row = in_tile / (uint32_t)a.wpt;
-  const uint32_t chunk = tile * (uint32_t)a.wpt + (in_tile - row * (uint32_t)a.wpt);
-  const int64_t cbeg = (int64_t)chunk * (64 * V);
-  const int64_t col = cbeg + (int64_t)lane * V;
-  const bool active = col < a.batch;
-  const int64_t lcol = active ? col : cbeg;
+  return {row, tile * (uint32_t)a.wpt + (in_tile - row * (uint32_t)a.wpt), tile < (uint32_t)a.ntiles};
+}
 
-  float acc[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-
-  if (a.xprev != nullptr && a.rowptr != nullptr) {
-    const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
-    const S *base = a.xprev + lcol;
-    int32_t e = beg;
-    for (; e + UNROLL <= end; e += UNROLL) {
-      int2 cv[UNROLL];
-#pragma unroll
-      for (int j = 0; j < UNROLL; ++j) cv[j] = a.colval[e + j];
-      float xv[UNROLL][V];
-#pragma unroll
-      for (int j = 0; j < UNROLL; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
-#pragma unroll
-      for (int j = 0; j < UNROLL; ++j) {
-        const float w = __int_as_float(cv[j].y);
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = fmaf(w, xv[j][i], acc[i]);
-      }
-    }
-    for (; e < end; ++e) {
-      const int2 cv = a.colval[e];
-      float xv[V];
-      Lanes<S, V>::load(base + (int64_t)cv.x * a.ldx, xv);
-      const float w = __int_as_float(cv.y);
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] = fmaf(w, xv[i], acc[i]);
-    }
-  }
-  if (!active) return;
-
+// Input drive, clamp and leaky update of V columns of one row, then the store.
+template <typename S, typename U, int V, bool TORCH_LERP>
+__device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V]) {
   const RowParam p = a.params[row];
   float u[V];
 #pragma unroll
@@ -144,65 +125,202 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
     const float x = fminf(fmaxf((acc[i] + u[i]) + p.k, p.lo), p.hi) + p.e;
     out[i] = TORCH_LERP ? lerp_torch(pv[i], x, p.a) : fmaf(p.a, x - pv[i], pv[i]);
   }
-  Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out);
+  Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out, a.nt_store != 0);
+}
+
+// One non-zero at a time per wave: the {column, weight} pairs are wave-uniform scalar loads, every lane
+// gathers its V columns of the source row.  Chunk = 64 * V columns.
+template <typename S, typename U, int V, int UNROLL, bool TORCH_LERP>
+__global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
+  const WaveSlot w = wave_slot(a);
+  if (!w.valid) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t cbeg = (int64_t)w.chunk * (64 * V);
+  const int64_t col = cbeg + (int64_t)lane * V;
+  const bool active = col < a.batch;
+  const int64_t lcol = active ? col : cbeg;
+
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+  if (a.xprev != nullptr && a.rowptr != nullptr) {
+    const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
+    const S *base = a.xprev + lcol;
+    int32_t e = beg;
+    for (; e + UNROLL <= end; e += UNROLL) {
+      int2 cv[UNROLL];
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) cv[j] = a.colval[e + j];
+      float xv[UNROLL][V];
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) {
+        const float wt = __int_as_float(cv[j].y);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, xv[j][i], acc[i]);
+      }
+    }
+    for (; e < end; ++e) {
+      const int2 cv = a.colval[e];
+      float xv[V];
+      Lanes<S, V>::load(base + (int64_t)cv.x * a.ldx, xv);
+      const float wt = __int_as_float(cv.y);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, xv[i], acc[i]);
+    }
+  }
+  if (!active) return;
+  finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc);
+}
+
+// G non-zeros at a time per wave: the wave splits into G groups of 64/G lanes, group g gathers non-zero
+// e0 + j*G + g for the same chunk of (64/G) * V columns, so every load is V*sizeof(S) bytes per lane while
+// the chunk (and the gather working set of a sweep) is G times narrower.  Each lane reads its group's
+// {column, weight} pair with a vector load (one address per group); the pairs of the next round are loaded
+// while the current round's gathers are in flight.  The G partial sums meet through cross-lane shuffles,
+// and group 0 finishes the row.
+template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP>
+__global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U> a) {
+  constexpr int LPG = 64 / G;
+  const WaveSlot w = wave_slot(a);
+  if (!w.valid) return;
+  const int lane = threadIdx.x & 63;
+  const int g = lane / LPG, s = lane % LPG;
+  const int64_t cbeg = (int64_t)w.chunk * (LPG * V);
+  const int64_t col = cbeg + (int64_t)s * V;
+  const bool active = col < a.batch;
+  const int64_t lcol = active ? col : cbeg;
+
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+  if (a.xprev != nullptr && a.rowptr != nullptr) {
+    const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
+    const S *base = a.xprev + lcol;
+    // pairs past the row's end read as {column 0, weight 0}
+    auto pairs = [&](int32_t e0, int2 (&cv)[UNROLL]) {
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) {
+        const int32_t e = e0 + j * G + g;
+        cv[j] = e < end ? a.colval[e] : make_int2(0, 0);
+      }
+    };
+    int2 cv[UNROLL];
+    if (beg < end) pairs(beg, cv);
+    for (int32_t e0 = beg; e0 < end; e0 += G * UNROLL) {
+      float xv[UNROLL][V];
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
+      int2 nx[UNROLL];
+      if (e0 + G * UNROLL < end) pairs(e0 + G * UNROLL, nx);
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) {
+        const float wt = __int_as_float(cv[j].y);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, xv[j][i], acc[i]);
+      }
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
+    }
+#pragma unroll
+    for (int off = LPG; off < 64; off <<= 1)
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += __shfl_xor(acc[i], off);
+  }
+  if (g != 0 || !active) return;
+  finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc);
 }
 
 // Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
 // with torch.lerp's formula, like the reference's CPU path.
 template <typename S, typename U, int V>
-void launch_v(const StepArgs<S, U> &a, int unroll, hipStream_t st) {
+void launch_v(const StepArgs<S, U> &a, int groups, int unroll, hipStream_t st) {
   const int64_t waves = (int64_t)a.nrows * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
-  constexpr bool kTorchLerp = sizeof(S) == 4;
+  constexpr bool kTL = sizeof(S) == 4;
+  if constexpr (V * sizeof(S) == 16) {
+    if (groups == 8) {
+      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
+      return;
+    }
+    if (groups == 4) {
+      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 4, 8, kTL>), grid, block, 0, st, a);
+      return;
+    }
+    if (groups == 2) {
+      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 2, 8, kTL>), grid, block, 0, st, a);
+      return;
+    }
+  }
   if (unroll >= 32)
-    hipLaunchKernelGGL((k_state_step<S, U, V, 32, kTorchLerp>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step<S, U, V, 32, kTL>), grid, block, 0, st, a);
   else if (unroll >= 16)
-    hipLaunchKernelGGL((k_state_step<S, U, V, 16, kTorchLerp>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step<S, U, V, 16, kTL>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTorchLerp>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTL>), grid, block, 0, st, a);
 }
 
 template <typename S>
 constexpr int max_vec() { return 16 / (int)sizeof(S); }
 
-// Largest V (elements per lane) that every V-wide access of the step allows, or the tuned value.
+// Elements per lane and lane groups of the step: the tuned values when set and allowed by the alignment of
+// every V-wide access, else 16-byte lanes in groups sized so a chunk is 64 columns below 2048 boards and
+// 256 above, which keeps each sweep's gather working set small inside the Infinity Cache.
 template <typename S, typename U>
-int pick_vec(const StepArgs<S, U> &a) {
-  auto ok = [&](int v) {
-    const size_t bytes = (size_t)v * sizeof(S);
-    if (a.ldo % v || !aligned(a.xout, bytes)) return false;
-    if (a.xprev && (a.ldx % v || !aligned(a.xprev, bytes))) return false;
+void pick_shape(const StepArgs<S, U> &a, int &v, int &groups) {
+  auto ok = [&](int vv) {
+    const size_t bytes = (size_t)vv * sizeof(S);
+    if (a.ldo % vv || !aligned(a.xout, bytes)) return false;
+    if (a.xprev && (a.ldx % vv || !aligned(a.xprev, bytes))) return false;
     return true;
   };
   const int want = tuning().vec;
-  if (want > 0 && want <= max_vec<S>() && (want & (want - 1)) == 0 && ok(want)) return want;
-  // Measured on MI355X: 4-byte lanes (128-column chunks of fp16) below 2048 boards, 8-byte lanes above;
-  // narrower chunks keep each sweep's gather working set inside the Infinity Cache.
-  const int best = std::max(1, std::min(max_vec<S>(), (a.batch < 2048 ? 4 : 8) / (int)sizeof(S)));
-  for (int v = best; v > 1; v >>= 1)
-    if (ok(v)) return v;
-  return 1;
+  if (want > 0 && want <= max_vec<S>() && (want & (want - 1)) == 0 && ok(want)) {
+    v = want;
+  } else {
+    v = 1;
+    for (int vv = max_vec<S>(); vv > 1; vv >>= 1)
+      if (ok(vv)) { v = vv; break; }
+  }
+  groups = 1;
+  if (v == max_vec<S>()) {
+    const int tg = tuning().groups;
+    if (tg == 1 || tg == 2 || tg == 4 || tg == 8) {
+      groups = tg;
+    } else {
+      // 64 columns per chunk below 2048 boards, 256 above (half lanes hold 8 columns, float lanes 4):
+      // measured best on MI355X at B = 256, 1120 and 4096
+      const int lanes = (a.batch < 2048 ? 64 : 256) / v;
+      groups = std::max(1, std::min(8, 64 / lanes));
+    }
+  }
 }
 
 template <typename S, typename U>
 void state_step(StepArgs<S, U> a, hipStream_t st) {
   if (a.nrows == 0 || a.batch == 0) return;
-  const int v = pick_vec(a);
+  int v = 1, groups = 1;
+  pick_shape(a, v, groups);
   a.u_vec = (a.u != nullptr && a.ldu % v == 0 && aligned(a.u, (size_t)v * sizeof(U))) ? 1 : 0;
-  const int chunks = (int)((a.batch + 64 * v - 1) / (64 * v));
+  const int width = (64 / groups) * v;
+  const int chunks = (int)((a.batch + width - 1) / width);
   int tiles = tuning().tiles > 0 ? (int)tuning().tiles : chunks;
   if (tiles > chunks || chunks % tiles) tiles = chunks;
   a.ntiles = tiles;
   a.wpt = chunks / tiles;
   const int unroll = tuning().unroll > 0 ? tuning().unroll : 8;
+  a.nt_store = tuning().nt_store;
   switch (v) {
-    case 1: launch_v<S, U, 1>(a, unroll, st); break;
-    case 2: launch_v<S, U, 2>(a, unroll, st); break;
-    case 4: launch_v<S, U, 4>(a, unroll, st); break;
+    case 1: launch_v<S, U, 1>(a, 1, unroll, st); break;
+    case 2: launch_v<S, U, 2>(a, sizeof(S) == 4 ? groups : 1, unroll, st); break;
+    case 4: launch_v<S, U, 4>(a, groups, unroll, st); break;
     default:
-      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, unroll, st);
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, groups, unroll, st);
       break;
   }
   check_launch("state step");
@@ -390,6 +508,8 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     const std::string k(key);
     if (k == "vec") tuning().vec = (int)value;
     else if (k == "unroll") tuning().unroll = (int)value;
+    else if (k == "groups") tuning().groups = (int)value;
+    else if (k == "nt_store") tuning().nt_store = (int)value;
     else if (k == "tiles") tuning().tiles = (int)value;
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });

@@ -175,7 +175,8 @@ int fly_profile_read(double *ms, int64_t *launches);
 /* ---- tuning (for sweeps; defaults are the measured best) --------------------------------------- */
 /* key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept
  * row-major (0 = automatic, 1 = all column chunks of a row back to back); "unroll": non-zeros each wave
- * gathers per iteration (8, 16 or 32; 0 = automatic). */
+ * gathers per iteration (8, 16 or 32; 0 = automatic); "nt_store": 1 writes the new state with non-temporal
+ * stores; "groups": lane groups per wave that gather different non-zeros (1, 2, 4, 8; 0 = automatic). */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus
