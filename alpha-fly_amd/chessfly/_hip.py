@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflyeval.
 
 MODE_DEVIATION_F16 = 0
 MODE_F32 = 1
+CONE_UNPRUNED = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -35,7 +36,7 @@ class HeadDesc(ctypes.Structure):
 SIGNATURES = {
     "fly_abi_version": (_i32, []),
     "fly_last_error": (ctypes.c_char_p, []),
-    "fly_cone_create": (_i32, [_i64, _i64, _p, _p, _p, _i64, _p, _i64, _i32, _p, _pp]),
+    "fly_cone_create": (_i32, [_i64, _i64, _p, _p, _p, _i64, _p, _i64, _i32, _i32, _p, _pp]),
     "fly_cone_destroy": (_i32, [_p]),
     "fly_cone_sizes": (_i32, [_p, _p, _p, _p]),
     "fly_cone_rows": (_i32, [_p, _i32, _p, _p]),

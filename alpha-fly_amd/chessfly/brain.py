@@ -95,18 +95,21 @@ class LightCone:
     from the device cone the first time they are used.
     """
 
-    def __init__(self, rnn: "ConnectomeRNN", in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int):
+    def __init__(self, rnn: "ConnectomeRNN", in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int,
+                 prune: bool = True):
         _hip.require_device(rnn.pre, "LightCone")
         lib = _hip.load()
         self.device = rnn.pre.device
         self.steps = int(steps)
+        self.pruned = bool(prune)
         self.out_idx = out_idx
         in32 = in_idx.to(device=self.device, dtype=torch.int32).contiguous()
         out32 = out_idx.to(device=self.device, dtype=torch.int32).contiguous()
         handle = ctypes.c_void_p()
         _hip.check(lib.fly_cone_create(rnn.n, rnn.n_edges, rnn.crow32.data_ptr(), rnn.pre32.data_ptr(),
                                        in32.data_ptr(), in32.numel(), out32.data_ptr(), out32.numel(), self.steps,
-                                       _hip.stream(self.device), ctypes.byref(handle)), "fly_cone_create")
+                                       0 if prune else _hip.CONE_UNPRUNED, _hip.stream(self.device),
+                                       ctypes.byref(handle)), "fly_cone_create")
         self._handle = handle
         T = self.steps
         rows = (ctypes.c_int64 * (T + 1))()
@@ -314,12 +317,14 @@ class ConnectomeRNN(nn.Module):
         return h
 
     # ---- the same function through the light cone ------------------------------------------------
-    def light_cone(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> LightCone:
-        key = (steps, in_idx.data_ptr(), out_idx.data_ptr(), str(self.pre.device))
+    def light_cone(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int, prune: bool = True) -> LightCone:
+        """The rows each step computes (cached by the index tensors, like brain.py:232-236).  prune=False
+        computes every neuron at every step: the same function without the light cone."""
+        key = (steps, in_idx.data_ptr(), out_idx.data_ptr(), str(self.pre.device), bool(prune))
         if self._cone is None or self._cone[0] != key:
             self._cone = None                         # release the old cone (and its plans) first
             self._plans = {k: v for k, v in self._plans.items() if k[0] == "full"}
-            self._cone = (key, LightCone(self, in_idx, out_idx, steps))
+            self._cone = (key, LightCone(self, in_idx, out_idx, steps, prune))
         return self._cone[1]
 
     def forward_io(self, u_in: torch.Tensor, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> torch.Tensor:

@@ -68,6 +68,9 @@ class FlyChessNet(nn.Module):
         # float16 selects the deviation-from-rest path (the only float16 inference the reference trusts,
         # chessfly/model.py:65-72); float32 selects the float32 light cone.
         self.infer_dtype = torch.float16
+        # The reference always evaluates through the light cone; False computes every neuron at every step
+        # (the same function, pruning off) for measurement.
+        self.light_cone_pruning = True
         if cfg.shuffled:
             conn = conn.shuffled()
         self.brain = ConnectomeRNN(conn, bias_init=cfg.bias_init, global_scale=cfg.weight_scale)
@@ -136,7 +139,7 @@ class FlyChessNet(nn.Module):
             x = x.contiguous()
         brain = self.brain
         brain._check_params("FlyChessNet.forward")
-        cone = brain.light_cone(self.in_idx, self.out_idx, self.cfg.steps)
+        cone = brain.light_cone(self.in_idx, self.out_idx, self.cfg.steps, prune=self.light_cone_pruning)
         mode = _hip.MODE_DEVIATION_F16 if dtype == torch.float16 else _hip.MODE_F32
         plan = brain._cone_plan(cone, mode)
         dense = self._dense(k)

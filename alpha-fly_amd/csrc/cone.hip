@@ -201,13 +201,14 @@ using namespace fly;
 
 extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, const int32_t *pre,
                                const int32_t *in_idx, int64_t n_in, const int32_t *out_idx, int64_t n_out,
-                               int32_t steps, void *stream, fly_cone **out) {
+                               int32_t steps, int32_t flags, void *stream, fly_cone **out) {
   return guard([&] {
     FLY_REQUIRE(out != nullptr, "out is null");
     *out = nullptr;
     FLY_REQUIRE(n > 0 && n < (int64_t)INT32_MAX, "n must be in [1, 2^31)");
     FLY_REQUIRE(n_edges >= 0 && n_edges < (int64_t)INT32_MAX, "n_edges must be in [0, 2^31)");
     FLY_REQUIRE(steps >= 0 && steps <= 64, "steps must be in [0, 64]");
+    FLY_REQUIRE((flags & ~FLY_CONE_UNPRUNED) == 0, "unknown cone flag");
     FLY_REQUIRE(n_in >= 0 && n_out >= 0, "negative index count");
     FLY_REQUIRE(crow && (pre || n_edges == 0), "graph pointer is null");
     FLY_REQUIRE((in_idx || n_in == 0) && (out_idx || n_out == 0), "index pointer is null");
@@ -241,13 +242,20 @@ extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, 
     auto D = [&](int t) { return bwd.p + (size_t)t * n; };
     hipLaunchKernelGGL(k_fill_u8, dim3(blocks_for((T + 1) * n, kThreads)), dim3(kThreads), 0, st, fwd.p, (uint8_t)0, (int64_t)(T + 1) * n);
     hipLaunchKernelGGL(k_fill_u8, dim3(blocks_for((T + 1) * n, kThreads)), dim3(kThreads), 0, st, bwd.p, (uint8_t)0, (int64_t)(T + 1) * n);
-    if (T >= 1 && n_in) hipLaunchKernelGGL(k_mark, dim3(blocks_for(n_in, kThreads)), dim3(kThreads), 0, st, V(1), in_idx, n_in);
-    for (int t = 2; t <= T; ++t)
-      hipLaunchKernelGGL(k_grow_forward, dim3(nb), dim3(kThreads), 0, st, crow, pre, V(t - 1), V(t), n);
-    if (n_out) hipLaunchKernelGGL(k_mark, dim3(blocks_for(n_out, kThreads)), dim3(kThreads), 0, st, D(T), out_idx, n_out);
-    for (int t = T - 1; t >= 0; --t) {
-      copy_d2d(D(t), D(t + 1), (size_t)n, st);
-      hipLaunchKernelGGL(k_grow_backward, dim3(nb), dim3(kThreads), 0, st, crow, pre, D(t + 1), D(t), n);
+    if (flags & FLY_CONE_UNPRUNED) {  // every neuron varies from step 1 and every neuron matters
+      if (T >= 1)
+        hipLaunchKernelGGL(k_fill_u8, dim3(blocks_for(T * n, kThreads)), dim3(kThreads), 0, st, V(1), (uint8_t)1, (int64_t)T * n);
+      hipLaunchKernelGGL(k_fill_u8, dim3(blocks_for((T + 1) * n, kThreads)), dim3(kThreads), 0, st, D(0), (uint8_t)1,
+                         (int64_t)(T + 1) * n);
+    } else {
+      if (T >= 1 && n_in) hipLaunchKernelGGL(k_mark, dim3(blocks_for(n_in, kThreads)), dim3(kThreads), 0, st, V(1), in_idx, n_in);
+      for (int t = 2; t <= T; ++t)
+        hipLaunchKernelGGL(k_grow_forward, dim3(nb), dim3(kThreads), 0, st, crow, pre, V(t - 1), V(t), n);
+      if (n_out) hipLaunchKernelGGL(k_mark, dim3(blocks_for(n_out, kThreads)), dim3(kThreads), 0, st, D(T), out_idx, n_out);
+      for (int t = T - 1; t >= 0; --t) {
+        copy_d2d(D(t), D(t + 1), (size_t)n, st);
+        hipLaunchKernelGGL(k_grow_backward, dim3(nb), dim3(kThreads), 0, st, crow, pre, D(t + 1), D(t), n);
+      }
     }
     check_launch("reach masks");
 

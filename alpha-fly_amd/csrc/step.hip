@@ -75,6 +75,7 @@ struct StepArgs {
   S *xout;                 // X_t (|R_t|, ldo)
   int64_t ldo;
   int32_t nrows, batch, wpt, ntiles;
+  int32_t slots;           // row slots per chunk: nrows, or ceil(nrows / G) when each wave takes G rows
   int32_t u_vec;           // the drive can be read with V-wide loads
   int32_t nt_store;        // write the new state with non-temporal stores
 };
@@ -89,7 +90,7 @@ struct WaveSlot {
 template <typename S, typename U>
 __device__ __forceinline__ WaveSlot wave_slot(const StepArgs<S, U> &a) {
   const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t per_tile = (uint32_t)a.nrows * (uint32_t)a.wpt;
+  const uint32_t per_tile = (uint32_t)a.slots * (uint32_t)a.wpt;
   const uint32_t tile = wave / per_tile;
   const uint32_t in_tile = wave - tile * per_tile;
   const uint32_t row = in_tile / (uint32_t)a.wpt;
@@ -234,16 +235,75 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
   finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc);
 }
 
+// G rows at a time per wave, for steps whose rows hold few non-zeros: group g of 64/G lanes owns row
+// G*slot + g and walks its non-zeros, gathering (64/G) * V columns per load; the wave loops to the longest
+// of its rows with the shorter rows' loads masked off, and every group finishes its own row.
+template <typename S, typename U, int V, int G, bool TORCH_LERP>
+__global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a) {
+  constexpr int LPG = 64 / G;
+  const WaveSlot w = wave_slot(a);                // w.row counts slots of G rows
+  if (!w.valid) return;
+  const int lane = threadIdx.x & 63;
+  const int g = lane / LPG, s = lane % LPG;
+  const uint32_t row = w.row * G + g;
+  const bool has_row = row < (uint32_t)a.nrows;
+  const int64_t cbeg = (int64_t)w.chunk * (LPG * V);
+  const int64_t col = cbeg + (int64_t)s * V;
+  const bool active = has_row && col < a.batch;
+  const int64_t lcol = col < a.batch ? col : cbeg;
+
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+  if (a.xprev != nullptr && a.rowptr != nullptr) {
+    const int32_t beg = has_row ? a.rowptr[row] : 0, end = has_row ? a.rowptr[row + 1] : 0;
+    int32_t len = end - beg;
+#pragma unroll
+    for (int off = LPG; off < 64; off <<= 1) len = max(len, __shfl_xor(len, off));
+    const S *base = a.xprev + lcol;
+    constexpr int UNROLL = 4;
+    for (int32_t k = 0; k < len; k += UNROLL) {
+      float xv[UNROLL][V];
+      float wt[UNROLL];
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) {
+        const int32_t e = beg + k + j;
+        wt[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) xv[j][i] = 0.0f;
+        if (e < end) {
+          const int2 cv = a.colval[e];
+          wt[j] = __int_as_float(cv.y);
+          Lanes<S, V>::load(base + (int64_t)cv.x * a.ldx, xv[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt[j], xv[j][i], acc[i]);
+    }
+  }
+  if (!active) return;
+  finish_row<S, U, V, TORCH_LERP>(a, row, col, acc);
+}
+
 // Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
 // with torch.lerp's formula, like the reference's CPU path.
 template <typename S, typename U, int V>
-void launch_v(const StepArgs<S, U> &a, int groups, int unroll, hipStream_t st) {
-  const int64_t waves = (int64_t)a.nrows * a.wpt * a.ntiles;
+void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, hipStream_t st) {
+  const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
   constexpr bool kTL = sizeof(S) == 4;
   if constexpr (V * sizeof(S) == 16) {
+    if (rows_mode) {
+      if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, kTL>), grid, block, 0, st, a);
+      else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, kTL>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, kTL>), grid, block, 0, st, a);
+      return;
+    }
     if (groups == 8) {
       hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
       return;
@@ -302,7 +362,7 @@ void pick_shape(const StepArgs<S, U> &a, int &v, int &groups) {
 }
 
 template <typename S, typename U>
-void state_step(StepArgs<S, U> a, hipStream_t st) {
+void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   if (a.nrows == 0 || a.batch == 0) return;
   int v = 1, groups = 1;
   pick_shape(a, v, groups);
@@ -315,12 +375,19 @@ void state_step(StepArgs<S, U> a, hipStream_t st) {
   a.wpt = chunks / tiles;
   const int unroll = tuning().unroll > 0 ? tuning().unroll : 8;
   a.nt_store = tuning().nt_store;
+  // Rows shorter than 16 non-zeros on average (or no matrix at all) would leave most of a round of G
+  // interleaved gathers empty: give each lane group its own row instead of its own non-zero.
+  const bool rows_mode = groups > 1 && tuning().rows_mode >= 0 &&
+                         (tuning().rows_mode > 0 || a.rowptr == nullptr || a.xprev == nullptr || avg_nnz < 16.0);
+  a.slots = rows_mode ? (a.nrows + groups - 1) / groups : a.nrows;
   switch (v) {
-    case 1: launch_v<S, U, 1>(a, 1, unroll, st); break;
-    case 2: launch_v<S, U, 2>(a, sizeof(S) == 4 ? groups : 1, unroll, st); break;
-    case 4: launch_v<S, U, 4>(a, groups, unroll, st); break;
+    // only 16-byte lanes (V = 16 / sizeof(S)) have grouped and row-slot kernels; pick_shape sets groups to
+    // 1 for every other V, so rows_mode is false there too
+    case 1: launch_v<S, U, 1>(a, 1, unroll, false, st); break;
+    case 2: launch_v<S, U, 2>(a, 1, unroll, false, st); break;
+    case 4: launch_v<S, U, 4>(a, groups, unroll, rows_mode, st); break;
     default:
-      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, groups, unroll, st);
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, groups, unroll, rows_mode, st);
       break;
   }
   check_launch("state step");
@@ -391,7 +458,7 @@ const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t b
     a.ldo = lds;
     a.nrows = (int32_t)nr;
     a.batch = (int32_t)batch;
-    state_step(a, st);
+    state_step(a, nr ? (double)plan.nnz[t] / (double)nr : 0.0, st);
     prev = buf[cur];
     cur ^= 1;
   }
@@ -495,7 +562,7 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
       a.ldo = last ? ldh : lds;
       a.nrows = (int32_t)n;
       a.batch = (int32_t)batch;
-      state_step(a, st);
+      state_step(a, (double)plan->nnz[0] / (double)n, st);
       prev = buf[cur];
       cur ^= 1;
     }
@@ -509,6 +576,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     if (k == "vec") tuning().vec = (int)value;
     else if (k == "unroll") tuning().unroll = (int)value;
     else if (k == "groups") tuning().groups = (int)value;
+    else if (k == "rows_mode") tuning().rows_mode = (int)value;
     else if (k == "nt_store") tuning().nt_store = (int)value;
     else if (k == "tiles") tuning().tiles = (int)value;
     else FLY_REQUIRE(false, "unknown tuning key " + k);

@@ -50,9 +50,10 @@ def algorithmic_bytes(cone, batch: int, state_bytes: int) -> list[int]:
     return out
 
 
-def cpu_baseline(net, conn, x_cpu, threads: int, seconds: float = 12.0):
-    """The reference's CPU forward (float32 light cone, constants cached per weight version, as
-    chessfly/brain.py:295-306 does) on the host cores; returns (evals/s, per-forward seconds, logits, wdl)."""
+def cpu_baseline(net, conn, x_cpu, threads: int, prune: bool = True, seconds: float = 12.0):
+    """The reference's CPU forward on the host cores: the float32 light cone with its constants cached per
+    weight version (chessfly/brain.py:295-306), or with pruning off the literal recurrence
+    (chessfly/brain.py:211-223); returns (evals/s, per-forward seconds, logits, wdl, repetitions)."""
     import warnings
 
     import numpy as np
@@ -78,12 +79,22 @@ def cpu_baseline(net, conn, x_cpu, threads: int, seconds: float = 12.0):
     cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), in_idx, out_idx, net.cfg.steps)
     prep = F.prepare_f32(ba, cone)
     x = torch.as_tensor(x_cpu)
-    logits, wdl = F.model_forward(ba, hp, cone, x, "f32", prep=prep)          # warm-up
+    steps = net.cfg.steps
+    out_t = torch.as_tensor(out_idx)
+    in_t = torch.as_tensor(in_idx)
+
+    def forward():
+        if prune:
+            return F.model_forward(ba, hp, cone, x, "f32", prep=prep)
+        u = torch.zeros(conn.n_neurons, x.shape[0]).index_copy_(0, in_t, F.encode_input(hp, x, torch.float32))
+        return F.heads(hp, F.norm(hp, F.literal(ba, u, steps)[out_t].T))
+
+    logits, wdl = forward()                                                   # warm-up
     times = []
     start = time.perf_counter()
     while len(times) < 3 or (time.perf_counter() - start < seconds and len(times) < 20):
         t0 = time.perf_counter()
-        logits, wdl = F.model_forward(ba, hp, cone, x, "f32", prep=prep)
+        logits, wdl = forward()
         times.append(time.perf_counter() - t0)
     per = statistics.median(times)
     return x.shape[0] / per, per, logits, wdl, len(times)
@@ -99,6 +110,8 @@ def main() -> int:
     ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
     ap.add_argument("--graph", choices=["synthetic", "shuffled"], default="synthetic")
     ap.add_argument("--ones", default="40", help="ones per board: N or LO-HI")
+    ap.add_argument("--no-prune", action="store_true",
+                    help="compute every neuron at every step (the same function without the light cone)")
     ap.add_argument("--cpu-boards", type=int, default=256, help="boards in the CPU baseline sample (0: skip)")
     ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -128,6 +141,7 @@ def main() -> int:
     t0 = time.perf_counter()
     net, conn = synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev)
     net.infer_dtype = torch.float16 if args.dtype == "f16" else torch.float32
+    net.light_cone_pruning = not args.no_prune
     ones = tuple(int(v) for v in args.ones.split("-")) if "-" in args.ones else int(args.ones)
     x_np = synthetic_boards(args.batch, seed=1, ones=ones)
     x = torch.as_tensor(x_np, device=dev)
@@ -136,7 +150,7 @@ def main() -> int:
 
     brain = net.brain
     t0 = time.perf_counter()
-    cone = brain.light_cone(net.in_idx, net.out_idx, args.recurrent_steps)
+    cone = brain.light_cone(net.in_idx, net.out_idx, args.recurrent_steps, prune=not args.no_prune)
     torch.cuda.synchronize()
     t_cone = time.perf_counter() - t0
     mode = _hip.MODE_DEVIATION_F16 if args.dtype == "f16" else _hip.MODE_F32
@@ -201,10 +215,11 @@ def main() -> int:
         nb = min(args.cpu_boards, args.batch)
         threads = max(1, min(len(os.sched_getaffinity(0)), 16))
         log(f"CPU baseline: {nb} boards on {threads} threads ...")
-        rate, per, ref_logits, ref_wdl, reps = cpu_baseline(net, conn, x_np[:nb], threads)
+        rate, per, ref_logits, ref_wdl, reps = cpu_baseline(net, conn, x_np[:nb], threads, prune=not args.no_prune)
+        path = ("float32 literal recurrence (reference CPU path, chessfly/brain.py:211-223)" if args.no_prune else
+                "float32 light cone with cached constants (reference CPU path, chessfly/brain.py:295-329)")
         cpu = {"value": round(rate, 1), "unit": "board-evals/s", "cores": threads, "kind": "port",
-               "sample": f"{nb} of the {args.batch} boards, full graph, float32 light cone with cached constants "
-                         f"(reference CPU path, chessfly/brain.py:295-329), median of {reps} forwards "
+               "sample": f"{nb} of the {args.batch} boards, full graph, {path}, median of {reps} forwards "
                          f"({per:.2f} s each)"}
         dl = float((logits[:nb].float().cpu() - ref_logits).abs().max())
         dw = float((wdl[:nb].float().cpu() - ref_wdl).abs().max())
@@ -218,11 +233,13 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": (f"FlyChessNet.forward, {args.graph} connectome {conn.n_neurons} neurons / "
-                                f"{conn.n_edges} synapses, B={args.batch}, {args.recurrent_steps} steps, light cone, "
+                                f"{conn.n_edges} synapses, B={args.batch}, {args.recurrent_steps} steps, "
+                                + ("no pruning, " if args.no_prune else "light cone, ")
                                 + ("fp16 deviation state, fp32 math" if args.dtype == "f16" else "fp32 state")),
                    "batch": args.batch, "recurrent_steps": args.recurrent_steps, "graph": args.graph,
                    "state": "fp16 deviation from fp32 resting trajectory" if args.dtype == "f16" else "fp32",
-                   "edge_visits": cone.edge_visits, "rows": cone.row_counts[1:], "ones_per_board": args.ones},
+                   "light_cone": not args.no_prune, "edge_visits": cone.edge_visits, "rows": cone.row_counts[1:],
+                   "ones_per_board": args.ones},
         "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
         "kernel_ms_per_forward": shares, "gpu_event_ms_per_step": round(gpu_ms / args.steps, 4),
         "one_off_ms": {"light_cone": round(t_cone * 1e3, 1), "plan": round(t_plan * 1e3, 1)},

@@ -56,10 +56,13 @@ const char *fly_last_error(void);
 
 /* ---- light cone (integer, bit-exact with chessfly/brain.py:126-173) ------------------------------
  * crow_dev (n+1), pre_dev (n_edges): CSR of W; in_idx_dev (n_in), out_idx_dev (n_out): neuron ids.
- * Validates every index on the device first (FLY_ERR_INVALID if any is out of range). */
+ * flags: 0 prunes to the light cone; FLY_CONE_UNPRUNED computes every neuron at every step t >= 1 (the
+ * same function without pruning).  Validates every index on the device first (FLY_ERR_INVALID if any is
+ * out of range). */
+#define FLY_CONE_UNPRUNED 1
 int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow_dev, const int32_t *pre_dev,
                     const int32_t *in_idx_dev, int64_t n_in, const int32_t *out_idx_dev, int64_t n_out,
-                    int32_t steps, void *stream, fly_cone **out);
+                    int32_t steps, int32_t flags, void *stream, fly_cone **out);
 int fly_cone_destroy(fly_cone *cone);
 /* rows[t] = |R_t| for t = 0..steps; nnz[t] = non-zeros of A_t (0 where A_t is None); has_op[t] = 1 where
  * A_t exists (R_{t-1} non-empty).  Arrays have steps+1 entries; any may be NULL. */
@@ -176,7 +179,8 @@ int fly_profile_read(double *ms, int64_t *launches);
 /* key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept
  * row-major (0 = automatic, 1 = all column chunks of a row back to back); "unroll": non-zeros each wave
  * gathers per iteration (8, 16 or 32; 0 = automatic); "nt_store": 1 writes the new state with non-temporal
- * stores; "groups": lane groups per wave that gather different non-zeros (1, 2, 4, 8; 0 = automatic). */
+ * stores; "groups": lane groups per wave that gather different non-zeros (1, 2, 4, 8; 0 = automatic);
+ * "rows_mode": 1 gives each lane group its own row, -1 never, 0 for steps with short rows. */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus

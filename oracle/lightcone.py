@@ -88,12 +88,18 @@ def sub_matrix(n: int, pre: np.ndarray, post: np.ndarray, rows: np.ndarray, cols
     return SubMatrix(edges, lpost, lpre, crow, (len(rows), len(cols)))
 
 
-def light_cone(n: int, pre, post, in_idx, out_idx, steps: int) -> Cone:
+def light_cone(n: int, pre, post, in_idx, out_idx, steps: int, prune: bool = True) -> Cone:
+    """prune=False keeps every neuron at every step t >= 1 (R_t = all, R_0 empty): the literal recurrence
+    in the same bookkeeping."""
     pre = np.asarray(pre, dtype=np.int64)
     post = np.asarray(post, dtype=np.int64)
     in_idx = np.asarray(in_idx, dtype=np.int64)
     out_idx = np.asarray(out_idx, dtype=np.int64)
-    fwd, bwd = reach_sets(n, pre, post, in_idx, out_idx, steps)
+    if prune:
+        fwd, bwd = reach_sets(n, pre, post, in_idx, out_idx, steps)
+    else:
+        fwd = [np.zeros(n, dtype=bool)] + [np.ones(n, dtype=bool) for _ in range(steps)]
+        bwd = [np.ones(n, dtype=bool) for _ in range(steps + 1)]
     rows = [np.flatnonzero(fwd[t] & bwd[t]).astype(np.int64) for t in range(steps + 1)]
     in_at = _positions(n, in_idx)
     ops, keep_next, keep_prev, carried, prev_row, u_pos, u_src = ([None] for _ in range(7))

@@ -51,7 +51,7 @@ def test_version_and_error_reporting_on_host(lib):
     assert lib.fly_set_tuning(b"no-such-knob", 1) == 1          # FLY_ERR_INVALID
     assert b"no-such-knob" in lib.fly_last_error()
     out = ctypes.c_void_p()
-    assert lib.fly_cone_create(0, 0, None, None, None, 0, None, 0, 1, None, ctypes.byref(out)) == 1
+    assert lib.fly_cone_create(0, 0, None, None, None, 0, None, 0, 1, 0, None, ctypes.byref(out)) == 1
     assert out.value is None
     assert lib.fly_forward_io_workspace(None, 64) == 0
 

@@ -85,6 +85,27 @@ def test_light_cone_bit_exact_on_shuffled_control_with_repeats():
         assert_cone_equal(cone, oracle_cone(conn, in_idx, out_idx, steps))
 
 
+@pytest.mark.parametrize("steps", [1, 3, 6])
+def test_unpruned_cone_bit_exact_and_same_function(steps):
+    """Pruning off (every neuron, every step) builds the trivial cone bit-exactly and computes the same
+    outputs as the pruned cone, in both state modes."""
+    conn = tiny_connectome(120, 700, seed=3)
+    lg, b, al = random_params(conn, 4)
+    rnn = product_rnn(conn, 3.0, lg, b, al)
+    in_idx, out_idx = np.arange(0, 9), np.arange(100, 120)
+    ind, outd = torch.as_tensor(in_idx, device=DEV), torch.as_tensor(out_idx, device=DEV)
+    u = torch.randn(9, 33, generator=torch.Generator().manual_seed(steps)).to(DEV)
+    with torch.no_grad():
+        outs = {}
+        for prune in (True, False):
+            cone = rnn.light_cone(ind, outd, steps, prune=prune)
+            ref = L.light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), in_idx, out_idx, steps, prune=prune)
+            assert_cone_equal(cone, ref)
+            outs[prune] = (rnn.forward_io(u, ind, outd, steps), rnn.forward_io(u.half(), ind, outd, steps))
+    torch.testing.assert_close(outs[True][0], outs[False][0], rtol=2e-5, atol=2e-5)
+    torch.testing.assert_close(outs[True][1], outs[False][1], rtol=5e-3, atol=5e-3)
+
+
 def _medium(seed=0):
     from chessfly.synthetic import GraphSpec, synthetic_connectome
     spec = GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=80, seed=seed)

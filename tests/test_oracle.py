@@ -101,6 +101,10 @@ def test_cone_forward_equals_literal_recurrence_fp64(steps):
     torch.testing.assert_close(F.cone_f32(ba, cone, u_in, steps), full, rtol=1e-9, atol=1e-11)
     # the deviation algebra without float16 rounding is the same function
     torch.testing.assert_close(F.cone_half(ba, cone, u_in, steps, half=False), full, rtol=1e-9, atol=1e-11)
+    # and so is the bookkeeping with pruning off (every neuron at every step)
+    flat = L.light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), in_idx, out_idx, steps, prune=False)
+    assert all(len(flat.rows[t]) == conn.n_neurons for t in range(1, steps + 1)) and len(flat.rows[0]) == 0
+    torch.testing.assert_close(F.cone_f32(ba, flat, u_in, steps), full, rtol=1e-9, atol=1e-11)
     assert cone.edge_visits < 4 * conn.n_edges
 
 
