@@ -207,6 +207,17 @@ def main() -> int:
                 "avg_launch_ms": round(avg_launch_ms, 4),
                 "gather_bytes_per_forward": int(gather),
                 "gather_GBps": round(gather / (step_ms / max(step_launches, 1) * launches_per_fwd * 1e-3) / 1e9, 1)}
+    # HBM traffic per launch comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed beside the
+    # profile of the same workload (counters cannot be read in-process); null for any other workload.
+    traffic_file = os.path.join(REPO, "profiles", "state_step_b1120_traffic.json")
+    if os.path.exists(traffic_file) and not args.tune:
+        with open(traffic_file) as f:
+            measured = json.load(f)
+        here = {"batch": args.batch, "dtype": args.dtype, "prune": not args.no_prune, "graph": args.graph,
+                "recurrent_steps": args.recurrent_steps, "ones": args.ones}
+        if measured["workload"] == here:
+            roofline["traffic"] = measured["traffic_bytes_per_launch"]
+            roofline["traffic_source"] = measured["source"]
     shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
 
     cpu = None
