@@ -32,10 +32,19 @@ __device__ __forceinline__ float lerp_torch(float start, float end, float weight
   return fmaf(small ? weight : weight - 1.0f, end - start, small ? start : end);
 }
 
-// V elements of S as one vector access.
+// V elements of S as one vector access.  `raw` keeps a gathered vector in its storage type until the FMA
+// (fp16 operands then feed v_fma_mix_f32 directly and take half the registers).
 template <typename S, int V>
 struct Lanes {
   typedef S vec __attribute__((ext_vector_type(V)));
+  static __device__ __forceinline__ vec raw(const S *p) { return *reinterpret_cast<const vec *>(p); }
+  static __device__ __forceinline__ vec zero() {
+    vec v;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = static_cast<S>(0.0f);
+    return v;
+  }
+  static __device__ __forceinline__ float at(const vec &v, int i) { return static_cast<float>(v[i]); }
   static __device__ __forceinline__ void load(const S *p, float (&f)[V]) {
     const vec v = *reinterpret_cast<const vec *>(p);
 #pragma unroll
@@ -54,6 +63,10 @@ struct Lanes {
 
 template <typename S>
 struct Lanes<S, 1> {
+  typedef S vec;
+  static __device__ __forceinline__ vec raw(const S *p) { return *p; }
+  static __device__ __forceinline__ vec zero() { return static_cast<S>(0.0f); }
+  static __device__ __forceinline__ float at(const vec &v, int) { return static_cast<float>(v); }
   static __device__ __forceinline__ void load(const S *p, float (&f)[1]) { f[0] = static_cast<float>(*p); }
   static __device__ __forceinline__ void store(S *p, const float (&f)[1], bool nt = false) {
     if (nt)
@@ -97,34 +110,48 @@ __device__ __forceinline__ WaveSlot wave_slot(const StepArgs<S, U> &a) {
   return {row, tile * (uint32_t)a.wpt + (in_tile - row * (uint32_t)a.wpt), tile < (uint32_t)a.ntiles};
 }
 
-// Input drive, clamp and leaky update of V columns of one row, then the store.
-template <typename S, typename U, int V, bool TORCH_LERP>
-__device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V]) {
-  const RowParam p = a.params[row];
+// A row's constants, input drive and carried state for V columns, loaded before the gathers so their
+// latency overlaps the gather loop.
+template <int V>
+struct RowInputs {
+  RowParam p;
   float u[V];
+  float pv[V];
+};
+
+template <typename S, typename U, int V>
+__device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_t row, int64_t col, bool active,
+                                                RowInputs<V> &in) {
+  in.p = a.params[row];
 #pragma unroll
-  for (int i = 0; i < V; ++i) u[i] = 0.0f;
-  if (a.u != nullptr && p.usrc >= 0) {
-    const U *src = a.u + (int64_t)p.usrc * a.ldu + col;
+  for (int i = 0; i < V; ++i) in.u[i] = 0.0f;
+  if (active && a.u != nullptr && in.p.usrc >= 0) {
+    const U *src = a.u + (int64_t)in.p.usrc * a.ldu + col;
     if (a.u_vec) {
-      Lanes<U, V>::load(src, u);
+      Lanes<U, V>::load(src, in.u);
     } else {
 #pragma unroll
-      for (int i = 0; i < V; ++i) u[i] = (col + i < a.batch) ? static_cast<float>(src[i]) : 0.0f;
+      for (int i = 0; i < V; ++i) in.u[i] = (col + i < a.batch) ? static_cast<float>(src[i]) : 0.0f;
     }
   }
-  float pv[V];
-  if (a.xprev != nullptr && p.prev >= 0) {
-    Lanes<S, V>::load(a.xprev + (int64_t)p.prev * a.ldx + col, pv);
+  if (active && a.xprev != nullptr && in.p.prev >= 0) {
+    Lanes<S, V>::load(a.xprev + (int64_t)in.p.prev * a.ldx + col, in.pv);
   } else {
 #pragma unroll
-    for (int i = 0; i < V; ++i) pv[i] = p.pdef;
+    for (int i = 0; i < V; ++i) in.pv[i] = in.p.pdef;
   }
+}
+
+// Input drive, clamp and leaky update of V columns of one row, then the store.
+template <typename S, typename U, int V, bool TORCH_LERP>
+__device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V],
+                                           const RowInputs<V> &in) {
+  const RowParam &p = in.p;
   float out[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    const float x = fminf(fmaxf((acc[i] + u[i]) + p.k, p.lo), p.hi) + p.e;
-    out[i] = TORCH_LERP ? lerp_torch(pv[i], x, p.a) : fmaf(p.a, x - pv[i], pv[i]);
+    const float x = fminf(fmaxf((acc[i] + in.u[i]) + p.k, p.lo), p.hi) + p.e;
+    out[i] = TORCH_LERP ? lerp_torch(in.pv[i], x, p.a) : fmaf(p.a, x - in.pv[i], in.pv[i]);
   }
   Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out, a.nt_store != 0);
 }
@@ -144,6 +171,8 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  RowInputs<V> in;
+  load_row_inputs(a, w.row, col, active, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
     const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
@@ -153,14 +182,14 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
       int2 cv[UNROLL];
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) cv[j] = a.colval[e + j];
-      float xv[UNROLL][V];
+      typename Lanes<S, V>::vec xr[UNROLL];
 #pragma unroll
-      for (int j = 0; j < UNROLL; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
+      for (int j = 0; j < UNROLL; ++j) xr[j] = Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx);
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) {
         const float wt = __int_as_float(cv[j].y);
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, xv[j][i], acc[i]);
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, Lanes<S, V>::at(xr[j], i), acc[i]);
       }
     }
     for (; e < end; ++e) {
@@ -173,7 +202,7 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
     }
   }
   if (!active) return;
-  finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc);
+  finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc, in);
 }
 
 // G non-zeros at a time per wave: the wave splits into G groups of 64/G lanes, group g gathers non-zero
@@ -197,6 +226,8 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  RowInputs<V> in;
+  load_row_inputs(a, w.row, col, active && g == 0, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
     const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
@@ -212,16 +243,16 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
     int2 cv[UNROLL];
     if (beg < end) pairs(beg, cv);
     for (int32_t e0 = beg; e0 < end; e0 += G * UNROLL) {
-      float xv[UNROLL][V];
+      typename Lanes<S, V>::vec xr[UNROLL];
 #pragma unroll
-      for (int j = 0; j < UNROLL; ++j) Lanes<S, V>::load(base + (int64_t)cv[j].x * a.ldx, xv[j]);
+      for (int j = 0; j < UNROLL; ++j) xr[j] = Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx);
       int2 nx[UNROLL];
       if (e0 + G * UNROLL < end) pairs(e0 + G * UNROLL, nx);
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) {
         const float wt = __int_as_float(cv[j].y);
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, xv[j][i], acc[i]);
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, Lanes<S, V>::at(xr[j], i), acc[i]);
       }
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
@@ -232,13 +263,13 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
       for (int i = 0; i < V; ++i) acc[i] += __shfl_xor(acc[i], off);
   }
   if (g != 0 || !active) return;
-  finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc);
+  finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc, in);
 }
 
 // G rows at a time per wave, for steps whose rows hold few non-zeros: group g of 64/G lanes owns row
 // G*slot + g and walks its non-zeros, gathering (64/G) * V columns per load; the wave loops to the longest
 // of its rows with the shorter rows' loads masked off, and every group finishes its own row.
-template <typename S, typename U, int V, int G, bool TORCH_LERP>
+template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP>
 __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a) {
   constexpr int LPG = 64 / G;
   const WaveSlot w = wave_slot(a);                // w.row counts slots of G rows
@@ -255,6 +286,8 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  RowInputs<V> in;
+  if (has_row) load_row_inputs(a, row, col, active, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
     const int32_t beg = has_row ? a.rowptr[row] : 0, end = has_row ? a.rowptr[row + 1] : 0;
@@ -262,30 +295,36 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
 #pragma unroll
     for (int off = LPG; off < 64; off <<= 1) len = max(len, __shfl_xor(len, off));
     const S *base = a.xprev + lcol;
-    constexpr int UNROLL = 4;
-    for (int32_t k = 0; k < len; k += UNROLL) {
-      float xv[UNROLL][V];
-      float wt[UNROLL];
+    // pairs past a row's end read as {column 0, weight 0} and their gathers are skipped; the next round's
+    // pairs load while this round's gathers are in flight
+    auto pairs = [&](int32_t k, int2 (&cv)[UNROLL]) {
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) {
         const int32_t e = beg + k + j;
-        wt[j] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < V; ++i) xv[j][i] = 0.0f;
-        if (e < end) {
-          const int2 cv = a.colval[e];
-          wt[j] = __int_as_float(cv.y);
-          Lanes<S, V>::load(base + (int64_t)cv.x * a.ldx, xv[j]);
-        }
+        cv[j] = e < end ? a.colval[e] : make_int2(0, 0);
       }
+    };
+    int2 cv[UNROLL];
+    if (len > 0) pairs(0, cv);
+    for (int32_t k = 0; k < len; k += UNROLL) {
+      typename Lanes<S, V>::vec xr[UNROLL];
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j)
+        xr[j] = (beg + k + j < end) ? Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx) : Lanes<S, V>::zero();
+      int2 nx[UNROLL];
+      if (k + UNROLL < len) pairs(k + UNROLL, nx);
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt[j], xv[j][i], acc[i]);
+      for (int j = 0; j < UNROLL; ++j) {
+        const float wt = __int_as_float(cv[j].y);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, Lanes<S, V>::at(xr[j], i), acc[i]);
+      }
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
     }
   }
   if (!active) return;
-  finish_row<S, U, V, TORCH_LERP>(a, row, col, acc);
+  finish_row<S, U, V, TORCH_LERP>(a, row, col, acc, in);
 }
 
 // Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
@@ -299,9 +338,15 @@ void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, h
   constexpr bool kTL = sizeof(S) == 4;
   if constexpr (V * sizeof(S) == 16) {
     if (rows_mode) {
-      if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, kTL>), grid, block, 0, st, a);
-      else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, kTL>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, kTL>), grid, block, 0, st, a);
+      if (unroll <= 4) {   // 4 measured best for the row slots
+        if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
+        else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, 4, kTL>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, 4, kTL>), grid, block, 0, st, a);
+      } else {
+        if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 8, kTL>), grid, block, 0, st, a);
+        else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, 8, kTL>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, 8, kTL>), grid, block, 0, st, a);
+      }
       return;
     }
     if (groups == 8) {
@@ -319,7 +364,7 @@ void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, h
   }
   if (unroll >= 32)
     hipLaunchKernelGGL((k_state_step<S, U, V, 32, kTL>), grid, block, 0, st, a);
-  else if (unroll >= 16)
+  else if (unroll >= 16)   // 8 (also for 0) measured best for one non-zero per wave
     hipLaunchKernelGGL((k_state_step<S, U, V, 16, kTL>), grid, block, 0, st, a);
   else
     hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTL>), grid, block, 0, st, a);
@@ -373,7 +418,7 @@ void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   if (tiles > chunks || chunks % tiles) tiles = chunks;
   a.ntiles = tiles;
   a.wpt = chunks / tiles;
-  const int unroll = tuning().unroll > 0 ? tuning().unroll : 8;
+  const int unroll = tuning().unroll > 0 ? tuning().unroll : 0;   // 0: each kernel's measured default
   a.nt_store = tuning().nt_store;
   // Rows shorter than 16 non-zeros on average (or no matrix at all) would leave most of a round of G
   // interleaved gathers empty: give each lane group its own row instead of its own non-zero.
