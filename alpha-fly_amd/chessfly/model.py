@@ -122,7 +122,8 @@ class FlyChessNet(nn.Module):
         return self._dense_cache
 
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """x: (B, >= N_BASE) -> policy logits (B, N_MOVES), WDL logits (B, 3), both float32."""
+        """x: (B, >= N_BASE) -> policy logits (B, N_MOVES), WDL logits (B, 3), both float32.  Half-precision
+        boards (what the search sends) are read as they are: widening them to float32 is exact."""
         _no_grad_only("FlyChessNet.forward")
         _hip.require_device(x, "FlyChessNet.forward")
         if self.training:
@@ -133,7 +134,7 @@ class FlyChessNet(nn.Module):
         k = N_FEATURES if self.cfg.attack_planes else N_BASE
         if x.dim() != 2 or x.shape[1] < k:
             raise RuntimeError(f"FlyChessNet.forward: x must be (B, >= {k}), got {tuple(x.shape)}")
-        if x.dtype != torch.float32:
+        if x.dtype not in (torch.float32, torch.float16):
             x = x.float()
         if x.stride(1) != 1:
             x = x.contiguous()
@@ -149,7 +150,8 @@ class FlyChessNet(nn.Module):
         lib = _hip.load()
         ws = _hip.workspace(lib.fly_model_workspace(plan.handle, dense.handle, batch), x.device)
         ldx = x.stride(0) if batch > 1 else x.shape[1]
-        _hip.check(lib.fly_model_forward(plan.handle, dense.handle, x.data_ptr(), ldx, batch,
+        x_f16 = int(x.dtype == torch.float16)
+        _hip.check(lib.fly_model_forward(plan.handle, dense.handle, x.data_ptr(), x_f16, ldx, batch,
                                          float(self.cfg.input_gain), logits.data_ptr(), wdl.data_ptr(), ws.data_ptr(),
                                          ws.numel(), _hip.stream(x.device)), "fly_model_forward")
         return logits, wdl
@@ -161,10 +163,39 @@ class FlyChessNet(nn.Module):
         return p[..., 0] - p[..., 2]
 
 
+def _upload(a: np.ndarray, device) -> torch.Tensor:
+    """Host array -> device tensor through pinned memory, so the copy is queued on the stream and `submit`
+    returns before it has run.  torch's pinned-block cache keeps the block until the copy has finished."""
+    host = torch.empty(a.shape, dtype=torch.from_numpy(a[:0]).dtype, pin_memory=True)
+    host.numpy()[...] = a
+    return host.to(device, non_blocking=True)
+
+
+class _Submitted:
+    """A batch in flight: the pinned host buffers the device copies its answers into, and the event
+    recorded after the last copy."""
+
+    def __init__(self, device_outputs, stream):
+        self.host = [torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for t in device_outputs]
+        for h, t in zip(self.host, device_outputs):
+            h.copy_(t, non_blocking=True)
+        self.done = torch.cuda.Event()
+        self.done.record(stream)
+
+    def wait(self):
+        self.done.synchronize()
+        policy, values, bad = self.host
+        if int(bad[0]):
+            raise IndexError("Evaluator: a legal-move index lies outside the (batch, N_MOVES) policy")
+        return policy.numpy(), values.numpy()        # views that keep their pinned block alive
+
+
 class Evaluator:
     """The `evaluate` callable of the search: numpy in, numpy out (chessfly/model.py:113-135).  `submit`
-    launches the evaluation and returns before the GPU finishes; `result` waits for it.  Legal-move logits
-    are gathered on the device, so only the requested entries cross back to the host."""
+    queues the upload, the forward and the download on the device's current stream and returns before the
+    GPU finishes; `result` waits for it.  One kernel (fly_evaluator_outputs) computes the expected values
+    and either rounds the whole policy to half precision (lazy search) or gathers the legal moves' logits
+    (eager search), so only the requested bytes cross back to the host."""
 
     def __init__(self, net: FlyChessNet, device):
         self.net, self.device = net, device
@@ -172,16 +203,39 @@ class Evaluator:
     @torch.no_grad()
     def submit(self, x, rows, cols):
         self.net.eval()
-        logits, wdl = self.net(torch.from_numpy(x).to(self.device, non_blocking=True).float())
+        x = np.ascontiguousarray(x)
+        if x.dtype not in (np.float16, np.float32):
+            x = x.astype(np.float32)
+        logits, wdl = self.net(_upload(x, self.device))
+        batch, n_moves = logits.shape
+        device = logits.device
+        values = torch.empty(batch, dtype=torch.float32, device=device)
+        bad = torch.empty(1, dtype=torch.int32, device=device)
         if rows is None:                      # lazy search: the whole policy vector, half precision
-            return logits.half(), self.net.expected_value(wdl.float())
-        legal = logits[torch.from_numpy(rows).to(self.device, non_blocking=True),
-                       torch.from_numpy(cols).to(self.device, non_blocking=True)]
-        return legal.float(), self.net.expected_value(wdl.float())
+            policy = torch.empty(batch, n_moves, dtype=torch.float16, device=device)
+            r = c = None
+            n_legal, out16, legal = 0, policy.data_ptr(), None
+        else:
+            rows = np.ascontiguousarray(rows, dtype=np.int64)
+            cols = np.ascontiguousarray(cols, dtype=np.int64)
+            if rows.shape != cols.shape or rows.ndim != 1:
+                raise IndexError(f"Evaluator: rows {rows.shape} and cols {cols.shape} must be equal 1-d shapes")
+            n_legal = len(rows)
+            if n_legal:
+                r, c = _upload(rows, device), _upload(cols, device)
+            else:                             # non-null pointers still select the legal-move form
+                r = c = torch.zeros(1, dtype=torch.int64, device=device)
+            policy = torch.empty(n_legal, dtype=torch.float32, device=device)
+            out16, legal = None, policy.data_ptr()
+        stream = torch.cuda.current_stream(device)
+        _hip.check(_hip.load().fly_evaluator_outputs(logits.data_ptr(), wdl.data_ptr(), batch, n_moves, _hip.ptr(r),
+                                                     _hip.ptr(c), n_legal, out16, legal, values.data_ptr(),
+                                                     bad.data_ptr(), stream.cuda_stream), "fly_evaluator_outputs")
+        return _Submitted((policy, values, bad), stream)
 
     @staticmethod
     def result(handle):
-        return handle[0].cpu().numpy(), handle[1].float().cpu().numpy()
+        return handle.wait()
 
     def __call__(self, x, rows, cols):
         return self.result(self.submit(x, rows, cols))

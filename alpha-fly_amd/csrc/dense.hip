@@ -51,13 +51,15 @@ constexpr int GBM = 64, GBN = 64, GBK = 32, LDK = GBK + 8;  // LDS rows padded t
 
 int64_t pad_k(int64_t k) { return round_up(std::max<int64_t>(k, 1), GBK); }
 
-// hi = fp16(v * scale), lo = fp16(v * scale - hi), rows x kp, zero beyond k.
-__global__ void k_split_rows(const float *__restrict__ src, int64_t ld, int64_t rows, int64_t k, float scale,
+// hi = fp16(v * scale), lo = fp16(v * scale - hi), rows x kp, zero beyond k.  A float16 source widens
+// exactly, so with scale 1 its lo half is zero.
+template <typename T>
+__global__ void k_split_rows(const T *__restrict__ src, int64_t ld, int64_t rows, int64_t k, float scale,
                              _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, int64_t kp) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= rows * kp) return;
   const int64_t r = i / kp, c = i - r * kp;
-  const float v = c < k ? src[r * ld + c] * scale : 0.0f;
+  const float v = c < k ? static_cast<float>(src[r * ld + c]) * scale : 0.0f;
   const _Float16 h = static_cast<_Float16>(v);
   hi[i] = h;
   lo[i] = static_cast<_Float16>(v - static_cast<float>(h));
@@ -243,11 +245,12 @@ float weight_scale(const float *w, int64_t ld, int64_t rows, int64_t k, hipStrea
   return std::ldexp(1.0f, e);
 }
 
-void split_into(const float *w, int64_t ld, int64_t rows, int64_t k, float scale, _Float16 *hi, _Float16 *lo,
+template <typename T>
+void split_into(const T *w, int64_t ld, int64_t rows, int64_t k, float scale, _Float16 *hi, _Float16 *lo,
                 int64_t kp, hipStream_t st) {
   if (rows == 0) return;
-  hipLaunchKernelGGL(k_split_rows, dim3(blocks_for(rows * kp, kThreads)), dim3(kThreads), 0, st, w, ld, rows, k, scale,
-                     hi, lo, kp);
+  hipLaunchKernelGGL(k_split_rows<T>, dim3(blocks_for(rows * kp, kThreads)), dim3(kThreads), 0, st, w, ld, rows, k,
+                     scale, hi, lo, kp);
   check_launch("split");
 }
 
@@ -263,12 +266,15 @@ size_t head_ws(const fly_dense &d, int64_t batch) {
   return 2 * split_bytes(batch, d.kp_head) + align256((size_t)batch * head_ld(d) * sizeof(float));
 }
 
-void run_encoder(const fly_dense &d, const float *x, int64_t ldx, int64_t batch, float gain, float *u, _Float16 *u16,
-                 int64_t ldu, void *ws, hipStream_t st) {
+void run_encoder(const fly_dense &d, const void *x, bool x_f16, int64_t ldx, int64_t batch, float gain, float *u,
+                 _Float16 *u16, int64_t ldu, void *ws, hipStream_t st) {
   LaunchTimer timer(FLY_K_ENCODER, st);
   _Float16 *xh = static_cast<_Float16 *>(ws);
   _Float16 *xl = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + split_bytes(batch, d.kp_enc));
-  split_into(x, ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st);
+  if (x_f16)
+    split_into(static_cast<const _Float16 *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st);
+  else
+    split_into(static_cast<const float *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st);
   gemm_split(Split{d.enc_hi.p, d.enc_lo.p, d.n_in}, Split{xh, xl, batch}, d.kp_enc, d.enc_unscale,
              EncoderEpilogue{d.enc_b.p, gain, u, u16, ldu}, st);
 }
@@ -387,15 +393,15 @@ extern "C" int fly_dense_destroy(fly_dense *d) {
 
 extern "C" size_t fly_encoder_workspace(const fly_dense *d, int64_t batch) { return d ? encoder_ws(*d, batch) : 0; }
 
-extern "C" int fly_encoder(const fly_dense *d, const float *x, int64_t ldx, int64_t batch, float gain, void *u,
-                           int64_t ldu, int32_t out_f16, void *ws, size_t ws_bytes, void *stream) {
+extern "C" int fly_encoder(const fly_dense *d, const void *x, int32_t x_f16, int64_t ldx, int64_t batch, float gain,
+                           void *u, int64_t ldu, int32_t out_f16, void *ws, size_t ws_bytes, void *stream) {
   return guard([&] {
     check_dense(d);
     FLY_REQUIRE(batch >= 0, "negative batch");
     if (!batch || !d->n_in) return;
     FLY_REQUIRE(x && u && ldx >= d->k && ldu >= batch, "bad argument");
     FLY_REQUIRE(ws && ws_bytes >= encoder_ws(*d, batch) && aligned(ws, 256), "workspace too small or misaligned");
-    run_encoder(*d, x, ldx, batch, gain, out_f16 ? nullptr : static_cast<float *>(u),
+    run_encoder(*d, x, x_f16 != 0, ldx, batch, gain, out_f16 ? nullptr : static_cast<float *>(u),
                 out_f16 ? static_cast<_Float16 *>(u) : nullptr, ldu, ws, as_stream(stream));
   });
 }
@@ -420,8 +426,9 @@ extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_dense *d, 
          std::max(encoder_ws(*d, batch), head_ws(*d, batch));
 }
 
-extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const float *x, int64_t ldx, int64_t batch,
-                                 float input_gain, float *logits, float *wdl, void *ws, size_t ws_bytes, void *stream) {
+extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const void *x, int32_t x_f16, int64_t ldx,
+                                 int64_t batch, float input_gain, float *logits, float *wdl, void *ws, size_t ws_bytes,
+                                 void *stream) {
   return guard([&] {
     check_plan_device(plan);
     check_dense(d);
@@ -442,7 +449,7 @@ extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const
     void *scratch = base;  // the encoder's operand split, then the head's
     const int64_t lds = state_ld(batch);
     // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
-    run_encoder(*d, x, ldx, batch, input_gain, u, nullptr, ldu, scratch, st);
+    run_encoder(*d, x, x_f16 != 0, ldx, batch, input_gain, u, nullptr, ldu, scratch, st);
     if (plan->mode == FLY_MODE_DEVIATION_F16) {
       const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, batch, states, st);
       run_head<_Float16>(*d, fin, lds, plan->out_src.p, plan->cbase.p, batch, logits, wdl, scratch, st);

@@ -100,6 +100,35 @@ def cpu_baseline(net, conn, x_cpu, threads: int, prune: bool = True, seconds: fl
     return x.shape[0] / per, per, logits, wdl, len(times)
 
 
+def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> dict:
+    """The search's view (chessfly/model.py:113-135): fp16 boards from host numpy through Evaluator.submit
+    and result, one batch at a time, so the pinned H2D copy of the boards, the forward, the output kernel and
+    the D2H copy of the answers are all inside the clock.  Lazy returns the whole fp16 policy; eager returns
+    `legal_per_board` gathered logits per board."""
+    import numpy as np
+    import torch
+    from chessfly.encoding import N_MOVES
+    from chessfly.model import Evaluator
+
+    ev = Evaluator(net, dev)
+    x16 = x_np.astype(np.float16)
+    rng = np.random.default_rng(3)
+    rows = np.repeat(np.arange(len(x16)), legal_per_board)
+    cols = rng.integers(0, N_MOVES, size=len(rows))
+    out = {}
+    for name, r, c in (("lazy", None, None), ("eager", rows, cols)):
+        ev(x16, r, c)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ev.result(ev.submit(x16, r, c))
+        dt = (time.perf_counter() - t0) / steps
+        out[name] = {"evals_per_s": round(len(x16) / dt, 1), "ms_per_batch": round(dt * 1e3, 3)}
+    out["note"] = (f"B={len(x16)} fp16 boards from host numpy, pinned staging; lazy: fp16 (B, {N_MOVES}) policy "
+                   f"back; eager: {legal_per_board} legal logits per board back; plus values")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,6 +142,8 @@ def main() -> int:
     ap.add_argument("--no-prune", action="store_true",
                     help="compute every neuron at every step (the same function without the light cone)")
     ap.add_argument("--cpu-boards", type=int, default=256, help="boards in the CPU baseline sample (0: skip)")
+    ap.add_argument("--evaluator-steps", type=int, default=10,
+                    help="batches through Evaluator.submit/result from host numpy, PCIe included (0: skip)")
     ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed loop, run a plain float32 streaming copy of MIB MiB three times (a kernel "
@@ -220,6 +251,11 @@ def main() -> int:
             roofline["traffic_source"] = measured["source"]
     shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
 
+    evaluator = None
+    if args.evaluator_steps > 0:
+        evaluator = evaluator_figure(net, dev, x_np, args.evaluator_steps)
+        log(f"Evaluator from host numpy: {evaluator}")
+
     cpu = None
     parity = None
     if args.cpu_boards > 0:
@@ -254,6 +290,7 @@ def main() -> int:
         "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
         "kernel_ms_per_forward": shares, "gpu_event_ms_per_step": round(gpu_ms / args.steps, 4),
         "one_off_ms": {"light_cone": round(t_cone * 1e3, 1), "plan": round(t_plan * 1e3, 1)},
+        "evaluator": evaluator,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -22,6 +22,8 @@
  *   fly_encoder           chessfly/model.py:99-102 (encoder linear map, input gain, cast, transpose)
  *   fly_head              chessfly/model.py:103-105 and :51-58 (RunningNorm eval, policy/from/to/value)
  *   fly_model_forward     chessfly/model.py:95-105 FlyChessNet.forward (no-grad, device inputs)
+ *   fly_evaluator_outputs chessfly/model.py:120-128 and :107-110 (Evaluator.submit's half cast or legal gather,
+ *                         expected_value)
  */
 #ifndef FLYEVAL_H
 #define FLYEVAL_H
@@ -140,11 +142,11 @@ int fly_dense_create(const fly_head_desc *head, const float *enc_w_dev, int64_t 
                      const float *enc_b_dev, int64_t n_in, void *stream, fly_dense **out);
 int fly_dense_destroy(fly_dense *dense);
 
-/* u (n_in, ldu) = cast((x[:, :k] W[:, :k]^T + b) * gain): x (batch, ldx) float32; out_f16 != 0 stores
- * __half, else float. */
+/* u (n_in, ldu) = cast((x[:, :k] W[:, :k]^T + b) * gain): x (batch, ldx) float32, or __half when x_f16 != 0
+ * (the search's boards, model.py:124, widened exactly as .float() does); out_f16 != 0 stores __half, else float. */
 size_t fly_encoder_workspace(const fly_dense *dense, int64_t batch);
-int fly_encoder(const fly_dense *dense, const float *x_dev, int64_t ldx, int64_t batch, float gain, void *u_dev,
-                int64_t ldu, int32_t out_f16, void *workspace_dev, size_t workspace_bytes, void *stream);
+int fly_encoder(const fly_dense *dense, const void *x_dev, int32_t x_f16, int64_t ldx, int64_t batch, float gain,
+                void *u_dev, int64_t ldu, int32_t out_f16, void *workspace_dev, size_t workspace_bytes, void *stream);
 
 /* logits (batch, n_moves) and wdl (batch, 3), float32 row-major, from the output activity
  * r (n_out, ldr) float32 (column b = board b), through the eval-mode normaliser. */
@@ -152,12 +154,26 @@ size_t fly_head_workspace(const fly_dense *dense, int64_t batch);
 int fly_head(const fly_dense *dense, const float *r_dev, int64_t ldr, int64_t batch, float *logits_dev,
              float *wdl_dev, void *workspace_dev, size_t workspace_bytes, void *stream);
 
-/* FlyChessNet.forward: x (batch, ldx) float32 -> logits (batch, n_moves), wdl (batch, 3).  The plan's mode
- * selects the state arithmetic; the encoder output (times input_gain) is kept in float32 in both modes. */
+/* FlyChessNet.forward: x (batch, ldx) float32 (or __half, x_f16 != 0) -> logits (batch, n_moves), wdl (batch, 3).
+ * The plan's mode selects the state arithmetic; the encoder output (times input_gain) is kept in float32 in
+ * both modes. */
 size_t fly_model_workspace(const fly_plan *plan, const fly_dense *dense, int64_t batch);
-int fly_model_forward(const fly_plan *plan, const fly_dense *dense, const float *x_dev, int64_t ldx, int64_t batch,
-                      float input_gain, float *logits_dev, float *wdl_dev, void *workspace_dev,
+int fly_model_forward(const fly_plan *plan, const fly_dense *dense, const void *x_dev, int32_t x_f16, int64_t ldx,
+                      int64_t batch, float input_gain, float *logits_dev, float *wdl_dev, void *workspace_dev,
                       size_t workspace_bytes, void *stream);
+
+/* What the search's evaluate callable returns (chessfly/model.py:120-128), from logits (batch, n_moves) and
+ * wdl (batch, 3), float32 row-major:
+ *   values[b] = P(win) - P(loss) under the softmax of wdl[b] (expected_value, model.py:107-110);
+ *   rows == NULL (lazy search): logits16 (batch, n_moves) __half = logits rounded to nearest even;
+ *   else (eager search): legal[m] = logits[rows[m], cols[m]] for m < n_legal, rows/cols int64 indexed as
+ *   torch does (negative values count from the end).
+ * An index outside the shape cannot be reported before the kernel has run, so the kernel writes NaN for
+ * that entry and sets *bad_dev to 1; *bad_dev is 0 otherwise (the call clears it first).  The caller reads
+ * it back with the outputs. */
+int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t batch, int64_t n_moves,
+                          const int64_t *rows_dev, const int64_t *cols_dev, int64_t n_legal, void *logits16_dev,
+                          float *legal_dev, float *values_dev, int32_t *bad_dev, void *stream);
 
 /* ---- measurement ------------------------------------------------------------------------------- */
 /* Kernel classes timed by the profiler. */

@@ -67,3 +67,16 @@ def test_product_refuses_cpu_tensors():
             rnn.forward_io(torch.zeros(5, 4), torch.arange(5), torch.arange(25, 30), 3)
     with pytest.raises(NotImplementedError):
         rnn(torch.zeros(30, 4), 3)                              # grad mode: training is not part of the evaluator
+
+
+def test_evaluator_outputs_checks_arguments_on_host(lib):
+    """fly_evaluator_outputs refuses null or negative arguments before launching anything."""
+    assert lib.fly_evaluator_outputs(None, None, 1, 5, None, None, 0, None, None, None, None, None) == 1
+    assert b"flag" in lib.fly_last_error()
+    flag = ctypes.c_int32(0)
+    assert lib.fly_evaluator_outputs(None, None, -1, 5, None, None, 0, None, None, None, ctypes.addressof(flag),
+                                     None) == 1
+    assert b"negative" in lib.fly_last_error()
+    assert lib.fly_evaluator_outputs(None, None, 2, 5, None, None, 0, None, None, None, ctypes.addressof(flag),
+                                     None) == 1
+    assert b"wdl" in lib.fly_last_error()

@@ -240,11 +240,18 @@ def test_encoder_and_head_gemms_match_fp64(batch, n_in, k, ld, n_out, moves):
     for f16 in (0, 1):
         ldu = batch + 3
         u = torch.zeros(n_in, ldu, dtype=torch.float16 if f16 else torch.float32, device=DEV)
-        _hip.check(lib.fly_encoder(dense.handle, xd.data_ptr(), ld, batch, 5.0, u.data_ptr(), ldu, f16, ws.data_ptr(),
-                                   ws.numel(), _hip.stream(torch.device(DEV))), "fly_encoder")
+        _hip.check(lib.fly_encoder(dense.handle, xd.data_ptr(), 0, ld, batch, 5.0, u.data_ptr(), ldu, f16,
+                                   ws.data_ptr(), ws.numel(), _hip.stream(torch.device(DEV))), "fly_encoder")
         got = u[:, :batch].double().cpu()
         tol = ref.abs() * (2 ** -10) + 1e-6 if f16 else ref.abs() * 2e-6 + 2e-6
         assert bool(((got - ref).abs() <= tol).all()), float((got - ref).abs().max())
+    # Half-precision boards (what the search sends) widen exactly: the same bits as their float32 copy.
+    xh = x.half().to(DEV)
+    u_h, u_f = (torch.zeros(n_in, batch, device=DEV) for _ in range(2))
+    for src, is_half, u in ((xh, 1, u_h), (xh.float(), 0, u_f)):
+        _hip.check(lib.fly_encoder(dense.handle, src.data_ptr(), is_half, ld, batch, 5.0, u.data_ptr(), batch, 0,
+                                   ws.data_ptr(), ws.numel(), _hip.stream(torch.device(DEV))), "fly_encoder")
+    assert torch.equal(u_h, u_f)
     r = torch.as_tensor(rng.normal(0, 3, (n_out, batch)), dtype=torch.float32)
     logits = torch.empty(batch, moves, device=DEV)
     wdl = torch.empty(batch, 3, device=DEV)
@@ -364,20 +371,96 @@ def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
     assert dl < 1e-3 and dw < 1e-3 and agree >= 0.999
 
 
+def _softmax_value(wdl: np.ndarray) -> np.ndarray:
+    w = wdl.astype(np.float64)
+    p = np.exp(w - w.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    return p[:, 0] - p[:, 2]
+
+
+def _evaluator_outputs(lib, _hip, logits, wdl, rows=None, cols=None):
+    batch, n_moves = logits.shape
+    lg, wd = torch.as_tensor(logits, device=DEV), torch.as_tensor(wdl, device=DEV)
+    values = torch.full((batch,), 7.0, device=DEV)
+    bad = torch.full((1,), 5, dtype=torch.int32, device=DEV)             # the call clears it
+    if rows is None:
+        out = torch.zeros(batch, n_moves, dtype=torch.float16, device=DEV)
+        args = (None, None, 0, out.data_ptr(), None)
+    else:
+        # an empty index list still needs non-null pointers: null rows selects the lazy form
+        r, c = (torch.as_tensor(np.asarray(v, dtype=np.int64) if len(v) else np.zeros(1, np.int64), device=DEV)
+                for v in (rows, cols))
+        out = torch.zeros(len(rows), device=DEV)
+        args = (r.data_ptr(), c.data_ptr(), len(rows), None, out.data_ptr())
+    _hip.check(lib.fly_evaluator_outputs(lg.data_ptr(), wd.data_ptr(), batch, n_moves, *args, values.data_ptr(),
+                                         bad.data_ptr(), _hip.stream(torch.device(DEV))), "fly_evaluator_outputs")
+    return out.cpu().numpy(), values.cpu().numpy(), int(bad.item())
+
+
+@pytest.mark.parametrize("batch,n_moves", [(37, 4168), (3, 5)])     # four-wide and one-wide conversion loops
+def test_evaluator_outputs_kernel(batch, n_moves):
+    """fly_evaluator_outputs against numpy: half rounding to nearest even (ties, overflow to inf, underflow,
+    NaN), torch's wrapping of negative indices, flagged out-of-range indices, and the expected value against
+    a float64 softmax (chessfly/model.py:107-110, 124-128)."""
+    from chessfly import _hip
+    lib = _hip.load()
+    rng = np.random.default_rng(batch)
+    logits = rng.normal(0, 4, (batch, n_moves)).astype(np.float32)
+    logits.flat[:5] = [65504.0, 65520.0, -1e6, np.nan, 2.0 ** -25]        # max half, tie to inf, -inf, NaN, tie to 0
+    logits.flat[-1] = 1.0 + 2.0 ** -11                                    # tie between 1 and 1 + 2^-10: rounds to 1
+    wdl = rng.normal(0, 3, (batch, 3)).astype(np.float32)
+    wdl[0] = [80.0, -80.0, 0.0]
+    lazy, values, bad = _evaluator_outputs(lib, _hip, logits, wdl)
+    want = logits.astype(np.float16)
+    assert bad == 0
+    assert np.array_equal(np.isnan(lazy), np.isnan(want))
+    assert np.array_equal(lazy.view(np.uint16)[~np.isnan(want)], want.view(np.uint16)[~np.isnan(want)])
+    assert np.isinf(lazy.flat[1]) and lazy.flat[2] == -np.inf and lazy.flat[4] == 0 and lazy.flat[-1] == 1
+    np.testing.assert_allclose(values, _softmax_value(wdl), rtol=0, atol=1e-6)
+    rows = np.concatenate([rng.integers(0, batch, 50), [-1, 0, -batch]])
+    cols = np.concatenate([rng.integers(0, n_moves, 50), [-1, -n_moves, 2]])
+    legal, values2, bad = _evaluator_outputs(lib, _hip, logits, wdl, rows, cols)
+    want = logits[rows, cols]                                             # numpy wraps negatives as torch does
+    assert bad == 0 and np.array_equal(legal.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(values2, values)
+    rows[3], cols[7] = batch, -n_moves - 1                                # out of range: NaN and the flag, no read
+    legal, _, bad = _evaluator_outputs(lib, _hip, logits, wdl, rows, cols)
+    assert bad == 1 and np.isnan(legal[3]) and np.isnan(legal[7])
+    keep = np.ones(len(rows), dtype=bool)
+    keep[[3, 7]] = False
+    assert np.array_equal(legal[keep].view(np.uint32), want[keep].view(np.uint32))
+    _, values3, bad = _evaluator_outputs(lib, _hip, logits, wdl, rows[:0], cols[:0])
+    assert bad == 0 and np.array_equal(values3, values)
+
+
 def test_evaluator_protocol(full_net):
-    """Evaluator.submit/result (chessfly/model.py:113-135): lazy fp16 policy vectors, eager legal gathers."""
+    """Evaluator.submit/result (chessfly/model.py:113-135): lazy fp16 policy vectors and eager legal gathers
+    agree with FlyChessNet.forward on the same boards; several batches may be in flight at once."""
     from chessfly.model import Evaluator
     from chessfly.synthetic import synthetic_boards
     from chessfly.encoding import N_MOVES
     net, _ = full_net
     ev = Evaluator(net, torch.device(DEV))
     x = synthetic_boards(9, seed=2).astype(np.float16)
+    with torch.no_grad():
+        logits, wdl = (t.cpu().numpy() for t in net(torch.as_tensor(x, device=DEV).float()))
     lazy_logits, values = ev(x, None, None)
     assert lazy_logits.shape == (9, N_MOVES) and lazy_logits.dtype == np.float16 and values.shape == (9,)
+    assert values.dtype == np.float32
+    assert np.array_equal(lazy_logits.view(np.uint16), logits.astype(np.float16).view(np.uint16))
+    np.testing.assert_allclose(values, _softmax_value(wdl), rtol=0, atol=1e-6)
     rows = np.repeat(np.arange(9), 5)
     cols = np.random.default_rng(0).integers(0, N_MOVES, size=45)
-    legal, values2 = ev(x, rows, cols)
+    first = ev.submit(x, rows, cols)                     # two batches in flight before either is read
+    second = ev.submit(x[:4], None, None)
+    legal, values2 = ev.result(first)
+    lazy4, values4 = ev.result(second)
     assert legal.dtype == np.float32 and legal.shape == (45,)
-    np.testing.assert_allclose(legal, lazy_logits[rows, cols].astype(np.float32), rtol=2e-3, atol=2e-3)
-    np.testing.assert_allclose(values, values2, rtol=1e-6)
+    assert np.array_equal(legal, logits[rows, cols])
+    assert np.array_equal(values2, values) and np.array_equal(values4, values[:4])
+    assert np.array_equal(lazy4, lazy_logits[:4])
     assert np.all(np.abs(values) <= 1)
+    legal0, values0 = ev(x, rows[:0], cols[:0])
+    assert legal0.shape == (0,) and np.array_equal(values0, values)
+    with pytest.raises(IndexError):
+        ev(x, np.array([9]), np.array([0]))
