@@ -91,6 +91,7 @@ struct StepArgs {
   int32_t slots;           // row slots per chunk: nrows, or ceil(nrows / G) when each wave takes G rows
   int32_t u_vec;           // the drive can be read with V-wide loads
   int32_t nt_store;        // write the new state with non-temporal stores
+  uint32_t xbytes;         // bytes of X_{t-1} (rows of X_{t-1} * ldx * sizeof(S)) when below 2^31, else 0
 };
 
 // Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
@@ -156,6 +157,33 @@ __device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row
   Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out, a.nt_store != 0);
 }
 
+// V elements of S at byte offset voff (per lane) + soff (wave-uniform) of a buffer: the source row's offset
+// stays a scalar operand, so a gather costs the vector ALU no address arithmetic, and offsets past the end
+// of the buffer read zeros instead of faulting.
+template <typename S, int V>
+__device__ __forceinline__ typename Lanes<S, V>::vec bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  typedef typename Lanes<S, V>::vec vec;
+  constexpr int kBytes = V * (int)sizeof(S);
+  if constexpr (kBytes == 32) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u8 __attribute__((ext_vector_type(8)));
+    const u4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const u4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+    return __builtin_bit_cast(vec, (u8)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  } else if constexpr (kBytes == 16) {
+    return __builtin_bit_cast(vec, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  } else if constexpr (kBytes == 8) {
+    return __builtin_bit_cast(vec, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+  } else if constexpr (kBytes == 4) {
+    return __builtin_bit_cast(vec, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  } else {
+    static_assert(kBytes == 2, "buffer gathers of 2, 4, 8, 16 or 32 bytes");
+    return __builtin_bit_cast(vec, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+  }
+}
+
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: 32-bit data, no swizzle
+
 // One non-zero at a time per wave: the {column, weight} pairs are wave-uniform scalar loads, every lane
 // gathers its V columns of the source row.  Chunk = 64 * V columns.
 template <typename S, typename U, int V, int UNROLL, bool TORCH_LERP>
@@ -205,6 +233,21 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc, in);
 }
 
+// Sum of v over the lanes l, l + LPG, l + 2 LPG, ... of the wave, exact in lanes 0 .. LPG-1: a DPP
+// rotation inside 16-lane rows for the stride of 8, then the permlane swaps across 16- and 32-lane halves
+// (the swapped-in half of the source register holds the partner lanes).  Pairs add in the same order as
+// a butterfly over strides 8, 16, 32.
+template <int LPG>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(LPG == 8 || LPG == 16 || LPG == 32, "lane groups of 8, 16 or 32");
+  if constexpr (LPG == 8)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
+  if constexpr (LPG <= 16)
+    v += __int_as_float(__builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
+  v += __int_as_float(__builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
+  return v;
+}
+
 // G non-zeros at a time per wave: the wave splits into G groups of 64/G lanes, group g gathers non-zero
 // e0 + j*G + g for the same chunk of (64/G) * V columns, so every load is V*sizeof(S) bytes per lane while
 // the chunk (and the gather working set of a sweep) is G times narrower.  Each lane reads its group's
@@ -240,14 +283,46 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
         cv[j] = e < end ? a.colval[e] : make_int2(0, 0);
       }
     };
+    // With the state below 2^31 bytes a gather's address is one 24-bit multiply-add into a buffer offset
+    // instead of a 64-bit product.
+    const bool buf = a.xbytes != 0;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
+    const uint32_t row_bytes = (uint32_t)a.ldx * (uint32_t)sizeof(S), voff = (uint32_t)lcol * (uint32_t)sizeof(S);
+    // The row's pairs as a buffer of (end - beg) records: pairs past the row's end read as {0, 0} with no
+    // bounds test, and the round's offset is a scalar operand.
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int2 *>(a.colval + beg), (short)0, (end - beg) * (int)sizeof(int2), kBufferWord3);
+    auto buf_pairs = [&](int32_t k, int2 (&cv)[UNROLL]) {
+#pragma unroll
+      for (int j = 0; j < UNROLL; ++j)
+        cv[j] = __builtin_bit_cast(int2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             rp, (j * G + g) * (int)sizeof(int2), k * (int)sizeof(int2), 0));
+    };
     int2 cv[UNROLL];
-    if (beg < end) pairs(beg, cv);
+    if (beg < end) {
+      if (buf)
+        buf_pairs(0, cv);
+      else
+        pairs(beg, cv);
+    }
     for (int32_t e0 = beg; e0 < end; e0 += G * UNROLL) {
       typename Lanes<S, V>::vec xr[UNROLL];
+      if (buf) {
 #pragma unroll
-      for (int j = 0; j < UNROLL; ++j) xr[j] = Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx);
+        for (int j = 0; j < UNROLL; ++j)
+          xr[j] = bload<S, V>(r, (int)(__umul24((uint32_t)cv[j].x, row_bytes) + voff), 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < UNROLL; ++j) xr[j] = Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx);
+      }
       int2 nx[UNROLL];
-      if (e0 + G * UNROLL < end) pairs(e0 + G * UNROLL, nx);
+      if (e0 + G * UNROLL < end) {
+        if (buf)
+          buf_pairs(e0 + G * UNROLL - beg, nx);
+        else
+          pairs(e0 + G * UNROLL, nx);
+      }
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) {
         const float wt = __int_as_float(cv[j].y);
@@ -258,9 +333,7 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
       for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
     }
 #pragma unroll
-    for (int off = LPG; off < 64; off <<= 1)
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += __shfl_xor(acc[i], off);
+    for (int i = 0; i < V; ++i) acc[i] = group_sum<LPG>(acc[i]);
   }
   if (g != 0 || !active) return;
   finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc, in);
@@ -304,13 +377,24 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
         cv[j] = e < end ? a.colval[e] : make_int2(0, 0);
       }
     };
+    const bool buf = a.xbytes != 0;   // 24-bit multiply-add buffer offsets, as in the grouped kernel
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
+    const uint32_t row_bytes = (uint32_t)a.ldx * (uint32_t)sizeof(S), voff = (uint32_t)lcol * (uint32_t)sizeof(S);
     int2 cv[UNROLL];
     if (len > 0) pairs(0, cv);
     for (int32_t k = 0; k < len; k += UNROLL) {
       typename Lanes<S, V>::vec xr[UNROLL];
+      if (buf) {
 #pragma unroll
-      for (int j = 0; j < UNROLL; ++j)
-        xr[j] = (beg + k + j < end) ? Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx) : Lanes<S, V>::zero();
+        for (int j = 0; j < UNROLL; ++j)
+          xr[j] = (beg + k + j < end) ? bload<S, V>(r, (int)(__umul24((uint32_t)cv[j].x, row_bytes) + voff), 0)
+                                      : Lanes<S, V>::zero();
+      } else {
+#pragma unroll
+        for (int j = 0; j < UNROLL; ++j)
+          xr[j] = (beg + k + j < end) ? Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx) : Lanes<S, V>::zero();
+      }
       int2 nx[UNROLL];
       if (k + UNROLL < len) pairs(k + UNROLL, nx);
 #pragma unroll
@@ -326,6 +410,7 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
   if (!active) return;
   finish_row<S, U, V, TORCH_LERP>(a, row, col, acc, in);
 }
+
 
 // Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
 // with torch.lerp's formula, like the reference's CPU path.
@@ -472,6 +557,12 @@ __global__ void k_zero_rows(float *__restrict__ h, int64_t ld, int64_t n, int64_
 
 int64_t state_ld(int64_t batch) { return round_up(batch, 64); }
 
+// Size of a state buffer for 32-bit buffer addressing, or 0 when it does not fit below 2^31 bytes.
+uint32_t buffer_bytes(int64_t rows, int64_t ld, size_t elem) {
+  const int64_t bytes = rows * ld * (int64_t)elem;
+  return bytes > 0 && bytes <= (int64_t)INT32_MAX ? (uint32_t)bytes : 0u;
+}
+
 size_t io_workspace(const fly_plan &plan, int64_t batch) {
   const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? 2 : 4;
   return 2 * (size_t)plan.max_rows * (size_t)state_ld(batch) * es + 256;
@@ -503,6 +594,7 @@ const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t b
     a.ldo = lds;
     a.nrows = (int32_t)nr;
     a.batch = (int32_t)batch;
+    a.xbytes = prev ? buffer_bytes(plan.rows_n[t - 1], lds, sizeof(S)) : 0;
     state_step(a, nr ? (double)plan.nnz[t] / (double)nr : 0.0, st);
     prev = buf[cur];
     cur ^= 1;
@@ -607,6 +699,7 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
       a.ldo = last ? ldh : lds;
       a.nrows = (int32_t)n;
       a.batch = (int32_t)batch;
+      a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
       state_step(a, (double)plan->nnz[0] / (double)n, st);
       prev = buf[cur];
       cur ^= 1;
