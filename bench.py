@@ -100,6 +100,37 @@ def cpu_baseline(net, conn, x_cpu, threads: int, prune: bool = True, seconds: fl
     return x.shape[0] / per, per, logits, wdl, len(times)
 
 
+def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> dict:
+    """GB/s of random 128-byte row gathers in the state step's access pattern (fly_gather_probe: 8 rows per
+    wave load, 16 bytes per lane), over working sets that fit one XCD's L2 (2 MB), the Infinity Cache (21 MB:
+    one 64-column chunk of all 166,700 state rows, what a sweep of the state step touches) and neither
+    (373 MB: the whole B=1120 fp16 state)."""
+    import torch
+    from chessfly import _hip
+    lib = _hip.load()
+    sink = torch.zeros(256, device=dev)
+    st = _hip.stream(dev)
+    out = {}
+    for name, rows in (("l2_2MB", 16384), ("infinity_cache_21MB", 166700), ("hbm_373MB", 166700 * 35 // 2)):
+        base = torch.randint(0, 256, (rows * 128,), dtype=torch.uint8, device=dev)
+        idx = torch.randint(0, rows, (n,), dtype=torch.int32, device=dev)
+
+        def once():
+            _hip.check(lib.fly_gather_probe(base.data_ptr(), base.numel(), 128, idx.data_ptr(), n, sink.data_ptr(),
+                                            st), "fly_gather_probe")
+        once()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            once()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(n * 128 / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9, 1)
+        del base, idx
+    return out
+
+
 def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> dict:
     """The search's view (chessfly/model.py:113-135): fp16 boards from host numpy through Evaluator.submit
     and result, one batch at a time, so the pinned H2D copy of the boards, the forward, the output kernel and
@@ -142,6 +173,8 @@ def main() -> int:
     ap.add_argument("--no-prune", action="store_true",
                     help="compute every neuron at every step (the same function without the light cone)")
     ap.add_argument("--cpu-boards", type=int, default=256, help="boards in the CPU baseline sample (0: skip)")
+    ap.add_argument("--no-gather-ceiling", action="store_true",
+                    help="skip the random-row gather probe that measures the state step's access-pattern ceiling")
     ap.add_argument("--evaluator-steps", type=int, default=10,
                     help="batches through Evaluator.submit/result from host numpy, PCIe included (0: skip)")
     ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
@@ -250,6 +283,11 @@ def main() -> int:
             roofline["traffic"] = measured["traffic_bytes_per_launch"]
             roofline["traffic_source"] = measured["source"]
     shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
+    if not args.no_gather_ceiling:
+        ceiling = gather_ceiling(dev)
+        roofline["gather_ceiling_GBps"] = ceiling
+        roofline["gather_frac_of_ceiling"] = round(roofline["gather_GBps"] / ceiling["infinity_cache_21MB"], 4)
+        log(f"random-row gather ceiling {ceiling} GB/s; state step gathers at {roofline['gather_GBps']} GB/s")
 
     evaluator = None
     if args.evaluator_steps > 0:

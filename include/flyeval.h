@@ -176,6 +176,13 @@ int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t
                           float *legal_dev, float *values_dev, int32_t *bad_dev, void *stream);
 
 /* ---- measurement ------------------------------------------------------------------------------- */
+/* No counterpart in the reference; for benchmarks.  The random-row gather rate of this GPU for the state
+ * step's access pattern: n reads of 128 bytes at byte offset idx[e] * row_bytes (16 bytes per lane, 8 rows
+ * per wave instruction) of base (`bytes` long).  Offsets past `bytes` read zeros, so any idx is safe.
+ * sink: 256 floats, written only if the data sum to a sentinel value. */
+int fly_gather_probe(const void *base_dev, int64_t bytes, int64_t row_bytes, const int32_t *idx_dev, int64_t n,
+                     float *sink_dev, void *stream);
+
 /* Kernel classes timed by the profiler. */
 enum fly_kernel_class {
     FLY_K_STATE_STEP = 0,   /* the fused SpMM + update step */
