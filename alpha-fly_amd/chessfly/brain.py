@@ -15,8 +15,11 @@ attributes).  What runs underneath is libflyeval.so:
 * `light_cone` (brain.py:126-173, 232-236): reach masks, row compaction and sub-matrix extraction on the
   device, integer and bit-exact with the reference's definition.
 
-Inference only: with autograd enabled (training, brain.py:66-99, 289-294) the forward methods raise.  The
-tensors must live on a HIP device; nothing here falls back to the CPU.
+Training (autograd enabled, brain.py:66-99, 225-229, 238-252, 289-329) runs the reference's float32
+recurrence under autograd with its sparse products on the device: `_SparseRecurrent` computes y = A h with
+fly_spmm, the state gradient A^T grad_y with fly_spmm over the transposed structure and the per-synapse
+gradient sum_b h[pre_e, b] grad_y[post_e, b] with fly_sddmm.  The tensors must live on a HIP device; nothing
+here falls back to the CPU.
 """
 
 from __future__ import annotations
@@ -37,10 +40,62 @@ def _crow(sorted_rows: torch.Tensor, n: int) -> torch.Tensor:
     return crow
 
 
-def _no_grad_only(what: str) -> None:
-    if torch.is_grad_enabled():
-        raise NotImplementedError(f"{what}: this evaluator is inference-only; run it under torch.no_grad() "
-                                  "(the training backward is not part of the HIP forward evaluator)")
+def _transpose_order(rows: torch.Tensor, cols: torch.Tensor, n_rows: int) -> torch.Tensor:
+    """Edge order of the transposed CSR: by column, then row, ties in edge order (brain.py:120, 190)."""
+    return torch.argsort(cols * n_rows + rows, stable=True)
+
+
+def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor) -> torch.Tensor:
+    """y (n_rows, B) = A x on the device (fly_spmm); x (n_cols, B) float32."""
+    x = x.contiguous()
+    batch = x.shape[1]
+    y = torch.empty(n_rows, batch, dtype=torch.float32, device=x.device)
+    _hip.check(_hip.load().fly_spmm(crow32.data_ptr(), col32.data_ptr(), val.data_ptr(), n_rows, n_cols, x.data_ptr(),
+                                    max(batch, 1), batch, y.data_ptr(), max(batch, 1), _hip.stream(x.device)),
+               "fly_spmm")
+    return y
+
+
+def _sddmm(crow32, col32, n_rows: int, n_cols: int, g: torch.Tensor, x: torch.Tensor, nnz: int) -> torch.Tensor:
+    """out[e] = sum_b g[row_e, b] x[col_e, b] on the device (fly_sddmm)."""
+    g, x = g.contiguous(), x.contiguous()
+    batch = x.shape[1]
+    out = torch.empty(nnz, dtype=torch.float32, device=x.device)
+    if nnz:
+        _hip.check(_hip.load().fly_sddmm(crow32.data_ptr(), col32.data_ptr(), n_rows, n_cols, g.data_ptr(),
+                                         max(batch, 1), x.data_ptr(), max(batch, 1), batch, out.data_ptr(),
+                                         _hip.stream(x.device)), "fly_sddmm")
+    return out
+
+
+class _SparseRecurrent(torch.autograd.Function):
+    """y = A h for A in CSR, the state (rows, batch) batch-fastest (brain.py:66-99).  Forward and the state
+    gradient are device SpMMs over A's structure and its transposed structure; the per-synapse gradient
+    dL/dw_e = sum_b h[col_e, b] grad_y[row_e, b] is a device SDDMM.  `op` is a ConnectomeRNN (the whole W)
+    or a _SubMatrix.  float32 only."""
+
+    @staticmethod
+    def forward(ctx, h, w, op):
+        if h.dtype != torch.float32 or w.dtype != torch.float32:
+            raise RuntimeError("training runs in float32: the state and the weights must be float32")
+        h = h.contiguous()
+        ctx.save_for_backward(h, w)
+        ctx.op = op
+        crow32, col32, n_rows, n_cols = op._structure()
+        return _spmm(crow32, col32, w.contiguous(), n_rows, n_cols, h)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        h, w = ctx.saved_tensors
+        op = ctx.op
+        grad_h = grad_w = None
+        crow32, col32, n_rows, n_cols = op._structure()
+        if ctx.needs_input_grad[0]:
+            t_crow32, t_col32, t_order = op._transposed()
+            grad_h = _spmm(t_crow32, t_col32, w[t_order].contiguous(), n_cols, n_rows, grad_y)
+        if ctx.needs_input_grad[1]:
+            grad_w = _sddmm(crow32, col32, n_rows, n_cols, grad_y, h, w.numel())
+        return grad_h, grad_w, None
 
 
 class _SubMatrix:
@@ -49,6 +104,7 @@ class _SubMatrix:
 
     def __init__(self, cone: "LightCone", t: int, n_rows: int, n_cols: int, nnz: int):
         self._cone, self._t, self._nnz = cone, t, nnz
+        self._tr = None
         self.shape = (n_rows, n_cols)
         self._data = None
 
@@ -59,10 +115,43 @@ class _SubMatrix:
             col = torch.empty(self._nnz, dtype=torch.int32, device=dev)
             edge = torch.empty(self._nnz, dtype=torch.int32, device=dev)
             self._cone._step_export(self._t, crow=crow, col=col, edge=edge)
-            crow = crow.long()
-            rows = torch.repeat_interleave(torch.arange(self.shape[0], device=dev), crow[1:] - crow[:-1])
-            self._data = (edge.long(), rows, col.long(), crow)
+            crow64 = crow.long()
+            rows = torch.repeat_interleave(torch.arange(self.shape[0], device=dev), crow64[1:] - crow64[:-1])
+            self._data = (edge.long(), rows, col.long(), crow64, crow, col)
         return self._data
+
+    def _structure(self):
+        d = self._load()
+        return d[4], d[5], self.shape[0], self.shape[1]
+
+    def _transposed(self):
+        """CSR of A^T (brain.py:120-121): order, int32 row pointer and columns, built on first use."""
+        if getattr(self, "_tr", None) is None:
+            post, pre = self.post, self.pre
+            order = _transpose_order(post, pre, self.shape[0])
+            t_crow = _crow(pre[order], self.shape[1])
+            t_col = post[order]
+            self._tr = (order, t_crow, t_col, t_crow.to(torch.int32), t_col.to(torch.int32))
+        return self._tr[3], self._tr[4], self._tr[0]
+
+    @property
+    def t_order(self) -> torch.Tensor:
+        self._transposed()
+        return self._tr[0]
+
+    @property
+    def t_crow(self) -> torch.Tensor:
+        self._transposed()
+        return self._tr[1]
+
+    @property
+    def t_col(self) -> torch.Tensor:
+        self._transposed()
+        return self._tr[2]
+
+    def csr_t(self, w: torch.Tensor) -> torch.Tensor:
+        return torch.sparse_csr_tensor(self.t_crow, self.t_col, w[self.t_order], self.shape[::-1],
+                                       check_invariants=False)
 
     @property
     def edges(self) -> torch.Tensor:
@@ -234,6 +323,13 @@ class ConnectomeRNN(nn.Module):
         # int32 copies of the CSR structure for the device library
         self.register_buffer("crow32", self.crow.to(torch.int32), persistent=False)
         self.register_buffer("pre32", conn.pre.to(torch.int32), persistent=False)
+        # CSR of W^T, for the state gradient of training (brain.py:190-193)
+        t_order = _transpose_order(conn.post, conn.pre, self.n)
+        self.register_buffer("t_order", t_order, persistent=False)
+        self.register_buffer("t_crow", _crow(conn.pre[t_order], self.n), persistent=False)
+        self.register_buffer("t_col", conn.post[t_order], persistent=False)
+        self.register_buffer("t_crow32", self.t_crow.to(torch.int32), persistent=False)
+        self.register_buffer("t_col32", self.t_col.to(torch.int32), persistent=False)
         self.log_gain = nn.Parameter(torch.zeros(conn.n_edges))
         self.bias = nn.Parameter(torch.full((self.n,), float(bias_init)))
         a = torch.full((self.n,), float(alpha_init))
@@ -253,7 +349,10 @@ class ConnectomeRNN(nn.Module):
                 raise RuntimeError(f"{what}: {name} must be a contiguous float32 tensor, got {t.dtype}")
 
     def edge_weights(self) -> torch.Tensor:
-        """sign * w0 * exp(log_gain) per edge, in CSR order (brain.py:201-202)."""
+        """sign * w0 * exp(log_gain) per edge, in CSR order (brain.py:201-202).  Under autograd, the
+        differentiable expression; otherwise one device kernel."""
+        if torch.is_grad_enabled() and self.log_gain.requires_grad:
+            return self.sign * self.w0 * torch.exp(self.log_gain)
         self._check_params("edge_weights")
         w = torch.empty_like(self.w0)
         dev = self.w0.device
@@ -263,6 +362,16 @@ class ConnectomeRNN(nn.Module):
 
     def csr(self, w: torch.Tensor) -> torch.Tensor:
         return torch.sparse_csr_tensor(self.crow, self.pre, w, (self.n, self.n), check_invariants=False)
+
+    def csr_t(self, w: torch.Tensor) -> torch.Tensor:
+        return torch.sparse_csr_tensor(self.t_crow, self.t_col, w[self.t_order], (self.n, self.n),
+                                       check_invariants=False)
+
+    def _structure(self):
+        return self.crow32, self.pre32, self.n, self.n
+
+    def _transposed(self):
+        return self.t_crow32, self.t_col32, self.t_order
 
     # ---- plans (everything that depends on the weights only; rebuilt when a parameter changes) -------
     def _plan(self, key_extra, build):
@@ -301,9 +410,10 @@ class ConnectomeRNN(nn.Module):
         """u: (N, B) contiguous constant external drive.  Returns the state after `steps` updates, (N, B).
         As in the reference's inference path, u is updated in place to u + bias (brain.py:218)."""
         assert u.is_contiguous()
-        _no_grad_only("ConnectomeRNN.forward")
         _hip.require_device(u, "ConnectomeRNN.forward")
         self._check_params("ConnectomeRNN.forward")
+        if torch.is_grad_enabled():
+            return self._forward_autograd(u, steps)
         if u.dtype != torch.float32 or u.dim() != 2 or u.shape[0] != self.n:
             raise RuntimeError(f"ConnectomeRNN.forward: u must be float32 ({self.n}, B), got {u.dtype} {tuple(u.shape)}")
         lib = _hip.load()
@@ -315,6 +425,59 @@ class ConnectomeRNN(nn.Module):
                                            h.data_ptr(), batch, ws.data_ptr(), ws.numel(), _hip.stream(u.device)),
                    "fly_forward_literal")
         return h
+
+    def _forward_autograd(self, u: torch.Tensor, steps: int) -> torch.Tensor:
+        """The literal recurrence under autograd, float32 (brain.py:225-229); u is not modified."""
+        if u.dtype != torch.float32:
+            raise RuntimeError(f"ConnectomeRNN.forward under autograd runs in float32, got {u.dtype}")
+        alpha = torch.sigmoid(self.alpha_logit).unsqueeze(1)
+        w = self.edge_weights()
+        drive = self.bias.unsqueeze(1) + u
+        h = torch.zeros_like(drive)
+        for _ in range(steps):
+            x = (_SparseRecurrent.apply(h, w, self) + drive).clamp(0, self.h_max)
+            h = torch.lerp(h, x, alpha)
+        return h
+
+    def _constants(self, cone: LightCone, w: torch.Tensor, alpha: torch.Tensor):
+        """The resting trajectory c_0..c_T of a network that sees no position and, per step, the drive the
+        rows of R_t get from outside the cone, k_t = (W c_{t-1} + b)[R_t] - A_t c_{t-1}[R_{t-1}]
+        (brain.py:238-252), under autograd.  W c_0 = 0."""
+        c = torch.zeros(self.n, 1, dtype=w.dtype, device=w.device)
+        cs, ks = [c], [None]
+        bias = self.bias.unsqueeze(1)
+        for t in range(1, cone.steps + 1):
+            full = (_SparseRecurrent.apply(c, w, self) if t > 1 else torch.zeros_like(c)) + bias
+            k = full[cone.rows[t]]
+            op = cone.ops[t]
+            if op is not None:
+                k = k - _SparseRecurrent.apply(c[cone.rows[t - 1]], w[op.edges], op)
+            ks.append(k)
+            c = torch.lerp(c, full.clamp(0, self.h_max), alpha)
+            cs.append(c)
+        return cs, ks
+
+    def _forward_io_autograd(self, u_in: torch.Tensor, cone: LightCone, out_idx: torch.Tensor,
+                             steps: int) -> torch.Tensor:
+        """forward_io under autograd, float32 (brain.py:289-329): rows outside R_t follow the resting
+        trajectory, rows of R_t take the sub-matrix product plus their constant drive and input."""
+        if u_in.dtype != torch.float32:
+            raise RuntimeError(f"forward_io under autograd runs in float32, got {u_in.dtype}")
+        batch = u_in.shape[1]
+        w = self.edge_weights()
+        alpha = torch.sigmoid(self.alpha_logit).unsqueeze(1)
+        cs, ks = self._constants(cone, w, alpha)
+        h = None
+        for t in range(1, steps + 1):
+            rows, op = cone.rows[t], cone.ops[t]
+            x = ks[t].expand(-1, batch) if op is None else _SparseRecurrent.apply(h, w[op.edges], op) + ks[t]
+            x = x.index_add(0, cone.u_pos[t], u_in[cone.u_src[t]]).clamp(0, self.h_max)
+            prev = cs[t - 1][rows].expand(-1, batch)
+            if len(cone.keep_next[t]):
+                prev = prev.index_copy(0, cone.keep_next[t], h[cone.keep_prev[t]])
+            h = torch.lerp(prev, x, alpha[rows])
+        out = cs[steps][out_idx].expand(-1, batch)
+        return out.index_copy(0, cone.out_pos, h[cone.out_src])
 
     # ---- the same function through the light cone ------------------------------------------------
     def light_cone(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int, prune: bool = True) -> LightCone:
@@ -330,10 +493,15 @@ class ConnectomeRNN(nn.Module):
     def forward_io(self, u_in: torch.Tensor, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> torch.Tensor:
         """u_in: (len(in_idx), B) drive of the input neurons.  Returns the output neurons after `steps`
         updates, (len(out_idx), B): forward(u, steps)[out_idx] with u zero outside in_idx.  float16 u_in
-        takes the deviation path and returns float32; float32 u_in takes the float32 path."""
-        _no_grad_only("ConnectomeRNN.forward_io")
+        takes the deviation path and returns float32; float32 u_in takes the float32 path.  Under autograd the
+        float32 light cone runs differentiably (training)."""
         _hip.require_device(u_in, "ConnectomeRNN.forward_io")
         self._check_params("ConnectomeRNN.forward_io")
+        if torch.is_grad_enabled():
+            if u_in.dim() != 2 or u_in.shape[0] != len(in_idx):
+                raise RuntimeError(f"forward_io: u_in must be (len(in_idx), B), got {tuple(u_in.shape)}")
+            cone = self.light_cone(in_idx, out_idx, steps)
+            return self._forward_io_autograd(u_in, cone, out_idx, steps)
         if u_in.dtype == torch.float16:
             mode = _hip.MODE_DEVIATION_F16
         elif u_in.dtype == torch.float32:

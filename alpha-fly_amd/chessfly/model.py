@@ -4,10 +4,12 @@
                    --RunningNorm--> move logits (+ from/to-square terms), WDL logits
 
 Drop-in for chessfly/model.py of the reference (ModelConfig, RunningNorm, FlyChessNet, Evaluator,
-load_weights): same constructor, parameters, state_dict keys and forward signature.  FlyChessNet.forward
-runs as one call into libflyeval.so (fly_model_forward): the encoder GEMM on the matrix cores, the light-cone
-recurrence (float16 deviation path when `infer_dtype` is float16, float32 otherwise), and the head GEMMs whose
-operand loader gathers the output neurons and applies the eval-mode normaliser in place.
+load_weights): same constructor, parameters, state_dict keys and forward signature.  In evaluation (eval
+mode, autograd off) FlyChessNet.forward runs as one call into libflyeval.so (fly_model_forward): the encoder
+GEMM on the matrix cores, the light-cone recurrence (float16 deviation path when `infer_dtype` is float16,
+float32 otherwise), and the head GEMMs whose operand loader gathers the output neurons and applies the
+eval-mode normaliser in place.  In training it runs the same layers separately, differentiably, with the
+recurrence's sparse products on the device (ConnectomeRNN.forward_io under autograd).
 """
 
 from __future__ import annotations
@@ -20,7 +22,7 @@ import torch
 from torch import nn
 
 from . import _hip
-from .brain import ConnectomeRNN, _no_grad_only
+from .brain import ConnectomeRNN
 from .connectome import Connectome
 from .encoding import N_BASE, N_FEATURES, N_MOVES, move_squares
 
@@ -121,13 +123,30 @@ class FlyChessNet(nn.Module):
         self._dense_cache = _hip.Handle(handle, "fly_dense_destroy", key)
         return self._dense_cache
 
+    def _forward_layers(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """The forward as separate differentiable layers (chessfly/model.py:95-105): training, or any call
+        with autograd enabled.  Under autograd the recurrence is float32 (its sparse products on the device);
+        without it, in training mode, the recurrence is the fused device forward_io in infer_dtype and the
+        normaliser updates its running statistics."""
+        dtype = torch.float32 if torch.is_grad_enabled() else self.infer_dtype
+        if x.dtype != torch.float32:
+            x = x.float()
+        if self.cfg.attack_planes:
+            enc = self.encoder(x)
+        else:                                   # the attack planes are never seen and their weights get no gradient
+            enc = nn.functional.linear(x[:, :N_BASE], self.encoder.weight[:, :N_BASE], self.encoder.bias)
+        u_in = (enc * self.cfg.input_gain).to(dtype).T.contiguous()
+        r = self.norm(self.brain.forward_io(u_in, self.in_idx, self.out_idx, self.cfg.steps).T.float())
+        logits = self.policy(r) + self.policy_from(r)[:, self.move_from] + self.policy_to(r)[:, self.move_to]
+        return logits, self.value(r)
+
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """x: (B, >= N_BASE) -> policy logits (B, N_MOVES), WDL logits (B, 3), both float32.  Half-precision
-        boards (what the search sends) are read as they are: widening them to float32 is exact."""
-        _no_grad_only("FlyChessNet.forward")
+        boards (what the search sends) are read as they are: widening them to float32 is exact.  Evaluation
+        (eval mode, no autograd) is one fused device call; training goes through the layers."""
         _hip.require_device(x, "FlyChessNet.forward")
-        if self.training:
-            raise NotImplementedError("FlyChessNet.forward: the evaluator runs the eval-mode normaliser; call .eval()")
+        if torch.is_grad_enabled() or self.training:
+            return self._forward_layers(x)
         dtype = self.infer_dtype
         if dtype not in (torch.float16, torch.float32):
             raise RuntimeError(f"infer_dtype must be float16 or float32, got {dtype}")

@@ -4,12 +4,12 @@
 // spends 8 FMAs).  Timing it over working sets that fit the L2, the Infinity Cache or neither gives the
 // random-line gather rate the state step can at best reach.
 #include "common.hpp"
+#include "device.hpp"
 
 namespace fly {
 namespace {
 
 constexpr int kRoundsPerWave = 64;
-constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: 32-bit data, no swizzle
 
 __global__ __launch_bounds__(256) void k_gather_probe(const char *base, uint32_t bytes, uint32_t row_bytes,
                                                       const int32_t *__restrict__ idx, int64_t n,

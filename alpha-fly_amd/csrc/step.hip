@@ -17,6 +17,7 @@
 // tile of batch columns is swept over all rows before the next, so the previous state's working set of one
 // sweep is the tile's columns only (sized to stay in the 256 MB Infinity Cache at large batches).
 #include "common.hpp"
+#include "device.hpp"
 
 namespace fly {
 
@@ -182,7 +183,6 @@ __device__ __forceinline__ typename Lanes<S, V>::vec bload(__amdgpu_buffer_rsrc_
   }
 }
 
-constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: 32-bit data, no swizzle
 
 // One non-zero at a time per wave: the {column, weight} pairs are wave-uniform scalar loads, every lane
 // gathers its V columns of the source row.  Chunk = 64 * V columns.
@@ -233,20 +233,6 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc, in);
 }
 
-// Sum of v over the lanes l, l + LPG, l + 2 LPG, ... of the wave, exact in lanes 0 .. LPG-1: a DPP
-// rotation inside 16-lane rows for the stride of 8, then the permlane swaps across 16- and 32-lane halves
-// (the swapped-in half of the source register holds the partner lanes).  Pairs add in the same order as
-// a butterfly over strides 8, 16, 32.
-template <int LPG>
-__device__ __forceinline__ float group_sum(float v) {
-  static_assert(LPG == 8 || LPG == 16 || LPG == 32, "lane groups of 8, 16 or 32");
-  if constexpr (LPG == 8)
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
-  if constexpr (LPG <= 16)
-    v += __int_as_float(__builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
-  v += __int_as_float(__builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
-  return v;
-}
 
 // G non-zeros at a time per wave: the wave splits into G groups of 64/G lanes, group g gathers non-zero
 // e0 + j*G + g for the same chunk of (64/G) * V columns, so every load is V*sizeof(S) bytes per lane while

@@ -24,6 +24,7 @@
  *   fly_model_forward     chessfly/model.py:95-105 FlyChessNet.forward (no-grad, device inputs)
  *   fly_evaluator_outputs chessfly/model.py:120-128 and :107-110 (Evaluator.submit's half cast or legal gather,
  *                         expected_value)
+ *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
  */
 #ifndef FLYEVAL_H
 #define FLYEVAL_H
@@ -174,6 +175,20 @@ int fly_model_forward(const fly_plan *plan, const fly_dense *dense, const void *
 int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t batch, int64_t n_moves,
                           const int64_t *rows_dev, const int64_t *cols_dev, int64_t n_legal, void *logits16_dev,
                           float *legal_dev, float *values_dev, int32_t *bad_dev, void *stream);
+
+/* ---- training: the sparse products of the differentiable recurrence ----------------------------- */
+/* chessfly/brain.py:66-99 (_SparseRecurrent), float32.  A is CSR (rowptr nrows+1, col/val nnz, int32 and
+ * float); operands are row-major with the batch fastest.
+ *   fly_spmm:  y (nrows, ldy) = A x, x (ncols, ldx).  The forward product, and with the transposed
+ *              structure of A (and its values in that order) the state gradient A^T grad_y.
+ *   fly_sddmm: out[e] = sum_b g[row_e, b] x[col_e, b] for every non-zero e, CSR order: the per-synapse
+ *              gradient of y = A x with g = dL/dy.  out must not overlap g.
+ * Gathered operands must be below 2 GiB; rows and columns below 2^24; column indices are not range-checked
+ * (a wrong index reads wrong data, never outside x). */
+int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, int64_t nrows, int64_t ncols,
+             const float *x_dev, int64_t ldx, int64_t batch, float *y_dev, int64_t ldy, void *stream);
+int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
+              int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, void *stream);
 
 /* ---- measurement ------------------------------------------------------------------------------- */
 /* No counterpart in the reference; for benchmarks.  The random-row gather rate of this GPU for the state

@@ -65,8 +65,10 @@ def test_product_refuses_cpu_tensors():
             rnn(torch.zeros(30, 4), 3)
         with pytest.raises(RuntimeError, match="HIP device"):
             rnn.forward_io(torch.zeros(5, 4), torch.arange(5), torch.arange(25, 30), 3)
-    with pytest.raises(NotImplementedError):
-        rnn(torch.zeros(30, 4), 3)                              # grad mode: training is not part of the evaluator
+    with pytest.raises(RuntimeError, match="HIP device"):
+        rnn(torch.zeros(30, 4), 3)                              # the training path refuses the host as well
+    with pytest.raises(RuntimeError, match="HIP device"):
+        rnn.forward_io(torch.zeros(5, 4), torch.arange(5), torch.arange(25, 30), 3)
 
 
 def test_evaluator_outputs_checks_arguments_on_host(lib):

@@ -95,9 +95,12 @@ def test_expected_value():
     np.testing.assert_allclose(FlyChessNet.expected_value(wdl).numpy(), p[:, 0] - p[:, 2], rtol=1e-6)
 
 
-def test_forward_refuses_without_device_or_in_training():
+def test_forward_refuses_host_tensors_in_every_mode():
     net = _net().eval()
     with torch.no_grad(), pytest.raises(RuntimeError, match="HIP device"):
         net(torch.zeros(2, 967))
-    with pytest.raises(NotImplementedError):
-        net(torch.zeros(2, 967))                          # autograd on: training is not part of the evaluator
+    with pytest.raises(RuntimeError, match="HIP device"):
+        net(torch.zeros(2, 967))                          # autograd on: the training path is device-only too
+    net.train()
+    with torch.no_grad(), pytest.raises(RuntimeError, match="HIP device"):
+        net(torch.zeros(2, 967))

@@ -1,0 +1,223 @@
+"""GPU tests of the training path: the device sparse products (fly_spmm, fly_sddmm, through the C ABI and
+through _SparseRecurrent) and the gradients of ConnectomeRNN.forward / forward_io / FlyChessNet.forward
+under autograd, against the CPU training oracle (float64)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import brain_arrays, random_params, tiny_connectome
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _close(got: torch.Tensor, ref: torch.Tensor, rel: float, what: str) -> None:
+    """max |got - ref| within rel * max |ref| (float32 device arithmetic against a float64 oracle)."""
+    got, ref = got.detach().double().cpu(), ref.detach().double().cpu()
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    scale = float(ref.abs().max()) if ref.numel() else 0.0
+    err = float((got - ref).abs().max()) if ref.numel() else 0.0
+    assert err <= rel * scale + 1e-30, f"{what}: max error {err:.3e} against max {scale:.3e}"
+
+
+def _random_csr(rows: int, cols: int, nnz: int, seed: int):
+    """Row-sorted non-zeros with empty rows, columns never used and repeated (row, column) pairs."""
+    rng = np.random.default_rng(seed)
+    r = np.sort(rng.integers(0, max(rows - 2, 1), nnz))          # the last rows stay empty
+    c = rng.integers(0, max(cols - 1, 1), nnz)                   # the last column is never read
+    c[1::7] = c[::7][:len(c[1::7])]
+    r[1::7] = r[::7][:len(r[1::7])]                               # repeats of the previous pair
+    order = np.lexsort((c, r))
+    r, c = r[order], c[order]
+    crow = np.zeros(rows + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=rows), out=crow[1:])
+    return crow, r, c, rng.normal(0, 1, nnz)
+
+
+@pytest.mark.parametrize("batch,ld_pad", [(1, 0), (3, 0), (5, 3), (64, 0), (256, 0), (130, 2)])
+def test_spmm_and_sddmm_match_float64(batch, ld_pad):
+    """y = A x and out[e] = sum_b g[row_e, b] x[col_e, b] against float64, on 4-byte and 16-byte lanes."""
+    from chessfly import _hip
+    lib = _hip.load()
+    rows, cols, nnz = 700, 500, 9000
+    crow, r, c, val = _random_csr(rows, cols, nnz, batch)
+    rng = np.random.default_rng(batch + 1)
+    x = rng.normal(0, 1, (cols, batch + ld_pad))
+    g = rng.normal(0, 1, (rows, batch + ld_pad))
+    dense = np.zeros((rows, cols))
+    np.add.at(dense, (r, c), val)
+    d32 = lambda a, dt=torch.int32: torch.as_tensor(np.ascontiguousarray(a), device=DEV).to(dt)
+    crow_d, col_d, val_d = d32(crow), d32(c), d32(val, torch.float32)
+    x_d, g_d = d32(x, torch.float32), d32(g, torch.float32)
+    ld = batch + ld_pad
+    y = torch.full((rows, ld), 7.0, device=DEV)
+    st = _hip.stream(torch.device(DEV))
+    _hip.check(lib.fly_spmm(crow_d.data_ptr(), col_d.data_ptr(), val_d.data_ptr(), rows, cols, x_d.data_ptr(), ld,
+                            batch, y.data_ptr(), ld, st), "fly_spmm")
+    ref = dense @ x[:, :batch]
+    _close(y[:, :batch], torch.as_tensor(ref), 1e-5, "spmm")
+    if ld_pad:
+        assert bool((y[:, batch:] == 7.0).all())                # padding columns are not written
+    out = torch.empty(nnz, device=DEV)
+    _hip.check(lib.fly_sddmm(crow_d.data_ptr(), col_d.data_ptr(), rows, cols, g_d.data_ptr(), ld, x_d.data_ptr(), ld,
+                             batch, out.data_ptr(), st), "fly_sddmm")
+    ref_w = (g[r, :batch] * x[c, :batch]).sum(1)
+    _close(out, torch.as_tensor(ref_w), 1e-5, "sddmm")
+
+
+def _rnn_pair(conn, seed: int, scale: float = 3.0):
+    from chessfly.brain import ConnectomeRNN
+    lg, bias, al = random_params(conn, seed)
+    rnn = ConnectomeRNN(conn, global_scale=scale).to(DEV)
+    with torch.no_grad():
+        rnn.log_gain.copy_(torch.as_tensor(lg))
+        rnn.bias.copy_(torch.as_tensor(bias))
+        rnn.alpha_logit.copy_(torch.as_tensor(al))
+    b = brain_arrays(conn, scale, lg, bias, al, dtype=torch.double)
+    for name in ("log_gain", "bias", "alpha_logit"):
+        setattr(b, name, getattr(b, name).clone().requires_grad_(True))
+    return rnn, b
+
+
+def _device_grads(rnn, *extra):
+    return [t.grad for t in (*extra, rnn.log_gain, rnn.bias, rnn.alpha_logit)]
+
+
+def test_forward_gradients_match_the_oracle():
+    """ConnectomeRNN.forward under autograd: the state and the gradients of u, log_gain, bias and alpha_logit
+    (chessfly/brain.py:224-229 with _SparseRecurrent, 66-99)."""
+    from oracle import training as T
+    conn = tiny_connectome(200, 3000, seed=1)
+    rnn, b = _rnn_pair(conn, 2)
+    rng = np.random.default_rng(3)
+    u = rng.random((conn.n_neurons, 16))
+    target = rng.random((conn.n_neurons, 16))
+    u_d = torch.tensor(u, dtype=torch.float32, device=DEV, requires_grad=True)
+    out = rnn(u_d, 4)
+    ((out - torch.as_tensor(target, dtype=torch.float32, device=DEV)) ** 2).sum().backward()
+    u_r = torch.tensor(u, requires_grad=True)
+    ref = T.literal_grad(b, u_r, 4)
+    ((ref - torch.as_tensor(target)) ** 2).sum().backward()
+    _close(out, ref, 2e-6, "state")
+    for got, want, name in zip(_device_grads(rnn, u_d), (u_r.grad, b.log_gain.grad, b.bias.grad, b.alpha_logit.grad),
+                               ("u", "log_gain", "bias", "alpha_logit")):
+        _close(got, want, 5e-5, name)
+    assert float(rnn.log_gain.grad.abs().sum()) > 0
+
+
+@pytest.mark.parametrize("steps", [1, 2, 4, 6])
+def test_forward_io_gradients_match_the_oracle_and_the_full_recurrence(steps):
+    """forward_io under autograd (the light cone, chessfly/brain.py:289-329) against the oracle, and against
+    forward()[out_idx] on the device: the same function with every gradient."""
+    from oracle import training as T
+    from oracle.lightcone import light_cone
+    conn = tiny_connectome(120, 700, seed=3)
+    rnn, b = _rnn_pair(conn, 4)
+    in_idx, out_idx = torch.arange(0, 9, device=DEV), torch.arange(100, 120, device=DEV)
+    rng = np.random.default_rng(steps)
+    u_in = rng.normal(0, 1, (9, 5))
+    target = torch.as_tensor(rng.normal(0, 1, (20, 5)))
+    results = []
+    for mode in ("full", "cone"):
+        rnn.zero_grad()
+        u_d = torch.tensor(u_in, dtype=torch.float32, device=DEV, requires_grad=True)
+        if mode == "full":
+            u = torch.zeros(conn.n_neurons, 5, device=DEV).index_add(0, in_idx, u_d)
+            out = rnn(u.contiguous(), steps)[out_idx]
+        else:
+            out = rnn.forward_io(u_d, in_idx, out_idx, steps)
+        ((out - target.float().to(DEV)) ** 2).sum().backward()
+        results.append([out.detach()] + [g.clone() if g is not None else None for g in _device_grads(rnn, u_d)])
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), np.arange(9), np.arange(100, 120), steps)
+    u_r = torch.tensor(u_in, requires_grad=True)
+    ref = T.cone_grad(b, cone, u_r)
+    ((ref - target) ** 2).sum().backward()
+    refs = [ref.detach(), u_r.grad, b.log_gain.grad, b.bias.grad, b.alpha_logit.grad]
+    names = ("out", "u_in", "log_gain", "bias", "alpha_logit")
+    for got_full, got_cone, want, name in zip(results[0], results[1], refs, names):
+        if want is None:                                      # one step never uses W
+            assert got_cone is None or float(got_cone.abs().max()) == 0.0
+            continue
+        _close(got_cone, want, 5e-5, f"cone {name}")
+        _close(got_full, want, 5e-5, f"full {name}")
+
+
+def test_train_step_gradients_match_the_oracle():
+    """One train_step loss (chessfly/train.py:126-132) through FlyChessNet under autograd on a 3,000-neuron
+    synthetic graph: every parameter's gradient against the oracle in float64."""
+    from chessfly.encoding import N_BASE, N_MOVES
+    from chessfly.model import FlyChessNet, ModelConfig
+    from chessfly.synthetic import GraphSpec, synthetic_boards, synthetic_connectome
+    from oracle import training as T
+    from oracle.forward import HeadArrays
+    from oracle.lightcone import light_cone
+    spec = GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=100, seed=5)
+    conn = synthetic_connectome(spec)
+    torch.manual_seed(0)
+    net = FlyChessNet(conn, ModelConfig(steps=4)).to(DEV).eval()
+    with torch.no_grad():
+        for p in net.parameters():
+            p.add_(torch.randn_like(p) * 0.05)
+    batch = 12
+    x = torch.as_tensor(synthetic_boards(batch, seed=3), dtype=torch.float32)
+    rng = np.random.default_rng(0)
+    legal = torch.as_tensor(rng.random((batch, N_MOVES)) < 0.01)
+    legal[:, 0] = True
+    pi = torch.where(legal, torch.as_tensor(rng.random((batch, N_MOVES))), torch.zeros(()))
+    pi = pi / pi.sum(1, keepdim=True)
+    wdl = torch.as_tensor(rng.integers(0, 3, batch))
+    net.zero_grad()
+    logits, wdl_logits = net(x.to(DEV))
+    T.train_loss(logits, wdl_logits, pi.float().to(DEV), legal.to(DEV), wdl.to(DEV)).backward()
+
+    brain = net.brain
+    d = lambda t: t.detach().double().cpu().clone().requires_grad_(True)
+    b = brain_arrays(conn, net.cfg.weight_scale, brain.log_gain.detach().cpu(), brain.bias.detach().cpu(),
+                     brain.alpha_logit.detach().cpu(), dtype=torch.double)
+    for name in ("log_gain", "bias", "alpha_logit"):
+        setattr(b, name, getattr(b, name).clone().requires_grad_(True))
+    hp = HeadArrays(d(net.encoder.weight), d(net.encoder.bias), net.cfg.input_gain, N_BASE, d(net.policy.weight),
+                    d(net.policy.bias), d(net.policy_from.weight), d(net.policy_from.bias), d(net.policy_to.weight),
+                    d(net.policy_to.bias), d(net.value.weight), d(net.value.bias), net.move_from.cpu(),
+                    net.move_to.cpu(), net.norm.mean.double().cpu(), net.norm.var.double().cpu())
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), net.in_idx.cpu().numpy(),
+                      net.out_idx.cpu().numpy(), net.cfg.steps)
+    rl, rw = T.model_grad(hp, b, cone, x.double())
+    T.train_loss(rl, rw, pi.double(), legal, wdl).backward()
+    _close(logits, rl, 1e-5, "logits")
+    pairs = [(net.encoder.weight.grad[:, :N_BASE], hp.enc_w.grad[:, :N_BASE], "encoder.weight"),
+             (net.encoder.bias.grad, hp.enc_b.grad, "encoder.bias"),
+             (brain.log_gain.grad, b.log_gain.grad, "brain.log_gain"), (brain.bias.grad, b.bias.grad, "brain.bias"),
+             (brain.alpha_logit.grad, b.alpha_logit.grad, "brain.alpha_logit"),
+             (net.policy.weight.grad, hp.policy_w.grad, "policy.weight"),
+             (net.policy_from.weight.grad, hp.from_w.grad, "policy_from.weight"),
+             (net.policy_to.bias.grad, hp.to_b.grad, "policy_to.bias"),
+             (net.value.weight.grad, hp.value_w.grad, "value.weight")]
+    for got, want, name in pairs:
+        assert float(want.abs().max()) > 0, name
+        _close(got, want, 2e-4, name)
+    assert float(net.encoder.weight.grad[:, N_BASE:].abs().sum()) == 0   # attack planes off: no gradient
+
+
+def test_training_mode_without_autograd_updates_the_normaliser_and_matches_eval():
+    """Training mode with autograd off (the reference's self-play-time calls between steps) runs the fused
+    recurrence, then the normaliser updates its running statistics as RunningNorm does."""
+    from chessfly.model import FlyChessNet, ModelConfig
+    from chessfly.synthetic import GraphSpec, synthetic_boards, synthetic_connectome
+    conn = synthetic_connectome(GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=100, seed=6))
+    net = FlyChessNet(conn, ModelConfig(steps=4)).to(DEV)
+    with torch.no_grad():                       # the zero-initialised heads would hide the normaliser
+        for layer in (net.policy, net.value):
+            layer.weight.normal_(0, 0.1)
+    x = torch.as_tensor(synthetic_boards(16, seed=2), dtype=torch.float32, device=DEV)
+    net.train()
+    with torch.no_grad():
+        logits_train, _ = net(x)
+    assert bool(net.norm.initialised) and float(net.norm.mean.abs().sum()) > 0
+    net.eval()
+    with torch.no_grad():
+        logits_eval, _ = net(x)
+    _close(logits_eval, logits_train, 2e-3, "eval after the first training-mode call")
