@@ -263,6 +263,21 @@ class Evaluator:
 NEW_HEADS = ("policy_from.", "policy_to.")
 
 
+def load_net(path, data_dir: str = "data", device="cuda", conn: Connectome | None = None) -> FlyChessNet:
+    """The network of a checkpoint or snapshot, ready to evaluate (chessfly/model.py:154-161): a dict with
+    "config" (ModelConfig fields) and "model" (the state dict), read with torch.load(weights_only=True).  The
+    connectome is `conn` or, as in the reference, the MaleCNS release in data_dir (chessfly.connectome.
+    load_malecns, local files only)."""
+    ck = torch.load(path, map_location="cpu", weights_only=True)
+    cfg = ModelConfig(**ck["config"])
+    if conn is None:
+        from .connectome import load_malecns
+        conn = load_malecns(data_dir, cfg.min_syn)
+    net = FlyChessNet(conn, cfg)
+    load_weights(net, ck["model"])
+    return net.to(device).eval()
+
+
 def load_weights(net: FlyChessNet, state: dict) -> None:
     """Load a state dict (chessfly/model.py:141-151): an encoder saved before the attack planes is padded
     with zero columns, and the zero-initialised from/to heads may be missing; nothing else may be."""

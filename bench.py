@@ -100,6 +100,135 @@ def cpu_baseline(net, conn, x_cpu, threads: int, prune: bool = True, seconds: fl
     return x.shape[0] / per, per, logits, wdl, len(times)
 
 
+def _train_targets(batch: int, dev, seed: int = 4):
+    """Synthetic train_step targets (chessfly/train.py:113-124): ~30 legal moves per position with a visit
+    distribution over them, and a WDL class."""
+    import numpy as np
+    import torch
+    from chessfly.encoding import N_MOVES
+    rng = np.random.default_rng(seed)
+    legal = rng.random((batch, N_MOVES)) < 30 / N_MOVES
+    legal[:, 0] = True
+    pi = np.where(legal, rng.random((batch, N_MOVES)), 0.0)
+    pi /= pi.sum(1, keepdims=True)
+    t = lambda a, dt: torch.as_tensor(a, dtype=dt, device=dev)
+    return t(pi, torch.float32), t(legal, torch.bool), t(rng.integers(0, 3, batch), torch.long)
+
+
+def _train_loss(logits, wdl_logits, pi, legal, wdl):
+    """policy_loss + value_loss of train_step with q_ratio 0 (chessfly/train.py:126-132)."""
+    import torch.nn.functional as F
+    logp = logits.masked_fill(~legal, -1e9).log_softmax(-1)
+    return -(pi * logp).sum(-1).mean() + F.cross_entropy(wdl_logits, wdl)
+
+
+def cpu_train_baseline(net, conn, x_cpu, threads: int, seconds: float = 15.0):
+    """The reference's training forward + backward on the host cores (the float32 light cone under autograd
+    with the CPU branch of _SparseRecurrent, chessfly/brain.py:66-99, 289-329; model.py:95-105), on the
+    oracle's restatement with the net's current parameters; returns (positions/s, seconds, repetitions)."""
+    import warnings
+
+    import torch
+    warnings.filterwarnings("ignore", message="Sparse CSR tensor support is in beta")
+    from chessfly.encoding import N_BASE
+    from oracle import forward as F
+    from oracle import training as T
+    from oracle.lightcone import light_cone
+
+    torch.set_num_threads(threads)
+    leaf = lambda p: p.detach().float().cpu().clone().requires_grad_(True)
+    brain = net.brain
+    w0 = F.normalised_weight(conn.n_neurons, conn.post, conn.syn_count) * net.cfg.weight_scale
+    ba = F.BrainArrays(conn.n_neurons, conn.pre, conn.post, conn.sign, w0, leaf(brain.log_gain), leaf(brain.bias),
+                       leaf(brain.alpha_logit))
+    hp = F.HeadArrays(leaf(net.encoder.weight), leaf(net.encoder.bias), net.cfg.input_gain, N_BASE,
+                      leaf(net.policy.weight), leaf(net.policy.bias), leaf(net.policy_from.weight),
+                      leaf(net.policy_from.bias), leaf(net.policy_to.weight), leaf(net.policy_to.bias),
+                      leaf(net.value.weight), leaf(net.value.bias), net.move_from.cpu(), net.move_to.cpu(),
+                      net.norm.mean.cpu(), net.norm.var.cpu())
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), net.in_idx.cpu().numpy(),
+                      net.out_idx.cpu().numpy(), net.cfg.steps)
+    x = torch.as_tensor(x_cpu)
+    pi, legal, wdl = _train_targets(x.shape[0], "cpu")
+
+    def step():
+        logits, wdl_logits = T.model_grad(hp, ba, cone, x)
+        _train_loss(logits, wdl_logits, pi, legal, wdl).backward()
+
+    step()
+    times = []
+    start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - start < seconds and len(times) < 10):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    per = statistics.median(times)
+    return x.shape[0] / per, per, len(times)
+
+
+def train_bench(args, dev) -> dict:
+    """One train_step per step (chessfly/train.py:126-138): the float32 forward under autograd, the masked
+    policy cross-entropy and value cross-entropy, backward, gradient clipping at 5 and an AdamW step, on the
+    full synthetic graph at `--batch` positions."""
+    import torch
+    from chessfly import _hip
+    from chessfly.synthetic import synthetic_boards, synthetic_net
+
+    net, conn = synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev)
+    net.train()
+    opt = torch.optim.AdamW(net.parameters(), lr=1e-4, weight_decay=0.0)
+    x_np = synthetic_boards(args.batch, seed=1)
+    x = torch.as_tensor(x_np, dtype=torch.float32, device=dev)
+    pi, legal, wdl = _train_targets(args.batch, dev)
+
+    def step():
+        logits, wdl_logits = net(x)
+        loss = _train_loss(logits, wdl_logits, pi, legal, wdl)
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(net.parameters(), 5.0)
+        opt.step()
+        return loss
+
+    for _ in range(args.warmup):
+        loss0 = step()
+    torch.cuda.synchronize()
+    _hip.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prof = _hip.profile_read()
+    _hip.profile_enable(False)
+    value = args.batch * args.steps / wall
+    sparse_ms = prof["other"][0] / args.steps
+    log(f"{args.steps} train steps: {wall * 1e3 / args.steps:.2f} ms each, {value:,.0f} positions/s; device sparse "
+        f"products {sparse_ms:.2f} ms per step; loss {float(loss0):.4f} -> {float(loss):.4f}")
+    cpu = None
+    if args.cpu_boards > 0:
+        nb = min(args.cpu_boards, args.batch, 64)
+        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+        log(f"CPU training baseline: {nb} positions on {threads} threads ...")
+        rate, per, reps = cpu_train_baseline(net, conn, x_np[:nb], threads)
+        cpu = {"value": round(rate, 2), "unit": "positions/s", "cores": threads, "kind": "port",
+               "sample": f"{nb} positions, full graph, float32 light cone forward + backward under autograd "
+                         f"(reference CPU path, chessfly/brain.py:66-99, 289-329), median of {reps} ({per:.2f} s each)"}
+        log(f"CPU {rate:,.2f} positions/s")
+    return {
+        "metric": f"training positions/s (train_step: forward + backward + AdamW), B={args.batch}, "
+                  f"{args.recurrent_steps} steps, fp32",
+        "value": round(value, 1), "unit": "positions/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"FlyChessNet train_step, synthetic connectome {conn.n_neurons} neurons / "
+                               f"{conn.n_edges} synapses, B={args.batch}, {args.recurrent_steps} steps, light cone",
+                   "batch": args.batch, "recurrent_steps": args.recurrent_steps, "graph": args.graph},
+        "sparse_kernel_ms_per_step": round(sparse_ms, 3), "sparse_launches_per_step": prof["other"][1] // args.steps,
+        "cpu_baseline": cpu,
+    }
+
+
 def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> dict:
     """GB/s of random 128-byte row gathers in the state step's access pattern (fly_gather_probe: 8 rows per
     wave load, 16 bytes per lane), over working sets that fit one XCD's L2 (2 MB), the Infinity Cache (21 MB:
@@ -173,6 +302,9 @@ def main() -> int:
     ap.add_argument("--no-prune", action="store_true",
                     help="compute every neuron at every step (the same function without the light cone)")
     ap.add_argument("--cpu-boards", type=int, default=256, help="boards in the CPU baseline sample (0: skip)")
+    ap.add_argument("--train", action="store_true",
+                    help="time the training step (forward + backward + AdamW, float32) instead of the evaluator; "
+                         "--batch defaults to 256 here")
     ap.add_argument("--no-gather-ceiling", action="store_true",
                     help="skip the random-row gather probe that measures the state step's access-pattern ceiling")
     ap.add_argument("--evaluator-steps", type=int, default=10,
@@ -199,6 +331,11 @@ def main() -> int:
     from chessfly.synthetic import synthetic_boards, synthetic_net
 
     dev = torch.device("cuda:0")
+    if args.train:
+        if "--batch" not in sys.argv:
+            args.batch = 256
+        print(json.dumps(train_bench(args, dev)), flush=True)
+        return 0
     for kv in args.tune:
         k, v = kv.split("=")
         _hip.set_tuning(k, int(v))
