@@ -45,34 +45,177 @@ def _transpose_order(rows: torch.Tensor, cols: torch.Tensor, n_rows: int) -> tor
     return torch.argsort(cols * n_rows + rows, stable=True)
 
 
-def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor) -> torch.Tensor:
-    """y (n_rows, B) = A x on the device (fly_spmm); x (n_cols, B) float32."""
+def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, out: torch.Tensor | None = None,
+          val_ids32: torch.Tensor | None = None) -> torch.Tensor:
+    """y (n_rows, B) = A x on the device (fly_spmm); x (n_cols, B) float32.  With `out`, y is added to it; with
+    `val_ids32` the values are val[val_ids32[e]]."""
     x = x.contiguous()
     batch = x.shape[1]
-    y = torch.empty(n_rows, batch, dtype=torch.float32, device=x.device)
-    _hip.check(_hip.load().fly_spmm(crow32.data_ptr(), col32.data_ptr(), val.data_ptr(), n_rows, n_cols, x.data_ptr(),
-                                    max(batch, 1), batch, y.data_ptr(), max(batch, 1), _hip.stream(x.device)),
-               "fly_spmm")
+    y = torch.empty(n_rows, batch, dtype=torch.float32, device=x.device) if out is None else out
+    _hip.check(_hip.load().fly_spmm(crow32.data_ptr(), col32.data_ptr(), val.data_ptr(), _hip.ptr(val_ids32),
+                                    val.numel(), n_rows, n_cols, x.data_ptr(), max(batch, 1), batch, y.data_ptr(),
+                                    max(batch, 1), int(out is not None), _hip.stream(x.device)), "fly_spmm")
     return y
 
 
-def _sddmm(crow32, col32, n_rows: int, n_cols: int, g: torch.Tensor, x: torch.Tensor, nnz: int) -> torch.Tensor:
-    """out[e] = sum_b g[row_e, b] x[col_e, b] on the device (fly_sddmm)."""
+def _sddmm(crow32, col32, n_rows: int, n_cols: int, g: torch.Tensor, x: torch.Tensor, nnz: int,
+           out: torch.Tensor | None = None, ids32: torch.Tensor | None = None) -> torch.Tensor:
+    """out[e] = sum_b g[row_e, b] x[col_e, b] on the device (fly_sddmm).  With `out` and `ids32` the values are
+    added to out[ids32[e]] (a sub-matrix's gradient straight into the whole weight vector)."""
     g, x = g.contiguous(), x.contiguous()
     batch = x.shape[1]
-    out = torch.empty(nnz, dtype=torch.float32, device=x.device)
+    if out is None:
+        out = torch.empty(nnz, dtype=torch.float32, device=x.device)
     if nnz:
         _hip.check(_hip.load().fly_sddmm(crow32.data_ptr(), col32.data_ptr(), n_rows, n_cols, g.data_ptr(),
                                          max(batch, 1), x.data_ptr(), max(batch, 1), batch, out.data_ptr(),
-                                         _hip.stream(x.device)), "fly_sddmm")
+                                         _hip.ptr(ids32), int(ids32 is not None), _hip.stream(x.device)), "fly_sddmm")
     return out
 
 
+class _TakeRows(torch.autograd.Function):
+    """x[rows] for distinct rows, whose gradient is one index_add_ into a zero tensor instead of the sort
+    that the general index backward needs when indices may repeat."""
+
+    @staticmethod
+    def forward(ctx, x, rows):
+        ctx.save_for_backward(rows)
+        ctx.shape = x.shape
+        return x.index_select(0, rows)
+
+    @staticmethod
+    def backward(ctx, g):
+        (rows,) = ctx.saved_tensors
+        return g.new_zeros(ctx.shape).index_add_(0, rows, g), None
+
+
+def _take_rows(x: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    return _TakeRows.apply(x, rows) if torch.is_grad_enabled() and x.requires_grad else x.index_select(0, rows)
+
+
+def _gathered(op, w: torch.Tensor, transposed: bool) -> torch.Tensor:
+    """op's values taken from the whole weight vector w, in CSR order or in the transposed structure's order,
+    gathered once per weight tensor: the forward, its backward and the resting trajectory's products share
+    them."""
+    import weakref
+    slot = "_vals_t" if transposed else "_vals"
+    cached = getattr(op, slot, None)
+    if cached is not None and cached[0]() is w:
+        return cached[1]
+    if transposed:
+        vals = w[op._transposed()[2].long()] if op._edge_ids() is not None else w[op.t_order]
+    else:
+        ids = op._edge_ids()
+        vals = w if ids is None else w[ids[1]]
+    setattr(op, slot, (weakref.ref(w), vals))
+    return vals
+
+
+def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out: torch.Tensor | None = None):
+    """A x (or A^T x) with A's values from w: one column reads w through value ids, more columns read values
+    gathered once per weight tensor (a dependent load per non-zero would sit on the gather's critical path)."""
+    if transposed:
+        crow32, col32, ids32 = op._transposed()
+        _, _, n_cols, n_rows = op._structure()
+    else:
+        crow32, col32, n_rows, n_cols = op._structure()
+        ids = op._edge_ids()
+        ids32 = None if ids is None else ids[0]
+    if x.shape[1] == 1 and (ids32 is not None or transposed):
+        return _spmm(crow32, col32, w, n_rows, n_cols, x, out=out, val_ids32=ids32)
+    return _spmm(crow32, col32, _gathered(op, w, transposed), n_rows, n_cols, x, out=out)
+
+
+class _ConeRecurrence(torch.autograd.Function):
+    """Steps 1..T of the light cone under autograd, float32 (brain.py:313-327): per step the sub-matrix
+    product on the device (its values read from the whole edge-weight vector w at the sub-matrix's edge ids),
+    then one fused kernel for the constant drive, the input, the clamp and the lerp (fly_train_step_forward).
+    The backward runs per step one fused kernel for the gradients of those (fly_train_step_backward), the
+    state gradient A_t^T grad_y added to the carried rows' share (fly_spmm) and the per-synapse gradient
+    written straight into dL/dw at the edge ids (fly_sddmm).  Inputs after u_in and w, per step t: k_t, the
+    previous resting state c_{t-1}[R_t] and alpha[R_t] (each (|R_t|, 1)).  Returns h_T, (|R_T|, B)."""
+
+    @staticmethod
+    def forward(ctx, cone, h_max, u_in, w, *flat):
+        lib = _hip.load()
+        dev = u_in.device
+        st = _hip.stream(dev)
+        u_in = u_in.contiguous()
+        batch = u_in.shape[1]
+        ld = max(batch, 1)
+        hs, ys = [], []
+        h = None
+        for t in range(1, cone.steps + 1):
+            k, pdef, alpha = flat[3 * (t - 1):3 * t]
+            rows, op = cone.row_counts[t], cone.ops[t]
+            prev32, usrc32 = cone.step_tables32(t)
+            if op is not None:
+                crow32, col32, n_rows, n_cols = op._structure()
+                y = _product(op, w, h)
+            else:
+                y = torch.empty(rows, batch, dtype=torch.float32, device=dev)
+            hn = torch.empty(rows, batch, dtype=torch.float32, device=dev)
+            _hip.check(lib.fly_train_step_forward(
+                rows, batch, y.data_ptr(), ld, int(op is not None), k.contiguous().data_ptr(),
+                pdef.contiguous().data_ptr(), alpha.contiguous().data_ptr(),
+                _hip.ptr(prev32 if h is not None and h.shape[0] else None), usrc32.data_ptr(), u_in.data_ptr(), ld,
+                _hip.ptr(h), ld, float(h_max), hn.data_ptr(), ld, st), "fly_train_step_forward")
+            hs.append(hn)
+            ys.append(y)
+            h = hn
+        ctx.cone, ctx.h_max = cone, float(h_max)
+        ctx.save_for_backward(u_in, w, *hs, *ys, *flat)
+        return h
+
+    @staticmethod
+    def backward(ctx, grad_h):
+        cone = ctx.cone
+        T = cone.steps
+        saved = ctx.saved_tensors
+        u_in, w = saved[0], saved[1]
+        hs, ys, flat = saved[2:2 + T], saved[2 + T:2 + 2 * T], saved[2 + 2 * T:]
+        lib = _hip.load()
+        dev = u_in.device
+        st = _hip.stream(dev)
+        batch = u_in.shape[1]
+        ld = max(batch, 1)
+        g = grad_h.contiguous()
+        gu = torch.zeros_like(u_in)
+        gw = torch.zeros_like(w)
+        grads = [None] * len(flat)
+        for t in range(T, 0, -1):
+            k, pdef, alpha = flat[3 * (t - 1):3 * t]
+            rows, op = cone.row_counts[t], cone.ops[t]
+            prev32, usrc32 = cone.step_tables32(t)
+            h_prev = hs[t - 2] if t > 1 else None
+            gy = torch.empty(rows, batch, dtype=torch.float32, device=dev)
+            gk = torch.empty(rows, dtype=torch.float32, device=dev)
+            ga = torch.empty_like(gk)
+            gpdef = torch.empty_like(gk)
+            gh_prev = torch.zeros(cone.row_counts[t - 1], batch, dtype=torch.float32, device=dev) if t > 1 else None
+            _hip.check(lib.fly_train_step_backward(
+                rows, batch, g.data_ptr(), ld, ys[t - 1].data_ptr(), ld, pdef.contiguous().data_ptr(),
+                alpha.contiguous().data_ptr(), _hip.ptr(prev32 if h_prev is not None and h_prev.shape[0] else None),
+                usrc32.data_ptr(), _hip.ptr(h_prev), ld, ctx.h_max, gy.data_ptr(), ld, gk.data_ptr(), ga.data_ptr(),
+                gpdef.data_ptr(), gu.data_ptr(), ld, _hip.ptr(gh_prev), ld, st), "fly_train_step_backward")
+            grads[3 * (t - 1)] = gk.view_as(k)
+            grads[3 * (t - 1) + 1] = gpdef.view_as(pdef)
+            grads[3 * (t - 1) + 2] = ga.view_as(alpha)
+            if op is not None:
+                crow32, col32, n_rows, n_cols = op._structure()
+                _product(op, w, gy, transposed=True, out=gh_prev)
+                ids32, ids = op._edge_ids()
+                _sddmm(crow32, col32, n_rows, n_cols, gy, h_prev, len(ids), out=gw, ids32=ids32)
+            g = gh_prev
+        return (None, None, gu, gw, *grads)
+
+
 class _SparseRecurrent(torch.autograd.Function):
-    """y = A h for A in CSR, the state (rows, batch) batch-fastest (brain.py:66-99).  Forward and the state
-    gradient are device SpMMs over A's structure and its transposed structure; the per-synapse gradient
-    dL/dw_e = sum_b h[col_e, b] grad_y[row_e, b] is a device SDDMM.  `op` is a ConnectomeRNN (the whole W)
-    or a _SubMatrix.  float32 only."""
+    """y = A h for A in CSR, the state (rows, batch) batch-fastest (brain.py:66-99), with A's values taken
+    from the whole edge-weight vector w (a _SubMatrix reads w at its edge ids; the whole W is w itself).
+    Forward and the state gradient are device SpMMs over A's structure and its transposed structure; the
+    per-synapse gradient dL/dw_e = sum_b h[col_e, b] grad_y[row_e, b] is a device SDDMM written straight at
+    the edge ids, so no index backward (sort and scatter) over the edges is needed.  float32 only."""
 
     @staticmethod
     def forward(ctx, h, w, op):
@@ -82,7 +225,7 @@ class _SparseRecurrent(torch.autograd.Function):
         ctx.save_for_backward(h, w)
         ctx.op = op
         crow32, col32, n_rows, n_cols = op._structure()
-        return _spmm(crow32, col32, w.contiguous(), n_rows, n_cols, h)
+        return _product(op, w, h)
 
     @staticmethod
     def backward(ctx, grad_y):
@@ -90,11 +233,15 @@ class _SparseRecurrent(torch.autograd.Function):
         op = ctx.op
         grad_h = grad_w = None
         crow32, col32, n_rows, n_cols = op._structure()
+        ids = op._edge_ids()
         if ctx.needs_input_grad[0]:
-            t_crow32, t_col32, t_order = op._transposed()
-            grad_h = _spmm(t_crow32, t_col32, w[t_order].contiguous(), n_cols, n_rows, grad_y)
+            grad_h = _product(op, w, grad_y.contiguous(), transposed=True)
         if ctx.needs_input_grad[1]:
-            grad_w = _sddmm(crow32, col32, n_rows, n_cols, grad_y, h, w.numel())
+            if ids is None:
+                grad_w = _sddmm(crow32, col32, n_rows, n_cols, grad_y, h, w.numel())
+            else:
+                grad_w = torch.zeros_like(w)
+                _sddmm(crow32, col32, n_rows, n_cols, grad_y, h, len(ids[1]), out=grad_w, ids32=ids[0])
         return grad_h, grad_w, None
 
 
@@ -117,8 +264,13 @@ class _SubMatrix:
             self._cone._step_export(self._t, crow=crow, col=col, edge=edge)
             crow64 = crow.long()
             rows = torch.repeat_interleave(torch.arange(self.shape[0], device=dev), crow64[1:] - crow64[:-1])
-            self._data = (edge.long(), rows, col.long(), crow64, crow, col)
+            self._data = (edge.long(), rows, col.long(), crow64, crow, col, edge)
         return self._data
+
+    def _edge_ids(self):
+        """(int32, int64) ids of the sub-matrix's edges in the whole weight vector."""
+        d = self._load()
+        return d[6], d[0]
 
     def _structure(self):
         d = self._load()
@@ -131,8 +283,9 @@ class _SubMatrix:
             order = _transpose_order(post, pre, self.shape[0])
             t_crow = _crow(pre[order], self.shape[1])
             t_col = post[order]
-            self._tr = (order, t_crow, t_col, t_crow.to(torch.int32), t_col.to(torch.int32))
-        return self._tr[3], self._tr[4], self._tr[0]
+            self._tr = (order, t_crow, t_col, t_crow.to(torch.int32), t_col.to(torch.int32),
+                        self.edges[order].to(torch.int32))
+        return self._tr[3], self._tr[4], self._tr[5]
 
     @property
     def t_order(self) -> torch.Tensor:
@@ -249,11 +402,13 @@ class LightCone:
     def _per_step(self):
         if self._steps_idx is None:
             keep_next, keep_prev, carried, prev_row, u_pos, u_src = ([None] for _ in range(6))
+            tables32 = [None]
             for t in range(1, self.steps + 1):
                 nr = self.row_counts[t]
                 prev = torch.empty(nr, dtype=torch.int32, device=self.device)
                 usrc = torch.empty(nr, dtype=torch.int32, device=self.device)
                 self._step_export(t, prev=prev, usrc=usrc)
+                tables32.append((prev, usrc))
                 prev, usrc = prev.long(), usrc.long()
                 is_carried = prev >= 0
                 keep_next.append(torch.nonzero(is_carried).squeeze(1))
@@ -263,8 +418,13 @@ class LightCone:
                 fed = usrc >= 0
                 u_pos.append(torch.nonzero(fed).squeeze(1))
                 u_src.append(usrc[fed])
-            self._steps_idx = (keep_next, keep_prev, carried, prev_row, u_pos, u_src)
+            self._steps_idx = (keep_next, keep_prev, carried, prev_row, u_pos, u_src, tables32)
         return self._steps_idx
+
+    def step_tables32(self, t: int):
+        """(prev, usrc) of step t as int32 device tensors: the row of R_{t-1} each row of R_t carries (-1: none)
+        and the row of the input it is fed from (-1: none)."""
+        return self._per_step()[6][t]
 
     keep_next = property(lambda self: self._per_step()[0])
     keep_prev = property(lambda self: self._per_step()[1])
@@ -371,7 +531,12 @@ class ConnectomeRNN(nn.Module):
         return self.crow32, self.pre32, self.n, self.n
 
     def _transposed(self):
-        return self.t_crow32, self.t_col32, self.t_order
+        if getattr(self, "_t_order32", None) is None or self._t_order32.device != self.t_order.device:
+            self._t_order32 = self.t_order.to(torch.int32)
+        return self.t_crow32, self.t_col32, self._t_order32
+
+    def _edge_ids(self):
+        return None
 
     # ---- plans (everything that depends on the weights only; rebuilt when a parameter changes) -------
     def _plan(self, key_extra, build):
@@ -448,10 +613,10 @@ class ConnectomeRNN(nn.Module):
         bias = self.bias.unsqueeze(1)
         for t in range(1, cone.steps + 1):
             full = (_SparseRecurrent.apply(c, w, self) if t > 1 else torch.zeros_like(c)) + bias
-            k = full[cone.rows[t]]
+            k = _take_rows(full, cone.rows[t])
             op = cone.ops[t]
             if op is not None:
-                k = k - _SparseRecurrent.apply(c[cone.rows[t - 1]], w[op.edges], op)
+                k = k - _SparseRecurrent.apply(_take_rows(c, cone.rows[t - 1]), w, op)
             ks.append(k)
             c = torch.lerp(c, full.clamp(0, self.h_max), alpha)
             cs.append(c)
@@ -467,17 +632,13 @@ class ConnectomeRNN(nn.Module):
         w = self.edge_weights()
         alpha = torch.sigmoid(self.alpha_logit).unsqueeze(1)
         cs, ks = self._constants(cone, w, alpha)
-        h = None
+        flat = []
         for t in range(1, steps + 1):
-            rows, op = cone.rows[t], cone.ops[t]
-            x = ks[t].expand(-1, batch) if op is None else _SparseRecurrent.apply(h, w[op.edges], op) + ks[t]
-            x = x.index_add(0, cone.u_pos[t], u_in[cone.u_src[t]]).clamp(0, self.h_max)
-            prev = cs[t - 1][rows].expand(-1, batch)
-            if len(cone.keep_next[t]):
-                prev = prev.index_copy(0, cone.keep_next[t], h[cone.keep_prev[t]])
-            h = torch.lerp(prev, x, alpha[rows])
-        out = cs[steps][out_idx].expand(-1, batch)
-        return out.index_copy(0, cone.out_pos, h[cone.out_src])
+            rows = cone.rows[t]
+            flat += [ks[t], _take_rows(cs[t - 1], rows), _take_rows(alpha, rows)]
+        h = _ConeRecurrence.apply(cone, self.h_max, u_in, w, *flat)
+        out = _take_rows(cs[steps], out_idx).expand(-1, batch)
+        return out.index_copy(0, cone.out_pos, _take_rows(h, cone.out_src))
 
     # ---- the same function through the light cone ------------------------------------------------
     def light_cone(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int, prune: bool = True) -> LightCone:

@@ -13,12 +13,15 @@ namespace {
 struct SpmmArgs {
   const int32_t *rowptr;  // nrows + 1
   const int32_t *col;     // nnz, column of each non-zero
-  const float *val;       // nnz
+  const float *val;       // nnz values, or the vector val_ids index into
+  const int32_t *val_ids; // null, or per non-zero the index of its value in val
+  uint32_t val_bytes;     // bytes of val when val_ids is given (reads past it give 0)
   const float *x;         // (ncols, ldx)
   float *y;               // (nrows, ldy)
   int64_t ldx, ldy;
   uint32_t xbytes;        // ncols * ldx * 4, below 2^31
   int32_t nrows, batch, chunks;
+  int32_t accumulate;     // y += A x instead of y = A x
 };
 
 // Wave -> (row, chunk of LPG * V columns), chunks outermost so one chunk is swept over every row before the
@@ -38,8 +41,10 @@ __global__ __launch_bounds__(256) void k_spmm(const SpmmArgs a) {
   const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
   const int32_t n = end - beg;
   const __amdgpu_buffer_rsrc_t rc = buffer_of(a.col + beg, (uint32_t)n * 4u);
-  const __amdgpu_buffer_rsrc_t rv = buffer_of(a.val + beg, (uint32_t)n * 4u);
+  const __amdgpu_buffer_rsrc_t rv = buffer_of(a.val_ids ? (const void *)(a.val_ids + beg) : (const void *)(a.val + beg),
+                                              (uint32_t)n * 4u);
   const __amdgpu_buffer_rsrc_t rx = buffer_of(a.x, a.xbytes);
+  const __amdgpu_buffer_rsrc_t rw = buffer_of(a.val, a.val_bytes);
   const uint32_t row_bytes = (uint32_t)a.ldx * 4u, voff = (uint32_t)col0 * 4u;
   for (int32_t e0 = 0; e0 < n; e0 += G * UNROLL) {
     int32_t c[UNROLL];
@@ -48,7 +53,10 @@ __global__ __launch_bounds__(256) void k_spmm(const SpmmArgs a) {
     for (int j = 0; j < UNROLL; ++j) {   // past the row's end: column 0, weight 0
       const int off = (e0 + j * G + g) * 4;
       c[j] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
-      w[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      const unsigned v = __builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0);
+      w[j] = a.val_ids ? (e0 + j * G + g < n ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, (int)(v * 4u), 0, 0))
+                                            : 0.0f)
+                       : __uint_as_float(v);
     }
     float xv[UNROLL][V];
 #pragma unroll
@@ -76,23 +84,29 @@ __global__ __launch_bounds__(256) void k_spmm(const SpmmArgs a) {
   float *dst = a.y + (int64_t)row * a.ldy + col0;
   if constexpr (V == 4) {
     if (col0 + 4 <= a.batch) {
-      *reinterpret_cast<float4 *>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      if (a.accumulate) {
+        const float4 o = *reinterpret_cast<const float4 *>(dst);
+        v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+      }
+      *reinterpret_cast<float4 *>(dst) = v;
       return;
     }
   }
 #pragma unroll
   for (int i = 0; i < V; ++i)
-    if (col0 + i < a.batch) dst[i] = acc[i];
+    if (col0 + i < a.batch) dst[i] = a.accumulate ? dst[i] + acc[i] : acc[i];
 }
 
 struct SddmmArgs {
   const int32_t *rowptr, *col;
-  const float *g;  // (nrows, ldg)
-  const float *x;  // (ncols, ldx)
-  float *out;      // nnz
+  const float *g;         // (nrows, ldg)
+  const float *x;         // (ncols, ldx)
+  float *out;             // nnz, or indexed by ids
+  const int32_t *ids;     // null: out[e]; else out[ids[e]] (distinct within a launch)
   int64_t ldg, ldx;
   uint32_t xbytes;
-  int32_t nrows, batch;
+  int32_t nrows, batch, accumulate;
 };
 
 // One wave per row, one lane per non-zero (64 at a time): lane e walks x[col_e, :] in 16-byte steps, 8 of
@@ -140,7 +154,188 @@ __global__ __launch_bounds__(256) void k_sddmm(const SddmmArgs a) {
     for (int32_t b = full; b < a.batch; ++b)
       acc = fmaf(grow[b], __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (int)(base + (uint32_t)b * 4u), 0, 0)),
                  acc);
-    if (live) a.out[e] = acc;
+    if (live) {
+      float *dst = a.out + (a.ids ? a.ids[e] : e);
+      *dst = a.accumulate ? *dst + acc : acc;
+    }
+  }
+}
+
+// y = A x for one column (the resting trajectory's products): a wave per row, its lanes across the row's
+// non-zeros, then one wave sum.
+__global__ __launch_bounds__(256) void k_spmv(const SpmmArgs a) {
+  const uint32_t row = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= (uint32_t)a.nrows) return;
+  const int lane = threadIdx.x & 63;
+  const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
+  const __amdgpu_buffer_rsrc_t rx = buffer_of(a.x, a.xbytes);
+  const __amdgpu_buffer_rsrc_t rw = buffer_of(a.val, a.val_bytes);
+  const uint32_t row_bytes = (uint32_t)a.ldx * 4u;
+  float acc = 0.0f;
+  for (int32_t e = beg + lane; e < end; e += 64)
+    acc = fmaf(a.val_ids ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, (int)((uint32_t)a.val_ids[e] * 4u), 0, 0))
+                         : a.val[e],
+               __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                             rx, (int)__umul24((uint32_t)a.col[e], row_bytes), 0, 0)), acc);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (lane == 0) {
+    float *dst = a.y + (int64_t)row * a.ldy;
+    *dst = a.accumulate ? *dst + acc : acc;
+  }
+}
+
+// ---- one recurrent step of training, elementwise parts (brain.py:313-327 under autograd) ---------------
+
+// torch.lerp(start, end, weight) for float32 (ATen's formula: from the nearer end)
+__device__ __forceinline__ float lerp_torch(float start, float end, float weight) {
+  const bool small = fabsf(weight) < 0.5f;
+  return fmaf(small ? weight : weight - 1.0f, end - start, small ? start : end);
+}
+
+template <int V>
+struct Vec {
+  float v[V];
+  static __device__ __forceinline__ Vec load(const float *p) {
+    Vec r;
+    if constexpr (V == 4) {
+      const float4 q = *reinterpret_cast<const float4 *>(p);
+      r.v[0] = q.x; r.v[1] = q.y; r.v[2] = q.z; r.v[3] = q.w;
+    } else {
+      r.v[0] = *p;
+    }
+    return r;
+  }
+  static __device__ __forceinline__ Vec fill(float x) {
+    Vec r;
+#pragma unroll
+    for (int i = 0; i < V; ++i) r.v[i] = x;
+    return r;
+  }
+  __device__ __forceinline__ void store(float *p) const {
+    if constexpr (V == 4)
+      *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    else
+      *p = v[0];
+  }
+};
+
+struct StepFwdArgs {
+  float *s_y;                  // in: s = A_t h_{t-1} (unless has_s == 0: s = 0); out: y, the pre-clamp drive
+  int64_t lds;
+  const float *k, *pdef, *a;   // per row: constant drive, resting state of the previous step, leak
+  const int32_t *prev, *usrc;  // per row: row of h_{t-1} carried over (or -1), row of u (or -1); null: none
+  const float *u;
+  int64_t ldu;
+  const float *hprev;
+  int64_t ldp;
+  float *h;
+  int64_t ldh;
+  float hmax;
+  int32_t rows, batch, has_s;
+};
+
+// y = s + k + u[usrc];  x = clamp(y, 0, hmax);  p = h_{t-1}[prev] or pdef;  h = lerp(p, x, a).  One wave per
+// row, V columns per lane.
+template <int V>
+__global__ __launch_bounds__(256) void k_train_fwd(const StepFwdArgs a) {
+  const uint32_t row = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= (uint32_t)a.rows) return;
+  const int lane = threadIdx.x & 63;
+  const float k = a.k[row], pd = a.pdef[row], al = a.a[row];
+  const int32_t pv = a.prev ? a.prev[row] : -1, us = a.usrc ? a.usrc[row] : -1;
+  float *sy = a.s_y + (int64_t)row * a.lds;
+  float *h = a.h + (int64_t)row * a.ldh;
+  const float *ur = us >= 0 ? a.u + (int64_t)us * a.ldu : nullptr;
+  const float *pr = pv >= 0 ? a.hprev + (int64_t)pv * a.ldp : nullptr;
+  for (int32_t c = lane * V; c < a.batch; c += 64 * V) {
+    Vec<V> s = a.has_s ? Vec<V>::load(sy + c) : Vec<V>::fill(0.0f);
+    const Vec<V> u = ur ? Vec<V>::load(ur + c) : Vec<V>::fill(0.0f);
+    const Vec<V> p = pr ? Vec<V>::load(pr + c) : Vec<V>::fill(pd);
+    Vec<V> out;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float y = (s.v[i] + k) + u.v[i];
+      s.v[i] = y;
+      out.v[i] = lerp_torch(p.v[i], fminf(fmaxf(y, 0.0f), a.hmax), al);
+    }
+    s.store(sy + c);
+    out.store(h + c);
+  }
+}
+
+struct StepBwdArgs {
+  const float *g;              // dL/dh_t
+  int64_t ldg;
+  const float *y;              // the forward's pre-clamp drive
+  int64_t ldy;
+  const float *pdef, *a;
+  const int32_t *prev, *usrc;
+  const float *hprev;
+  int64_t ldp;
+  float *gy;                   // out: dL/dy (rows, batch)
+  int64_t ldgy;
+  float *gk, *ga, *gpdef;      // out per row: dL/dk, dL/da, dL/dpdef
+  float *gu;                   // dL/du, accumulated over steps (rows of u fed at this step are distinct)
+  int64_t ldgu;
+  float *ghprev;               // out: dL/dh_{t-1} of the carried rows (the caller zeroes the rest)
+  int64_t ldgh;
+  float hmax;
+  int32_t rows, batch;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// The gradients of h = lerp(p, clamp(y, 0, hmax), a): dL/dy = g a [0 <= y <= hmax] (torch.clamp passes the
+// bounds), dL/dp = g (1 - a), dL/da = sum_b g (x - p); dL/dk = sum_b dL/dy; dL/dpdef = sum_b dL/dp on rows
+// that are not carried; carried rows pass dL/dp to h_{t-1}[prev]; input rows add dL/dy to u[usrc].
+template <int V>
+__global__ __launch_bounds__(256) void k_train_bwd(const StepBwdArgs a) {
+  const uint32_t row = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= (uint32_t)a.rows) return;
+  const int lane = threadIdx.x & 63;
+  const float pd = a.pdef[row], al = a.a[row];
+  const int32_t pv = a.prev ? a.prev[row] : -1, us = a.usrc ? a.usrc[row] : -1;
+  const float *gr = a.g + (int64_t)row * a.ldg;
+  const float *yr = a.y + (int64_t)row * a.ldy;
+  float *gyr = a.gy + (int64_t)row * a.ldgy;
+  const float *pr = pv >= 0 ? a.hprev + (int64_t)pv * a.ldp : nullptr;
+  float *ghr = pv >= 0 ? a.ghprev + (int64_t)pv * a.ldgh : nullptr;
+  float *gur = us >= 0 ? a.gu + (int64_t)us * a.ldgu : nullptr;
+  float sk = 0.0f, sa = 0.0f, sp = 0.0f;
+  for (int32_t c = lane * V; c < a.batch; c += 64 * V) {
+    const Vec<V> g = Vec<V>::load(gr + c), y = Vec<V>::load(yr + c);
+    const Vec<V> p = pr ? Vec<V>::load(pr + c) : Vec<V>::fill(pd);
+    Vec<V> gy, gp;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float x = fminf(fmaxf(y.v[i], 0.0f), a.hmax);
+      gy.v[i] = (y.v[i] >= 0.0f && y.v[i] <= a.hmax) ? g.v[i] * al : 0.0f;
+      gp.v[i] = g.v[i] * (1.0f - al);
+      sk += gy.v[i];
+      sa += g.v[i] * (x - p.v[i]);
+      sp += gp.v[i];
+    }
+    gy.store(gyr + c);
+    if (ghr) gp.store(ghr + c);
+    if (gur) {
+      Vec<V> u = Vec<V>::load(gur + c);
+#pragma unroll
+      for (int i = 0; i < V; ++i) u.v[i] += gy.v[i];
+      u.store(gur + c);
+    }
+  }
+  sk = wave_sum(sk);
+  sa = wave_sum(sa);
+  sp = wave_sum(sp);
+  if (lane == 0) {
+    a.gk[row] = sk;
+    a.ga[row] = sa;
+    a.gpdef[row] = pv >= 0 ? 0.0f : sp;
   }
 }
 
@@ -164,8 +359,9 @@ void launch_spmm(const SpmmArgs &a, hipStream_t st) {
 
 using namespace fly;
 
-extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *val, int64_t nrows, int64_t ncols,
-                        const float *x, int64_t ldx, int64_t batch, float *y, int64_t ldy, void *stream) {
+extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *val, const int32_t *val_ids,
+                        int64_t n_val, int64_t nrows, int64_t ncols, const float *x, int64_t ldx, int64_t batch,
+                        float *y, int64_t ldy, int32_t accumulate, void *stream) {
   return guard([&] {
     FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0, "negative size");
     FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
@@ -173,11 +369,15 @@ extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *
     FLY_REQUIRE(rowptr && y && ldy >= batch, "bad argument");
     FLY_REQUIRE(ncols == 0 || (col && val && x && ldx >= batch && ldx < (1 << 22)), "bad argument");
     LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
-    SpmmArgs a{rowptr, col, val, x, y, ldx, ldy, checked_bytes(ncols, ldx), (int32_t)nrows, (int32_t)batch, 0};
+    FLY_REQUIRE(!val_ids || (n_val >= 0 && n_val < (int64_t)1 << 29), "n_val out of range");
+    SpmmArgs a{rowptr, col, val, val_ids, (uint32_t)(val_ids ? n_val * 4 : 0), x, y, ldx, ldy,
+               checked_bytes(ncols, ldx), (int32_t)nrows, (int32_t)batch, 0, accumulate != 0};
     if (ncols == 0) a.xbytes = 0;   // every gather reads zeros: y = 0
-    // 16-byte lanes in groups of 16 (64 columns per chunk) when the rows allow them, else 4-byte lanes in
-    // groups of 8
-    if (batch >= 4 && vec4_ok(x, ldx) && vec4_ok(y, ldy)) {
+    // one column: lanes across the non-zeros; else 16-byte lanes in groups of 16 (64 columns per chunk) when
+    // the rows allow them, else 4-byte lanes in groups of 8
+    if (batch == 1) {
+      hipLaunchKernelGGL(k_spmv, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), a);
+    } else if (batch >= 4 && vec4_ok(x, ldx) && vec4_ok(y, ldy)) {
       a.chunks = (int32_t)((batch + 63) / 64);
       launch_spmm<4, 4>(a, as_stream(stream));
     } else {
@@ -189,7 +389,8 @@ extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *
 }
 
 extern "C" int fly_sddmm(const int32_t *rowptr, const int32_t *col, int64_t nrows, int64_t ncols, const float *g,
-                         int64_t ldg, const float *x, int64_t ldx, int64_t batch, float *out, void *stream) {
+                         int64_t ldg, const float *x, int64_t ldx, int64_t batch, float *out, const int32_t *ids,
+                         int32_t accumulate, void *stream) {
   return guard([&] {
     FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0, "negative size");
     FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
@@ -197,13 +398,63 @@ extern "C" int fly_sddmm(const int32_t *rowptr, const int32_t *col, int64_t nrow
     FLY_REQUIRE(rowptr && col && out && g && ldg >= batch, "bad argument");
     FLY_REQUIRE(ncols == 0 || (x && ldx >= batch && ldx < (1 << 22)), "bad argument");
     LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
-    SddmmArgs a{rowptr, col, g, x, out, ldg, ldx, ncols ? checked_bytes(ncols, ldx) : 0u, (int32_t)nrows,
-                (int32_t)batch};
+    SddmmArgs a{rowptr, col, g, x, out, ids, ldg, ldx, ncols ? checked_bytes(ncols, ldx) : 0u, (int32_t)nrows,
+                (int32_t)batch, accumulate != 0};
     const dim3 grid(blocks_for(nrows, 4)), block(256);
     if (batch >= 4 && vec4_ok(x, ldx))
       hipLaunchKernelGGL(k_sddmm<4>, grid, block, 0, as_stream(stream), a);
     else
       hipLaunchKernelGGL(k_sddmm<1>, grid, block, 0, as_stream(stream), a);
     check_launch("sddmm");
+  });
+}
+
+extern "C" int fly_train_step_forward(int64_t rows, int64_t batch, float *s_y, int64_t lds, int32_t has_s,
+                                      const float *k, const float *pdef, const float *alpha, const int32_t *prev,
+                                      const int32_t *usrc, const float *u, int64_t ldu, const float *hprev,
+                                      int64_t ldp, float h_max, float *h, int64_t ldh, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(rows >= 0 && batch >= 0 && rows < (int64_t)1 << 30, "size out of range");
+    if (!rows || !batch) return;
+    FLY_REQUIRE(s_y && lds >= batch && k && pdef && alpha && h && ldh >= batch, "bad argument");
+    FLY_REQUIRE(!usrc || (u && ldu >= batch), "input rows need u");
+    FLY_REQUIRE(!prev || (hprev && ldp >= batch), "carried rows need the previous state");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    StepFwdArgs a{s_y, lds, k, pdef, alpha, prev, usrc, u, ldu, hprev, ldp, h, ldh, h_max, (int32_t)rows,
+                  (int32_t)batch, has_s != 0};
+    const bool v4 = batch % 4 == 0 && vec4_ok(s_y, lds) && vec4_ok(h, ldh) && (!usrc || vec4_ok(u, ldu)) &&
+                    (!prev || vec4_ok(hprev, ldp));
+    const dim3 grid(blocks_for(rows, 4)), block(256);
+    if (v4)
+      hipLaunchKernelGGL(k_train_fwd<4>, grid, block, 0, as_stream(stream), a);
+    else
+      hipLaunchKernelGGL(k_train_fwd<1>, grid, block, 0, as_stream(stream), a);
+    check_launch("train step forward");
+  });
+}
+
+extern "C" int fly_train_step_backward(int64_t rows, int64_t batch, const float *g, int64_t ldg, const float *y,
+                                       int64_t ldy, const float *pdef, const float *alpha, const int32_t *prev,
+                                       const int32_t *usrc, const float *hprev, int64_t ldp, float h_max, float *gy,
+                                       int64_t ldgy, float *gk, float *ga, float *gpdef, float *gu, int64_t ldgu,
+                                       float *ghprev, int64_t ldgh, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(rows >= 0 && batch >= 0 && rows < (int64_t)1 << 30, "size out of range");
+    if (!rows) return;
+    FLY_REQUIRE(g && y && pdef && alpha && gy && gk && ga && gpdef, "bad argument");
+    FLY_REQUIRE(ldg >= batch && ldy >= batch && ldgy >= batch, "bad leading dimension");
+    FLY_REQUIRE(!usrc || (gu && ldgu >= batch), "input rows need gu");
+    FLY_REQUIRE(!prev || (hprev && ghprev && ldp >= batch && ldgh >= batch), "carried rows need the previous state");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    StepBwdArgs a{g, ldg, y, ldy, pdef, alpha, prev, usrc, hprev, ldp, gy, ldgy, gk, ga, gpdef, gu, ldgu, ghprev,
+                  ldgh, h_max, (int32_t)rows, (int32_t)batch};
+    const bool v4 = batch % 4 == 0 && vec4_ok(g, ldg) && vec4_ok(y, ldy) && vec4_ok(gy, ldgy) &&
+                    (!usrc || vec4_ok(gu, ldgu)) && (!prev || (vec4_ok(hprev, ldp) && vec4_ok(ghprev, ldgh)));
+    const dim3 grid(blocks_for(rows, 4)), block(256);
+    if (v4)
+      hipLaunchKernelGGL(k_train_bwd<4>, grid, block, 0, as_stream(stream), a);
+    else
+      hipLaunchKernelGGL(k_train_bwd<1>, grid, block, 0, as_stream(stream), a);
+    check_launch("train step backward");
   });
 }

@@ -25,6 +25,8 @@
  *   fly_evaluator_outputs chessfly/model.py:120-128 and :107-110 (Evaluator.submit's half cast or legal gather,
  *                         expected_value)
  *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
+ *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
+ *                         gradients)
  */
 #ifndef FLYEVAL_H
 #define FLYEVAL_H
@@ -179,16 +181,41 @@ int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t
 /* ---- training: the sparse products of the differentiable recurrence ----------------------------- */
 /* chessfly/brain.py:66-99 (_SparseRecurrent), float32.  A is CSR (rowptr nrows+1, col/val nnz, int32 and
  * float); operands are row-major with the batch fastest.
- *   fly_spmm:  y (nrows, ldy) = A x, x (ncols, ldx).  The forward product, and with the transposed
- *              structure of A (and its values in that order) the state gradient A^T grad_y.
+ *   fly_spmm:  y (nrows, ldy) = A x (accumulate != 0: y += A x), x (ncols, ldx).  The values are val[e], or
+ *              val[val_ids[e]] when val_ids is given (a sub-matrix read from the whole weight vector of n_val
+ *              entries; an index past it reads 0).  The
+ *              forward product, and with the transposed structure of A the state gradient A^T grad_y.
  *   fly_sddmm: out[e] = sum_b g[row_e, b] x[col_e, b] for every non-zero e, CSR order: the per-synapse
- *              gradient of y = A x with g = dL/dy.  out must not overlap g.
+ *              gradient of y = A x with g = dL/dy.  With ids (distinct), out[ids[e]] instead (a sub-matrix's
+ *              gradient straight into the whole weight vector); accumulate != 0 adds.  out must not overlap g.
  * Gathered operands must be below 2 GiB; rows and columns below 2^24; column indices are not range-checked
  * (a wrong index reads wrong data, never outside x). */
-int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, int64_t nrows, int64_t ncols,
-             const float *x_dev, int64_t ldx, int64_t batch, float *y_dev, int64_t ldy, void *stream);
+int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, const int32_t *val_ids_dev,
+             int64_t n_val, int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx, int64_t batch,
+             float *y_dev, int64_t ldy, int32_t accumulate, void *stream);
 int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
-              int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, void *stream);
+              int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, const int32_t *ids_dev,
+              int32_t accumulate, void *stream);
+
+/* One recurrent step of training, the elementwise parts fused (brain.py:313-327 under autograd), float32,
+ * one row of R_t per wave; rows are (rows, batch) with leading dimensions ld*:
+ *   forward:  y = s + k[r] + (usrc[r] >= 0 ? u[usrc[r]] : 0)   (s = A_t h_{t-1} in s_y, or 0 when has_s == 0;
+ *             y overwrites s_y), x = clamp(y, 0, h_max), p = prev[r] >= 0 ? hprev[prev[r]] : pdef[r],
+ *             h = torch.lerp(p, x, alpha[r]).
+ *   backward: from g = dL/dh:  gy = g alpha [0 <= y <= h_max];  gk[r] = sum_b gy;  ga[r] = sum_b g (x - p);
+ *             gpdef[r] = sum_b g (1 - alpha) on rows not carried, else 0;  carried rows store g (1 - alpha)
+ *             into ghprev[prev[r]] (the caller zeroes ghprev, then adds A_t^T gy with fly_spmm accumulate);
+ *             input rows add gy to gu[usrc[r]] (distinct rows per step).
+ * prev / usrc may be NULL (no carried rows / no input rows). */
+int fly_train_step_forward(int64_t rows, int64_t batch, float *s_y_dev, int64_t lds, int32_t has_s,
+                           const float *k_dev, const float *pdef_dev, const float *alpha_dev, const int32_t *prev_dev,
+                           const int32_t *usrc_dev, const float *u_dev, int64_t ldu, const float *hprev_dev,
+                           int64_t ldp, float h_max, float *h_dev, int64_t ldh, void *stream);
+int fly_train_step_backward(int64_t rows, int64_t batch, const float *g_dev, int64_t ldg, const float *y_dev,
+                            int64_t ldy, const float *pdef_dev, const float *alpha_dev, const int32_t *prev_dev,
+                            const int32_t *usrc_dev, const float *hprev_dev, int64_t ldp, float h_max, float *gy_dev,
+                            int64_t ldgy, float *gk_dev, float *ga_dev, float *gpdef_dev, float *gu_dev,
+                            int64_t ldgu, float *ghprev_dev, int64_t ldgh, void *stream);
 
 /* ---- measurement ------------------------------------------------------------------------------- */
 /* No counterpart in the reference; for benchmarks.  The random-row gather rate of this GPU for the state

@@ -55,17 +55,34 @@ def test_spmm_and_sddmm_match_float64(batch, ld_pad):
     ld = batch + ld_pad
     y = torch.full((rows, ld), 7.0, device=DEV)
     st = _hip.stream(torch.device(DEV))
-    _hip.check(lib.fly_spmm(crow_d.data_ptr(), col_d.data_ptr(), val_d.data_ptr(), rows, cols, x_d.data_ptr(), ld,
-                            batch, y.data_ptr(), ld, st), "fly_spmm")
+    _hip.check(lib.fly_spmm(crow_d.data_ptr(), col_d.data_ptr(), val_d.data_ptr(), None, 0, rows, cols,
+                            x_d.data_ptr(), ld, batch, y.data_ptr(), ld, 0, st), "fly_spmm")
     ref = dense @ x[:, :batch]
     _close(y[:, :batch], torch.as_tensor(ref), 1e-5, "spmm")
+    y2 = y.clone()
+    # values through an index into a larger vector, accumulating
+    perm = torch.randperm(3 * nnz, device=DEV)[:nnz]
+    big = torch.zeros(3 * nnz, device=DEV)
+    big[perm] = val_d
+    _hip.check(lib.fly_spmm(crow_d.data_ptr(), col_d.data_ptr(), big.data_ptr(), perm.to(torch.int32).data_ptr(),
+                            big.numel(), rows, cols, x_d.data_ptr(), ld, batch, y2.data_ptr(), ld, 1, st),
+               "fly_spmm accumulate")
+    _close(y2[:, :batch], torch.as_tensor(2 * ref), 1e-5, "spmm accumulate through value ids")
     if ld_pad:
         assert bool((y[:, batch:] == 7.0).all())                # padding columns are not written
     out = torch.empty(nnz, device=DEV)
     _hip.check(lib.fly_sddmm(crow_d.data_ptr(), col_d.data_ptr(), rows, cols, g_d.data_ptr(), ld, x_d.data_ptr(), ld,
-                             batch, out.data_ptr(), st), "fly_sddmm")
+                             batch, out.data_ptr(), None, 0, st), "fly_sddmm")
     ref_w = (g[r, :batch] * x[c, :batch]).sum(1)
     _close(out, torch.as_tensor(ref_w), 1e-5, "sddmm")
+    # scattered into a larger vector by distinct ids, accumulating
+    ids = torch.randperm(2 * nnz, device=DEV)[:nnz].to(torch.int32)
+    big = torch.ones(2 * nnz, device=DEV)
+    _hip.check(lib.fly_sddmm(crow_d.data_ptr(), col_d.data_ptr(), rows, cols, g_d.data_ptr(), ld, x_d.data_ptr(), ld,
+                             batch, big.data_ptr(), ids.data_ptr(), 1, st), "fly_sddmm ids")
+    want = torch.ones(2 * nnz, dtype=torch.float64)
+    want[ids.long().cpu()] += torch.as_tensor(ref_w)
+    _close(big, want, 1e-5, "sddmm scattered")
 
 
 def _rnn_pair(conn, seed: int, scale: float = 3.0):
