@@ -703,6 +703,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "rows_mode") tuning().rows_mode = (int)value;
     else if (k == "nt_store") tuning().nt_store = (int)value;
     else if (k == "tiles") tuning().tiles = (int)value;
+    else if (k == "spmm_groups") tuning().spmm_groups = (int)value;
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });
 }

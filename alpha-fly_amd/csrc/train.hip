@@ -378,8 +378,15 @@ extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *
     if (batch == 1) {
       hipLaunchKernelGGL(k_spmv, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), a);
     } else if (batch >= 4 && vec4_ok(x, ldx) && vec4_ok(y, ldy)) {
-      a.chunks = (int32_t)((batch + 63) / 64);
-      launch_spmm<4, 4>(a, as_stream(stream));
+      const int g = tuning().spmm_groups == 2 || tuning().spmm_groups == 8 ? tuning().spmm_groups : 4;
+      const int width = 64 / g * 4;   // columns per chunk
+      a.chunks = (int32_t)((batch + width - 1) / width);
+      if (g == 2)
+        launch_spmm<2, 4>(a, as_stream(stream));
+      else if (g == 8)
+        launch_spmm<8, 4>(a, as_stream(stream));
+      else
+        launch_spmm<4, 4>(a, as_stream(stream));
     } else {
       a.chunks = (int32_t)((batch + 7) / 8);
       launch_spmm<8, 1>(a, as_stream(stream));

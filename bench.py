@@ -331,14 +331,14 @@ def main() -> int:
     from chessfly.synthetic import synthetic_boards, synthetic_net
 
     dev = torch.device("cuda:0")
+    for kv in args.tune:
+        k, v = kv.split("=")
+        _hip.set_tuning(k, int(v))
     if args.train:
         if "--batch" not in sys.argv:
             args.batch = 256
         print(json.dumps(train_bench(args, dev)), flush=True)
         return 0
-    for kv in args.tune:
-        k, v = kv.split("=")
-        _hip.set_tuning(k, int(v))
     t0 = time.perf_counter()
     net, conn = synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev)
     net.infer_dtype = torch.float16 if args.dtype == "f16" else torch.float32

@@ -38,18 +38,28 @@ class Csr:
         return torch.sparse_csr_tensor(self.crow, self.col, w, self.shape, check_invariants=False)
 
     def mat_t(self, w: torch.Tensor) -> torch.Tensor:
-        order = torch.argsort(self.col * self.shape[0] + self.row, stable=True)
-        return torch.sparse_csr_tensor(_crow(self.col[order], self.shape[1]), self.row[order], w[order],
-                                       self.shape[::-1], check_invariants=False)
+        if getattr(self, "_t", None) is None:          # the transposed structure, sorted once per matrix
+            order = torch.argsort(self.col * self.shape[0] + self.row, stable=True)
+            self._t = (order, _crow(self.col[order], self.shape[1]), self.row[order])
+        order, crow, col = self._t
+        return torch.sparse_csr_tensor(crow, col, w[order], self.shape[::-1], check_invariants=False)
 
 
 def full_csr(b: BrainArrays) -> Csr:
-    return Csr(_crow(b.post, b.n), b.pre, b.post, (b.n, b.n))
+    cached = getattr(b, "_csr", None)
+    if cached is None:
+        cached = Csr(_crow(b.post, b.n), b.pre, b.post, (b.n, b.n))
+        object.__setattr__(b, "_csr", cached)
+    return cached
 
 
 def sub_csr(op) -> Csr:
-    t = lambda a: torch.as_tensor(a)
-    return Csr(t(op.crow), t(op.pre), t(op.post), tuple(op.shape))
+    cached = getattr(op, "_csr", None)
+    if cached is None:
+        t = lambda a: torch.as_tensor(a)
+        cached = Csr(t(op.crow), t(op.pre), t(op.post), tuple(op.shape))
+        object.__setattr__(op, "_csr", cached)
+    return cached
 
 
 class SparseRecurrent(torch.autograd.Function):

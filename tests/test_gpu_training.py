@@ -238,3 +238,53 @@ def test_training_mode_without_autograd_updates_the_normaliser_and_matches_eval(
     with torch.no_grad():
         logits_eval, _ = net(x)
     _close(logits_eval, logits_train, 2e-3, "eval after the first training-mode call")
+
+
+def test_full_scale_train_step_gradients_match_the_oracle(full_net):
+    """The train_step loss on the full 166,700-neuron synthetic network (6 steps, 4 positions): every
+    parameter's gradient against the oracle in float64.  Only gradients are computed; the shared network's
+    parameters are not changed."""
+    from chessfly.encoding import N_BASE, N_MOVES
+    from chessfly.synthetic import synthetic_boards
+    from oracle import training as T
+    from oracle.forward import HeadArrays
+    from oracle.lightcone import light_cone
+    net, conn = full_net
+    batch = 4
+    x = torch.as_tensor(synthetic_boards(batch, seed=11), dtype=torch.float32)
+    rng = np.random.default_rng(1)
+    legal = torch.as_tensor(rng.random((batch, N_MOVES)) < 0.01)
+    legal[:, 0] = True
+    pi = torch.where(legal, torch.as_tensor(rng.random((batch, N_MOVES))), torch.zeros(()))
+    pi = pi / pi.sum(1, keepdim=True)
+    wdl = torch.as_tensor(rng.integers(0, 3, batch))
+    net.zero_grad(set_to_none=True)
+    try:
+        logits, wdl_logits = net(x.to(DEV))
+        T.train_loss(logits, wdl_logits, pi.float().to(DEV), legal.to(DEV), wdl.to(DEV)).backward()
+        got = {"log_gain": net.brain.log_gain.grad.cpu(), "bias": net.brain.bias.grad.cpu(),
+               "alpha_logit": net.brain.alpha_logit.grad.cpu(), "encoder": net.encoder.weight.grad[:, :N_BASE].cpu(),
+               "policy": net.policy.weight.grad.cpu(), "value": net.value.weight.grad.cpu()}
+        logits = logits.detach().cpu()
+    finally:
+        net.zero_grad(set_to_none=True)
+    brain = net.brain
+    d = lambda t: t.detach().double().cpu().clone().requires_grad_(True)
+    b = brain_arrays(conn, net.cfg.weight_scale, brain.log_gain.detach().cpu(), brain.bias.detach().cpu(),
+                     brain.alpha_logit.detach().cpu(), dtype=torch.double)
+    for name in ("log_gain", "bias", "alpha_logit"):
+        setattr(b, name, getattr(b, name).clone().requires_grad_(True))
+    hp = HeadArrays(d(net.encoder.weight), d(net.encoder.bias), net.cfg.input_gain, N_BASE, d(net.policy.weight),
+                    d(net.policy.bias), d(net.policy_from.weight), d(net.policy_from.bias), d(net.policy_to.weight),
+                    d(net.policy_to.bias), d(net.value.weight), d(net.value.bias), net.move_from.cpu(),
+                    net.move_to.cpu(), net.norm.mean.double().cpu(), net.norm.var.double().cpu())
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), net.in_idx.cpu().numpy(),
+                      net.out_idx.cpu().numpy(), net.cfg.steps)
+    rl, rw = T.model_grad(hp, b, cone, x.double())
+    T.train_loss(rl, rw, pi.double(), legal, wdl).backward()
+    _close(logits, rl, 1e-4, "logits")
+    want = {"log_gain": b.log_gain.grad, "bias": b.bias.grad, "alpha_logit": b.alpha_logit.grad,
+            "encoder": hp.enc_w.grad[:, :N_BASE], "policy": hp.policy_w.grad, "value": hp.value_w.grad}
+    for name in got:
+        assert float(want[name].abs().max()) > 0, name
+        _close(got[name], want[name], 1e-3, name)
