@@ -69,7 +69,8 @@ def _sddmm(crow32, col32, n_rows: int, n_cols: int, g: torch.Tensor, x: torch.Te
     if nnz:
         _hip.check(_hip.load().fly_sddmm(crow32.data_ptr(), col32.data_ptr(), n_rows, n_cols, g.data_ptr(),
                                          max(batch, 1), x.data_ptr(), max(batch, 1), batch, out.data_ptr(),
-                                         _hip.ptr(ids32), int(ids32 is not None), _hip.stream(x.device)), "fly_sddmm")
+                                         out.numel(), _hip.ptr(ids32), int(ids32 is not None),
+                                         _hip.stream(x.device)), "fly_sddmm")
     return out
 
 
@@ -155,9 +156,12 @@ class _ConeRecurrence(torch.autograd.Function):
             else:
                 y = torch.empty(rows, batch, dtype=torch.float32, device=dev)
             hn = torch.empty(rows, batch, dtype=torch.float32, device=dev)
+            # operands bound to names: a temporary freed inside the argument list could be reused (and
+            # overwritten on the stream) by the next one before the kernel reads it
+            k, pdef, alpha = k.contiguous(), pdef.contiguous(), alpha.contiguous()
             _hip.check(lib.fly_train_step_forward(
-                rows, batch, y.data_ptr(), ld, int(op is not None), k.contiguous().data_ptr(),
-                pdef.contiguous().data_ptr(), alpha.contiguous().data_ptr(),
+                rows, batch, y.data_ptr(), ld, int(op is not None), k.data_ptr(),
+                pdef.data_ptr(), alpha.data_ptr(),
                 _hip.ptr(prev32 if h is not None and h.shape[0] else None), usrc32.data_ptr(), u_in.data_ptr(), ld,
                 _hip.ptr(h), ld, float(h_max), hn.data_ptr(), ld, st), "fly_train_step_forward")
             hs.append(hn)
@@ -193,9 +197,10 @@ class _ConeRecurrence(torch.autograd.Function):
             ga = torch.empty_like(gk)
             gpdef = torch.empty_like(gk)
             gh_prev = torch.zeros(cone.row_counts[t - 1], batch, dtype=torch.float32, device=dev) if t > 1 else None
+            pdef, alpha = pdef.contiguous(), alpha.contiguous()
             _hip.check(lib.fly_train_step_backward(
-                rows, batch, g.data_ptr(), ld, ys[t - 1].data_ptr(), ld, pdef.contiguous().data_ptr(),
-                alpha.contiguous().data_ptr(), _hip.ptr(prev32 if h_prev is not None and h_prev.shape[0] else None),
+                rows, batch, g.data_ptr(), ld, ys[t - 1].data_ptr(), ld, pdef.data_ptr(),
+                alpha.data_ptr(), _hip.ptr(prev32 if h_prev is not None and h_prev.shape[0] else None),
                 usrc32.data_ptr(), _hip.ptr(h_prev), ld, ctx.h_max, gy.data_ptr(), ld, gk.data_ptr(), ga.data_ptr(),
                 gpdef.data_ptr(), gu.data_ptr(), ld, _hip.ptr(gh_prev), ld, st), "fly_train_step_backward")
             grads[3 * (t - 1)] = gk.view_as(k)
@@ -203,9 +208,17 @@ class _ConeRecurrence(torch.autograd.Function):
             grads[3 * (t - 1) + 2] = ga.view_as(alpha)
             if op is not None:
                 crow32, col32, n_rows, n_cols = op._structure()
-                _product(op, w, gy, transposed=True, out=gh_prev)
-                ids32, ids = op._edge_ids()
-                _sddmm(crow32, col32, n_rows, n_cols, gy, h_prev, len(ids), out=gw, ids32=ids32)
+                if batch % 4 == 0:          # one pass over A^T: the state gradient and dL/dw together
+                    t_crow32, t_col32, t_ids32 = op._transposed()
+                    vals_t = _gathered(op, w, True)
+                    _hip.check(lib.fly_transposed_backward(
+                        t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(), t_ids32.data_ptr(),
+                        t_ids32.numel(), n_cols, n_rows, gy.data_ptr(), ld, h_prev.data_ptr(), ld, batch,
+                        gh_prev.data_ptr(), ld, 1, gw.data_ptr(), gw.numel(), st), "fly_transposed_backward")
+                else:
+                    _product(op, w, gy, transposed=True, out=gh_prev)
+                    ids32, ids = op._edge_ids()
+                    _sddmm(crow32, col32, n_rows, n_cols, gy, h_prev, len(ids), out=gw, ids32=ids32)
             g = gh_prev
         return (None, None, gu, gw, *grads)
 

@@ -107,6 +107,7 @@ struct SddmmArgs {
   int64_t ldg, ldx;
   uint32_t xbytes;
   int32_t nrows, batch, accumulate;
+  uint32_t n_out;         // entries of out: ids at or past it are skipped
 };
 
 // One wave per row, one lane per non-zero (64 at a time): lane e walks x[col_e, :] in 16-byte steps, 8 of
@@ -154,8 +155,9 @@ __global__ __launch_bounds__(256) void k_sddmm(const SddmmArgs a) {
     for (int32_t b = full; b < a.batch; ++b)
       acc = fmaf(grow[b], __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (int)(base + (uint32_t)b * 4u), 0, 0)),
                  acc);
-    if (live) {
-      float *dst = a.out + (a.ids ? a.ids[e] : e);
+    const uint32_t slot = live ? (a.ids ? (uint32_t)a.ids[e] : (uint32_t)e) : a.n_out;
+    if (slot < a.n_out) {
+      float *dst = a.out + slot;
       *dst = a.accumulate ? *dst + acc : acc;
     }
   }
@@ -339,6 +341,115 @@ __global__ __launch_bounds__(256) void k_train_bwd(const StepBwdArgs a) {
   }
 }
 
+// ---- backward of y = A h in one pass: grad_h = A^T grad_y and dL/dw ----------------------------------
+struct TransposedArgs {
+  const int32_t *t_rowptr;  // CSR of A^T: rows are A's columns (rows of h)
+  const int32_t *t_col;     // A's row of each non-zero (row of grad_y)
+  const float *vals;        // values in A^T's order
+  const int32_t *ids;       // index of each non-zero in the weight vector gw
+  const float *gy;          // (rows of A, ldgy)
+  const float *h;           // (rows of h, ldh)
+  float *gh;                // (rows of h, ldgh)
+  float *gw;                // weight gradient, += per non-zero
+  int64_t ldgy, ldh, ldgh;
+  uint32_t gybytes;
+  int32_t nrows, batch, accumulate;
+  int32_t nnz;              // non-zeros of A^T: row pointers are clamped into [0, nnz]
+  uint32_t n_w;             // entries of gw: ids at or past it are skipped
+};
+
+// Sum over the 16 lanes of each DPP row (lanes 16 r .. 16 r + 15), in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false));  // row_ror:2
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false));  // row_ror:1
+  return v;
+}
+
+// One wave per row j of A^T, 4 lane groups of 16 lanes x 4 columns (64 columns per chunk).  The row's
+// non-zeros go in blocks of 64: group g takes non-zeros 4 r + g of the block (r = 0..15).  Per chunk every
+// gathered grad_y row serves both products: it accumulates w * grad_y into grad_h[j] (the groups meet
+// through the permlane sum) and its dot with h[j] accumulates into the non-zero's partial in a register, so
+// dL/dw needs no second gather.  After the last chunk each group sums its 16 lanes' partials per non-zero.
+__global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArgs a) {
+  constexpr int R = 16;                    // rounds per block of 64 non-zeros
+  const uint32_t j = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (j >= (uint32_t)a.nrows) return;
+  const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
+  // a malformed row pointer gives wrong results, never an access outside the arrays
+  const int32_t beg = min(max(a.t_rowptr[j], 0), a.nnz);
+  const int32_t end = min(max(a.t_rowptr[j + 1], beg), a.nnz), n = end - beg;
+  const int32_t chunks = (a.batch + 63) / 64;
+  const __amdgpu_buffer_rsrc_t rc = buffer_of(a.t_col + beg, (uint32_t)n * 4u);
+  const __amdgpu_buffer_rsrc_t rv = buffer_of(a.vals + beg, (uint32_t)n * 4u);
+  const __amdgpu_buffer_rsrc_t ri = buffer_of(a.ids + beg, (uint32_t)n * 4u);
+  const __amdgpu_buffer_rsrc_t rgy = buffer_of(a.gy, a.gybytes);
+  const uint32_t gy_row = (uint32_t)a.ldgy * 4u;
+  const float *hj = a.h + (int64_t)j * a.ldh;
+  float *ghj = a.gh + (int64_t)j * a.ldgh;
+  bool first = true;
+  for (int32_t blk = 0; blk < n || (blk == 0 && !a.accumulate); blk += 64) {
+    int32_t c[R];
+    float w[R], dot[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {          // past the row's end: column 0, weight 0 (no share of grad_h)
+      const int off = (blk + 4 * r + g) * 4;
+      c[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
+      w[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      dot[r] = 0.0f;
+    }
+    for (int32_t ch = 0; ch < chunks; ++ch) {
+      const int32_t col0 = ch * 64 + s * 4;
+      const bool live = col0 < a.batch;    // the batch is a multiple of 4 on this path
+      float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (live) hv = *reinterpret_cast<const float4 *>(hj + col0);
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r0 = 0; r0 < R; r0 += 4) {
+        float4 x[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          typedef unsigned u4 __attribute__((ext_vector_type(4)));
+          const u4 v = __builtin_amdgcn_raw_buffer_load_b128(
+              rgy, (int)(__umul24((uint32_t)c[r0 + q], gy_row) + (uint32_t)col0 * 4u), 0, 0);
+          x[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float wq = w[r0 + q];
+          acc[0] = fmaf(wq, x[q].x, acc[0]);
+          acc[1] = fmaf(wq, x[q].y, acc[1]);
+          acc[2] = fmaf(wq, x[q].z, acc[2]);
+          acc[3] = fmaf(wq, x[q].w, acc[3]);
+          dot[r0 + q] = fmaf(x[q].x, hv.x, fmaf(x[q].y, hv.y, fmaf(x[q].z, hv.z, fmaf(x[q].w, hv.w, dot[r0 + q]))));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = group_sum<16>(acc[i]);
+      if (g == 0 && live) {
+        float4 *dst = reinterpret_cast<float4 *>(ghj + col0);
+        float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        if (a.accumulate || !first) {
+          const float4 o = *dst;
+          v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        }
+        *dst = v;
+      }
+    }
+    first = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float d = row16_sum(dot[r]);
+      const int32_t e = blk + 4 * r + g;
+      if (s == 0 && e < n) {
+        const uint32_t id = __builtin_amdgcn_raw_buffer_load_b32(ri, e * 4, 0, 0);
+        if (id < a.n_w) a.gw[id] += d;
+      }
+    }
+  }
+}
+
 bool vec4_ok(const void *p, int64_t ld) { return ld % 4 == 0 && aligned(p, 16); }
 
 uint32_t checked_bytes(int64_t rows, int64_t ld) {
@@ -396,8 +507,8 @@ extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *
 }
 
 extern "C" int fly_sddmm(const int32_t *rowptr, const int32_t *col, int64_t nrows, int64_t ncols, const float *g,
-                         int64_t ldg, const float *x, int64_t ldx, int64_t batch, float *out, const int32_t *ids,
-                         int32_t accumulate, void *stream) {
+                         int64_t ldg, const float *x, int64_t ldx, int64_t batch, float *out, int64_t n_out,
+                         const int32_t *ids, int32_t accumulate, void *stream) {
   return guard([&] {
     FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0, "negative size");
     FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
@@ -405,8 +516,9 @@ extern "C" int fly_sddmm(const int32_t *rowptr, const int32_t *col, int64_t nrow
     FLY_REQUIRE(rowptr && col && out && g && ldg >= batch, "bad argument");
     FLY_REQUIRE(ncols == 0 || (x && ldx >= batch && ldx < (1 << 22)), "bad argument");
     LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    FLY_REQUIRE(n_out >= 0 && n_out < (int64_t)1 << 32, "n_out out of range");
     SddmmArgs a{rowptr, col, g, x, out, ids, ldg, ldx, ncols ? checked_bytes(ncols, ldx) : 0u, (int32_t)nrows,
-                (int32_t)batch, accumulate != 0};
+                (int32_t)batch, accumulate != 0, (uint32_t)n_out};
     const dim3 grid(blocks_for(nrows, 4)), block(256);
     if (batch >= 4 && vec4_ok(x, ldx))
       hipLaunchKernelGGL(k_sddmm<4>, grid, block, 0, as_stream(stream), a);
@@ -463,5 +575,29 @@ extern "C" int fly_train_step_backward(int64_t rows, int64_t batch, const float 
     else
       hipLaunchKernelGGL(k_train_bwd<1>, grid, block, 0, as_stream(stream), a);
     check_launch("train step backward");
+  });
+}
+
+extern "C" int fly_transposed_backward(const int32_t *t_rowptr, const int32_t *t_col, const float *vals,
+                                       const int32_t *ids, int64_t nnz, int64_t nrows, int64_t ncols,
+                                       const float *gy, int64_t ldgy, const float *h, int64_t ldh, int64_t batch,
+                                       float *gh, int64_t ldgh, int32_t accumulate, float *gw, int64_t n_w,
+                                       void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0, "negative size");
+    FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
+    if (!nrows || !batch) return;
+    FLY_REQUIRE(t_rowptr && t_col && vals && ids && gw && h && gh, "bad argument");
+    FLY_REQUIRE(batch % 4 == 0 && vec4_ok(h, ldh) && vec4_ok(gh, ldgh) && vec4_ok(gy, ldgy) && ldh >= batch &&
+                    ldgh >= batch && ldgy >= batch && ldgy < (1 << 22),
+                "the fused backward needs a batch that is a multiple of 4 and 16-byte aligned rows");
+    FLY_REQUIRE(ncols == 0 || gy, "bad argument");
+    FLY_REQUIRE(nnz >= 0 && nnz < (int64_t)1 << 30 && n_w >= 0 && n_w < (int64_t)1 << 32, "nnz or n_w out of range");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    TransposedArgs a{t_rowptr, t_col, vals, ids, gy, h, gh, gw, ldgy, ldh, ldgh,
+                     ncols ? checked_bytes(ncols, ldgy) : 0u, (int32_t)nrows, (int32_t)batch, accumulate != 0,
+                     (int32_t)nnz, (uint32_t)n_w};
+    hipLaunchKernelGGL(k_transposed_backward, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), a);
+    check_launch("transposed backward");
   });
 }

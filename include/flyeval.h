@@ -187,15 +187,27 @@ int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t
  *              forward product, and with the transposed structure of A the state gradient A^T grad_y.
  *   fly_sddmm: out[e] = sum_b g[row_e, b] x[col_e, b] for every non-zero e, CSR order: the per-synapse
  *              gradient of y = A x with g = dL/dy.  With ids (distinct), out[ids[e]] instead (a sub-matrix's
- *              gradient straight into the whole weight vector); accumulate != 0 adds.  out must not overlap g.
+ *              gradient straight into the whole weight vector); accumulate != 0 adds; out holds n_out entries and slots at
+ *              or past it are skipped.  out must not overlap g.
  * Gathered operands must be below 2 GiB; rows and columns below 2^24; column indices are not range-checked
  * (a wrong index reads wrong data, never outside x). */
 int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, const int32_t *val_ids_dev,
              int64_t n_val, int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx, int64_t batch,
              float *y_dev, int64_t ldy, int32_t accumulate, void *stream);
 int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
-              int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, const int32_t *ids_dev,
-              int32_t accumulate, void *stream);
+              int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, int64_t n_out,
+              const int32_t *ids_dev, int32_t accumulate, void *stream);
+
+/* The backward of y = A h in one pass over A^T (CSR t_rowptr / t_col, values vals in that order, ids = each
+ * non-zero's index in the weight vector): gh (ncols of A, ldgh) (+)= A^T gy and gw[ids[e]] += sum_b
+ * gy[row_e, b] h[col_e, b].  Every gathered row of gy serves both.  nrows = rows of A^T (= rows of h),
+ * ncols = columns of A^T (= rows of gy); nnz = non-zeros of A^T; n_w = entries of gw.  The batch must be a
+ * multiple of 4 and the rows 16-byte aligned; ids distinct.  Row pointers are clamped into [0, nnz] and ids at
+ * or past n_w skipped, so a malformed structure gives wrong results, never an access outside the arrays. */
+int fly_transposed_backward(const int32_t *t_rowptr_dev, const int32_t *t_col_dev, const float *vals_dev,
+                            const int32_t *ids_dev, int64_t nnz, int64_t nrows, int64_t ncols, const float *gy_dev,
+                            int64_t ldgy, const float *h_dev, int64_t ldh, int64_t batch, float *gh_dev,
+                            int64_t ldgh, int32_t accumulate, float *gw_dev, int64_t n_w, void *stream);
 
 /* One recurrent step of training, the elementwise parts fused (brain.py:313-327 under autograd), float32,
  * one row of R_t per wave; rows are (rows, batch) with leading dimensions ld*:

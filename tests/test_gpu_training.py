@@ -64,7 +64,8 @@ def test_spmm_and_sddmm_match_float64(batch, ld_pad):
     perm = torch.randperm(3 * nnz, device=DEV)[:nnz]
     big = torch.zeros(3 * nnz, device=DEV)
     big[perm] = val_d
-    _hip.check(lib.fly_spmm(crow_d.data_ptr(), col_d.data_ptr(), big.data_ptr(), perm.to(torch.int32).data_ptr(),
+    perm32 = perm.to(torch.int32)
+    _hip.check(lib.fly_spmm(crow_d.data_ptr(), col_d.data_ptr(), big.data_ptr(), perm32.data_ptr(),
                             big.numel(), rows, cols, x_d.data_ptr(), ld, batch, y2.data_ptr(), ld, 1, st),
                "fly_spmm accumulate")
     _close(y2[:, :batch], torch.as_tensor(2 * ref), 1e-5, "spmm accumulate through value ids")
@@ -72,17 +73,53 @@ def test_spmm_and_sddmm_match_float64(batch, ld_pad):
         assert bool((y[:, batch:] == 7.0).all())                # padding columns are not written
     out = torch.empty(nnz, device=DEV)
     _hip.check(lib.fly_sddmm(crow_d.data_ptr(), col_d.data_ptr(), rows, cols, g_d.data_ptr(), ld, x_d.data_ptr(), ld,
-                             batch, out.data_ptr(), None, 0, st), "fly_sddmm")
+                             batch, out.data_ptr(), out.numel(), None, 0, st), "fly_sddmm")
     ref_w = (g[r, :batch] * x[c, :batch]).sum(1)
     _close(out, torch.as_tensor(ref_w), 1e-5, "sddmm")
     # scattered into a larger vector by distinct ids, accumulating
     ids = torch.randperm(2 * nnz, device=DEV)[:nnz].to(torch.int32)
     big = torch.ones(2 * nnz, device=DEV)
     _hip.check(lib.fly_sddmm(crow_d.data_ptr(), col_d.data_ptr(), rows, cols, g_d.data_ptr(), ld, x_d.data_ptr(), ld,
-                             batch, big.data_ptr(), ids.data_ptr(), 1, st), "fly_sddmm ids")
+                             batch, big.data_ptr(), big.numel(), ids.data_ptr(), 1, st), "fly_sddmm ids")
     want = torch.ones(2 * nnz, dtype=torch.float64)
     want[ids.long().cpu()] += torch.as_tensor(ref_w)
     _close(big, want, 1e-5, "sddmm scattered")
+
+
+@pytest.mark.parametrize("batch", [4, 64, 200, 256])
+def test_transposed_backward_matches_float64(batch):
+    """fly_transposed_backward: grad_h (+)= A^T g and gw[ids[e]] += sum_b g[row_e, b] h[col_e, b] in one pass,
+    against float64, on a matrix with rows of A^T longer than one block of 64 non-zeros and empty ones."""
+    from chessfly import _hip
+    lib = _hip.load()
+    rows, cols, nnz = 400, 300, 30000                            # ~100 non-zeros per row of A^T
+    crow, r, c, val = _random_csr(rows, cols, nnz, batch + 7)
+    order = np.lexsort((r, c))                                  # A^T in CSR: by column, then row
+    t_crow = np.zeros(cols + 1, np.int64)
+    np.cumsum(np.bincount(c, minlength=cols), out=t_crow[1:])
+    rng = np.random.default_rng(batch)
+    g = rng.normal(0, 1, (rows, batch))
+    h = rng.normal(0, 1, (cols, batch))
+    gh0 = rng.normal(0, 1, (cols, batch))
+    ids = rng.permutation(2 * nnz)[:nnz]                         # each non-zero's slot in a longer vector
+    gw0 = rng.normal(0, 1, 2 * nnz)
+    d = lambda a, dt=torch.float32: torch.as_tensor(np.ascontiguousarray(a), device=DEV).to(dt)
+    # every operand bound to a name that lives across the call (a temporary freed in the argument list
+    # could be handed to the next one and overwritten before the kernel reads it)
+    t_crow_d, t_col_d, t_val_d, t_ids_d = d(t_crow, torch.int32), d(r[order], torch.int32), d(val[order]), \
+        d(ids[order], torch.int32)
+    g_d, h_d, gh, gw = d(g), d(h), d(gh0), d(gw0)
+    st = _hip.stream(torch.device(DEV))
+    _hip.check(lib.fly_transposed_backward(t_crow_d.data_ptr(), t_col_d.data_ptr(), t_val_d.data_ptr(),
+                                           t_ids_d.data_ptr(), nnz, cols, rows, g_d.data_ptr(), batch, h_d.data_ptr(),
+                                           batch, batch, gh.data_ptr(), batch, 1, gw.data_ptr(), gw.numel(), st),
+               "fly_transposed_backward")
+    dense = np.zeros((rows, cols))
+    np.add.at(dense, (r, c), val)
+    _close(gh, torch.as_tensor(gh0 + dense.T @ g), 1e-5, "grad_h")
+    want = gw0.copy()
+    want[ids] += (g[r] * h[c]).sum(1)
+    _close(gw, torch.as_tensor(want), 1e-5, "dL/dw")
 
 
 def _rnn_pair(conn, seed: int, scale: float = 3.0):
