@@ -12,9 +12,12 @@
 // the boards and the normalised outputs are split per forward by small prologue kernels, the latter reading
 // the final recurrent state in place (output gather, normaliser and transpose in one pass).
 //
-// GEMM tiling: C = A B^T with both operands K-contiguous (K padded to 32 with zeros), 64x64 output tiles per
-// workgroup of 4 waves (2x2 waves of 32x32, each 2x2 MFMA 16x16 tiles), K staged 32 at a time through LDS
-// as hi/lo halves, 16-byte global loads and 16-byte LDS fragment reads.
+// GEMM tiling: C = A B^T with both operands K-contiguous (K padded to 64 with zeros).  A workgroup of 4 waves
+// owns a 128 x 128, 128 x 64 or 64 x 64 output tile (2 x 2 waves, each a grid of 16 x 16 MFMA tiles); K is staged 64
+// at a time through LDS as hi/lo halves with the next stage's 16-byte global loads in flight, and tiles are
+// ordered so the workgroups one XCD runs together share operand rows in its L2.  The boards' lo half is zero when
+// they are exact in float16 (binary planes always are); the split records that per board and a tile whose boards
+// are all exact leaves out the A_hi B_lo product.
 #include "common.hpp"
 
 #include <cmath>
@@ -47,22 +50,31 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int GBM = 64, GBN = 64, GBK = 32, LDK = GBK + 8;  // LDS rows padded to 80 bytes
+constexpr int GBK = 64, LDK = GBK + 8;  // K per LDS stage; LDS rows padded to 144 bytes
 
 int64_t pad_k(int64_t k) { return round_up(std::max<int64_t>(k, 1), GBK); }
 
-// hi = fp16(v * scale), lo = fp16(v * scale - hi), rows x kp, zero beyond k.  A float16 source widens
-// exactly, so with scale 1 its lo half is zero.
+// hi = fp16(v * scale), lo = fp16(v * scale - hi), rows x kp, zero beyond k; one workgroup per row.  A float16
+// source widens exactly, so with scale 1 its lo half is zero.  flag[r] (when given) records whether any lo of row r
+// is non-zero, so the GEMM can leave out the product with a tile's lo half when every row of the tile is exact.
 template <typename T>
-__global__ void k_split_rows(const T *__restrict__ src, int64_t ld, int64_t rows, int64_t k, float scale,
-                             _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, int64_t kp) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= rows * kp) return;
-  const int64_t r = i / kp, c = i - r * kp;
-  const float v = c < k ? static_cast<float>(src[r * ld + c]) * scale : 0.0f;
-  const _Float16 h = static_cast<_Float16>(v);
-  hi[i] = h;
-  lo[i] = static_cast<_Float16>(v - static_cast<float>(h));
+__global__ __launch_bounds__(256) void k_split_rows(const T *__restrict__ src, int64_t ld, int64_t k, float scale,
+                                                    _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, int64_t kp,
+                                                    int32_t *__restrict__ flag) {
+  const int64_t r = blockIdx.x;
+  bool any = false;
+  for (int64_t c = threadIdx.x; c < kp; c += blockDim.x) {
+    const float v = c < k ? static_cast<float>(src[r * ld + c]) * scale : 0.0f;
+    const _Float16 h = static_cast<_Float16>(v);
+    const _Float16 l = static_cast<_Float16>(v - static_cast<float>(h));
+    hi[r * kp + c] = h;
+    lo[r * kp + c] = l;
+    any |= l != static_cast<_Float16>(0.0f);
+  }
+  if (flag != nullptr) {
+    const int a = __syncthreads_or(any);
+    if (threadIdx.x == 0) flag[r] = a;
+  }
 }
 
 // Normalised outputs r[n, k] split into (N x kp) hi/lo rows, read from the state (rows, lds) where output k
@@ -102,7 +114,8 @@ __global__ __launch_bounds__(256) void k_norm_split(const S *__restrict__ state,
 
 struct Split {
   const _Float16 *hi, *lo;
-  int64_t rows;  // leading dimension is the padded K
+  int64_t rows;          // leading dimension is the padded K
+  const int32_t *flag;   // per row: lo is non-zero somewhere (null: assume it is)
 };
 
 struct EncoderEpilogue {
@@ -127,69 +140,148 @@ struct HeadEpilogue {
 
 __device__ __forceinline__ half8 load8(const _Float16 *p) { return *reinterpret_cast<const half8 *>(p); }
 
-template <class EP>
-__global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B, int64_t kp, float unscale, const EP ep) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][GBM][LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][GBN][LDK];
+// Tile order: the dispatcher hands workgroup L to XCD L mod 8, so the tile of workgroup L is chosen to give each
+// XCD a contiguous run of tiles in row-major (A-tile, B-tile) order.  The tiles an XCD runs together then share
+// their A rows and sweep the same B rows, and each operand crosses into an XCD's L2 about once.
+__device__ __forceinline__ void xcd_tile(int tiles, int gx, int &ty, int &tx) {
+  const int L = blockIdx.x, xcd = L & 7, slot = L >> 3, per = tiles >> 3, rem = tiles & 7;
+  const int q = xcd * per + min(xcd, rem) + slot;
+  ty = q / gx;
+  tx = q - ty * gx;
+}
+
+// C = A B^T on split operands.  4 waves in 2 x 2, each owning (16 TM) x (16 TN) of the (32 TM) x (32 TN) tile.
+// K is staged 64 at a time through LDS: each row of a stage is one 128-byte line, loaded by 8 consecutive lanes and
+// written to LDS in one piece; rows are padded to 144 bytes so 16-byte fragment reads are free of bank conflicts.  The
+// next stage's global loads are issued before the current stage's MFMAs.  BLO = false leaves out A_hi B_lo, for tiles
+// whose B rows are all exact in float16.
+template <int TM, int TN, bool BLO, class EP>
+__device__ __forceinline__ void gemm_tile(const Split &A, const Split &B, int64_t kp, float unscale, const EP &ep,
+                                          int64_t m0, int64_t n0, _Float16 (*As)[32 * TM][LDK],
+                                          _Float16 (*Bs)[32 * TN][LDK]) {
+  constexpr int OCT = GBK / 8, RPP = 256 / OCT;          // 16-byte pieces per row, rows per pass of 256 threads
+  constexpr int AL = 32 * TM / RPP, BL = 32 * TN / RPP;  // passes per operand half
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.y * GBM, n0 = (int64_t)blockIdx.x * GBN;
-  const int lr = tid >> 2, lk = (tid & 3) * 8;  // this thread's 16-byte piece of a 64x32 tile
+  const int lr = tid / OCT, lk = (tid % OCT) * 8;  // one full 128-byte line of K per row and stage
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  floatx4 acc[2][2];
+  int64_t aoff[AL], boff[BL];
+  bool aok[AL], bok[BL];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < AL; ++i) {
+    aok[i] = m0 + lr + RPP * i < A.rows;
+    aoff[i] = (aok[i] ? m0 + lr + RPP * i : 0) * kp + lk;
+  }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const bool a_ok = m0 + lr < A.rows, b_ok = n0 + lr < B.rows;
-  const int64_t arow = a_ok ? m0 + lr : 0, brow = b_ok ? n0 + lr : 0;
-  const _Float16 *ah = A.hi + arow * kp + lk, *al = A.lo + arow * kp + lk;
-  const _Float16 *bh = B.hi + brow * kp + lk, *bl = B.lo + brow * kp + lk;
-  for (int64_t k0 = 0; k0 < kp; k0 += GBK) {
-    const half8 vah = a_ok ? load8(ah + k0) : zero, val = a_ok ? load8(al + k0) : zero;
-    const half8 vbh = b_ok ? load8(bh + k0) : zero, vbl = b_ok ? load8(bl + k0) : zero;
-    *reinterpret_cast<half8 *>(&As[0][lr][lk]) = vah;
-    *reinterpret_cast<half8 *>(&As[1][lr][lk]) = val;
-    *reinterpret_cast<half8 *>(&Bs[0][lr][lk]) = vbh;
-    *reinterpret_cast<half8 *>(&Bs[1][lr][lk]) = vbl;
-    __syncthreads();
-    const int fk = 8 * (lane >> 4), fr = lane & 15;
-    half8 a_hi[2], a_lo[2], b_hi[2], b_lo[2];
+  for (int i = 0; i < BL; ++i) {
+    bok[i] = n0 + lr + RPP * i < B.rows;
+    boff[i] = (bok[i] ? n0 + lr + RPP * i : 0) * kp + lk;
+  }
+  half8 rah[AL], ral[AL], rbh[BL], rbl[BL];
+  auto fetch = [&](int64_t k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      a_hi[i] = *reinterpret_cast<const half8 *>(&As[0][wm * 32 + i * 16 + fr][fk]);
-      a_lo[i] = *reinterpret_cast<const half8 *>(&As[1][wm * 32 + i * 16 + fr][fk]);
-      b_hi[i] = *reinterpret_cast<const half8 *>(&Bs[0][wn * 32 + i * 16 + fr][fk]);
-      b_lo[i] = *reinterpret_cast<const half8 *>(&Bs[1][wn * 32 + i * 16 + fr][fk]);
+    for (int i = 0; i < AL; ++i) {
+      rah[i] = aok[i] ? load8(A.hi + aoff[i] + k0) : zero;
+      ral[i] = aok[i] ? load8(A.lo + aoff[i] + k0) : zero;
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < BL; ++i) {
+      rbh[i] = bok[i] ? load8(B.hi + boff[i] + k0) : zero;
+      if (BLO) rbl[i] = bok[i] ? load8(B.lo + boff[i] + k0) : zero;
+    }
+  };
+  floatx4 acc[TM][TN];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[i], b_hi[j], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[i], b_lo[j], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[i], b_hi[j], acc[i][j], 0, 0, 0);
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int fk = 8 * (lane >> 4), fr = lane & 15;
+  fetch(0);
+  for (int64_t k0 = 0; k0 < kp; k0 += GBK) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+      *reinterpret_cast<half8 *>(&As[0][lr + RPP * i][lk]) = rah[i];
+      *reinterpret_cast<half8 *>(&As[1][lr + RPP * i][lk]) = ral[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      *reinterpret_cast<half8 *>(&Bs[0][lr + RPP * i][lk]) = rbh[i];
+      if (BLO) *reinterpret_cast<half8 *>(&Bs[1][lr + RPP * i][lk]) = rbl[i];
+    }
+    __syncthreads();
+    if (k0 + GBK < kp) fetch(k0 + GBK);
+#pragma unroll
+    for (int kk = 0; kk < GBK; kk += 32) {
+      half8 bh[TN], bl[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        bh[j] = *reinterpret_cast<const half8 *>(&Bs[0][wn * 16 * TN + j * 16 + fr][kk + fk]);
+        if (BLO) bl[j] = *reinterpret_cast<const half8 *>(&Bs[1][wn * 16 * TN + j * 16 + fr][kk + fk]);
       }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const half8 ah = *reinterpret_cast<const half8 *>(&As[0][wm * 16 * TM + i * 16 + fr][kk + fk]);
+        const half8 al = *reinterpret_cast<const half8 *>(&As[1][wm * 16 * TM + i * 16 + fr][kk + fk]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], acc[i][j], 0, 0, 0);
+          if (BLO) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
-        const int64_t n = n0 + wn * 32 + j * 16 + (lane & 15);
+        const int64_t m = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + r;
+        const int64_t n = n0 + wn * 16 * TN + j * 16 + (lane & 15);
         if (m < A.rows && n < B.rows) ep(m, n, acc[i][j][r] * unscale);
       }
 }
 
+template <int TM, int TN, class EP>
+__global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B, int64_t kp, float unscale, const EP ep,
+                                                    int tiles, int gx) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][32 * TM][LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][32 * TN][LDK];
+  int ty, tx;
+  xcd_tile(tiles, gx, ty, tx);
+  const int64_t m0 = (int64_t)ty * (32 * TM), n0 = (int64_t)tx * (32 * TN);
+  bool blo = true;
+  if (B.flag != nullptr) {  // uniform over the workgroup
+    const int i = threadIdx.x;
+    blo = __syncthreads_or(i < 32 * TN && n0 + i < B.rows && B.flag[n0 + i] != 0);
+  }
+  if (blo)
+    gemm_tile<TM, TN, true>(A, B, kp, unscale, ep, m0, n0, As, Bs);
+  else
+    gemm_tile<TM, TN, false>(A, B, kp, unscale, ep, m0, n0, As, Bs);
+}
+
+// Wave tiles of 64 x 64 (128 x 128 per workgroup) where that gives at least four tiles per CU, else 32 x 32 (64 x 64
+// per workgroup, up to four workgroups per CU): measured on the 17,937 x 1120 encoder and the 4,299 x 1120 head.
+// The gemm_tile tuning key forces one (1: 64 x 64 tiles, 2: 128 x 64, 3: 128 x 128).
 template <class EP>
 void gemm_split(const Split &A, const Split &B, int64_t kp, float unscale, const EP &ep, hipStream_t st) {
   if (A.rows == 0 || B.rows == 0) return;
-  const int64_t gy = (A.rows + GBM - 1) / GBM, gx = (B.rows + GBN - 1) / GBN;
-  FLY_REQUIRE(gy < 65536 && gx < INT32_MAX, "GEMM grid too large");
-  hipLaunchKernelGGL((k_gemm_split<EP>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, st, A, B, kp, unscale, ep);
+  auto count = [&](int bm, int bn) { return ((A.rows + bm - 1) / bm) * ((B.rows + bn - 1) / bn); };
+  int shape = tuning().gemm_tile;
+  if (shape < 1 || shape > 3) shape = count(128, 128) >= 1024 ? 3 : 1;
+  const int bm = shape == 1 ? 64 : 128, bn = shape == 3 ? 128 : 64;
+  const int64_t gx = (B.rows + bn - 1) / bn, tiles = count(bm, bn);
+  FLY_REQUIRE(tiles < INT32_MAX, "GEMM grid too large");
+  const dim3 grid((unsigned)tiles), block(256);
+  if (shape == 3)
+    hipLaunchKernelGGL((k_gemm_split<4, 4, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx);
+  else if (shape == 2)
+    hipLaunchKernelGGL((k_gemm_split<4, 2, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx);
+  else
+    hipLaunchKernelGGL((k_gemm_split<2, 2, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx);
   check_launch("split gemm");
 }
 
@@ -209,12 +301,17 @@ __global__ void k_assemble(const float *__restrict__ ct, int64_t ldc, int64_t n_
   }
 }
 
+// Grid-stride max of |w| with one atomic per wave (a fixed grid keeps the atomics on the one word few).
 __global__ void k_max_abs(const float *__restrict__ w, int64_t ld, int64_t rows, int64_t k, unsigned *__restrict__ out) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= rows * k) return;
-  const int64_t r = i / k, c = i - r * k;
-  const float a = fabsf(w[r * ld + c]);
-  if (a > 0.0f) atomicMax(out, __float_as_uint(a));   // non-negative floats order like their bit patterns
+  float a = 0.0f;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < rows * k; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / k, c = i - r * k;
+    a = fmaxf(a, fabsf(w[r * ld + c]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+  // non-negative floats order like their bit patterns
+  if ((threadIdx.x & 63) == 0 && a > 0.0f) atomicMax(out, __float_as_uint(a));
 }
 
 __global__ void k_check_squares(const int32_t *__restrict__ sq, int64_t n, int32_t *__restrict__ bad) {
@@ -232,7 +329,8 @@ float weight_scale(const float *w, int64_t ld, int64_t rows, int64_t k, hipStrea
   if (rows * k == 0) return 1.0f;
   DevArray<unsigned> mx(1);
   hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(1), 0, st, mx.p);
-  hipLaunchKernelGGL(k_max_abs, dim3(blocks_for(rows * k, kThreads)), dim3(kThreads), 0, st, w, ld, rows, k, mx.p);
+  hipLaunchKernelGGL(k_max_abs, dim3((unsigned)std::min<int64_t>(blocks_for(rows * k, kThreads), 1024)), dim3(kThreads), 0,
+                     st, w, ld, rows, k, mx.p);
   check_launch("max abs");
   unsigned bits = 0;
   FLY_HIP(hipMemcpyAsync(&bits, mx.p, sizeof(bits), hipMemcpyDeviceToHost, st));
@@ -247,10 +345,10 @@ float weight_scale(const float *w, int64_t ld, int64_t rows, int64_t k, hipStrea
 
 template <typename T>
 void split_into(const T *w, int64_t ld, int64_t rows, int64_t k, float scale, _Float16 *hi, _Float16 *lo,
-                int64_t kp, hipStream_t st) {
+                int64_t kp, hipStream_t st, int32_t *flag = nullptr) {
   if (rows == 0) return;
-  hipLaunchKernelGGL(k_split_rows<T>, dim3(blocks_for(rows * kp, kThreads)), dim3(kThreads), 0, st, w, ld, rows, k,
-                     scale, hi, lo, kp);
+  FLY_REQUIRE(rows < INT32_MAX, "too many rows to split");
+  hipLaunchKernelGGL(k_split_rows<T>, dim3((unsigned)rows), dim3(kThreads), 0, st, w, ld, k, scale, hi, lo, kp, flag);
   check_launch("split");
 }
 
@@ -260,7 +358,9 @@ int64_t head_ld(const fly_dense &d) { return round_up(d.head_rows(), 4); }
 
 size_t split_bytes(int64_t rows, int64_t kp) { return align256((size_t)rows * kp * sizeof(_Float16)); }
 
-size_t encoder_ws(const fly_dense &d, int64_t batch) { return 2 * split_bytes(batch, d.kp_enc); }
+size_t encoder_ws(const fly_dense &d, int64_t batch) {
+  return 2 * split_bytes(batch, d.kp_enc) + align256((size_t)batch * sizeof(int32_t));
+}
 
 size_t head_ws(const fly_dense &d, int64_t batch) {
   return 2 * split_bytes(batch, d.kp_head) + align256((size_t)batch * head_ld(d) * sizeof(float));
@@ -271,11 +371,12 @@ void run_encoder(const fly_dense &d, const void *x, bool x_f16, int64_t ldx, int
   LaunchTimer timer(FLY_K_ENCODER, st);
   _Float16 *xh = static_cast<_Float16 *>(ws);
   _Float16 *xl = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + split_bytes(batch, d.kp_enc));
+  int32_t *exact = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + 2 * split_bytes(batch, d.kp_enc));
   if (x_f16)
-    split_into(static_cast<const _Float16 *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st);
+    split_into(static_cast<const _Float16 *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st, exact);
   else
-    split_into(static_cast<const float *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st);
-  gemm_split(Split{d.enc_hi.p, d.enc_lo.p, d.n_in}, Split{xh, xl, batch}, d.kp_enc, d.enc_unscale,
+    split_into(static_cast<const float *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st, exact);
+  gemm_split(Split{d.enc_hi.p, d.enc_lo.p, d.n_in, nullptr}, Split{xh, xl, batch, exact}, d.kp_enc, d.enc_unscale,
              EncoderEpilogue{d.enc_b.p, gain, u, u16, ldu}, st);
 }
 
@@ -292,7 +393,8 @@ void run_head(const fly_dense &d, const S *state, int64_t lds, const int32_t *sr
                      d.clip, d.n_out, batch, rh, rl, d.kp_head);
   check_launch("normalised outputs");
   const int64_t ldc = head_ld(d);
-  gemm_split(Split{d.head_hi.p, d.head_lo.p, d.head_rows()}, Split{rh, rl, batch}, d.kp_head, d.head_unscale,
+  gemm_split(Split{d.head_hi.p, d.head_lo.p, d.head_rows(), nullptr}, Split{rh, rl, batch, nullptr}, d.kp_head,
+             d.head_unscale,
              HeadEpilogue{ct, ldc}, st);
   const dim3 agrid(blocks_for(d.n_moves, 256), (unsigned)std::min<int64_t>(batch, 65535));
   hipLaunchKernelGGL(k_assemble, agrid, dim3(256), 0, st, ct, ldc, d.n_moves, d.head_b.p, d.move_from.p, d.move_to.p,

@@ -704,6 +704,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "nt_store") tuning().nt_store = (int)value;
     else if (k == "tiles") tuning().tiles = (int)value;
     else if (k == "spmm_groups") tuning().spmm_groups = (int)value;
+    else if (k == "gemm_tile") tuning().gemm_tile = (int)value;
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });
 }

@@ -222,18 +222,30 @@ def _dense_plan(lib, _hip, n_in, k, ld, n_out, moves, rng, scale_w=0.05):
     return _hip.Handle(h, "fly_dense_destroy"), {key: T(v) for key, v in P.items()}, frm[:moves], to[:moves]
 
 
+@pytest.fixture
+def gemm_tile(request):
+    from chessfly import _hip
+    _hip.set_tuning("gemm_tile", request.param)
+    yield request.param
+    _hip.set_tuning("gemm_tile", 0)
+
+
+@pytest.mark.parametrize("gemm_tile", [0, 1, 2, 3], indirect=True)
 @pytest.mark.parametrize("batch,n_in,k,ld,n_out,moves", [(5, 70, 30, 33, 40, 100), (130, 300, 838, 967, 150, 4168),
                                                           (1, 17, 838, 967, 2333, 4168)])
-def test_encoder_and_head_gemms_match_fp64(batch, n_in, k, ld, n_out, moves):
-    """The split-fp16 matrix-core GEMMs hold float32 accuracy: encoder and head against fp64."""
+def test_encoder_and_head_gemms_match_fp64(batch, n_in, k, ld, n_out, moves, gemm_tile):
+    """The split-fp16 matrix-core GEMMs hold float32 accuracy: encoder and head against fp64, for every workgroup
+    tile shape (0: the automatic choice)."""
     from chessfly import _hip
     from oracle.forward import HeadArrays
     lib = _hip.load()
     rng = np.random.default_rng(batch)
     dense, P, frm, to = _dense_plan(lib, _hip, n_in, k, ld, n_out, moves, rng)
     x = torch.as_tensor(rng.random((batch, ld)) < 0.1, dtype=torch.float32)
-    x[:, 0] = 0.37
-    x[:, 1] = 1.0 / 3.0                      # not representable in fp16: exercises the low half of the split
+    # Values not representable in fp16 in the first three boards only: their tile runs the product with the boards'
+    # low half, the tiles of the later boards (exact in fp16) leave it out.
+    x[:3, 0] = 0.37
+    x[:3, 1] = 1.0 / 3.0
     ref = ((x[:, :k].double() @ P["enc_w"][:, :k].double().T + P["enc_b"].double()) * 5.0).T
     xd = x.to(DEV)
     ws = _hip.workspace(lib.fly_encoder_workspace(dense.handle, batch), torch.device(DEV))
