@@ -197,6 +197,45 @@ def test_deviation_path_matches_exact_function(batch):
     assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
 
 
+STEP_SHAPES = [{"groups": 4}, {"groups": 2}, {"groups": 1}, {"groups": 1, "unroll": 16}, {"groups": 1, "unroll": 32},
+               {"rows_mode": 1}, {"rows_mode": 1, "groups": 4}, {"rows_mode": 1, "unroll": 8}, {"rows_mode": -1},
+               {"vec": 4}, {"vec": 2}, {"vec": 1}, {"nt_store": 1}]
+
+
+@pytest.fixture
+def step_shape(request):
+    from chessfly import _hip
+    for key, value in request.param.items():
+        _hip.set_tuning(key, value)
+    yield request.param
+    for key in request.param:
+        _hip.set_tuning(key, 0)
+
+
+@pytest.mark.parametrize("step_shape", STEP_SHAPES, indirect=True, ids=lambda p: "-".join(f"{k}{v}" for k, v in p.items()))
+def test_every_step_kernel_shape_matches_the_oracle(step_shape):
+    """Every lane-group, row-slot, unroll and lane-width variant of the state step (selected with
+    fly_set_tuning) computes the same function: the fp16 deviation path within its tolerance of the exact
+    function and the float32 light cone within float32 round-off, at a batch that ends inside a chunk."""
+    conn = _medium(2)
+    lg, b, al = random_params(conn, 8, gain_sd=0.1)
+    rnn = product_rnn(conn, 4.0, lg, b, al)
+    ba = brain_arrays(conn, 4.0, lg, b, al, dtype=torch.float64)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    batch, steps = 100, 6
+    u_in = torch.randn(len(in_idx), batch, generator=torch.Generator().manual_seed(3))
+    cone = oracle_cone(conn, in_idx, out_idx, steps)
+    with torch.no_grad():
+        half = rnn.forward_io(u_in.half().to(DEV), in_idx.to(DEV), out_idx.to(DEV), steps)
+        full = rnn.forward_io(u_in.to(DEV), in_idx.to(DEV), out_idx.to(DEV), steps)
+    exact = F.cone_f32(ba, cone, u_in.half().double(), steps).numpy()
+    dev_scale = np.abs(exact - F.cone_f32(ba, cone, torch.zeros_like(u_in).double(), steps).numpy()).max()
+    err = np.abs(half.cpu().numpy() - exact).max()
+    assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
+    np.testing.assert_allclose(full.cpu().numpy(), F.cone_f32(ba, cone, u_in.double(), steps).numpy(),
+                               rtol=2e-5, atol=2e-5)
+
+
 def _dense_plan(lib, _hip, n_in, k, ld, n_out, moves, rng, scale_w=0.05):
     """A dense plan over random weights; returns (handle, host copies of the weights)."""
     import ctypes
