@@ -113,17 +113,15 @@ def _gathered(op, w: torch.Tensor, transposed: bool) -> torch.Tensor:
 
 
 def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out: torch.Tensor | None = None):
-    """A x (or A^T x) with A's values from w: one column reads w through value ids, more columns read values
-    gathered once per weight tensor (a dependent load per non-zero would sit on the gather's critical path)."""
+    """A x (or A^T x) with A's values from w, gathered once per weight tensor into the structure's order.
+    Every product of a training step over one structure shares the gathered copy, so each reads its values as
+    a stream; reading w through value ids instead would cost a random line per non-zero in the transposed
+    order, on every call."""
     if transposed:
-        crow32, col32, ids32 = op._transposed()
+        crow32, col32, _ = op._transposed()
         _, _, n_cols, n_rows = op._structure()
     else:
         crow32, col32, n_rows, n_cols = op._structure()
-        ids = op._edge_ids()
-        ids32 = None if ids is None else ids[0]
-    if x.shape[1] == 1 and (ids32 is not None or transposed):
-        return _spmm(crow32, col32, w, n_rows, n_cols, x, out=out, val_ids32=ids32)
     return _spmm(crow32, col32, _gathered(op, w, transposed), n_rows, n_cols, x, out=out)
 
 

@@ -37,13 +37,33 @@ def _random_csr(rows: int, cols: int, nnz: int, seed: int):
     return crow, r, c, rng.normal(0, 1, nnz)
 
 
-@pytest.mark.parametrize("batch,ld_pad", [(1, 0), (3, 0), (5, 3), (64, 0), (256, 0), (130, 2)])
-def test_spmm_and_sddmm_match_float64(batch, ld_pad):
-    """y = A x and out[e] = sum_b g[row_e, b] x[col_e, b] against float64, on 4-byte and 16-byte lanes."""
+def _heavy_csr(rows: int, cols: int, seed: int):
+    """Lognormal row lengths (like a transposed connectome) with rows of 700 and 1500 non-zeros, one of them in a
+    last, partial group of 8 rows, and empty rows."""
+    rng = np.random.default_rng(seed)
+    counts = np.minimum(rng.lognormal(np.log(20), 1.2, rows).astype(np.int64), 400)
+    counts[5], counts[rows - 3], counts[rows - 1] = 1500, 700, 0
+    counts[40:48] = 0
+    r = np.repeat(np.arange(rows), counts)
+    c = rng.integers(0, max(cols - 1, 1), len(r))
+    order = np.lexsort((c, r))
+    r, c = r[order], c[order]
+    crow = np.zeros(rows + 1, np.int64)
+    np.cumsum(counts, out=crow[1:])
+    return crow, r, c, rng.normal(0, 1, len(r))
+
+
+@pytest.mark.parametrize("batch,ld_pad,heavy", [(1, 0, False), (3, 0, False), (5, 3, False), (64, 0, False),
+                                                (256, 0, False), (130, 2, False), (1, 0, True), (1, 3, True),
+                                                (64, 0, True)])
+def test_spmm_and_sddmm_match_float64(batch, ld_pad, heavy):
+    """y = A x and out[e] = sum_b g[row_e, b] x[col_e, b] against float64, on 4-byte and 16-byte lanes; the
+    heavy-tailed matrices take the batch-1 kernels' whole-wave path for rows past 256 non-zeros."""
     from chessfly import _hip
     lib = _hip.load()
-    rows, cols, nnz = 700, 500, 9000
-    crow, r, c, val = _random_csr(rows, cols, nnz, batch)
+    rows, cols = 701, 500
+    crow, r, c, val = _heavy_csr(rows, cols, batch) if heavy else _random_csr(rows, cols, 9000, batch)
+    nnz = len(r)
     rng = np.random.default_rng(batch + 1)
     x = rng.normal(0, 1, (cols, batch + ld_pad))
     g = rng.normal(0, 1, (rows, batch + ld_pad))
