@@ -112,6 +112,32 @@ def _gathered(op, w: torch.Tensor, transposed: bool) -> torch.Tensor:
     return vals
 
 
+def backward_work(t_crow: torch.Tensor, seg: int = 256):
+    """The work list of fly_transposed_backward over the rows of A^T with row pointer t_crow: each row in
+    segments of at most `seg` non-zeros (a multiple of 64), longest first, so the heavy-tailed rows of A^T
+    (out-degrees) spread over several waves.  Returns (items (n, 4) int32 {row, first non-zero, count, slot},
+    splits (m, 4) int32 {row, first slot, slot count, 0}, number of partial slots)."""
+    if seg <= 0 or seg % 64:
+        raise ValueError("segments are whole blocks of 64 non-zeros")
+    dev = t_crow.device
+    crow = t_crow.to(torch.int64)
+    lens = crow[1:] - crow[:-1]
+    nseg = torch.clamp((lens + seg - 1) // seg, min=1)
+    rows = torch.repeat_interleave(torch.arange(lens.numel(), device=dev), nseg)
+    start = torch.cumsum(nseg, 0) - nseg                 # each row's first item, in row order
+    k = torch.arange(rows.numel(), device=dev) - start[rows]
+    off = k * seg
+    count = torch.clamp(torch.clamp(lens[rows] - off, max=seg), min=0)
+    extra = k > 0
+    slot = torch.where(extra, torch.cumsum(extra.to(torch.int64), 0) - 1, torch.full_like(k, -1))
+    order = torch.argsort(count, descending=True, stable=True)
+    items = torch.stack([rows, off, count, slot], 1)[order].to(torch.int32).contiguous()
+    split_rows = torch.nonzero(nseg > 1).squeeze(1)
+    splits = torch.stack([split_rows, slot[start[split_rows] + 1], nseg[split_rows] - 1,
+                          torch.zeros_like(split_rows)], 1).to(torch.int32).contiguous()
+    return items, splits, int(extra.sum())
+
+
 def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out: torch.Tensor | None = None):
     """A x (or A^T x) with A's values from w, gathered once per weight tensor into the structure's order.
     Every product of a training step over one structure shares the gathered copy, so each reads its values as
@@ -209,10 +235,14 @@ class _ConeRecurrence(torch.autograd.Function):
                 if batch % 4 == 0:          # one pass over A^T: the state gradient and dL/dw together
                     t_crow32, t_col32, t_ids32 = op._transposed()
                     vals_t = _gathered(op, w, True)
+                    items, splits, n_slots = op._backward_work()
+                    partials = torch.empty(n_slots, ld, dtype=torch.float32, device=dev) if n_slots else None
                     _hip.check(lib.fly_transposed_backward(
                         t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(), t_ids32.data_ptr(),
                         t_ids32.numel(), n_cols, n_rows, gy.data_ptr(), ld, h_prev.data_ptr(), ld, batch,
-                        gh_prev.data_ptr(), ld, 1, gw.data_ptr(), gw.numel(), st), "fly_transposed_backward")
+                        gh_prev.data_ptr(), ld, 1, gw.data_ptr(), gw.numel(), items.data_ptr(), items.shape[0],
+                        splits.data_ptr(), splits.shape[0], _hip.ptr(partials), n_slots, st),
+                        "fly_transposed_backward")
                 else:
                     _product(op, w, gy, transposed=True, out=gh_prev)
                     ids32, ids = op._edge_ids()
@@ -262,7 +292,7 @@ class _SubMatrix:
 
     def __init__(self, cone: "LightCone", t: int, n_rows: int, n_cols: int, nnz: int):
         self._cone, self._t, self._nnz = cone, t, nnz
-        self._tr = None
+        self._tr = self._tw = None
         self.shape = (n_rows, n_cols)
         self._data = None
 
@@ -297,6 +327,13 @@ class _SubMatrix:
             self._tr = (order, t_crow, t_col, t_crow.to(torch.int32), t_col.to(torch.int32),
                         self.edges[order].to(torch.int32))
         return self._tr[3], self._tr[4], self._tr[5]
+
+    def _backward_work(self):
+        """The transposed backward's work list (backward_work), built on first use."""
+        if getattr(self, "_tw", None) is None:
+            self._transposed()
+            self._tw = backward_work(self._tr[3])
+        return self._tw
 
     @property
     def t_order(self) -> torch.Tensor:

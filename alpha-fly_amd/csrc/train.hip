@@ -356,6 +356,9 @@ struct TransposedArgs {
   int32_t nrows, batch, accumulate;
   int32_t nnz;              // non-zeros of A^T: row pointers are clamped into [0, nnz]
   uint32_t n_w;             // entries of gw: ids at or past it are skipped
+  const int4 *items;        // null: one wave per row; else per wave {row, first non-zero, count, slot}
+  int32_t n_items, n_slots;
+  float *partials;          // (n_slots, ldgh): the state-gradient share of a row's later segments
 };
 
 // Sum over the 16 lanes of each DPP row (lanes 16 r .. 16 r + 15), in every lane of the row.
@@ -372,14 +375,32 @@ __device__ __forceinline__ float row16_sum(float v) {
 // gathered grad_y row serves both products: it accumulates w * grad_y into grad_h[j] (the groups meet
 // through the permlane sum) and its dot with h[j] accumulates into the non-zero's partial in a register, so
 // dL/dw needs no second gather.  After the last chunk each group sums its 16 lanes' partials per non-zero.
+//
+// With a work list, a wave takes one item: a segment {first non-zero, count} of row j of A^T, longest first.
+// A row's first segment (slot -1) writes grad_h[j] as above; its later segments write their share of it to
+// partials[slot], which k_add_partials adds in slot order, so long rows spread over several waves and the
+// sums stay deterministic.
 __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArgs a) {
   constexpr int R = 16;                    // rounds per block of 64 non-zeros
-  const uint32_t j = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint32_t j = wave;
+  int32_t first_nz = 0, count = INT32_MAX, slot = -1;
+  if (a.items != nullptr) {
+    if (wave >= (uint32_t)a.n_items) return;
+    const int4 it = a.items[wave];
+    j = (uint32_t)it.x;
+    first_nz = it.y;
+    count = it.z;
+    slot = it.w;
+    if (slot >= a.n_slots) return;
+  }
   if (j >= (uint32_t)a.nrows) return;
   const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
-  // a malformed row pointer gives wrong results, never an access outside the arrays
-  const int32_t beg = min(max(a.t_rowptr[j], 0), a.nnz);
-  const int32_t end = min(max(a.t_rowptr[j + 1], beg), a.nnz), n = end - beg;
+  // a malformed row pointer or work item gives wrong results, never an access outside the arrays
+  const int32_t row_beg = min(max(a.t_rowptr[j], 0), a.nnz);
+  const int32_t row_end = min(max(a.t_rowptr[j + 1], row_beg), a.nnz);
+  const int32_t beg = row_beg + min(max(first_nz, 0), row_end - row_beg);
+  const int32_t n = min(max(count, 0), row_end - beg);
   const int32_t chunks = (a.batch + 63) / 64;
   const __amdgpu_buffer_rsrc_t rc = buffer_of(a.t_col + beg, (uint32_t)n * 4u);
   const __amdgpu_buffer_rsrc_t rv = buffer_of(a.vals + beg, (uint32_t)n * 4u);
@@ -387,9 +408,10 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
   const __amdgpu_buffer_rsrc_t rgy = buffer_of(a.gy, a.gybytes);
   const uint32_t gy_row = (uint32_t)a.ldgy * 4u;
   const float *hj = a.h + (int64_t)j * a.ldh;
-  float *ghj = a.gh + (int64_t)j * a.ldgh;
+  float *ghj = slot < 0 ? a.gh + (int64_t)j * a.ldgh : a.partials + (int64_t)slot * a.ldgh;
+  const bool add = slot < 0 && a.accumulate;   // a later segment's share starts from zero
   bool first = true;
-  for (int32_t blk = 0; blk < n || (blk == 0 && !a.accumulate); blk += 64) {
+  for (int32_t blk = 0; blk < n || (blk == 0 && !add); blk += 64) {
     int32_t c[R];
     float w[R], dot[R];
 #pragma unroll
@@ -430,7 +452,7 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
       if (g == 0 && live) {
         float4 *dst = reinterpret_cast<float4 *>(ghj + col0);
         float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        if (a.accumulate || !first) {
+        if (add || !first) {
           const float4 o = *dst;
           v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
         }
@@ -447,6 +469,27 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
         if (id < a.n_w) a.gw[id] += d;
       }
     }
+  }
+}
+
+// grad_h[row] += partials[slot_beg .. slot_beg + count) in slot order, one wave per split row
+// ({row, slot_beg, count, unused} per entry); batch a multiple of 4, rows 16-byte aligned.
+__global__ __launch_bounds__(256) void k_add_partials(const int4 *__restrict__ splits, int32_t n_splits,
+                                                      const float *__restrict__ partials, int32_t n_slots,
+                                                      float *__restrict__ gh, int64_t ldgh, int32_t nrows,
+                                                      int32_t batch) {
+  const uint32_t w = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (w >= (uint32_t)n_splits) return;
+  const int4 sp = splits[w];
+  if ((uint32_t)sp.x >= (uint32_t)nrows || sp.y < 0 || sp.z < 0 || sp.y > n_slots - sp.z) return;
+  float *dst = gh + (int64_t)sp.x * ldgh;
+  for (int32_t c = (threadIdx.x & 63) * 4; c < batch; c += 256) {
+    float4 v = *reinterpret_cast<const float4 *>(dst + c);
+    for (int32_t k = 0; k < sp.z; ++k) {
+      const float4 p = *reinterpret_cast<const float4 *>(partials + (int64_t)(sp.y + k) * ldgh + c);
+      v = make_float4(v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w);
+    }
+    *reinterpret_cast<float4 *>(dst + c) = v;
   }
 }
 
@@ -582,7 +625,8 @@ extern "C" int fly_transposed_backward(const int32_t *t_rowptr, const int32_t *t
                                        const int32_t *ids, int64_t nnz, int64_t nrows, int64_t ncols,
                                        const float *gy, int64_t ldgy, const float *h, int64_t ldh, int64_t batch,
                                        float *gh, int64_t ldgh, int32_t accumulate, float *gw, int64_t n_w,
-                                       void *stream) {
+                                       const int32_t *items, int64_t n_items, const int32_t *splits,
+                                       int64_t n_splits, float *partials, int64_t n_slots, void *stream) {
   return guard([&] {
     FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0, "negative size");
     FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
@@ -594,10 +638,23 @@ extern "C" int fly_transposed_backward(const int32_t *t_rowptr, const int32_t *t
     FLY_REQUIRE(ncols == 0 || gy, "bad argument");
     FLY_REQUIRE(nnz >= 0 && nnz < (int64_t)1 << 30 && n_w >= 0 && n_w < (int64_t)1 << 32, "nnz or n_w out of range");
     LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    FLY_REQUIRE(!items || (n_items >= 0 && n_items < (int64_t)1 << 30 && n_slots >= 0 && n_slots < (int64_t)1 << 30 &&
+                           n_splits >= 0 && n_splits <= n_slots && aligned(items, 16)),
+                "bad work list");
+    FLY_REQUIRE(!items || n_slots == 0 || (partials && splits && vec4_ok(partials, ldgh) && aligned(splits, 16)),
+                "a work list with split rows needs partials and splits");
     TransposedArgs a{t_rowptr, t_col, vals, ids, gy, h, gh, gw, ldgy, ldh, ldgh,
                      ncols ? checked_bytes(ncols, ldgy) : 0u, (int32_t)nrows, (int32_t)batch, accumulate != 0,
-                     (int32_t)nnz, (uint32_t)n_w};
-    hipLaunchKernelGGL(k_transposed_backward, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), a);
+                     (int32_t)nnz, (uint32_t)n_w, reinterpret_cast<const int4 *>(items),
+                     items ? (int32_t)n_items : 0, items ? (int32_t)n_slots : 0, partials};
+    const int64_t waves = items ? n_items : nrows;
+    hipLaunchKernelGGL(k_transposed_backward, dim3(blocks_for(waves, 4)), dim3(256), 0, as_stream(stream), a);
     check_launch("transposed backward");
+    if (items && n_splits > 0) {
+      hipLaunchKernelGGL(k_add_partials, dim3(blocks_for(n_splits, 4)), dim3(256), 0, as_stream(stream),
+                         reinterpret_cast<const int4 *>(splits), (int32_t)n_splits, partials, (int32_t)n_slots, gh,
+                         ldgh, (int32_t)nrows, (int32_t)batch);
+      check_launch("partials");
+    }
   });
 }

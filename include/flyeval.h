@@ -203,11 +203,22 @@ int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, 
  * gy[row_e, b] h[col_e, b].  Every gathered row of gy serves both.  nrows = rows of A^T (= rows of h),
  * ncols = columns of A^T (= rows of gy); nnz = non-zeros of A^T; n_w = entries of gw.  The batch must be a
  * multiple of 4 and the rows 16-byte aligned; ids distinct.  Row pointers are clamped into [0, nnz] and ids at
- * or past n_w skipped, so a malformed structure gives wrong results, never an access outside the arrays. */
+ * or past n_w skipped, so a malformed structure gives wrong results, never an access outside the arrays.
+ *
+ * items (null: one wave per row of A^T) is a work list of n_items int32 quadruples {row, first non-zero
+ * within the row, count, slot}, 16-byte aligned, covering every non-zero once and every row's first non-zero
+ * with a slot -1 item.  A slot -1 item writes gh[row]; an item with slot s in [0, n_slots) writes its share of
+ * gh[row] to partials (n_slots, ldgh), and splits (n_splits quadruples {row, first slot, slot count, unused})
+ * then adds each split row's slots to gh[row] in slot order.  Long rows of A^T can so run on several waves at
+ * once with deterministic sums; the list's order is the waves' order (longest first keeps the tail short).
+ * Items and splits are clamped like the row pointers.  Replaces _SparseRecurrent.backward (brain.py:79-99),
+ * whose grad_h is a cuSPARSE SpMM over W^T and whose grad_w a column-blocked SDDMM. */
 int fly_transposed_backward(const int32_t *t_rowptr_dev, const int32_t *t_col_dev, const float *vals_dev,
                             const int32_t *ids_dev, int64_t nnz, int64_t nrows, int64_t ncols, const float *gy_dev,
                             int64_t ldgy, const float *h_dev, int64_t ldh, int64_t batch, float *gh_dev,
-                            int64_t ldgh, int32_t accumulate, float *gw_dev, int64_t n_w, void *stream);
+                            int64_t ldgh, int32_t accumulate, float *gw_dev, int64_t n_w, const int32_t *items_dev,
+                            int64_t n_items, const int32_t *splits_dev, int64_t n_splits, float *partials_dev,
+                            int64_t n_slots, void *stream);
 
 /* One recurrent step of training, the elementwise parts fused (brain.py:313-327 under autograd), float32,
  * one row of R_t per wave; rows are (rows, batch) with leading dimensions ld*:

@@ -106,14 +106,24 @@ def test_spmm_and_sddmm_match_float64(batch, ld_pad, heavy):
     _close(big, want, 1e-5, "sddmm scattered")
 
 
-@pytest.mark.parametrize("batch", [4, 64, 200, 256])
-def test_transposed_backward_matches_float64(batch):
+@pytest.mark.parametrize("batch,heavy,seg", [(4, False, None), (64, False, None), (200, False, None),
+                                             (256, False, None), (64, False, 64), (256, True, None), (256, True, 256),
+                                             (4, True, 64), (200, True, 128)])
+def test_transposed_backward_matches_float64(batch, heavy, seg):
     """fly_transposed_backward: grad_h (+)= A^T g and gw[ids[e]] += sum_b g[row_e, b] h[col_e, b] in one pass,
-    against float64, on a matrix with rows of A^T longer than one block of 64 non-zeros and empty ones."""
+    against float64, on a matrix with rows of A^T longer than one block of 64 non-zeros and empty ones; with a
+    work list (seg: segment length) long rows run as several segments whose shares meet in slot order."""
     from chessfly import _hip
+    from chessfly.brain import backward_work
     lib = _hip.load()
-    rows, cols, nnz = 400, 300, 30000                            # ~100 non-zeros per row of A^T
-    crow, r, c, val = _random_csr(rows, cols, nnz, batch + 7)
+    rows, cols = 400, 300
+    if heavy:                                                   # lognormal rows of A^T, up to 1500 non-zeros
+        t_crow_h, rt, ct, val = _heavy_csr(cols, rows, batch + 7)
+        r, c = ct, rt
+        nnz = len(r)
+    else:                                                       # ~100 non-zeros per row of A^T
+        nnz = 30000
+        crow, r, c, val = _random_csr(rows, cols, nnz, batch + 7)
     order = np.lexsort((r, c))                                  # A^T in CSR: by column, then row
     t_crow = np.zeros(cols + 1, np.int64)
     np.cumsum(np.bincount(c, minlength=cols), out=t_crow[1:])
@@ -130,9 +140,18 @@ def test_transposed_backward_matches_float64(batch):
         d(ids[order], torch.int32)
     g_d, h_d, gh, gw = d(g), d(h), d(gh0), d(gw0)
     st = _hip.stream(torch.device(DEV))
+    items = splits = partials = None
+    n_items = n_splits = n_slots = 0
+    if seg is not None:
+        items, splits, n_slots = backward_work(t_crow_d, seg)
+        n_items, n_splits = items.shape[0], splits.shape[0]
+        partials = torch.full((n_slots, batch), float("nan"), device=DEV)   # every slot is written before use
+        assert n_slots > 0 or not heavy
     _hip.check(lib.fly_transposed_backward(t_crow_d.data_ptr(), t_col_d.data_ptr(), t_val_d.data_ptr(),
                                            t_ids_d.data_ptr(), nnz, cols, rows, g_d.data_ptr(), batch, h_d.data_ptr(),
-                                           batch, batch, gh.data_ptr(), batch, 1, gw.data_ptr(), gw.numel(), st),
+                                           batch, batch, gh.data_ptr(), batch, 1, gw.data_ptr(), gw.numel(),
+                                           _hip.ptr(items), n_items, _hip.ptr(splits), n_splits, _hip.ptr(partials),
+                                           n_slots, st),
                "fly_transposed_backward")
     dense = np.zeros((rows, cols))
     np.add.at(dense, (r, c), val)
