@@ -18,8 +18,9 @@ attributes).  What runs underneath is libflyeval.so:
 Training (autograd enabled, brain.py:66-99, 225-229, 238-252, 289-329) runs the reference's float32
 recurrence under autograd with its sparse products on the device: `_SparseRecurrent` computes y = A h with
 fly_spmm, the state gradient A^T grad_y with fly_spmm over the transposed structure and the per-synapse
-gradient sum_b h[pre_e, b] grad_y[post_e, b] with fly_sddmm.  The tensors must live on a HIP device; nothing
-here falls back to the CPU.
+gradient sum_b h[pre_e, b] grad_y[post_e, b] with fly_sddmm; the light cone's steps (`_ConeRecurrence`) fuse
+those two backward products into one pass over A^T (fly_transposed_backward).  The tensors must live on a HIP
+device; nothing here falls back to the CPU.
 """
 
 from __future__ import annotations
@@ -155,10 +156,12 @@ class _ConeRecurrence(torch.autograd.Function):
     """Steps 1..T of the light cone under autograd, float32 (brain.py:313-327): per step the sub-matrix
     product on the device (its values read from the whole edge-weight vector w at the sub-matrix's edge ids),
     then one fused kernel for the constant drive, the input, the clamp and the lerp (fly_train_step_forward).
-    The backward runs per step one fused kernel for the gradients of those (fly_train_step_backward), the
-    state gradient A_t^T grad_y added to the carried rows' share (fly_spmm) and the per-synapse gradient
-    written straight into dL/dw at the edge ids (fly_sddmm).  Inputs after u_in and w, per step t: k_t, the
-    previous resting state c_{t-1}[R_t] and alpha[R_t] (each (|R_t|, 1)).  Returns h_T, (|R_T|, B)."""
+    The backward runs per step one fused kernel for the gradients of those (fly_train_step_backward), then
+    one pass over A_t^T (fly_transposed_backward, from the sub-matrix's longest-first work list) that adds the
+    state gradient A_t^T grad_y to the carried rows' share and writes the per-synapse gradient straight into
+    dL/dw at the edge ids; batches that are not a multiple of 4 take fly_spmm and fly_sddmm instead.  Inputs
+    after u_in and w, per step t: k_t, the previous resting state c_{t-1}[R_t] and alpha[R_t] (each
+    (|R_t|, 1)).  Returns h_T, (|R_T|, B)."""
 
     @staticmethod
     def forward(ctx, cone, h_max, u_in, w, *flat):
@@ -175,7 +178,6 @@ class _ConeRecurrence(torch.autograd.Function):
             rows, op = cone.row_counts[t], cone.ops[t]
             prev32, usrc32 = cone.step_tables32(t)
             if op is not None:
-                crow32, col32, n_rows, n_cols = op._structure()
                 y = _product(op, w, h)
             else:
                 y = torch.empty(rows, batch, dtype=torch.float32, device=dev)
@@ -265,7 +267,6 @@ class _SparseRecurrent(torch.autograd.Function):
         h = h.contiguous()
         ctx.save_for_backward(h, w)
         ctx.op = op
-        crow32, col32, n_rows, n_cols = op._structure()
         return _product(op, w, h)
 
     @staticmethod
