@@ -404,6 +404,39 @@ def test_full_scale_model_matches_oracle(full_net):
     net.infer_dtype = torch.float16
 
 
+def test_full_scale_outputs_do_not_depend_on_the_batch(full_net):
+    """A board's logits do not depend on the batch around it: the first boards of batches of 1, 65, 2100 and 4096
+    (the last two sweep 256-column chunks, the others 64) match the 24-board forward, float32 within float32
+    round-off of the summation order and float16 deviation within its tolerance; at every size the float16
+    deviation path agrees with float32 within 1e-3 and on >= 99.9% of the argmaxes."""
+    from chessfly.synthetic import synthetic_boards
+    net, _ = full_net
+    x = torch.as_tensor(synthetic_boards(4096, seed=21)).to(DEV)
+    ref = {}
+    for dtype in (torch.float32, torch.float16):
+        net.infer_dtype = dtype
+        with torch.no_grad():
+            ref[dtype] = net(x[:24])
+    try:
+        for batch in (1, 65, 2100, 4096):
+            out = {}
+            for dtype in (torch.float32, torch.float16):
+                net.infer_dtype = dtype
+                with torch.no_grad():
+                    out[dtype] = net(x[:batch])
+                k = min(batch, 24)
+                tol = 5e-5 if dtype == torch.float32 else 1e-3
+                dl = float((out[dtype][0][:k] - ref[dtype][0][:k]).abs().max())
+                dw = float((out[dtype][1][:k] - ref[dtype][1][:k]).abs().max())
+                print(f"B={batch} {dtype}: first {k} boards vs B=24: {dl:.2e} / {dw:.2e}", flush=True)
+                assert dl < tol and dw < tol, (batch, dtype, dl, dw)
+            (l32, w32), (l16, w16) = out[torch.float32], out[torch.float16]
+            assert float((l16 - l32).abs().max()) < 1e-3 and float((w16 - w32).abs().max()) < 1e-3
+            assert float((l16.argmax(1) == l32.argmax(1)).float().mean()) >= 0.999
+    finally:
+        net.infer_dtype = torch.float16
+
+
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
     """The bench configuration: B = 1120 boards, float16 deviation vs float32 on the device."""
     from chessfly.synthetic import synthetic_boards
