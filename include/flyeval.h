@@ -25,6 +25,7 @@
  *   fly_evaluator_outputs chessfly/model.py:120-128 and :107-110 (Evaluator.submit's half cast or legal gather,
  *                         expected_value)
  *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
+ *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass)
  *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
  *                         gradients)
  */
@@ -227,7 +228,8 @@ int fly_transposed_backward(const int32_t *t_rowptr_dev, const int32_t *t_col_de
  *             h = torch.lerp(p, x, alpha[r]).
  *   backward: from g = dL/dh:  gy = g alpha [0 <= y <= h_max];  gk[r] = sum_b gy;  ga[r] = sum_b g (x - p);
  *             gpdef[r] = sum_b g (1 - alpha) on rows not carried, else 0;  carried rows store g (1 - alpha)
- *             into ghprev[prev[r]] (the caller zeroes ghprev, then adds A_t^T gy with fly_spmm accumulate);
+ *             into ghprev[prev[r]] (the caller zeroes ghprev, then adds A_t^T gy with fly_spmm accumulate or
+ *             fly_transposed_backward);
  *             input rows add gy to gu[usrc[r]] (distinct rows per step).
  * prev / usrc may be NULL (no carried rows / no input rows). */
 int fly_train_step_forward(int64_t rows, int64_t batch, float *s_y_dev, int64_t lds, int32_t has_s,
@@ -253,7 +255,7 @@ enum fly_kernel_class {
     FLY_K_STATE_STEP = 0,   /* the fused SpMM + update step */
     FLY_K_ENCODER = 1,      /* encoder GEMM */
     FLY_K_HEAD = 2,         /* head GEMMs and logit assembly */
-    FLY_K_OTHER = 3,        /* output gather, bias add, zero fill */
+    FLY_K_OTHER = 3,        /* output gather, bias add, zero fill, the training products */
     FLY_K_CLASSES = 4
 };
 /* While enabled, every launch of the forward entry points is bracketed by HIP events on its stream (no
@@ -268,7 +270,10 @@ int fly_profile_read(double *ms, int64_t *launches);
  * row-major (0 = automatic, 1 = all column chunks of a row back to back); "unroll": non-zeros each wave
  * gathers per iteration (8, 16 or 32; 0 = automatic); "nt_store": 1 writes the new state with non-temporal
  * stores; "groups": lane groups per wave that gather different non-zeros (1, 2, 4, 8; 0 = automatic);
- * "rows_mode": 1 gives each lane group its own row, -1 never, 0 for steps with short rows. */
+ * "rows_mode": 1 gives each lane group its own row, -1 never, 0 for steps with short rows; "spmm_groups":
+ * lane groups of fly_spmm on 16-byte lanes (2, 4, 8; 0 = automatic); "gemm_tile": workgroup tile of the dense
+ * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128; 0 = automatic).  Every selectable shape computes the same
+ * function. */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus
