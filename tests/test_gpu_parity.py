@@ -548,3 +548,35 @@ def test_evaluator_protocol(full_net):
     assert legal0.shape == (0,) and np.array_equal(values0, values)
     with pytest.raises(IndexError):
         ev(x, np.array([9]), np.array([0]))
+
+
+def test_empty_batches_give_empty_outputs():
+    """Zero boards through every public entry (as the reference's torch ops allow): empty outputs of the right
+    shapes and dtypes, no launch errors, and the next non-empty call still correct."""
+    from chessfly.encoding import N_FEATURES, N_MOVES
+    from chessfly.model import Evaluator, FlyChessNet, ModelConfig
+    from chessfly.synthetic import GraphSpec, synthetic_boards, synthetic_connectome
+    conn = synthetic_connectome(GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=100, seed=4))
+    torch.manual_seed(0)
+    net = FlyChessNet(conn, ModelConfig(steps=4)).to(DEV).eval()
+    rnn, n_in, n_out = net.brain, len(net.in_idx), len(net.out_idx)
+    with torch.no_grad():
+        for dtype in (torch.float32, torch.float16):
+            out = rnn.forward_io(torch.zeros(n_in, 0, device=DEV, dtype=dtype), net.in_idx, net.out_idx, 4)
+            assert out.shape == (n_out, 0) and out.dtype == torch.float32
+            net.infer_dtype = dtype
+            logits, wdl = net(torch.zeros(0, N_FEATURES, device=DEV))
+            assert logits.shape == (0, N_MOVES) and wdl.shape == (0, 3)
+        h = rnn(torch.zeros(conn.n_neurons, 0, device=DEV), 3)
+        assert h.shape == (conn.n_neurons, 0)
+        net.infer_dtype = torch.float16
+        ev = Evaluator(net, torch.device(DEV))
+        lazy, values = ev(np.zeros((0, N_FEATURES), np.float16), None, None)
+        assert lazy.shape == (0, N_MOVES) and lazy.dtype == np.float16 and values.shape == (0,)
+        legal, values = ev(np.zeros((0, N_FEATURES), np.float16), np.zeros(0, np.int64), np.zeros(0, np.int64))
+        assert legal.shape == (0,) and values.shape == (0,)
+        x = torch.as_tensor(synthetic_boards(5, seed=1), device=DEV)
+        l5, _ = net(x)
+        l1, _ = net(x[:1])
+        torch.testing.assert_close(l5[:1], l1, rtol=0, atol=0)
+    torch.cuda.synchronize()
