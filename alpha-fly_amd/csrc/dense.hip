@@ -25,7 +25,7 @@
 
 namespace fly {
 
-int64_t state_ld(int64_t batch);
+int64_t state_ld(int64_t batch, size_t elem);
 size_t io_workspace(const fly_plan &plan, int64_t batch);
 template <typename S, typename U>
 const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st);
@@ -524,7 +524,8 @@ extern "C" int fly_head(const fly_dense *d, const float *r, int64_t ldr, int64_t
 
 extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_dense *d, int64_t batch) {
   if (!plan || !d) return 0;
-  return align256((size_t)plan->n_in * state_ld(batch) * sizeof(float)) + align256(io_workspace(*plan, batch)) +
+  return align256((size_t)plan->n_in * state_ld(batch, sizeof(float)) * sizeof(float)) +
+         align256(io_workspace(*plan, batch)) +
          std::max(encoder_ws(*d, batch), head_ws(*d, batch));
 }
 
@@ -542,14 +543,14 @@ extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const
     FLY_REQUIRE(ws && ws_bytes >= fly_model_workspace(plan, d, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     hipStream_t st = as_stream(stream);
-    const int64_t ldu = state_ld(batch);
+    const int64_t ldu = state_ld(batch, sizeof(float));
     char *base = static_cast<char *>(ws);
     float *u = reinterpret_cast<float *>(base);
     base += align256((size_t)plan->n_in * ldu * sizeof(float));
     void *states = base;
     base += align256(io_workspace(*plan, batch));
     void *scratch = base;  // the encoder's operand split, then the head's
-    const int64_t lds = state_ld(batch);
+    const int64_t lds = state_ld(batch, plan->mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float));
     // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
     run_encoder(*d, x, x_f16 != 0, ldx, batch, input_gain, u, nullptr, ldu, scratch, st);
     if (plan->mode == FLY_MODE_DEVIATION_F16) {
