@@ -26,6 +26,7 @@
 namespace fly {
 
 int64_t state_ld(int64_t batch, size_t elem);
+int64_t io_block(const fly_plan &plan, int64_t batch);
 size_t io_workspace(const fly_plan &plan, int64_t batch);
 template <typename S, typename U>
 const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st);
@@ -524,9 +525,9 @@ extern "C" int fly_head(const fly_dense *d, const float *r, int64_t ldr, int64_t
 
 extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_dense *d, int64_t batch) {
   if (!plan || !d) return 0;
-  return align256((size_t)plan->n_in * state_ld(batch, sizeof(float)) * sizeof(float)) +
-         align256(io_workspace(*plan, batch)) +
-         std::max(encoder_ws(*d, batch), head_ws(*d, batch));
+  const int64_t blk = io_block(*plan, batch);   // boards per block (the whole batch below 2 GiB of state)
+  return align256((size_t)plan->n_in * state_ld(blk, sizeof(float)) * sizeof(float)) +
+         align256(io_workspace(*plan, blk)) + std::max(encoder_ws(*d, blk), head_ws(*d, blk));
 }
 
 extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const void *x, int32_t x_f16, int64_t ldx,
@@ -543,22 +544,30 @@ extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const
     FLY_REQUIRE(ws && ws_bytes >= fly_model_workspace(plan, d, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     hipStream_t st = as_stream(stream);
-    const int64_t ldu = state_ld(batch, sizeof(float));
+    // Boards run in blocks whose state stays below 2 GiB (one block below about 6,400 boards in float16).
+    const int64_t blk = io_block(*plan, batch);
     char *base = static_cast<char *>(ws);
     float *u = reinterpret_cast<float *>(base);
-    base += align256((size_t)plan->n_in * ldu * sizeof(float));
+    base += align256((size_t)plan->n_in * state_ld(blk, sizeof(float)) * sizeof(float));
     void *states = base;
-    base += align256(io_workspace(*plan, batch));
+    base += align256(io_workspace(*plan, blk));
     void *scratch = base;  // the encoder's operand split, then the head's
-    const int64_t lds = state_ld(batch, plan->mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float));
-    // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
-    run_encoder(*d, x, x_f16 != 0, ldx, batch, input_gain, u, nullptr, ldu, scratch, st);
-    if (plan->mode == FLY_MODE_DEVIATION_F16) {
-      const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, batch, states, st);
-      run_head<_Float16>(*d, fin, lds, plan->out_src.p, plan->cbase.p, batch, logits, wdl, scratch, st);
-    } else {
-      const float *fin = run_cone_steps<float, float>(*plan, u, ldu, batch, states, st);
-      run_head<float>(*d, fin, lds, plan->out_src.p, plan->cbase.p, batch, logits, wdl, scratch, st);
+    const size_t xelem = x_f16 ? sizeof(_Float16) : sizeof(float);
+    for (int64_t c0 = 0; c0 < batch; c0 += blk) {
+      const int64_t nb = std::min(blk, batch - c0);
+      const void *xb = static_cast<const char *>(x) + (size_t)c0 * ldx * xelem;
+      float *lb = logits + c0 * d->n_moves, *wb = wdl + c0 * 3;
+      const int64_t ldu = state_ld(nb, sizeof(float));
+      const int64_t lds = state_ld(nb, plan->mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float));
+      // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
+      run_encoder(*d, xb, x_f16 != 0, ldx, nb, input_gain, u, nullptr, ldu, scratch, st);
+      if (plan->mode == FLY_MODE_DEVIATION_F16) {
+        const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, nb, states, st);
+        run_head<_Float16>(*d, fin, lds, plan->out_src.p, plan->cbase.p, nb, lb, wb, scratch, st);
+      } else {
+        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, states, st);
+        run_head<float>(*d, fin, lds, plan->out_src.p, plan->cbase.p, nb, lb, wb, scratch, st);
+      }
     }
   });
 }

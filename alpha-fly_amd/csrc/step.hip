@@ -559,9 +559,24 @@ uint32_t buffer_bytes(int64_t rows, int64_t ld, size_t elem) {
   return bytes > 0 && bytes <= (int64_t)INT32_MAX ? (uint32_t)bytes : 0u;
 }
 
+// Boards per block of a forward: the whole batch while a state buffer of `rows` rows stays below 2 GiB, so the
+// gathers keep 32-bit buffer offsets; a larger batch runs as equal blocks of whole 64-column chunks that do
+// (the boards are independent).
+int64_t block_cols(int64_t rows, size_t elem, int64_t batch) {
+  auto fits = [&](int64_t b) { return rows == 0 || buffer_bytes(rows, state_ld(b, elem), elem) != 0; };
+  for (int64_t n = 1;; ++n) {
+    const int64_t b = n == 1 ? batch : round_up((batch + n - 1) / n, 64);
+    if (fits(b) || b <= 64) return b;
+  }
+}
+
+size_t state_bytes(const fly_plan &plan) { return plan.mode == FLY_MODE_DEVIATION_F16 ? 2 : 4; }
+
+int64_t io_block(const fly_plan &plan, int64_t batch) { return block_cols(plan.max_rows, state_bytes(plan), batch); }
+
 size_t io_workspace(const fly_plan &plan, int64_t batch) {
-  const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? 2 : 4;
-  return 2 * (size_t)plan.max_rows * (size_t)state_ld(batch, es) * es + 256;
+  const size_t es = state_bytes(plan);
+  return 2 * (size_t)plan.max_rows * (size_t)state_ld(io_block(plan, batch), es) * es + 256;
 }
 
 // Runs steps 1..T of a light-cone plan.  Returns the final state (null if R_T is empty) in one of the two
@@ -639,19 +654,26 @@ extern "C" int fly_forward_io(const fly_plan *plan, const void *u_in, int64_t ld
     FLY_REQUIRE(ws && ws_bytes >= io_workspace(*plan, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     hipStream_t st = as_stream(stream);
-    if (plan->mode == FLY_MODE_DEVIATION_F16) {
-      const _Float16 *fin =
-          run_cone_steps<_Float16, _Float16>(*plan, static_cast<const _Float16 *>(u_in), ldu, batch, ws, st);
-      write_outputs<_Float16>(*plan, fin, batch, out, ldo, st);
-    } else {
-      const float *fin = run_cone_steps<float, float>(*plan, static_cast<const float *>(u_in), ldu, batch, ws, st);
-      write_outputs<float>(*plan, fin, batch, out, ldo, st);
+    const int64_t blk = io_block(*plan, batch);
+    for (int64_t c0 = 0; c0 < batch; c0 += blk) {
+      const int64_t nb = std::min(blk, batch - c0);
+      if (plan->mode == FLY_MODE_DEVIATION_F16) {
+        const _Float16 *u = plan->n_in ? static_cast<const _Float16 *>(u_in) + c0 : nullptr;
+        const _Float16 *fin = run_cone_steps<_Float16, _Float16>(*plan, u, ldu, nb, ws, st);
+        write_outputs<_Float16>(*plan, fin, nb, out + c0, ldo, st);
+      } else {
+        const float *u = plan->n_in ? static_cast<const float *>(u_in) + c0 : nullptr;
+        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, ws, st);
+        write_outputs<float>(*plan, fin, nb, out + c0, ldo, st);
+      }
     }
   });
 }
 
 extern "C" size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch) {
-  return plan ? 2 * (size_t)plan->n * (size_t)state_ld(batch, sizeof(float)) * sizeof(float) + 256 : 0;
+  if (!plan) return 0;
+  const int64_t blk = block_cols(plan->n, sizeof(float), batch);
+  return 2 * (size_t)plan->n * (size_t)state_ld(blk, sizeof(float)) * sizeof(float) + 256;
 }
 
 extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, const float *bias, int64_t batch,
@@ -678,28 +700,32 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
     }
     FLY_REQUIRE(ws && ws_bytes >= fly_forward_literal_workspace(plan, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
-    const int64_t lds = state_ld(batch, sizeof(float));
-    float *buf[2] = {static_cast<float *>(ws), static_cast<float *>(ws) + (size_t)n * lds};
-    const float *prev = nullptr;
-    int cur = 0;
-    for (int t = 1; t <= steps; ++t) {
-      const bool last = t == steps;
-      StepArgs<float, float> a{};
-      a.rowptr = plan->rowptr[0].p;
-      a.colval = plan->colval[0].p;
-      a.params = plan->params[0].p;
-      a.xprev = prev;
-      a.ldx = lds;
-      a.u = u;
-      a.ldu = ldu;
-      a.xout = last ? h : buf[cur];
-      a.ldo = last ? ldh : lds;
-      a.nrows = (int32_t)n;
-      a.batch = (int32_t)batch;
-      a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
-      state_step(a, (double)plan->nnz[0] / (double)n, st);
-      prev = buf[cur];
-      cur ^= 1;
+    const int64_t blk = block_cols(n, sizeof(float), batch);
+    for (int64_t c0 = 0; c0 < batch; c0 += blk) {
+      const int64_t nb = std::min(blk, batch - c0);
+      const int64_t lds = state_ld(nb, sizeof(float));
+      float *buf[2] = {static_cast<float *>(ws), static_cast<float *>(ws) + (size_t)n * lds};
+      const float *prev = nullptr;
+      int cur = 0;
+      for (int t = 1; t <= steps; ++t) {
+        const bool last = t == steps;
+        StepArgs<float, float> a{};
+        a.rowptr = plan->rowptr[0].p;
+        a.colval = plan->colval[0].p;
+        a.params = plan->params[0].p;
+        a.xprev = prev;
+        a.ldx = lds;
+        a.u = u + c0;
+        a.ldu = ldu;
+        a.xout = last ? h + c0 : buf[cur];
+        a.ldo = last ? ldh : lds;
+        a.nrows = (int32_t)n;
+        a.batch = (int32_t)nb;
+        a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
+        state_step(a, (double)plan->nnz[0] / (double)n, st);
+        prev = buf[cur];
+        cur ^= 1;
+      }
     }
   });
 }

@@ -103,7 +103,8 @@ int fly_plan_destroy(fly_plan *plan);
 int fly_plan_resting(const fly_plan *plan, float *c_out_dev, void *stream);
 
 /* ---- forward ----------------------------------------------------------------------------------- */
-/* Bytes of scratch the forward entry points need for `batch` columns (pass at least this many). */
+/* Bytes of scratch the forward entry points need for `batch` columns (pass at least this many).  A batch whose
+ * state would pass 2 GiB runs internally as column blocks below it, and the workspace is sized for one block. */
 size_t fly_forward_io_workspace(const fly_plan *plan, int64_t batch);
 /* u_in (n_in, ldu): __half for FLY_MODE_DEVIATION_F16, float for FLY_MODE_F32.
  * out (n_out, ldo) float32 = forward_io(u_in)[out rows]. */

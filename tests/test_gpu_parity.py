@@ -405,20 +405,21 @@ def test_full_scale_model_matches_oracle(full_net):
 
 
 def test_full_scale_outputs_do_not_depend_on_the_batch(full_net):
-    """A board's logits do not depend on the batch around it: the first boards of batches of 1, 65, 2100 and 4096
-    (the last two sweep 256-column chunks, the others 64) match the 24-board forward, float32 within float32
-    round-off of the summation order and float16 deviation within its tolerance; at every size the float16
-    deviation path agrees with float32 within 1e-3 and on >= 99.9% of the argmaxes."""
+    """A board's logits do not depend on the batch around it: the first boards of batches of 1, 65, 2100, 4096 and
+    8192 match the 24-board forward, float32 within float32 round-off of the summation order and float16
+    deviation within its tolerance; at every size the float16 deviation path agrees with float32 within 1e-3 and
+    on >= 99.9% of the argmaxes.  Batches whose state would pass 2 GiB (float32 from about 3,200 boards, float16
+    from about 6,400) run as column blocks."""
     from chessfly.synthetic import synthetic_boards
     net, _ = full_net
-    x = torch.as_tensor(synthetic_boards(4096, seed=21)).to(DEV)
+    x = torch.as_tensor(synthetic_boards(8192, seed=21)).to(DEV)
     ref = {}
     for dtype in (torch.float32, torch.float16):
         net.infer_dtype = dtype
         with torch.no_grad():
             ref[dtype] = net(x[:24])
     try:
-        for batch in (1, 65, 2100, 4096):
+        for batch in (1, 65, 2100, 4096, 8192):
             out = {}
             for dtype in (torch.float32, torch.float16):
                 net.infer_dtype = dtype
@@ -435,6 +436,25 @@ def test_full_scale_outputs_do_not_depend_on_the_batch(full_net):
             assert float((l16.argmax(1) == l32.argmax(1)).float().mean()) >= 0.999
     finally:
         net.infer_dtype = torch.float16
+
+
+def test_full_scale_blocked_columns_match_unblocked(full_net):
+    """forward_io and the literal recurrence over more columns than fit one 2 GiB float32 state (run as column
+    blocks) give the same columns as a call on those columns alone."""
+    net, _ = full_net
+    rnn = net.brain
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        u_in = (torch.randn(len(net.in_idx), 4100, generator=g) * 0.5).to(DEV)
+        big = rnn.forward_io(u_in, net.in_idx, net.out_idx, 6)
+        for cols in (slice(0, 24), slice(4076, 4100)):
+            small = rnn.forward_io(u_in[:, cols].contiguous(), net.in_idx, net.out_idx, 6)
+            torch.testing.assert_close(big[:, cols], small, rtol=0, atol=2e-5)
+        u = (torch.randn(rnn.n, 3300, generator=g) * 0.5).to(DEV)
+        head, tail = u[:, :24].clone(), u[:, -24:].clone()
+        h = rnn(u, 4)
+        torch.testing.assert_close(h[:, :24], rnn(head, 4), rtol=0, atol=2e-5)
+        torch.testing.assert_close(h[:, -24:], rnn(tail, 4), rtol=0, atol=2e-5)
 
 
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
