@@ -87,27 +87,79 @@ __device__ int32_t block_inclusive_scan(int32_t v, int32_t *part) {
   return part[tid];
 }
 
-// One workgroup: rows = sorted {i : a[i] && b[i]}, where[i] = position in rows or -1, count[0] = |rows|.
-// Thread j owns the contiguous segment [j*seg, (j+1)*seg), so positions follow index order.
-__global__ __launch_bounds__(kScanThreads) void k_compact(const uint8_t *__restrict__ a, const uint8_t *__restrict__ b,
-                                                          int64_t n, int32_t *__restrict__ rows,
-                                                          int32_t *__restrict__ where, int32_t *__restrict__ count) {
+// Multi-workgroup order-preserving compaction and scan: a workgroup owns a tile of kTile indices, thread j the
+// 8 consecutive indices [8j, 8j + 8) of it, so positions follow index order.  Three passes: per-tile totals,
+// one single-workgroup scan of those (k_scan), then per-tile positions from the tile's offset.
+constexpr int kPer = 8, kTile = kScanThreads * kPer;
+
+__device__ __forceinline__ int64_t tile_base() { return (int64_t)blockIdx.x * kTile + (int64_t)threadIdx.x * kPer; }
+
+__global__ __launch_bounds__(kScanThreads) void k_tile_flags(const uint8_t *__restrict__ a, const uint8_t *__restrict__ b,
+                                                             int64_t n, int32_t *__restrict__ tile_sum) {
   __shared__ int32_t part[kScanThreads];
-  const int64_t seg = (n + kScanThreads - 1) / kScanThreads;
-  const int64_t beg = min(n, (int64_t)threadIdx.x * seg), end = min(n, beg + seg);
+  const int64_t base = tile_base();
   int32_t c = 0;
-  for (int64_t i = beg; i < end; ++i) c += (a[i] & b[i]) ? 1 : 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) c += (base + k < n && (a[base + k] & b[base + k])) ? 1 : 0;
   const int32_t incl = block_inclusive_scan(c, part);
-  int32_t run = incl - c;
-  for (int64_t i = beg; i < end; ++i) {
-    if (a[i] & b[i]) {
+  if (threadIdx.x == kScanThreads - 1) tile_sum[blockIdx.x] = incl;
+}
+
+// rows = sorted {i : a[i] && b[i]}, where[i] = position in rows or -1
+__global__ __launch_bounds__(kScanThreads) void k_tile_compact(const uint8_t *__restrict__ a,
+                                                               const uint8_t *__restrict__ b, int64_t n,
+                                                               const int32_t *__restrict__ tile_off,
+                                                               int32_t *__restrict__ rows, int32_t *__restrict__ where) {
+  __shared__ int32_t part[kScanThreads];
+  const int64_t base = tile_base();
+  int32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) c += (base + k < n && (a[base + k] & b[base + k])) ? 1 : 0;
+  const int32_t incl = block_inclusive_scan(c, part);
+  int32_t run = tile_off[blockIdx.x] + incl - c;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int64_t i = base + k;
+    if (i >= n) break;
+    if (a[i] && b[i]) {
       rows[run] = (int32_t)i;
       where[i] = run++;
     } else {
       where[i] = -1;
     }
   }
-  if (threadIdx.x == kScanThreads - 1) count[0] = incl;
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_tile_sums(const int32_t *__restrict__ in, int64_t n,
+                                                            int32_t *__restrict__ tile_sum) {
+  __shared__ int32_t part[kScanThreads];
+  const int64_t base = tile_base();
+  int32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) c += base + k < n ? in[base + k] : 0;
+  const int32_t incl = block_inclusive_scan(c, part);
+  if (threadIdx.x == kScanThreads - 1) tile_sum[blockIdx.x] = incl;
+}
+
+// out[i] = sum of in[0..i) from the tile offsets; the last tile also writes out[n] = total
+__global__ __launch_bounds__(kScanThreads) void k_tile_scan(const int32_t *__restrict__ in, int64_t n,
+                                                            const int32_t *__restrict__ tile_off, int64_t ntiles,
+                                                            int32_t *__restrict__ out) {
+  __shared__ int32_t part[kScanThreads];
+  const int64_t base = tile_base();
+  int32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) c += base + k < n ? in[base + k] : 0;
+  const int32_t incl = block_inclusive_scan(c, part);
+  int32_t run = tile_off[blockIdx.x] + incl - c;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int64_t i = base + k;
+    if (i >= n) break;
+    out[i] = run;
+    run += in[i];
+  }
+  if (blockIdx.x == ntiles - 1 && threadIdx.x == 0) out[n] = tile_off[ntiles];
 }
 
 // One workgroup: out[i] = sum of in[0..i), out[n] = total.
@@ -136,35 +188,44 @@ __global__ void k_step_index(const int32_t *__restrict__ rows, int64_t nr, const
   usrc[i] = in_pos[r];
 }
 
-// cnt[i] = edges of row R_t[i] whose presynaptic neuron is in R_{t-1}
-__global__ void k_row_count(const int32_t *__restrict__ rows, int64_t nr, const int32_t *__restrict__ crow,
-                            const int32_t *__restrict__ pre, const int32_t *__restrict__ where_prev,
-                            int32_t *__restrict__ cnt) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+// Per row of R_t (one wave each, lanes across the row's edges in W's order): how many of its presynaptic partners
+// lie in R_{t-1}, and their local columns and edge ids, written in edge order from the lanes' ballot.
+__global__ __launch_bounds__(256) void k_row_count(const int32_t *__restrict__ rows, int64_t nr,
+                                                   const int32_t *__restrict__ crow, const int32_t *__restrict__ pre,
+                                                   const int32_t *__restrict__ where_prev, int32_t *__restrict__ cnt) {
+  const int64_t i = blockIdx.x * 4 + (int64_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (i >= nr) return;
-  const int32_t r = rows[i];
+  const int lane = threadIdx.x & 63;
+  const int32_t r = rows[i], beg = crow[r], end = crow[r + 1];
   int32_t c = 0;
-  const int32_t end = crow[r + 1];
-  for (int32_t e = crow[r]; e < end; ++e) c += where_prev[pre[e]] >= 0 ? 1 : 0;
-  cnt[i] = c;
+  for (int32_t e0 = beg; e0 < end; e0 += 64) {
+    const int32_t e = e0 + lane;
+    c += __popcll(__ballot(e < end && where_prev[pre[e]] >= 0));
+  }
+  if (lane == 0) cnt[i] = c;
 }
 
-// Write the kept edges of row R_t[i] in edge order: local column and global edge id.
-__global__ void k_row_fill(const int32_t *__restrict__ rows, int64_t nr, const int32_t *__restrict__ crow,
-                           const int32_t *__restrict__ pre, const int32_t *__restrict__ where_prev,
-                           const int32_t *__restrict__ rowptr, int32_t *__restrict__ col, int32_t *__restrict__ edge) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void k_row_fill(const int32_t *__restrict__ rows, int64_t nr,
+                                                  const int32_t *__restrict__ crow, const int32_t *__restrict__ pre,
+                                                  const int32_t *__restrict__ where_prev,
+                                                  const int32_t *__restrict__ rowptr, int32_t *__restrict__ col,
+                                                  int32_t *__restrict__ edge) {
+  const int64_t i = blockIdx.x * 4 + (int64_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (i >= nr) return;
-  const int32_t r = rows[i];
+  const int lane = threadIdx.x & 63;
+  const int32_t r = rows[i], beg = crow[r], end = crow[r + 1];
+  const uint64_t below = (1ull << lane) - 1ull;
   int32_t p = rowptr[i];
-  const int32_t end = crow[r + 1];
-  for (int32_t e = crow[r]; e < end; ++e) {
-    const int32_t w = where_prev[pre[e]];
+  for (int32_t e0 = beg; e0 < end; e0 += 64) {
+    const int32_t e = e0 + lane;
+    const int32_t w = e < end ? where_prev[pre[e]] : -1;
+    const uint64_t m = __ballot(w >= 0);
     if (w >= 0) {
-      col[p] = w;
-      edge[p] = e;
-      ++p;
+      const int32_t pos = p + __popcll(m & below);
+      col[pos] = w;
+      edge[pos] = e;
     }
+    p += __popcll(m);
   }
 }
 
@@ -178,6 +239,19 @@ constexpr int kThreads = 256;
 
 void copy_d2d(void *dst, const void *src, size_t bytes, hipStream_t st) {
   if (bytes) FLY_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st));
+}
+
+// out[i] = sum of in[0..i), out[n] = total: one workgroup up to one tile, else the tile totals, their scan and
+// the per-tile passes.  tile_sum and tile_off hold ceil(n / kTile) and one more entries.
+void exclusive_scan(const int32_t *in, int64_t n, int32_t *out, int32_t *tile_sum, int32_t *tile_off, hipStream_t st) {
+  if (n <= kTile) {
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, st, in, n, out);
+    return;
+  }
+  const int64_t ntiles = (n + kTile - 1) / kTile;
+  hipLaunchKernelGGL(k_tile_sums, dim3((unsigned)ntiles), dim3(kScanThreads), 0, st, in, n, tile_sum);
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, st, tile_sum, ntiles, tile_off);
+  hipLaunchKernelGGL(k_tile_scan, dim3((unsigned)ntiles), dim3(kScanThreads), 0, st, in, n, tile_off, ntiles, out);
 }
 
 }  // namespace
@@ -263,11 +337,16 @@ extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, 
     std::vector<DevArray<int32_t>> where(T + 1);
     cone->rows.resize(T + 1);
     DevArray<int32_t> counts(T + 1);
+    const int64_t ntiles = (n + kTile - 1) / kTile;
+    DevArray<int32_t> tile_sum(ntiles), tile_off(ntiles + 1);
     for (int t = 0; t <= T; ++t) {
       where[t].alloc(n);
       cone->rows[t].alloc(n);
-      hipLaunchKernelGGL(k_compact, dim3(1), dim3(kScanThreads), 0, st, V(t), D(t), n, cone->rows[t].p, where[t].p,
-                         counts.p + t);
+      hipLaunchKernelGGL(k_tile_flags, dim3((unsigned)ntiles), dim3(kScanThreads), 0, st, V(t), D(t), n, tile_sum.p);
+      hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, st, tile_sum.p, ntiles, tile_off.p);
+      hipLaunchKernelGGL(k_tile_compact, dim3((unsigned)ntiles), dim3(kScanThreads), 0, st, V(t), D(t), n, tile_off.p,
+                         cone->rows[t].p, where[t].p);
+      copy_d2d(counts.p + t, tile_off.p + ntiles, sizeof(int32_t), st);
     }
     check_launch("row compaction");
     std::vector<int32_t> hcount(T + 1);
@@ -300,9 +379,9 @@ extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, 
       if (op) {
         cone->rowptr[t].alloc(nr + 1);
         if (nr)
-          hipLaunchKernelGGL(k_row_count, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, cone->rows[t].p, nr,
-                             crow, pre, where[t - 1].p, cnt.p);
-        hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, st, cnt.p, nr, cone->rowptr[t].p);
+          hipLaunchKernelGGL(k_row_count, dim3(blocks_for(nr, 4)), dim3(256), 0, st, cone->rows[t].p, nr, crow, pre,
+                             where[t - 1].p, cnt.p);
+        exclusive_scan(cnt.p, nr, cone->rowptr[t].p, tile_sum.p, tile_off.p, st);
         // read back nnz_t before the count buffer is reused by the next step
         int32_t h = 0;
         FLY_HIP(hipMemcpyAsync(&h, cone->rowptr[t].p + nr, sizeof(h), hipMemcpyDeviceToHost, st));
@@ -311,8 +390,8 @@ extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, 
         cone->col[t].alloc(h);
         cone->edge[t].alloc(h);
         if (nr && h)
-          hipLaunchKernelGGL(k_row_fill, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, cone->rows[t].p, nr,
-                             crow, pre, where[t - 1].p, cone->rowptr[t].p, cone->col[t].p, cone->edge[t].p);
+          hipLaunchKernelGGL(k_row_fill, dim3(blocks_for(nr, 4)), dim3(256), 0, st, cone->rows[t].p, nr, crow, pre,
+                             where[t - 1].p, cone->rowptr[t].p, cone->col[t].p, cone->edge[t].p);
       }
     }
     cone->out_src.alloc(n_out);
