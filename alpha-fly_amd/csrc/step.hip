@@ -407,6 +407,11 @@ void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, h
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
   constexpr bool kTL = sizeof(S) == 4;
+  if constexpr (V * sizeof(S) == 32) {
+    // 32-byte lanes exist for the row slots of half states only (state_step picks them for nothing else)
+    hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
+    return;
+  }
   if constexpr (V * sizeof(S) == 16) {
     if (rows_mode) {
       if (unroll <= 4) {   // 4 measured best for the row slots
@@ -482,6 +487,16 @@ void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   if (a.nrows == 0 || a.batch == 0) return;
   int v = 1, groups = 1;
   pick_shape(a, v, groups);
+  // Rows shorter than 16 non-zeros on average (or no matrix at all) would leave most of a round of G
+  // interleaved gathers empty: give each lane group its own row instead of its own non-zero.
+  const bool rows_mode = groups > 1 && tuning().rows_mode >= 0 &&
+                         (tuning().rows_mode > 0 || a.rowptr == nullptr || a.xprev == nullptr || avg_nnz < 16.0);
+  // Row slots of half states read 32 bytes per lane and non-zero (two 16-byte loads, 128 columns per group):
+  // a short row's wave is paced by its few dependent loads, so each round trip should carry more bytes.
+  if constexpr (sizeof(S) == 2) {
+    const bool wide_ok = a.ldo % 16 == 0 && aligned(a.xout, 32) && (!a.xprev || (a.ldx % 16 == 0 && aligned(a.xprev, 32)));
+    if (rows_mode && v == 8 && groups == 8 && tuning().rows_vec != 8 && wide_ok) v = 16;
+  }
   a.u_vec = (a.u != nullptr && a.ldu % v == 0 && aligned(a.u, (size_t)v * sizeof(U))) ? 1 : 0;
   const int width = (64 / groups) * v;
   const int chunks = (int)((a.batch + width - 1) / width);
@@ -491,19 +506,18 @@ void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   a.wpt = chunks / tiles;
   const int unroll = tuning().unroll > 0 ? tuning().unroll : 0;   // 0: each kernel's measured default
   a.nt_store = tuning().nt_store;
-  // Rows shorter than 16 non-zeros on average (or no matrix at all) would leave most of a round of G
-  // interleaved gathers empty: give each lane group its own row instead of its own non-zero.
-  const bool rows_mode = groups > 1 && tuning().rows_mode >= 0 &&
-                         (tuning().rows_mode > 0 || a.rowptr == nullptr || a.xprev == nullptr || avg_nnz < 16.0);
   a.slots = rows_mode ? (a.nrows + groups - 1) / groups : a.nrows;
   switch (v) {
-    // only 16-byte lanes (V = 16 / sizeof(S)) have grouped and row-slot kernels; pick_shape sets groups to
-    // 1 for every other V, so rows_mode is false there too
+    // only 16-byte lanes (V = 16 / sizeof(S)) have grouped and row-slot kernels, and 32-byte lanes of half
+    // states a row-slot kernel; pick_shape sets groups to 1 for every other V, so rows_mode is false there too
     case 1: launch_v<S, U, 1>(a, 1, unroll, false, st); break;
     case 2: launch_v<S, U, 2>(a, 1, unroll, false, st); break;
     case 4: launch_v<S, U, 4>(a, groups, unroll, rows_mode, st); break;
-    default:
+    case 8:
       if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, groups, unroll, rows_mode, st);
+      break;
+    default:
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 16>(a, groups, unroll, rows_mode, st);
       break;
   }
   check_launch("state step");
@@ -738,6 +752,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "unroll") tuning().unroll = (int)value;
     else if (k == "groups") tuning().groups = (int)value;
     else if (k == "rows_mode") tuning().rows_mode = (int)value;
+    else if (k == "rows_vec") tuning().rows_vec = (int)value;
     else if (k == "nt_store") tuning().nt_store = (int)value;
     else if (k == "tiles") tuning().tiles = (int)value;
     else if (k == "spmm_groups") tuning().spmm_groups = (int)value;

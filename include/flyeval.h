@@ -271,7 +271,8 @@ int fly_profile_read(double *ms, int64_t *launches);
  * row-major (0 = automatic, 1 = all column chunks of a row back to back); "unroll": non-zeros each wave
  * gathers per iteration (8, 16 or 32; 0 = automatic); "nt_store": 1 writes the new state with non-temporal
  * stores; "groups": lane groups per wave that gather different non-zeros (1, 2, 4, 8; 0 = automatic);
- * "rows_mode": 1 gives each lane group its own row, -1 never, 0 for steps with short rows; "spmm_groups":
+ * "rows_mode": 1 gives each lane group its own row, -1 never, 0 for steps with short rows; "rows_vec":
+ * half-state elements per lane of those row slots (8 = 16 bytes, 16 = 32 bytes; 0 = automatic); "spmm_groups":
  * lane groups of fly_spmm on 16-byte lanes (2, 4, 8; 0 = automatic); "gemm_tile": workgroup tile of the dense
  * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128; 0 = automatic).  Every selectable shape computes the same
  * function. */

@@ -199,6 +199,7 @@ def test_deviation_path_matches_exact_function(batch):
 
 STEP_SHAPES = [{"groups": 4}, {"groups": 2}, {"groups": 1}, {"groups": 1, "unroll": 16}, {"groups": 1, "unroll": 32},
                {"rows_mode": 1}, {"rows_mode": 1, "groups": 4}, {"rows_mode": 1, "unroll": 8}, {"rows_mode": -1},
+               {"rows_mode": 1, "rows_vec": 8}, {"rows_mode": 1, "rows_vec": 16}, {"rows_mode": 1, "rows_vec": 16, "unroll": 8},
                {"vec": 4}, {"vec": 2}, {"vec": 1}, {"nt_store": 1}]
 
 
