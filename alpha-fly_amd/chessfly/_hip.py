@@ -68,6 +68,7 @@ SIGNATURES = {
     "fly_train_step_backward": (_i32, [_i64, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _f32, _p, _i64, _p,
                                        _p, _p, _p, _i64, _p, _i64, _p]),
     "fly_sddmm": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _i32, _p]),
+    "fly_spmv_work": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p]),
     "fly_gather_probe": (_i32, [_p, _i64, _i64, _p, _i64, _p, _p]),
     "fly_profile_enable": (_i32, [_i32]),
     "fly_profile_read": (_i32, [_p, _p]),

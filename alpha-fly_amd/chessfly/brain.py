@@ -59,6 +59,22 @@ def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, out: to
     return y
 
 
+def _spmv_work(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, work,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """y (n_rows, 1) = A x for one column over a work list (fly_spmv_work): rows split into segments of at most
+    256 non-zeros, longest first, so a transposed connectome's heavy rows spread over several waves.  With
+    `out`, y is added to it."""
+    x = x.contiguous()
+    items, splits, n_slots = work
+    y = torch.empty(n_rows, 1, dtype=torch.float32, device=x.device) if out is None else out
+    partials = torch.empty(n_slots, dtype=torch.float32, device=x.device) if n_slots else None
+    _hip.check(_hip.load().fly_spmv_work(crow32.data_ptr(), col32.data_ptr(), val.data_ptr(), val.numel(), n_rows,
+                                         n_cols, x.data_ptr(), 1, y.data_ptr(), 1, int(out is not None),
+                                         items.data_ptr(), items.shape[0], splits.data_ptr(), splits.shape[0],
+                                         _hip.ptr(partials), n_slots, _hip.stream(x.device)), "fly_spmv_work")
+    return y
+
+
 def _sddmm(crow32, col32, n_rows: int, n_cols: int, g: torch.Tensor, x: torch.Tensor, nnz: int,
            out: torch.Tensor | None = None, ids32: torch.Tensor | None = None) -> torch.Tensor:
     """out[e] = sum_b g[row_e, b] x[col_e, b] on the device (fly_sddmm).  With `out` and `ids32` the values are
@@ -147,6 +163,8 @@ def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out
     if transposed:
         crow32, col32, _ = op._transposed()
         _, _, n_cols, n_rows = op._structure()
+        if x.shape[1] == 1 and (out is None or out.is_contiguous()):
+            return _spmv_work(crow32, col32, _gathered(op, w, True), n_rows, n_cols, x, op._backward_work(), out=out)
     else:
         crow32, col32, n_rows, n_cols = op._structure()
     return _spmm(crow32, col32, _gathered(op, w, transposed), n_rows, n_cols, x, out=out)
@@ -586,6 +604,14 @@ class ConnectomeRNN(nn.Module):
 
     def _edge_ids(self):
         return None
+
+    def _backward_work(self):
+        """The work list of products over W^T (backward_work), built on first use for the current structure."""
+        t_crow32 = self._transposed()[0]
+        cached = getattr(self, "_t_work", None)
+        if cached is None or cached[0] is not t_crow32:
+            self._t_work = (t_crow32, backward_work(t_crow32))
+        return self._t_work[1]
 
     # ---- plans (everything that depends on the weights only; rebuilt when a parameter changes) -------
     def _plan(self, key_extra, build):

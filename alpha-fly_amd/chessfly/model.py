@@ -56,7 +56,9 @@ class RunningNorm(nn.Module):
     def forward(self, r: torch.Tensor) -> torch.Tensor:
         if self.training and r.shape[0] > 1:
             with torch.no_grad():
-                m = 1.0 if not self.initialised else self.momentum
+                # the first batch's weight 1, then the momentum, chosen on the device: reading the flag on
+                # the host would wait for the whole forward and leave the GPU idle while the backward queues
+                m = torch.where(self.initialised, self.momentum, 1.0)
                 self.mean.lerp_(r.mean(0), m)
                 self.var.lerp_(r.var(0), m)
                 self.initialised.fill_(True)
@@ -89,6 +91,13 @@ class FlyChessNet(nn.Module):
         self.register_buffer("move_to", torch.as_tensor(to), persistent=False)
         self.register_buffer("move_from32", torch.as_tensor(frm.astype(np.int32)), persistent=False)
         self.register_buffer("move_to32", torch.as_tensor(to.astype(np.int32)), persistent=False)
+        # (64, N_MOVES) one-hot maps of each move's from and to square: f[:, move_from] as f @ onehot, exact in
+        # the forward (one value times 1 plus zeros per output), and in the backward a product instead of the
+        # index backward's radix sort of 4,168 repeated indices
+        for name, sq in (("move_from_onehot", frm), ("move_to_onehot", to)):
+            onehot = torch.zeros(64, len(sq))
+            onehot[torch.as_tensor(sq), torch.arange(len(sq))] = 1.0
+            self.register_buffer(name, onehot, persistent=False)
         for layer in (self.policy_from, self.policy_to):
             nn.init.zeros_(layer.weight)
             nn.init.zeros_(layer.bias)
@@ -137,7 +146,7 @@ class FlyChessNet(nn.Module):
             enc = nn.functional.linear(x[:, :N_BASE], self.encoder.weight[:, :N_BASE], self.encoder.bias)
         u_in = (enc * self.cfg.input_gain).to(dtype).T.contiguous()
         r = self.norm(self.brain.forward_io(u_in, self.in_idx, self.out_idx, self.cfg.steps).T.float())
-        logits = self.policy(r) + self.policy_from(r)[:, self.move_from] + self.policy_to(r)[:, self.move_to]
+        logits = self.policy(r) + self.policy_from(r) @ self.move_from_onehot + self.policy_to(r) @ self.move_to_onehot
         return logits, self.value(r)
 
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

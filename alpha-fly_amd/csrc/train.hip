@@ -163,27 +163,127 @@ __global__ __launch_bounds__(256) void k_sddmm(const SddmmArgs a) {
   }
 }
 
-// y = A x for one column (the resting trajectory's products): a wave per row, its lanes across the row's
-// non-zeros, then one wave sum.
-__global__ __launch_bounds__(256) void k_spmv(const SpmmArgs a) {
-  const uint32_t row = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (row >= (uint32_t)a.nrows) return;
-  const int lane = threadIdx.x & 63;
-  const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
+// One column (the resting trajectory's products, batch 1): 16 lanes per row or work item, four per wave.  Lane
+// s of a unit takes its non-zeros s, s + 16, ..., four loads in flight per round, and the unit's 16 partial sums
+// meet through xor shuffles.  A wave per row would leave most of the wave on one dependent chain of loads per
+// row of ~63 non-zeros; four units per wave keep four times the loads in flight.
+struct Spmv1Args {
+  const int32_t *rowptr, *col;
+  const float *val;
+  const int32_t *val_ids;   // null, or per non-zero the index of its value in val (rows mode only)
+  uint32_t val_bytes;       // bytes of val when val_ids is given (reads past it give 0)
+  const float *x;           // x[col * ldx]
+  float *y;                 // y[row * ldy]
+  int64_t ldx, ldy;
+  uint32_t xbytes;
+  int32_t nrows, nnz, accumulate;
+  const int4 *items;        // work items {row, first non-zero, count, slot}, or null: one unit per row
+  int32_t n_items, n_slots;
+  float *partials;          // slot >= 0: the unit's sum goes to partials[slot] (k_spmv_partials adds them)
+};
+
+__global__ __launch_bounds__(256) void k_spmv(const Spmv1Args a) {
+  const int s = threadIdx.x & 15;
+  const uint32_t unit = blockIdx.x * 16u + (threadIdx.x >> 4);
+  uint32_t row = unit;
+  int32_t first = 0, count = INT32_MAX, slot = -1;
+  bool has = true;
+  if (a.items != nullptr) {
+    has = unit < (uint32_t)a.n_items;
+    if (has) {
+      const int4 it = a.items[unit];
+      row = (uint32_t)it.x;
+      first = it.y;
+      count = it.z;
+      slot = it.w;
+      has = slot < a.n_slots;
+    }
+  }
+  has = has && row < (uint32_t)a.nrows;
+  // a malformed row pointer or work item gives wrong results, never an access outside the arrays
+  int32_t beg = 0, end = 0;
+  if (has) {
+    const int32_t row_beg = min(max(a.rowptr[row], 0), a.nnz);
+    const int32_t row_end = min(max(a.rowptr[row + 1], row_beg), a.nnz);
+    beg = row_beg + min(max(first, 0), row_end - row_beg);
+    end = beg + min(max(count, 0), row_end - beg);
+  }
   const __amdgpu_buffer_rsrc_t rx = buffer_of(a.x, a.xbytes);
   const __amdgpu_buffer_rsrc_t rw = buffer_of(a.val, a.val_bytes);
   const uint32_t row_bytes = (uint32_t)a.ldx * 4u;
   float acc = 0.0f;
-  for (int32_t e = beg + lane; e < end; e += 64)
-    acc = fmaf(a.val_ids ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, (int)((uint32_t)a.val_ids[e] * 4u), 0, 0))
-                         : a.val[e],
-               __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                             rx, (int)__umul24((uint32_t)a.col[e], row_bytes), 0, 0)), acc);
+  for (int32_t e0 = beg + s; e0 < end; e0 += 64) {
+    float v[4], xv[4];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-  if (lane == 0) {
+    for (int j = 0; j < 4; ++j) {
+      const int32_t e = e0 + 16 * j;
+      const bool live = e < end;
+      const uint32_t c = live ? (uint32_t)a.col[e] : 0u;
+      v[j] = !live ? 0.0f
+             : a.val_ids ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, (int)((uint32_t)a.val_ids[e] * 4u), 0, 0))
+                         : a.val[e];
+      xv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (int)__umul24(c, row_bytes), 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(v[j], xv[j], acc);
+  }
+  acc += __shfl_xor(acc, 8);
+  acc += __shfl_xor(acc, 4);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 1);
+  if (!has || s != 0) return;
+  if (slot >= 0) {
+    a.partials[slot] = acc;
+  } else {
     float *dst = a.y + (int64_t)row * a.ldy;
     *dst = a.accumulate ? *dst + acc : acc;
+  }
+}
+
+// y[row] += the row's partial sums {row, first slot, slot count}, in slot order (one column).  The row's first
+// segment wrote y[row] itself, so the sum runs first segment, then its later segments in order.
+__global__ __launch_bounds__(256) void k_spmv_partials(const int4 *__restrict__ splits, int32_t n_splits,
+                                                       const float *__restrict__ partials, int32_t n_slots,
+                                                       float *__restrict__ y, int64_t ldy, int32_t nrows) {
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  if (i >= n_splits) return;
+  const int4 sp = splits[i];
+  if ((uint32_t)sp.x >= (uint32_t)nrows || sp.y < 0 || sp.z < 0 || sp.y > n_slots - sp.z) return;
+  float *dst = y + (int64_t)sp.x * ldy;
+  float v = *dst;
+  for (int32_t k = 0; k < sp.z; ++k) v += partials[sp.y + k];
+  *dst = v;
+}
+
+// out[e] (+)= g[row_e] x[col_e] for one column: 16 lanes per row, four rows per wave, four non-zeros per lane
+// in flight.  Each value is one rounded product, as k_sddmm's batch loop computes it for one column.
+__global__ __launch_bounds__(256) void k_sddmm1(const SddmmArgs a) {
+  const int s = threadIdx.x & 15;
+  const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 4);
+  if (row >= (uint32_t)a.nrows) return;
+  const int32_t beg = a.rowptr[row], end = a.rowptr[row + 1];
+  const float gr = a.g[(int64_t)row * a.ldg];
+  const __amdgpu_buffer_rsrc_t rx = buffer_of(a.x, a.xbytes);
+  const uint32_t row_bytes = (uint32_t)a.ldx * 4u;
+  for (int32_t e0 = beg + s; e0 < end; e0 += 64) {
+    float xv[4];
+    uint32_t slot[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t e = e0 + 16 * j;
+      const bool live = e < end;
+      xv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          rx, (int)__umul24(live ? (uint32_t)a.col[e] : 0u, row_bytes), 0, 0));
+      slot[j] = live ? (a.ids ? (uint32_t)a.ids[e] : (uint32_t)e) : a.n_out;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (slot[j] < a.n_out) {
+        const float v = fmaf(gr, xv[j], 0.0f);
+        float *dst = a.out + slot[j];
+        *dst = a.accumulate ? *dst + v : v;
+      }
+    }
   }
 }
 
@@ -530,7 +630,9 @@ extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *
     // one column: lanes across the non-zeros; else 16-byte lanes in groups of 16 (64 columns per chunk) when
     // the rows allow them, else 4-byte lanes in groups of 8
     if (batch == 1) {
-      hipLaunchKernelGGL(k_spmv, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), a);
+      Spmv1Args b{rowptr, col, val, val_ids, a.val_bytes, x, y, ldx, ldy, a.xbytes, (int32_t)nrows, INT32_MAX,
+                  accumulate != 0, nullptr, 0, 0, nullptr};
+      hipLaunchKernelGGL(k_spmv, dim3(blocks_for(nrows, 16)), dim3(256), 0, as_stream(stream), b);
     } else if (batch >= 4 && vec4_ok(x, ldx) && vec4_ok(y, ldy)) {
       const int g = tuning().spmm_groups == 2 || tuning().spmm_groups == 8 ? tuning().spmm_groups : 4;
       const int width = 64 / g * 4;   // columns per chunk
@@ -563,11 +665,40 @@ extern "C" int fly_sddmm(const int32_t *rowptr, const int32_t *col, int64_t nrow
     SddmmArgs a{rowptr, col, g, x, out, ids, ldg, ldx, ncols ? checked_bytes(ncols, ldx) : 0u, (int32_t)nrows,
                 (int32_t)batch, accumulate != 0, (uint32_t)n_out};
     const dim3 grid(blocks_for(nrows, 4)), block(256);
-    if (batch >= 4 && vec4_ok(x, ldx))
+    if (batch == 1)
+      hipLaunchKernelGGL(k_sddmm1, dim3(blocks_for(nrows, 16)), block, 0, as_stream(stream), a);
+    else if (batch >= 4 && vec4_ok(x, ldx))
       hipLaunchKernelGGL(k_sddmm<4>, grid, block, 0, as_stream(stream), a);
     else
       hipLaunchKernelGGL(k_sddmm<1>, grid, block, 0, as_stream(stream), a);
     check_launch("sddmm");
+  });
+}
+
+extern "C" int fly_spmv_work(const int32_t *rowptr, const int32_t *col, const float *val, int64_t nnz, int64_t nrows,
+                             int64_t ncols, const float *x, int64_t ldx, float *y, int64_t ldy, int32_t accumulate,
+                             const int32_t *items, int64_t n_items, const int32_t *splits, int64_t n_splits,
+                             float *partials, int64_t n_slots, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(nrows >= 0 && ncols >= 0 && nnz >= 0 && n_items >= 0 && n_splits >= 0 && n_slots >= 0, "negative size");
+    FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
+    FLY_REQUIRE(nnz < (int64_t)INT32_MAX && n_items < (int64_t)INT32_MAX && n_splits < (int64_t)INT32_MAX &&
+                n_slots < (int64_t)INT32_MAX, "size out of range");
+    if (!nrows || !n_items) return;
+    FLY_REQUIRE(rowptr && y && ldy >= 1 && items, "bad argument");
+    FLY_REQUIRE(nnz == 0 || (col && val), "bad argument");
+    FLY_REQUIRE(ncols == 0 || (x && ldx >= 1 && ldx < (1 << 22)), "bad argument");
+    FLY_REQUIRE((n_splits == 0 || splits) && (n_slots == 0 || partials), "split rows need splits and partials");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    Spmv1Args a{rowptr, col, val, nullptr, 0u, x, y, ldx, ldy, ncols ? checked_bytes(ncols, ldx) : 0u,
+                (int32_t)nrows, (int32_t)nnz, accumulate != 0, reinterpret_cast<const int4 *>(items),
+                (int32_t)n_items, (int32_t)n_slots, partials};
+    hipLaunchKernelGGL(k_spmv, dim3(blocks_for(n_items, 16)), dim3(256), 0, as_stream(stream), a);
+    if (n_splits)
+      hipLaunchKernelGGL(k_spmv_partials, dim3(blocks_for(n_splits, 256)), dim3(256), 0, as_stream(stream),
+                         reinterpret_cast<const int4 *>(splits), (int32_t)n_splits, partials, (int32_t)n_slots, y, ldy,
+                         (int32_t)nrows);
+    check_launch("spmv work");
   });
 }
 

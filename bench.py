@@ -193,16 +193,21 @@ def train_bench(args, dev) -> dict:
     for _ in range(args.warmup):
         loss0 = step()
     torch.cuda.synchronize()
-    _hip.profile_enable(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         loss = step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # the device products' share from a shorter second pass with the library's launch events on
+    prof_steps = min(args.steps, 5)
+    _hip.profile_enable(True)
+    for _ in range(prof_steps):
+        step()
+    torch.cuda.synchronize()
     prof = _hip.profile_read()
     _hip.profile_enable(False)
     value = args.batch * args.steps / wall
-    sparse_ms = prof["other"][0] / args.steps
+    sparse_ms = prof["other"][0] / prof_steps
     log(f"{args.steps} train steps: {wall * 1e3 / args.steps:.2f} ms each, {value:,.0f} positions/s; device sparse "
         f"products {sparse_ms:.2f} ms per step; loss {float(loss0):.4f} -> {float(loss):.4f}")
     cpu = None
@@ -224,7 +229,7 @@ def train_bench(args, dev) -> dict:
         "config": {"workload": f"FlyChessNet train_step, synthetic connectome {conn.n_neurons} neurons / "
                                f"{conn.n_edges} synapses, B={args.batch}, {args.recurrent_steps} steps, light cone",
                    "batch": args.batch, "recurrent_steps": args.recurrent_steps, "graph": args.graph},
-        "sparse_kernel_ms_per_step": round(sparse_ms, 3), "sparse_launches_per_step": prof["other"][1] // args.steps,
+        "sparse_kernel_ms_per_step": round(sparse_ms, 3), "sparse_launches_per_step": prof["other"][1] // prof_steps,
         "cpu_baseline": cpu,
     }
 
@@ -372,7 +377,6 @@ def main() -> int:
         for _ in range(args.warmup):
             net(x)
         torch.cuda.synchronize()
-        _hip.profile_enable(True)
         stream = torch.cuda.current_stream(dev)
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -383,6 +387,12 @@ def main() -> int:
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - w0
+        # the per-kernel-class split comes from a second pass with the library's launch events on, so the
+        # timed pass above carries no measurement overhead
+        _hip.profile_enable(True)
+        for _ in range(args.steps):
+            net(x)
+        torch.cuda.synchronize()
         prof = _hip.profile_read()
         _hip.profile_enable(False)
     if args.calibrate_copy > 0:

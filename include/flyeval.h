@@ -26,6 +26,8 @@
  *                         expected_value)
  *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
  *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass)
+ *   fly_spmv_work         chessfly/brain.py:79-99 and :238-252 (grad_h = A^T grad_y of the resting trajectory's
+ *                         one-column products, under autograd)
  *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
  *                         gradients)
  */
@@ -199,6 +201,20 @@ int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val
 int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
               int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, int64_t n_out,
               const int32_t *ids_dev, int32_t accumulate, void *stream);
+
+/* y (+)= A x for one column over a work list: items_dev (n_items, 4) int32 {row, first non-zero, count, slot}
+ * cover every row, each row's segments in order (as chessfly.brain.backward_work builds them for a row
+ * pointer: a row's first segment has slot -1, its later ones slots >= 0).  An item with slot < 0 writes
+ * y[row * ldy] (adds to it when accumulate != 0); slot >= 0 writes partials_dev[slot], and splits_dev
+ * (n_splits, 4) int32 {row, first slot, slot count, 0} then add those slots to y[row * ldy] in slot order.
+ * Long rows (a transposed connectome's out-degrees run to thousands) thus spread over several waves and the
+ * sums stay deterministic.
+ * x[col * ldx].  Row pointers are clamped into [0, nnz] and items into their rows, so a malformed structure
+ * gives wrong results, never an access outside the arrays. */
+int fly_spmv_work(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, int64_t nnz,
+                  int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx, float *y_dev, int64_t ldy,
+                  int32_t accumulate, const int32_t *items_dev, int64_t n_items, const int32_t *splits_dev,
+                  int64_t n_splits, float *partials_dev, int64_t n_slots, void *stream);
 
 /* The backward of y = A h in one pass over A^T (CSR t_rowptr / t_col, values vals in that order, ids = each
  * non-zero's index in the weight vector): gh (ncols of A, ldgh) (+)= A^T gy and gw[ids[e]] += sum_b

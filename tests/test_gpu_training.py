@@ -161,6 +161,35 @@ def test_transposed_backward_matches_float64(batch, heavy, seg):
     _close(gw, torch.as_tensor(want), 1e-5, "dL/dw")
 
 
+@pytest.mark.parametrize("heavy,seg,accumulate", [(True, 256, 0), (True, 64, 1), (False, 64, 0), (False, 256, 1)])
+def test_one_column_product_over_a_work_list_matches_float64(heavy, seg, accumulate):
+    """fly_spmv_work: y (+)= A x for one column from backward_work's longest-first items, long rows as several
+    segments whose partial sums are added in slot order, against float64; empty rows get 0 (or keep y)."""
+    from chessfly import _hip
+    from chessfly.brain import backward_work
+    lib = _hip.load()
+    rows, cols = 601, 450
+    crow, r, c, val = _heavy_csr(rows, cols, seg + accumulate) if heavy else _random_csr(rows, cols, 20000, seg)
+    nnz = len(r)
+    rng = np.random.default_rng(seg)
+    x = rng.normal(0, 1, (cols, 1))
+    y0 = rng.normal(0, 1, (rows, 1))
+    d = lambda a, dt=torch.float32: torch.as_tensor(np.ascontiguousarray(a), device=DEV).to(dt)
+    crow_d, col_d, val_d, x_d, y = d(crow, torch.int32), d(c, torch.int32), d(val), d(x), d(y0)
+    items, splits, n_slots = backward_work(crow_d, seg)
+    assert n_slots > 0 or not heavy
+    partials = torch.full((max(n_slots, 1),), float("nan"), device=DEV)   # every slot is written before use
+    st = _hip.stream(torch.device(DEV))
+    _hip.check(lib.fly_spmv_work(crow_d.data_ptr(), col_d.data_ptr(), val_d.data_ptr(), nnz, rows, cols,
+                                 x_d.data_ptr(), 1, y.data_ptr(), 1, accumulate, items.data_ptr(), items.shape[0],
+                                 splits.data_ptr(), splits.shape[0], partials.data_ptr(), n_slots, st),
+               "fly_spmv_work")
+    dense = np.zeros((rows, cols))
+    np.add.at(dense, (r, c), val)
+    want = dense @ x + (y0 if accumulate else 0.0)
+    _close(y, torch.as_tensor(want), 1e-5, "spmv over the work list")
+
+
 def _rnn_pair(conn, seed: int, scale: float = 3.0):
     from chessfly.brain import ConnectomeRNN
     lg, bias, al = random_params(conn, seed)
@@ -293,6 +322,18 @@ def test_train_step_gradients_match_the_oracle():
         assert float(want.abs().max()) > 0, name
         _close(got, want, 2e-4, name)
     assert float(net.encoder.weight.grad[:, N_BASE:].abs().sum()) == 0   # attack planes off: no gradient
+
+
+def test_training_head_square_maps_equal_the_indexing_exactly():
+    """The training forward adds the from/to-square heads as f @ one-hot maps (model.py:104-110 index them):
+    bit-identical on the device to f[:, move_from] and f[:, move_to]."""
+    from chessfly.model import FlyChessNet, ModelConfig
+    from chessfly.synthetic import GraphSpec, synthetic_connectome
+    conn = synthetic_connectome(GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=100, seed=5))
+    net = FlyChessNet(conn, ModelConfig(steps=4)).to(DEV)
+    f = torch.randn(37, 64, device=DEV, generator=torch.Generator(device=DEV).manual_seed(1)) * 100
+    assert torch.equal(f @ net.move_from_onehot, f[:, net.move_from])
+    assert torch.equal(f @ net.move_to_onehot, f[:, net.move_to])
 
 
 def test_training_mode_without_autograd_updates_the_normaliser_and_matches_eval():
