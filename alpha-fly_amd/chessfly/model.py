@@ -201,14 +201,17 @@ def _upload(a: np.ndarray, device) -> torch.Tensor:
 
 class _Submitted:
     """A batch in flight: the pinned host buffers the device copies its answers into, and the event
-    recorded after the last copy."""
+    recorded after the last copy.  The copies run on `down` after the compute stream's work so far."""
 
-    def __init__(self, device_outputs, stream):
+    def __init__(self, device_outputs, compute, down):
+        down.wait_stream(compute)
         self.host = [torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for t in device_outputs]
-        for h, t in zip(self.host, device_outputs):
-            h.copy_(t, non_blocking=True)
+        with torch.cuda.stream(down):
+            for h, t in zip(self.host, device_outputs):
+                h.copy_(t, non_blocking=True)
+                t.record_stream(down)          # the allocator keeps t until this copy has read it
         self.done = torch.cuda.Event()
-        self.done.record(stream)
+        self.done.record(down)
 
     def wait(self):
         self.done.synchronize()
@@ -220,13 +223,24 @@ class _Submitted:
 
 class Evaluator:
     """The `evaluate` callable of the search: numpy in, numpy out (chessfly/model.py:113-135).  `submit`
-    queues the upload, the forward and the download on the device's current stream and returns before the
-    GPU finishes; `result` waits for it.  One kernel (fly_evaluator_outputs) computes the expected values
-    and either rounds the whole policy to half precision (lazy search) or gathers the legal moves' logits
-    (eager search), so only the requested bytes cross back to the host."""
+    queues the upload, the forward and the download and returns before the GPU finishes; `result` waits for
+    it.  One kernel (fly_evaluator_outputs) computes the expected values and either rounds the whole policy to
+    half precision (lazy search) or gathers the legal moves' logits (eager search), so only the requested
+    bytes cross back to the host.
+
+    Uploads and downloads run on two copy streams of their own, ordered with the compute stream (the
+    device's current stream) by events: with two batches in flight, as the search's workers keep them
+    (workers.py:118-167), batch i+1's boards go up and batch i's answers come down while the GPU computes."""
 
     def __init__(self, net: FlyChessNet, device):
         self.net, self.device = net, device
+        self._up = self._down = None
+
+    def _streams(self):
+        if self._up is None:
+            self._up = torch.cuda.Stream(device=self.device)      # default priority
+            self._down = torch.cuda.Stream(device=self.device)
+        return self._up, self._down
 
     @torch.no_grad()
     def submit(self, x, rows, cols):
@@ -234,32 +248,41 @@ class Evaluator:
         x = np.ascontiguousarray(x)
         if x.dtype not in (np.float16, np.float32):
             x = x.astype(np.float32)
-        logits, wdl = self.net(_upload(x, self.device))
+        up, down = self._streams()
+        compute = torch.cuda.current_stream(self.device)
+        r = c = None
+        n_legal = 0
+        with torch.cuda.stream(up):
+            xd = _upload(x, self.device)
+            if rows is not None:
+                rows = np.ascontiguousarray(rows, dtype=np.int64)
+                cols = np.ascontiguousarray(cols, dtype=np.int64)
+                if rows.shape != cols.shape or rows.ndim != 1:
+                    raise IndexError(f"Evaluator: rows {rows.shape} and cols {cols.shape} must be equal 1-d shapes")
+                n_legal = len(rows)
+                if n_legal:
+                    r, c = _upload(rows, self.device), _upload(cols, self.device)
+        compute.wait_stream(up)
+        for t in (xd, r, c):
+            if t is not None:
+                t.record_stream(compute)       # allocated on the upload stream, read on the compute stream
+        logits, wdl = self.net(xd)
         batch, n_moves = logits.shape
         device = logits.device
         values = torch.empty(batch, dtype=torch.float32, device=device)
         bad = torch.empty(1, dtype=torch.int32, device=device)
         if rows is None:                      # lazy search: the whole policy vector, half precision
             policy = torch.empty(batch, n_moves, dtype=torch.float16, device=device)
-            r = c = None
-            n_legal, out16, legal = 0, policy.data_ptr(), None
+            out16, legal = policy.data_ptr(), None
         else:
-            rows = np.ascontiguousarray(rows, dtype=np.int64)
-            cols = np.ascontiguousarray(cols, dtype=np.int64)
-            if rows.shape != cols.shape or rows.ndim != 1:
-                raise IndexError(f"Evaluator: rows {rows.shape} and cols {cols.shape} must be equal 1-d shapes")
-            n_legal = len(rows)
-            if n_legal:
-                r, c = _upload(rows, device), _upload(cols, device)
-            else:                             # non-null pointers still select the legal-move form
+            if not n_legal:                   # non-null pointers still select the legal-move form
                 r = c = torch.zeros(1, dtype=torch.int64, device=device)
             policy = torch.empty(n_legal, dtype=torch.float32, device=device)
             out16, legal = None, policy.data_ptr()
-        stream = torch.cuda.current_stream(device)
         _hip.check(_hip.load().fly_evaluator_outputs(logits.data_ptr(), wdl.data_ptr(), batch, n_moves, _hip.ptr(r),
                                                      _hip.ptr(c), n_legal, out16, legal, values.data_ptr(),
-                                                     bad.data_ptr(), stream.cuda_stream), "fly_evaluator_outputs")
-        return _Submitted((policy, values, bad), stream)
+                                                     bad.data_ptr(), compute.cuda_stream), "fly_evaluator_outputs")
+        return _Submitted((policy, values, bad), compute, down)
 
     @staticmethod
     def result(handle):

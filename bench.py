@@ -267,9 +267,11 @@ def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> dict:
 
 def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> dict:
     """The search's view (chessfly/model.py:113-135): fp16 boards from host numpy through Evaluator.submit
-    and result, one batch at a time, so the pinned H2D copy of the boards, the forward, the output kernel and
-    the D2H copy of the answers are all inside the clock.  Lazy returns the whole fp16 policy; eager returns
-    `legal_per_board` gathered logits per board."""
+    and result, so the pinned H2D copy of the boards, the forward, the output kernel and the D2H copy of the
+    answers are all inside the clock.  Lazy returns the whole fp16 policy; eager returns `legal_per_board`
+    gathered logits per board.  "lazy"/"eager" run one batch at a time; "*_pipelined" keep two batches in
+    flight, as the search's workers do (workers.py:118-167: submit the next batch, then take the previous
+    result), so one batch's copies overlap the other's forward."""
     import numpy as np
     import torch
     from chessfly.encoding import N_MOVES
@@ -289,8 +291,19 @@ def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> d
             ev.result(ev.submit(x16, r, c))
         dt = (time.perf_counter() - t0) / steps
         out[name] = {"evals_per_s": round(len(x16) / dt, 1), "ms_per_batch": round(dt * 1e3, 3)}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pending = ev.submit(x16, r, c)
+        for _ in range(steps - 1):
+            nxt = ev.submit(x16, r, c)
+            ev.result(pending)
+            pending = nxt
+        ev.result(pending)
+        dt = (time.perf_counter() - t0) / steps
+        out[name + "_pipelined"] = {"evals_per_s": round(len(x16) / dt, 1), "ms_per_batch": round(dt * 1e3, 3)}
     out["note"] = (f"B={len(x16)} fp16 boards from host numpy, pinned staging; lazy: fp16 (B, {N_MOVES}) policy "
-                   f"back; eager: {legal_per_board} legal logits per board back; plus values")
+                   f"back; eager: {legal_per_board} legal logits per board back; plus values; pipelined: two "
+                   f"batches in flight")
     return out
 
 

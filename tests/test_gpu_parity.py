@@ -569,6 +569,19 @@ def test_evaluator_protocol(full_net):
     assert legal0.shape == (0,) and np.array_equal(values0, values)
     with pytest.raises(IndexError):
         ev(x, np.array([9]), np.array([0]))
+    # six batches of different boards in flight (uploads, forwards and downloads on three streams): each
+    # answer belongs to its own boards, bit for bit
+    xs = [synthetic_boards(7 + i, seed=10 + i).astype(np.float16) for i in range(6)]
+    handles = [ev.submit(xi, None, None) if i % 2 else ev.submit(xi, np.arange(len(xi)), np.arange(len(xi)))
+               for i, xi in enumerate(xs)]
+    for i, (xi, h) in enumerate(zip(xs, handles)):
+        got, _ = ev.result(h)
+        with torch.no_grad():
+            want = net(torch.as_tensor(xi, device=DEV).float())[0].cpu().numpy()
+        if i % 2:
+            assert np.array_equal(got.view(np.uint16), want.astype(np.float16).view(np.uint16))
+        else:
+            assert np.array_equal(got, want[np.arange(len(xi)), np.arange(len(xi))])
 
 
 def test_empty_batches_give_empty_outputs():
