@@ -450,8 +450,8 @@ template <typename S>
 constexpr int max_vec() { return 16 / (int)sizeof(S); }
 
 // Elements per lane and lane groups of the step: the tuned values when set and allowed by the alignment of
-// every V-wide access, else 16-byte lanes in groups sized so a chunk is 64 columns below 2048 boards and
-// 256 above, which keeps each sweep's gather working set small inside the Infinity Cache.
+// every V-wide access, else 16-byte lanes in groups of 8 lanes, so each group gathers one 128-byte line per
+// non-zero and a chunk sweep's working set is one line per source row.
 template <typename S, typename U>
 void pick_shape(const StepArgs<S, U> &a, int &v, int &groups) {
   auto ok = [&](int vv) {
@@ -474,9 +474,10 @@ void pick_shape(const StepArgs<S, U> &a, int &v, int &groups) {
     if (tg == 1 || tg == 2 || tg == 4 || tg == 8) {
       groups = tg;
     } else {
-      // 64 columns per chunk (half lanes hold 8 columns, float lanes 4): measured best on MI355X at B = 256,
-      // 1120, 2048 and 4096 with the state's odd-line row stride
-      const int lanes = 64 / v;
+      // one 128-byte line per lane group and gather (64 half or 32 float columns), with the state's odd-line
+      // row stride: measured best on MI355X for half states at B = 256-4096, and for float states 10-12% ahead
+      // of 64-column chunks at B = 64-4096, light cone or not
+      const int lanes = 128 / (v * (int)sizeof(S));
       groups = std::max(1, std::min(8, 64 / lanes));
     }
   }
