@@ -271,6 +271,85 @@ class _ConeRecurrence(torch.autograd.Function):
         return (None, None, gu, gw, *grads)
 
 
+class _RestingTrajectory(torch.autograd.Function):
+    """The resting trajectory and the light cone's constant drives (brain.py:238-252) as one autograd function
+    over device kernels, one column.  Per step one pass over W (fly_rest_forward) gives W c_{t-1} + b for
+    c_t = lerp(c_{t-1}, clamp(W c_{t-1} + b, 0, H), alpha) and, summed over the edges from outside R_{t-1}, the
+    drive k_t = (W c_{t-1} + b - A_t c_{t-1}[R_{t-1}])[R_t] of the step's rows.  The backward runs per step one
+    elementwise kernel (fly_rest_backward) and one pass over W and W^T (fly_rest_products_backward) into a
+    single dL/dw.  Inputs w (E), bias (n), alpha = sigmoid(alpha_logit) (n, 1); returns k_1..k_T, then
+    p_1..p_T = c_{t-1}[R_t] (each (|R_t|, 1)), then c_T[out_idx] (n_out, 1)."""
+
+    @staticmethod
+    def forward(ctx, rnn, cone, out_idx, w, bias, alpha):
+        ctx.set_materialize_grads(False)
+        lib = _hip.load()
+        dev = w.device
+        st = _hip.stream(dev)
+        n, T = rnn.n, cone.steps
+        member, _ = cone.rest_tables(n)
+        w, bias, alpha = w.contiguous(), bias.contiguous(), alpha.contiguous()
+        x2 = c_prev = None
+        ks, ps, saved = [], [], []
+        for t in range(1, T + 1):
+            full = torch.empty(n, device=dev)
+            outside = torch.empty(n, device=dev)
+            c_next = torch.empty(n, device=dev)
+            x2_next = torch.empty(n, 2, device=dev)
+            _hip.check(lib.fly_rest_forward(rnn.crow32.data_ptr(), rnn.pre32.data_ptr(), w.data_ptr(), n,
+                                            rnn.n_edges, _hip.ptr(x2), bias.data_ptr(), alpha.data_ptr(),
+                                            _hip.ptr(c_prev), float(rnn.h_max), member[t].data_ptr(),
+                                            full.data_ptr(), outside.data_ptr(), c_next.data_ptr(),
+                                            x2_next.data_ptr(), st), "fly_rest_forward")
+            rows = cone.rows[t]
+            ks.append(outside.index_select(0, rows).unsqueeze(1))
+            ps.append((c_prev.index_select(0, rows) if c_prev is not None
+                       else torch.zeros(rows.numel(), device=dev)).unsqueeze(1))
+            saved.append((full, c_prev, x2))
+            x2, c_prev = x2_next, c_next
+        c_out = c_prev.index_select(0, out_idx).unsqueeze(1)
+        ctx.rnn, ctx.cone, ctx.out_idx, ctx.steps_saved = rnn, cone, out_idx, saved
+        ctx.save_for_backward(w, alpha)
+        return (*ks, *ps, c_out)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        rnn, cone, out_idx = ctx.rnn, ctx.cone, ctx.out_idx
+        w, alpha = ctx.saved_tensors
+        lib = _hip.load()
+        dev = w.device
+        st = _hip.stream(dev)
+        n, T = rnn.n, cone.steps
+        member, pos = cone.rest_tables(n)
+        flat = lambda g: None if g is None else g.reshape(-1).contiguous()
+        g_ks, g_ps, g_out = [flat(g) for g in grads[:T]], [flat(g) for g in grads[T:2 * T]], flat(grads[2 * T])
+        gw = torch.zeros_like(w)
+        gbias = torch.zeros(n, device=dev)
+        galpha = torch.zeros(n, device=dev)
+        gc = None if g_out is None else torch.zeros(n, device=dev).index_copy_(0, out_idx, g_out)
+        t_crow32, t_col32, _ = rnn._transposed()
+        vals_t = _gathered(rnn, w, True)
+        items, splits, n_slots = rnn._backward_work()
+        partials = torch.empty(max(n_slots, 1), device=dev)
+        for t in range(T, 0, -1):
+            full, c_prev, x2 = ctx.steps_saved[t - 1]
+            g2 = torch.empty(n, 2, device=dev)
+            gc_prev = torch.empty(n, device=dev)
+            gk, gp = g_ks[t - 1], g_ps[t - 1]
+            _hip.check(lib.fly_rest_backward(_hip.ptr(gc), pos[t].data_ptr(), _hip.ptr(gk), _hip.ptr(gp),
+                                             full.data_ptr(), _hip.ptr(c_prev), alpha.data_ptr(), float(rnn.h_max),
+                                             n, g2.data_ptr(), gc_prev.data_ptr(), gbias.data_ptr(),
+                                             galpha.data_ptr(), st), "fly_rest_backward")
+            if x2 is not None:                 # t > 1: the products over W (c_0 = 0 has none)
+                _hip.check(lib.fly_rest_products_backward(
+                    rnn.crow32.data_ptr(), rnn.pre32.data_ptr(), n, rnn.n_edges, g2.data_ptr(), x2.data_ptr(),
+                    gw.data_ptr(), t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(),
+                    member[t - 1].data_ptr(), items.data_ptr(), items.shape[0], splits.data_ptr(), splits.shape[0],
+                    partials.data_ptr(), n_slots, gc_prev.data_ptr(), st), "fly_rest_products_backward")
+            gc = gc_prev
+        return None, None, None, gw, gbias, galpha.view_as(alpha)
+
+
 class _SparseRecurrent(torch.autograd.Function):
     """y = A h for A in CSR, the state (rows, batch) batch-fastest (brain.py:66-99), with A's values taken
     from the whole edge-weight vector w (a _SubMatrix reads w at its edge ids; the whole W is w itself).
@@ -433,6 +512,7 @@ class LightCone:
         self._rows = None
         self._steps_idx = None
         self._outs = None
+        self._rest = None
         self.ops = [None] + [_SubMatrix(self, t, self.row_counts[t], self.row_counts[t - 1], self.nnz[t])
                              if self.has_op[t] else None for t in range(1, T + 1)]
 
@@ -513,6 +593,23 @@ class LightCone:
 
     out_pos = property(lambda self: self._outputs()[0])
     out_src = property(lambda self: self._outputs()[1])
+
+    def rest_tables(self, n: int):
+        """Per step t = 0..T, R_t as a uint8 mask over the n neurons and each neuron's place in R_t (int32, -1
+        outside): the resting trajectory's kernels read them (built on first use)."""
+        if self._rest is None:
+            member, pos = [], []
+            for t in range(self.steps + 1):
+                r = self.rows[t]
+                m = torch.zeros(n, dtype=torch.uint8, device=self.device)
+                p = torch.full((n,), -1, dtype=torch.int32, device=self.device)
+                if r.numel():
+                    m[r] = 1
+                    p[r] = torch.arange(r.numel(), dtype=torch.int32, device=self.device)
+                member.append(m)
+                pos.append(p)
+            self._rest = (member, pos)
+        return self._rest
 
 
 class _Plan:
@@ -679,24 +776,6 @@ class ConnectomeRNN(nn.Module):
             h = torch.lerp(h, x, alpha)
         return h
 
-    def _constants(self, cone: LightCone, w: torch.Tensor, alpha: torch.Tensor):
-        """The resting trajectory c_0..c_T of a network that sees no position and, per step, the drive the
-        rows of R_t get from outside the cone, k_t = (W c_{t-1} + b)[R_t] - A_t c_{t-1}[R_{t-1}]
-        (brain.py:238-252), under autograd.  W c_0 = 0."""
-        c = torch.zeros(self.n, 1, dtype=w.dtype, device=w.device)
-        cs, ks = [c], [None]
-        bias = self.bias.unsqueeze(1)
-        for t in range(1, cone.steps + 1):
-            full = (_SparseRecurrent.apply(c, w, self) if t > 1 else torch.zeros_like(c)) + bias
-            k = _take_rows(full, cone.rows[t])
-            op = cone.ops[t]
-            if op is not None:
-                k = k - _SparseRecurrent.apply(_take_rows(c, cone.rows[t - 1]), w, op)
-            ks.append(k)
-            c = torch.lerp(c, full.clamp(0, self.h_max), alpha)
-            cs.append(c)
-        return cs, ks
-
     def _forward_io_autograd(self, u_in: torch.Tensor, cone: LightCone, out_idx: torch.Tensor,
                              steps: int) -> torch.Tensor:
         """forward_io under autograd, float32 (brain.py:289-329): rows outside R_t follow the resting
@@ -706,13 +785,12 @@ class ConnectomeRNN(nn.Module):
         batch = u_in.shape[1]
         w = self.edge_weights()
         alpha = torch.sigmoid(self.alpha_logit).unsqueeze(1)
-        cs, ks = self._constants(cone, w, alpha)
+        rest = _RestingTrajectory.apply(self, cone, out_idx, w, self.bias, alpha)
         flat = []
         for t in range(1, steps + 1):
-            rows = cone.rows[t]
-            flat += [ks[t], _take_rows(cs[t - 1], rows), _take_rows(alpha, rows)]
+            flat += [rest[t - 1], rest[steps + t - 1], _take_rows(alpha, cone.rows[t])]
         h = _ConeRecurrence.apply(cone, self.h_max, u_in, w, *flat)
-        out = _take_rows(cs[steps], out_idx).expand(-1, batch)
+        out = rest[2 * steps].expand(-1, batch)
         return out.index_copy(0, cone.out_pos, _take_rows(h, cone.out_src))
 
     # ---- the same function through the light cone ------------------------------------------------

@@ -593,6 +593,187 @@ __global__ __launch_bounds__(256) void k_add_partials(const int4 *__restrict__ s
   }
 }
 
+// ---- the resting trajectory under training (brain.py:238-252, one column) ----------------------------
+// c_t = lerp(c_{t-1}, clamp(W c_{t-1} + b, 0, H), alpha) over the whole network, and the drive the rows of R_t
+// get from outside the light cone, k_t = (W c_{t-1} + b - A_t c_{t-1}[R_{t-1}])[R_t], which is the same sum
+// over the edges whose presynaptic neuron lies outside R_{t-1}.  One pass over W gathers, per edge, the pair
+// x2[j] = {c_{t-1}[j], c_{t-1}[j] if j is outside R_{t-1} else 0} and keeps both sums; the full one is summed
+// in k_spmv's order, so c_t has the same bits as a separate product would give.
+
+struct RestFwdArgs {
+  const int32_t *crow, *pre;   // W in CSR, rows = postsynaptic neurons
+  const float *w;
+  const float2 *x2;            // the pairs of c_{t-1}, or null: c_{t-1} = 0 and no edge terms
+  const float *bias, *alpha;   // alpha: sigmoid(alpha_logit), n
+  const float *c_prev;         // c_{t-1}, or null: 0
+  const uint8_t *member;       // neurons of R_t, or null: none (builds the next step's pairs)
+  float *full, *outside, *c_next;
+  float2 *x2_next;
+  float hmax;
+  int32_t n, nnz;
+  uint32_t x2bytes;
+};
+
+__global__ __launch_bounds__(256) void k_rest_fwd(const RestFwdArgs a) {
+  const int s = threadIdx.x & 15;
+  const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const bool has = row < (uint32_t)a.n;
+  float acc = 0.0f, out = 0.0f;
+  if (has && a.x2 != nullptr) {
+    const int32_t beg = min(max(a.crow[row], 0), a.nnz);
+    const int32_t end = min(max(a.crow[row + 1], beg), a.nnz);
+    const __amdgpu_buffer_rsrc_t rx = buffer_of(a.x2, a.x2bytes);
+    for (int32_t e0 = beg + s; e0 < end; e0 += 64) {
+      float v[4];
+      float2 xv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t e = e0 + 16 * j;
+        const bool live = e < end;
+        v[j] = live ? a.w[e] : 0.0f;
+        xv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                               rx, (int)((live ? (uint32_t)a.pre[e] : 0u) * 8u), 0, 0));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = fmaf(v[j], xv[j].x, acc);
+        out = fmaf(v[j], xv[j].y, out);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) {
+    acc += __shfl_xor(acc, off);
+    out += __shfl_xor(out, off);
+  }
+  if (!has || s != 0) return;
+  const float b = a.bias[row];
+  const float f = acc + b;
+  a.full[row] = f;
+  a.outside[row] = out + b;
+  const float cn = lerp_torch(a.c_prev ? a.c_prev[row] : 0.0f, fminf(fmaxf(f, 0.0f), a.hmax), a.alpha[row]);
+  a.c_next[row] = cn;
+  a.x2_next[row] = make_float2(cn, (a.member && a.member[row]) ? 0.0f : cn);
+}
+
+// The backward of one step's elementwise part (torch.lerp's and clamp's gradients), per neuron: from
+// dL/dc_t, dL/dk_t and dL/dp_t (p_t = c_{t-1}[R_t], both scattered through pos = each neuron's place in R_t
+// or -1), the pair g2 = {dL/dfull, dL/doutside} for the products, dL/dc_{t-1} through the lerp and p_t, and
+// the bias and alpha gradients (accumulated).
+struct RestBwdArgs {
+  const float *gc;             // dL/dc_t, or null: 0
+  const int32_t *pos;
+  const float *gk, *gp;        // |R_t| each, or null: 0
+  const float *full, *c_prev, *alpha;   // c_prev null: 0
+  float2 *g2;
+  float *gc_prev, *gbias, *galpha;
+  float hmax;
+  int32_t n;
+};
+
+__global__ __launch_bounds__(256) void k_rest_bwd(const RestBwdArgs a) {
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  if (i >= a.n) return;
+  const float g = a.gc ? a.gc[i] : 0.0f;
+  const float al = a.alpha[i], f = a.full[i];
+  const float cp = a.c_prev ? a.c_prev[i] : 0.0f;
+  const int32_t p = a.pos[i];
+  const float gout = (p >= 0 && a.gk) ? a.gk[p] : 0.0f;
+  const float gfull = (f >= 0.0f && f <= a.hmax) ? g * al : 0.0f;   // clamp passes its bounds
+  a.g2[i] = make_float2(gfull, gout);
+  a.gbias[i] += gfull + gout;
+  a.galpha[i] += g * (fminf(fmaxf(f, 0.0f), a.hmax) - cp);
+  a.gc_prev[i] = g * (1.0f - al) + ((p >= 0 && a.gp) ? a.gp[p] : 0.0f);
+}
+
+// dL/dw_e += g2[post_e] . x2[pre_e] over W's rows (16 lanes per row): the full product's and the outside
+// sum's shares of each weight gradient in one pass.
+__global__ __launch_bounds__(256) void k_rest_sddmm(const int32_t *__restrict__ crow, const int32_t *__restrict__ pre,
+                                                    int32_t n, int32_t nnz, const float2 *__restrict__ g2,
+                                                    const float2 *__restrict__ x2, uint32_t x2bytes,
+                                                    float *__restrict__ gw) {
+  const int s = threadIdx.x & 15;
+  const uint32_t row = blockIdx.x * 16u + (threadIdx.x >> 4);
+  if (row >= (uint32_t)n) return;
+  const float2 gr = g2[row];
+  if (gr.x == 0.0f && gr.y == 0.0f) return;          // adds of 0 change nothing
+  const int32_t beg = min(max(crow[row], 0), nnz), end = min(max(crow[row + 1], beg), nnz);
+  const __amdgpu_buffer_rsrc_t rx = buffer_of(x2, x2bytes);
+  for (int32_t e0 = beg + s; e0 < end; e0 += 64) {
+    float2 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t e = e0 + 16 * j;
+      xv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             rx, (int)((e < end ? (uint32_t)pre[e] : 0u) * 8u), 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t e = e0 + 16 * j;
+      if (e < end) gw[e] += fmaf(gr.x, xv[j].x, gr.y * xv[j].y);
+    }
+  }
+}
+
+// dL/dc_{t-1}[j] += sum over W^T's row j of w_e (g2[post_e].x + (j outside R_{t-1} ? g2[post_e].y : 0)), over
+// the work list of W^T (as k_spmv's work items: first segments write, later ones go to partial slots).
+struct RestTArgs {
+  const int32_t *rowptr, *col;
+  const float *val;
+  const float2 *g2;
+  uint32_t g2bytes;
+  const uint8_t *member_prev;  // neurons of R_{t-1}, or null: none
+  float *y;
+  int32_t nrows, nnz;
+  const int4 *items;
+  int32_t n_items, n_slots;
+  float *partials;
+};
+
+__global__ __launch_bounds__(256) void k_rest_spmv_t(const RestTArgs a) {
+  const int s = threadIdx.x & 15;
+  const uint32_t unit = blockIdx.x * 16u + (threadIdx.x >> 4);
+  bool has = unit < (uint32_t)a.n_items;
+  uint32_t row = 0;
+  int32_t beg = 0, end = 0, slot = -1;
+  if (has) {
+    const int4 it = a.items[unit];
+    row = (uint32_t)it.x;
+    slot = it.w;
+    has = row < (uint32_t)a.nrows && slot < a.n_slots;
+    if (has) {
+      const int32_t row_beg = min(max(a.rowptr[row], 0), a.nnz);
+      const int32_t row_end = min(max(a.rowptr[row + 1], row_beg), a.nnz);
+      beg = row_beg + min(max(it.y, 0), row_end - row_beg);
+      end = beg + min(max(it.z, 0), row_end - beg);
+    }
+  }
+  const bool outside = has && !(a.member_prev && a.member_prev[row]);
+  const __amdgpu_buffer_rsrc_t rx = buffer_of(a.g2, a.g2bytes);
+  float acc = 0.0f;
+  for (int32_t e0 = beg + s; e0 < end; e0 += 64) {
+    float v[4];
+    float2 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t e = e0 + 16 * j;
+      const bool live = e < end;
+      v[j] = live ? a.val[e] : 0.0f;
+      xv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             rx, (int)((live ? (uint32_t)a.col[e] : 0u) * 8u), 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(v[j], outside ? xv[j].x + xv[j].y : xv[j].x, acc);
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (!has || s != 0) return;
+  if (slot >= 0)
+    a.partials[slot] = acc;
+  else
+    a.y[row] += acc;
+}
+
 bool vec4_ok(const void *p, int64_t ld) { return ld % 4 == 0 && aligned(p, 16); }
 
 uint32_t checked_bytes(int64_t rows, int64_t ld) {
@@ -699,6 +880,72 @@ extern "C" int fly_spmv_work(const int32_t *rowptr, const int32_t *col, const fl
                          reinterpret_cast<const int4 *>(splits), (int32_t)n_splits, partials, (int32_t)n_slots, y, ldy,
                          (int32_t)nrows);
     check_launch("spmv work");
+  });
+}
+
+extern "C" int fly_rest_forward(const int32_t *crow, const int32_t *pre, const float *w, int64_t n, int64_t nnz,
+                                const float *x2, const float *bias, const float *alpha, const float *c_prev,
+                                float h_max, const uint8_t *member, float *full, float *outside, float *c_next,
+                                float *x2_next, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(n >= 0 && n < (int64_t)1 << 28 && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
+    if (!n) return;
+    FLY_REQUIRE(crow && bias && alpha && full && outside && c_next && x2_next, "bad argument");
+    FLY_REQUIRE(!x2 || (nnz == 0 || (pre && w)), "bad argument");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    RestFwdArgs a{crow, pre, w, reinterpret_cast<const float2 *>(x2), bias, alpha, c_prev, member, full, outside,
+                  c_next, reinterpret_cast<float2 *>(x2_next), h_max, (int32_t)n, (int32_t)nnz,
+                  (uint32_t)(n * 8)};
+    hipLaunchKernelGGL(k_rest_fwd, dim3(blocks_for(n, 16)), dim3(256), 0, as_stream(stream), a);
+    check_launch("resting step");
+  });
+}
+
+extern "C" int fly_rest_backward(const float *gc, const int32_t *pos, const float *gk, const float *gp,
+                                 const float *full, const float *c_prev, const float *alpha, float h_max, int64_t n,
+                                 float *g2, float *gc_prev, float *gbias, float *galpha, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(n >= 0 && n < (int64_t)1 << 28, "size out of range");
+    if (!n) return;
+    FLY_REQUIRE(pos && full && alpha && g2 && gc_prev && gbias && galpha, "bad argument");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    RestBwdArgs a{gc, pos, gk, gp, full, c_prev, alpha, reinterpret_cast<float2 *>(g2), gc_prev, gbias, galpha,
+                  h_max, (int32_t)n};
+    hipLaunchKernelGGL(k_rest_bwd, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), a);
+    check_launch("resting step backward");
+  });
+}
+
+extern "C" int fly_rest_products_backward(const int32_t *crow, const int32_t *pre, int64_t n, int64_t nnz,
+                                          const float *g2, const float *x2, float *gw, const int32_t *t_rowptr,
+                                          const int32_t *t_col, const float *t_val, const uint8_t *member_prev,
+                                          const int32_t *items, int64_t n_items, const int32_t *splits,
+                                          int64_t n_splits, float *partials, int64_t n_slots, float *gc_prev,
+                                          void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(n >= 0 && n < (int64_t)1 << 28 && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
+    FLY_REQUIRE(n_items >= 0 && n_items < (int64_t)INT32_MAX && n_splits >= 0 && n_splits < (int64_t)INT32_MAX &&
+                n_slots >= 0 && n_slots < (int64_t)INT32_MAX, "work list out of range");
+    if (!n) return;
+    FLY_REQUIRE(crow && g2 && x2 && gw && t_rowptr && gc_prev && (n_items == 0 || items), "bad argument");
+    FLY_REQUIRE(nnz == 0 || (pre && t_col && t_val), "bad argument");
+    FLY_REQUIRE((n_splits == 0 || splits) && (n_slots == 0 || partials), "split rows need splits and partials");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    const uint32_t pair_bytes = (uint32_t)(n * 8);
+    hipLaunchKernelGGL(k_rest_sddmm, dim3(blocks_for(n, 16)), dim3(256), 0, st, crow, pre, (int32_t)n, (int32_t)nnz,
+                       reinterpret_cast<const float2 *>(g2), reinterpret_cast<const float2 *>(x2), pair_bytes, gw);
+    if (n_items) {
+      RestTArgs a{t_rowptr, t_col, t_val, reinterpret_cast<const float2 *>(g2), pair_bytes, member_prev, gc_prev,
+                  (int32_t)n, (int32_t)nnz, reinterpret_cast<const int4 *>(items), (int32_t)n_items,
+                  (int32_t)n_slots, partials};
+      hipLaunchKernelGGL(k_rest_spmv_t, dim3(blocks_for(n_items, 16)), dim3(256), 0, st, a);
+      if (n_splits)
+        hipLaunchKernelGGL(k_spmv_partials, dim3(blocks_for(n_splits, 256)), dim3(256), 0, st,
+                           reinterpret_cast<const int4 *>(splits), (int32_t)n_splits, partials, (int32_t)n_slots,
+                           gc_prev, (int64_t)1, (int32_t)n);
+    }
+    check_launch("resting products backward");
   });
 }
 

@@ -28,6 +28,8 @@
  *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass)
  *   fly_spmv_work         chessfly/brain.py:79-99 and :238-252 (grad_h = A^T grad_y of the resting trajectory's
  *                         one-column products, under autograd)
+ *   fly_rest_*            chessfly/brain.py:238-252 (_constants under autograd: the resting trajectory and the
+ *                         constant drives k_t, forward and backward)
  *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
  *                         gradients)
  */
@@ -201,6 +203,41 @@ int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val
 int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
               int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, int64_t n_out,
               const int32_t *ids_dev, int32_t accumulate, void *stream);
+
+/* The resting trajectory of training (chessfly/brain.py:238-252: the network with no position, one column) and
+ * the drive the rows of each light-cone step get from outside the cone, k_t = (W c_{t-1} + b -
+ * A_t c_{t-1}[R_{t-1}])[R_t], which is the sum over the edges whose presynaptic neuron lies outside R_{t-1}.
+ *
+ * fly_rest_forward, one step over W's CSR (crow, pre, w; rows are postsynaptic neurons, n of them):
+ *   full[i] = sum_e w_e x2[pre_e].x + bias[i], outside[i] = sum_e w_e x2[pre_e].y + bias[i],
+ *   c_next[i] = lerp(c_prev[i], clamp(full[i], 0, h_max), alpha[i]) (torch.lerp's formula),
+ *   x2_next[i] = {c_next[i], member[i] ? 0 : c_next[i]}  (the next step's pairs; member = this step's rows).
+ * x2 holds n float pairs {c_{t-1}, c_{t-1} outside R_{t-1}}, or NULL for the first step (c_0 = 0, no edge terms);
+ * c_prev NULL means 0; member NULL means no rows.  alpha = sigmoid(alpha_logit).
+ *
+ * fly_rest_backward, that step's elementwise gradients per neuron: from gc = dL/dc_t (NULL: 0), gk = dL/dk_t and
+ * gp = dL/dp_t with p_t = c_{t-1}[R_t] (|R_t| each, NULL: 0; pos[i] = i's place in R_t or -1), writes
+ * g2[i] = {dL/dfull_i, dL/doutside_i} and gc_prev = dL/dc_{t-1} through the lerp and p_t, and adds to gbias and
+ * galpha.
+ *
+ * fly_rest_products_backward, that step's products: gw[e] += g2[post_e] . x2[pre_e] over W, then
+ * gc_prev[j] += sum over row j of W^T of w_e (g2[i].x + (member_prev[j] ? 0 : g2[i].y)) over W^T's work list
+ * (t_rowptr / t_col / t_val, items / splits / partials as for fly_spmv_work; member_prev = R_{t-1}, NULL: none).
+ * Row pointers are clamped and pair reads bounded, so a malformed structure gives wrong results, never an access
+ * outside the arrays; n below 2^28. */
+int fly_rest_forward(const int32_t *crow_dev, const int32_t *pre_dev, const float *w_dev, int64_t n, int64_t nnz,
+                     const float *x2_dev, const float *bias_dev, const float *alpha_dev, const float *c_prev_dev,
+                     float h_max, const uint8_t *member_dev, float *full_dev, float *outside_dev, float *c_next_dev,
+                     float *x2_next_dev, void *stream);
+int fly_rest_backward(const float *gc_dev, const int32_t *pos_dev, const float *gk_dev, const float *gp_dev,
+                      const float *full_dev, const float *c_prev_dev, const float *alpha_dev, float h_max, int64_t n,
+                      float *g2_dev, float *gc_prev_dev, float *gbias_dev, float *galpha_dev, void *stream);
+int fly_rest_products_backward(const int32_t *crow_dev, const int32_t *pre_dev, int64_t n, int64_t nnz,
+                               const float *g2_dev, const float *x2_dev, float *gw_dev, const int32_t *t_rowptr_dev,
+                               const int32_t *t_col_dev, const float *t_val_dev, const uint8_t *member_prev_dev,
+                               const int32_t *items_dev, int64_t n_items, const int32_t *splits_dev,
+                               int64_t n_splits, float *partials_dev, int64_t n_slots, float *gc_prev_dev,
+                               void *stream);
 
 /* y (+)= A x for one column over a work list: items_dev (n_items, 4) int32 {row, first non-zero, count, slot}
  * cover every row, each row's segments in order (as chessfly.brain.backward_work builds them for a row
