@@ -69,6 +69,7 @@ SIGNATURES = {
                                        _p, _p, _p, _i64, _p, _i64, _p]),
     "fly_sddmm": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _i32, _p]),
     "fly_spmv_work": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p]),
+    "fly_gather_values": (_i32, [_p, _i64, _p, _i64, _p, _p]),
     "fly_rest_forward": (_i32, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _p, _p]),
     "fly_rest_backward": (_i32, [_p, _p, _p, _p, _p, _p, _p, _f32, _i64, _p, _p, _p, _p, _p]),
     "fly_rest_products_backward": (_i32, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64,

@@ -121,10 +121,17 @@ def _gathered(op, w: torch.Tensor, transposed: bool) -> torch.Tensor:
     if cached is not None and cached[0]() is w:
         return cached[1]
     if transposed:
-        vals = w[op._transposed()[2].long()] if op._edge_ids() is not None else w[op.t_order]
+        ids32 = op._transposed()[2]                  # the transpose's edge ids (W^T: its order in W)
     else:
         ids = op._edge_ids()
-        vals = w if ids is None else w[ids[1]]
+        ids32 = None if ids is None else ids[0]
+    if ids32 is None:
+        vals = w
+    else:
+        w = w.contiguous()
+        vals = torch.empty(ids32.numel(), dtype=torch.float32, device=w.device)
+        _hip.check(_hip.load().fly_gather_values(w.data_ptr(), w.numel(), ids32.data_ptr(), ids32.numel(),
+                                                 vals.data_ptr(), _hip.stream(w.device)), "fly_gather_values")
     setattr(op, slot, (weakref.ref(w), vals))
     return vals
 

@@ -774,6 +774,18 @@ __global__ __launch_bounds__(256) void k_rest_spmv_t(const RestTArgs a) {
     a.y[row] += acc;
 }
 
+// out[i] = w[ids[i]]: a sub-matrix's weights in its own (or its transpose's) order, from int32 ids in one pass;
+// ids past the weight vector read 0.
+__global__ __launch_bounds__(256) void k_gather_values(const float *__restrict__ w, uint32_t wbytes,
+                                                       const int32_t *__restrict__ ids, int64_t n,
+                                                       float *__restrict__ out) {
+  const __amdgpu_buffer_rsrc_t rw = buffer_of(w, wbytes);
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const uint32_t id = (uint32_t)ids[i];
+    out[i] = id < wbytes / 4u ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, (int)(id * 4u), 0, 0)) : 0.0f;
+  }
+}
+
 bool vec4_ok(const void *p, int64_t ld) { return ld % 4 == 0 && aligned(p, 16); }
 
 uint32_t checked_bytes(int64_t rows, int64_t ld) {
@@ -946,6 +958,20 @@ extern "C" int fly_rest_products_backward(const int32_t *crow, const int32_t *pr
                            gc_prev, (int64_t)1, (int32_t)n);
     }
     check_launch("resting products backward");
+  });
+}
+
+extern "C" int fly_gather_values(const float *w, int64_t n_w, const int32_t *ids, int64_t n, float *out,
+                                 void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(n_w >= 0 && n_w < (int64_t)1 << 29 && n >= 0 && n < (int64_t)1 << 40, "size out of range");
+    if (!n) return;
+    FLY_REQUIRE(ids && out && (n_w == 0 || w), "bad argument");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    const int64_t blocks = std::min<int64_t>(blocks_for(n, 256), 65536);
+    hipLaunchKernelGGL(k_gather_values, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), w,
+                       (uint32_t)(n_w * 4), ids, n, out);
+    check_launch("gather values");
   });
 }
 

@@ -30,6 +30,7 @@
  *                         one-column products, under autograd)
  *   fly_rest_*            chessfly/brain.py:238-252 (_constants under autograd: the resting trajectory and the
  *                         constant drives k_t, forward and backward)
+ *   fly_gather_values     chessfly/brain.py:123, 208, 248, 293 (w[op.edges], w[t_order]: a sub-matrix's values)
  *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
  *                         gradients)
  */
@@ -203,6 +204,11 @@ int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val
 int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
               int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, int64_t n_out,
               const int32_t *ids_dev, int32_t accumulate, void *stream);
+
+/* out[i] = w[ids[i]] for i < n (a sub-matrix's values in its own or its transpose's order); ids at or past n_w
+ * read 0.  n_w below 2^29. */
+int fly_gather_values(const float *w_dev, int64_t n_w, const int32_t *ids_dev, int64_t n, float *out_dev,
+                      void *stream);
 
 /* The resting trajectory of training (chessfly/brain.py:238-252: the network with no position, one column) and
  * the drive the rows of each light-cone step get from outside the cone, k_t = (W c_{t-1} + b -

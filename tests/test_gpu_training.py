@@ -190,6 +190,24 @@ def test_one_column_product_over_a_work_list_matches_float64(heavy, seg, accumul
     _close(y, torch.as_tensor(want), 1e-5, "spmv over the work list")
 
 
+def test_gather_values_reads_the_weight_vector_at_int32_ids():
+    """fly_gather_values: out[i] = w[ids[i]] (a sub-matrix's values in its own or its transpose's order), ids past
+    the vector (and negative ones) read 0, bit for bit."""
+    from chessfly import _hip
+    lib = _hip.load()
+    g = torch.Generator(device=DEV).manual_seed(4)
+    w = torch.randn(100_003, device=DEV, generator=g)
+    ids = torch.randint(0, w.numel(), (300_001,), device=DEV, generator=g, dtype=torch.int32)
+    ids[::97] = w.numel()
+    ids[5::101] = -3
+    out = torch.full((ids.numel(),), float("nan"), device=DEV)
+    _hip.check(lib.fly_gather_values(w.data_ptr(), w.numel(), ids.data_ptr(), ids.numel(), out.data_ptr(),
+                                     _hip.stream(torch.device(DEV))), "fly_gather_values")
+    ok = (ids >= 0) & (ids < w.numel())
+    want = torch.where(ok, w[ids.clamp(0, w.numel() - 1).long()], torch.zeros(()).to(DEV))
+    assert torch.equal(out, want)
+
+
 def _rnn_pair(conn, seed: int, scale: float = 3.0):
     from chessfly.brain import ConnectomeRNN
     lg, bias, al = random_params(conn, seed)
