@@ -119,7 +119,11 @@ struct Split {
   const int32_t *flag;   // per row: lo is non-zero somewhere (null: assume it is)
 };
 
+// u[m, n] = (C[m, n] + bias[m]) * gain.  The tile is staged through LDS and written as whole rows (kRows):
+// per element, a wave's stores covered four 64-byte pieces of four rows, and the encoder's 80 MB output took a
+// quarter of its time.
 struct EncoderEpilogue {
+  static constexpr bool kRows = true;
   const float *bias;
   float gain;
   float *u;
@@ -130,13 +134,30 @@ struct EncoderEpilogue {
     if (u16) u16[m * ldu + n] = static_cast<_Float16>(x);
     else u[m * ldu + n] = x;
   }
+  // columns n .. n + 3 of row m (avail of them inside the output); 16-byte stores when the row allows them
+  __device__ __forceinline__ void row4(int64_t m, int64_t n, float4 v, int64_t avail) const {
+    const float b = bias[m];
+    const float x[4] = {(v.x + b) * gain, (v.y + b) * gain, (v.z + b) * gain, (v.w + b) * gain};
+    if (!u16 && avail >= 4 && (reinterpret_cast<uintptr_t>(u + m * ldu + n) & 15) == 0) {
+      *reinterpret_cast<float4 *>(u + m * ldu + n) = make_float4(x[0], x[1], x[2], x[3]);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < avail) {
+        if (u16) u16[m * ldu + n + i] = static_cast<_Float16>(x[i]);
+        else u[m * ldu + n + i] = x[i];
+      }
+  }
 };
 
-// ct[n, m] = C[m, n]: one row of all head outputs per board.
+// ct[n, m] = C[m, n]: one row of all head outputs per board (measured: its element stores cost about 4 us).
 struct HeadEpilogue {
+  static constexpr bool kRows = false;
   float *ct;
   int64_t ldc;
   __device__ __forceinline__ void operator()(int64_t m, int64_t n, float v) const { ct[n * ldc + m] = v; }
+  __device__ __forceinline__ void row4(int64_t, int64_t, float4, int64_t) const {}
 };
 
 __device__ __forceinline__ half8 load8(const _Float16 *p) { return *reinterpret_cast<const half8 *>(p); }
@@ -233,23 +254,49 @@ __device__ __forceinline__ void gemm_tile(const Split &A, const Split &B, int64_
     }
     __syncthreads();
   }
+  if constexpr (EP::kRows) {
+    // The operand stages are free after the last barrier: C goes through them, rows padded by 4 floats, and
+    // leaves as 16-byte pieces of whole rows (a wave writes two 512-byte rows per store at 128 columns).
+    constexpr int LDC = 32 * TN + 4, V4 = 32 * TN / 4;
+    static_assert(32 * TM * LDC * sizeof(float) <= sizeof(_Float16) * 2 * LDK * 32 * (TM + TN),
+                  "the C tile fits the operand stages");
+    float *Cs = reinterpret_cast<float *>(&As[0][0][0]);
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + r;
-        const int64_t n = n0 + wn * 16 * TN + j * 16 + (lane & 15);
-        if (m < A.rows && n < B.rows) ep(m, n, acc[i][j][r] * unscale);
-      }
+        for (int r = 0; r < 4; ++r)
+          Cs[(wm * 16 * TM + i * 16 + 4 * (lane >> 4) + r) * LDC + wn * 16 * TN + j * 16 + (lane & 15)] =
+              acc[i][j][r] * unscale;
+    __syncthreads();
+    for (int idx = tid; idx < 32 * TM * V4; idx += 256) {
+      const int rr = idx / V4, c4 = idx - rr * V4;
+      const int64_t m = m0 + rr, n = n0 + 4 * c4;
+      if (m < A.rows && n < B.rows)
+        ep.row4(m, n, *reinterpret_cast<const float4 *>(&Cs[rr * LDC + 4 * c4]), B.rows - n);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + r;
+          const int64_t n = n0 + wn * 16 * TN + j * 16 + (lane & 15);
+          if (m < A.rows && n < B.rows) ep(m, n, acc[i][j][r] * unscale);
+        }
+  }
 }
 
 template <int TM, int TN, class EP>
 __global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B, int64_t kp, float unscale, const EP ep,
                                                     int tiles, int gx) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][32 * TM][LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][32 * TN][LDK];
+  // one block of LDS for both operands' stages (and, after the K loop, the C tile of a row-wise epilogue)
+  __shared__ __attribute__((aligned(16))) _Float16 smem[2 * LDK * 32 * (TM + TN)];
+  auto As = reinterpret_cast<_Float16 (*)[32 * TM][LDK]>(smem);
+  auto Bs = reinterpret_cast<_Float16 (*)[32 * TN][LDK]>(smem + 2 * LDK * 32 * TM);
   int ty, tx;
   xcd_tile(tiles, gx, ty, tx);
   const int64_t m0 = (int64_t)ty * (32 * TM), n0 = (int64_t)tx * (32 * TN);

@@ -297,6 +297,7 @@ def test_encoder_and_head_gemms_match_fp64(batch, n_in, k, ld, n_out, moves, gem
         got = u[:, :batch].double().cpu()
         tol = ref.abs() * (2 ** -10) + 1e-6 if f16 else ref.abs() * 2e-6 + 2e-6
         assert bool(((got - ref).abs() <= tol).all()), float((got - ref).abs().max())
+        assert bool((u[:, batch:] == 0).all())             # the padding columns past the batch stay untouched
     # Half-precision boards (what the search sends) widen exactly: the same bits as their float32 copy.
     xh = x.half().to(DEV)
     u_h, u_f = (torch.zeros(n_in, batch, device=DEV) for _ in range(2))
