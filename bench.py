@@ -336,7 +336,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         msg = (f"bench.py measures one GPU: the evaluator shards by board across GPUs with no collective on the "
-               f"critical path, and this build runs on a single MI355X only (asked for --gpus {args.gpus}, "
+               f"critical path, and this evaluator runs on a single MI355X only (asked for --gpus {args.gpus}, "
                f"WORLD_SIZE {world})")
         print(msg, file=sys.stderr)
         print(msg)

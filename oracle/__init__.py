@@ -1,6 +1,6 @@
 """CPU restatement of the reference's forward evaluator.  TEST INFRASTRUCTURE ONLY.
 
-This package is the checker, never the thing measured or shipped: only `tests/`,
+This package checks results and is never the thing measured or shipped: only `tests/`,
 `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it.  The product
 (`alpha-fly_amd/chessfly` over the HIP library) must never call into it.
 
