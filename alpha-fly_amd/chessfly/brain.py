@@ -128,9 +128,9 @@ def _gathered(op, w: torch.Tensor, transposed: bool) -> torch.Tensor:
     if ids32 is None:
         vals = w
     else:
-        w = w.contiguous()
+        src = w.contiguous()
         vals = torch.empty(ids32.numel(), dtype=torch.float32, device=w.device)
-        _hip.check(_hip.load().fly_gather_values(w.data_ptr(), w.numel(), ids32.data_ptr(), ids32.numel(),
+        _hip.check(_hip.load().fly_gather_values(src.data_ptr(), src.numel(), ids32.data_ptr(), ids32.numel(),
                                                  vals.data_ptr(), _hip.stream(w.device)), "fly_gather_values")
     setattr(op, slot, (weakref.ref(w), vals))
     return vals

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kScanThreads) void k_tile_flags(const uint8_t *__re
   const int64_t base = tile_base();
   int32_t c = 0;
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) c += (base + k < n && (a[base + k] & b[base + k])) ? 1 : 0;
+  for (int k = 0; k < kPer; ++k) c += (base + k < n && a[base + k] && b[base + k]) ? 1 : 0;
   const int32_t incl = block_inclusive_scan(c, part);
   if (threadIdx.x == kScanThreads - 1) tile_sum[blockIdx.x] = incl;
 }
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kScanThreads) void k_tile_compact(const uint8_t *__
   const int64_t base = tile_base();
   int32_t c = 0;
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) c += (base + k < n && (a[base + k] & b[base + k])) ? 1 : 0;
+  for (int k = 0; k < kPer; ++k) c += (base + k < n && a[base + k] && b[base + k]) ? 1 : 0;
   const int32_t incl = block_inclusive_scan(c, part);
   int32_t run = tile_off[blockIdx.x] + incl - c;
 #pragma unroll
