@@ -26,6 +26,7 @@ device; nothing here falls back to the CPU.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 from torch import nn
@@ -111,27 +112,34 @@ def _take_rows(x: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
     return _TakeRows.apply(x, rows) if torch.is_grad_enabled() and x.requires_grad else x.index_select(0, rows)
 
 
-def _gathered(op, w: torch.Tensor, transposed: bool) -> torch.Tensor:
+def _take(src: torch.Tensor, ids32: torch.Tensor) -> torch.Tensor:
+    """src[ids32] for a float32 vector on the device (fly_gather_values)."""
+    src = src.contiguous()
+    out = torch.empty(ids32.numel(), dtype=torch.float32, device=src.device)
+    _hip.check(_hip.load().fly_gather_values(src.data_ptr(), src.numel(), ids32.data_ptr(), ids32.numel(),
+                                             out.data_ptr(), _hip.stream(src.device)), "fly_gather_values")
+    return out
+
+
+def _gathered(op, w: torch.Tensor, transposed: bool, via: tuple | None = None) -> torch.Tensor:
     """op's values taken from the whole weight vector w, in CSR order or in the transposed structure's order,
     gathered once per weight tensor: the forward, its backward and the resting trajectory's products share
-    them."""
-    import weakref
+    them.  `via` = (src, ids32) names the same values as src[ids32]: a sub-matrix's transposed values read
+    from w in W^T's order, where its ids rise, instead of from w at random."""
     slot = "_vals_t" if transposed else "_vals"
     cached = getattr(op, slot, None)
     if cached is not None and cached[0]() is w:
         return cached[1]
+    if via is not None:
+        vals = _take(*via)
+        setattr(op, slot, (weakref.ref(w), vals))
+        return vals
     if transposed:
         ids32 = op._transposed()[2]                  # the transpose's edge ids (W^T: its order in W)
     else:
         ids = op._edge_ids()
         ids32 = None if ids is None else ids[0]
-    if ids32 is None:
-        vals = w
-    else:
-        src = w.contiguous()
-        vals = torch.empty(ids32.numel(), dtype=torch.float32, device=w.device)
-        _hip.check(_hip.load().fly_gather_values(src.data_ptr(), src.numel(), ids32.data_ptr(), ids32.numel(),
-                                                 vals.data_ptr(), _hip.stream(w.device)), "fly_gather_values")
+    vals = w if ids32 is None else _take(w, ids32)
     setattr(op, slot, (weakref.ref(w), vals))
     return vals
 
@@ -184,12 +192,15 @@ class _ConeRecurrence(torch.autograd.Function):
     The backward runs per step one fused kernel for the gradients of those (fly_train_step_backward), then
     one pass over A_t^T (fly_transposed_backward, from the sub-matrix's longest-first work list) that adds the
     state gradient A_t^T grad_y to the carried rows' share and writes the per-synapse gradient straight into
-    dL/dw at the edge ids; batches that are not a multiple of 4 take fly_spmm and fly_sddmm instead.  Inputs
-    after u_in and w, per step t: k_t, the previous resting state c_{t-1}[R_t] and alpha[R_t] (each
-    (|R_t|, 1)).  Returns h_T, (|R_T|, B)."""
+    dL/dw (chunk-major above 64 columns, so the gathers share one chunk of grad_y in the caches); batches that
+    are not a multiple of 4 take fly_spmm and fly_sddmm instead.  The transposed passes work in the transposed
+    order of the whole weight vector (rnn's W^T), where every step's ids rise along the pass: they read A_t^T's
+    values from w in that order and add into dL/dw kept in that order, which one gather at the end puts back
+    in the weight vector's order.  Inputs after u_in and w, per step t: k_t, the previous resting state
+    c_{t-1}[R_t] and alpha[R_t] (each (|R_t|, 1)).  Returns h_T, (|R_T|, B)."""
 
     @staticmethod
-    def forward(ctx, cone, h_max, u_in, w, *flat):
+    def forward(ctx, cone, h_max, rnn, u_in, w, *flat):
         lib = _hip.load()
         dev = u_in.device
         st = _hip.stream(dev)
@@ -218,7 +229,7 @@ class _ConeRecurrence(torch.autograd.Function):
             hs.append(hn)
             ys.append(y)
             h = hn
-        ctx.cone, ctx.h_max = cone, float(h_max)
+        ctx.cone, ctx.h_max, ctx.rnn = cone, float(h_max), rnn
         ctx.save_for_backward(u_in, w, *hs, *ys, *flat)
         return h
 
@@ -237,6 +248,7 @@ class _ConeRecurrence(torch.autograd.Function):
         g = grad_h.contiguous()
         gu = torch.zeros_like(u_in)
         gw = torch.zeros_like(w)
+        gw_t = w_pos32 = None                         # dL/dw in W^T's order, for the transposed passes
         grads = [None] * len(flat)
         for t in range(T, 0, -1):
             k, pdef, alpha = flat[3 * (t - 1):3 * t]
@@ -260,22 +272,34 @@ class _ConeRecurrence(torch.autograd.Function):
             if op is not None:
                 crow32, col32, n_rows, n_cols = op._structure()
                 if batch % 4 == 0:          # one pass over A^T: the state gradient and dL/dw together
-                    t_crow32, t_col32, t_ids32 = op._transposed()
-                    vals_t = _gathered(op, w, True)
+                    t_crow32, t_col32, _ = op._transposed()
+                    if w_pos32 is None:
+                        w_pos32 = ctx.rnn._transposed_positions()
+                        w_t = _gathered(ctx.rnn, w, True)     # shared with the resting trajectory's backward
+                    wt_ids32 = op._whole_transposed_ids(w_pos32)
+                    vals_t = _gathered(op, w, True, via=(w_t, wt_ids32))
                     items, splits, n_slots = op._backward_work()
                     partials = torch.empty(n_slots, ld, dtype=torch.float32, device=dev) if n_slots else None
+                    # more than one 64-column chunk: chunk-major, each chunk's dot products kept in a workspace
+                    chunks = (batch + 63) // 64
+                    dots = torch.empty(chunks * wt_ids32.numel(), dtype=torch.float32, device=dev) \
+                        if chunks > 1 else None
+                    if gw_t is None:
+                        gw_t = torch.zeros_like(w)
                     _hip.check(lib.fly_transposed_backward(
-                        t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(), t_ids32.data_ptr(),
-                        t_ids32.numel(), n_cols, n_rows, gy.data_ptr(), ld, h_prev.data_ptr(), ld, batch,
-                        gh_prev.data_ptr(), ld, 1, gw.data_ptr(), gw.numel(), items.data_ptr(), items.shape[0],
-                        splits.data_ptr(), splits.shape[0], _hip.ptr(partials), n_slots, st),
-                        "fly_transposed_backward")
+                        t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(), wt_ids32.data_ptr(),
+                        wt_ids32.numel(), n_cols, n_rows, gy.data_ptr(), ld, h_prev.data_ptr(), ld, batch,
+                        gh_prev.data_ptr(), ld, 1, gw_t.data_ptr(), gw_t.numel(), items.data_ptr(), items.shape[0],
+                        splits.data_ptr(), splits.shape[0], _hip.ptr(partials), n_slots, _hip.ptr(dots),
+                        dots.numel() if dots is not None else 0, st), "fly_transposed_backward")
                 else:
                     _product(op, w, gy, transposed=True, out=gh_prev)
                     ids32, ids = op._edge_ids()
                     _sddmm(crow32, col32, n_rows, n_cols, gy, h_prev, len(ids), out=gw, ids32=ids32)
             g = gh_prev
-        return (None, None, gu, gw, *grads)
+        if gw_t is not None:                          # back to the weight vector's order: gw[i] += gw_t[pos[i]]
+            gw += _take(gw_t, w_pos32)
+        return (None, None, None, gu, gw, *grads)
 
 
 class _RestingTrajectory(torch.autograd.Function):
@@ -439,6 +463,17 @@ class _SubMatrix:
             self._transposed()
             self._tw = backward_work(self._tr[3])
         return self._tw
+
+    def _whole_transposed_ids(self, w_pos32: torch.Tensor) -> torch.Tensor:
+        """int32: each non-zero of A^T (in its order) as a position in the transposed order of the whole
+        weight vector, from w_pos32 = each edge's position in that order.  Rows and columns keep their
+        relative order in the sub-matrix, so A^T's order is a subsequence of W^T's and these ids rise along
+        the transposed backward.  Cached per w_pos32."""
+        cached = getattr(self, "_wt_ids", None)
+        if cached is None or cached[0]() is not w_pos32:
+            ids = w_pos32[self._transposed()[2].long()]
+            self._wt_ids = cached = (weakref.ref(w_pos32), ids)
+        return cached[1]
 
     @property
     def t_order(self) -> torch.Tensor:
@@ -706,6 +741,16 @@ class ConnectomeRNN(nn.Module):
             self._t_order32 = self.t_order.to(torch.int32)
         return self.t_crow32, self.t_col32, self._t_order32
 
+    def _transposed_positions(self) -> torch.Tensor:
+        """int32 (E,): each edge's position in the transposed order (the inverse of t_order), built on first
+        use."""
+        cached = getattr(self, "_t_pos32", None)
+        if cached is None or cached.device != self.t_order.device:
+            pos = torch.empty_like(self.t_order)
+            pos[self.t_order] = torch.arange(self.t_order.numel(), device=self.t_order.device)
+            self._t_pos32 = cached = pos.to(torch.int32)
+        return cached
+
     def _edge_ids(self):
         return None
 
@@ -796,7 +841,7 @@ class ConnectomeRNN(nn.Module):
         flat = []
         for t in range(1, steps + 1):
             flat += [rest[t - 1], rest[steps + t - 1], _take_rows(alpha, cone.rows[t])]
-        h = _ConeRecurrence.apply(cone, self.h_max, u_in, w, *flat)
+        h = _ConeRecurrence.apply(cone, self.h_max, self, u_in, w, *flat)
         out = rest[2 * steps].expand(-1, batch)
         return out.index_copy(0, cone.out_pos, _take_rows(h, cone.out_src))
 

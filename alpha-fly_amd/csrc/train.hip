@@ -572,6 +572,115 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
   }
 }
 
+// The same pass in chunk-major order, for batches of more than one 64-column chunk: wave w takes chunk
+// w / units of unit w % units (a work-list item, or row j without one), so the waves of one chunk run together
+// and their gathers share that chunk's slice of grad_y (rows x 256 B) in L2 and the Infinity Cache instead of
+// the whole of grad_y.  grad_h is written per chunk exactly as above.  Each non-zero's dot over the chunk's 64
+// columns goes to dots[chunk * nnz + e] in one coalesced store per block (lane (g, s) holds the sum of round
+// s), and k_dots_to_gw adds the chunks in order into gw[ids[e]].
+__global__ __launch_bounds__(256) void k_transposed_backward_chunks(const TransposedArgs a, float *__restrict__ dots) {
+  constexpr int R = 16;
+  const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t units = a.items != nullptr ? (uint32_t)a.n_items : (uint32_t)a.nrows;   // > 0 (host)
+  const int32_t chunks = (a.batch + 63) / 64;
+  const uint32_t ch = wave / units, unit = wave - ch * units;
+  if (ch >= (uint32_t)chunks) return;
+  uint32_t j = unit;
+  int32_t first_nz = 0, count = INT32_MAX, slot = -1;
+  if (a.items != nullptr) {
+    const int4 it = a.items[unit];
+    j = (uint32_t)it.x;
+    first_nz = it.y;
+    count = it.z;
+    slot = it.w;
+    if (slot >= a.n_slots) return;
+  }
+  if (j >= (uint32_t)a.nrows) return;
+  const int lane = threadIdx.x & 63, g = lane >> 4, s = lane & 15;
+  const int32_t row_beg = min(max(a.t_rowptr[j], 0), a.nnz);
+  const int32_t row_end = min(max(a.t_rowptr[j + 1], row_beg), a.nnz);
+  const int32_t beg = row_beg + min(max(first_nz, 0), row_end - row_beg);
+  const int32_t n = min(max(count, 0), row_end - beg);
+  const __amdgpu_buffer_rsrc_t rc = buffer_of(a.t_col + beg, (uint32_t)n * 4u);
+  const __amdgpu_buffer_rsrc_t rv = buffer_of(a.vals + beg, (uint32_t)n * 4u);
+  const __amdgpu_buffer_rsrc_t rgy = buffer_of(a.gy, a.gybytes);
+  const uint32_t gy_row = (uint32_t)a.ldgy * 4u;
+  const int32_t col0 = (int32_t)ch * 64 + s * 4;
+  const bool live = col0 < a.batch;        // the batch is a multiple of 4 on this path
+  float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (live) hv = *reinterpret_cast<const float4 *>(a.h + (int64_t)j * a.ldh + col0);
+  float *ghj = slot < 0 ? a.gh + (int64_t)j * a.ldgh : a.partials + (int64_t)slot * a.ldgh;
+  float *drow = dots + (int64_t)ch * a.nnz + beg;   // this unit's non-zeros, [0, n), in chunk ch
+  const bool add = slot < 0 && a.accumulate;
+  bool first = true;
+  for (int32_t blk = 0; blk < n || (blk == 0 && !add); blk += 64) {
+    int32_t c[R];
+    float w[R], dot[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {          // past the segment's end: column 0, weight 0
+      const int off = (blk + 4 * r + g) * 4;
+      c[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
+      w[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      dot[r] = 0.0f;
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r0 = 0; r0 < R; r0 += 4) {
+      float4 x[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(
+            rgy, (int)(__umul24((uint32_t)c[r0 + q], gy_row) + (uint32_t)col0 * 4u), 0, 0);
+        x[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float wq = w[r0 + q];
+        acc[0] = fmaf(wq, x[q].x, acc[0]);
+        acc[1] = fmaf(wq, x[q].y, acc[1]);
+        acc[2] = fmaf(wq, x[q].z, acc[2]);
+        acc[3] = fmaf(wq, x[q].w, acc[3]);
+        dot[r0 + q] = fmaf(x[q].x, hv.x, fmaf(x[q].y, hv.y, fmaf(x[q].z, hv.z, fmaf(x[q].w, hv.w, dot[r0 + q]))));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = group_sum<16>(acc[i]);
+    if (g == 0 && live) {
+      float4 *dst = reinterpret_cast<float4 *>(ghj + col0);
+      float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      if (add || !first) {
+        const float4 o = *dst;
+        v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+      }
+      *dst = v;
+    }
+    first = false;
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float d = row16_sum(dot[r]);
+      mine = s == r ? d : mine;
+    }
+    const int32_t e = blk + 4 * s + g;
+    if (e < n) drow[e] = mine;
+  }
+}
+
+// gw[ids[e]] += dots[0][e] + dots[1][e] + ... (chunks in order), one thread per non-zero; ids distinct, ids at or
+// past n_w skipped.  With gw kept in the transposed order of the whole weight vector the ids rise with e and
+// dL/dw streams.
+__global__ __launch_bounds__(256) void k_dots_to_gw(const float *__restrict__ dots, int32_t nnz, int32_t chunks,
+                                                    const int32_t *__restrict__ ids, uint32_t n_w,
+                                                    float *__restrict__ gw) {
+  const int32_t e = (int32_t)(blockIdx.x * 256u + threadIdx.x);
+  if (e >= nnz) return;
+  float d = dots[e];
+  for (int32_t c = 1; c < chunks; ++c) d += dots[(int64_t)c * nnz + e];
+  const uint32_t id = (uint32_t)ids[e];
+  if (id < n_w) gw[id] += d;
+}
+
 // grad_h[row] += partials[slot_beg .. slot_beg + count) in slot order, one wave per split row
 // ({row, slot_beg, count, unused} per entry); batch a multiple of 4, rows 16-byte aligned.
 __global__ __launch_bounds__(256) void k_add_partials(const int4 *__restrict__ splits, int32_t n_splits,
@@ -1030,7 +1139,8 @@ extern "C" int fly_transposed_backward(const int32_t *t_rowptr, const int32_t *t
                                        const float *gy, int64_t ldgy, const float *h, int64_t ldh, int64_t batch,
                                        float *gh, int64_t ldgh, int32_t accumulate, float *gw, int64_t n_w,
                                        const int32_t *items, int64_t n_items, const int32_t *splits,
-                                       int64_t n_splits, float *partials, int64_t n_slots, void *stream) {
+                                       int64_t n_splits, float *partials, int64_t n_slots, float *dots,
+                                       int64_t n_dots, void *stream) {
   return guard([&] {
     FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0, "negative size");
     FLY_REQUIRE(nrows < (int64_t)1 << 24 && ncols < (int64_t)1 << 24, "more than 2^24 rows or columns");
@@ -1051,9 +1161,24 @@ extern "C" int fly_transposed_backward(const int32_t *t_rowptr, const int32_t *t
                      ncols ? checked_bytes(ncols, ldgy) : 0u, (int32_t)nrows, (int32_t)batch, accumulate != 0,
                      (int32_t)nnz, (uint32_t)n_w, reinterpret_cast<const int4 *>(items),
                      items ? (int32_t)n_items : 0, items ? (int32_t)n_slots : 0, partials};
-    const int64_t waves = items ? n_items : nrows;
-    hipLaunchKernelGGL(k_transposed_backward, dim3(blocks_for(waves, 4)), dim3(256), 0, as_stream(stream), a);
-    check_launch("transposed backward");
+    const int64_t units = items ? n_items : nrows, chunks = (batch + 63) / 64;
+    if (dots) {
+      FLY_REQUIRE(n_dots >= chunks * nnz, "dots must hold ceil(batch / 64) * nnz floats");
+      FLY_REQUIRE(units * chunks < (int64_t)1 << 31, "chunk-major grid too large");
+    }
+    if (dots && units) {
+      hipLaunchKernelGGL(k_transposed_backward_chunks, dim3(blocks_for(units * chunks, 4)), dim3(256), 0,
+                         as_stream(stream), a, dots);
+      check_launch("transposed backward (chunks)");
+      if (nnz) {
+        hipLaunchKernelGGL(k_dots_to_gw, dim3(blocks_for(nnz, 256)), dim3(256), 0, as_stream(stream), dots,
+                           (int32_t)nnz, (int32_t)chunks, ids, (uint32_t)n_w, gw);
+        check_launch("dots to gw");
+      }
+    } else if (units) {
+      hipLaunchKernelGGL(k_transposed_backward, dim3(blocks_for(units, 4)), dim3(256), 0, as_stream(stream), a);
+      check_launch("transposed backward");
+    }
     if (items && n_splits > 0) {
       hipLaunchKernelGGL(k_add_partials, dim3(blocks_for(n_splits, 4)), dim3(256), 0, as_stream(stream),
                          reinterpret_cast<const int4 *>(splits), (int32_t)n_splits, partials, (int32_t)n_slots, gh,

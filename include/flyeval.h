@@ -272,14 +272,24 @@ int fly_spmv_work(const int32_t *rowptr_dev, const int32_t *col_dev, const float
  * gh[row] to partials (n_slots, ldgh), and splits (n_splits quadruples {row, first slot, slot count, unused})
  * then adds each split row's slots to gh[row] in slot order.  Long rows of A^T can so run on several waves at
  * once with deterministic sums; the list's order is the waves' order (longest first keeps the tail short).
- * Items and splits are clamped like the row pointers.  Replaces _SparseRecurrent.backward (brain.py:79-99),
- * whose grad_h is a cuSPARSE SpMM over W^T and whose grad_w a column-blocked SDDMM. */
+ * Items and splits are clamped like the row pointers.
+ *
+ * dots (NULL: one fused pass) is a workspace of n_dots >= ceil(batch / 64) * nnz floats.  With it the pass
+ * runs chunk-major: every wave of one 64-column chunk of gy runs before the next chunk's, so the gathers share
+ * that chunk's slice of gy in the caches.  Each non-zero's dot over a chunk is stored in dots, and a second
+ * kernel adds the chunks in order into gw[ids[e]]; results stay deterministic.  Worth it for batches of more
+ * than 64 columns.
+ *
+ * Either way gw is updated in A^T's order.  A caller that keeps gw in the transposed order of the whole
+ * weight vector, with ids = each non-zero's position in that order, has ids that rise along the pass, so the
+ * updates of gw stream instead of landing on random lines.  Replaces _SparseRecurrent.backward
+ * (brain.py:79-99), whose grad_h is a cuSPARSE SpMM over W^T and whose grad_w a column-blocked SDDMM. */
 int fly_transposed_backward(const int32_t *t_rowptr_dev, const int32_t *t_col_dev, const float *vals_dev,
                             const int32_t *ids_dev, int64_t nnz, int64_t nrows, int64_t ncols, const float *gy_dev,
                             int64_t ldgy, const float *h_dev, int64_t ldh, int64_t batch, float *gh_dev,
                             int64_t ldgh, int32_t accumulate, float *gw_dev, int64_t n_w, const int32_t *items_dev,
                             int64_t n_items, const int32_t *splits_dev, int64_t n_splits, float *partials_dev,
-                            int64_t n_slots, void *stream);
+                            int64_t n_slots, float *dots_dev, int64_t n_dots, void *stream);
 
 /* One recurrent step of training, the elementwise parts fused (brain.py:313-327 under autograd), float32,
  * one row of R_t per wave; rows are (rows, batch) with leading dimensions ld*:

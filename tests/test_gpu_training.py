@@ -106,13 +106,17 @@ def test_spmm_and_sddmm_match_float64(batch, ld_pad, heavy):
     _close(big, want, 1e-5, "sddmm scattered")
 
 
-@pytest.mark.parametrize("batch,heavy,seg", [(4, False, None), (64, False, None), (200, False, None),
-                                             (256, False, None), (64, False, 64), (256, True, None), (256, True, 256),
-                                             (4, True, 64), (200, True, 128)])
-def test_transposed_backward_matches_float64(batch, heavy, seg):
+@pytest.mark.parametrize("batch,heavy,seg,chunked", [
+    (4, False, None, False), (64, False, None, False), (200, False, None, False), (256, False, None, False),
+    (64, False, 64, False), (256, True, None, False), (256, True, 256, False), (4, True, 64, False),
+    (200, True, 128, False),
+    (4, False, None, True), (200, False, None, True), (256, True, None, True), (256, True, 256, True),
+    (64, False, 64, True), (200, True, 128, True), (328, True, 64, True)])
+def test_transposed_backward_matches_float64(batch, heavy, seg, chunked):
     """fly_transposed_backward: grad_h (+)= A^T g and gw[ids[e]] += sum_b g[row_e, b] h[col_e, b] in one pass,
     against float64, on a matrix with rows of A^T longer than one block of 64 non-zeros and empty ones; with a
-    work list (seg: segment length) long rows run as several segments whose shares meet in slot order."""
+    work list (seg: segment length) long rows run as several segments whose shares meet in slot order.  Chunked:
+    the chunk-major pass with its dots workspace (a ragged last chunk at 200 and 328 columns)."""
     from chessfly import _hip
     from chessfly.brain import backward_work
     lib = _hip.load()
@@ -147,11 +151,13 @@ def test_transposed_backward_matches_float64(batch, heavy, seg):
         n_items, n_splits = items.shape[0], splits.shape[0]
         partials = torch.full((n_slots, batch), float("nan"), device=DEV)   # every slot is written before use
         assert n_slots > 0 or not heavy
+    # every (chunk, non-zero) dot is written before k_dots_to_gw reads it
+    dots = torch.full(((batch + 63) // 64 * nnz,), float("nan"), device=DEV) if chunked else None
     _hip.check(lib.fly_transposed_backward(t_crow_d.data_ptr(), t_col_d.data_ptr(), t_val_d.data_ptr(),
                                            t_ids_d.data_ptr(), nnz, cols, rows, g_d.data_ptr(), batch, h_d.data_ptr(),
                                            batch, batch, gh.data_ptr(), batch, 1, gw.data_ptr(), gw.numel(),
                                            _hip.ptr(items), n_items, _hip.ptr(splits), n_splits, _hip.ptr(partials),
-                                           n_slots, st),
+                                           n_slots, _hip.ptr(dots), dots.numel() if chunked else 0, st),
                "fly_transposed_backward")
     dense = np.zeros((rows, cols))
     np.add.at(dense, (r, c), val)
