@@ -512,14 +512,21 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
   const bool add = slot < 0 && a.accumulate;   // a later segment's share starts from zero
   bool first = true;
   for (int32_t blk = 0; blk < n || (blk == 0 && !add); blk += 64) {
+    // wave-uniform: the groups of 16 non-zeros wholly past the row's end are neither loaded nor gathered;
+    // inside the last group the slots past the end read column 0 with weight 0 (no share of grad_h)
+    const int32_t groups = min(max(n - blk, 0) + 15, R * 4) / 16;
     int32_t c[R];
     float w[R], dot[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {          // past the row's end: column 0, weight 0 (no share of grad_h)
-      const int off = (blk + 4 * r + g) * 4;
-      c[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
-      w[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+    for (int r = 0; r < R; ++r) {
+      c[r] = 0;
+      w[r] = 0.0f;
       dot[r] = 0.0f;
+      if (r / 4 < groups) {
+        const int off = (blk + 4 * r + g) * 4;
+        c[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
+        w[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      }
     }
     for (int32_t ch = 0; ch < chunks; ++ch) {
       const int32_t col0 = ch * 64 + s * 4;
@@ -529,6 +536,7 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int r0 = 0; r0 < R; r0 += 4) {
+        if (r0 / 4 >= groups) break;
         float4 x[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -562,6 +570,7 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
     first = false;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+      if (r / 4 >= groups) break;
       const float d = row16_sum(dot[r]);
       const int32_t e = blk + 4 * r + g;
       if (s == 0 && e < n) {
@@ -614,34 +623,37 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
   const bool add = slot < 0 && a.accumulate;
   bool first = true;
   for (int32_t blk = 0; blk < n || (blk == 0 && !add); blk += 64) {
-    int32_t c[R];
-    float w[R], dot[R];
+    float dot[R], acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < R; ++r) {          // past the segment's end: column 0, weight 0
-      const int off = (blk + 4 * r + g) * 4;
-      c[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
-      w[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
-      dot[r] = 0.0f;
-    }
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < R; ++r) dot[r] = 0.0f;
 #pragma unroll
     for (int r0 = 0; r0 < R; r0 += 4) {
+      // wave-uniform: a group of 16 non-zeros wholly past the segment's end is not loaded; inside the last
+      // group the slots past the end read column 0 with weight 0
+      if (blk + 4 * r0 >= n) break;
+      int32_t c[4];
+      float w[4];
       float4 x[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int off = (blk + 4 * (r0 + q) + g) * 4;
+        c[q] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
+        w[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         typedef unsigned u4 __attribute__((ext_vector_type(4)));
         const u4 v = __builtin_amdgcn_raw_buffer_load_b128(
-            rgy, (int)(__umul24((uint32_t)c[r0 + q], gy_row) + (uint32_t)col0 * 4u), 0, 0);
+            rgy, (int)(__umul24((uint32_t)c[q], gy_row) + (uint32_t)col0 * 4u), 0, 0);
         x[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float wq = w[r0 + q];
-        acc[0] = fmaf(wq, x[q].x, acc[0]);
-        acc[1] = fmaf(wq, x[q].y, acc[1]);
-        acc[2] = fmaf(wq, x[q].z, acc[2]);
-        acc[3] = fmaf(wq, x[q].w, acc[3]);
-        dot[r0 + q] = fmaf(x[q].x, hv.x, fmaf(x[q].y, hv.y, fmaf(x[q].z, hv.z, fmaf(x[q].w, hv.w, dot[r0 + q]))));
+        acc[0] = fmaf(w[q], x[q].x, acc[0]);
+        acc[1] = fmaf(w[q], x[q].y, acc[1]);
+        acc[2] = fmaf(w[q], x[q].z, acc[2]);
+        acc[3] = fmaf(w[q], x[q].w, acc[3]);
+        dot[r0 + q] = fmaf(x[q].x, hv.x, fmaf(x[q].y, hv.y, fmaf(x[q].z, hv.z, x[q].w * hv.w)));
       }
     }
 #pragma unroll
@@ -658,12 +670,16 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
     first = false;
     float mine = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float d = row16_sum(dot[r]);
-      mine = s == r ? d : mine;
+    for (int r0 = 0; r0 < R; r0 += 4) {
+      if (blk + 4 * r0 >= n) break;        // the same groups as above
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float d = row16_sum(dot[r0 + q]);
+        mine = s == r0 + q ? d : mine;
+      }
     }
     const int32_t e = blk + 4 * s + g;
-    if (e < n) drow[e] = mine;
+    if (e < n) __builtin_nontemporal_store(mine, drow + e);
   }
 }
 
