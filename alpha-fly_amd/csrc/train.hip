@@ -531,6 +531,9 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
     for (int32_t ch = 0; ch < chunks; ++ch) {
       const int32_t col0 = ch * 64 + s * 4;
       const bool live = col0 < a.batch;    // the batch is a multiple of 4 on this path
+      // lanes past the batch gather zeros (an offset past any buffer of at most 2^31 - 1 bytes): their
+      // columns may be a padded row's uninitialised tail, and the dot sums across the group's columns
+      const uint32_t coff = live ? (uint32_t)col0 * 4u : 0x80000000u;
       float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
       if (live) hv = *reinterpret_cast<const float4 *>(hj + col0);
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -542,7 +545,7 @@ __global__ __launch_bounds__(256) void k_transposed_backward(const TransposedArg
         for (int q = 0; q < 4; ++q) {
           typedef unsigned u4 __attribute__((ext_vector_type(4)));
           const u4 v = __builtin_amdgcn_raw_buffer_load_b128(
-              rgy, (int)(__umul24((uint32_t)c[r0 + q], gy_row) + (uint32_t)col0 * 4u), 0, 0);
+              rgy, (int)(__umul24((uint32_t)c[r0 + q], gy_row) + coff), 0, 0);
           x[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
         }
 #pragma unroll
@@ -616,6 +619,9 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
   const uint32_t gy_row = (uint32_t)a.ldgy * 4u;
   const int32_t col0 = (int32_t)ch * 64 + s * 4;
   const bool live = col0 < a.batch;        // the batch is a multiple of 4 on this path
+  // lanes past the batch gather zeros (an offset past any buffer of at most 2^31 - 1 bytes): their columns
+  // may be a padded row's uninitialised tail, and the dot sums across the group's columns
+  const uint32_t coff = live ? (uint32_t)col0 * 4u : 0x80000000u;
   float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
   if (live) hv = *reinterpret_cast<const float4 *>(a.h + (int64_t)j * a.ldh + col0);
   float *ghj = slot < 0 ? a.gh + (int64_t)j * a.ldgh : a.partials + (int64_t)slot * a.ldgh;
@@ -644,7 +650,7 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
       for (int q = 0; q < 4; ++q) {
         typedef unsigned u4 __attribute__((ext_vector_type(4)));
         const u4 v = __builtin_amdgcn_raw_buffer_load_b128(
-            rgy, (int)(__umul24((uint32_t)c[q], gy_row) + (uint32_t)col0 * 4u), 0, 0);
+            rgy, (int)(__umul24((uint32_t)c[q], gy_row) + coff), 0, 0);
         x[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
       }
 #pragma unroll
