@@ -291,6 +291,42 @@ def test_forward_io_gradients_match_the_oracle_and_the_full_recurrence(steps):
         _close(got_full, want, 5e-5, f"full {name}")
 
 
+@pytest.mark.parametrize("batch", [8, 200])
+def test_cone_gradients_over_the_transposed_pass_match_the_oracle_and_repeat_exactly(batch):
+    """forward_io under autograd at batches that take the one pass over A^T (multiples of 4): one chunk (8
+    boards) and chunk-major with a ragged last chunk (200), on a 3,000-neuron synthetic graph whose longest rows
+    of A^T (out-degrees up to 870) run as several work-list segments.  Gradients against the oracle in float64
+    (chessfly/brain.py:289-329), and a second run from the same state gives the same bits: partial rows meet
+    in slot order, the chunks' dots add in order, and dL/dw returns from W^T's order by a gather."""
+    from chessfly.synthetic import GraphSpec, synthetic_connectome
+    from oracle import training as T
+    from oracle.lightcone import light_cone
+    conn = synthetic_connectome(GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=100, seed=5))
+    rnn, b = _rnn_pair(conn, 6)
+    in_idx, out_idx = torch.arange(0, 300, device=DEV), torch.arange(2900, 3000, device=DEV)
+    rng = np.random.default_rng(batch)
+    u_in = rng.normal(0, 1, (300, batch))
+    target = torch.as_tensor(rng.normal(0, 1, (100, batch)))
+    runs = []
+    for _ in range(2):
+        rnn.zero_grad()
+        u_d = torch.tensor(u_in, dtype=torch.float32, device=DEV, requires_grad=True)
+        out = rnn.forward_io(u_d, in_idx, out_idx, 6)
+        ((out - target.float().to(DEV)) ** 2).sum().backward()
+        runs.append([out.detach().clone()] + [g.clone() for g in _device_grads(rnn, u_d)])
+    names = ("out", "u_in", "log_gain", "bias", "alpha_logit")
+    for first, second, name in zip(runs[0], runs[1], names):
+        assert torch.equal(first, second), f"{name} differs between two identical runs"
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), np.arange(300), np.arange(2900, 3000), 6)
+    u_r = torch.tensor(u_in, requires_grad=True)
+    ref = T.cone_grad(b, cone, u_r)
+    ((ref - target) ** 2).sum().backward()
+    refs = (ref.detach(), u_r.grad, b.log_gain.grad, b.bias.grad, b.alpha_logit.grad)
+    for got, want, name in zip(runs[0], refs, names):
+        assert float(want.abs().max()) > 0, name
+        _close(got, want, 1e-4, name)
+
+
 def test_train_step_gradients_match_the_oracle():
     """One train_step loss (chessfly/train.py:126-132) through FlyChessNet under autograd on a 3,000-neuron
     synthetic graph: every parameter's gradient against the oracle in float64."""
