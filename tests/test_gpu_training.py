@@ -417,17 +417,18 @@ def test_training_mode_without_autograd_updates_the_normaliser_and_matches_eval(
     _close(logits_eval, logits_train, 2e-3, "eval after the first training-mode call")
 
 
-def test_full_scale_train_step_gradients_match_the_oracle(full_net):
-    """The train_step loss on the full 166,700-neuron synthetic network (6 steps, 4 positions): every
-    parameter's gradient against the oracle in float64.  Only gradients are computed; the shared network's
-    parameters are not changed."""
+@pytest.mark.parametrize("batch", [4, 68])
+def test_full_scale_train_step_gradients_match_the_oracle(full_net, batch):
+    """The train_step loss on the full 166,700-neuron synthetic network (6 steps): every parameter's gradient
+    against the oracle in float64.  4 positions take the one-chunk pass over A^T; 68 take the chunk-major pass
+    with a ragged second chunk.  Only gradients are computed; the shared network's parameters are not
+    changed."""
     from chessfly.encoding import N_BASE, N_MOVES
     from chessfly.synthetic import synthetic_boards
     from oracle import training as T
     from oracle.forward import HeadArrays
     from oracle.lightcone import light_cone
     net, conn = full_net
-    batch = 4
     x = torch.as_tensor(synthetic_boards(batch, seed=11), dtype=torch.float32)
     rng = np.random.default_rng(1)
     legal = torch.as_tensor(rng.random((batch, N_MOVES)) < 0.01)
