@@ -74,7 +74,7 @@ SIGNATURES = {
     "fly_rest_backward": (_i32, [_p, _p, _p, _p, _p, _p, _p, _f32, _i64, _p, _p, _p, _p, _p]),
     "fly_rest_products_backward": (_i32, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64,
                                           _p, _p]),
-    "fly_gather_probe": (_i32, [_p, _i64, _i64, _p, _i64, _p, _p]),
+    "fly_gather_probe": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _p]),
     "fly_profile_enable": (_i32, [_i32]),
     "fly_profile_read": (_i32, [_p, _p]),
     "fly_set_tuning": (_i32, [ctypes.c_char_p, _i64]),

@@ -234,24 +234,27 @@ def train_bench(args, dev) -> dict:
     }
 
 
-def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> dict:
+def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dict]:
     """GB/s of random 128-byte row gathers in the state step's access pattern (fly_gather_probe: 8 rows per
     wave load, 16 bytes per lane), over working sets that fit one XCD's L2 (2 MB), the Infinity Cache (21 MB:
     one 64-column chunk of all 166,700 state rows, what a sweep of the state step touches) and neither
-    (373 MB: the whole B=1120 fp16 state)."""
+    (373 MB: the whole B=1120 fp16 state).  Second, rows per second (G/s) over the 21 MB set for 128-byte reads
+    and for 64-byte reads (16 rows per wave load, a half chunk such as the last chunk at 1120 boards): equal
+    rates say a gathered row costs the same whatever part of its line is used."""
     import torch
     from chessfly import _hip
     lib = _hip.load()
     sink = torch.zeros(256, device=dev)
     st = _hip.stream(dev)
-    out = {}
-    for name, rows in (("l2_2MB", 16384), ("infinity_cache_21MB", 166700), ("hbm_373MB", 166700 * 35 // 2)):
+    gbps, rows_per_s = {}, {}
+    for name, rows, read in (("l2_2MB", 16384, 128), ("infinity_cache_21MB", 166700, 128),
+                             ("hbm_373MB", 166700 * 35 // 2, 128), ("infinity_cache_21MB_64B", 166700, 64)):
         base = torch.randint(0, 256, (rows * 128,), dtype=torch.uint8, device=dev)
         idx = torch.randint(0, rows, (n,), dtype=torch.int32, device=dev)
 
         def once():
-            _hip.check(lib.fly_gather_probe(base.data_ptr(), base.numel(), 128, idx.data_ptr(), n, sink.data_ptr(),
-                                            st), "fly_gather_probe")
+            _hip.check(lib.fly_gather_probe(base.data_ptr(), base.numel(), 128, read, idx.data_ptr(), n,
+                                            sink.data_ptr(), st), "fly_gather_probe")
         once()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -260,9 +263,13 @@ def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> dict:
             once()
         e1.record()
         torch.cuda.synchronize()
-        out[name] = round(n * 128 / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9, 1)
+        sec = e0.elapsed_time(e1) / reps * 1e-3
+        if read == 128:
+            gbps[name] = round(n * 128 / sec / 1e9, 1)
+        if rows == 166700:
+            rows_per_s[f"{read}B"] = round(n / sec / 1e9, 1)
         del base, idx
-    return out
+    return gbps, rows_per_s
 
 
 def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> dict:
@@ -449,8 +456,9 @@ def main() -> int:
             roofline["traffic_source"] = measured["source"]
     shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
     if not args.no_gather_ceiling:
-        ceiling = gather_ceiling(dev)
+        ceiling, rows_per_s = gather_ceiling(dev)
         roofline["gather_ceiling_GBps"] = ceiling
+        roofline["gather_rows_per_s_21MB_G"] = rows_per_s
         roofline["gather_frac_of_ceiling"] = round(roofline["gather_GBps"] / ceiling["infinity_cache_21MB"], 4)
         log(f"random-row gather ceiling {ceiling} GB/s; state step gathers at {roofline['gather_GBps']} GB/s")
 

@@ -314,11 +314,12 @@ int fly_train_step_backward(int64_t rows, int64_t batch, const float *g_dev, int
 
 /* ---- measurement ------------------------------------------------------------------------------- */
 /* No counterpart in the reference; for benchmarks.  The random-row gather rate of this GPU for the state
- * step's access pattern: n reads of 128 bytes at byte offset idx[e] * row_bytes (16 bytes per lane, 8 rows
- * per wave instruction) of base (`bytes` long).  Offsets past `bytes` read zeros, so any idx is safe.
- * sink: 256 floats, written only if the data sum to a sentinel value. */
-int fly_gather_probe(const void *base_dev, int64_t bytes, int64_t row_bytes, const int32_t *idx_dev, int64_t n,
-                     float *sink_dev, void *stream);
+ * step's access pattern: n reads of read_bytes (128: 8 rows per wave instruction, a 64-column fp16 chunk; 64:
+ * 16 rows, a half chunk) at byte offset idx[e] * row_bytes (16 bytes per lane, row_bytes >= read_bytes) of
+ * base (`bytes` long).  Offsets past `bytes` read zeros, so any idx is safe.  sink: 256 floats, written only if
+ * the data sum to a sentinel value. */
+int fly_gather_probe(const void *base_dev, int64_t bytes, int64_t row_bytes, int64_t read_bytes,
+                     const int32_t *idx_dev, int64_t n, float *sink_dev, void *stream);
 
 /* Kernel classes timed by the profiler. */
 enum fly_kernel_class {

@@ -86,9 +86,11 @@ def test_evaluator_outputs_checks_arguments_on_host(lib):
 
 def test_gather_probe_checks_arguments_on_host(lib):
     """The measurement probe refuses null pointers and out-of-range sizes before launching anything."""
-    assert lib.fly_gather_probe(None, 1024, 128, None, 10, None, None) == 1
+    assert lib.fly_gather_probe(None, 1024, 128, 128, None, 10, None, None) == 1
     buf = ctypes.create_string_buffer(16)
     p = ctypes.addressof(buf)
-    assert lib.fly_gather_probe(p, 1 << 31, 128, p, 10, p, None) == 1
-    assert lib.fly_gather_probe(p, 1024, 64, p, 10, p, None) == 1
+    assert lib.fly_gather_probe(p, 1 << 31, 128, 128, p, 10, p, None) == 1
+    assert lib.fly_gather_probe(p, 1024, 64, 128, p, 10, p, None) == 1
     assert b"row_bytes" in lib.fly_last_error()
+    assert lib.fly_gather_probe(p, 1024, 128, 96, p, 10, p, None) == 1
+    assert b"read_bytes" in lib.fly_last_error()
