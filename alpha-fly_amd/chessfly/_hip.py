@@ -47,10 +47,12 @@ SIGNATURES = {
     "fly_plan_create_full": (_i32, [_i64, _i64, _p, _p, _p, _p, _f32, _p, _pp]),
     "fly_plan_destroy": (_i32, [_p]),
     "fly_plan_resting": (_i32, [_p, _p, _p]),
+    "fly_plan_matrix": (_i32, [_p, _i32, _p, _p, _p, _p]),
     "fly_forward_io_workspace": (_sz, [_p, _i64]),
     "fly_forward_io": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_forward_literal_workspace": (_sz, [_p, _i64]),
     "fly_forward_literal": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
+    "fly_plan_step": (_i32, [_p, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p]),
     "fly_dense_create": (_i32, [ctypes.POINTER(HeadDesc), _p, _i64, _i64, _p, _i64, _p, _pp]),
     "fly_dense_destroy": (_i32, [_p]),
     "fly_encoder_workspace": (_sz, [_p, _i64]),
@@ -74,9 +76,9 @@ SIGNATURES = {
     "fly_rest_backward": (_i32, [_p, _p, _p, _p, _p, _p, _p, _f32, _i64, _p, _p, _p, _p, _p]),
     "fly_rest_products_backward": (_i32, [_p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64,
                                           _p, _p]),
-    "fly_gather_probe": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _p]),
     "fly_profile_enable": (_i32, [_i32]),
     "fly_profile_read": (_i32, [_p, _p]),
+    "fly_profile_launches": (_i64, [_p, _p, _i64]),
     "fly_set_tuning": (_i32, [ctypes.c_char_p, _i64]),
 }
 
@@ -136,6 +138,19 @@ def profile_read() -> dict:
     n = (ctypes.c_int64 * 4)()
     check(load().fly_profile_read(ms, n), "fly_profile_read")
     return {name: (float(ms[i]), int(n[i])) for i, name in enumerate(KERNEL_CLASSES)}
+
+
+def profile_launches() -> list[tuple[str, float]]:
+    """(kernel class, milliseconds) of every launch recorded since profiling was enabled, in launch order."""
+    lib = load()
+    n = lib.fly_profile_launches(None, None, 0)
+    if n < 0:
+        raise RuntimeError(f"fly_profile_launches failed: {lib.fly_last_error().decode(errors='replace')}")
+    cls = (ctypes.c_int32 * max(n, 1))()
+    ms = (ctypes.c_double * max(n, 1))()
+    if lib.fly_profile_launches(cls, ms, n) != n:
+        raise RuntimeError(f"fly_profile_launches failed: {lib.fly_last_error().decode(errors='replace')}")
+    return [(KERNEL_CLASSES[cls[i]], float(ms[i])) for i in range(n)]
 
 
 class Handle:

@@ -26,6 +26,7 @@ device; nothing here falls back to the CPU.
 from __future__ import annotations
 
 import ctypes
+import math
 import weakref
 
 import torch
@@ -329,7 +330,7 @@ class _RestingTrajectory(torch.autograd.Function):
             x2_next = torch.empty(n, 2, device=dev)
             _hip.check(lib.fly_rest_forward(rnn.crow32.data_ptr(), rnn.pre32.data_ptr(), w.data_ptr(), n,
                                             rnn.n_edges, _hip.ptr(x2), bias.data_ptr(), alpha.data_ptr(),
-                                            _hip.ptr(c_prev), float(rnn.h_max), member[t].data_ptr(),
+                                            _hip.ptr(c_prev), rnn._h_bound, member[t].data_ptr(),
                                             full.data_ptr(), outside.data_ptr(), c_next.data_ptr(),
                                             x2_next.data_ptr(), st), "fly_rest_forward")
             rows = cone.rows[t]
@@ -368,7 +369,7 @@ class _RestingTrajectory(torch.autograd.Function):
             gc_prev = torch.empty(n, device=dev)
             gk, gp = g_ks[t - 1], g_ps[t - 1]
             _hip.check(lib.fly_rest_backward(_hip.ptr(gc), pos[t].data_ptr(), _hip.ptr(gk), _hip.ptr(gp),
-                                             full.data_ptr(), _hip.ptr(c_prev), alpha.data_ptr(), float(rnn.h_max),
+                                             full.data_ptr(), _hip.ptr(c_prev), alpha.data_ptr(), rnn._h_bound,
                                              n, g2.data_ptr(), gc_prev.data_ptr(), gbias.data_ptr(),
                                              galpha.data_ptr(), st), "fly_rest_backward")
             if x2 is not None:                 # t > 1: the products over W (c_0 = 0 has none)
@@ -673,14 +674,15 @@ class _Plan:
 class ConnectomeRNN(nn.Module):
     def __init__(self, conn: Connectome, alpha_init: float = 0.5, bias_init: float = 0.0,
                  global_scale: float = 1.0, h_max: float | None = 10.0):
-        """global_scale multiplies the normalised connectome weights; activity is clamped to [0, h_max]
-        (brain.py:176-199).  The wiring is rebuilt from the connectome, never stored in checkpoints."""
+        """global_scale multiplies the normalised connectome weights; activity is clamped to [0, h_max], or only
+        below at 0 when h_max is None (brain.py:176-199, 221).  The wiring is rebuilt from the connectome, never
+        stored in checkpoints."""
         super().__init__()
-        if h_max is None:
-            raise ValueError("the evaluator clamps activity to [0, h_max]; h_max=None is not supported")
         self.n = conn.n_neurons
         self.n_edges = conn.n_edges
-        self.h_max = float(h_max)
+        self.h_max = None if h_max is None else float(h_max)
+        # the upper bound the kernels clamp to: h_max, or +inf (no upper clamp) for None
+        self._h_bound = math.inf if h_max is None else float(h_max)
         self.register_buffer("pre", conn.pre, persistent=False)      # (post, pre) order = CSR order of W
         self.register_buffer("post", conn.post, persistent=False)
         self.register_buffer("sign", conn.sign, persistent=False)
@@ -780,7 +782,7 @@ class ConnectomeRNN(nn.Module):
             w = self.edge_weights()
             _hip.check(_hip.load().fly_plan_create_full(self.n, self.n_edges, self.crow32.data_ptr(),
                                                         self.pre32.data_ptr(), w.data_ptr(),
-                                                        self.alpha_logit.data_ptr(), self.h_max,
+                                                        self.alpha_logit.data_ptr(), self._h_bound,
                                                         _hip.stream(w.device), ctypes.byref(handle)),
                        "fly_plan_create_full")
         return self._plan(("full",), build)
@@ -790,7 +792,7 @@ class ConnectomeRNN(nn.Module):
             w = self.edge_weights()
             _hip.check(_hip.load().fly_plan_create(cone.handle, self.crow32.data_ptr(), self.pre32.data_ptr(),
                                                    w.data_ptr(), self.bias.data_ptr(), self.alpha_logit.data_ptr(),
-                                                   self.h_max, mode, _hip.stream(w.device), ctypes.byref(handle)),
+                                                   self._h_bound, mode, _hip.stream(w.device), ctypes.byref(handle)),
                        "fly_plan_create")
         return self._plan(("cone", mode, id(cone)), build)
 
@@ -841,7 +843,7 @@ class ConnectomeRNN(nn.Module):
         flat = []
         for t in range(1, steps + 1):
             flat += [rest[t - 1], rest[steps + t - 1], _take_rows(alpha, cone.rows[t])]
-        h = _ConeRecurrence.apply(cone, self.h_max, self, u_in, w, *flat)
+        h = _ConeRecurrence.apply(cone, self._h_bound, self, u_in, w, *flat)
         out = rest[2 * steps].expand(-1, batch)
         return out.index_copy(0, cone.out_pos, _take_rows(h, cone.out_src))
 

@@ -298,13 +298,13 @@ NEW_HEADS = ("policy_from.", "policy_to.")
 def load_net(path, data_dir: str = "data", device="cuda", conn: Connectome | None = None) -> FlyChessNet:
     """The network of a checkpoint or snapshot, ready to evaluate (chessfly/model.py:154-161): a dict with
     "config" (ModelConfig fields) and "model" (the state dict), read with torch.load(weights_only=True).  The
-    connectome is `conn` or, as in the reference, the MaleCNS release in data_dir (chessfly.connectome.
-    load_malecns, local files only)."""
+    wiring is `conn`, which is required: the reference parses the MaleCNS release from data_dir here, and this
+    package has no reader for it (the release is a network download).  `data_dir` stays for the signature."""
+    if conn is None:
+        raise ValueError("load_net needs the connectome the checkpoint was trained on (conn=...): this package "
+                         "does not read the MaleCNS release")
     ck = torch.load(path, map_location="cpu", weights_only=True)
     cfg = ModelConfig(**ck["config"])
-    if conn is None:
-        from .connectome import load_malecns
-        conn = load_malecns(data_dir, cfg.min_syn)
     net = FlyChessNet(conn, cfg)
     load_weights(net, ck["model"])
     return net.to(device).eval()

@@ -1,6 +1,7 @@
 // Version, error reporting and launch timing of the C ABI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -104,4 +105,22 @@ extern "C" int fly_profile_read(double *ms, int64_t *launches) {
       if (launches) launches[c] = cnt[c];
     }
   });
+}
+
+extern "C" int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap) {
+  int64_t n = -1;
+  const int rc = guard([&] {
+    Profiler &p = profiler();
+    std::lock_guard<std::mutex> lock(p.mu);
+    n = (int64_t)p.records.size();
+    for (int64_t i = 0; i < std::min<int64_t>(n, cap); ++i) {
+      const Record &r = p.records[(size_t)i];
+      FLY_HIP(hipEventSynchronize(r.stop));
+      float t = 0.f;
+      FLY_HIP(hipEventElapsedTime(&t, r.start, r.stop));
+      if (cls) cls[i] = r.cls;
+      if (ms) ms[i] = t;
+    }
+  });
+  return rc == FLY_OK ? n : -1;
 }

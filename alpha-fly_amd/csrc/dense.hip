@@ -25,11 +25,11 @@
 
 namespace fly {
 
-int64_t state_ld(int64_t batch, size_t elem);
 int64_t io_block(const fly_plan &plan, int64_t batch);
 size_t io_workspace(const fly_plan &plan, int64_t batch);
 template <typename S, typename U>
-const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, void *ws, hipStream_t st);
+const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, bool u_padded, void *ws,
+                        hipStream_t st);
 void check_plan_device(const fly_plan *plan);
 
 }  // namespace fly
@@ -609,10 +609,10 @@ extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const
       // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
       run_encoder(*d, xb, x_f16 != 0, ldx, nb, input_gain, u, nullptr, ldu, scratch, st);
       if (plan->mode == FLY_MODE_DEVIATION_F16) {
-        const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, nb, states, st);
+        const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, nb, true, states, st);
         run_head<_Float16>(*d, fin, lds, plan->out_src.p, plan->cbase.p, nb, lb, wb, scratch, st);
       } else {
-        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, states, st);
+        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, true, states, st);
         run_head<float>(*d, fin, lds, plan->out_src.p, plan->cbase.p, nb, lb, wb, scratch, st);
       }
     }

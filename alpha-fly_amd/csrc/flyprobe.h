@@ -1,0 +1,43 @@
+/*
+ * flyprobe.h - measurement probes for bench.py (libflyprobe.so).  Not part of the evaluator's ABI
+ * (include/flyeval.h) and not loaded by it: the library exists to put a ceiling beside the state step's time.
+ *
+ * Every entry point returns 0 on success and 1 on a bad argument or a HIP error, with a message from
+ * flyprobe_last_error().  Pointers are device pointers; launches go on `stream`.
+ */
+#ifndef FLYPROBE_H
+#define FLYPROBE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char *flyprobe_last_error(void);
+
+/* pairs (nnz) = {col[q], bits of val[q]}: a plan matrix (fly_plan_matrix) packed back into the 8-byte records
+ * the state step streams. */
+int flyprobe_pack(const int32_t *col_dev, const float *val_dev, int64_t nnz, void *pairs_dev, void *stream);
+
+/* The replay of one state step's gather stream: the state step's own kernel (same launch shape, wave order,
+ * pair loads and gathers, chosen by the same rule from nrows, nnz and the layout) with the FMAs replaced by an
+ * XOR fold and no row constants, input, carried state, cross-lane sums or stores.  rowptr (nrows+1) and pairs
+ * (nnz records) are A_t; xprev (prev_rows, ldx) the previous state, __half if state_f16 else float; batch
+ * columns.  sink: at least 1 KiB, written only if the folded bits hit one value. */
+int flyprobe_replay_step(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
+                         const void *xprev_dev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
+                         void *sink_dev, void *stream);
+
+/* Uniform-random row gathers in the state step's lane layout: n reads of read_bytes (128: 8 rows per wave
+ * instruction; 64: 16 rows) at byte offset idx[e] * row_bytes (16 bytes per lane) of base (`bytes` long).
+ * Offsets past `bytes` read zeros.  sink: 256 floats, written only if the data sum to a sentinel value. */
+int flyprobe_random_gather(const void *base_dev, int64_t bytes, int64_t row_bytes, int64_t read_bytes,
+                           const int32_t *idx_dev, int64_t n, float *sink_dev, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLYPROBE_H */

@@ -126,6 +126,14 @@ __global__ void k_pack(const int32_t *__restrict__ col, const int32_t *__restric
   cv[q] = make_int2(col[q], __float_as_int(w[e]));
 }
 
+__global__ void k_unpack(const int2 *__restrict__ cv, int64_t nnz, int32_t *__restrict__ col, float *__restrict__ val) {
+  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q >= nnz) return;
+  const int2 p = cv[q];
+  if (col) col[q] = p.x;
+  if (val) val[q] = __int_as_float(p.y);
+}
+
 // c_out[j] = c_T[out_idx[j]]; cbase is what the head adds to the carried state at output j: the resting
 // value in deviation mode, and in float32 mode the resting value only where the output is not carried.
 __global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *__restrict__ out_src,
@@ -163,6 +171,7 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
     *out = nullptr;
     FLY_REQUIRE(cone != nullptr, "cone is null");
     FLY_REQUIRE(mode == FLY_MODE_DEVIATION_F16 || mode == FLY_MODE_F32, "unknown mode");
+    FLY_REQUIRE(h_max >= 0.0f, "h_max must be >= 0 (+inf: no upper clamp)");
     FLY_REQUIRE(crow && bias && alpha_logit && (cone->n_edges == 0 || (pre && w)), "null argument");
     FLY_REQUIRE(current_device() == cone->device, "the cone lives on another device");
     hipStream_t st = as_stream(stream);
@@ -238,6 +247,7 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
     *out = nullptr;
     FLY_REQUIRE(n > 0 && n < (int64_t)INT32_MAX && n_edges >= 0 && n_edges < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(crow && alpha_logit && (n_edges == 0 || (pre && w)), "null argument");
+    FLY_REQUIRE(h_max >= 0.0f, "h_max must be >= 0 (+inf: no upper clamp)");
     hipStream_t st = as_stream(stream);
     validate_graph(n, n_edges, crow, pre, st);
     auto plan = std::make_unique<fly_plan>();
@@ -282,5 +292,25 @@ extern "C" int fly_plan_resting(const fly_plan *plan, float *c_out, void *stream
     FLY_REQUIRE(!plan->full, "the literal-recurrence plan has no resting outputs");
     if (plan->n_out)
       FLY_HIP(hipMemcpyAsync(c_out, plan->c_out.p, sizeof(float) * plan->n_out, hipMemcpyDeviceToDevice, as_stream(stream)));
+  });
+}
+
+extern "C" int fly_plan_matrix(const fly_plan *plan, int32_t t, int32_t *rowptr, int32_t *col, float *val,
+                               void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(plan != nullptr, "plan is null");
+    FLY_REQUIRE(current_device() == plan->device, "the plan lives on another device");
+    FLY_REQUIRE(plan->full ? t == 1 : (t >= 1 && t <= plan->steps), "step out of range");
+    const int ti = plan->full ? 0 : t;
+    if (plan->rowptr[ti].p == nullptr) return;   // A_t does not exist (R_{t-1} is empty)
+    hipStream_t st = as_stream(stream);
+    const int64_t nr = plan->rows_n[ti], nnz = plan->nnz[ti];
+    if (rowptr)
+      FLY_HIP(hipMemcpyAsync(rowptr, plan->rowptr[ti].p, sizeof(int32_t) * (nr + 1), hipMemcpyDeviceToDevice, st));
+    if (nnz && (col || val)) {
+      hipLaunchKernelGGL(k_unpack, dim3(blocks_for(nnz, kThreads)), dim3(kThreads), 0, st, plan->colval[ti].p, nnz,
+                         col, val);
+      check_launch("plan matrix");
+    }
   });
 }

@@ -1,21 +1,74 @@
-// Measurement only: the ceiling of the state step's memory access pattern on this GPU.  A wave splits into
-// G groups of 64 / G lanes; per round group g reads the first 1024 / G bytes of row idx[e + g] (16 bytes per
-// lane) and folds them into one register with 4 adds (the step spends 8 FMAs).  G = 8 (128 bytes per row) is
-// exactly the gather of the state step's 64-column chunks; G = 16 (64 bytes per row) is a half chunk, as the
-// last chunk of a batch of 32 columns past a multiple of 64.  Timing it over working sets that fit the L2, the
-// Infinity Cache or neither gives the random-row gather rate the state step can at best reach.
-#include "common.hpp"
-#include "device.hpp"
+// libflyprobe.so: measurement probes for bench.py, built apart from the evaluator library.
+//
+// flyprobe_replay_step runs the state step's own kernels (step_kernels.hpp) built with REPLAY = true: the same
+// launch shape, wave numbering, per-row pair records and buffer-offset gathers as the evaluator's step on the
+// same matrix and state layout, without the arithmetic, the row inputs or the stores.  Its time is what the
+// step's memory stream alone costs, which is the ceiling the fused step is measured against.
+//
+// flyprobe_random_gather reads rows picked uniformly at random in the same lane layout (8 rows of 128 bytes
+// per wave load, or 16 of 64 bytes): the gather rate of a working set of a given size with no reuse beyond
+// chance, for context.
+#include <string>
+
+#include "flyprobe.h"
+#include "step_kernels.hpp"
 
 namespace fly {
 namespace {
 
+thread_local std::string g_probe_error;
+
+template <typename F>
+int probe_guard(F &&f) {
+  try {
+    f();
+    return 0;
+  } catch (const Error &e) {
+    g_probe_error = e.msg;
+  } catch (const std::exception &e) {
+    g_probe_error = e.what();
+  } catch (...) {
+    g_probe_error = "unknown exception";
+  }
+  return 1;
+}
+
+__global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__restrict__ val, int64_t nnz,
+                             int2 *__restrict__ out) {
+  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q < nnz) out[q] = make_int2(col[q], __float_as_int(val[q]));
+}
+
+// The evaluator's default shapes only (no tuning knobs): lane groups of 16-byte lanes, or row slots of 16- or
+// 32-byte lanes, in groups of 8 lanes with 4 rounds in flight.
+template <typename S>
+void replay(StepArgs<S, S> a, double avg_nnz, hipStream_t st) {
+  const StepShape sh = shape_step(a, avg_nnz, Tuning{});
+  const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
+  FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "replay grid too large");
+  const dim3 grid(blocks_for(waves, 4)), block(256);
+  constexpr int kV16 = 16 / (int)sizeof(S);
+  FLY_REQUIRE(sh.groups == 8, "no replay for this launch shape");
+  if (sh.rows_mode && sh.v == 2 * kV16) {
+    if constexpr (sizeof(S) == 2)
+      hipLaunchKernelGGL((k_state_step_rows<S, S, 2 * kV16, 8, 4, false, true>), grid, block, 0, st, a);
+  } else if (sh.rows_mode && sh.v == kV16) {
+    hipLaunchKernelGGL((k_state_step_rows<S, S, kV16, 8, 4, false, true>), grid, block, 0, st, a);
+  } else if (!sh.rows_mode && sh.v == kV16) {
+    hipLaunchKernelGGL((k_state_step_grouped<S, S, kV16, 8, 4, false, true>), grid, block, 0, st, a);
+  } else {
+    FLY_REQUIRE(false, "no replay for this launch shape");
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) throw Error{1, std::string("replay launch: ") + hipGetErrorString(e)};
+}
+
 constexpr int kRoundsPerWave = 64;
 
 template <int G>
-__global__ __launch_bounds__(256) void k_gather_probe(const char *base, uint32_t bytes, uint32_t row_bytes,
-                                                      const int32_t *__restrict__ idx, int64_t n,
-                                                      float *__restrict__ sink) {
+__global__ __launch_bounds__(256) void k_random_gather(const char *base, uint32_t bytes, uint32_t row_bytes,
+                                                       const int32_t *__restrict__ idx, int64_t n,
+                                                       float *__restrict__ sink) {
   constexpr int LPG = 64 / G;
   const int lane = threadIdx.x & 63, g = lane / LPG, s = lane % LPG;
   const int64_t wave = blockIdx.x * 4ll + (threadIdx.x >> 6);
@@ -41,9 +94,53 @@ __global__ __launch_bounds__(256) void k_gather_probe(const char *base, uint32_t
 
 using namespace fly;
 
-extern "C" int fly_gather_probe(const void *base, int64_t bytes, int64_t row_bytes, int64_t read_bytes,
-                                const int32_t *idx, int64_t n, float *sink, void *stream) {
-  return guard([&] {
+extern "C" const char *flyprobe_last_error(void) { return g_probe_error.c_str(); }
+
+extern "C" int flyprobe_pack(const int32_t *col, const float *val, int64_t nnz, void *pairs, void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(nnz >= 0 && nnz < (int64_t)INT32_MAX, "nnz out of range");
+    if (!nnz) return;
+    FLY_REQUIRE(col && val && pairs && aligned(pairs, 8), "null or misaligned argument");
+    hipLaunchKernelGGL(k_pack_pairs, dim3(blocks_for(nnz, 256)), dim3(256), 0, as_stream(stream), col, val, nnz,
+                       static_cast<int2 *>(pairs));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error{1, std::string("pack launch: ") + hipGetErrorString(e)};
+  });
+}
+
+extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
+                                    const void *xprev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
+                                    void *sink, void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(rowptr && pairs && xprev && sink, "null argument");
+    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
+    FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
+    FLY_REQUIRE(aligned(sink, 256), "sink must be 256-byte aligned");
+    auto run = [&](auto zero) {
+      using S = decltype(zero);
+      StepArgs<S, S> a{};
+      a.rowptr = rowptr;
+      a.colval = static_cast<const int2 *>(pairs);
+      a.params = nullptr;
+      a.xprev = static_cast<const S *>(xprev);
+      a.ldx = ldx;
+      a.xout = static_cast<S *>(sink);   // the sink stands in for the new state: same alignment, ldo = ldx
+      a.ldo = ldx;
+      a.nrows = (int32_t)nrows;
+      a.batch = (int32_t)batch;
+      a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
+      replay<S>(a, (double)nnz / (double)nrows, as_stream(stream));
+    };
+    if (state_f16)
+      run(_Float16(0));
+    else
+      run(0.0f);
+  });
+}
+
+extern "C" int flyprobe_random_gather(const void *base, int64_t bytes, int64_t row_bytes, int64_t read_bytes,
+                                      const int32_t *idx, int64_t n, float *sink, void *stream) {
+  return probe_guard([&] {
     FLY_REQUIRE(base && idx && sink, "null argument");
     FLY_REQUIRE(bytes > 0 && bytes <= INT32_MAX, "the probed buffer must hold 1 .. 2^31-1 bytes");
     FLY_REQUIRE(read_bytes == 64 || read_bytes == 128, "read_bytes must be 64 or 128");
@@ -52,13 +149,14 @@ extern "C" int fly_gather_probe(const void *base, int64_t bytes, int64_t row_byt
     const int G = read_bytes == 128 ? 8 : 16;
     const int64_t waves = (n + kRoundsPerWave * G - 1) / (kRoundsPerWave * G);
     FLY_REQUIRE(waves < (int64_t)UINT32_MAX, "probe grid too large");
-    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    hipStream_t st = as_stream(stream);
     if (G == 8)
-      hipLaunchKernelGGL(k_gather_probe<8>, dim3(blocks_for(waves, 4)), dim3(256), 0, as_stream(stream),
+      hipLaunchKernelGGL(k_random_gather<8>, dim3(blocks_for(waves, 4)), dim3(256), 0, st,
                          static_cast<const char *>(base), (uint32_t)bytes, (uint32_t)row_bytes, idx, n, sink);
     else
-      hipLaunchKernelGGL(k_gather_probe<16>, dim3(blocks_for(waves, 4)), dim3(256), 0, as_stream(stream),
+      hipLaunchKernelGGL(k_random_gather<16>, dim3(blocks_for(waves, 4)), dim3(256), 0, st,
                          static_cast<const char *>(base), (uint32_t)bytes, (uint32_t)row_bytes, idx, n, sink);
-    check_launch("gather probe");
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error{1, std::string("gather launch: ") + hipGetErrorString(e)};
   });
 }

@@ -50,6 +50,19 @@ def algorithmic_bytes(cone, batch: int, state_bytes: int) -> list[int]:
     return out
 
 
+def cpu_threads(requested: int = 0) -> tuple[int, int, str]:
+    """Threads for the CPU baseline: len(os.sched_getaffinity(0)), capped at OMP_NUM_THREADS where the
+    environment sets it (the CPU share a GPU job declares; a shared host's affinity mask can list cores other
+    jobs use).  Returns (threads, affinity cores, a note on the choice)."""
+    affinity = len(os.sched_getaffinity(0))
+    if requested > 0:
+        return requested, affinity, "--cpu-threads"
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < affinity:
+        return int(omp), affinity, f"capped at OMP_NUM_THREADS={omp}"
+    return affinity, affinity, "all affinity cores"
+
+
 def cpu_baseline(net, conn, x_cpu, threads: int, prune: bool = True, seconds: float = 12.0):
     """The reference's CPU forward on the host cores: the float32 light cone with its constants cached per
     weight version (chessfly/brain.py:295-306), or with pruning off the literal recurrence
@@ -213,10 +226,11 @@ def train_bench(args, dev) -> dict:
     cpu = None
     if args.cpu_boards > 0:
         nb = min(args.cpu_boards, args.batch, 64)
-        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
-        log(f"CPU training baseline: {nb} positions on {threads} threads ...")
+        threads, affinity, cap = cpu_threads(args.cpu_threads)
+        log(f"CPU training baseline: {nb} positions on {threads} threads ({affinity} affinity cores; {cap}) ...")
         rate, per, reps = cpu_train_baseline(net, conn, x_np[:nb], threads)
-        cpu = {"value": round(rate, 2), "unit": "positions/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(rate, 2), "unit": "positions/s", "cores": threads, "affinity_cores": affinity,
+               "threads_note": cap, "kind": "port",
                "sample": f"{nb} positions, full graph, float32 light cone forward + backward under autograd "
                          f"(reference CPU path, chessfly/brain.py:66-99, 289-329), median of {reps} ({per:.2f} s each)"}
         log(f"CPU {rate:,.2f} positions/s")
@@ -234,16 +248,99 @@ def train_bench(args, dev) -> dict:
     }
 
 
-def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dict]:
-    """GB/s of random 128-byte row gathers in the state step's access pattern (fly_gather_probe: 8 rows per
-    wave load, 16 bytes per lane), over working sets that fit one XCD's L2 (2 MB), the Infinity Cache (21 MB:
-    one 64-column chunk of all 166,700 state rows, what a sweep of the state step touches) and neither
-    (373 MB: the whole B=1120 fp16 state).  Second, rows per second (G/s) over the 21 MB set for 128-byte reads
-    and for 64-byte reads (16 rows per wave load, a half chunk such as the last chunk at 1120 boards): equal
-    rates say a gathered row costs the same whatever part of its line is used."""
+PROBE_LIB = os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so")
+
+
+def _probe_lib():
+    """libflyprobe.so (measurement probes, csrc/probe.hip), loaded with its argument types."""
+    import ctypes
+    if not os.path.exists(PROBE_LIB):
+        raise RuntimeError(f"{PROBE_LIB} is missing: build it with `make -C alpha-fly_amd/csrc`")
+    lib = ctypes.CDLL(PROBE_LIB)
+    p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.flyprobe_last_error.restype, lib.flyprobe_last_error.argtypes = ctypes.c_char_p, []
+    for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
+                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p]),
+                       ("flyprobe_random_gather", [p, i64, i64, i64, p, i64, p, p])):
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = i32, args
+    return lib
+
+
+def _probe_check(lib, status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed: {lib.flyprobe_last_error().decode(errors='replace')}")
+
+
+def state_ld(batch: int, elem: int) -> int:
+    """Row stride of the evaluator's state buffers (the batch rounded up to 64 columns, plus one 128-byte line
+    when that leaves an even number of lines per row)."""
+    line = 128 // elem
+    ld = -(-batch // 64) * 64
+    return ld + line if (ld // line) % 2 == 0 else ld
+
+
+def _events_ms(fn, reps: int) -> float:
+    """Average milliseconds of fn() over `reps` calls, between HIP events on torch's current stream (where fn
+    launches)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def replay_ceiling(plan, cone, batch: int, state_f16: bool, dev, reps: int = 20) -> list[dict]:
+    """Per step with a matrix, the time of the replay of that step's gather stream (flyprobe_replay_step: the
+    state step's own kernel, launch shape and wave order over this plan's A_t and a state of this layout, with
+    the arithmetic, row inputs and stores taken out)."""
     import torch
     from chessfly import _hip
-    lib = _hip.load()
+    lib, probe = _hip.load(), _probe_lib()
+    st = _hip.stream(dev)
+    elem = 2 if state_f16 else 4
+    ld = state_ld(batch, elem)
+    dtype = torch.float16 if state_f16 else torch.float32
+    sink = torch.empty(4096, dtype=torch.uint8, device=dev)
+    out = []
+    for t in range(1, cone.steps + 1):
+        nr, nnz, prev_rows = cone.row_counts[t], cone.nnz[t], cone.row_counts[t - 1]
+        if cone.ops[t] is None or nr == 0 or nnz == 0:
+            continue
+        rowptr = torch.empty(nr + 1, dtype=torch.int32, device=dev)
+        col = torch.empty(nnz, dtype=torch.int32, device=dev)
+        val = torch.empty(nnz, dtype=torch.float32, device=dev)
+        _hip.check(lib.fly_plan_matrix(plan.handle, t, rowptr.data_ptr(), col.data_ptr(), val.data_ptr(), st),
+                   "fly_plan_matrix")
+        pairs = torch.empty(2 * nnz, dtype=torch.int32, device=dev)
+        _probe_check(probe, probe.flyprobe_pack(col.data_ptr(), val.data_ptr(), nnz, pairs.data_ptr(), st),
+                     "flyprobe_pack")
+        del col, val
+        xprev = (torch.randn(prev_rows, ld, device=dev) * 0.01).to(dtype)
+
+        def once():
+            _probe_check(probe, probe.flyprobe_replay_step(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz,
+                                                           xprev.data_ptr(), prev_rows, ld, batch, int(state_f16),
+                                                           sink.data_ptr(), st), "flyprobe_replay_step")
+        out.append({"t": t, "rows": nr, "nnz": nnz, "replay_ms": round(_events_ms(once, reps), 4)})
+        del rowptr, pairs, xprev
+    return out
+
+
+def random_gather_rates(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dict]:
+    """Context for the replay: GB/s of uniformly random 128-byte row reads in the state step's lane layout
+    (flyprobe_random_gather: 8 rows per wave load, 16 bytes per lane) over working sets that fit one XCD's L2
+    (2 MB), the Infinity Cache (21 MB: one 64-column chunk of 166,700 rows) and neither (373 MB), and rows per
+    second over the 21 MB set for 128- and 64-byte reads.  The state step's rows are not uniform (a source row
+    is picked in proportion to its out-degree), so this is no ceiling for it: the replay is."""
+    import torch
+    from chessfly import _hip
+    probe = _probe_lib()
     sink = torch.zeros(256, device=dev)
     st = _hip.stream(dev)
     gbps, rows_per_s = {}, {}
@@ -253,17 +350,9 @@ def gather_ceiling(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dict]:
         idx = torch.randint(0, rows, (n,), dtype=torch.int32, device=dev)
 
         def once():
-            _hip.check(lib.fly_gather_probe(base.data_ptr(), base.numel(), 128, read, idx.data_ptr(), n,
-                                            sink.data_ptr(), st), "fly_gather_probe")
-        once()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            once()
-        e1.record()
-        torch.cuda.synchronize()
-        sec = e0.elapsed_time(e1) / reps * 1e-3
+            _probe_check(probe, probe.flyprobe_random_gather(base.data_ptr(), base.numel(), 128, read, idx.data_ptr(),
+                                                             n, sink.data_ptr(), st), "flyprobe_random_gather")
+        sec = _events_ms(once, reps) * 1e-3
         if read == 128:
             gbps[name] = round(n * 128 / sec / 1e9, 1)
         if rows == 166700:
@@ -331,7 +420,11 @@ def main() -> int:
                     help="time the training step (forward + backward + AdamW, float32) instead of the evaluator; "
                          "--batch defaults to 256 here")
     ap.add_argument("--no-gather-ceiling", action="store_true",
-                    help="skip the random-row gather probe that measures the state step's access-pattern ceiling")
+                    help="skip the uniform random-row gather rates (context for the replay)")
+    ap.add_argument("--no-replay", action="store_true",
+                    help="skip the replay of each step's gather stream (the state step's ceiling)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (0: the affinity cores, capped at OMP_NUM_THREADS when set)")
     ap.add_argument("--evaluator-steps", type=int, default=10,
                     help="batches through Evaluator.submit/result from host numpy, PCIe included (0: skip)")
     ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
@@ -414,6 +507,7 @@ def main() -> int:
             net(x)
         torch.cuda.synchronize()
         prof = _hip.profile_read()
+        launches = _hip.profile_launches()
         _hip.profile_enable(False)
     if args.calibrate_copy > 0:
         src = torch.ones(args.calibrate_copy * 2**18, device=dev)
@@ -455,12 +549,33 @@ def main() -> int:
             roofline["traffic"] = measured["traffic_bytes_per_launch"]
             roofline["traffic_source"] = measured["source"]
     shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
+    # per-step state-step times of the forward: the profiled pass's state-step launches, in step order
+    step_launch_ms = [ms for cls, ms in launches if cls == "state_step"]
+    live = [t for t in range(1, cone.steps + 1) if cone.row_counts[t] > 0]
+    per_step = {t: statistics.mean(step_launch_ms[i::len(live)]) for i, t in enumerate(live)} \
+        if len(step_launch_ms) == args.steps * len(live) else {}
+    if not args.no_replay and per_step:
+        # the ceiling: each step's own gather stream replayed alone (same kernel, shape and order, no arithmetic)
+        plan = brain._cone_plan(cone, mode)
+        rows = replay_ceiling(plan, cone, args.batch, args.dtype == "f16", dev)
+        for r in rows:
+            r["step_ms"] = round(per_step[r["t"]], 4)
+            r["replay_over_step"] = round(r["replay_ms"] / r["step_ms"], 4)
+        tot_replay = sum(r["replay_ms"] for r in rows)
+        tot_step = sum(r["step_ms"] for r in rows)
+        roofline["replay"] = {
+            "per_step": rows, "replay_ms": round(tot_replay, 4), "step_ms": round(tot_step, 4),
+            "frac_of_replay": round(tot_replay / tot_step, 4) if tot_step else None,
+            "note": "replay = the state step's own kernel over the same A_t and state layout with the FMAs, row "
+                    "inputs and stores taken out (libflyprobe.so); frac_of_replay = replay time / state-step time "
+                    "over the steps with a matrix (1.0: the step costs no more than its gather stream)"}
+        log(f"replay of the gather stream: {tot_replay:.3f} ms against {tot_step:.3f} ms of state steps "
+            f"(per step {[(r['t'], r['replay_ms'], r['step_ms']) for r in rows]})")
     if not args.no_gather_ceiling:
-        ceiling, rows_per_s = gather_ceiling(dev)
-        roofline["gather_ceiling_GBps"] = ceiling
-        roofline["gather_rows_per_s_21MB_G"] = rows_per_s
-        roofline["gather_frac_of_ceiling"] = round(roofline["gather_GBps"] / ceiling["infinity_cache_21MB"], 4)
-        log(f"random-row gather ceiling {ceiling} GB/s; state step gathers at {roofline['gather_GBps']} GB/s")
+        rates, rows_per_s = random_gather_rates(dev)
+        roofline["random_gather_GBps"] = rates
+        roofline["random_gather_rows_per_s_21MB_G"] = rows_per_s
+        log(f"uniform random-row gathers {rates} GB/s; state step gathers at {roofline['gather_GBps']} GB/s")
 
     evaluator = None
     if args.evaluator_steps > 0:
@@ -471,12 +586,13 @@ def main() -> int:
     parity = None
     if args.cpu_boards > 0:
         nb = min(args.cpu_boards, args.batch)
-        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
-        log(f"CPU baseline: {nb} boards on {threads} threads ...")
+        threads, affinity, cap = cpu_threads(args.cpu_threads)
+        log(f"CPU baseline: {nb} boards on {threads} threads ({affinity} affinity cores; {cap}) ...")
         rate, per, ref_logits, ref_wdl, reps = cpu_baseline(net, conn, x_np[:nb], threads, prune=not args.no_prune)
         path = ("float32 literal recurrence (reference CPU path, chessfly/brain.py:211-223)" if args.no_prune else
                 "float32 light cone with cached constants (reference CPU path, chessfly/brain.py:295-329)")
-        cpu = {"value": round(rate, 1), "unit": "board-evals/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(rate, 1), "unit": "board-evals/s", "cores": threads, "affinity_cores": affinity,
+               "threads_note": cap, "kind": "port",
                "sample": f"{nb} of the {args.batch} boards, full graph, {path}, median of {reps} forwards "
                          f"({per:.2f} s each)"}
         dl = float((logits[:nb].float().cpu() - ref_logits).abs().max())

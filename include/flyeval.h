@@ -18,6 +18,7 @@
  *   fly_plan_create_full  chessfly/brain.py:215-216 (per-call weights of the literal recurrence)
  *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280)
  *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch)
+ *   fly_plan_step         chessfly/brain.py:273-277 and :310-313 (one step of forward_io; :219-220 one literal step)
  *   fly_dense_create      chessfly/model.py:79-93 (the encoder and head weights, as the matrix cores read them)
  *   fly_encoder           chessfly/model.py:99-102 (encoder linear map, input gain, cast, transpose)
  *   fly_head              chessfly/model.py:103-105 and :51-58 (RunningNorm eval, policy/from/to/value)
@@ -95,7 +96,9 @@ int fly_edge_weights(const float *sign_dev, const float *w0_dev, const float *lo
 
 /* Weight-set plan for forward_io: per-step sub-matrices with float32 values, per-row constants and the
  * resting trajectory, from the cone and the graph (crow/pre as given to fly_cone_create), edge weights w
- * (n_edges), bias and alpha_logit (n).  The plan is self-contained: the inputs may be freed afterwards. */
+ * (n_edges), bias and alpha_logit (n).  The plan is self-contained: the inputs may be freed afterwards.
+ * Activity is clamped to [0, h_max]; h_max = +INFINITY clamps only below (the reference's h_max=None,
+ * chessfly/brain.py:178-182, 221).  A negative or NaN h_max is FLY_ERR_INVALID. */
 int fly_plan_create(const fly_cone *cone, const int32_t *crow_dev, const int32_t *pre_dev, const float *w_dev,
                     const float *bias_dev, const float *alpha_logit_dev, float h_max, int32_t mode,
                     void *stream, fly_plan **out);
@@ -106,6 +109,12 @@ int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *crow_dev, co
 int fly_plan_destroy(fly_plan *plan);
 /* c_T[out_idx] (n_out floats): the outputs of a network that sees no position. */
 int fly_plan_resting(const fly_plan *plan, float *c_out_dev, void *stream);
+/* The plan's sub-matrix A_t as the step kernels read it, the cached per-step matrix of chessfly/brain.py:267-268
+ * (fp16 path) and :303 (float32 path): row pointer (|R_t|+1), local column and float32 value (nnz_t each), in
+ * W's edge order.  Nothing is written where A_t does not exist; NULL skips an array.  A literal plan has one
+ * matrix, t = 1 (W itself). */
+int fly_plan_matrix(const fly_plan *plan, int32_t t, int32_t *rowptr_dev, int32_t *col_dev, float *val_dev,
+                    void *stream);
 
 /* ---- forward ----------------------------------------------------------------------------------- */
 /* Bytes of scratch the forward entry points need for `batch` columns (pass at least this many).  A batch whose
@@ -121,6 +130,17 @@ size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch);
 int fly_forward_literal(const fly_plan *plan, float *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
                         int32_t steps, float *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
                         void *stream);
+
+/* One state step of a plan, the per-step op of chessfly/brain.py:273-277 (float16 deviation: s = A_t d_{t-1},
+ * index_add_ of the input, FUSED_DEVIATION) and :310-313 (float32: A_t h + input, FUSED_UPDATE with k_t):
+ * xout (|R_t|, ldo) from xprev (|R_{t-1}|, ldx) and the input drive u_in (n_in, ldu).  States and u_in are __half
+ * (the deviation from the resting trajectory) for FLY_MODE_DEVIATION_F16 and float for FLY_MODE_F32.  xprev is
+ * NULL when R_{t-1} is empty (t = 1) and required otherwise; u_in NULL adds no input.  For a plan from
+ * fly_plan_create_full, t is 1 and the step is one literal update of every row, x = clamp(W h + u, 0, h_max),
+ * h' = lerp(h, x, alpha), with u_in (n, ldu) holding u + bias and xprev NULL for h = 0.  Only columns
+ * [0, batch) of the caller's rows are read or written. */
+int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev_dev, int64_t ldx, const void *u_in_dev,
+                  int64_t ldu, int64_t batch, void *xout_dev, int64_t ldo, void *stream);
 
 /* ---- dense maps -------------------------------------------------------------------------------- */
 /* Weights of the read-out: RunningNorm statistics and the four linear maps over the n_out outputs. */
@@ -313,13 +333,6 @@ int fly_train_step_backward(int64_t rows, int64_t batch, const float *g_dev, int
                             int64_t ldgu, float *ghprev_dev, int64_t ldgh, void *stream);
 
 /* ---- measurement ------------------------------------------------------------------------------- */
-/* No counterpart in the reference; for benchmarks.  The random-row gather rate of this GPU for the state
- * step's access pattern: n reads of read_bytes (128: 8 rows per wave instruction, a 64-column fp16 chunk; 64:
- * 16 rows, a half chunk) at byte offset idx[e] * row_bytes (16 bytes per lane, row_bytes >= read_bytes) of
- * base (`bytes` long).  Offsets past `bytes` read zeros, so any idx is safe.  sink: 256 floats, written only if
- * the data sum to a sentinel value. */
-int fly_gather_probe(const void *base_dev, int64_t bytes, int64_t row_bytes, int64_t read_bytes,
-                     const int32_t *idx_dev, int64_t n, float *sink_dev, void *stream);
 
 /* Kernel classes timed by the profiler. */
 enum fly_kernel_class {
@@ -335,6 +348,9 @@ int fly_profile_enable(int32_t on);
 /* Waits for the recorded events and returns, per kernel class, the summed milliseconds and the number of
  * launches (arrays of FLY_K_CLASSES entries; either may be NULL). */
 int fly_profile_read(double *ms, int64_t *launches);
+/* Waits for the recorded events and returns the number of launches recorded; the first min(that, cap) get their
+ * kernel class and milliseconds, in launch order (either array may be NULL).  -1 on error. */
+int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
 
 /* ---- tuning (for sweeps; defaults are the measured best) --------------------------------------- */
 /* key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept

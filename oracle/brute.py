@@ -24,8 +24,9 @@ def dense_matrix(n: int, pre, post, w) -> np.ndarray:
     return W
 
 
-def dense_recurrence(W: np.ndarray, bias, alpha, u: np.ndarray, steps: int, h_max: float = 10.0) -> np.ndarray:
-    """u: (N, B) fp64.  Returns h_steps (N, B)."""
+def dense_recurrence(W: np.ndarray, bias, alpha, u: np.ndarray, steps: int, h_max: float | None = 10.0) -> np.ndarray:
+    """u: (N, B) fp64.  Returns h_steps (N, B).  h_max None clamps only below (brain.py:178-182, 221)."""
+    h_max = np.inf if h_max is None else h_max
     bias = np.asarray(bias, dtype=np.float64)[:, None]
     alpha = np.asarray(alpha, dtype=np.float64)[:, None]
     h = np.zeros_like(u, dtype=np.float64)

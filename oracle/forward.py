@@ -5,9 +5,13 @@ It mirrors the reference's CPU code path op for op (sparse CSR matmul, index_add
 it is also the CPU baseline the GPU evaluator is timed beside:
 
   literal          ConnectomeRNN.forward, no-grad branch            chessfly/brain.py:211-223
+                   (literal_step: one update, brain.py:219-220)
   constants        ConnectomeRNN._constants                         chessfly/brain.py:238-252
   cone_f32         ConnectomeRNN.forward_io, float32 CPU branch      chessfly/brain.py:282-329 (295-329)
+                   (f32_step: one step of it, brain.py:313-327)
   cone_half        ConnectomeRNN._forward_io_half                   chessfly/brain.py:254-280, with the
+                   per-weight-version constants (deviation_constants, brain.py:257-270) and one step
+                   (deviation_step, brain.py:273-277 and 53-58) apart, and
                    float16 storage points (s, u, lo/hi/e/a, A_t values, d) and float16 arithmetic of the
                    fused deviation update (brain.py:53-58) emulated on the CPU
   model_forward    FlyChessNet.forward                               chessfly/model.py:95-105
@@ -88,17 +92,29 @@ def _sub(op, w: torch.Tensor) -> torch.Tensor:
                                    op.shape, check_invariants=False)
 
 
+def literal_step(b: BrainArrays, mat: torch.Tensor, alpha: torch.Tensor, h: torch.Tensor,
+                 drive: torch.Tensor) -> torch.Tensor:
+    """One update of the literal recurrence, h' = lerp(h, clamp(W h + drive, 0, H), alpha), with drive = u + b
+    (brain.py:219-220)."""
+    x = (mat @ h).add_(drive).clamp_(0, b.h_max)
+    return torch.lerp(h, x, alpha)
+
+
+def literal_operands(b: BrainArrays, dtype):
+    """W as a sparse CSR tensor and alpha (N, 1), in dtype, as the literal recurrence uses them (brain.py:215-216)."""
+    wdt = torch.float64 if dtype == torch.float64 else torch.float32
+    alpha = torch.sigmoid(b.alpha_logit.to(wdt)).to(dtype).unsqueeze(1)
+    return full_matrix(b, edge_weights(b, wdt).to(dtype)), alpha
+
+
 def literal(b: BrainArrays, u: torch.Tensor, steps: int) -> torch.Tensor:
     """Literal recurrence h <- lerp(h, clamp(W h + b + u, 0, H), alpha) from h = 0; u (N, B)."""
     dtype = u.dtype
-    wdt = torch.float64 if dtype == torch.float64 else torch.float32
-    alpha = torch.sigmoid(b.alpha_logit.to(wdt)).to(dtype).unsqueeze(1)
-    mat = full_matrix(b, edge_weights(b, wdt).to(dtype))
+    mat, alpha = literal_operands(b, dtype)
     drive = u + b.bias.to(dtype).unsqueeze(1)
     h = torch.zeros_like(drive)
     for _ in range(steps):
-        x = (mat @ h).add_(drive).clamp_(0, b.h_max)
-        h = torch.lerp(h, x, alpha)
+        h = literal_step(b, mat, alpha, h, drive)
     return h
 
 
@@ -138,23 +154,34 @@ def prepare_f32(b: BrainArrays, cone: Cone, dtype=torch.float32) -> dict:
             "out_idx": idx(cone.out_idx), "out_pos": idx(cone.out_pos), "out_src": idx(cone.out_src), **lists}
 
 
-def run_f32(prep: dict, steps: int, u_in: torch.Tensor) -> torch.Tensor:
-    """The per-position part of the float32 light-cone forward_io (brain.py:307-329, CPU branch)."""
+def f32_step(prep: dict, t: int, h: torch.Tensor | None, u_in: torch.Tensor) -> torch.Tensor:
+    """Step t of the float32 light cone (brain.py:313-327, CPU branch): the state of R_t from the state of
+    R_{t-1} (None at t = 1) and the input drive u_in (len(in_idx), B)."""
     batch = u_in.shape[1]
     cs, ks, mats, alpha = prep["cs"], prep["ks"], prep["mats"], prep["alpha"]
+    rows = prep["rows"][t]
+    if mats[t] is None:
+        x = ks[t].expand(-1, batch)
+    else:
+        x = (mats[t] @ h).add_(ks[t])
+    x = x.index_add(0, prep["u_pos"][t], u_in[prep["u_src"][t]])
+    x = x.clamp(0, prep["h_max"])
+    prev = cs[t - 1][rows].expand(-1, batch)
+    if len(prep["keep_next"][t]):
+        prev = prev.index_copy(0, prep["keep_next"][t], h[prep["keep_prev"][t]])
+    return torch.lerp(prev, x, alpha[rows])
+
+
+def run_f32(prep: dict, steps: int, u_in: torch.Tensor, states: list | None = None) -> torch.Tensor:
+    """The per-position part of the float32 light-cone forward_io (brain.py:307-329, CPU branch).  `states`, if
+    given, collects h_1..h_T (the state of R_t after each step)."""
+    batch = u_in.shape[1]
+    cs = prep["cs"]
     h = None
     for t in range(1, steps + 1):
-        rows = prep["rows"][t]
-        if mats[t] is None:
-            x = ks[t].expand(-1, batch)
-        else:
-            x = (mats[t] @ h).add_(ks[t])
-        x = x.index_add(0, prep["u_pos"][t], u_in[prep["u_src"][t]])
-        x = x.clamp(0, prep["h_max"])
-        prev = cs[t - 1][rows].expand(-1, batch)
-        if len(prep["keep_next"][t]):
-            prev = prev.index_copy(0, prep["keep_next"][t], h[prep["keep_prev"][t]])
-        h = torch.lerp(prev, x, alpha[rows])
+        h = f32_step(prep, t, h, u_in)
+        if states is not None:
+            states.append(h)
     out = cs[steps][prep["out_idx"]].expand(-1, batch)
     return out.index_copy(0, prep["out_pos"], h[prep["out_src"]])
 
@@ -170,22 +197,12 @@ def _h(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.float16).to(torch.float32)
 
 
-def cone_half(b: BrainArrays, cone: Cone, u_in: torch.Tensor, steps: int, half: bool = True) -> torch.Tensor:
-    """Deviation-from-rest forward_io (brain.py:254-280).
-
-    Constants come from the exact resting trajectory: k_full_t = (t > 1 ? W c_{t-1} : 0) + b and
-    c_t = lerp(c_{t-1}, clamp(k_full_t, 0, H), alpha); per step lo = -k, hi = H - k, e = k - clamp(k, 0, H)
-    and a = alpha[R_t] with k = k_full_t[R_t].  At run time s = A_t d_{t-1} plus the input on input rows,
-    x = clamp(s, lo, hi) + e, p = carried ? d_{t-1} : 0 and d_t = p + a (x - p); the result is
-    c_T[out_idx] + d_T at out_pos.
-
-    half=True emulates the reference's float16 storage in float32: lo/hi/e/a, the sub-matrix values, s, the
-    input and d are rounded to float16, s accumulates in float32, and every operation of the fused update is
-    rounded to float16 (c10::Half arithmetic).  half=False runs the same algebra in float64 with no
-    rounding, where it must equal the float64 light cone exactly up to summation order.
-    """
-    assert steps == cone.steps
-    batch = u_in.shape[1]
+def deviation_constants(b: BrainArrays, cone: Cone, half: bool = True) -> dict:
+    """What the deviation path caches per weight version (brain.py:257-270): from the exact resting trajectory,
+    k_full_t = (t > 1 ? W c_{t-1} : 0) + b and c_t = lerp(c_{t-1}, clamp(k_full_t, 0, H), alpha); per step
+    lo = -k, hi = H - k, e = k - clamp(k, 0, H), a = alpha[R_t] with k = k_full_t[R_t], the carried flags and A_t;
+    and c_T[out_idx].  half=True rounds lo/hi/e/a and A_t's values to float16 (the reference's storage);
+    half=False keeps everything float64."""
     dt = torch.float32 if half else torch.float64
     r = _h if half else (lambda v: v)
     w = edge_weights(b, dt)
@@ -194,7 +211,7 @@ def cone_half(b: BrainArrays, cone: Cone, u_in: torch.Tensor, steps: int, half: 
     bias = b.bias.to(dt).unsqueeze(1)
     c = torch.zeros(b.n, 1, dtype=dt)
     per_step = [None]
-    for t in range(1, steps + 1):
+    for t in range(1, cone.steps + 1):
         k_full = (mat @ c if t > 1 else torch.zeros_like(c)) + bias
         k = k_full[torch.as_tensor(cone.rows[t])]
         xc = k.clamp(0, b.h_max)
@@ -206,20 +223,49 @@ def cone_half(b: BrainArrays, cone: Cone, u_in: torch.Tensor, steps: int, half: 
         per_step.append((r(-k), r(b.h_max - k), r(k - xc), r(alpha[torch.as_tensor(cone.rows[t])]),
                          torch.as_tensor(cone.carried[t]).unsqueeze(1), sub))
         c = torch.lerp(c, k_full.clamp(0, b.h_max), alpha)
-    c_out = c[torch.as_tensor(cone.out_idx)]
-    u = r(u_in.to(dt))
+    return {"per_step": per_step, "c_out": c[torch.as_tensor(cone.out_idx)], "half": half, "dtype": dt}
+
+
+def deviation_step(consts: dict, cone: Cone, t: int, d: torch.Tensor | None, u: torch.Tensor) -> torch.Tensor:
+    """Step t of the deviation path (brain.py:273-277 with FUSED_DEVIATION, brain.py:53-58): s = A_t d_{t-1}
+    plus the input on input rows, x = clamp(s, lo, hi) + e, p = carried ? d_{t-1} : 0, d_t = p + a (x - p).
+    d is the deviation of R_{t-1} (None at t = 1), u the input drive (len(in_idx), B) in the path's storage."""
+    r = _h if consts["half"] else (lambda v: v)
+    dt = consts["dtype"]
+    batch = u.shape[1]
+    lo, hi, e, a, carried, sub = consts["per_step"][t]
+    s = r(sub @ d) if sub is not None else torch.zeros(len(cone.rows[t]), batch, dtype=dt)
+    pos = torch.as_tensor(cone.u_pos[t])
+    s = s.clone()
+    s[pos] = r(s[pos] + u[torch.as_tensor(cone.u_src[t])])
+    x = r(torch.minimum(torch.maximum(s, lo), hi) + e)
+    p = torch.where(carried, d[torch.as_tensor(cone.prev_row[t])], torch.zeros_like(s)) if d is not None \
+        else torch.zeros_like(s)
+    return r(p + r(a * r(x - p)))
+
+
+def cone_half(b: BrainArrays, cone: Cone, u_in: torch.Tensor, steps: int, half: bool = True,
+              states: list | None = None) -> torch.Tensor:
+    """Deviation-from-rest forward_io (brain.py:254-280): deviation_constants, then deviation_step for t = 1..T;
+    the result is c_T[out_idx] + d_T at out_pos.
+
+    half=True emulates the reference's float16 storage in float32: lo/hi/e/a, the sub-matrix values, s, the
+    input and d are rounded to float16, s accumulates in float32, and every operation of the fused update is
+    rounded to float16 (c10::Half arithmetic).  half=False runs the same algebra in float64 with no
+    rounding, where it must equal the float64 light cone exactly up to summation order.  `states`, if given,
+    collects d_1..d_T.
+    """
+    assert steps == cone.steps
+    batch = u_in.shape[1]
+    consts = deviation_constants(b, cone, half)
+    r = _h if half else (lambda v: v)
+    u = r(u_in.to(consts["dtype"]))
     d = None
     for t in range(1, steps + 1):
-        lo, hi, e, a, carried, sub = per_step[t]
-        s = r(sub @ d) if sub is not None else torch.zeros(len(cone.rows[t]), batch, dtype=dt)
-        pos = torch.as_tensor(cone.u_pos[t])
-        s = s.clone()
-        s[pos] = r(s[pos] + u[torch.as_tensor(cone.u_src[t])])
-        x = r(torch.minimum(torch.maximum(s, lo), hi) + e)
-        p = torch.where(carried, d[torch.as_tensor(cone.prev_row[t])], torch.zeros_like(s)) if d is not None \
-            else torch.zeros_like(s)
-        d = r(p + r(a * r(x - p)))
-    out = c_out.expand(-1, batch).clone()
+        d = deviation_step(consts, cone, t, d, u)
+        if states is not None:
+            states.append(d)
+    out = consts["c_out"].expand(-1, batch).clone()
     pos = torch.as_tensor(cone.out_pos)
     out[pos] += d[torch.as_tensor(cone.out_src)]
     return out

@@ -84,13 +84,29 @@ def test_evaluator_outputs_checks_arguments_on_host(lib):
     assert b"wdl" in lib.fly_last_error()
 
 
-def test_gather_probe_checks_arguments_on_host(lib):
-    """The measurement probe refuses null pointers and out-of-range sizes before launching anything."""
-    assert lib.fly_gather_probe(None, 1024, 128, 128, None, 10, None, None) == 1
+def test_probe_library_is_apart_and_checks_arguments_on_host():
+    """The bench's measurement probes live in libflyprobe.so, not in the evaluator's ABI: libflyeval.so exports
+    no probe, and the probe library refuses null pointers and out-of-range sizes before launching anything."""
+    from chessfly import _hip
+    lib = _hip.load()
+    assert not hasattr(lib, "fly_gather_probe")
+    path = os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so")
+    if not os.path.exists(path):
+        subprocess.run(["make", "-C", os.path.join(REPO, "alpha-fly_amd", "csrc"), "-j8"], check=True)
+    probe = ctypes.CDLL(path)
+    probe.flyprobe_last_error.restype = ctypes.c_char_p
+    i64, p_ = ctypes.c_int64, ctypes.c_void_p
+    probe.flyprobe_random_gather.argtypes = [p_, i64, i64, i64, p_, i64, p_, p_]
+    probe.flyprobe_replay_step.argtypes = [p_, p_, i64, i64, p_, i64, i64, i64, ctypes.c_int32, p_, p_]
+    assert probe.flyprobe_random_gather(None, 1024, 128, 128, None, 10, None, None) == 1
     buf = ctypes.create_string_buffer(16)
     p = ctypes.addressof(buf)
-    assert lib.fly_gather_probe(p, 1 << 31, 128, 128, p, 10, p, None) == 1
-    assert lib.fly_gather_probe(p, 1024, 64, 128, p, 10, p, None) == 1
-    assert b"row_bytes" in lib.fly_last_error()
-    assert lib.fly_gather_probe(p, 1024, 128, 96, p, 10, p, None) == 1
-    assert b"read_bytes" in lib.fly_last_error()
+    assert probe.flyprobe_random_gather(p, 1 << 31, 128, 128, p, 10, p, None) == 1
+    assert probe.flyprobe_random_gather(p, 1024, 64, 128, p, 10, p, None) == 1
+    assert b"row_bytes" in probe.flyprobe_last_error()
+    assert probe.flyprobe_random_gather(p, 1024, 128, 96, p, 10, p, None) == 1
+    assert b"read_bytes" in probe.flyprobe_last_error()
+    assert probe.flyprobe_replay_step(None, None, 10, 10, None, 10, 64, 64, 1, None, None) == 1
+    assert b"null" in probe.flyprobe_last_error()
+    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 32, 64, 1, p, None) == 1
+    assert b"layout" in probe.flyprobe_last_error()

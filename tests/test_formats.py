@@ -122,48 +122,9 @@ def test_load_net_reads_a_checkpoint(tmp_path):
         assert torch.equal(got.state_dict()[k], v), k
 
 
-def _write_release(d, annotations, transmitters, weights):
-    import pyarrow as pa
-    import pyarrow.feather as feather
-    feather.write_feather(pa.table(annotations), os.path.join(d, "body-annotations.feather"))
-    feather.write_feather(pa.table(transmitters), os.path.join(d, "body-neurotransmitters.feather"))
-    feather.write_feather(pa.table(weights), os.path.join(d, "connectome-weights.feather"), chunksize=5)
-
-
-def test_load_malecns_parses_local_release_files(tmp_path):
-    """Bodies without a super class are dropped, the rest sorted by id; pairs below min_syn and pairs touching
-    a dropped body are dropped, repeated pairs summed; edges in (post, pre) order with the presynaptic sign."""
-    from chessfly.connectome import load_malecns
-    d = str(tmp_path)
-    ann = {"bodyId": [50, 10, 30, 20, 40, 60], "superclass": ["vnc_motor", "ol_sensory", None, "central", "cb_sensory",
-                                                              "descending_neuron"],
-           "type": ["m", None, "x", "c", "s", "dn"]}
-    nts = {"body": [10, 20, 40, 50, 60, 99], "consensus_nt": ["acetylcholine", "gaba", "glutamate", "dopamine",
-                                                              None, "gaba"]}
-    wts = {"body_pre": [10, 20, 20, 40, 10, 30, 50, 60, 10, 40, 20, 60],
-           "body_post": [20, 50, 50, 10, 50, 10, 60, 10, 20, 40, 40, 20],
-           "weight": [5, 2, 2, 9, 1, 7, 3, 4, 4, 6, 3, 3]}
-    _write_release(d, ann, nts, wts)
-    conn = load_malecns(d, min_syn=3)
-    # the same parse written out by hand
-    ids = [10, 20, 40, 50, 60]
-    flow = {10: "afferent", 20: "intrinsic", 40: "afferent", 50: "efferent", 60: "intrinsic"}
-    nt = {10: "acetylcholine", 20: "gaba", 40: "glutamate", 50: "dopamine", 60: "unclear"}
-    sign = {"acetylcholine": 1.0, "gaba": -1.0, "glutamate": -1.0, "dopamine": 1.0, "unclear": 1.0}
-    assert conn.neurons["root_id"].tolist() == ids
-    assert conn.neurons["flow"].tolist() == [flow[i] for i in ids]
-    assert conn.neurons["nt"].tolist() == [nt[i] for i in ids]
-    syn = {}
-    for a, b, w in zip(wts["body_pre"], wts["body_post"], wts["weight"]):
-        if a in ids and b in ids and w >= 3:
-            syn[(a, b)] = syn.get((a, b), 0) + w
-    node = {b: i for i, b in enumerate(ids)}
-    want = sorted((node[b], node[a], float(w), sign[nt[a]]) for (a, b), w in syn.items())
-    got = list(zip(conn.post.tolist(), conn.pre.tolist(), conn.syn_count.tolist(), conn.sign.tolist()))
-    assert got == want
-    cached = load_malecns(d, min_syn=3)                       # second call: from the pickle-free cache
-    assert cached.neurons.equals(conn.neurons.astype(cached.neurons.dtypes.to_dict()))
-    assert torch.equal(cached.pre, conn.pre) and torch.equal(cached.syn_count, conn.syn_count)
-    with pytest.raises(FileNotFoundError, match="connectome-weights"):
-        os.remove(os.path.join(d, "connectome-weights.feather"))
-        load_malecns(d, min_syn=4)
+def test_load_net_requires_the_connectome(tmp_path):
+    """The reference's load_net parses the MaleCNS release when no graph is given; this package has no reader
+    for it, so the graph must be passed (and nothing is read before that is checked)."""
+    from chessfly.model import load_net
+    with pytest.raises(ValueError, match="conn="):
+        load_net(os.path.join(str(tmp_path), "missing.pt"), device="cpu")

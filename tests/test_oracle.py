@@ -87,6 +87,64 @@ def test_literal_matches_dense_closed_form_with_repeated_pairs():
         assert np.abs(ref).sum() > 0
 
 
+def test_unbounded_activity_matches_dense_closed_form():
+    """h_max=None (brain.py:178-182, 221): the clamp keeps only its lower bound.  Biases large enough that
+    activity passes 10, so a bound left in place would show; the light cone with h_max None is the same
+    function as the literal recurrence."""
+    conn = tiny_connectome(60, 900, 4).shuffled(2)
+    lg, b, al = random_params(conn, 9, bias_mean=6.0, bias_sd=4.0)
+    ba = brain_arrays(conn, 2.5, lg, b, al, h_max=None, dtype=torch.float64)
+    u = torch.randn(conn.n_neurons, 4, dtype=torch.float64, generator=torch.Generator().manual_seed(3)) * 3
+    W = brute.dense_matrix(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), F.edge_weights(ba, torch.float64).numpy())
+    alpha = 1 / (1 + np.exp(-al.astype(np.float64)))
+    for steps in (1, 3, 6):
+        ref = brute.dense_recurrence(W, b.astype(np.float64), alpha, u.numpy(), steps, h_max=None)
+        got = F.literal(ba, u, steps).numpy()
+        np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+        assert ref.max() > 10.0                       # the missing upper clamp matters here
+        bounded = brute.dense_recurrence(W, b.astype(np.float64), alpha, u.numpy(), steps, h_max=10.0)
+        assert np.abs(bounded - ref).max() > 1e-3
+    in_idx, out_idx = np.arange(0, 8), np.arange(45, 60)
+    for steps in (2, 5):
+        cone = _cone(conn, in_idx, out_idx, steps)
+        u_in = u[torch.as_tensor(in_idx)]
+        full = torch.zeros_like(u).index_add(0, torch.as_tensor(in_idx), u_in)
+        torch.testing.assert_close(F.cone_f32(ba, cone, u_in, steps),
+                                   F.literal(ba, full, steps)[torch.as_tensor(out_idx)], rtol=1e-9, atol=1e-10)
+
+
+def test_per_step_functions_compose_to_the_pinned_forwards():
+    """literal_step, f32_step and deviation_step are the loop bodies of the pinned forwards: their states,
+    collected step by step, end in the pinned outputs, and the first deviation step from d_0 = None matches
+    its definition (s = input on input rows only, nothing carried)."""
+    conn = tiny_connectome(120, 700, seed=3)
+    lg, b, al = random_params(conn, 11)
+    ba = brain_arrays(conn, 3.0, lg, b, al, dtype=torch.float64)
+    in_idx, out_idx = np.arange(0, 9), np.arange(100, 120)
+    steps = 4
+    cone = _cone(conn, in_idx, out_idx, steps)
+    u_in = torch.randn(9, 5, dtype=torch.float64, generator=torch.Generator().manual_seed(9))
+    hs, ds = [], []
+    out32 = F.cone_f32(ba, cone, u_in, steps)
+    F.run_f32(F.prepare_f32(ba, cone, torch.float64), steps, u_in, states=hs)
+    F.cone_half(ba, cone, u_in, steps, half=False, states=ds)
+    assert [h.shape[0] for h in hs] == [len(cone.rows[t]) for t in range(1, steps + 1)]
+    # deviation + resting trajectory = state, step by step (the deviation algebra, exact in float64)
+    prep = F.prepare_f32(ba, cone, torch.float64)
+    for t in range(1, steps + 1):
+        c = prep["cs"][t][torch.as_tensor(cone.rows[t])]
+        torch.testing.assert_close(ds[t - 1] + c, hs[t - 1], rtol=1e-10, atol=1e-12)
+    last = torch.as_tensor(cone.out_src)
+    torch.testing.assert_close(out32[torch.as_tensor(cone.out_pos)], hs[-1][last], rtol=0, atol=0)
+    u = torch.zeros(conn.n_neurons, 5, dtype=torch.float64).index_add(0, torch.as_tensor(in_idx), u_in)
+    mat, alpha = F.literal_operands(ba, torch.float64)
+    drive = u + ba.bias.unsqueeze(1)
+    h = torch.zeros_like(drive)
+    for _ in range(steps):
+        h = F.literal_step(ba, mat, alpha, h, drive)
+    torch.testing.assert_close(h, F.literal(ba, u, steps), rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("steps", [1, 2, 4, 6])
 def test_cone_forward_equals_literal_recurrence_fp64(steps):
     """The reference's light-cone invariant (tests/test_core.py:309-338): forward_io == forward[out_idx]."""
