@@ -42,7 +42,15 @@ Profiler &profiler() {
 
 void set_error(const std::string &msg) { g_last_error = msg; }
 
+namespace {
+thread_local int g_quiet = 0;
+}  // namespace
+
+NoLaunchEvents::NoLaunchEvents() { ++g_quiet; }
+NoLaunchEvents::~NoLaunchEvents() { --g_quiet; }
+
 LaunchTimer::LaunchTimer(int kernel_class, hipStream_t st) : cls_(kernel_class), st_(st) {
+  if (g_quiet) return;
   Profiler &p = profiler();
   std::lock_guard<std::mutex> lock(p.mu);
   if (!p.on) return;

@@ -147,6 +147,16 @@ class LaunchTimer {
   hipEvent_t start_ = nullptr;
 };
 
+// While one exists on a thread, LaunchTimer records nothing on that thread (and creates no events): the entry
+// point that allocates nothing runs under it.
+class NoLaunchEvents {
+ public:
+  NoLaunchEvents();
+  ~NoLaunchEvents();
+  NoLaunchEvents(const NoLaunchEvents &) = delete;
+  NoLaunchEvents &operator=(const NoLaunchEvents &) = delete;
+};
+
 // Tuning knobs set through fly_set_tuning.
 struct Tuning {
   int vec = 0;    // elements per lane of the step kernel, 0 = automatic

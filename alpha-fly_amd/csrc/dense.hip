@@ -22,6 +22,8 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
+#include <string>
 
 namespace fly {
 
@@ -570,51 +572,134 @@ extern "C" int fly_head(const fly_dense *d, const float *r, int64_t ldr, int64_t
   });
 }
 
+namespace fly {
+namespace {
+
+// Scratch of one block of `blk` boards of the model forward: the encoder's output u (float32, padded rows), the
+// two state buffers, then the encoder's operand split or the head's (they never live at once).
+size_t model_ws_block(const fly_plan &plan, const fly_dense &d, int64_t blk) {
+  const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float);
+  return align256((size_t)plan.n_in * state_ld(blk, sizeof(float)) * sizeof(float)) +
+         align256(2 * (size_t)plan.max_rows * (size_t)state_ld(blk, es) * es + 256) +
+         std::max(encoder_ws(d, blk), head_ws(d, blk));
+}
+
+void check_model_args(const fly_plan *plan, const fly_dense *d, const void *x, int64_t ldx, int64_t batch,
+                      const float *logits, const float *wdl) {
+  check_plan_device(plan);
+  check_dense(d);
+  FLY_REQUIRE(!plan->full, "the model forward needs a light-cone plan");
+  FLY_REQUIRE(d->n_out == plan->n_out && d->n_in == plan->n_in, "dense maps and plan disagree on sizes");
+  FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+  if (batch) FLY_REQUIRE(x && ldx >= d->k && logits && wdl, "bad argument");
+}
+
+// The forward in blocks of at most `blk` boards, each using the scratch at ws (model_ws_block(blk) bytes).
+void model_forward_blocks(const fly_plan &plan, const fly_dense &d, const void *x, bool x_f16, int64_t ldx,
+                          int64_t batch, float input_gain, float *logits, float *wdl, void *ws, int64_t blk,
+                          hipStream_t st) {
+  char *base = static_cast<char *>(ws);
+  float *u = reinterpret_cast<float *>(base);
+  base += align256((size_t)plan.n_in * state_ld(blk, sizeof(float)) * sizeof(float));
+  void *states = base;
+  const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float);
+  base += align256(2 * (size_t)plan.max_rows * (size_t)state_ld(blk, es) * es + 256);
+  void *scratch_ops = base;  // the encoder's operand split, then the head's
+  const size_t xelem = x_f16 ? sizeof(_Float16) : sizeof(float);
+  for (int64_t c0 = 0; c0 < batch; c0 += blk) {
+    const int64_t nb = std::min(blk, batch - c0);
+    const void *xb = static_cast<const char *>(x) + (size_t)c0 * ldx * xelem;
+    float *lb = logits + c0 * d.n_moves, *wb = wdl + c0 * 3;
+    const int64_t ldu = state_ld(nb, sizeof(float));
+    const int64_t lds = state_ld(nb, es);
+    // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
+    run_encoder(d, xb, x_f16, ldx, nb, input_gain, u, nullptr, ldu, scratch_ops, st);
+    if (plan.mode == FLY_MODE_DEVIATION_F16) {
+      const _Float16 *fin = run_cone_steps<_Float16, float>(plan, u, ldu, nb, true, states, st);
+      run_head<_Float16>(d, fin, lds, plan.out_src.p, plan.cbase.p, nb, lb, wb, scratch_ops, st);
+    } else {
+      const float *fin = run_cone_steps<float, float>(plan, u, ldu, nb, true, states, st);
+      run_head<float>(d, fin, lds, plan.out_src.p, plan.cbase.p, nb, lb, wb, scratch_ops, st);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace fly
+
+// ---- the forward that allocates nothing -------------------------------------------------------------------------
+// Its scratch is one file-scope device array per GPU (FLY_STATIC_SCRATCH_BYTES), held until the process ends.  In
+// host code `scratch` names a host-side stand-in, never device memory: the array's address on the current device
+// comes from hipGetSymbolAddress, once per device, and only that address is passed to kernels.
+static __device__ __align__(256) char scratch[FLY_STATIC_SCRATCH_BYTES];
+
+namespace fly {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the current device (looked up on the first call on that device).
+void *static_scratch() {
+  const int dev = current_device();
+  FLY_REQUIRE(dev >= 0 && dev < kMaxDevices, "device id out of range for the static scratch");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    FLY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    FLY_REQUIRE(p != nullptr && aligned(p, 256), "the static scratch has no usable device address");
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+// Boards per block that fit the static scratch: the whole batch if it fits, else the largest multiple of 64
+// that does; 0 when not even min(batch, 64) boards fit.
+int64_t static_block(const fly_plan &plan, const fly_dense &d, int64_t batch) {
+  const size_t cap = FLY_STATIC_SCRATCH_BYTES;
+  if (model_ws_block(plan, d, batch) <= cap) return batch;
+  for (int64_t b = (batch - 1) / 64 * 64; b >= 64; b -= 64)
+    if (model_ws_block(plan, d, b) <= cap) return b;
+  return 0;
+}
+
+}  // namespace
+}  // namespace fly
+
+extern "C" int fly_model_forward_static(const fly_plan *plan, const fly_dense *d, const void *x, int32_t x_f16,
+                                        int64_t ldx, int64_t batch, float input_gain, float *logits, float *wdl,
+                                        void *stream) {
+  return guard([&] {
+    check_model_args(plan, d, x, ldx, batch, logits, wdl);
+    if (!batch) return;
+    const int64_t blk = static_block(*plan, *d, batch);
+    FLY_REQUIRE(blk > 0, "fly_model_forward_static: one block of " + std::to_string(std::min<int64_t>(batch, 64)) +
+                             " boards needs " + std::to_string(model_ws_block(*plan, *d, std::min<int64_t>(batch, 64))) +
+                             " bytes of scratch, above the static array's " +
+                             std::to_string((size_t)FLY_STATIC_SCRATCH_BYTES) + " (use fly_model_forward)");
+    void *ws = static_scratch();
+    NoLaunchEvents quiet;   // the profiler's launch events would be created here: this entry point creates nothing
+    model_forward_blocks(*plan, *d, x, x_f16 != 0, ldx, batch, input_gain, logits, wdl, ws, blk, as_stream(stream));
+  });
+}
+
 extern "C" size_t fly_model_workspace(const fly_plan *plan, const fly_dense *d, int64_t batch) {
   if (!plan || !d) return 0;
-  const int64_t blk = io_block(*plan, batch);   // boards per block (the whole batch below 2 GiB of state)
-  return align256((size_t)plan->n_in * state_ld(blk, sizeof(float)) * sizeof(float)) +
-         align256(io_workspace(*plan, blk)) + std::max(encoder_ws(*d, blk), head_ws(*d, blk));
+  // boards per block: the whole batch while the state stays below 2 GiB (io_block)
+  return model_ws_block(*plan, *d, io_block(*plan, batch));
 }
 
 extern "C" int fly_model_forward(const fly_plan *plan, const fly_dense *d, const void *x, int32_t x_f16, int64_t ldx,
                                  int64_t batch, float input_gain, float *logits, float *wdl, void *ws, size_t ws_bytes,
                                  void *stream) {
   return guard([&] {
-    check_plan_device(plan);
-    check_dense(d);
-    FLY_REQUIRE(!plan->full, "the model forward needs a light-cone plan");
-    FLY_REQUIRE(d->n_out == plan->n_out && d->n_in == plan->n_in, "dense maps and plan disagree on sizes");
-    FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+    check_model_args(plan, d, x, ldx, batch, logits, wdl);
     if (!batch) return;
-    FLY_REQUIRE(x && ldx >= d->k && logits && wdl, "bad argument");
     FLY_REQUIRE(ws && ws_bytes >= fly_model_workspace(plan, d, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
-    hipStream_t st = as_stream(stream);
     // Boards run in blocks whose state stays below 2 GiB (one block below about 6,400 boards in float16).
-    const int64_t blk = io_block(*plan, batch);
-    char *base = static_cast<char *>(ws);
-    float *u = reinterpret_cast<float *>(base);
-    base += align256((size_t)plan->n_in * state_ld(blk, sizeof(float)) * sizeof(float));
-    void *states = base;
-    base += align256(io_workspace(*plan, blk));
-    void *scratch = base;  // the encoder's operand split, then the head's
-    const size_t xelem = x_f16 ? sizeof(_Float16) : sizeof(float);
-    for (int64_t c0 = 0; c0 < batch; c0 += blk) {
-      const int64_t nb = std::min(blk, batch - c0);
-      const void *xb = static_cast<const char *>(x) + (size_t)c0 * ldx * xelem;
-      float *lb = logits + c0 * d->n_moves, *wb = wdl + c0 * 3;
-      const int64_t ldu = state_ld(nb, sizeof(float));
-      const int64_t lds = state_ld(nb, plan->mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float));
-      // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
-      run_encoder(*d, xb, x_f16 != 0, ldx, nb, input_gain, u, nullptr, ldu, scratch, st);
-      if (plan->mode == FLY_MODE_DEVIATION_F16) {
-        const _Float16 *fin = run_cone_steps<_Float16, float>(*plan, u, ldu, nb, true, states, st);
-        run_head<_Float16>(*d, fin, lds, plan->out_src.p, plan->cbase.p, nb, lb, wb, scratch, st);
-      } else {
-        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, true, states, st);
-        run_head<float>(*d, fin, lds, plan->out_src.p, plan->cbase.p, nb, lb, wb, scratch, st);
-      }
-    }
+    model_forward_blocks(*plan, *d, x, x_f16 != 0, ldx, batch, input_gain, logits, wdl, ws, io_block(*plan, batch),
+                         as_stream(stream));
   });
 }

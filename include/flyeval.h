@@ -192,6 +192,19 @@ int fly_model_forward(const fly_plan *plan, const fly_dense *dense, const void *
                       int64_t batch, float input_gain, float *logits_dev, float *wdl_dev, void *workspace_dev,
                       size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): fly_model_forward with the same inputs, outputs and
+ * results, whose scratch is a static device array of FLY_STATIC_SCRATCH_BYTES that the library holds on each GPU it
+ * runs on until the process ends; the call allocates nothing.  Boards run in blocks sized to that array: the full-scale
+ * network (166,700 neurons) in blocks of 256 boards for FLY_MODE_DEVIATION_F16 and 128 for FLY_MODE_F32.
+ * FLY_ERR_INVALID when not even a block of min(batch, 64) boards fits.  Every call on one GPU shares that GPU's array
+ * and nothing in it must start at zero; calls that overlap on one GPU (other streams or threads) race, so the caller
+ * serialises them.  Launches under it record no profiler events. */
+#define FLY_STATIC_SCRATCH_BYTES ((size_t)256 << 20)
+int fly_model_forward_static(const fly_plan *plan, const fly_dense *dense, const void *x_dev, int32_t x_f16,
+                             int64_t ldx, int64_t batch, float input_gain, float *logits_dev, float *wdl_dev,
+                             void *stream);
+
 /* What the search's evaluate callable returns (chessfly/model.py:120-128), from logits (batch, n_moves) and
  * wdl (batch, 3), float32 row-major:
  *   values[b] = P(win) - P(loss) under the softmax of wdl[b] (expected_value, model.py:107-110);
