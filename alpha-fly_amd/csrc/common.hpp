@@ -168,6 +168,7 @@ struct Tuning {
   int rows_vec = 0;  // elements per lane of row-slot steps on half states: 8 (16 bytes) or 16 (32 bytes), 0 = automatic
   int spmm_groups = 0;  // lane groups of the training SpMM on 16-byte lanes (2, 4, 8), 0 = automatic
   int gemm_tile = 0;    // dense-map workgroup tile: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, 0 = automatic
+  int step_lds = 0;     // bytes of LDS each state-step workgroup reserves (caps waves per SIMD), 0 = none
 };
 Tuning &tuning();
 

@@ -30,6 +30,19 @@ int flyprobe_replay_step(const int32_t *rowptr_dev, const void *pairs_dev, int64
                          const void *xprev_dev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
                          void *sink_dev, void *stream);
 
+/* params (nrows 32-byte row records) with zero constants and the given prev (position in R_{t-1}, -1: not carried)
+ * and usrc (input row, -1: none), as fly_cone_step exports them: the row reads of a replay with I/O. */
+int flyprobe_pack_params(const int32_t *prev_dev, const int32_t *usrc_dev, int64_t nrows, void *params_dev,
+                         void *stream);
+
+/* The replay with the step's row I/O: as flyprobe_replay_step, plus each row's constants, carried state and input
+ * drive u (n_in, ldu float32, padded like the model forward's; NULL: none) read and the new state xout (nrows, ldx)
+ * written, without the arithmetic of the sum. */
+int flyprobe_replay_step_io(const int32_t *rowptr_dev, const void *pairs_dev, const void *params_dev, int64_t nrows,
+                            int64_t nnz, const void *xprev_dev, int64_t prev_rows, int64_t ldx, const float *u_dev,
+                            int64_t n_in, int64_t ldu, void *xout_dev, int64_t batch, int32_t state_f16,
+                            void *stream);
+
 /* Uniform-random row gathers in the state step's lane layout: n reads of read_bytes (128: 8 rows per wave
  * instruction; 64: 16 rows) at byte offset idx[e] * row_bytes (16 bytes per lane) of base (`bytes` long).
  * Offsets past `bytes` read zeros.  sink: 256 floats, written only if the data sum to a sentinel value. */

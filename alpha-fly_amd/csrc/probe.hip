@@ -1,9 +1,11 @@
 // libflyprobe.so: measurement probes for bench.py, built apart from the evaluator library.
 //
-// flyprobe_replay_step runs the state step's own kernels (step_kernels.hpp) built with REPLAY = true: the same
+// flyprobe_replay_step runs the state step's own kernels (step_kernels.hpp) built with REPLAY = 1: the same
 // launch shape, wave numbering, per-row pair records and buffer-offset gathers as the evaluator's step on the
 // same matrix and state layout, without the arithmetic, the row inputs or the stores.  Its time is what the
-// step's memory stream alone costs, which is the ceiling the fused step is measured against.
+// step's gather stream alone costs, which is the ceiling the fused step is measured against.
+// flyprobe_replay_step_io (REPLAY = 2) adds the step's row reads (carried state, input drive, constants) and its
+// stores: everything but the arithmetic of the sum.
 //
 // flyprobe_random_gather reads rows picked uniformly at random in the same lane layout (8 rows of 128 bytes
 // per wave load, or 16 of 64 bytes): the gather rate of a working set of a given size with no reuse beyond
@@ -33,6 +35,12 @@ int probe_guard(F &&f) {
   return 1;
 }
 
+__global__ void k_pack_params(const int32_t *__restrict__ prev, const int32_t *__restrict__ usrc, int64_t n,
+                              RowParam *__restrict__ out) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) out[i] = RowParam{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, prev[i], usrc[i]};
+}
+
 __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__restrict__ val, int64_t nnz,
                              int2 *__restrict__ out) {
   const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -41,8 +49,8 @@ __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__res
 
 // The evaluator's default shapes only (no tuning knobs): lane groups of 16-byte lanes, or row slots of 16- or
 // 32-byte lanes, in groups of 8 lanes with 4 rounds in flight.
-template <typename S>
-void replay(StepArgs<S, S> a, double avg_nnz, hipStream_t st) {
+template <int MODE, typename S, typename U>
+void replay(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   const StepShape sh = shape_step(a, avg_nnz, Tuning{});
   const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "replay grid too large");
@@ -51,11 +59,11 @@ void replay(StepArgs<S, S> a, double avg_nnz, hipStream_t st) {
   FLY_REQUIRE(sh.groups == 8, "no replay for this launch shape");
   if (sh.rows_mode && sh.v == 2 * kV16) {
     if constexpr (sizeof(S) == 2)
-      hipLaunchKernelGGL((k_state_step_rows<S, S, 2 * kV16, 8, 4, false, true>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((k_state_step_rows<S, U, 2 * kV16, 8, 4, sizeof(S) == 4, MODE>), grid, block, 0, st, a);
   } else if (sh.rows_mode && sh.v == kV16) {
-    hipLaunchKernelGGL((k_state_step_rows<S, S, kV16, 8, 4, false, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step_rows<S, U, kV16, 8, 4, sizeof(S) == 4, MODE>), grid, block, 0, st, a);
   } else if (!sh.rows_mode && sh.v == kV16) {
-    hipLaunchKernelGGL((k_state_step_grouped<S, S, kV16, 8, 4, false, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step_grouped<S, U, kV16, 8, 4, sizeof(S) == 4, MODE>), grid, block, 0, st, a);
   } else {
     FLY_REQUIRE(false, "no replay for this launch shape");
   }
@@ -129,7 +137,54 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       a.nrows = (int32_t)nrows;
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
-      replay<S>(a, (double)nnz / (double)nrows, as_stream(stream));
+      replay<1>(a, (double)nnz / (double)nrows, as_stream(stream));
+    };
+    if (state_f16)
+      run(_Float16(0));
+    else
+      run(0.0f);
+  });
+}
+
+extern "C" int flyprobe_pack_params(const int32_t *prev, const int32_t *usrc, int64_t nrows, void *params,
+                                    void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(nrows >= 0 && nrows < (int64_t)INT32_MAX, "nrows out of range");
+    if (!nrows) return;
+    FLY_REQUIRE(prev && usrc && params && aligned(params, 16), "null or misaligned argument");
+    hipLaunchKernelGGL(k_pack_params, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), prev, usrc, nrows,
+                       static_cast<RowParam *>(params));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error{1, std::string("params launch: ") + hipGetErrorString(e)};
+  });
+}
+
+extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs, const void *params, int64_t nrows,
+                                       int64_t nnz, const void *xprev, int64_t prev_rows, int64_t ldx, const float *u,
+                                       int64_t n_in, int64_t ldu, void *xout, int64_t batch, int32_t state_f16,
+                                       void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(rowptr && pairs && params && xprev && xout, "null argument");
+    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
+    FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
+    FLY_REQUIRE(!u || (n_in > 0 && ldu >= batch), "bad input drive");
+    auto run = [&](auto zero) {
+      using S = decltype(zero);
+      StepArgs<S, float> a{};
+      a.rowptr = rowptr;
+      a.colval = static_cast<const int2 *>(pairs);
+      a.params = static_cast<const RowParam *>(params);
+      a.xprev = static_cast<const S *>(xprev);
+      a.ldx = ldx;
+      a.u = u;
+      a.ldu = ldu;
+      a.u_padded = 1;   // the model forward's drive: the library's padded workspace
+      a.xout = static_cast<S *>(xout);
+      a.ldo = ldx;
+      a.nrows = (int32_t)nrows;
+      a.batch = (int32_t)batch;
+      a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
+      replay<2>(a, (double)nnz / (double)nrows, as_stream(stream));
     };
     if (state_f16)
       run(_Float16(0));

@@ -24,43 +24,45 @@ void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, h
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
   constexpr bool kTL = sizeof(S) == 4;
+  // the kernels use no LDS: a reservation only caps the workgroups (waves per SIMD) a CU runs at once
+  const unsigned lds = (unsigned)std::max(0, tuning().step_lds);
   if constexpr (V * sizeof(S) == 32) {
     // 32-byte lanes exist for the row slots of half states only (state_step picks them for nothing else)
-    hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, lds, st, a);
     return;
   }
   if constexpr (V * sizeof(S) == 16) {
     if (rows_mode) {
       if (unroll <= 4) {   // 4 measured best for the row slots
-        if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
-        else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, 4, kTL>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, 4, kTL>), grid, block, 0, st, a);
+        if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, lds, st, a);
+        else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, 4, kTL>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, 4, kTL>), grid, block, lds, st, a);
       } else {
-        if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 8, kTL>), grid, block, 0, st, a);
-        else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, 8, kTL>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, 8, kTL>), grid, block, 0, st, a);
+        if (groups == 8) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 8, kTL>), grid, block, lds, st, a);
+        else if (groups == 4) hipLaunchKernelGGL((k_state_step_rows<S, U, V, 4, 8, kTL>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((k_state_step_rows<S, U, V, 2, 8, kTL>), grid, block, lds, st, a);
       }
       return;
     }
     if (groups == 8) {
-      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 8, 4, kTL>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 8, 4, kTL>), grid, block, lds, st, a);
       return;
     }
     if (groups == 4) {
-      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 4, 8, kTL>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 4, 8, kTL>), grid, block, lds, st, a);
       return;
     }
     if (groups == 2) {
-      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 2, 8, kTL>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((k_state_step_grouped<S, U, V, 2, 8, kTL>), grid, block, lds, st, a);
       return;
     }
   }
   if (unroll >= 32)
-    hipLaunchKernelGGL((k_state_step<S, U, V, 32, kTL>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step<S, U, V, 32, kTL>), grid, block, lds, st, a);
   else if (unroll >= 16)   // 8 (also for 0) measured best for one non-zero per wave
-    hipLaunchKernelGGL((k_state_step<S, U, V, 16, kTL>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step<S, U, V, 16, kTL>), grid, block, lds, st, a);
   else
-    hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTL>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTL>), grid, block, lds, st, a);
 }
 
 template <typename S, typename U>
@@ -350,6 +352,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "tiles") tuning().tiles = (int)value;
     else if (k == "spmm_groups") tuning().spmm_groups = (int)value;
     else if (k == "gemm_tile") tuning().gemm_tile = (int)value;
+    else if (k == "step_lds") tuning().step_lds = (int)std::min<int64_t>(std::max<int64_t>(value, 0), 65536);
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });
 }

@@ -10,8 +10,9 @@
 // Kernels: k_state_step_grouped (lane groups each gather their own non-zero of one row), k_state_step_rows
 // (lane groups each own a row: steps of short rows) and k_state_step (one non-zero per wave: other lane
 // widths).  Waves are numbered (tile, row, chunk-in-tile): a chunk of batch columns is swept over every row
-// before the next starts, so one sweep gathers one line per source row.  REPLAY = true builds the gather
-// stream alone (measurement; the evaluator library never instantiates it).
+// before the next starts, so one sweep gathers one line per source row.  REPLAY = 1 builds the gather stream
+// alone, REPLAY = 2 the gathers plus the row reads and stores without the arithmetic of the sum (measurement
+// builds; the evaluator library instantiates only REPLAY = 0).
 #pragma once
 
 #include "common.hpp"
@@ -106,17 +107,19 @@ __device__ __forceinline__ WaveSlot wave_slot(const StepArgs<S, U> &a) {
 }
 
 // A row's constants, input drive and carried state for V columns, loaded before the gathers so their
-// latency overlaps the gather loop.
-template <int V>
+// latency overlaps the gather loop.  The carried state stays in its storage type until the epilogue (half the
+// registers for a float16 state, held across the whole loop).
+template <typename S, int V>
 struct RowInputs {
   RowParam p;
   float u[V];
-  float pv[V];
+  typename Lanes<S, V>::vec pv;
+  bool carried;
 };
 
 template <typename S, typename U, int V>
 __device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_t row, int64_t col, bool active,
-                                                RowInputs<V> &in) {
+                                                RowInputs<S, V> &in) {
   in.p = a.params[row];
 #pragma unroll
   for (int i = 0; i < V; ++i) in.u[i] = 0.0f;
@@ -129,24 +132,21 @@ __device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_
       for (int i = 0; i < V; ++i) in.u[i] = (col + i < a.batch) ? static_cast<float>(src[i]) : 0.0f;
     }
   }
-  if (active && a.xprev != nullptr && in.p.prev >= 0) {
-    Lanes<S, V>::load(a.xprev + (int64_t)in.p.prev * a.ldx + col, in.pv);
-  } else {
-#pragma unroll
-    for (int i = 0; i < V; ++i) in.pv[i] = in.p.pdef;
-  }
+  in.carried = active && a.xprev != nullptr && in.p.prev >= 0;
+  in.pv = in.carried ? Lanes<S, V>::raw(a.xprev + (int64_t)in.p.prev * a.ldx + col) : Lanes<S, V>::zero();
 }
 
 // Input drive, clamp and leaky update of V columns of one row, then the store.
 template <typename S, typename U, int V, bool TORCH_LERP>
 __device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V],
-                                           const RowInputs<V> &in) {
+                                           const RowInputs<S, V> &in) {
   const RowParam &p = in.p;
   float out[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
+    const float pv = in.carried ? Lanes<S, V>::at(in.pv, i) : p.pdef;
     const float x = fminf(fmaxf((acc[i] + in.u[i]) + p.k, p.lo), p.hi) + p.e;
-    out[i] = TORCH_LERP ? lerp_torch(in.pv[i], x, p.a) : fmaf(p.a, x - in.pv[i], in.pv[i]);
+    out[i] = TORCH_LERP ? lerp_torch(pv, x, p.a) : fmaf(p.a, x - pv, pv);
   }
   Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out, a.nt_store != 0);
 }
@@ -177,10 +177,11 @@ __device__ __forceinline__ typename Lanes<S, V>::vec bload(__amdgpu_buffer_rsrc_
 }
 
 
-// The replay of a step's gather stream (a measurement build of the kernels below, REPLAY = true): the same
-// pair loads and gathers, with each gathered vector folded into a few registers by XOR instead of the FMAs,
-// no row constants, input or carried state, no cross-lane sums and no epilogue.  `sink` writes nothing unless
-// the folded bits hit one value (so the loads stay live), into xout.
+// The replay of a step's memory streams (measurement builds of the kernels below): the same pair loads and
+// gathers, with each gathered vector folded into a few registers by XOR instead of the FMAs, and no cross-lane
+// sums.  REPLAY = 1: no row constants, input or carried state and no store; `sink` writes nothing unless the
+// folded bits hit one value (so the loads stay live), into xout.  REPLAY = 2: the row reads and the store of
+// the step as well, with `seed` turning the folded bits into the summed values (a denormal or zero).
 template <typename S, int V>
 struct ReplayBits {
   static constexpr int kWords = (V * (int)sizeof(S) + 3) / 4;
@@ -201,6 +202,10 @@ struct ReplayBits {
     for (int i = 0; i < kWords; ++i) folded ^= bits[i];
     if (folded == 0x9E3779B9u) reinterpret_cast<unsigned *>(a.xout)[threadIdx.x] = folded;
   }
+  template <int N>
+  static __device__ __forceinline__ void seed(float (&acc)[N], const vec &bits) {
+    acc[0] = __uint_as_float(bits[0] & 1u);
+  }
 };
 
 // One non-zero at a time per wave: the {column, weight} pairs are wave-uniform scalar loads, every lane
@@ -218,7 +223,7 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-  RowInputs<V> in;
+  RowInputs<S, V> in;
   load_row_inputs(a, w.row, col, active, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
 // {column, weight} pair with a vector load (one address per group); the pairs of the next round are loaded
 // while the current round's gathers are in flight.  The G partial sums meet through cross-lane shuffles,
 // and group 0 finishes the row.
-template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, bool REPLAY = false>
+template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, int REPLAY = 0>
 __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U> a) {
   constexpr int LPG = 64 / G;
   const WaveSlot w = wave_slot(a);
@@ -275,8 +280,8 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  RowInputs<V> in;
-  if constexpr (!REPLAY) load_row_inputs(a, w.row, col, active && g == 0, in);
+  RowInputs<S, V> in;
+  if constexpr (REPLAY != 1) load_row_inputs(a, w.row, col, active && g == 0, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
     const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
         else
           pairs(e0 + G * UNROLL, nx);
       }
-      if constexpr (REPLAY) {
+      if constexpr (REPLAY != 0) {
 #pragma unroll
         for (int j = 0; j < UNROLL; ++j) ReplayBits<S, V>::fold(bits, xr[j], cv[j].y);
       } else {
@@ -343,15 +348,16 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
     }
-    if constexpr (!REPLAY) {
+    if constexpr (REPLAY == 0) {
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[i] = group_sum<LPG>(acc[i]);
     }
   }
-  if constexpr (REPLAY) {
+  if constexpr (REPLAY == 1) {
     ReplayBits<S, V>::sink(a, bits);
     return;
   }
+  if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc, bits);
   if (g != 0 || !active) return;
   finish_row<S, U, V, TORCH_LERP>(a, w.row, col, acc, in);
 }
@@ -359,7 +365,7 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
 // G rows at a time per wave, for steps whose rows hold few non-zeros: group g of 64/G lanes owns row
 // G*slot + g and walks its non-zeros, gathering (64/G) * V columns per load; the wave loops to the longest
 // of its rows with the shorter rows' loads masked off, and every group finishes its own row.
-template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, bool REPLAY = false>
+template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, int REPLAY = 0>
 __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a) {
   constexpr int LPG = 64 / G;
   const WaveSlot w = wave_slot(a);                // w.row counts slots of G rows
@@ -377,8 +383,8 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  RowInputs<V> in;
-  if constexpr (!REPLAY) {
+  RowInputs<S, V> in;
+  if constexpr (REPLAY != 1) {
     if (has_row) load_row_inputs(a, row, col, active, in);
   }
 
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
       }
       int2 nx[UNROLL];
       if (k + UNROLL < len) pairs(k + UNROLL, nx);
-      if constexpr (REPLAY) {
+      if constexpr (REPLAY != 0) {
 #pragma unroll
         for (int j = 0; j < UNROLL; ++j) ReplayBits<S, V>::fold(bits, xr[j], cv[j].y);
       } else {
@@ -432,10 +438,11 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
       for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
     }
   }
-  if constexpr (REPLAY) {
+  if constexpr (REPLAY == 1) {
     ReplayBits<S, V>::sink(a, bits);
     return;
   }
+  if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc, bits);
   if (!active) return;
   finish_row<S, U, V, TORCH_LERP>(a, row, col, acc, in);
 }

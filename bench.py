@@ -261,6 +261,8 @@ def _probe_lib():
     lib.flyprobe_last_error.restype, lib.flyprobe_last_error.argtypes = ctypes.c_char_p, []
     for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
                        ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p]),
+                       ("flyprobe_pack_params", [p, p, i64, p, p]),
+                       ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p]),
                        ("flyprobe_random_gather", [p, i64, i64, i64, p, i64, p, p])):
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = i32, args
@@ -295,10 +297,11 @@ def _events_ms(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def replay_ceiling(plan, cone, batch: int, state_f16: bool, dev, reps: int = 20) -> list[dict]:
+def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps: int = 20) -> list[dict]:
     """Per step with a matrix, the time of the replay of that step's gather stream (flyprobe_replay_step: the
     state step's own kernel, launch shape and wave order over this plan's A_t and a state of this layout, with
-    the arithmetic, row inputs and stores taken out)."""
+    the arithmetic, row inputs and stores taken out), and of the replay that keeps the row reads and stores
+    (flyprobe_replay_step_io: everything but the arithmetic of the sum)."""
     import torch
     from chessfly import _hip
     lib, probe = _hip.load(), _probe_lib()
@@ -327,8 +330,27 @@ def replay_ceiling(plan, cone, batch: int, state_f16: bool, dev, reps: int = 20)
             _probe_check(probe, probe.flyprobe_replay_step(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz,
                                                            xprev.data_ptr(), prev_rows, ld, batch, int(state_f16),
                                                            sink.data_ptr(), st), "flyprobe_replay_step")
-        out.append({"t": t, "rows": nr, "nnz": nnz, "replay_ms": round(_events_ms(once, reps), 4)})
-        del rowptr, pairs, xprev
+        row = {"t": t, "rows": nr, "nnz": nnz, "replay_ms": round(_events_ms(once, reps), 4)}
+        # with the row I/O: each row's constants, carried state and input drive (float32, as the model forward's
+        # encoder writes it) read, and the new state written
+        prev32 = torch.empty(nr, dtype=torch.int32, device=dev)
+        usrc32 = torch.empty(nr, dtype=torch.int32, device=dev)
+        cone._step_export(t, prev=prev32, usrc=usrc32)
+        params = torch.empty(nr * 8, dtype=torch.int32, device=dev)
+        _probe_check(probe, probe.flyprobe_pack_params(prev32.data_ptr(), usrc32.data_ptr(), nr, params.data_ptr(), st),
+                     "flyprobe_pack_params")
+        ldu = state_ld(batch, 4)
+        u = torch.randn(n_in, ldu, device=dev) * 0.01
+        xout = torch.empty(nr, ld, dtype=dtype, device=dev)
+
+        def once_io():
+            _probe_check(probe, probe.flyprobe_replay_step_io(rowptr.data_ptr(), pairs.data_ptr(), params.data_ptr(),
+                                                              nr, nnz, xprev.data_ptr(), prev_rows, ld, u.data_ptr(),
+                                                              n_in, ldu, xout.data_ptr(), batch, int(state_f16),
+                                                              st), "flyprobe_replay_step_io")
+        row["replay_io_ms"] = round(_events_ms(once_io, reps), 4)
+        out.append(row)
+        del rowptr, pairs, xprev, prev32, usrc32, params, u, xout
     return out
 
 
@@ -557,20 +579,26 @@ def main() -> int:
     if not args.no_replay and per_step:
         # the ceiling: each step's own gather stream replayed alone (same kernel, shape and order, no arithmetic)
         plan = brain._cone_plan(cone, mode)
-        rows = replay_ceiling(plan, cone, args.batch, args.dtype == "f16", dev)
+        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev)
         for r in rows:
             r["step_ms"] = round(per_step[r["t"]], 4)
             r["replay_over_step"] = round(r["replay_ms"] / r["step_ms"], 4)
+            r["replay_io_over_step"] = round(r["replay_io_ms"] / r["step_ms"], 4)
         tot_replay = sum(r["replay_ms"] for r in rows)
+        tot_io = sum(r["replay_io_ms"] for r in rows)
         tot_step = sum(r["step_ms"] for r in rows)
         roofline["replay"] = {
-            "per_step": rows, "replay_ms": round(tot_replay, 4), "step_ms": round(tot_step, 4),
+            "per_step": rows, "replay_ms": round(tot_replay, 4), "replay_io_ms": round(tot_io, 4),
+            "step_ms": round(tot_step, 4),
             "frac_of_replay": round(tot_replay / tot_step, 4) if tot_step else None,
+            "frac_of_replay_io": round(tot_io / tot_step, 4) if tot_step else None,
             "note": "replay = the state step's own kernel over the same A_t and state layout with the FMAs, row "
-                    "inputs and stores taken out (libflyprobe.so); frac_of_replay = replay time / state-step time "
-                    "over the steps with a matrix (1.0: the step costs no more than its gather stream)"}
-        log(f"replay of the gather stream: {tot_replay:.3f} ms against {tot_step:.3f} ms of state steps "
-            f"(per step {[(r['t'], r['replay_ms'], r['step_ms']) for r in rows]})")
+                    "inputs and stores taken out; replay_io = the same with the row reads and stores kept, i.e. "
+                    "everything but the arithmetic of the sum (libflyprobe.so); frac_of_replay(_io) = replay time / "
+                    "state-step time over the steps with a matrix (1.0: the step costs no more than that stream)"}
+        log(f"replay of the gather stream: {tot_replay:.3f} ms, with the row I/O {tot_io:.3f} ms, against "
+            f"{tot_step:.3f} ms of state steps (per step t, replay, replay_io, step: "
+            f"{[(r['t'], r['replay_ms'], r['replay_io_ms'], r['step_ms']) for r in rows]})")
     if not args.no_gather_ceiling:
         rates, rows_per_s = random_gather_rates(dev)
         roofline["random_gather_GBps"] = rates

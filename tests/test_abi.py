@@ -110,3 +110,9 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     assert b"null" in probe.flyprobe_last_error()
     assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 32, 64, 1, p, None) == 1
     assert b"layout" in probe.flyprobe_last_error()
+    probe.flyprobe_replay_step_io.argtypes = [p_, p_, p_, i64, i64, p_, i64, i64, p_, i64, i64, p_, i64,
+                                              ctypes.c_int32, p_]
+    assert probe.flyprobe_replay_step_io(p, p, None, 10, 10, p, 10, 64, None, 0, 0, p, 64, 1, None) == 1
+    assert b"null" in probe.flyprobe_last_error()
+    assert probe.flyprobe_replay_step_io(p, p, p, 10, 10, p, 10, 64, p, 5, 32, p, 64, 1, None) == 1
+    assert b"input drive" in probe.flyprobe_last_error()
