@@ -167,7 +167,7 @@ struct Tuning {
   int rows_mode = 0; // lane groups own rows instead of non-zeros: 1 always, -1 never, 0 for short rows
   int rows_vec = 0;  // elements per lane of row-slot steps on half states: 8 (16 bytes) or 16 (32 bytes), 0 = automatic
   int spmm_groups = 0;  // lane groups of the training SpMM on 16-byte lanes (2, 4, 8), 0 = automatic
-  int gemm_tile = 0;    // dense-map workgroup tile: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, 0 = automatic
+  int gemm_tile = 0;    // dense-map workgroup tile: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, 10 TM + TN, 0 = auto
   int step_lds = 0;     // bytes of LDS each state-step workgroup reserves (caps waves per SIMD), 0 = none
 };
 Tuning &tuning();

@@ -260,9 +260,7 @@ __device__ __forceinline__ void gemm_tile(const Split &A, const Split &B, int64_
     // The operand stages are free after the last barrier: C goes through them, rows padded by 4 floats, and
     // leaves as 16-byte pieces of whole rows (a wave writes two 512-byte rows per store at 128 columns).
     constexpr int LDC = 32 * TN + 4, V4 = 32 * TN / 4;
-    static_assert(32 * TM * LDC * sizeof(float) <= sizeof(_Float16) * 2 * LDK * 32 * (TM + TN),
-                  "the C tile fits the operand stages");
-    float *Cs = reinterpret_cast<float *>(&As[0][0][0]);
+    float *Cs = reinterpret_cast<float *>(&As[0][0][0]);   // k_gemm_split sizes its LDS for the C tile too
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -295,8 +293,11 @@ __device__ __forceinline__ void gemm_tile(const Split &A, const Split &B, int64_
 template <int TM, int TN, class EP>
 __global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B, int64_t kp, float unscale, const EP ep,
                                                     int tiles, int gx) {
-  // one block of LDS for both operands' stages (and, after the K loop, the C tile of a row-wise epilogue)
-  __shared__ __attribute__((aligned(16))) _Float16 smem[2 * LDK * 32 * (TM + TN)];
+  // one block of LDS for both operands' stages and, after the K loop, the C tile of a row-wise epilogue (rows
+  // padded by 4 floats)
+  constexpr size_t kStages = 2 * LDK * 32 * (TM + TN);
+  constexpr size_t kCTile = EP::kRows ? (size_t)32 * TM * (32 * TN + 4) * 2 : 0;   // in halves
+  __shared__ __attribute__((aligned(16))) _Float16 smem[kStages > kCTile ? kStages : kCTile];
   auto As = reinterpret_cast<_Float16 (*)[32 * TM][LDK]>(smem);
   auto Bs = reinterpret_cast<_Float16 (*)[32 * TN][LDK]>(smem + 2 * LDK * 32 * TM);
   int ty, tx;
@@ -315,23 +316,40 @@ __global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B
 
 // Wave tiles of 64 x 64 (128 x 128 per workgroup) where that gives at least four tiles per CU, else 32 x 32 (64 x 64
 // per workgroup, up to four workgroups per CU): measured on the 17,937 x 1120 encoder and the 4,299 x 1120 head.
-// The gemm_tile tuning key forces one (1: 64 x 64 tiles, 2: 128 x 64, 3: 128 x 128).
+// The gemm_tile tuning key forces one: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, or 10 TM + TN for a workgroup tile
+// of 32 TM x 32 TN with TM in {2, 3, 4} and TN in {2, 4, 5}.
 template <class EP>
 void gemm_split(const Split &A, const Split &B, int64_t kp, float unscale, const EP &ep, hipStream_t st) {
   if (A.rows == 0 || B.rows == 0) return;
   auto count = [&](int bm, int bn) { return ((A.rows + bm - 1) / bm) * ((B.rows + bn - 1) / bn); };
   int shape = tuning().gemm_tile;
-  if (shape < 1 || shape > 3) shape = count(128, 128) >= 1024 ? 3 : 1;
-  const int bm = shape == 1 ? 64 : 128, bn = shape == 3 ? 128 : 64;
+  if (shape == 1) shape = 22;
+  else if (shape == 2) shape = 42;
+  else if (shape == 3) shape = 44;
+  const int tm = shape / 10, tn = shape % 10;
+  const bool known = (tm == 2 || tm == 3 || tm == 4) && (tn == 2 || tn == 4 || tn == 5);
+  if (!known) shape = count(128, 128) >= 1024 ? 44 : 22;
+  const int bm = 32 * (shape / 10), bn = 32 * (shape % 10);
   const int64_t gx = (B.rows + bn - 1) / bn, tiles = count(bm, bn);
   FLY_REQUIRE(tiles < INT32_MAX, "GEMM grid too large");
   const dim3 grid((unsigned)tiles), block(256);
-  if (shape == 3)
-    hipLaunchKernelGGL((k_gemm_split<4, 4, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx);
-  else if (shape == 2)
-    hipLaunchKernelGGL((k_gemm_split<4, 2, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx);
-  else
-    hipLaunchKernelGGL((k_gemm_split<2, 2, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx);
+#define FLY_GEMM_CASE(TM_, TN_)                                                                                    \
+  case 10 * TM_ + TN_:                                                                                             \
+    hipLaunchKernelGGL((k_gemm_split<TM_, TN_, EP>), grid, block, 0, st, A, B, kp, unscale, ep, (int)tiles, (int)gx); \
+    break;
+  switch (shape) {
+    FLY_GEMM_CASE(2, 2)
+    FLY_GEMM_CASE(2, 4)
+    FLY_GEMM_CASE(2, 5)
+    FLY_GEMM_CASE(3, 2)
+    FLY_GEMM_CASE(3, 4)
+    FLY_GEMM_CASE(3, 5)
+    FLY_GEMM_CASE(4, 2)
+    FLY_GEMM_CASE(4, 4)
+    FLY_GEMM_CASE(4, 5)
+    default: FLY_REQUIRE(false, "unknown GEMM tile");
+  }
+#undef FLY_GEMM_CASE
   check_launch("split gemm");
 }
 

@@ -559,8 +559,11 @@ def main() -> int:
                 "avg_launch_ms": round(avg_launch_ms, 4),
                 "gather_bytes_per_forward": int(gather),
                 "gather_GBps": round(gather / (step_ms / max(step_launches, 1) * launches_per_fwd * 1e-3) / 1e9, 1)}
-    # HBM traffic per launch comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed beside the
-    # profile of the same workload (counters cannot be read in-process); null for any other workload.
+    # Traffic per launch comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed beside the profile of
+    # the same workload (counters cannot be read in-process); null for any other workload.  Those counters count
+    # what leaves the L2 for the data fabric, which the 256 MB Infinity Cache or HBM then serves: gfx950 has no
+    # counter that separates the two (TCC_EA0_RDREQ_DRAM counts every request "destined for DRAM", cache hits
+    # included), so the figure is L2-to-fabric bytes, an upper bound on HBM bytes.
     traffic_file = os.path.join(REPO, "profiles", "state_step_b1120_traffic.json")
     if os.path.exists(traffic_file) and not args.tune:
         with open(traffic_file) as f:
@@ -569,6 +572,8 @@ def main() -> int:
                 "recurrent_steps": args.recurrent_steps, "ones": args.ones}
         if measured["workload"] == here:
             roofline["traffic"] = measured["traffic_bytes_per_launch"]
+            roofline["traffic_kind"] = ("L2-to-fabric bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE): served by "
+                                        "the Infinity Cache or HBM, which no gfx950 counter separates")
             roofline["traffic_source"] = measured["source"]
     shares = {k: round(v[0] / args.steps, 4) for k, v in prof.items()}
     # per-step state-step times of the forward: the profiled pass's state-step launches, in step order

@@ -373,8 +373,9 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * "rows_mode": 1 gives each lane group its own row, -1 never, 0 for steps with short rows; "rows_vec":
  * half-state elements per lane of those row slots (8 = 16 bytes, 16 = 32 bytes; 0 = automatic); "spmm_groups":
  * lane groups of fly_spmm on 16-byte lanes (2, 4, 8; 0 = automatic); "gemm_tile": workgroup tile of the dense
- * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128; 0 = automatic).  Every selectable shape computes the same
- * function. */
+ * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, or 10 TM + TN for 32 TM x 32 TN with TM in {2, 3, 4} and TN in
+ * {2, 4, 5}; 0 = automatic); "step_lds": bytes of LDS each state-step workgroup reserves, which caps the
+ * workgroups a CU runs at once (0 = none).  Every selectable shape computes the same function. */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus

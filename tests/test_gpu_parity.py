@@ -270,7 +270,7 @@ def gemm_tile(request):
     _hip.set_tuning("gemm_tile", 0)
 
 
-@pytest.mark.parametrize("gemm_tile", [0, 1, 2, 3], indirect=True)
+@pytest.mark.parametrize("gemm_tile", [0, 1, 2, 3, 24, 25, 32, 34, 35, 45], indirect=True)
 @pytest.mark.parametrize("batch,n_in,k,ld,n_out,moves", [(5, 70, 30, 33, 40, 100), (130, 300, 838, 967, 150, 4168),
                                                           (1, 17, 838, 967, 2333, 4168)])
 def test_encoder_and_head_gemms_match_fp64(batch, n_in, k, ld, n_out, moves, gemm_tile):
