@@ -52,6 +52,8 @@ SIGNATURES = {
     "fly_forward_io": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_forward_literal_workspace": (_sz, [_p, _i64]),
     "fly_forward_literal": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
+    "fly_forward_literal_f64_workspace": (_sz, [_p, _i64]),
+    "fly_forward_literal_f64": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
     "fly_plan_step": (_i32, [_p, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p]),
     "fly_dense_create": (_i32, [ctypes.POINTER(HeadDesc), _p, _i64, _i64, _p, _i64, _p, _pp]),
     "fly_dense_destroy": (_i32, [_p]),

@@ -805,16 +805,21 @@ class ConnectomeRNN(nn.Module):
         self._check_params("ConnectomeRNN.forward")
         if torch.is_grad_enabled():
             return self._forward_autograd(u, steps)
-        if u.dtype != torch.float32 or u.dim() != 2 or u.shape[0] != self.n:
-            raise RuntimeError(f"ConnectomeRNN.forward: u must be float32 ({self.n}, B), got {u.dtype} {tuple(u.shape)}")
+        if u.dtype not in (torch.float32, torch.float64) or u.dim() != 2 or u.shape[0] != self.n:
+            raise RuntimeError(f"ConnectomeRNN.forward: u must be float32 or float64 ({self.n}, B), got {u.dtype} "
+                               f"{tuple(u.shape)}")
         lib = _hip.load()
         plan = self._full_plan()
         batch = u.shape[1]
         h = torch.empty_like(u)
-        ws = _hip.workspace(lib.fly_forward_literal_workspace(plan.handle, batch), u.device)
-        _hip.check(lib.fly_forward_literal(plan.handle, u.data_ptr(), batch, self.bias.data_ptr(), batch, int(steps),
-                                           h.data_ptr(), batch, ws.data_ptr(), ws.numel(), _hip.stream(u.device)),
-                   "fly_forward_literal")
+        # the recurrence runs in u's dtype (brain.py:215-216): float64 widens the float32 weights exactly
+        f64 = u.dtype == torch.float64
+        size = lib.fly_forward_literal_f64_workspace if f64 else lib.fly_forward_literal_workspace
+        run = lib.fly_forward_literal_f64 if f64 else lib.fly_forward_literal
+        ws = _hip.workspace(size(plan.handle, batch), u.device)
+        _hip.check(run(plan.handle, u.data_ptr(), batch, self.bias.data_ptr(), batch, int(steps), h.data_ptr(), batch,
+                       ws.data_ptr(), ws.numel(), _hip.stream(u.device)),
+                   "fly_forward_literal_f64" if f64 else "fly_forward_literal")
         return h
 
     def _forward_autograd(self, u: torch.Tensor, steps: int) -> torch.Tensor:

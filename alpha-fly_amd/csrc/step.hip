@@ -105,16 +105,47 @@ __global__ void k_outputs(const S *__restrict__ state, int64_t lds, const int32_
   }
 }
 
-__global__ void k_add_bias(float *__restrict__ u, int64_t ldu, const float *__restrict__ bias, int64_t n, int64_t batch) {
+template <typename T>
+__global__ void k_add_bias(T *__restrict__ u, int64_t ldu, const float *__restrict__ bias, int64_t n, int64_t batch) {
   const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (b >= batch) return;
-  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) u[r * ldu + b] += bias[r];
+  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) u[r * ldu + b] += static_cast<T>(bias[r]);
 }
 
-__global__ void k_zero_rows(float *__restrict__ h, int64_t ld, int64_t n, int64_t batch) {
+template <typename T>
+__global__ void k_zero_rows(T *__restrict__ h, int64_t ld, int64_t n, int64_t batch) {
   const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (b >= batch) return;
-  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) h[r * ld + b] = 0.0f;
+  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) h[r * ld + b] = T(0);
+}
+
+// One float64 update of the literal recurrence (brain.py:219-220 in u's dtype): per row, the CSR sum in edge
+// order, x = clamp(s + drive, 0, H), h' = torch.lerp(h, x, alpha), all in double.  The plan's float32 weights,
+// alphas and bound widen exactly, as the reference's .to(u.dtype) does.  One wave per (row, 64 columns), one column
+// per lane; the row's pairs are wave-uniform.
+__global__ __launch_bounds__(256) void k_literal_step_f64(const int32_t *__restrict__ rowptr, const int2 *__restrict__ colval,
+                                                          const RowParam *__restrict__ params, const double *hprev,
+                                                          int64_t ldp, const double *__restrict__ drive, int64_t ldd,
+                                                          double *__restrict__ hout, int64_t ldo, int32_t nrows,
+                                                          int32_t batch, int32_t chunks) {
+  const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t row = wave / (uint32_t)chunks, chunk = wave - row * (uint32_t)chunks;
+  if (row >= (uint32_t)nrows) return;
+  const int64_t b = (int64_t)chunk * 64 + (threadIdx.x & 63);
+  if (b >= batch) return;
+  double acc = 0.0;
+  if (hprev != nullptr) {
+    const int32_t end = rowptr[row + 1];
+    for (int32_t e = rowptr[row]; e < end; ++e) {
+      const int2 cv = colval[e];
+      acc = fma((double)__int_as_float(cv.y), hprev[(int64_t)cv.x * ldp + b], acc);
+    }
+  }
+  const RowParam p = params[row];
+  const double x = fmin(fmax(acc + drive[(int64_t)row * ldd + b], 0.0), (double)p.hi);
+  const double h = hprev != nullptr ? hprev[(int64_t)row * ldp + b] : 0.0;
+  const double a = (double)p.a;
+  hout[(int64_t)row * ldo + b] = fabs(a) < 0.5 ? h + a * (x - h) : x - (x - h) * (1.0 - a);
 }
 
 }  // namespace
@@ -253,12 +284,12 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
     hipStream_t st = as_stream(stream);
     {
       LaunchTimer timer(FLY_K_OTHER, st);
-      hipLaunchKernelGGL(k_add_bias, rows_grid(n, batch), dim3(256), 0, st, u, ldu, bias, n, batch);
+      hipLaunchKernelGGL(k_add_bias<float>, rows_grid(n, batch), dim3(256), 0, st, u, ldu, bias, n, batch);
     }
     check_launch("bias add");
     if (steps == 0) {
       LaunchTimer timer(FLY_K_OTHER, st);
-      hipLaunchKernelGGL(k_zero_rows, rows_grid(n, batch), dim3(256), 0, st, h, ldh, n, batch);
+      hipLaunchKernelGGL(k_zero_rows<float>, rows_grid(n, batch), dim3(256), 0, st, h, ldh, n, batch);
       check_launch("zero state");
       return;
     }
@@ -291,6 +322,51 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
         prev = buf[cur];
         cur ^= 1;
       }
+    }
+  });
+}
+
+extern "C" size_t fly_forward_literal_f64_workspace(const fly_plan *plan, int64_t batch) {
+  if (!plan) return 0;
+  return 2 * (size_t)plan->n * (size_t)std::max<int64_t>(batch, 1) * sizeof(double) + 256;
+}
+
+extern "C" int fly_forward_literal_f64(const fly_plan *plan, double *u, int64_t ldu, const float *bias, int64_t batch,
+                                       int32_t steps, double *h, int64_t ldh, void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] {
+    check_plan_device(plan);
+    FLY_REQUIRE(plan->full, "the literal recurrence needs a plan from fly_plan_create_full");
+    FLY_REQUIRE(steps >= 0, "negative steps");
+    FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+    if (batch == 0) return;
+    FLY_REQUIRE(u && bias && h && ldu >= batch && ldh >= batch, "bad argument");
+    const int64_t n = plan->n;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(k_add_bias<double>, rows_grid(n, batch), dim3(256), 0, st, u, ldu, bias, n, batch);
+    check_launch("bias add");
+    if (steps == 0) {
+      hipLaunchKernelGGL(k_zero_rows<double>, rows_grid(n, batch), dim3(256), 0, st, h, ldh, n, batch);
+      check_launch("zero state");
+      return;
+    }
+    FLY_REQUIRE(ws && ws_bytes >= fly_forward_literal_f64_workspace(plan, batch), "workspace too small");
+    FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
+    const int32_t chunks = (int32_t)((batch + 63) / 64);
+    const int64_t waves = n * chunks;
+    FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "grid too large");
+    double *buf[2] = {static_cast<double *>(ws), static_cast<double *>(ws) + (size_t)n * batch};
+    const double *prev = nullptr;
+    int64_t ldp = batch;
+    for (int t = 1; t <= steps; ++t) {
+      const bool last = t == steps;
+      double *out = last ? h : buf[(t - 1) & 1];
+      const int64_t ldo = last ? ldh : batch;
+      hipLaunchKernelGGL(k_literal_step_f64, dim3(blocks_for(waves, 4)), dim3(256), 0, st, plan->rowptr[0].p,
+                         plan->colval[0].p, plan->params[0].p, prev, ldp, u, ldu, out, ldo, (int32_t)n, (int32_t)batch,
+                         chunks);
+      check_launch("literal step (float64)");
+      prev = out;
+      ldp = ldo;
     }
   });
 }

@@ -17,7 +17,7 @@
  *                         :238-252 _constants
  *   fly_plan_create_full  chessfly/brain.py:215-216 (per-call weights of the literal recurrence)
  *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280)
- *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch)
+ *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch); _f64 in float64
  *   fly_plan_step         chessfly/brain.py:273-277 and :310-313 (one step of forward_io; :219-220 one literal step)
  *   fly_dense_create      chessfly/model.py:79-93 (the encoder and head weights, as the matrix cores read them)
  *   fly_encoder           chessfly/model.py:99-102 (encoder linear map, input gain, cast, transpose)
@@ -130,6 +130,13 @@ size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch);
 int fly_forward_literal(const fly_plan *plan, float *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
                         int32_t steps, float *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
                         void *stream);
+/* The same recurrence in float64 (chessfly/brain.py:215-223 with u float64: the float32 weights, alphas and bias
+ * widen exactly, and every sum, clamp and lerp is float64; the reference's tests run it this way).  u (n, ldu) is
+ * updated in place to u + bias; h (n, ldh) float64. */
+size_t fly_forward_literal_f64_workspace(const fly_plan *plan, int64_t batch);
+int fly_forward_literal_f64(const fly_plan *plan, double *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
+                            int32_t steps, double *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
+                            void *stream);
 
 /* One state step of a plan, the per-step op of chessfly/brain.py:273-277 (float16 deviation: s = A_t d_{t-1},
  * index_add_ of the input, FUSED_DEVIATION) and :310-313 (float32: A_t h + input, FUSED_UPDATE with k_t):

@@ -101,10 +101,12 @@ def literal_step(b: BrainArrays, mat: torch.Tensor, alpha: torch.Tensor, h: torc
 
 
 def literal_operands(b: BrainArrays, dtype):
-    """W as a sparse CSR tensor and alpha (N, 1), in dtype, as the literal recurrence uses them (brain.py:215-216)."""
-    wdt = torch.float64 if dtype == torch.float64 else torch.float32
-    alpha = torch.sigmoid(b.alpha_logit.to(wdt)).to(dtype).unsqueeze(1)
-    return full_matrix(b, edge_weights(b, wdt).to(dtype)), alpha
+    """W as a sparse CSR tensor and alpha (N, 1), in dtype, as the literal recurrence uses them (brain.py:215-216):
+    computed in the parameters' own dtype, then converted to the state's (float32 parameters widen exactly into a
+    float64 recurrence)."""
+    pdt = b.alpha_logit.dtype
+    alpha = torch.sigmoid(b.alpha_logit).to(dtype).unsqueeze(1)
+    return full_matrix(b, edge_weights(b, pdt).to(dtype)), alpha
 
 
 def literal(b: BrainArrays, u: torch.Tensor, steps: int) -> torch.Tensor:

@@ -393,3 +393,49 @@ def test_plan_matrix_is_the_sub_matrix_with_its_weights():
                    "fly_plan_matrix")
         assert torch.equal(crow.long(), op.crow) and torch.equal(col.long(), op.pre)
         assert torch.equal(val, w[op.edges])
+
+
+# ---- the literal recurrence in float64 ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("h_max", [10.0, None])
+def test_literal_recurrence_in_float64(h_max):
+    """ConnectomeRNN.forward runs in u's dtype (brain.py:215-223); the reference's tests run it in float64.  The
+    float32 weights, alphas and bias widen exactly and every sum and update is float64.  With log_gain = 0 and
+    alpha_logit = 0 the float32 transforms (exp, sigmoid) are exact on any implementation, so the device must match
+    the oracle's float64 recurrence to 1e-12, on a 3,000-neuron graph and, against the dense brute force, on the
+    shuffled control of the reference's test graph (repeated pairs, self-loops); with random parameters it matches
+    to float32-parameter round-off (1e-5).  u is left holding u + bias."""
+    g = torch.Generator().manual_seed(9)
+    for exact in (True, False):
+        conn = _medium(8)
+        lg, b, al = random_params(conn, 25, gain_sd=0.1, bias_mean=2.0 if h_max is None else 0.1)
+        if exact:
+            lg, al = np.zeros_like(lg), np.zeros_like(al)
+        rnn = _rnn(conn, 4.0, lg, b, al, h_max=h_max)
+        ba = brain_arrays(conn, 4.0, lg, b, al, h_max=h_max)          # float32 parameters, as the product's
+        ba.w0 = rnn.w0.cpu()
+        tol = 1e-12 if exact else 1e-5
+        for batch, steps in ((1, 1), (70, 3), (130, 6)):
+            u = torch.randn(conn.n_neurons, batch, generator=g, dtype=torch.float64)
+            u_dev = u.to(DEV)
+            with torch.no_grad():
+                h = rnn(u_dev, steps)
+            assert h.dtype == torch.float64
+            ref = F.literal(ba, u, steps).numpy()
+            assert ref.dtype == np.float64
+            np.testing.assert_allclose(h.cpu().numpy(), ref, rtol=tol, atol=tol)
+            np.testing.assert_array_equal(u_dev.cpu().numpy(),
+                                          (u + torch.as_tensor(b).to(torch.float64)[:, None]).numpy())
+    conn = tiny_connectome(80, 2000, 4).shuffled(3)
+    lg, b, al = random_params(conn, 26, gain_sd=0.3)
+    lg, al = np.zeros_like(lg), np.zeros_like(al)
+    rnn = _rnn(conn, 3.0, lg, b, al, h_max=h_max)
+    W = brute.dense_matrix(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(),
+                           (rnn.sign * rnn.w0).cpu().numpy().astype(np.float64))
+    alpha = np.full(conn.n_neurons, 0.5)
+    u = torch.randn(conn.n_neurons, 33, generator=g, dtype=torch.float64)
+    with torch.no_grad():
+        h = rnn(u.clone().to(DEV), 5)
+    dense = brute.dense_recurrence(W, np.asarray(b, dtype=np.float32).astype(np.float64), alpha, u.numpy(), 5,
+                                   h_max=h_max)
+    np.testing.assert_allclose(h.cpu().numpy(), dense, rtol=1e-12, atol=1e-12)
