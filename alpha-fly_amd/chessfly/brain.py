@@ -866,8 +866,9 @@ class ConnectomeRNN(nn.Module):
     def forward_io(self, u_in: torch.Tensor, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> torch.Tensor:
         """u_in: (len(in_idx), B) drive of the input neurons.  Returns the output neurons after `steps`
         updates, (len(out_idx), B): forward(u, steps)[out_idx] with u zero outside in_idx.  float16 u_in
-        takes the deviation path and returns float32; float32 u_in takes the float32 path.  Under autograd the
-        float32 light cone runs differentiably (training)."""
+        takes the deviation path and returns float32; float32 u_in takes the float32 path; float64 u_in runs the
+        light cone in float64 over the float32 cache (brain.py:295-329 in u_in's dtype) and returns float64.
+        Under autograd the float32 light cone runs differentiably (training)."""
         _hip.require_device(u_in, "ConnectomeRNN.forward_io")
         self._check_params("ConnectomeRNN.forward_io")
         if torch.is_grad_enabled():
@@ -877,10 +878,10 @@ class ConnectomeRNN(nn.Module):
             return self._forward_io_autograd(u_in, cone, out_idx, steps)
         if u_in.dtype == torch.float16:
             mode = _hip.MODE_DEVIATION_F16
-        elif u_in.dtype == torch.float32:
+        elif u_in.dtype in (torch.float32, torch.float64):
             mode = _hip.MODE_F32
         else:
-            raise RuntimeError(f"forward_io: u_in must be float16 or float32, got {u_in.dtype}")
+            raise RuntimeError(f"forward_io: u_in must be float16, float32 or float64, got {u_in.dtype}")
         if u_in.dim() != 2 or u_in.shape[0] != len(in_idx):
             raise RuntimeError(f"forward_io: u_in must be (len(in_idx), B), got {tuple(u_in.shape)}")
         cone = self.light_cone(in_idx, out_idx, steps)
@@ -888,12 +889,15 @@ class ConnectomeRNN(nn.Module):
         batch = u_in.shape[1]
         if u_in.stride(1) != 1 or (batch > 1 and u_in.stride(0) < batch):
             u_in = u_in.contiguous()
-        out = torch.empty(len(out_idx), batch, dtype=torch.float32, device=u_in.device)
+        f64 = u_in.dtype == torch.float64
+        out = torch.empty(len(out_idx), batch, dtype=torch.float64 if f64 else torch.float32, device=u_in.device)
         lib = _hip.load()
-        ws = _hip.workspace(lib.fly_forward_io_workspace(plan.handle, batch), u_in.device)
+        size = lib.fly_forward_io_f64_workspace if f64 else lib.fly_forward_io_workspace
+        run = lib.fly_forward_io_f64 if f64 else lib.fly_forward_io
+        ws = _hip.workspace(size(plan.handle, batch), u_in.device)
         ldu = u_in.stride(0) if u_in.shape[0] > 1 else batch
-        _hip.check(lib.fly_forward_io(plan.handle, u_in.data_ptr(), ldu, batch, out.data_ptr(), batch, ws.data_ptr(),
-                                      ws.numel(), _hip.stream(u_in.device)), "fly_forward_io")
+        _hip.check(run(plan.handle, u_in.data_ptr(), ldu, batch, out.data_ptr(), batch, ws.data_ptr(), ws.numel(),
+                       _hip.stream(u_in.device)), "fly_forward_io_f64" if f64 else "fly_forward_io")
         return out
 
     def resting_outputs(self, in_idx: torch.Tensor, out_idx: torch.Tensor, steps: int) -> torch.Tensor:

@@ -148,6 +148,51 @@ __global__ __launch_bounds__(256) void k_literal_step_f64(const int32_t *__restr
   hout[(int64_t)row * ldo + b] = fabs(a) < 0.5 ? h + a * (x - h) : x - (x - h) * (1.0 - a);
 }
 
+// One float64 step of the light cone (brain.py:307-327 with u_in float64).  The reference builds its cache in
+// the parameters' dtype (float32) and widens it with .to(dtype): the float32 plan's k_t, c_{t-1}, alphas and A_t
+// values widen exactly here, and the sum, input add, clamp and lerp are double.  The order is the fused update's
+// (brain.py:310-313): x = clamp((A_t h + u) + k_t, 0, H), p = carried ? h_{t-1}[prev] : c_{t-1}.  One wave per
+// (row, 64 columns), one column per lane; the row's pairs are wave-uniform.
+__global__ __launch_bounds__(256) void k_cone_step_f64(const int32_t *__restrict__ rowptr, const int2 *__restrict__ colval,
+                                                       const RowParam *__restrict__ params, const double *hprev,
+                                                       int64_t ldp, const double *__restrict__ u, int64_t ldu,
+                                                       double *__restrict__ hout, int64_t ldo, int32_t nrows,
+                                                       int32_t batch, int32_t chunks) {
+  const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t row = wave / (uint32_t)chunks, chunk = wave - row * (uint32_t)chunks;
+  if (row >= (uint32_t)nrows) return;
+  const int64_t b = (int64_t)chunk * 64 + (threadIdx.x & 63);
+  if (b >= batch) return;
+  double acc = 0.0;
+  if (hprev != nullptr && rowptr != nullptr) {
+    const int32_t end = rowptr[row + 1];
+    for (int32_t e = rowptr[row]; e < end; ++e) {
+      const int2 cv = colval[e];
+      acc = fma((double)__int_as_float(cv.y), hprev[(int64_t)cv.x * ldp + b], acc);
+    }
+  }
+  const RowParam p = params[row];
+  if (u != nullptr && p.usrc >= 0) acc += u[(int64_t)p.usrc * ldu + b];
+  const double x = fmin(fmax(acc + (double)p.k, (double)p.lo), (double)p.hi) + (double)p.e;
+  const double h = (hprev != nullptr && p.prev >= 0) ? hprev[(int64_t)p.prev * ldp + b] : (double)p.pdef;
+  const double a = (double)p.a;
+  hout[(int64_t)row * ldo + b] = fabs(a) < 0.5 ? h + a * (x - h) : x - (x - h) * (1.0 - a);
+}
+
+// out[j] = c_T[out_idx[j]] widened, or the state of out_idx[j] in R_T where it has one (float32 plans carry a
+// zero base there).
+__global__ void k_outputs_f64(const double *__restrict__ state, int64_t lds, const int32_t *__restrict__ out_src,
+                              const float *__restrict__ cbase, int64_t n_out, int64_t batch, double *__restrict__ out,
+                              int64_t ldo) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  for (int64_t j = blockIdx.y; j < n_out; j += gridDim.y) {
+    const int32_t src = out_src[j];
+    out[j * ldo + b] = (state != nullptr && src >= 0) ? state[(int64_t)src * lds + b] + (double)cbase[j]
+                                                      : (double)cbase[j];
+  }
+}
+
 }  // namespace
 
 // Boards per block of a forward: the whole batch while a state buffer of `rows` rows stays below 2 GiB, so the
@@ -261,6 +306,50 @@ extern "C" int fly_forward_io(const fly_plan *plan, const void *u_in, int64_t ld
         const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, false, ws, st);
         write_outputs<float>(*plan, fin, nb, out + c0, ldo, st);
       }
+    }
+  });
+}
+
+extern "C" size_t fly_forward_io_f64_workspace(const fly_plan *plan, int64_t batch) {
+  if (!plan) return 0;
+  return 2 * (size_t)plan->max_rows * (size_t)std::max<int64_t>(batch, 1) * sizeof(double) + 256;
+}
+
+extern "C" int fly_forward_io_f64(const fly_plan *plan, const double *u_in, int64_t ldu, int64_t batch, double *out,
+                                  int64_t ldo, void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] {
+    check_plan_device(plan);
+    FLY_REQUIRE(!plan->full, "forward_io needs a light-cone plan");
+    FLY_REQUIRE(plan->mode == FLY_MODE_F32, "the float64 light cone needs a FLY_MODE_F32 plan");
+    FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+    if (batch == 0) return;
+    FLY_REQUIRE(out && ldo >= batch, "bad output");
+    FLY_REQUIRE(plan->n_in == 0 || (u_in && ldu >= batch), "bad input drive");
+    FLY_REQUIRE(ws && ws_bytes >= fly_forward_io_f64_workspace(plan, batch), "workspace too small");
+    FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
+    hipStream_t st = as_stream(stream);
+    const int32_t chunks = (int32_t)((batch + 63) / 64);
+    FLY_REQUIRE(plan->max_rows * (int64_t)chunks < (int64_t)UINT32_MAX / 2, "grid too large");
+    double *buf[2] = {static_cast<double *>(ws), static_cast<double *>(ws) + (size_t)plan->max_rows * batch};
+    const double *prev = nullptr;
+    int cur = 0;
+    for (int t = 1; t <= plan->steps; ++t) {
+      const int64_t nr = plan->rows_n[t];
+      if (nr == 0) {
+        prev = nullptr;
+        continue;
+      }
+      hipLaunchKernelGGL(k_cone_step_f64, dim3(blocks_for(nr * chunks, 4)), dim3(256), 0, st, plan->rowptr[t].p,
+                         plan->colval[t].p, plan->params[t].p, prev, batch, plan->n_in ? u_in : nullptr, ldu,
+                         buf[cur], batch, (int32_t)nr, (int32_t)batch, chunks);
+      check_launch("light-cone step (float64)");
+      prev = buf[cur];
+      cur ^= 1;
+    }
+    if (plan->n_out) {
+      hipLaunchKernelGGL(k_outputs_f64, rows_grid(plan->n_out, batch), dim3(256), 0, st, prev, batch, plan->out_src.p,
+                         plan->cbase.p, plan->n_out, batch, out, ldo);
+      check_launch("outputs (float64)");
     }
   });
 }

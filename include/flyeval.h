@@ -16,7 +16,7 @@
  *   fly_plan_create       chessfly/brain.py:257-270 (_forward_io_half cache) and :295-306 (float32 cache),
  *                         :238-252 _constants
  *   fly_plan_create_full  chessfly/brain.py:215-216 (per-call weights of the literal recurrence)
- *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280)
+ *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280); _f64 in float64
  *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch); _f64 in float64
  *   fly_plan_step         chessfly/brain.py:273-277 and :310-313 (one step of forward_io; :219-220 one literal step)
  *   fly_dense_create      chessfly/model.py:79-93 (the encoder and head weights, as the matrix cores read them)
@@ -124,6 +124,12 @@ size_t fly_forward_io_workspace(const fly_plan *plan, int64_t batch);
  * out (n_out, ldo) float32 = forward_io(u_in)[out rows]. */
 int fly_forward_io(const fly_plan *plan, const void *u_in_dev, int64_t ldu, int64_t batch, float *out_dev,
                    int64_t ldo, void *workspace_dev, size_t workspace_bytes, void *stream);
+/* forward_io with u_in float64 (chessfly/brain.py:295-329 in u_in's dtype): a FLY_MODE_F32 plan's float32 cache
+ * (k_t, c_t, alphas, A_t values) widens exactly, as the reference's .to(dtype) of its float32 cache does, and the
+ * state, sums, clamp and lerp are float64.  u_in (n_in, ldu) and out (n_out, ldo) float64. */
+size_t fly_forward_io_f64_workspace(const fly_plan *plan, int64_t batch);
+int fly_forward_io_f64(const fly_plan *plan, const double *u_in_dev, int64_t ldu, int64_t batch, double *out_dev,
+                       int64_t ldo, void *workspace_dev, size_t workspace_bytes, void *stream);
 /* Literal recurrence (plan from fly_plan_create_full): u (n, ldu) float32 is updated in place to u + bias
  * (as the reference's no-grad path does), then h_steps (n, ldh) = steps updates from h = 0. */
 size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch);

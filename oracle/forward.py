@@ -140,10 +140,13 @@ def constants(b: BrainArrays, cone: Cone, w: torch.Tensor, alpha: torch.Tensor, 
     return [x.to(dtype) for x in cs], ks
 
 
-def prepare_f32(b: BrainArrays, cone: Cone, dtype=torch.float32) -> dict:
+def prepare_f32(b: BrainArrays, cone: Cone, dtype=torch.float32, weights_dtype=None) -> dict:
     """Everything the float32 light cone caches per weight version (brain.py:295-306): the resting
-    trajectory, the per-step drive k_t, the sub-matrices and alpha, in `dtype` (float32 or float64)."""
-    wdt = torch.float64 if dtype == torch.float64 else torch.float32
+    trajectory, the per-step drive k_t, the sub-matrices and alpha, in `dtype` (float32 or float64).
+    weights_dtype is the parameters' dtype the reference computes the cache in before its .to(dtype)
+    (brain.py:299-303): `dtype` by default (the reference's tests on a .double() network), float32 for
+    float64 inputs to a float32 network."""
+    wdt = weights_dtype or (torch.float64 if dtype == torch.float64 else torch.float32)
     w = edge_weights(b, wdt)
     alpha = torch.sigmoid(b.alpha_logit.to(wdt)).unsqueeze(1)
     cs, ks = constants(b, cone, w, alpha, dtype)

@@ -439,3 +439,46 @@ def test_literal_recurrence_in_float64(h_max):
     dense = brute.dense_recurrence(W, np.asarray(b, dtype=np.float32).astype(np.float64), alpha, u.numpy(), 5,
                                    h_max=h_max)
     np.testing.assert_allclose(h.cpu().numpy(), dense, rtol=1e-12, atol=1e-12)
+
+
+# ---- forward_io in float64 ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("h_max", [10.0, None])
+def test_forward_io_in_float64(h_max):
+    """forward_io with float64 u_in (brain.py:295-329 in u_in's dtype): the float32 cache widens, the state and
+    every sum and update are float64, and the outputs come back float64.  With log_gain, bias and alpha_logit zero
+    the cache is exact (resting trajectory 0, weights sign * w0, alpha 1/2), so the device matches the float64
+    literal recurrence's outputs to 1e-12; with random parameters it matches the oracle's float64 cone over a
+    float32 cache within that cache's round-off (1e-5), and the float32 path within float32 round-off."""
+    g = torch.Generator().manual_seed(12)
+    conn = _medium(8)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    ind, outd = in_idx.to(DEV), out_idx.to(DEV)
+    for exact in (True, False):
+        lg, b, al = random_params(conn, 27, gain_sd=0.1, bias_mean=2.0 if h_max is None else 0.1)
+        if exact:
+            lg, b, al = np.zeros_like(lg), np.zeros_like(b), np.zeros_like(al)
+        rnn = _rnn(conn, 4.0, lg, b, al, h_max=h_max)
+        ba = brain_arrays(conn, 4.0, lg, b, al, h_max=h_max)          # float32 parameters, as the product's
+        ba.w0 = rnn.w0.cpu()
+        for batch, steps in ((1, 1), (70, 3), (130, 6)):
+            print(f"float64 forward_io: exact={exact} h_max={h_max} batch={batch} steps={steps}", flush=True)
+            u_in = torch.randn(len(in_idx), batch, generator=g, dtype=torch.float64)
+            with torch.no_grad():
+                out = rnn.forward_io(u_in.to(DEV), ind, outd, steps)
+                out32 = rnn.forward_io(u_in.float().to(DEV), ind, outd, steps)
+            assert out.dtype == torch.float64 and out.shape == (len(out_idx), batch)
+            got = out.cpu().numpy()
+            if exact:
+                u = torch.zeros(conn.n_neurons, batch, dtype=torch.float64).index_add(0, in_idx, u_in)
+                ref = F.literal(ba, u, steps)[out_idx].numpy()
+                tol = 1e-12
+            else:
+                cone = _cone(conn, in_idx, out_idx, steps)
+                prep = F.prepare_f32(ba, cone, torch.float64, weights_dtype=torch.float32)
+                ref = F.run_f32(prep, steps, u_in).numpy()
+                tol = 1e-5
+            assert ref.dtype == np.float64
+            scale = max(np.abs(ref).max(), 1.0)
+            np.testing.assert_allclose(got, ref, rtol=tol, atol=tol * scale)
+            np.testing.assert_allclose(out32.cpu().numpy(), got, rtol=2e-5, atol=2e-5 * scale)

@@ -166,6 +166,31 @@ def test_cone_forward_equals_literal_recurrence_fp64(steps):
     assert cone.edge_visits < 4 * conn.n_edges
 
 
+@pytest.mark.parametrize("steps", [2, 6])
+def test_float64_cone_over_a_float32_cache(steps):
+    """float64 inputs to a float32 network (brain.py:295-306 with dtype float64): the cache is computed in the
+    parameters' float32 and widened, so every cached value is a float32 and the float64 cone stays within the
+    cache's float32 rounding of the exact function."""
+    conn = tiny_connectome(120, 700, seed=3)
+    lg, b, al = random_params(conn, 11)
+    ba32 = brain_arrays(conn, 3.0, lg, b, al)
+    ba64 = brain_arrays(conn, 3.0, lg, b, al, dtype=torch.float64)
+    in_idx, out_idx = np.arange(0, 9), np.arange(100, 120)
+    cone = _cone(conn, in_idx, out_idx, steps)
+    prep = F.prepare_f32(ba32, cone, torch.float64, weights_dtype=torch.float32)
+    for t in range(1, steps + 1):
+        for v in (prep["cs"][t - 1], prep["ks"][t], prep["alpha"]) + \
+                 ((prep["mats"][t].values(),) if prep["mats"][t] is not None else ()):
+            assert v.dtype == torch.float64 and torch.equal(v.to(torch.float32).to(torch.float64), v)
+    u_in = torch.randn(9, 5, dtype=torch.float64, generator=torch.Generator().manual_seed(steps))
+    out = F.run_f32(prep, steps, u_in)
+    assert out.dtype == torch.float64
+    u = torch.zeros(conn.n_neurons, 5, dtype=torch.float64).index_add(0, torch.as_tensor(in_idx), u_in)
+    exact = F.literal(ba64, u, steps)[torch.as_tensor(out_idx)]
+    torch.testing.assert_close(out, exact, rtol=1e-5, atol=1e-5)
+    assert (out - exact).abs().max() > 0          # the float32 cache does round
+
+
 def test_deviation_algebra_on_clamped_rows_fp64():
     """Rows resting below 0 and above h_max: the clamp identity clamp(k+s,0,H) - clamp(k,0,H) =
     clamp(s,-k,H-k) + (k - clamp(k,0,H)) must hold exactly (brain.py:47-52)."""
