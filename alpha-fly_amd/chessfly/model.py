@@ -199,22 +199,48 @@ def _upload(a: np.ndarray, device) -> torch.Tensor:
     return host.to(device, non_blocking=True)
 
 
+# Workgroups of the answers' download (fly_evaluator_download).  With another batch in flight the copy shares the
+# GPU with that batch's forward, and its stores to host memory stall the CUs that issue them: 4 workgroups measured
+# best (B = 1120, lazy answers, two batches in flight: 6.846 ms per batch against 6.793 for the bare forward; 16
+# workgroups 6.943, the runtime's copy on every CU 7.036).  Alone, the copy only has to be fast: 64 workgroups.
+DOWNLOAD_SHARED, DOWNLOAD_ALONE = 4, 64
+
+
 class _Submitted:
     """A batch in flight: the pinned host buffers the device copies its answers into, and the event
-    recorded after the last copy.  The copies run on `down` after the compute stream's work so far."""
+    recorded after the last copy.  The copies run on `down` after the compute stream's work so far, as a
+    download kernel of `workgroups` workgroups (fly_evaluator_download)."""
 
-    def __init__(self, device_outputs, compute, down):
+    def __init__(self, device_outputs, compute, down, workgroups: int, on_done=None):
+        self._on_done = on_done
         down.wait_stream(compute)
         self.host = [torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for t in device_outputs]
+        lib = _hip.load()
         with torch.cuda.stream(down):
             for h, t in zip(self.host, device_outputs):
-                h.copy_(t, non_blocking=True)
+                _hip.check(lib.fly_evaluator_download(t.data_ptr(), h.data_ptr(), t.numel() * t.element_size(),
+                                                      workgroups, down.cuda_stream), "fly_evaluator_download")
                 t.record_stream(down)          # the allocator keeps t until this copy has read it
         self.done = torch.cuda.Event()
         self.done.record(down)
 
+    def _finish(self):
+        if self._on_done is not None:
+            self._on_done()
+            self._on_done = None
+
+    def __del__(self):
+        # torch's pinned-block cache does not see the download kernel's writes: a batch dropped unread keeps its
+        # host buffers until the kernel is done, so no later batch is handed a block still being written
+        try:
+            self.done.synchronize()
+        except Exception:
+            pass
+        self._finish()
+
     def wait(self):
         self.done.synchronize()
+        self._finish()
         policy, values, bad = self.host
         if int(bad[0]):
             raise IndexError("Evaluator: a legal-move index lies outside the (batch, N_MOVES) policy")
@@ -230,11 +256,14 @@ class Evaluator:
 
     Uploads and downloads run on two copy streams of their own, ordered with the compute stream (the
     device's current stream) by events: with two batches in flight, as the search's workers keep them
-    (workers.py:118-167), batch i+1's boards go up and batch i's answers come down while the GPU computes."""
+    (workers.py:118-167), batch i+1's boards go up and batch i's answers come down while the GPU computes.
+    A batch submitted while another is in flight downloads its answers on a few CUs (DOWNLOAD_SHARED), so
+    the forward it overlaps keeps the rest of the GPU."""
 
     def __init__(self, net: FlyChessNet, device):
         self.net, self.device = net, device
         self._up = self._down = None
+        self._in_flight = 0          # batches submitted and not yet read
 
     def _streams(self):
         if self._up is None:
@@ -282,7 +311,13 @@ class Evaluator:
         _hip.check(_hip.load().fly_evaluator_outputs(logits.data_ptr(), wdl.data_ptr(), batch, n_moves, _hip.ptr(r),
                                                      _hip.ptr(c), n_legal, out16, legal, values.data_ptr(),
                                                      bad.data_ptr(), compute.cuda_stream), "fly_evaluator_outputs")
-        return _Submitted((policy, values, bad), compute, down)
+        shared = self._in_flight > 0        # another batch still computes: keep the download to a few CUs
+        self._in_flight += 1
+        return _Submitted((policy, values, bad), compute, down, DOWNLOAD_SHARED if shared else DOWNLOAD_ALONE,
+                          self._landed)
+
+    def _landed(self):
+        self._in_flight -= 1
 
     @staticmethod
     def result(handle):

@@ -169,6 +169,7 @@ struct Tuning {
   int spmm_groups = 0;  // lane groups of the training SpMM on 16-byte lanes (2, 4, 8), 0 = automatic
   int gemm_tile = 0;    // dense-map workgroup tile: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, 10 TM + TN, 0 = auto
   int step_lds = 0;     // bytes of LDS each state-step workgroup reserves (caps waves per SIMD), 0 = none
+  int download_blocks = 0;  // workgroups of fly_evaluator_download when the call passes 0, 0 = automatic
 };
 Tuning &tuning();
 

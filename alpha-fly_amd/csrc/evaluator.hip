@@ -74,6 +74,21 @@ unsigned grid_for(int64_t work) {
   return std::max(1u, std::min<unsigned>(kMaxBlocks, blocks_for(std::max<int64_t>(work, 1), kThreads)));
 }
 
+// dst (pinned host memory, through its device address) = src (device memory), by a few workgroups that stride
+// over 16-byte pieces and then the tail bytes.  Stores to host memory wait on the bus, and a CU's memory pipeline
+// is in order: a full grid would stall every CU's other work behind them for the whole transfer, so only
+// `gridDim.x` CUs carry it while the next batch's forward runs on the rest.
+__global__ __launch_bounds__(kThreads) void k_host_copy(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                        int64_t bytes) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const int64_t first = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  const int64_t n16 = bytes / 16;
+  const uint4 *s16 = reinterpret_cast<const uint4 *>(src);
+  uint4 *d16 = reinterpret_cast<uint4 *>(dst);
+  for (int64_t i = first; i < n16; i += stride) d16[i] = s16[i];
+  for (int64_t i = n16 * 16 + first; i < bytes; i += stride) dst[i] = src[i];
+}
+
 }  // namespace
 }  // namespace fly
 
@@ -105,5 +120,29 @@ extern "C" int fly_evaluator_outputs(const float *logits, const float *wdl, int6
                          wdl, batch, n_moves, rows, cols, n_legal, legal, values, bad);
       check_launch("legal outputs");
     }
+  });
+}
+
+extern "C" int fly_evaluator_download(const void *src, void *dst_host, size_t bytes, int32_t workgroups,
+                                      void *stream) {
+  return guard([&] {
+    if (bytes == 0) return;
+    FLY_REQUIRE(src != nullptr && dst_host != nullptr, "null pointer");
+    FLY_REQUIRE(aligned(src, 16) && aligned(dst_host, 16), "source and destination must be 16-byte aligned");
+    hipPointerAttribute_t attr{};
+    const hipError_t e = hipPointerGetAttributes(&attr, dst_host);
+    if (e != hipSuccess) (void)hipGetLastError();   // an unknown host pointer: clear it, report it below
+    FLY_REQUIRE(e == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr,
+                "the destination must be pinned host memory (hipHostMalloc, torch pin_memory=True)");
+    const int wg = workgroups > 0 ? workgroups : (tuning().download_blocks > 0 ? tuning().download_blocks : 16);
+    const int64_t pieces = (int64_t)((bytes + 15) / 16);
+    const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(wg, (pieces + kThreads - 1) / kThreads));
+    // the device address of dst_host itself, whether the runtime reports the allocation's base or the pointer's own
+    // addresses (they then differ by the same offset)
+    uint8_t *dst = static_cast<uint8_t *>(attr.devicePointer);
+    if (attr.hostPointer != nullptr) dst += static_cast<uint8_t *>(dst_host) - static_cast<uint8_t *>(attr.hostPointer);
+    hipLaunchKernelGGL(k_host_copy, dim3(grid), dim3(kThreads), 0, as_stream(stream), static_cast<const uint8_t *>(src),
+                       dst, (int64_t)bytes);
+    check_launch("download");
   });
 }

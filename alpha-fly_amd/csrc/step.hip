@@ -517,6 +517,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "tiles") tuning().tiles = (int)value;
     else if (k == "spmm_groups") tuning().spmm_groups = (int)value;
     else if (k == "gemm_tile") tuning().gemm_tile = (int)value;
+    else if (k == "download_blocks") tuning().download_blocks = (int)value;
     else if (k == "step_lds") tuning().step_lds = (int)std::min<int64_t>(std::max<int64_t>(value, 0), 65536);
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });

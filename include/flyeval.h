@@ -25,6 +25,7 @@
  *   fly_model_forward     chessfly/model.py:95-105 FlyChessNet.forward (no-grad, device inputs)
  *   fly_evaluator_outputs chessfly/model.py:120-128 and :107-110 (Evaluator.submit's half cast or legal gather,
  *                         expected_value)
+ *   fly_evaluator_download chessfly/model.py:130-131 (Evaluator.result's copies of the answers to the host)
  *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
  *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass)
  *   fly_spmv_work         chessfly/brain.py:79-99 and :238-252 (grad_h = A^T grad_y of the resting trajectory's
@@ -230,6 +231,12 @@ int fly_model_forward_static(const fly_plan *plan, const fly_dense *dense, const
 int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t batch, int64_t n_moves,
                           const int64_t *rows_dev, const int64_t *cols_dev, int64_t n_legal, void *logits16_dev,
                           float *legal_dev, float *values_dev, int32_t *bad_dev, void *stream);
+/* The answers' trip to the host (chessfly/model.py:130-131, Evaluator.result's .cpu() of the policy and values):
+ * bytes from device memory to pinned host memory (hipHostMalloc, torch pin_memory=True), both 16-byte aligned,
+ * as a kernel on `stream` whose `workgroups` (0: the default, 16) write through the host buffer's device address.
+ * Stores to host memory wait on the bus and hold up the other work of the CUs that issue them; a copy queued on
+ * a stream of its own while the next batch computes therefore keeps to a few CUs. */
+int fly_evaluator_download(const void *src_dev, void *dst_host, size_t bytes, int32_t workgroups, void *stream);
 
 /* ---- training: the sparse products of the differentiable recurrence ----------------------------- */
 /* chessfly/brain.py:66-99 (_SparseRecurrent), float32.  A is CSR (rowptr nrows+1, col/val nnz, int32 and
@@ -388,7 +395,8 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * lane groups of fly_spmm on 16-byte lanes (2, 4, 8; 0 = automatic); "gemm_tile": workgroup tile of the dense
  * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, or 10 TM + TN for 32 TM x 32 TN with TM in {2, 3, 4} and TN in
  * {2, 4, 5}; 0 = automatic); "step_lds": bytes of LDS each state-step workgroup reserves, which caps the
- * workgroups a CU runs at once (0 = none).  Every selectable shape computes the same function. */
+ * workgroups a CU runs at once (0 = none); "download_blocks": workgroups of fly_evaluator_download when its call
+ * passes 0 (0 = 16).  Every selectable shape computes the same function. */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus

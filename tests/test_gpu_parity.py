@@ -539,6 +539,30 @@ def test_evaluator_outputs_kernel(batch, n_moves):
     assert bad == 0 and np.array_equal(values3, values)
 
 
+@pytest.mark.parametrize("nbytes", [4, 16, 100, 4100, 9_336_320])
+def test_evaluator_download_copies_to_pinned_host_memory(nbytes):
+    """fly_evaluator_download (the answers' copy to the host on a few CUs): every byte lands, for any length (16-byte
+    pieces and a tail) and any workgroup count; a destination that is not pinned host memory is refused, and the
+    refusal leaves no error behind for the next call."""
+    from chessfly import _hip
+    lib = _hip.load()
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=DEV)
+    st = _hip.stream(torch.device(DEV))
+    for wg in (0, 1, 3, 64):
+        dst = torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True)
+        _hip.check(lib.fly_evaluator_download(src.data_ptr(), dst.data_ptr(), nbytes, wg, st), "fly_evaluator_download")
+        torch.cuda.synchronize()
+        assert torch.equal(dst, src.cpu()), wg
+    plain = np.zeros(nbytes + 16, dtype=np.uint8)
+    addr = plain.ctypes.data + (-plain.ctypes.data) % 16
+    assert lib.fly_evaluator_download(src.data_ptr(), addr, nbytes, 0, st) != 0
+    assert b"pinned host memory" in lib.fly_last_error()
+    dst = torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True)
+    _hip.check(lib.fly_evaluator_download(src.data_ptr(), dst.data_ptr(), nbytes, 0, st), "fly_evaluator_download")
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src.cpu())
+
+
 def test_evaluator_protocol(full_net):
     """Evaluator.submit/result (chessfly/model.py:113-135): lazy fp16 policy vectors and eager legal gathers
     agree with FlyChessNet.forward on the same boards; several batches may be in flight at once."""
