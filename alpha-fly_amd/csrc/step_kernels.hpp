@@ -106,46 +106,63 @@ __device__ __forceinline__ WaveSlot wave_slot(const StepArgs<S, U> &a) {
   return {row, tile * (uint32_t)a.wpt + (in_tile - row * (uint32_t)a.wpt), tile < (uint32_t)a.ntiles};
 }
 
-// A row's constants, input drive and carried state for V columns, loaded before the gathers so their
-// latency overlaps the gather loop.  The carried state stays in its storage type until the epilogue (half the
-// registers for a float16 state, held across the whole loop).
-template <typename S, int V>
+// An empty asm that takes v in and out of vector registers: the compiler cannot move v's uses (a conversion, a
+// select) above this point, so a value loaded before the gathers is waited for here and not before them.
+template <typename T>
+__device__ __forceinline__ void keep_opaque(T &v) {
+  asm volatile("" : "+v"(v));
+}
+
+// A row's constants, input drive and carried state for V columns, loaded before the gathers so their latency
+// overlaps the gather loop.  The drive and the carried state stay in their storage types until the epilogue
+// (half the registers for float16), held opaque until then, so no wave waits for them before its gathers are
+// issued.  Only lanes with a drive or a carried state load them (measured: unconditional loads of row 0 for the
+// rest cost step 2, whose rows are 90% without a drive, 4% of its time).
+template <typename S, typename U, int V>
 struct RowInputs {
   RowParam p;
-  float u[V];
+  typename Lanes<U, V>::vec u;
   typename Lanes<S, V>::vec pv;
-  bool carried;
+  bool has_u, carried;
 };
 
 template <typename S, typename U, int V>
 __device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_t row, int64_t col, bool active,
-                                                RowInputs<S, V> &in) {
+                                                RowInputs<S, U, V> &in) {
   in.p = a.params[row];
-#pragma unroll
-  for (int i = 0; i < V; ++i) in.u[i] = 0.0f;
-  if (active && a.u != nullptr && in.p.usrc >= 0) {
+  in.has_u = active && a.u != nullptr && in.p.usrc >= 0;
+  in.carried = active && a.xprev != nullptr && in.p.prev >= 0;
+  in.u = Lanes<U, V>::zero();
+  in.pv = Lanes<S, V>::zero();
+  if (in.has_u) {
     const U *src = a.u + (int64_t)in.p.usrc * a.ldu + col;
     if (a.u_vec) {
-      Lanes<U, V>::load(src, in.u);
+      in.u = Lanes<U, V>::raw(src);
     } else {
+      // element by element inside the batch; past it element 0 again, masked in finish_row
 #pragma unroll
-      for (int i = 0; i < V; ++i) in.u[i] = (col + i < a.batch) ? static_cast<float>(src[i]) : 0.0f;
+      for (int i = 0; i < V; ++i) {
+        if constexpr (V == 1) in.u = src[0];
+        else in.u[i] = src[col + i < a.batch ? i : 0];
+      }
     }
   }
-  in.carried = active && a.xprev != nullptr && in.p.prev >= 0;
-  in.pv = in.carried ? Lanes<S, V>::raw(a.xprev + (int64_t)in.p.prev * a.ldx + col) : Lanes<S, V>::zero();
+  if (in.carried) in.pv = Lanes<S, V>::raw(a.xprev + (int64_t)in.p.prev * a.ldx + col);
 }
 
 // Input drive, clamp and leaky update of V columns of one row, then the store.
 template <typename S, typename U, int V, bool TORCH_LERP>
 __device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V],
-                                           const RowInputs<S, V> &in) {
+                                           RowInputs<S, U, V> &in) {
+  keep_opaque(in.u);
+  keep_opaque(in.pv);
   const RowParam &p = in.p;
   float out[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const float pv = in.carried ? Lanes<S, V>::at(in.pv, i) : p.pdef;
-    const float x = fminf(fmaxf((acc[i] + in.u[i]) + p.k, p.lo), p.hi) + p.e;
+    const float u = (in.has_u && (a.u_vec || col + i < a.batch)) ? Lanes<U, V>::at(in.u, i) : 0.0f;
+    const float x = fminf(fmaxf((acc[i] + u) + p.k, p.lo), p.hi) + p.e;
     out[i] = TORCH_LERP ? lerp_torch(pv, x, p.a) : fmaf(p.a, x - pv, pv);
   }
   Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out, a.nt_store != 0);
@@ -223,7 +240,7 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-  RowInputs<S, V> in;
+  RowInputs<S, U, V> in;
   load_row_inputs(a, w.row, col, active, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
@@ -280,7 +297,7 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  RowInputs<S, V> in;
+  RowInputs<S, U, V> in;
   if constexpr (REPLAY != 1) load_row_inputs(a, w.row, col, active && g == 0, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
@@ -383,7 +400,7 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  RowInputs<S, V> in;
+  RowInputs<S, U, V> in;
   if constexpr (REPLAY != 1) {
     if (has_row) load_row_inputs(a, row, col, active, in);
   }
