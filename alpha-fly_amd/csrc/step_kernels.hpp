@@ -15,6 +15,9 @@
 // builds; the evaluator library instantiates only REPLAY = 0).
 #pragma once
 
+#include <type_traits>
+#include <utility>
+
 #include "common.hpp"
 #include "device.hpp"
 
@@ -113,6 +116,23 @@ __device__ __forceinline__ void keep_opaque(T &v) {
   asm volatile("" : "+v"(v));
 }
 
+// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N - 1>), unrolled at compile time.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// Lane J of each group of 8 lanes, to every lane of the group (ds_swizzle in bit mode: the source of lane l is
+// (l & 0x18) | J within its half-wave).  Cross-lane traffic of the LDS unit, not a memory access.
+template <int J>
+__device__ __forceinline__ int bcast8(int v) {
+  return __builtin_amdgcn_ds_swizzle(v, 0x18 | (J << 5));
+}
+
 // A row's constants, input drive and carried state for V columns, loaded before the gathers so their latency
 // overlaps the gather loop.  The drive and the carried state stay in their storage types until the epilogue
 // (half the registers for float16), held opaque until then, so no wave waits for them before its gathers are
@@ -126,10 +146,29 @@ struct RowInputs {
   bool has_u, carried;
 };
 
+// The constants of each lane group's row for groups of 8 lanes: lane s reads word s of the 32-byte record and the
+// group's lanes exchange them, one 4-byte load per lane instead of eight lanes each reading all 32 bytes.
+template <typename S, typename U>
+__device__ __forceinline__ RowParam row_param_shared8(const StepArgs<S, U> &a, uint32_t row, bool has_row, int s) {
+  const int word = has_row ? reinterpret_cast<const int *>(a.params + row)[s] : 0;
+  int w[8];
+  static_for<8>([&](auto J) { w[decltype(J)::value] = bcast8<decltype(J)::value>(word); });
+  RowParam p;
+  p.k = __int_as_float(w[0]);
+  p.lo = __int_as_float(w[1]);
+  p.hi = __int_as_float(w[2]);
+  p.e = __int_as_float(w[3]);
+  p.a = __int_as_float(w[4]);
+  p.pdef = __int_as_float(w[5]);
+  p.prev = w[6];
+  p.usrc = w[7];
+  return p;
+}
+
+// The drive and carried state of a row whose constants in.p are already loaded.
 template <typename S, typename U, int V>
-__device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_t row, int64_t col, bool active,
-                                                RowInputs<S, U, V> &in) {
-  in.p = a.params[row];
+__device__ __forceinline__ void load_row_drive(const StepArgs<S, U> &a, int64_t col, bool active,
+                                               RowInputs<S, U, V> &in) {
   in.has_u = active && a.u != nullptr && in.p.usrc >= 0;
   in.carried = active && a.xprev != nullptr && in.p.prev >= 0;
   in.u = Lanes<U, V>::zero();
@@ -148,6 +187,26 @@ __device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_
     }
   }
   if (in.carried) in.pv = Lanes<S, V>::raw(a.xprev + (int64_t)in.p.prev * a.ldx + col);
+}
+
+// The constants of a wave-uniform row, through the scalar cache: the record is read once per wave, not by every
+// lane through the texture path (the params array is never written while a step runs).
+template <typename S, typename U>
+__device__ __forceinline__ RowParam row_param_uniform(const StepArgs<S, U> &a, uint32_t row) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __attribute__((address_space(4))) const RowParam const_param;   // the constant address space
+  return ((const_param *)a.params)[row];
+#else
+  return a.params[row];   // (the host pass only parses device code)
+#endif
+}
+
+template <typename S, typename U, int V, bool UNIFORM = false>
+__device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_t row, int64_t col, bool active,
+                                                RowInputs<S, U, V> &in) {
+  if constexpr (UNIFORM) in.p = row_param_uniform(a, row);
+  else in.p = a.params[row];
+  load_row_drive(a, col, active, in);
 }
 
 // Input drive, clamp and leaky update of V columns of one row, then the store.
@@ -241,7 +300,7 @@ __global__ __launch_bounds__(256) void k_state_step(const StepArgs<S, U> a) {
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   RowInputs<S, U, V> in;
-  load_row_inputs(a, w.row, col, active, in);
+  load_row_inputs<S, U, V, true>(a, w.row, col, active, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
     const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
@@ -298,7 +357,7 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
   RowInputs<S, U, V> in;
-  if constexpr (REPLAY != 1) load_row_inputs(a, w.row, col, active && g == 0, in);
+  if constexpr (REPLAY != 1) load_row_inputs<S, U, V, true>(a, w.row, col, active && g == 0, in);
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
     const int32_t beg = a.rowptr[w.row], end = a.rowptr[w.row + 1];
@@ -381,8 +440,11 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
 
 // G rows at a time per wave, for steps whose rows hold few non-zeros: group g of 64/G lanes owns row
 // G*slot + g and walks its non-zeros, gathering (64/G) * V columns per load; the wave loops to the longest
-// of its rows with the shorter rows' loads masked off, and every group finishes its own row.
-template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, int REPLAY = 0>
+// of its rows with the shorter rows' loads masked off, and every group finishes its own row.  With groups of 8
+// lanes (SHARED) the group's {column, weight} records and row constants are read once per group and passed
+// between its lanes (these steps are bound by the texture data path, which every per-lane copy of a record
+// goes through).
+template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, int REPLAY = 0, bool SHARED = true>
 __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a) {
   constexpr int LPG = 64 / G;
   const WaveSlot w = wave_slot(a);                // w.row counts slots of G rows
@@ -402,7 +464,12 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
   RowInputs<S, U, V> in;
   if constexpr (REPLAY != 1) {
-    if (has_row) load_row_inputs(a, row, col, active, in);
+    if constexpr (G == 8 && SHARED) {
+      in.p = row_param_shared8(a, row, has_row, s);
+      load_row_drive(a, col, active, in);
+    } else if (has_row) {
+      load_row_inputs(a, row, col, active, in);
+    }
   }
 
   if (a.xprev != nullptr && a.rowptr != nullptr) {
@@ -424,6 +491,50 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
     const uint32_t row_bytes = (uint32_t)a.ldx * (uint32_t)sizeof(S), voff = (uint32_t)lcol * (uint32_t)sizeof(S);
+    if constexpr (G == 8 && SHARED) {
+      if (buf) {
+        // One 8-byte load per lane brings the group's next 8 records (lane s: record k + s of its row, the index
+        // clamped into the row so every load is in bounds), and slot j of the block reaches the group's lanes by
+        // a broadcast of lane j: one record load per 8 gathers instead of one per gather.  Records past a row's
+        // end only feed gathers that are skipped.
+        auto block = [&](int32_t k) {
+          const int32_t e = max(min(beg + k + s, end - 1), 0);
+          return a.colval[e];
+        };
+        // (the next block loads unconditionally, clamped, so no branch makes the wave drain its loads; slots past
+        // a row's end gather at an offset past the buffer, which reads zeros without touching memory)
+        int2 rec = len > 0 ? block(0) : make_int2(0, 0);
+        for (int32_t k = 0; k < len; k += 8) {
+          const int2 nxt = block(k + 8);
+          static_for<8 / UNROLL>([&](auto H) {
+            constexpr int h0 = decltype(H)::value * UNROLL;
+            typename Lanes<S, V>::vec xr[UNROLL];
+            int wj[UNROLL];
+            static_for<UNROLL>([&](auto J) {
+              constexpr int j = decltype(J)::value, sl = h0 + j;
+              const int c = bcast8<sl>(rec.x);
+              wj[j] = bcast8<sl>(rec.y);
+              const uint32_t off = beg + k + sl < end ? __umul24((uint32_t)c, row_bytes) + voff : 0x80000000u;
+              xr[j] = bload<S, V>(r, (int)off, 0);
+            });
+            if constexpr (REPLAY != 0) {
+#pragma unroll
+              for (int j = 0; j < UNROLL; ++j) ReplayBits<S, V>::fold(bits, xr[j], wj[j]);
+            } else {
+#pragma unroll
+              for (int j = 0; j < UNROLL; ++j) {
+                const float wt = __int_as_float(wj[j]);
+#pragma unroll
+                for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, Lanes<S, V>::at(xr[j], i), acc[i]);
+              }
+            }
+          });
+          rec = nxt;
+        }
+        goto gathered;
+      }
+    }
+    {
     int2 cv[UNROLL];
     if (len > 0) pairs(0, cv);
     for (int32_t k = 0; k < len; k += UNROLL) {
@@ -454,7 +565,9 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
 #pragma unroll
       for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
     }
+    }
   }
+gathered:
   if constexpr (REPLAY == 1) {
     ReplayBits<S, V>::sink(a, bits);
     return;
