@@ -82,35 +82,62 @@ __global__ __launch_bounds__(256) void k_split_rows(const T *__restrict__ src, i
 
 // Normalised outputs r[n, k] split into (N x kp) hi/lo rows, read from the state (rows, lds) where output k
 // sits at row src[k] (-1: not carried; src null: row k), plus cbase[k] (null: 0).  A 64x64 tile goes through
-// LDS so both the state reads (n fastest) and the split writes (k fastest) are contiguous.
+// LDS so both the state reads (n fastest) and the split writes (k fastest) are contiguous; each thread reads 4
+// boards of a row (one 8- or 16-byte load when `vec`: the state's rows hold whole groups of 4) and writes 4
+// outputs of a board (8-byte stores of hi and lo).
 template <typename S>
-__global__ __launch_bounds__(256) void k_norm_split(const S *__restrict__ state, int64_t lds, const int32_t *__restrict__ src,
-                                                    const float *__restrict__ cbase, const float *__restrict__ mean,
-                                                    const float *__restrict__ var, float eps, float clip, int64_t K,
-                                                    int64_t N, _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
-                                                    int64_t kp) {
+__global__ __launch_bounds__(256) void k_norm_split(const S *__restrict__ state, int64_t lds, bool vec,
+                                                    const int32_t *__restrict__ src, const float *__restrict__ cbase,
+                                                    const float *__restrict__ mean, const float *__restrict__ var,
+                                                    float eps, float clip, int64_t K, int64_t N,
+                                                    _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, int64_t kp) {
+  typedef S vec4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
   __shared__ float tile[64][65];
   const int64_t k0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int kk = ty; kk < 64; kk += 4) {
-    const int64_t k = k0 + kk, n = n0 + tx;
-    float v = 0.0f;
-    if (k < K && n < N) {
+  const int q = (threadIdx.x & 15) * 4, r16 = threadIdx.x >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int kk = r16 + 16 * j;
+    const int64_t k = k0 + kk, n = n0 + q;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (k < K) {
       const int32_t row = src ? src[k] : (int32_t)k;
-      const float r = (cbase ? cbase[k] : 0.0f) +
-                      ((state != nullptr && row >= 0) ? static_cast<float>(state[(int64_t)row * lds + n]) : 0.0f);
-      v = fminf(fmaxf((r - mean[k]) / sqrtf(var[k] + eps), -clip), clip);
+      const float c = cbase ? cbase[k] : 0.0f, m = mean[k], sd = sqrtf(var[k] + eps);
+      float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (state != nullptr && row >= 0) {
+        const S *p = state + (int64_t)row * lds + n;
+        if (vec && n + 3 < N) {
+          const vec4 w = *reinterpret_cast<const vec4 *>(p);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = static_cast<float>(w[i]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = n + i < N ? static_cast<float>(p[i]) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < N) v[i] = fminf(fmaxf(((c + x[i]) - m) / sd, -clip), clip);
     }
-    tile[kk][tx] = v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tile[kk][q + i] = v[i];
   }
   __syncthreads();
-  for (int nn = ty; nn < 64; nn += 4) {
-    const int64_t n = n0 + nn, k = k0 + tx;
-    if (n < N && k < kp) {
-      const float v = tile[tx][nn];
-      const _Float16 h = static_cast<_Float16>(v);
-      hi[n * kp + k] = h;
-      lo[n * kp + k] = static_cast<_Float16>(v - static_cast<float>(h));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int nn = r16 + 16 * j;
+    const int64_t n = n0 + nn, k = k0 + q;
+    if (n < N && k < kp) {   // kp is a multiple of 64: the 4 outputs are inside the row
+      half4 h, l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = tile[q + i][nn];
+        h[i] = static_cast<_Float16>(v);
+        l[i] = static_cast<_Float16>(v - static_cast<float>(h[i]));
+      }
+      *reinterpret_cast<half4 *>(hi + n * kp + k) = h;
+      *reinterpret_cast<half4 *>(lo + n * kp + k) = l;
     }
   }
 }
@@ -457,8 +484,9 @@ void run_head(const fly_dense &d, const S *state, int64_t lds, const int32_t *sr
   _Float16 *rl = reinterpret_cast<_Float16 *>(base + split_bytes(batch, d.kp_head));
   float *ct = reinterpret_cast<float *>(base + 2 * split_bytes(batch, d.kp_head));
   const dim3 grid(blocks_for(batch, 64), (unsigned)((d.kp_head + 63) / 64));
-  hipLaunchKernelGGL(k_norm_split<S>, grid, dim3(256), 0, st, state, lds, src, cbase, d.norm_mean.p, d.norm_var.p, d.eps,
-                     d.clip, d.n_out, batch, rh, rl, d.kp_head);
+  const bool vec = lds % 4 == 0 && aligned(state, 4 * sizeof(S));
+  hipLaunchKernelGGL(k_norm_split<S>, grid, dim3(256), 0, st, state, lds, vec, src, cbase, d.norm_mean.p, d.norm_var.p,
+                     d.eps, d.clip, d.n_out, batch, rh, rl, d.kp_head);
   check_launch("normalised outputs");
   const int64_t ldc = head_ld(d);
   gemm_split(Split{d.head_hi.p, d.head_lo.p, d.head_rows(), nullptr}, Split{rh, rl, batch, nullptr}, d.kp_head,
