@@ -491,8 +491,10 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
     const uint32_t row_bytes = (uint32_t)a.ldx * (uint32_t)sizeof(S), voff = (uint32_t)lcol * (uint32_t)sizeof(S);
+    bool shared = false;   // the records came through the shared path below
     if constexpr (G == 8 && SHARED) {
       if (buf) {
+        shared = true;
         // One 8-byte load per lane brings the group's next 8 records (lane s: record k + s of its row, the index
         // clamped into the row so every load is in bounds), and slot j of the block reaches the group's lanes by
         // a broadcast of lane j: one record load per 8 gathers instead of one per gather.  Records past a row's
@@ -531,43 +533,41 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
           });
           rec = nxt;
         }
-        goto gathered;
       }
     }
-    {
-    int2 cv[UNROLL];
-    if (len > 0) pairs(0, cv);
-    for (int32_t k = 0; k < len; k += UNROLL) {
-      typename Lanes<S, V>::vec xr[UNROLL];
-      if (buf) {
+    if (!shared) {
+      int2 cv[UNROLL];
+      if (len > 0) pairs(0, cv);
+      for (int32_t k = 0; k < len; k += UNROLL) {
+        typename Lanes<S, V>::vec xr[UNROLL];
+        if (buf) {
 #pragma unroll
-        for (int j = 0; j < UNROLL; ++j)
-          xr[j] = (beg + k + j < end) ? bload<S, V>(r, (int)(__umul24((uint32_t)cv[j].x, row_bytes) + voff), 0)
-                                      : Lanes<S, V>::zero();
-      } else {
+          for (int j = 0; j < UNROLL; ++j)
+            xr[j] = (beg + k + j < end) ? bload<S, V>(r, (int)(__umul24((uint32_t)cv[j].x, row_bytes) + voff), 0)
+                                        : Lanes<S, V>::zero();
+        } else {
 #pragma unroll
-        for (int j = 0; j < UNROLL; ++j)
-          xr[j] = (beg + k + j < end) ? Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx) : Lanes<S, V>::zero();
-      }
-      int2 nx[UNROLL];
-      if (k + UNROLL < len) pairs(k + UNROLL, nx);
-      if constexpr (REPLAY != 0) {
-#pragma unroll
-        for (int j = 0; j < UNROLL; ++j) ReplayBits<S, V>::fold(bits, xr[j], cv[j].y);
-      } else {
-#pragma unroll
-        for (int j = 0; j < UNROLL; ++j) {
-          const float wt = __int_as_float(cv[j].y);
-#pragma unroll
-          for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, Lanes<S, V>::at(xr[j], i), acc[i]);
+          for (int j = 0; j < UNROLL; ++j)
+            xr[j] = (beg + k + j < end) ? Lanes<S, V>::raw(base + (int64_t)cv[j].x * a.ldx) : Lanes<S, V>::zero();
         }
-      }
+        int2 nx[UNROLL];
+        if (k + UNROLL < len) pairs(k + UNROLL, nx);
+        if constexpr (REPLAY != 0) {
 #pragma unroll
-      for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
-    }
+          for (int j = 0; j < UNROLL; ++j) ReplayBits<S, V>::fold(bits, xr[j], cv[j].y);
+        } else {
+#pragma unroll
+          for (int j = 0; j < UNROLL; ++j) {
+            const float wt = __int_as_float(cv[j].y);
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] = fmaf(wt, Lanes<S, V>::at(xr[j], i), acc[i]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < UNROLL; ++j) cv[j] = nx[j];
+      }
     }
   }
-gathered:
   if constexpr (REPLAY == 1) {
     ReplayBits<S, V>::sink(a, bits);
     return;
