@@ -382,17 +382,33 @@ void gemm_split(const Split &A, const Split &B, int64_t kp, float unscale, const
 
 // logits[n, i] = (ct[n, i] + b[i]) + (ct[n, M + f] + b[M + f]) + (ct[n, M + 64 + t] + b[M + 64 + t]),
 // wdl[n, j] = ct[n, M + 128 + j] + b[M + 128 + j], with M = n_moves and (f, t) the move's squares.
-__global__ void k_assemble(const float *__restrict__ ct, int64_t ldc, int64_t n_moves, const float *__restrict__ b,
-                           const int32_t *__restrict__ mfrom, const int32_t *__restrict__ mto, int64_t batch,
-                           float *__restrict__ logits, float *__restrict__ wdl) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  for (int64_t n = blockIdx.y; n < batch; n += gridDim.y) {
+// One workgroup per board: its from- and to-square terms (64 + 64 values plus biases) go to LDS once, then each
+// thread writes 4 consecutive moves with 16-byte loads and stores when `vec` (the move count and the rows allow
+// them), one move at a time otherwise.
+__global__ __launch_bounds__(256) void k_assemble(const float *__restrict__ ct, int64_t ldc, int64_t n_moves,
+                                                  const float *__restrict__ b, const int32_t *__restrict__ mfrom,
+                                                  const int32_t *__restrict__ mto, int64_t batch, bool vec,
+                                                  float *__restrict__ logits, float *__restrict__ wdl) {
+  __shared__ float sq[128];
+  for (int64_t n = blockIdx.x; n < batch; n += gridDim.x) {
     const float *row = ct + n * ldc;
-    if (i < n_moves) {
-      const int64_t f = n_moves + mfrom[i], t = n_moves + 64 + mto[i];
-      logits[n * n_moves + i] = ((row[i] + b[i]) + (row[f] + b[f])) + (row[t] + b[t]);
+    __syncthreads();   // the previous board's squares are read
+    if (threadIdx.x < 128) sq[threadIdx.x] = row[n_moves + threadIdx.x] + b[n_moves + threadIdx.x];
+    if (threadIdx.x < 3) wdl[n * 3 + threadIdx.x] = row[n_moves + 128 + threadIdx.x] + b[n_moves + 128 + threadIdx.x];
+    __syncthreads();
+    float *out = logits + n * n_moves;
+    if (vec) {
+      for (int64_t i = 4 * (int64_t)threadIdx.x; i < n_moves; i += 4 * (int64_t)blockDim.x) {
+        const float4 p = *reinterpret_cast<const float4 *>(row + i), bp = *reinterpret_cast<const float4 *>(b + i);
+        const int4 fr = *reinterpret_cast<const int4 *>(mfrom + i), to = *reinterpret_cast<const int4 *>(mto + i);
+        *reinterpret_cast<float4 *>(out + i) =
+            make_float4(((p.x + bp.x) + sq[fr.x]) + sq[64 + to.x], ((p.y + bp.y) + sq[fr.y]) + sq[64 + to.y],
+                        ((p.z + bp.z) + sq[fr.z]) + sq[64 + to.z], ((p.w + bp.w) + sq[fr.w]) + sq[64 + to.w]);
+      }
+    } else {
+      for (int64_t i = threadIdx.x; i < n_moves; i += blockDim.x)
+        out[i] = ((row[i] + b[i]) + sq[mfrom[i]]) + sq[64 + mto[i]];
     }
-    if (i < 3) wdl[n * 3 + i] = row[n_moves + 128 + i] + b[n_moves + 128 + i];
   }
 }
 
@@ -492,9 +508,9 @@ void run_head(const fly_dense &d, const S *state, int64_t lds, const int32_t *sr
   gemm_split(Split{d.head_hi.p, d.head_lo.p, d.head_rows(), nullptr}, Split{rh, rl, batch, nullptr}, d.kp_head,
              d.head_unscale,
              HeadEpilogue{ct, ldc}, st);
-  const dim3 agrid(blocks_for(d.n_moves, 256), (unsigned)std::min<int64_t>(batch, 65535));
-  hipLaunchKernelGGL(k_assemble, agrid, dim3(256), 0, st, ct, ldc, d.n_moves, d.head_b.p, d.move_from.p, d.move_to.p,
-                     batch, logits, wdl);
+  const bool avec = d.n_moves % 4 == 0 && ldc % 4 == 0 && aligned(logits, 16);
+  hipLaunchKernelGGL(k_assemble, dim3((unsigned)std::min<int64_t>(batch, 65535)), dim3(256), 0, st, ct, ldc, d.n_moves,
+                     d.head_b.p, d.move_from.p, d.move_to.p, batch, avec, logits, wdl);
   check_launch("head assembly");
 }
 
