@@ -279,6 +279,38 @@ def test_unbounded_activity_literal_and_light_cone():
     assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
 
 
+def test_other_activity_bounds_literal_and_light_cone():
+    """A bound other than 10 (the reference's fused kernel applies only at h_max == 10, brain.py:310; its general
+    path clamps to any h_max, brain.py:321): activity pushed past h_max = 3.5 by the biases, the literal recurrence
+    and forward_io in float32 against the float64 oracle, and the float16 deviation path against the exact
+    function, as for h_max = None."""
+    conn = _medium(5)
+    lg, b, al = random_params(conn, 22, gain_sd=0.1, bias_mean=2.0, bias_sd=2.0)
+    rnn = _rnn(conn, 3.0, lg, b, al, h_max=3.5)
+    ba = brain_arrays(conn, 3.0, lg, b, al, h_max=3.5, dtype=torch.float64)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    g = torch.Generator().manual_seed(8)
+    u = torch.randn(conn.n_neurons, 40, generator=g) * 2
+    ref = F.literal(ba, u.double(), 5).numpy()
+    free = F.literal(brain_arrays(conn, 3.0, lg, b, al, h_max=None, dtype=torch.float64), u.double(), 5).numpy()
+    assert ref.max() <= 3.5 and np.abs(ref - free).max() > 0.5      # the bound acts
+    with torch.no_grad():
+        h = rnn(u.clone().to(DEV), 5)
+    np.testing.assert_allclose(h.cpu().numpy(), ref, rtol=2e-5, atol=2e-5 * np.abs(ref).max())
+    u_in = torch.randn(len(in_idx), 40, generator=g) * 2
+    cone = _cone(conn, in_idx, out_idx, 6)
+    exact = F.cone_f32(ba, cone, u_in.double(), 6).numpy()
+    ind, outd = in_idx.to(DEV), out_idx.to(DEV)
+    with torch.no_grad():
+        out32 = rnn.forward_io(u_in.to(DEV), ind, outd, 6)
+        out16 = rnn.forward_io(u_in.half().to(DEV), ind, outd, 6)
+    np.testing.assert_allclose(out32.cpu().numpy(), exact, rtol=2e-5, atol=2e-5 * np.abs(exact).max())
+    exact16 = F.cone_f32(ba, cone, u_in.half().double(), 6).numpy()
+    dev_scale = np.abs(exact16 - F.cone_f32(ba, cone, torch.zeros_like(u_in).double(), 6).numpy()).max()
+    err = np.abs(out16.cpu().numpy() - exact16).max()
+    assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
+
+
 # ---- fly_plan_step: one step at a time ---------------------------------------------------------------------------
 
 def _plan_step(lib, _hip, plan, t, xprev, u, batch, xout):
