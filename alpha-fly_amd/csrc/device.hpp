@@ -3,6 +3,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace fly {
 
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer resource: 32-bit data, no swizzle
@@ -25,6 +28,25 @@ __device__ __forceinline__ float group_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
   v += __int_as_float(__builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
   return v;
+}
+
+// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N - 1>), unrolled at compile time.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// Lane J of each group of N consecutive lanes (N = 8 or 16), to every lane of the group: ds_swizzle in bit mode,
+// where lane l reads lane (l & (0x1F & ~(N - 1))) | J of its half-wave.  Cross-lane traffic of the LDS unit, not
+// a memory access: a record loaded once per group reaches all of its lanes.
+template <int N, int J>
+__device__ __forceinline__ int group_bcast(int v) {
+  static_assert((N == 8 || N == 16) && J >= 0 && J < N, "groups of 8 or 16 lanes");
+  return __builtin_amdgcn_ds_swizzle(v, (0x1F & ~(N - 1)) | (J << 5));
 }
 
 }  // namespace fly

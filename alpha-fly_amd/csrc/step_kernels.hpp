@@ -15,9 +15,6 @@
 // builds; the evaluator library instantiates only REPLAY = 0).
 #pragma once
 
-#include <type_traits>
-#include <utility>
-
 #include "common.hpp"
 #include "device.hpp"
 
@@ -116,23 +113,6 @@ __device__ __forceinline__ void keep_opaque(T &v) {
   asm volatile("" : "+v"(v));
 }
 
-// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N - 1>), unrolled at compile time.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_seq(f, std::make_integer_sequence<int, N>{});
-}
-
-// Lane J of each group of 8 lanes, to every lane of the group (ds_swizzle in bit mode: the source of lane l is
-// (l & 0x18) | J within its half-wave).  Cross-lane traffic of the LDS unit, not a memory access.
-template <int J>
-__device__ __forceinline__ int bcast8(int v) {
-  return __builtin_amdgcn_ds_swizzle(v, 0x18 | (J << 5));
-}
-
 // A row's constants, input drive and carried state for V columns, loaded before the gathers so their latency
 // overlaps the gather loop.  The drive and the carried state stay in their storage types until the epilogue
 // (half the registers for float16), held opaque until then, so no wave waits for them before its gathers are
@@ -152,7 +132,7 @@ template <typename S, typename U>
 __device__ __forceinline__ RowParam row_param_shared8(const StepArgs<S, U> &a, uint32_t row, bool has_row, int s) {
   const int word = has_row ? reinterpret_cast<const int *>(a.params + row)[s] : 0;
   int w[8];
-  static_for<8>([&](auto J) { w[decltype(J)::value] = bcast8<decltype(J)::value>(word); });
+  static_for<8>([&](auto J) { w[decltype(J)::value] = group_bcast<8, decltype(J)::value>(word); });
   RowParam p;
   p.k = __int_as_float(w[0]);
   p.lo = __int_as_float(w[1]);
@@ -514,8 +494,8 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
             int wj[UNROLL];
             static_for<UNROLL>([&](auto J) {
               constexpr int j = decltype(J)::value, sl = h0 + j;
-              const int c = bcast8<sl>(rec.x);
-              wj[j] = bcast8<sl>(rec.y);
+              const int c = group_bcast<8, sl>(rec.x);
+              wj[j] = group_bcast<8, sl>(rec.y);
               const uint32_t off = beg + k + sl < end ? __umul24((uint32_t)c, row_bytes) + voff : 0x80000000u;
               xr[j] = bload<S, V>(r, (int)off, 0);
             });
