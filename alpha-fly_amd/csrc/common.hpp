@@ -111,13 +111,15 @@ inline int64_t state_ld(int64_t batch, size_t elem) {
   return ld;
 }
 
-// Size of a state buffer for 32-bit buffer addressing, or 0 when it does not fit below 2^31 bytes or a row is
-// 2^24 bytes or more: a gather's offset is one 24-bit multiply (column times row bytes), so the row size must
-// fit 24 bits (a larger row takes the 64-bit path, or block_cols splits the batch below it).
+// Size of a state buffer for 32-bit buffer addressing, or 0 when it does not fit below 2^31 bytes, a row is
+// 2^24 bytes or more, or it holds more than 2^24 rows: a gather's offset is one 24-bit multiply (row index times
+// row bytes), so both operands must fit 24 bits (otherwise the 64-bit path runs, or block_cols splits the batch).
 inline uint32_t buffer_bytes(int64_t rows, int64_t ld, size_t elem) {
   const int64_t row_bytes = ld * (int64_t)elem;
   const int64_t bytes = rows * row_bytes;
-  return bytes > 0 && bytes <= (int64_t)INT32_MAX && row_bytes < (int64_t)(1 << 24) ? (uint32_t)bytes : 0u;
+  return bytes > 0 && bytes <= (int64_t)INT32_MAX && row_bytes < (int64_t)(1 << 24) && rows <= (int64_t)(1 << 24)
+             ? (uint32_t)bytes
+             : 0u;
 }
 
 // Constants of one row of a state step (32 bytes, read once per row by a wave):
