@@ -1,7 +1,8 @@
 """GPU parity for the benchmark workloads and call paths beyond the headline forward: the shuffled control graph
 (repeated pairs and self-loops summed), the unpruned float16-deviation and float32 forwards, 20-40-ones boards at
-B = 256, the attack-plane encoder, unbounded activity (h_max=None) and the per-step export fly_plan_step, each
-against the CPU oracle through the C ABI.
+B = 256, the attack-plane encoder, the factorised policy head, unbounded activity (h_max=None) and the per-step
+export fly_plan_step, each against the CPU oracle (or, for the policy head, the layer-by-layer path) through the
+C ABI.
 
 Tolerances: float32 paths within float32 round-off of the float64 oracle (2e-5); full models within 1e-3 max-abs
 of the oracle's float32 forward with the argmax equal; the float16 deviation path against the exact function
@@ -238,6 +239,39 @@ def test_full_scale_attack_planes(full_net):
         net.infer_dtype = torch.float16
         with torch.no_grad():
             net.encoder.weight.copy_(saved)
+
+
+# ---- the factorised policy head ----------------------------------------------------------------------------------
+
+def test_factorised_policy_head_is_a_no_op_until_trained():
+    """model.py:80-93 (test_core.py:394-415): the from- and to-square heads start at zero, and a checkpoint from
+    before them loads, so the fused forward's logits equal policy(norm(forward_io(...))).  Here the policy map is
+    random (at its zero initialisation both sides would be the bias alone).  Float32: to float32 round-off of the
+    layer-by-layer path; float16 deviation: within 1e-3 of it, the bound between the two precisions."""
+    from chessfly.encoding import N_BASE, N_FEATURES
+    from chessfly.model import FlyChessNet, ModelConfig, load_weights
+    net = FlyChessNet(tiny_connectome(60, 600), ModelConfig(steps=3)).to(DEV).eval()
+    old = {k: v for k, v in net.state_dict().items() if not k.startswith(("policy_from.", "policy_to."))}
+    load_weights(net, old)                                  # a checkpoint from before the shared terms
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        net.policy.weight.copy_(torch.randn(net.policy.weight.shape, generator=g) * 0.3)
+        assert float(net.policy_from.weight.abs().sum() + net.policy_to.weight.abs().sum()) == 0
+    x = torch.rand(3, N_FEATURES, generator=g).to(DEV)
+    with torch.no_grad():
+        enc = torch.nn.functional.linear(x[:, :N_BASE], net.encoder.weight[:, :N_BASE], net.encoder.bias)
+        u_in = (enc * net.cfg.input_gain).T.contiguous()
+        r = net.norm(net.brain.forward_io(u_in, net.in_idx, net.out_idx, 3).T.float())
+        nn_only = net.policy(r)
+        try:
+            for dtype, tol in ((torch.float32, 1e-5), (torch.float16, 1e-3)):
+                net.infer_dtype = dtype
+                logits, _ = net(x)
+                d = float((logits - nn_only).abs().max())
+                print(f"{dtype}: max |fused - policy(norm(forward_io))| {d:.3e}", flush=True)
+                torch.testing.assert_close(logits, nn_only, rtol=tol, atol=tol)
+        finally:
+            net.infer_dtype = torch.float16
 
 
 # ---- h_max=None: no upper clamp --------------------------------------------------------------------------------
