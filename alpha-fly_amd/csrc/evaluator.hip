@@ -129,9 +129,14 @@ extern "C" int fly_evaluator_download(const void *src, void *dst_host, size_t by
     if (bytes == 0) return;
     FLY_REQUIRE(src != nullptr && dst_host != nullptr, "null pointer");
     FLY_REQUIRE(aligned(src, 16) && aligned(dst_host, 16), "source and destination must be 16-byte aligned");
+    hipPointerAttribute_t sattr{};
+    const hipError_t se = hipPointerGetAttributes(&sattr, src);
+    if (se != hipSuccess) (void)hipGetLastError();   // an unknown pointer: clear the error, report it below
+    FLY_REQUIRE(se == hipSuccess && (sattr.type == hipMemoryTypeDevice || sattr.type == hipMemoryTypeManaged),
+                "the source must be device memory");
     hipPointerAttribute_t attr{};
     const hipError_t e = hipPointerGetAttributes(&attr, dst_host);
-    if (e != hipSuccess) (void)hipGetLastError();   // an unknown host pointer: clear it, report it below
+    if (e != hipSuccess) (void)hipGetLastError();
     FLY_REQUIRE(e == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr,
                 "the destination must be pinned host memory (hipHostMalloc, torch pin_memory=True)");
     const int wg = workgroups > 0 ? workgroups : (tuning().download_blocks > 0 ? tuning().download_blocks : 16);

@@ -234,6 +234,7 @@ int fly_evaluator_outputs(const float *logits_dev, const float *wdl_dev, int64_t
 /* The answers' trip to the host (chessfly/model.py:130-131, Evaluator.result's .cpu() of the policy and values):
  * bytes from device memory to pinned host memory (hipHostMalloc, torch pin_memory=True), both 16-byte aligned,
  * as a kernel on `stream` whose `workgroups` (0: the default, 16) write through the host buffer's device address.
+ * Any other kind of source or destination is FLY_ERR_INVALID.
  * Stores to host memory wait on the bus and hold up the other work of the CUs that issue them; a copy queued on
  * a stream of its own while the next batch computes therefore keeps to a few CUs. */
 int fly_evaluator_download(const void *src_dev, void *dst_host, size_t bytes, int32_t workgroups, void *stream);

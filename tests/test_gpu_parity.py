@@ -542,8 +542,8 @@ def test_evaluator_outputs_kernel(batch, n_moves):
 @pytest.mark.parametrize("nbytes", [4, 16, 100, 4100, 9_336_320])
 def test_evaluator_download_copies_to_pinned_host_memory(nbytes):
     """fly_evaluator_download (the answers' copy to the host on a few CUs): every byte lands, for any length (16-byte
-    pieces and a tail) and any workgroup count; a destination that is not pinned host memory is refused, and the
-    refusal leaves no error behind for the next call."""
+    pieces and a tail) and any workgroup count; a destination that is not pinned host memory, or a source that is
+    not device memory, is refused, and the refusal leaves no error behind for the next call."""
     from chessfly import _hip
     lib = _hip.load()
     src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=DEV)
@@ -557,6 +557,11 @@ def test_evaluator_download_copies_to_pinned_host_memory(nbytes):
     addr = plain.ctypes.data + (-plain.ctypes.data) % 16
     assert lib.fly_evaluator_download(src.data_ptr(), addr, nbytes, 0, st) != 0
     assert b"pinned host memory" in lib.fly_last_error()
+    pinned_src = src.cpu().pin_memory()
+    dst = torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True)
+    assert lib.fly_evaluator_download(pinned_src.data_ptr(), dst.data_ptr(), nbytes, 0, st) != 0
+    assert b"source must be device memory" in lib.fly_last_error()
+    assert lib.fly_evaluator_download(addr, dst.data_ptr(), nbytes, 0, st) != 0
     dst = torch.zeros(nbytes, dtype=torch.uint8, pin_memory=True)
     _hip.check(lib.fly_evaluator_download(src.data_ptr(), dst.data_ptr(), nbytes, 0, st), "fly_evaluator_download")
     torch.cuda.synchronize()
