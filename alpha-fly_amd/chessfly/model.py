@@ -213,6 +213,7 @@ class _Submitted:
 
     def __init__(self, device_outputs, compute, down, workgroups: int, on_done=None):
         self._on_done = on_done
+        self._down, self.done = down, None
         down.wait_stream(compute)
         self.host = [torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for t in device_outputs]
         lib = _hip.load()
@@ -233,7 +234,10 @@ class _Submitted:
         # torch's pinned-block cache does not see the download kernel's writes: a batch dropped unread keeps its
         # host buffers until the kernel is done, so no later batch is handed a block still being written
         try:
-            self.done.synchronize()
+            if self.done is not None:
+                self.done.synchronize()
+            else:                       # a download failed to queue: wait for any that were queued before it
+                self._down.synchronize()
         except Exception:
             pass
         self._finish()
