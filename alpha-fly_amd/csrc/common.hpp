@@ -172,6 +172,8 @@ struct Tuning {
   int gemm_tile = 0;    // dense-map workgroup tile: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, 10 TM + TN, 0 = auto
   int step_lds = 0;     // bytes of LDS each state-step workgroup reserves (caps waves per SIMD), 0 = none
   int download_blocks = 0;  // workgroups of fly_evaluator_download when the call passes 0, 0 = automatic
+  int swept = 0;        // long-row steps of half states as a banded sweep: 0 automatic, -1 never
+  int sweep_bands = 0;  // source bands of a swept step (3 or 4), read when a plan is created; 0 = automatic
 };
 Tuning &tuning();
 
@@ -201,6 +203,10 @@ struct fly_plan {
   std::vector<fly::DevArray<int32_t>> rowptr;
   std::vector<fly::DevArray<int2>> colval;  // {local column, float bits of the weight}
   std::vector<fly::DevArray<fly::RowParam>> params;
+  // Long-row steps run as a banded sweep: per row of A_t, where each of the sweep_bands bands of source rows begins
+  // among its non-zeros (|R_t|, sweep_bands + 1); empty for the other steps.
+  std::vector<fly::DevArray<int32_t>> band_off;
+  int32_t sweep_bands = 4;
   fly::DevArray<int32_t> out_src;  // position of out_idx[j] in R_T or -1
   fly::DevArray<float> cbase;      // value added to the carried state at the outputs
   fly::DevArray<float> c_out;      // c_T[out_idx]

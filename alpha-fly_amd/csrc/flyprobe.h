@@ -21,14 +21,21 @@ const char *flyprobe_last_error(void);
  * the state step streams. */
 int flyprobe_pack(const int32_t *col_dev, const float *val_dev, int64_t nnz, void *pairs_dev, void *stream);
 
+/* Per row of a step matrix (rowptr nrows+1, pairs), where each of `bands` (3 or 4) bands of source rows begins
+ * among its non-zeros: band_off (nrows, bands + 1) int32, as the evaluator builds it for the steps it runs as a
+ * banded sweep. */
+int flyprobe_band_table(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t prev_rows,
+                        int32_t bands, int32_t *band_off_dev, void *stream);
+
 /* The replay of one state step's gather stream: the state step's own kernel (same launch shape, wave order,
  * pair loads and gathers, chosen by the same rule from nrows, nnz and the layout) with the FMAs replaced by an
  * XOR fold and no row constants, input, carried state, cross-lane sums or stores.  rowptr (nrows+1) and pairs
  * (nnz records) are A_t; xprev (prev_rows, ldx) the previous state, __half if state_f16 else float; batch
- * columns.  sink: at least 1 KiB, written only if the folded bits hit one value. */
+ * columns.  band_off (from flyprobe_band_table, or NULL) and bands: where the evaluator runs the step as a banded
+ * sweep, its replay is the swept kernel's.  sink: at least 1 KiB, written only if the folded bits hit one value. */
 int flyprobe_replay_step(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
                          const void *xprev_dev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                         void *sink_dev, void *stream);
+                         const int32_t *band_off_dev, int32_t bands, void *sink_dev, void *stream);
 
 /* params (nrows 32-byte row records) with zero constants and the given prev (position in R_{t-1}, -1: not carried)
  * and usrc (input row, -1: none), as fly_cone_step exports them: the row reads of a replay with I/O. */
@@ -41,7 +48,7 @@ int flyprobe_pack_params(const int32_t *prev_dev, const int32_t *usrc_dev, int64
 int flyprobe_replay_step_io(const int32_t *rowptr_dev, const void *pairs_dev, const void *params_dev, int64_t nrows,
                             int64_t nnz, const void *xprev_dev, int64_t prev_rows, int64_t ldx, const float *u_dev,
                             int64_t n_in, int64_t ldu, void *xout_dev, int64_t batch, int32_t state_f16,
-                            void *stream);
+                            const int32_t *band_off_dev, int32_t bands, void *stream);
 
 /* Uniform-random row gathers in the state step's lane layout: n reads of read_bytes (128: 8 rows per wave
  * instruction; 64: 16 rows) at byte offset idx[e] * row_bytes (16 bytes per lane) of base (`bytes` long).

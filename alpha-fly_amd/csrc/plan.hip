@@ -5,6 +5,7 @@
 //   float32 mode        k_t = k_full_t[R_t] - A_t c_{t-1}[R_{t-1}], p_default = c_{t-1}[R_t]      (brain.py:238-252, 303-304)
 //   sub-matrices        {local column, float32 weight} pairs in W's edge order
 #include "common.hpp"
+#include "step_kernels.hpp"
 
 #include <memory>
 
@@ -14,13 +15,6 @@ void validate_graph(int64_t n, int64_t n_edges, const int32_t *crow, const int32
 namespace {
 
 constexpr int kThreads = 256;
-
-// torch.lerp(start, end, weight) in its CPU vector form: weight < 0.5 in magnitude interpolates from the
-// start, otherwise from the end, as one fused multiply-add.
-__device__ __forceinline__ float lerp_torch(float start, float end, float weight) {
-  const bool small = fabsf(weight) < 0.5f;
-  return fmaf(small ? weight : weight - 1.0f, end - start, small ? start : end);
-}
 
 __device__ __forceinline__ float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
 
@@ -195,6 +189,8 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
     plan->rowptr.resize(T + 1);
     plan->colval.resize(T + 1);
     plan->params.resize(T + 1);
+    plan->band_off.resize(T + 1);
+    plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
 
     DevArray<float> alpha(n), k_full(n), c_a(n), c_b(n);
     hipLaunchKernelGGL(k_sigmoid, dim3(nb), dim3(kThreads), 0, st, alpha_logit, n, alpha.p);
@@ -212,6 +208,11 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
         if (cone->nnz[t])
           hipLaunchKernelGGL(k_pack, dim3(blocks_for(cone->nnz[t], kThreads)), dim3(kThreads), 0, st, cone->col[t].p,
                              cone->edge[t].p, w, cone->nnz[t], plan->colval[t].p);
+        if (sweep_eligible(cone->rows_n[t - 1], nr, cone->nnz[t])) {
+          plan->band_off[t].alloc((size_t)nr * (plan->sweep_bands + 1));
+          hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
+                             plan->colval[t].p, nr, cone->rows_n[t - 1], plan->sweep_bands, plan->band_off[t].p);
+        }
       }
       if (nr) {
         if (mode == FLY_MODE_DEVIATION_F16)

@@ -2,7 +2,8 @@
 //
 // flyprobe_replay_step runs the state step's own kernels (step_kernels.hpp) built with REPLAY = 1: the same
 // launch shape, wave numbering, per-row pair records and buffer-offset gathers as the evaluator's step on the
-// same matrix and state layout, without the arithmetic, the row inputs or the stores.  Its time is what the
+// same matrix and state layout (the banded sweep where the evaluator sweeps, given the band table that
+// flyprobe_band_table builds), without the arithmetic, the row inputs or the stores.  Its time is what the
 // step's gather stream alone costs, which is the ceiling the fused step is measured against.
 // flyprobe_replay_step_io (REPLAY = 2) adds the step's row reads (carried state, input drive, constants) and its
 // stores: everything but the arithmetic of the sum.
@@ -47,11 +48,21 @@ __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__res
   if (q < nnz) out[q] = make_int2(col[q], __float_as_int(val[q]));
 }
 
-// The evaluator's default shapes only (no tuning knobs): lane groups of 16-byte lanes, or row slots of 16- or
-// 32-byte lanes, in groups of 8 lanes with 4 rounds in flight.
+// The evaluator's default shapes only (no tuning knobs): the banded sweep where the evaluator runs one (a band
+// table given and the step eligible), else lane groups of 16-byte lanes, or row slots of 16- or 32-byte lanes, in
+// groups of 8 lanes with 4 rounds in flight.
 template <int MODE, typename S, typename U>
-void replay(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
-  const StepShape sh = shape_step(a, avg_nnz, Tuning{});
+void replay(StepArgs<S, U> a, int64_t nnz, int64_t prev_rows, hipStream_t st) {
+  const StepShape sh = shape_step(a, (double)nnz / (double)a.nrows, Tuning{});
+  if constexpr (sizeof(S) == 2) {
+    if (a.band_off && sweep_eligible(prev_rows, a.nrows, nnz) && sh.v == 8 && sh.groups == 8 && !sh.rows_mode &&
+        a.xbytes) {
+      launch_swept<S, U, MODE>(a, st);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) throw Error{1, std::string("replay launch: ") + hipGetErrorString(e)};
+      return;
+    }
+  }
   const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "replay grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
@@ -116,10 +127,24 @@ extern "C" int flyprobe_pack(const int32_t *col, const float *val, int64_t nnz, 
   });
 }
 
+extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t prev_rows,
+                                   int32_t bands, int32_t *band_off, void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(rowptr && pairs && band_off, "null argument");
+    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0, "size out of range");
+    FLY_REQUIRE(bands == 3 || bands == 4, "bands must be 3 or 4");
+    hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
+                       static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error{1, std::string("band table launch: ") + hipGetErrorString(e)};
+  });
+}
+
 extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
                                     const void *xprev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                                    void *sink, void *stream) {
+                                    const int32_t *band_off, int32_t bands, void *sink, void *stream) {
   return probe_guard([&] {
+    FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
     FLY_REQUIRE(rowptr && pairs && xprev && sink, "null argument");
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
@@ -137,7 +162,9 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       a.nrows = (int32_t)nrows;
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
-      replay<1>(a, (double)nnz / (double)nrows, as_stream(stream));
+      a.band_off = band_off;
+      a.sweep_bands = bands;
+      replay<1>(a, nnz, prev_rows, as_stream(stream));
     };
     if (state_f16)
       run(_Float16(0));
@@ -162,8 +189,9 @@ extern "C" int flyprobe_pack_params(const int32_t *prev, const int32_t *usrc, in
 extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs, const void *params, int64_t nrows,
                                        int64_t nnz, const void *xprev, int64_t prev_rows, int64_t ldx, const float *u,
                                        int64_t n_in, int64_t ldu, void *xout, int64_t batch, int32_t state_f16,
-                                       void *stream) {
+                                       const int32_t *band_off, int32_t bands, void *stream) {
   return probe_guard([&] {
+    FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
     FLY_REQUIRE(rowptr && pairs && params && xprev && xout, "null argument");
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
@@ -184,7 +212,9 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       a.nrows = (int32_t)nrows;
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
-      replay<2>(a, (double)nnz / (double)nrows, as_stream(stream));
+      a.band_off = band_off;
+      a.sweep_bands = bands;
+      replay<2>(a, nnz, prev_rows, as_stream(stream));
     };
     if (state_f16)
       run(_Float16(0));

@@ -71,6 +71,16 @@ void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   const StepShape sh = shape_step(a, avg_nnz, tuning());
   const int v = sh.v, groups = sh.groups, unroll = sh.unroll;
   const bool rows_mode = sh.rows_mode;
+  // long-row steps of half states with a band table: the banded sweep, on the grouped kernel's lane layout
+  if constexpr (sizeof(S) == 2) {
+    if (a.band_off && tuning().swept >= 0 && v == 8 && groups == 8 && !rows_mode && a.rowptr && a.xprev &&
+        a.xbytes) {
+      LaunchTimer timer(FLY_K_STATE_STEP, st);
+      launch_swept<S, U, 0>(a, st);
+      check_launch("swept state step");
+      return;
+    }
+  }
   switch (v) {
     // only 16-byte lanes (V = 16 / sizeof(S)) have grouped and row-slot kernels, and 32-byte lanes of half
     // states a row-slot kernel; pick_shape sets groups to 1 for every other V, so rows_mode is false there too
@@ -245,6 +255,10 @@ const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t b
     a.nrows = (int32_t)nr;
     a.batch = (int32_t)batch;
     a.xbytes = prev ? buffer_bytes(plan.rows_n[t - 1], lds, sizeof(S)) : 0;
+    if ((size_t)t < plan.band_off.size()) {
+      a.band_off = plan.band_off[t].p;
+      a.sweep_bands = plan.sweep_bands;
+    }
     state_step(a, nr ? (double)plan.nnz[t] / (double)nr : 0.0, st);
     prev = buf[cur];
     cur ^= 1;
@@ -518,6 +532,8 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "spmm_groups") tuning().spmm_groups = (int)value;
     else if (k == "gemm_tile") tuning().gemm_tile = (int)value;
     else if (k == "download_blocks") tuning().download_blocks = (int)value;
+    else if (k == "swept") tuning().swept = (int)value;
+    else if (k == "sweep_bands") tuning().sweep_bands = (int)value;
     else if (k == "step_lds") tuning().step_lds = (int)std::min<int64_t>(std::max<int64_t>(value, 0), 65536);
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });

@@ -260,9 +260,11 @@ def _probe_lib():
     p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     lib.flyprobe_last_error.restype, lib.flyprobe_last_error.argtypes = ctypes.c_char_p, []
     for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
-                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p]),
+                       ("flyprobe_band_table", [p, p, i64, i64, i32, p, p]),
+                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, i32, p, p]),
                        ("flyprobe_pack_params", [p, p, i64, p, p]),
-                       ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p]),
+                       ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, i32,
+                                                    p]),
                        ("flyprobe_random_gather", [p, i64, i64, i64, p, i64, p, p])):
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = i32, args
@@ -297,7 +299,8 @@ def _events_ms(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps: int = 20) -> list[dict]:
+def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps: int = 20,
+                   sweep_bands: int = 4) -> list[dict]:
     """Per step with a matrix, the time of the replay of that step's gather stream (flyprobe_replay_step: the
     state step's own kernel, launch shape and wave order over this plan's A_t and a state of this layout, with
     the arithmetic, row inputs and stores taken out), and of the replay that keeps the row reads and stores
@@ -325,11 +328,17 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
                      "flyprobe_pack")
         del col, val
         xprev = (torch.randn(prev_rows, ld, device=dev) * 0.01).to(dtype)
+        # the band table of the evaluator's banded sweep; the probe replays the sweep where the evaluator runs one
+        bands = sweep_bands
+        band_off = torch.empty(nr * (bands + 1), dtype=torch.int32, device=dev)
+        _probe_check(probe, probe.flyprobe_band_table(rowptr.data_ptr(), pairs.data_ptr(), nr, prev_rows, bands,
+                                                      band_off.data_ptr(), st), "flyprobe_band_table")
 
         def once():
             _probe_check(probe, probe.flyprobe_replay_step(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz,
                                                            xprev.data_ptr(), prev_rows, ld, batch, int(state_f16),
-                                                           sink.data_ptr(), st), "flyprobe_replay_step")
+                                                           band_off.data_ptr(), bands, sink.data_ptr(), st),
+                         "flyprobe_replay_step")
         row = {"t": t, "rows": nr, "nnz": nnz, "replay_ms": round(_events_ms(once, reps), 4)}
         # with the row I/O: each row's constants, carried state and input drive (float32, as the model forward's
         # encoder writes it) read, and the new state written
@@ -347,10 +356,11 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
             _probe_check(probe, probe.flyprobe_replay_step_io(rowptr.data_ptr(), pairs.data_ptr(), params.data_ptr(),
                                                               nr, nnz, xprev.data_ptr(), prev_rows, ld, u.data_ptr(),
                                                               n_in, ldu, xout.data_ptr(), batch, int(state_f16),
-                                                              st), "flyprobe_replay_step_io")
+                                                              band_off.data_ptr(), bands, st),
+                         "flyprobe_replay_step_io")
         row["replay_io_ms"] = round(_events_ms(once_io, reps), 4)
         out.append(row)
-        del rowptr, pairs, xprev, prev32, usrc32, params, u, xout
+        del rowptr, pairs, xprev, prev32, usrc32, params, u, xout, band_off
     return out
 
 
@@ -584,7 +594,9 @@ def main() -> int:
     if not args.no_replay and per_step:
         # the ceiling: each step's own gather stream replayed alone (same kernel, shape and order, no arithmetic)
         plan = brain._cone_plan(cone, mode)
-        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev)
+        tuned = dict(kv.split("=") for kv in args.tune)
+        bands = 3 if tuned.get("sweep_bands") == "3" else 4      # the plan's band count (sweep_bands tuning)
+        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev, sweep_bands=bands)
         for r in rows:
             r["step_ms"] = round(per_step[r["t"]], 4)
             r["replay_over_step"] = round(r["replay_ms"] / r["step_ms"], 4)

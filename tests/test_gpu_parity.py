@@ -459,6 +459,42 @@ def test_full_scale_blocked_columns_match_unblocked(full_net):
         torch.testing.assert_close(h[:, -24:], rnn(tail, 4), rtol=0, atol=2e-5)
 
 
+def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
+    """The long-row float16 steps (166,539-166,700 and 77,286 rows of ~63 non-zeros over 166K sources) run as a
+    banded sweep of the sources (k_state_step_swept, 4 bands, or 3 from the sweep_bands tuning); with the sweep off
+    (tuning swept=-1) they run on the grouped kernel.  Same sums in another order: the logits agree within 5e-4
+    and the argmax on >= 99.9% of 1120 boards."""
+    from chessfly import _hip
+    from chessfly.synthetic import synthetic_boards
+    net, _ = full_net
+    x = torch.as_tensor(synthetic_boards(1120, seed=23), device=DEV)
+
+    def run():
+        with torch.no_grad():
+            net.brain.bias.add_(0.0)            # a new parameter version: the next forward builds a new plan
+            out = net(x)
+        torch.cuda.synchronize()
+        return out
+
+    try:
+        base = run()
+        _hip.set_tuning("swept", -1)
+        grouped = run()
+        _hip.set_tuning("swept", 0)
+        _hip.set_tuning("sweep_bands", 3)
+        three = run()
+        for label, (lg, wd) in (("4 bands", base), ("3 bands", three)):
+            dl = float((lg - grouped[0]).abs().max())
+            dw = float((wd - grouped[1]).abs().max())
+            agree = float((lg.argmax(1) == grouped[0].argmax(1)).float().mean())
+            print(f"swept ({label}) vs grouped: logits {dl:.3e}, wdl {dw:.3e}, argmax {agree:.4%}", flush=True)
+            assert dl < 5e-4 and dw < 5e-4 and agree >= 0.999, (label, dl, dw, agree)
+        assert not torch.equal(base[0], grouped[0])     # the sweep did run
+    finally:
+        _hip.set_tuning("swept", 0)
+        _hip.set_tuning("sweep_bands", 0)
+
+
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
     """The bench configuration: B = 1120 boards, float16 deviation vs float32 on the device."""
     from chessfly.synthetic import synthetic_boards
