@@ -277,6 +277,13 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
     plan->params[0].alloc(n);
     hipLaunchKernelGGL(k_params_full, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, alpha.p, h_max, n,
                        plan->params[0].p);
+    plan->band_off.resize(1);
+    plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
+    if (sweep_eligible(n, n, n_edges)) {
+      plan->band_off[0].alloc((size_t)n * (plan->sweep_bands + 1));
+      hipLaunchKernelGGL(k_band_off, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
+                         plan->colval[0].p, n, n, plan->sweep_bands, plan->band_off[0].p);
+    }
     check_launch("full plan");
     FLY_HIP(hipStreamSynchronize(st));
     *out = plan.release();

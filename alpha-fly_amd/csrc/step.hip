@@ -71,15 +71,13 @@ void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
   const StepShape sh = shape_step(a, avg_nnz, tuning());
   const int v = sh.v, groups = sh.groups, unroll = sh.unroll;
   const bool rows_mode = sh.rows_mode;
-  // long-row steps of half states with a band table: the banded sweep, on the grouped kernel's lane layout
-  if constexpr (sizeof(S) == 2) {
-    if (a.band_off && tuning().swept >= 0 && v == 8 && groups == 8 && !rows_mode && a.rowptr && a.xprev &&
-        a.xbytes) {
-      LaunchTimer timer(FLY_K_STATE_STEP, st);
-      launch_swept<S, U, 0>(a, st);
-      check_launch("swept state step");
-      return;
-    }
+  // long-row steps with a band table: the banded sweep, on the grouped kernel's lane layout
+  if (a.band_off && tuning().swept >= 0 && v == 16 / (int)sizeof(S) && groups == 8 && !rows_mode && a.rowptr &&
+      a.xprev && a.xbytes && !(a.out_exact && a.batch % v)) {
+    LaunchTimer timer(FLY_K_STATE_STEP, st);
+    launch_swept<S, U, 0>(a, st);
+    check_launch("swept state step");
+    return;
   }
   switch (v) {
     // only 16-byte lanes (V = 16 / sizeof(S)) have grouped and row-slot kernels, and 32-byte lanes of half
@@ -421,6 +419,10 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
         a.nrows = (int32_t)n;
         a.batch = (int32_t)nb;
         a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
+        if (!plan->band_off.empty()) {
+          a.band_off = plan->band_off[0].p;
+          a.sweep_bands = plan->sweep_bands;
+        }
         state_step(a, (double)plan->nnz[0] / (double)n, st);
         prev = buf[cur];
         cur ^= 1;
