@@ -21,18 +21,18 @@ const char *flyprobe_last_error(void);
  * the state step streams. */
 int flyprobe_pack(const int32_t *col_dev, const float *val_dev, int64_t nnz, void *pairs_dev, void *stream);
 
-/* Per row of a step matrix (rowptr nrows+1, pairs), where each of `bands` (3 or 4) bands of source rows begins
+/* Per row of a step matrix (rowptr nrows+1, pairs nnz), where each of `bands` (3 or 4) bands of source rows begins
  * among its non-zeros: band_off (nrows, bands + 1) int32, as the evaluator builds it for the steps it runs as a
- * banded sweep. */
-int flyprobe_band_table(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t prev_rows,
-                        int32_t bands, int32_t *band_off_dev, void *stream);
+ * banded sweep; *swept (host) = 1 where the evaluator would sweep this matrix, by the same rule.  Synchronises. */
+int flyprobe_band_table(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
+                        int64_t prev_rows, int32_t bands, int32_t *band_off_dev, int32_t *swept, void *stream);
 
 /* The replay of one state step's gather stream: the state step's own kernel (same launch shape, wave order,
  * pair loads and gathers, chosen by the same rule from nrows, nnz and the layout) with the FMAs replaced by an
  * XOR fold and no row constants, input, carried state, cross-lane sums or stores.  rowptr (nrows+1) and pairs
  * (nnz records) are A_t; xprev (prev_rows, ldx) the previous state, __half if state_f16 else float; batch
- * columns.  band_off (from flyprobe_band_table, or NULL) and bands: where the evaluator runs the step as a banded
- * sweep, its replay is the swept kernel's.  sink: at least 1 KiB, written only if the folded bits hit one value. */
+ * columns.  band_off (from flyprobe_band_table where it reports a sweep, else NULL) and bands: the replay of a
+ * swept step is the swept kernel's.  sink: at least 1 KiB, written only if the folded bits hit one value. */
 int flyprobe_replay_step(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
                          const void *xprev_dev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
                          const int32_t *band_off_dev, int32_t bands, void *sink_dev, void *stream);

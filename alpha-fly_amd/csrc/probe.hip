@@ -48,20 +48,18 @@ __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__res
   if (q < nnz) out[q] = make_int2(col[q], __float_as_int(val[q]));
 }
 
-// The evaluator's default shapes only (no tuning knobs): the banded sweep where the evaluator runs one (a band
-// table given and the step eligible), else lane groups of 16-byte lanes, or row slots of 16- or 32-byte lanes, in
-// groups of 8 lanes with 4 rounds in flight.
+// The evaluator's default shapes only (no tuning knobs): the banded sweep where the evaluator runs one (the caller
+// passes the band table of flyprobe_band_table then), else lane groups of 16-byte lanes, or row slots of 16- or
+// 32-byte lanes, in groups of 8 lanes with 4 rounds in flight.
 template <int MODE, typename S, typename U>
 void replay(StepArgs<S, U> a, int64_t nnz, int64_t prev_rows, hipStream_t st) {
   const StepShape sh = shape_step(a, (double)nnz / (double)a.nrows, Tuning{});
-  if constexpr (sizeof(S) == 2) {
-    if (a.band_off && sweep_eligible(prev_rows, a.nrows, nnz) && sh.v == 8 && sh.groups == 8 && !sh.rows_mode &&
-        a.xbytes) {
-      launch_swept<S, U, MODE>(a, st);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) throw Error{1, std::string("replay launch: ") + hipGetErrorString(e)};
-      return;
-    }
+  (void)prev_rows;
+  if (a.band_off && sh.v == 16 / (int)sizeof(S) && sh.groups == 8 && !sh.rows_mode && a.xbytes) {
+    launch_swept<S, U, MODE>(a, st);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error{1, std::string("replay launch: ") + hipGetErrorString(e)};
+    return;
   }
   const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "replay grid too large");
@@ -127,12 +125,14 @@ extern "C" int flyprobe_pack(const int32_t *col, const float *val, int64_t nnz, 
   });
 }
 
-extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t prev_rows,
-                                   int32_t bands, int32_t *band_off, void *stream) {
+extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
+                                   int64_t prev_rows, int32_t bands, int32_t *band_off, int32_t *swept,
+                                   void *stream) {
   return probe_guard([&] {
-    FLY_REQUIRE(rowptr && pairs && band_off, "null argument");
-    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0, "size out of range");
+    FLY_REQUIRE(rowptr && pairs && band_off && swept, "null argument");
+    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0 && nnz >= 0, "size out of range");
     FLY_REQUIRE(bands == 3 || bands == 4, "bands must be 3 or 4");
+    *swept = sweep_suits(rowptr, prev_rows, nrows, nnz, as_stream(stream)) ? 1 : 0;
     hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
                        static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
     const hipError_t e = hipGetLastError();

@@ -596,7 +596,34 @@ __global__ void k_band_off(const int32_t *__restrict__ rowptr, const int2 *__res
   off[i * (K + 1) + K] = end;
 }
 
+__global__ void k_zero_int(int32_t *p) { *p = 0; }
+
+// The longest row of a CSR matrix (rows: nr, into *out, which starts at 0).
+__global__ void k_max_row_length(const int32_t *__restrict__ rowptr, int64_t nr, int32_t *__restrict__ out) {
+  int32_t m = 0;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nr; i += (int64_t)gridDim.x * blockDim.x)
+    m = max(m, rowptr[i + 1] - rowptr[i]);
+  for (int off = 32; off > 0; off >>= 1) m = max(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+
 }  // namespace
+
+// Whether a step's matrix runs as a banded sweep: eligible by size, and no row much longer than the mean.  A slot's
+// rounds run to the longest of its 8 rows and a workgroup's waves wait for each other after every band, so a row
+// far above the mean (a hub of a graph with heavy-tailed in-degrees) would hold its whole workgroup; such a matrix
+// stays on the grouped kernel.  Synchronises the stream (a plan-time decision).
+inline bool sweep_suits(const int32_t *rowptr, int64_t prev_rows, int64_t nr, int64_t nnz, hipStream_t st) {
+  if (!sweep_eligible(prev_rows, nr, nnz)) return false;
+  DevArray<int32_t> mx(1);
+  hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(1), 0, st, mx.p);
+  hipLaunchKernelGGL(k_max_row_length, dim3((unsigned)std::min<int64_t>(blocks_for(nr, 256), 1024)), dim3(256), 0, st,
+                     rowptr, nr, mx.p);
+  int32_t longest = 0;
+  FLY_HIP(hipMemcpyAsync(&longest, mx.p, sizeof(longest), hipMemcpyDeviceToHost, st));
+  FLY_HIP(hipStreamSynchronize(st));
+  return (double)longest <= 4.0 * (double)nnz / (double)nr + 64.0;
+}
 
 // The largest v over all lanes of the wave, as a wave-uniform value (lanes of one group of 8 hold equal values:
 // the DPP rotation and the permlane swaps combine the groups as group_sum does).
