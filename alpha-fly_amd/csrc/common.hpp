@@ -174,6 +174,7 @@ struct Tuning {
   int download_blocks = 0;  // workgroups of fly_evaluator_download when the call passes 0, 0 = automatic
   int swept = 0;        // long-row steps of half states as a banded sweep: 0 automatic, -1 never
   int sweep_bands = 0;  // source bands of a swept step (3 or 4), read when a plan is created; 0 = automatic
+  int sweep_order = 0;  // swept waves take their rows longest first: 0 yes, -1 in index order
 };
 Tuning &tuning();
 
@@ -206,6 +207,7 @@ struct fly_plan {
   // Long-row steps run as a banded sweep: per row of A_t, where each of the sweep_bands bands of source rows begins
   // among its non-zeros (|R_t|, sweep_bands + 1); empty for the other steps.
   std::vector<fly::DevArray<int32_t>> band_off;
+  std::vector<fly::DevArray<int32_t>> sweep_rows;  // the same steps' rows in the order the swept waves take them
   int32_t sweep_bands = 4;
   fly::DevArray<int32_t> out_src;  // position of out_idx[j] in R_T or -1
   fly::DevArray<float> cbase;      // value added to the carried state at the outputs

@@ -7,6 +7,7 @@
 #include "common.hpp"
 #include "step_kernels.hpp"
 
+#include <algorithm>
 #include <memory>
 
 namespace fly {
@@ -140,6 +141,35 @@ __global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *_
   cbase[j] = (mode == FLY_MODE_F32 && out_src[j] >= 0) ? 0.0f : c;
 }
 
+// The order in which the swept kernel's waves take a step's rows: each wave's own `per` consecutive rows, longest
+// first (ties in index order), so the 8 rows of a slot are of like length and its rounds, which run to the longest
+// of them, waste fewer gathers, while every wave keeps the same rows and share of the work.  One thread per wave's
+// segment ranks each of its rows by counting the rows that go before it.
+__global__ void k_sweep_order(const int32_t *__restrict__ rowptr, int64_t nr, int64_t per, int32_t *__restrict__ order) {
+  const int64_t seg = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t b = seg * per;
+  if (b >= nr) return;
+  const int64_t e = min(b + per, nr);
+  for (int64_t i = b; i < e; ++i) {
+    const int32_t li = rowptr[i + 1] - rowptr[i];
+    int64_t rank = 0;
+    for (int64_t j = b; j < e; ++j) {
+      const int32_t lj = rowptr[j + 1] - rowptr[j];
+      rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
+    }
+    order[b + rank] = (int32_t)i;
+  }
+}
+
+void sweep_order(const int32_t *rowptr, int64_t nr, DevArray<int32_t> &order, hipStream_t st) {
+  FLY_REQUIRE(nr > 0 && nr < (int64_t)INT32_MAX, "rows out of range");
+  const int64_t waves = 16 * (int64_t)cu_count();
+  const int64_t per = (nr + waves - 1) / waves;   // launch_swept's rows_per_wave
+  order.alloc((size_t)nr);
+  hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for((nr + per - 1) / per, 64)), dim3(64), 0, st, rowptr, nr, per,
+                     order.p);
+}
+
 }  // namespace
 }  // namespace fly
 
@@ -190,6 +220,7 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
     plan->colval.resize(T + 1);
     plan->params.resize(T + 1);
     plan->band_off.resize(T + 1);
+    plan->sweep_rows.resize(T + 1);
     plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
 
     DevArray<float> alpha(n), k_full(n), c_a(n), c_b(n);
@@ -212,6 +243,7 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
           plan->band_off[t].alloc((size_t)nr * (plan->sweep_bands + 1));
           hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
                              plan->colval[t].p, nr, cone->rows_n[t - 1], plan->sweep_bands, plan->band_off[t].p);
+          sweep_order(plan->rowptr[t].p, nr, plan->sweep_rows[t], st);
         }
       }
       if (nr) {
@@ -278,11 +310,13 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
     hipLaunchKernelGGL(k_params_full, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, alpha.p, h_max, n,
                        plan->params[0].p);
     plan->band_off.resize(1);
+    plan->sweep_rows.resize(1);
     plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
     if (sweep_suits(plan->rowptr[0].p, n, n, n_edges, st)) {
       plan->band_off[0].alloc((size_t)n * (plan->sweep_bands + 1));
       hipLaunchKernelGGL(k_band_off, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
                          plan->colval[0].p, n, n, plan->sweep_bands, plan->band_off[0].p);
+      sweep_order(plan->rowptr[0].p, n, plan->sweep_rows[0], st);
     }
     check_launch("full plan");
     FLY_HIP(hipStreamSynchronize(st));

@@ -255,6 +255,7 @@ const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t b
     a.xbytes = prev ? buffer_bytes(plan.rows_n[t - 1], lds, sizeof(S)) : 0;
     if ((size_t)t < plan.band_off.size()) {
       a.band_off = plan.band_off[t].p;
+      a.sweep_rows = tuning().sweep_order >= 0 ? plan.sweep_rows[t].p : nullptr;
       a.sweep_bands = plan.sweep_bands;
     }
     state_step(a, nr ? (double)plan.nnz[t] / (double)nr : 0.0, st);
@@ -421,6 +422,7 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
         a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
         if (!plan->band_off.empty()) {
           a.band_off = plan->band_off[0].p;
+          a.sweep_rows = tuning().sweep_order >= 0 ? plan->sweep_rows[0].p : nullptr;
           a.sweep_bands = plan->sweep_bands;
         }
         state_step(a, (double)plan->nnz[0] / (double)n, st);
@@ -536,6 +538,7 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "download_blocks") tuning().download_blocks = (int)value;
     else if (k == "swept") tuning().swept = (int)value;
     else if (k == "sweep_bands") tuning().sweep_bands = (int)value;
+    else if (k == "sweep_order") tuning().sweep_order = (int)value;
     else if (k == "step_lds") tuning().step_lds = (int)std::min<int64_t>(std::max<int64_t>(value, 0), 65536);
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });

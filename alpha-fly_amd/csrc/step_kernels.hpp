@@ -88,7 +88,8 @@ struct StepArgs {
   int32_t nt_store;        // write the new state with non-temporal stores
   uint32_t xbytes;         // bytes of X_{t-1} (rows of X_{t-1} * ldx * sizeof(S)) when below 2^31, else 0
   const int32_t *band_off; // swept steps: (nrows, bands + 1) band boundaries in colval, or null
-  int32_t rows_per_wave;   // swept steps: consecutive rows each wave owns (set by launch_swept)
+  const int32_t *sweep_rows; // swept steps: the rows in the order the waves take them, or null (index order)
+  int32_t rows_per_wave;   // swept steps: consecutive positions of that order each wave owns (set by launch_swept)
   int32_t sweep_bands;     // swept steps: bands of band_off (3 or 4)
 };
 
@@ -635,8 +636,10 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 }
 
 // A long-row step as a sweep of the source rows in K bands, with each row's sums held in registers across it.
-// One workgroup of 16 waves per CU, all resident at once: wave w owns rows_per_wave consecutive rows (slot j of
-// lane group g: row w * rows_per_wave + 8 j + g, in passes of 8 * SLOTS) for every chunk of columns.  For each
+// One workgroup of 16 waves per CU, all resident at once: wave w owns rows_per_wave consecutive positions of the
+// sweep order (slot j of lane group g: position w * rows_per_wave + 8 j + g, in passes of 8 * SLOTS) for every
+// chunk of columns.  The order (sweep_rows) sorts each wave's own rows longest first, so a slot's 8 rows are of like
+// length while every wave keeps the same share of the work.  For each
 // chunk a wave gathers band 0 of all its rows, then band 1, and so on, and the workgroup's waves meet at a barrier
 // after each band: the CU's waves then draw from one band of the source rows at a time, so one XCD's L2 holds the
 // lines of one band instead of the whole chunk.  (Without the barrier, issue priority lets the oldest waves run
@@ -656,13 +659,15 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
   const int chunks = (a.batch + 8 * V - 1) / (8 * V);
   const int R = a.rows_per_wave;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
+  // position p of the sweep order holds row sweep_rows[p] (p itself without an order)
+  auto row_at = [&](uint32_t p) { return a.sweep_rows ? (uint32_t)a.sweep_rows[p] : p; };
   for (int k0 = 0; k0 < R; k0 += 8 * SLOTS) {
-    const uint32_t row0 = wave * (uint32_t)R + (uint32_t)(k0 + g);   // slot j: row0 + 8 j
+    const uint32_t pos0 = wave * (uint32_t)R + (uint32_t)(k0 + g);   // slot j: position pos0 + 8 j
     int off[SLOTS];   // lane s <= K: band_off[row][s]
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
-      const bool has = k0 + j * 8 + g < R && row0 + 8u * j < (uint32_t)a.nrows;
-      off[j] = has && s <= K ? a.band_off[(int64_t)(row0 + 8u * j) * (K + 1) + s] : 0;
+      const bool has = k0 + j * 8 + g < R && pos0 + 8u * j < (uint32_t)a.nrows;
+      off[j] = has && s <= K ? a.band_off[(int64_t)row_at(pos0 + 8u * j) * (K + 1) + s] : 0;
     }
     for (int c = 0; c < chunks; ++c) {
       const int64_t col = (int64_t)c * (8 * V) + (int64_t)s * V;
@@ -718,8 +723,9 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
       if constexpr (REPLAY != 1) {
 #pragma unroll
         for (int j = 0; j < SLOTS; ++j) {
-          const uint32_t rj = row0 + 8u * j;
-          if (k0 + j * 8 + g < R && rj < (uint32_t)a.nrows && in_batch) {
+          const uint32_t pj = pos0 + 8u * j;
+          if (k0 + j * 8 + g < R && pj < (uint32_t)a.nrows && in_batch) {
+            const uint32_t rj = row_at(pj);
             if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j], bits);
             RowInputs<S, U, V> in;
             load_row_inputs(a, rj, col, true, in);
