@@ -141,26 +141,7 @@ __global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *_
   cbase[j] = (mode == FLY_MODE_F32 && out_src[j] >= 0) ? 0.0f : c;
 }
 
-// The order in which the swept kernel's waves take a step's rows: each wave's own `per` consecutive rows, longest
-// first (ties in index order), so the 8 rows of a slot are of like length and its rounds, which run to the longest
-// of them, waste fewer gathers, while every wave keeps the same rows and share of the work.  One thread per wave's
-// segment ranks each of its rows by counting the rows that go before it.
-__global__ void k_sweep_order(const int32_t *__restrict__ rowptr, int64_t nr, int64_t per, int32_t *__restrict__ order) {
-  const int64_t seg = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t b = seg * per;
-  if (b >= nr) return;
-  const int64_t e = min(b + per, nr);
-  for (int64_t i = b; i < e; ++i) {
-    const int32_t li = rowptr[i + 1] - rowptr[i];
-    int64_t rank = 0;
-    for (int64_t j = b; j < e; ++j) {
-      const int32_t lj = rowptr[j + 1] - rowptr[j];
-      rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
-    }
-    order[b + rank] = (int32_t)i;
-  }
-}
-
+// The swept waves' order of a step's rows (k_sweep_order: each wave's own rows, longest first).
 void sweep_order(const int32_t *rowptr, int64_t nr, DevArray<int32_t> &order, hipStream_t st) {
   FLY_REQUIRE(nr > 0 && nr < (int64_t)INT32_MAX, "rows out of range");
   const int64_t waves = 16 * (int64_t)cu_count();

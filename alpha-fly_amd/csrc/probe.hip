@@ -126,15 +126,19 @@ extern "C" int flyprobe_pack(const int32_t *col, const float *val, int64_t nnz, 
 }
 
 extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
-                                   int64_t prev_rows, int32_t bands, int32_t *band_off, int32_t *swept,
+                                   int64_t prev_rows, int32_t bands, int32_t *band_off, int32_t *order, int32_t *swept,
                                    void *stream) {
   return probe_guard([&] {
-    FLY_REQUIRE(rowptr && pairs && band_off && swept, "null argument");
+    FLY_REQUIRE(rowptr && pairs && band_off && order && swept, "null argument");
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0 && nnz >= 0, "size out of range");
     FLY_REQUIRE(bands == 3 || bands == 4, "bands must be 3 or 4");
     *swept = sweep_suits(rowptr, prev_rows, nrows, nnz, as_stream(stream)) ? 1 : 0;
     hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
                        static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
+    const int64_t waves = 16 * (int64_t)cu_count();
+    const int64_t per = (nrows + waves - 1) / waves;   // launch_swept's rows_per_wave
+    hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for((nrows + per - 1) / per, 64)), dim3(64), 0, as_stream(stream),
+                       rowptr, nrows, per, order);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) throw Error{1, std::string("band table launch: ") + hipGetErrorString(e)};
   });
@@ -142,7 +146,8 @@ extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int
 
 extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
                                     const void *xprev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                                    const int32_t *band_off, int32_t bands, void *sink, void *stream) {
+                                    const int32_t *band_off, const int32_t *order, int32_t bands, void *sink,
+                                    void *stream) {
   return probe_guard([&] {
     FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
     FLY_REQUIRE(rowptr && pairs && xprev && sink, "null argument");
@@ -163,6 +168,7 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
       a.band_off = band_off;
+      a.sweep_rows = band_off ? order : nullptr;
       a.sweep_bands = bands;
       replay<1>(a, nnz, prev_rows, as_stream(stream));
     };
@@ -189,7 +195,7 @@ extern "C" int flyprobe_pack_params(const int32_t *prev, const int32_t *usrc, in
 extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs, const void *params, int64_t nrows,
                                        int64_t nnz, const void *xprev, int64_t prev_rows, int64_t ldx, const float *u,
                                        int64_t n_in, int64_t ldu, void *xout, int64_t batch, int32_t state_f16,
-                                       const int32_t *band_off, int32_t bands, void *stream) {
+                                       const int32_t *band_off, const int32_t *order, int32_t bands, void *stream) {
   return probe_guard([&] {
     FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
     FLY_REQUIRE(rowptr && pairs && params && xprev && xout, "null argument");
@@ -213,6 +219,7 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
       a.band_off = band_off;
+      a.sweep_rows = band_off ? order : nullptr;
       a.sweep_bands = bands;
       replay<2>(a, nnz, prev_rows, as_stream(stream));
     };

@@ -597,6 +597,26 @@ __global__ void k_band_off(const int32_t *__restrict__ rowptr, const int2 *__res
   off[i * (K + 1) + K] = end;
 }
 
+// The order in which the swept kernel's waves take a step's rows: each wave's own `per` consecutive rows, longest
+// first (ties in index order), so the 8 rows of a slot are of like length and its rounds, which run to the longest
+// of them, waste fewer gathers, while every wave keeps the same rows and share of the work.  One thread per wave's
+// segment ranks each of its rows by counting the rows that go before it.
+__global__ void k_sweep_order(const int32_t *__restrict__ rowptr, int64_t nr, int64_t per, int32_t *__restrict__ order) {
+  const int64_t seg = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t b = seg * per;
+  if (b >= nr) return;
+  const int64_t e = min(b + per, nr);
+  for (int64_t i = b; i < e; ++i) {
+    const int32_t li = rowptr[i + 1] - rowptr[i];
+    int64_t rank = 0;
+    for (int64_t j = b; j < e; ++j) {
+      const int32_t lj = rowptr[j + 1] - rowptr[j];
+      rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
+    }
+    order[b + rank] = (int32_t)i;
+  }
+}
+
 __global__ void k_zero_int(int32_t *p) { *p = 0; }
 
 // The longest row of a CSR matrix (rows: nr, into *out, which starts at 0).

@@ -397,7 +397,10 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, or 10 TM + TN for 32 TM x 32 TN with TM in {2, 3, 4} and TN in
  * {2, 4, 5}; 0 = automatic); "step_lds": bytes of LDS each state-step workgroup reserves, which caps the
  * workgroups a CU runs at once (0 = none); "download_blocks": workgroups of fly_evaluator_download when its call
- * passes 0 (0 = 16).  Every selectable shape computes the same function. */
+ * passes 0 (0 = 16); "swept": -1 keeps the long-row steps on the grouped kernel instead of the banded sweep (0 =
+ * automatic); "sweep_bands": source bands of the sweep, 3 or 4 (0 = 4), read when a plan is created;
+ * "sweep_order": -1 lets the swept waves take their rows in index order instead of longest first (0).  Every
+ * selectable shape computes the same function. */
 int fly_set_tuning(const char *key, int64_t value);
 
 #ifdef __cplusplus
