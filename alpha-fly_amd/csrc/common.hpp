@@ -175,6 +175,7 @@ struct Tuning {
   int swept = 0;        // long-row steps of half states as a banded sweep: 0 automatic, -1 never
   int sweep_bands = 0;  // source bands of a swept step (3 or 4), read when a plan is created; 0 = automatic
   int sweep_order = 0;  // swept waves take their rows longest first: 0 yes, -1 in index order
+  int sweep_paired = 0;  // swept waves walk two rows per pass: 1 always, -1 never, 0 for float32 states
 };
 Tuning &tuning();
 

@@ -91,6 +91,7 @@ struct StepArgs {
   const int32_t *sweep_rows; // swept steps: the rows in the order the waves take them, or null (index order)
   int32_t rows_per_wave;   // swept steps: consecutive positions of that order each wave owns (set by launch_swept)
   int32_t sweep_bands;     // swept steps: bands of band_off (3 or 4)
+  int32_t sweep_paired;    // swept steps: two rows per pass (1), one (-1), by the state type (0)
 };
 
 // Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
@@ -667,7 +668,7 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // colval[band_off[i][b] .. band_off[i][b+1]).  Lane groups of 8 lanes x 16 bytes gather one 128-byte line each; a
 // slot's rounds run to the longest of the wave's 8 rows in that slot and band, the shorter rows' extra gathers at
 // an offset past the buffer (zeros, no memory access).  REPLAY as for the other step kernels.
-template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0>
+template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, bool PAIRED = false>
 __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, U> a) {
   constexpr int UNR = 4;
   static_assert(K + 1 <= 8 && V * sizeof(S) == 16, "band starts in the lanes of a group, 16-byte lanes");
@@ -700,6 +701,59 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
         for (int i = 0; i < V; ++i) acc[j][i] = 0.0f;
       static_for<K>([&](auto B) {
         constexpr int b = decltype(B)::value;
+        if constexpr (PAIRED) {
+          // Two slots' rows per pass: the group walks row A's band-b non-zeros, then row B's, so a pass runs to
+          // the longest pair of the wave's 8 instead of each slot to its longest row; every gathered row feeds the
+          // sums of the row it belongs to (the other row's weight is zero).
+#pragma unroll
+          for (int j = 0; j < SLOTS; j += 2) {
+            const int bA = group_bcast<8, b>(off[j]), eA = group_bcast<8, b + 1>(off[j]);
+            const int bB = group_bcast<8, b>(off[j + 1]), eB = group_bcast<8, b + 1>(off[j + 1]);
+            const int nA = eA - bA, n = nA + (eB - bB);
+            const int rounds = wave_max_of_groups(n);
+            auto block = [&](int q0) {
+              const int q = q0 + s;
+              const int e = q < nA ? bA + q : (q < n ? bB + (q - nA) : (eB > bB ? eB - 1 : eA - 1));
+              return a.colval[max(e, 0)];
+            };
+            int2 rec = rounds > 0 ? block(0) : make_int2(0, 0);
+            for (int q0 = 0; q0 < rounds; q0 += 8) {
+              const int2 nxt = block(q0 + 8);
+              static_for<8 / UNR>([&](auto H) {
+                constexpr int h0 = decltype(H)::value * UNR;
+                if (q0 + h0 < rounds) {
+                  typename Lanes<S, V>::vec xr[UNR];
+                  int wj[UNR];
+                  static_for<UNR>([&](auto J) {
+                    constexpr int u = decltype(J)::value, sl = h0 + u;
+                    const int cc = group_bcast<8, sl>(rec.x);
+                    wj[u] = group_bcast<8, sl>(rec.y);
+                    const uint32_t o = q0 + sl < n ? __umul24((uint32_t)cc, row_bytes) + voff : 0x80000000u;
+                    xr[u] = bload<S, V>(r, (int)o, 0);
+                  });
+                  if constexpr (REPLAY != 0) {
+#pragma unroll
+                    for (int u = 0; u < UNR; ++u) ReplayBits<S, V>::fold(bits, xr[u], wj[u]);
+                  } else {
+#pragma unroll
+                    for (int u = 0; u < UNR; ++u) {
+                      const float wt = __int_as_float(wj[u]);
+                      const bool in_a = q0 + h0 + u < nA;
+                      const float wa = in_a ? wt : 0.0f, wb = in_a ? 0.0f : wt;
+#pragma unroll
+                      for (int i = 0; i < V; ++i) {
+                        const float x = Lanes<S, V>::at(xr[u], i);
+                        acc[j][i] = fmaf(wa, x, acc[j][i]);
+                        acc[j + 1][i] = fmaf(wb, x, acc[j + 1][i]);
+                      }
+                    }
+                  }
+                }
+              });
+              rec = nxt;
+            }
+          }
+        } else {
 #pragma unroll
         for (int j = 0; j < SLOTS; ++j) {
           const int beg = group_bcast<8, b>(off[j]), end = group_bcast<8, b + 1>(off[j]);
@@ -737,6 +791,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
             });
             rec = nxt;
           }
+        }
         }
         __syncthreads();   // the workgroup's waves start the next band together
       });
@@ -776,19 +831,21 @@ inline int cu_count() {
   return n;
 }
 
-template <typename S, typename U, int K, int SLOTS, int REPLAY>
+template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false>
 void launch_swept_shape(const StepArgs<S, U> &a, unsigned grid, hipStream_t st) {
   constexpr int V = 16 / (int)sizeof(S);
   static bool fits = false;
   if (!fits) {   // the kernel's registers allow one 16-wave workgroup on every CU
     int nb = 0;
     FLY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &nb, reinterpret_cast<const void *>(&k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY>), 1024, 0));
+        &nb,
+        reinterpret_cast<const void *>(&k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED>),
+        1024, 0));
     FLY_REQUIRE(nb >= 1, "the swept state step does not fit a CU");
     fits = true;
   }
-  hipLaunchKernelGGL((k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY>), dim3(grid), dim3(1024), 0, st,
-                     a);
+  hipLaunchKernelGGL((k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED>), dim3(grid), dim3(1024),
+                     0, st, a);
 }
 
 // One swept step: one workgroup per CU, the rows split evenly between the waves (one pass of up to 24 or 48 rows
@@ -805,6 +862,10 @@ void launch_swept(StepArgs<S, U> a, hipStream_t st) {
       break;
     case 4:
       if (few) launch_swept_shape<S, U, 4, 3, REPLAY>(a, grid, st);
+      // float32 states walk two rows per pass (measured +1.6% at B = 1120); half states not (-5%: 16 FMAs per
+      // gathered line of 8 halves cost more than the rounds they save)
+      else if (a.sweep_paired > 0 || (a.sweep_paired == 0 && sizeof(S) == 4))
+        launch_swept_shape<S, U, 4, 6, REPLAY, true>(a, grid, st);
       else launch_swept_shape<S, U, 4, 6, REPLAY>(a, grid, st);
       break;
     default:

@@ -460,10 +460,11 @@ def test_full_scale_blocked_columns_match_unblocked(full_net):
 
 
 def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
-    """The long-row float16 steps (166,539-166,700 and 77,286 rows of ~63 non-zeros over 166K sources) run as a
-    banded sweep of the sources (k_state_step_swept, 4 bands, or 3 from the sweep_bands tuning); with the sweep off
-    (tuning swept=-1) they run on the grouped kernel.  Same sums in another order: the logits agree within 5e-4
-    and the argmax on >= 99.9% of 1120 boards."""
+    """The long-row steps (166,539-166,700 and 77,286 rows of ~63 non-zeros over 166K sources) run as a banded sweep
+    of the sources (k_state_step_swept: 4 bands, or 3 from the sweep_bands tuning; one or two rows per pass; rows in
+    index order or longest first); with the sweep off (tuning swept=-1) they run on the grouped kernel.  Same sums
+    in another order: float16 deviation logits agree within 5e-4 and float32 within 2e-5, with the argmax on
+    >= 99.9% of 1120 boards."""
     from chessfly import _hip
     from chessfly.synthetic import synthetic_boards
     net, _ = full_net
@@ -477,22 +478,30 @@ def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
         return out
 
     try:
-        base = run()
-        _hip.set_tuning("swept", -1)
-        grouped = run()
-        _hip.set_tuning("swept", 0)
-        _hip.set_tuning("sweep_bands", 3)
-        three = run()
-        for label, (lg, wd) in (("4 bands", base), ("3 bands", three)):
-            dl = float((lg - grouped[0]).abs().max())
-            dw = float((wd - grouped[1]).abs().max())
-            agree = float((lg.argmax(1) == grouped[0].argmax(1)).float().mean())
-            print(f"swept ({label}) vs grouped: logits {dl:.3e}, wdl {dw:.3e}, argmax {agree:.4%}", flush=True)
-            assert dl < 5e-4 and dw < 5e-4 and agree >= 0.999, (label, dl, dw, agree)
-        assert not torch.equal(base[0], grouped[0])     # the sweep did run
+        for dtype, tol in ((torch.float16, 5e-4), (torch.float32, 2e-5)):
+            net.infer_dtype = dtype
+            _hip.set_tuning("swept", -1)
+            grouped = run()
+            _hip.set_tuning("swept", 0)
+            variants = {}
+            for label, key, value in (("default", "sweep_bands", 0), ("3 bands", "sweep_bands", 3),
+                                      ("index order", "sweep_order", -1), ("two rows per pass", "sweep_paired", 1),
+                                      ("one row per pass", "sweep_paired", -1)):
+                _hip.set_tuning(key, value)
+                variants[label] = run()
+                _hip.set_tuning(key, 0)
+            for label, (lg, wd) in variants.items():
+                dl = float((lg - grouped[0]).abs().max())
+                dw = float((wd - grouped[1]).abs().max())
+                agree = float((lg.argmax(1) == grouped[0].argmax(1)).float().mean())
+                print(f"{dtype} swept ({label}) vs grouped: logits {dl:.3e}, wdl {dw:.3e}, argmax {agree:.4%}",
+                      flush=True)
+                assert dl < tol and dw < tol and agree >= 0.999, (dtype, label, dl, dw, agree)
+            assert not torch.equal(variants["default"][0], grouped[0])     # the sweep did run
     finally:
-        _hip.set_tuning("swept", 0)
-        _hip.set_tuning("sweep_bands", 0)
+        for key in ("swept", "sweep_bands", "sweep_order", "sweep_paired"):
+            _hip.set_tuning(key, 0)
+        net.infer_dtype = torch.float16
 
 
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
