@@ -504,6 +504,64 @@ def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
         net.infer_dtype = torch.float16
 
 
+def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per):
+    """The swept step's plan tables restated: off[i][b] = row i's start plus its non-zeros with a column in the
+    bands before b (band of column c: c * bands // prev_rows), off[i][bands] = its end; the order lists each
+    consecutive segment of `per` rows longest first, ties by row index."""
+    nr = len(rowptr) - 1
+    lens = np.diff(rowptr)
+    band = cols.astype(np.int64) * bands // prev_rows
+    cnt = np.bincount(np.repeat(np.arange(nr), lens) * bands + band, minlength=nr * bands).reshape(nr, bands)
+    off = np.empty((nr, bands + 1), np.int64)
+    off[:, 0] = rowptr[:-1]
+    off[:, 1:bands] = rowptr[:-1, None] + np.cumsum(cnt, axis=1)[:, :bands - 1]
+    off[:, bands] = rowptr[1:]
+    order = np.empty(nr, np.int64)
+    for b in range(0, nr, per):
+        idx = np.arange(b, min(b + per, nr))
+        order[b:b + len(idx)] = idx[np.lexsort((idx, -lens[idx]))]
+    return off, order
+
+
+def test_sweep_band_table_order_and_rule_match_numpy():
+    """The plan-time work of a swept step (k_band_off, k_sweep_order and the suitability rule of sweep_suits, shared
+    by the plan and the probe library's flyprobe_band_table) against a numpy restatement, bit for bit, on random
+    CSR matrices of 70,000 rows: a plain one sweeps; one with a hub row (longer than 4 x the mean + 64) and one over
+    32,768 source rows or fewer do not."""
+    import ctypes
+    probe = ctypes.CDLL(os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so"))
+    probe.flyprobe_last_error.restype = ctypes.c_char_p
+    i64, i32, p_ = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
+    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, p_, p_, ctypes.POINTER(i32), p_]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng(41)
+    nr = 70_000
+    base_lens = rng.poisson(40, nr)
+    cases = [("plain", 40_000, base_lens, 1), ("small source", 32_768, base_lens, 0)]
+    hub = base_lens.copy()
+    hub[12_345] = 4 * int(hub.mean()) + 200
+    cases.append(("hub row", 40_000, hub, 0))
+    for label, prev_rows, lens, want_swept in cases:
+        rowptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        cols = np.concatenate([np.sort(rng.integers(0, prev_rows, n)) for n in lens]).astype(np.int32)
+        pairs = np.stack([cols, rng.standard_normal(len(cols)).astype(np.float32).view(np.int32)], axis=1)
+        d_rowptr = torch.as_tensor(rowptr, device=DEV)
+        d_pairs = torch.as_tensor(np.ascontiguousarray(pairs), device=DEV)
+        for bands in (3, 4):
+            d_off = torch.full((nr, bands + 1), -7, dtype=torch.int32, device=DEV)
+            d_order = torch.full((nr,), -7, dtype=torch.int32, device=DEV)
+            swept = i32(-1)
+            rc = probe.flyprobe_band_table(d_rowptr.data_ptr(), d_pairs.data_ptr(), nr, len(cols), prev_rows, bands,
+                                           d_off.data_ptr(), d_order.data_ptr(), ctypes.byref(swept), None)
+            assert rc == 0, probe.flyprobe_last_error()
+            torch.cuda.synchronize()
+            off, order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, -(-nr // (16 * cus)))
+            print(f"{label}, {bands} bands: swept {swept.value}", flush=True)
+            assert swept.value == want_swept, (label, bands, swept.value)
+            assert np.array_equal(d_off.cpu().numpy(), off), (label, bands)
+            assert np.array_equal(d_order.cpu().numpy(), order), (label, bands)
+
+
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
     """The bench configuration: B = 1120 boards, float16 deviation vs float32 on the device."""
     from chessfly.synthetic import synthetic_boards
