@@ -90,6 +90,8 @@ struct StepArgs {
   const int32_t *band_off; // swept steps: (nrows, bands + 1) band boundaries in colval, or null
   const int32_t *sweep_rows; // swept steps: the rows in the order the waves take them, or null (index order)
   int32_t rows_per_wave;   // swept steps: consecutive positions of that order each wave owns (set by launch_swept)
+  int32_t sweep_positions; // swept steps: positions of sweep_rows per wave when the order is laid out per wave
+                           // (-1 entries: no row), or 0: the rows split evenly between the waves
   int32_t sweep_bands;     // swept steps: bands of band_off (3 or 4)
   int32_t sweep_paired;    // swept steps: two rows per pass (1), one (-1), by the state type (0)
 };
@@ -647,6 +649,18 @@ inline bool sweep_suits(const int32_t *rowptr, int64_t prev_rows, int64_t nr, in
   return (double)longest <= 4.0 * (double)nnz / (double)nr + 64.0;
 }
 
+// The sum over each aligned block of 2^lf lane groups of 8 lanes (lf = 0..3, wave-uniform), in every lane of the
+// block: the first lf levels of group_sum's butterfly.
+__device__ __forceinline__ float groups_sum(float v, int lf) {
+  if (lf >= 1)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
+  if (lf >= 2)
+    v += __int_as_float(__builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
+  if (lf >= 3)
+    v += __int_as_float(__builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false)[1]);
+  return v;
+}
+
 // The largest v over all lanes of the wave, as a wave-uniform value (lanes of one group of 8 hold equal values:
 // the DPP rotation and the permlane swaps combine the groups as group_sum does).
 __device__ __forceinline__ int wave_max_of_groups(int v) {
@@ -679,16 +693,34 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
   const int chunks = (a.batch + 8 * V - 1) / (8 * V);
   const int R = a.rows_per_wave;
+  // positions of the order: R per wave when it is laid out per wave, else one per row
+  const uint32_t npos = a.sweep_positions > 0 ? (uint32_t)R * 16u * gridDim.x : (uint32_t)a.nrows;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  // position p of the sweep order holds row sweep_rows[p] (p itself without an order)
-  auto row_at = [&](uint32_t p) { return a.sweep_rows ? (uint32_t)a.sweep_rows[p] : p; };
+  // position p of the sweep order holds row sweep_rows[p] (-1: none; p itself without an order)
+  auto row_at = [&](uint32_t p) {
+    const int32_t r = a.sweep_rows ? a.sweep_rows[p] : (int32_t)p;
+    return r < a.nrows ? r : -1;
+  };
   for (int k0 = 0; k0 < R; k0 += 8 * SLOTS) {
-    const uint32_t pos0 = wave * (uint32_t)R + (uint32_t)(k0 + g);   // slot j: position pos0 + 8 j
+    const uint32_t base = wave * (uint32_t)R + (uint32_t)k0;   // slot j, row i of the slot: position base + 8 j + i
+    // Rows of slot j: a prefix of its 8 positions.  A slot of 4 rows or fewer (the last of an even split) spreads
+    // each row's records over 2^lf[j] groups (lane groups g with g >> lf[j] == i take row i, each a share of every
+    // band), and their sums meet before the epilogue: the slot's rounds then run to a share of its longest row
+    // instead of the whole row, with the other groups idle.
+    int nrow[SLOTS], lf[SLOTS];
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      const int64_t left = min((int64_t)R - k0 - 8 * j, (int64_t)npos - (int64_t)base - 8 * j);
+      nrow[j] = (int)max<int64_t>(0, min<int64_t>(8, left));
+      lf[j] = PAIRED || a.sweep_positions > 0 || nrow[j] >= 5 || nrow[j] == 0 ? 0
+              : (nrow[j] >= 3 ? 1 : (nrow[j] == 2 ? 2 : 3));
+    }
     int off[SLOTS];   // lane s <= K: band_off[row][s]
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
-      const bool has = k0 + j * 8 + g < R && pos0 + 8u * j < (uint32_t)a.nrows;
-      off[j] = has && s <= K ? a.band_off[(int64_t)row_at(pos0 + 8u * j) * (K + 1) + s] : 0;
+      const int i = g >> lf[j];
+      const int32_t rj = i < nrow[j] ? row_at(base + 8u * j + (uint32_t)i) : -1;
+      off[j] = rj >= 0 && s <= K ? a.band_off[(int64_t)rj * (K + 1) + s] : 0;
     }
     for (int c = 0; c < chunks; ++c) {
       const int64_t col = (int64_t)c * (8 * V) + (int64_t)s * V;
@@ -756,7 +788,12 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
         } else {
 #pragma unroll
         for (int j = 0; j < SLOTS; ++j) {
-          const int beg = group_bcast<8, b>(off[j]), end = group_bcast<8, b + 1>(off[j]);
+          int beg = group_bcast<8, b>(off[j]), end = group_bcast<8, b + 1>(off[j]);
+          if (lf[j]) {   // this group's share of the row's band
+            const int n = end - beg, p = g & ((1 << lf[j]) - 1), b0 = beg;
+            beg = b0 + ((n * p) >> lf[j]);
+            end = b0 + ((n * (p + 1)) >> lf[j]);
+          }
           const int rounds = wave_max_of_groups(end - beg);
           // lane s brings record q0 + s of its row's band (clamped into the row), and round q reaches the group's
           // lanes by a broadcast of lane q; the next block of 8 loads while this one's gathers are in flight
@@ -798,9 +835,15 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
       if constexpr (REPLAY != 1) {
 #pragma unroll
         for (int j = 0; j < SLOTS; ++j) {
-          const uint32_t pj = pos0 + 8u * j;
-          if (k0 + j * 8 + g < R && pj < (uint32_t)a.nrows && in_batch) {
-            const uint32_t rj = row_at(pj);
+          if (lf[j]) {   // the shares of a spread row meet in each of its groups
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[j][i] = groups_sum(acc[j][i], lf[j]);
+          }
+          const int i = g >> lf[j];
+          const bool first = (g & ((1 << lf[j]) - 1)) == 0;
+          const int32_t rs = first && i < nrow[j] && in_batch ? row_at(base + 8u * j + (uint32_t)i) : -1;
+          if (rs >= 0) {
+            const uint32_t rj = (uint32_t)rs;
             if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j], bits);
             RowInputs<S, U, V> in;
             load_row_inputs(a, rj, col, true, in);
@@ -853,7 +896,10 @@ void launch_swept_shape(const StepArgs<S, U> &a, unsigned grid, hipStream_t st) 
 template <typename S, typename U, int REPLAY>
 void launch_swept(StepArgs<S, U> a, hipStream_t st) {
   const unsigned grid = (unsigned)cu_count();
-  a.rows_per_wave = (int32_t)((a.nrows + 16 * (int64_t)grid - 1) / (16 * (int64_t)grid));
+  FLY_REQUIRE(a.sweep_positions == 0 || (a.sweep_rows && a.sweep_positions > 0),
+              "a per-wave sweep layout needs its order");
+  a.rows_per_wave = a.sweep_positions > 0 ? a.sweep_positions
+                                          : (int32_t)((a.nrows + 16 * (int64_t)grid - 1) / (16 * (int64_t)grid));
   const bool few = a.rows_per_wave <= 24;
   switch (a.sweep_bands) {
     case 3:
