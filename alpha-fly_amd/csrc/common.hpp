@@ -112,12 +112,13 @@ inline int64_t state_ld(int64_t batch, size_t elem) {
 }
 
 // Size of a state buffer for 32-bit buffer addressing, or 0 when it does not fit below 2^31 bytes, a row is
-// 2^24 bytes or more, or it holds more than 2^24 rows: a gather's offset is one 24-bit multiply (row index times
-// row bytes), so both operands must fit 24 bits (otherwise the 64-bit path runs, or block_cols splits the batch).
+// 2^24 bytes or more, or it holds 2^24 rows or more: a gather's offset is one 24-bit multiply (row index times
+// row bytes), so both operands must fit 24 bits, the index of the row just past the buffer included (the swept
+// step's gathers of zeros); otherwise the 64-bit path runs, or block_cols splits the batch.
 inline uint32_t buffer_bytes(int64_t rows, int64_t ld, size_t elem) {
   const int64_t row_bytes = ld * (int64_t)elem;
   const int64_t bytes = rows * row_bytes;
-  return bytes > 0 && bytes <= (int64_t)INT32_MAX && row_bytes < (int64_t)(1 << 24) && rows <= (int64_t)(1 << 24)
+  return bytes > 0 && bytes <= (int64_t)INT32_MAX && row_bytes < (int64_t)(1 << 24) && rows < (int64_t)(1 << 24)
              ? (uint32_t)bytes
              : 0u;
 }
@@ -176,6 +177,8 @@ struct Tuning {
   int sweep_bands = 0;  // source bands of a swept step (3 or 4), read when a plan is created; 0 = automatic
   int sweep_order = 0;  // swept waves take their rows longest first: 0 yes, -1 in index order
   int sweep_paired = 0;  // swept waves walk two rows per pass: 1 always, -1 never, 0 for float32 states
+  int sweep_slots = 0;   // swept passes of 3 slots: 3 always, 0 when a wave owns 24 rows or fewer (else 6)
+  int sweep_pipe = 0;    // swept gathers of the next four rounds in flight: 0 with 3 slots, 1 also 6, -1 never
 };
 Tuning &tuning();
 

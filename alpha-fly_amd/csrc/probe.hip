@@ -24,6 +24,8 @@ thread_local std::string g_probe_error;
 // The launch-time choices of the swept kernel that a replay mirrors (flyprobe_set_tuning; fly_set_tuning's keys).
 struct SweepChoice {
   int paired = 0;
+  int slots = 0;
+  int pipe = 0;
 };
 SweepChoice g_sweep;
 
@@ -136,7 +138,9 @@ extern "C" int flyprobe_set_tuning(const char *key, int64_t value) {
     FLY_REQUIRE(key != nullptr, "key is null");
     const std::string k(key);
     if (k == "sweep_paired") g_sweep.paired = (int)value;
-    else FLY_REQUIRE(false, "the replays mirror only sweep_paired, not " + k);
+    else if (k == "sweep_slots") g_sweep.slots = (int)value;
+    else if (k == "sweep_pipe") g_sweep.pipe = (int)value;
+    else FLY_REQUIRE(false, "the replays mirror only sweep_paired, sweep_slots and sweep_pipe, not " + k);
   });
 }
 
@@ -188,6 +192,8 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       a.sweep_positions = band_off && order ? positions : 0;
       a.sweep_bands = bands;
       a.sweep_paired = g_sweep.paired;
+      a.sweep_slots = g_sweep.slots;
+      a.sweep_pipe = g_sweep.pipe;
       replay<1>(a, nnz, prev_rows, as_stream(stream));
     };
     if (state_f16)
@@ -243,6 +249,8 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       a.sweep_positions = band_off && order ? positions : 0;
       a.sweep_bands = bands;
       a.sweep_paired = g_sweep.paired;
+      a.sweep_slots = g_sweep.slots;
+      a.sweep_pipe = g_sweep.pipe;
       replay<2>(a, nnz, prev_rows, as_stream(stream));
     };
     if (state_f16)

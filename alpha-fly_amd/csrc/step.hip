@@ -76,6 +76,8 @@ void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
       a.xprev && a.xbytes && !(a.out_exact && a.batch % v)) {
     LaunchTimer timer(FLY_K_STATE_STEP, st);
     a.sweep_paired = tuning().sweep_paired;
+    a.sweep_slots = tuning().sweep_slots;
+    a.sweep_pipe = tuning().sweep_pipe;
     launch_swept<S, U, 0>(a, st);
     check_launch("swept state step");
     return;
@@ -541,6 +543,8 @@ extern "C" int fly_set_tuning(const char *key, int64_t value) {
     else if (k == "sweep_bands") tuning().sweep_bands = (int)value;
     else if (k == "sweep_order") tuning().sweep_order = (int)value;
     else if (k == "sweep_paired") tuning().sweep_paired = (int)value;
+    else if (k == "sweep_slots") tuning().sweep_slots = (int)value;
+    else if (k == "sweep_pipe") tuning().sweep_pipe = (int)value;
     else if (k == "step_lds") tuning().step_lds = (int)std::min<int64_t>(std::max<int64_t>(value, 0), 65536);
     else FLY_REQUIRE(false, "unknown tuning key " + k);
   });

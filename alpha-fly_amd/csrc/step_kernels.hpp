@@ -94,6 +94,9 @@ struct StepArgs {
                            // (-1 entries: no row), or 0: the rows split evenly between the waves
   int32_t sweep_bands;     // swept steps: bands of band_off (3 or 4)
   int32_t sweep_paired;    // swept steps: two rows per pass (1), one (-1), by the state type (0)
+  int32_t sweep_slots;     // swept steps: 3 forces passes of 3 slots (0: 6 slots when a wave owns over 24 rows)
+  int32_t sweep_pipe;      // swept steps: the next four rounds' gathers in flight during the sums: 0 with 3 slots,
+                           // 1 also with 6, -1 never
 };
 
 // Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
@@ -682,7 +685,8 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // colval[band_off[i][b] .. band_off[i][b+1]).  Lane groups of 8 lanes x 16 bytes gather one 128-byte line each; a
 // slot's rounds run to the longest of the wave's 8 rows in that slot and band, the shorter rows' extra gathers at
 // an offset past the buffer (zeros, no memory access).  REPLAY as for the other step kernels.
-template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, bool PAIRED = false>
+template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, bool PAIRED = false,
+          bool PIPE = false>
 __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, U> a) {
   constexpr int UNR = 4;
   static_assert(K + 1 <= 8 && V * sizeof(S) == 16, "band starts in the lanes of a group, 16-byte lanes");
@@ -692,6 +696,9 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
   const __amdgpu_buffer_rsrc_t r =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
   const int chunks = (a.batch + 8 * V - 1) / (8 * V);
+  // the rows of X_{t-1}: as a column of a record, the row just past the buffer, whose gathers read zeros (below
+  // 2^24, so its 24-bit product with row_bytes is exact)
+  const uint32_t past_row = a.xbytes / row_bytes;
   const int R = a.rows_per_wave;
   // positions of the order: R per wave when it is laid out per wave, else one per row
   const uint32_t npos = a.sweep_positions > 0 ? (uint32_t)R * 16u * gridDim.x : (uint32_t)a.nrows;
@@ -712,7 +719,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
     for (int j = 0; j < SLOTS; ++j) {
       const int64_t left = min((int64_t)R - k0 - 8 * j, (int64_t)npos - (int64_t)base - 8 * j);
       nrow[j] = (int)max<int64_t>(0, min<int64_t>(8, left));
-      lf[j] = PAIRED || a.sweep_positions > 0 || nrow[j] >= 5 || nrow[j] == 0 ? 0
+      lf[j] = PAIRED || nrow[j] >= 5 || nrow[j] == 0 ? 0
               : (nrow[j] >= 3 ? 1 : (nrow[j] == 2 ? 2 : 3));
     }
     int off[SLOTS];   // lane s <= K: band_off[row][s]
@@ -746,7 +753,8 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
             auto block = [&](int q0) {
               const int q = q0 + s;
               const int e = q < nA ? bA + q : (q < n ? bB + (q - nA) : (eB > bB ? eB - 1 : eA - 1));
-              return a.colval[max(e, 0)];
+              const int2 rc = a.colval[max(e, 0)];
+              return q < n ? rc : make_int2((int)past_row, 0);   // past both rows: a gather of zeros
             };
             int2 rec = rounds > 0 ? block(0) : make_int2(0, 0);
             for (int q0 = 0; q0 < rounds; q0 += 8) {
@@ -760,7 +768,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                     constexpr int u = decltype(J)::value, sl = h0 + u;
                     const int cc = group_bcast<8, sl>(rec.x);
                     wj[u] = group_bcast<8, sl>(rec.y);
-                    const uint32_t o = q0 + sl < n ? __umul24((uint32_t)cc, row_bytes) + voff : 0x80000000u;
+                    const uint32_t o = __umul24((uint32_t)cc, row_bytes) + voff;
                     xr[u] = bload<S, V>(r, (int)o, 0);
                   });
                   if constexpr (REPLAY != 0) {
@@ -797,7 +805,71 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           const int rounds = wave_max_of_groups(end - beg);
           // lane s brings record q0 + s of its row's band (clamped into the row), and round q reaches the group's
           // lanes by a broadcast of lane q; the next block of 8 loads while this one's gathers are in flight
-          auto block = [&](int q0) { return a.colval[max(min(beg + q0 + s, end - 1), 0)]; };
+          auto block = [&](int q0) {
+            const int q = beg + q0 + s;
+            const int2 rc = a.colval[max(min(q, end - 1), 0)];
+            // past the row's band: the first row past the buffer (its gather reads zeros), weight 0
+            return q < end ? rc : make_int2((int)past_row, 0);
+          };
+          if constexpr (PIPE) {
+            // Four rounds' gathers stay in flight while the previous four are summed: the gathers of rounds
+            // q .. q+3 are issued before the sums of rounds q-4 .. q-1 wait for theirs.
+            using vec = typename Lanes<S, V>::vec;
+            auto gather4 = [&](const int2 &rc, auto H, int q0, vec (&xr)[4], int (&wj)[4]) {
+              constexpr int h0 = decltype(H)::value * 4;
+              static_for<4>([&](auto J) {
+                constexpr int u = decltype(J)::value, sl = h0 + u;
+                const int cc = group_bcast<8, sl>(rc.x);
+                wj[u] = group_bcast<8, sl>(rc.y);
+                const uint32_t o = __umul24((uint32_t)cc, row_bytes) + voff;
+                xr[u] = bload<S, V>(r, (int)o, 0);
+              });
+            };
+            auto sum4 = [&](const vec (&xr)[4], const int (&wj)[4]) {
+              if constexpr (REPLAY != 0) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) ReplayBits<S, V>::fold(bits, xr[u], wj[u]);
+              } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  const float wt = __int_as_float(wj[u]);
+#pragma unroll
+                  for (int i = 0; i < V; ++i) acc[j][i] = fmaf(wt, Lanes<S, V>::at(xr[u], i), acc[j][i]);
+                }
+              }
+            };
+            // halves of 4 rounds: half h is lanes 4 (h % 2) .. +3 of record block h / 2; the loop body has no
+            // branch, so each sum waits only for its own four gathers
+            const int nh = (rounds + 3) >> 2;
+            if (nh > 0) {
+              vec xa[4], xb[4];
+              int wa[4], wb[4];
+              int2 rec = block(0);
+              int2 nxt = nh > 2 ? block(8) : rec;
+              gather4(rec, std::integral_constant<int, 0>{}, 0, xa, wa);
+              int h = 0;
+              for (; h + 2 < nh; h += 2) {   // halves h + 1 and h + 2 exist
+                // the scheduler keeps this order: each sum then waits only for its own gathers
+                gather4(rec, std::integral_constant<int, 1>{}, 4 * h, xb, wb);
+                __builtin_amdgcn_sched_barrier(0);
+                sum4(xa, wa);
+                __builtin_amdgcn_sched_barrier(0);
+                gather4(nxt, std::integral_constant<int, 0>{}, 4 * h + 8, xa, wa);
+                rec = nxt;
+                nxt = block(4 * h + 16);
+                __builtin_amdgcn_sched_barrier(0);
+                sum4(xb, wb);
+                __builtin_amdgcn_sched_barrier(0);
+              }
+              if (h + 1 < nh) {
+                gather4(rec, std::integral_constant<int, 1>{}, 4 * h, xb, wb);
+                sum4(xa, wa);
+                sum4(xb, wb);
+              } else {
+                sum4(xa, wa);
+              }
+            }
+          } else {
           int2 rec = rounds > 0 ? block(0) : make_int2(0, 0);
           for (int q0 = 0; q0 < rounds; q0 += 8) {
             const int2 nxt = block(q0 + 8);
@@ -810,7 +882,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                   constexpr int u = decltype(J)::value, sl = h0 + u;
                   const int cc = group_bcast<8, sl>(rec.x);
                   wj[u] = group_bcast<8, sl>(rec.y);
-                  const uint32_t o = beg + q0 + sl < end ? __umul24((uint32_t)cc, row_bytes) + voff : 0x80000000u;
+                  const uint32_t o = __umul24((uint32_t)cc, row_bytes) + voff;
                   xr[u] = bload<S, V>(r, (int)o, 0);
                 });
                 if constexpr (REPLAY != 0) {
@@ -828,6 +900,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
             });
             rec = nxt;
           }
+          }
         }
         }
         __syncthreads();   // the workgroup's waves start the next band together
@@ -841,7 +914,10 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           }
           const int i = g >> lf[j];
           const bool first = (g & ((1 << lf[j]) - 1)) == 0;
-          const int32_t rs = first && i < nrow[j] && in_batch ? row_at(base + 8u * j + (uint32_t)i) : -1;
+          // the position is recomputed for every chunk rather than its address kept live across the bands
+          uint32_t pj = base + 8u * j + (uint32_t)i;
+          asm volatile("" : "+v"(pj));
+          const int32_t rs = first && i < nrow[j] && in_batch ? row_at(pj) : -1;
           if (rs >= 0) {
             const uint32_t rj = (uint32_t)rs;
             if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j], bits);
@@ -874,7 +950,7 @@ inline int cu_count() {
   return n;
 }
 
-template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false>
+template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false, bool PIPE = false>
 void launch_swept_shape(const StepArgs<S, U> &a, unsigned grid, hipStream_t st) {
   constexpr int V = 16 / (int)sizeof(S);
   static bool fits = false;
@@ -882,13 +958,13 @@ void launch_swept_shape(const StepArgs<S, U> &a, unsigned grid, hipStream_t st) 
     int nb = 0;
     FLY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
         &nb,
-        reinterpret_cast<const void *>(&k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED>),
+        reinterpret_cast<const void *>(&k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED, PIPE>),
         1024, 0));
     FLY_REQUIRE(nb >= 1, "the swept state step does not fit a CU");
     fits = true;
   }
-  hipLaunchKernelGGL((k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED>), dim3(grid), dim3(1024),
-                     0, st, a);
+  hipLaunchKernelGGL((k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED, PIPE>), dim3(grid),
+                     dim3(1024), 0, st, a);
 }
 
 // One swept step: one workgroup per CU, the rows split evenly between the waves (one pass of up to 24 or 48 rows
@@ -900,14 +976,18 @@ void launch_swept(StepArgs<S, U> a, hipStream_t st) {
               "a per-wave sweep layout needs its order");
   a.rows_per_wave = a.sweep_positions > 0 ? a.sweep_positions
                                           : (int32_t)((a.nrows + 16 * (int64_t)grid - 1) / (16 * (int64_t)grid));
-  const bool few = a.rows_per_wave <= 24;
+  const bool few = a.rows_per_wave <= 24 || a.sweep_slots == 3;
   switch (a.sweep_bands) {
     case 3:
       if (few) launch_swept_shape<S, U, 3, 3, REPLAY>(a, grid, st);
       else launch_swept_shape<S, U, 3, 6, REPLAY>(a, grid, st);
       break;
     case 4:
-      if (few) launch_swept_shape<S, U, 4, 3, REPLAY>(a, grid, st);
+      // passes of 3 slots keep the next four rounds' gathers in flight during the sums (step 5 at B = 1120:
+      // 1.006 -> 0.959 ms); at 6 slots the second set of gathers costs spills and gains nothing
+      if (few && a.sweep_pipe >= 0) launch_swept_shape<S, U, 4, 3, REPLAY, false, true>(a, grid, st);
+      else if (few) launch_swept_shape<S, U, 4, 3, REPLAY>(a, grid, st);
+      else if (a.sweep_pipe > 0) launch_swept_shape<S, U, 4, 6, REPLAY, false, true>(a, grid, st);
       // float32 states walk two rows per pass (measured +1.6% at B = 1120); half states not (-5%: 16 FMAs per
       // gathered line of 8 halves cost more than the rounds they save)
       else if (a.sweep_paired > 0 || (a.sweep_paired == 0 && sizeof(S) == 4))

@@ -605,7 +605,7 @@ def main() -> int:
         tuned = dict(kv.split("=") for kv in args.tune)
         bands = 3 if tuned.get("sweep_bands") == "3" else 4      # the plan's band count (sweep_bands tuning)
         probe = _probe_lib()
-        for key in ("sweep_paired",):     # the swept kernel's launch-time choice, mirrored
+        for key in ("sweep_paired", "sweep_slots", "sweep_pipe"):     # the swept kernel's launch-time choices
             if key in tuned:
                 _probe_check(probe, probe.flyprobe_set_tuning(key.encode(), int(tuned[key])), "flyprobe_set_tuning")
         rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev, sweep_bands=bands)

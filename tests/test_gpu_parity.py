@@ -462,7 +462,8 @@ def test_full_scale_blocked_columns_match_unblocked(full_net):
 def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
     """The long-row steps (166,539-166,700 and 77,286 rows of ~63 non-zeros over 166K sources) run as a banded sweep
     of the sources (k_state_step_swept: 4 bands, or 3 from the sweep_bands tuning; one or two rows per pass; rows in
-    index order or longest first); with the sweep off (tuning swept=-1) they run on the grouped kernel.  Same sums
+    index order or longest first; passes of 6 or 3 slots, with or without the next rounds' gathers in flight); with
+    the sweep off (tuning swept=-1) they run on the grouped kernel.  Same sums
     in another order: float16 deviation logits agree within 5e-4 and float32 within 2e-5, with the argmax on
     >= 99.9% of 1120 boards."""
     from chessfly import _hip
@@ -486,7 +487,8 @@ def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
             variants = {}
             for label, key, value in (("default", "sweep_bands", 0), ("3 bands", "sweep_bands", 3),
                                       ("index order", "sweep_order", -1), ("two rows per pass", "sweep_paired", 1),
-                                      ("one row per pass", "sweep_paired", -1)):
+                                      ("one row per pass", "sweep_paired", -1), ("3-slot passes", "sweep_slots", 3),
+                                      ("pipelined 6 slots", "sweep_pipe", 1), ("never pipelined", "sweep_pipe", -1)):
                 _hip.set_tuning(key, value)
                 variants[label] = run()
                 _hip.set_tuning(key, 0)
@@ -499,7 +501,7 @@ def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
                 assert dl < tol and dw < tol and agree >= 0.999, (dtype, label, dl, dw, agree)
             assert not torch.equal(variants["default"][0], grouped[0])     # the sweep did run
     finally:
-        for key in ("swept", "sweep_bands", "sweep_order", "sweep_paired"):
+        for key in ("swept", "sweep_bands", "sweep_order", "sweep_paired", "sweep_slots", "sweep_pipe"):
             _hip.set_tuning(key, 0)
         net.infer_dtype = torch.float16
 

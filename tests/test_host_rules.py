@@ -2,7 +2,8 @@
 
 The gathers address the previous state with one 24-bit multiply-add (row index times row bytes) into a 32-bit
 buffer offset.  `fly::buffer_bytes` must therefore refuse any state whose size passes 2^31 - 1 bytes, whose row
-is 2^24 bytes or more, or which holds more than 2^24 rows; the caller then takes the 64-bit path.  `state_ld`
+is 2^24 bytes or more, or which holds 2^24 rows or more (the index of the row just past the buffer, which the
+swept step gathers zeros from, must fit 24 bits too); the caller then takes the 64-bit path.  `state_ld`
 gives every state row an odd number of 128-byte lines.
 """
 
@@ -21,7 +22,7 @@ PROGRAM = r"""
 #include <cstdio>
 int main() {
   const long long cases[][3] = {
-      {166700, 1216, 2}, {166700, 1, 2}, {1 << 24, 1, 2}, {(1 << 24) + 1, 1, 2}, {(1 << 24) + 1, 64, 2},
+      {166700, 1216, 2}, {166700, 1, 2}, {(1 << 24) - 1, 1, 2}, {1 << 24, 1, 2}, {(1 << 24) + 1, 64, 2},
       {1, (1 << 23) - 1, 2}, {1, 1 << 23, 2}, {4, 1 << 21, 4}, {300, 1 << 21, 4}, {16384, 32768, 4}, {16383, 32768, 4},
       {0, 64, 2}, {10, 0, 2}};
   for (const auto &c : cases) printf("b %lld %lld %lld %u\n", c[0], c[1], c[2], fly::buffer_bytes(c[0], c[1], c[2]));
@@ -52,7 +53,7 @@ def test_buffer_bytes_accepts_what_24_bit_offsets_can_address(rules):
     bb, _ = rules
     assert bb[(166700, 1216, 2)] == 166700 * 1216 * 2          # the full-scale half state at 1120 boards
     assert bb[(166700, 1, 2)] == 166700 * 2
-    assert bb[(1 << 24, 1, 2)] == (1 << 24) * 2                # 2^24 rows: every row index fits 24 bits
+    assert bb[((1 << 24) - 1, 1, 2)] == ((1 << 24) - 1) * 2    # every row index and the one past the end fit 24 bits
     assert bb[(1, (1 << 23) - 1, 2)] == (1 << 24) - 2          # the largest row below 2^24 bytes
     assert bb[(4, 1 << 21, 4)] == 1 << 25
     assert bb[(16383, 32768, 4)] == 16383 * 32768 * 4           # just below 2 GiB
@@ -60,7 +61,7 @@ def test_buffer_bytes_accepts_what_24_bit_offsets_can_address(rules):
 
 def test_buffer_bytes_refuses_what_they_cannot(rules):
     bb, _ = rules
-    assert bb[((1 << 24) + 1, 1, 2)] == 0      # a row index past 24 bits would wrap in the multiply
+    assert bb[(1 << 24, 1, 2)] == 0            # the row past the end, 2^24, would wrap in the multiply
     assert bb[((1 << 24) + 1, 64, 2)] == 0
     assert bb[(1, 1 << 23, 2)] == 0            # a 2^24-byte row
     assert bb[(300, 1 << 21, 4)] == 0          # rows below 2^24 bytes, but 2.5 GB in all
