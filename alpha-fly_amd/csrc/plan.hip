@@ -141,16 +141,6 @@ __global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *_
   cbase[j] = (mode == FLY_MODE_F32 && out_src[j] >= 0) ? 0.0f : c;
 }
 
-// The swept waves' order of a step's rows (k_sweep_order: each wave's own rows, longest first).
-void sweep_order(const int32_t *rowptr, int64_t nr, DevArray<int32_t> &order, hipStream_t st) {
-  FLY_REQUIRE(nr > 0 && nr < (int64_t)INT32_MAX, "rows out of range");
-  const int64_t waves = 16 * (int64_t)cu_count();
-  const int64_t per = (nr + waves - 1) / waves;   // launch_swept's rows_per_wave
-  order.alloc((size_t)nr);
-  hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for((nr + per - 1) / per, 64)), dim3(64), 0, st, rowptr, nr, per,
-                     order.p);
-}
-
 }  // namespace
 }  // namespace fly
 
@@ -224,7 +214,8 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
           plan->band_off[t].alloc((size_t)nr * (plan->sweep_bands + 1));
           hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
                              plan->colval[t].p, nr, cone->rows_n[t - 1], plan->sweep_bands, plan->band_off[t].p);
-          sweep_order(plan->rowptr[t].p, nr, plan->sweep_rows[t], st);
+          plan->sweep_rows[t].alloc((size_t)nr);
+          build_sweep_order(plan->rowptr[t].p, plan->band_off[t].p, plan->sweep_bands, nr, plan->sweep_rows[t].p, st);
         }
       }
       if (nr) {
@@ -297,7 +288,8 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
       plan->band_off[0].alloc((size_t)n * (plan->sweep_bands + 1));
       hipLaunchKernelGGL(k_band_off, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
                          plan->colval[0].p, n, n, plan->sweep_bands, plan->band_off[0].p);
-      sweep_order(plan->rowptr[0].p, n, plan->sweep_rows[0], st);
+      plan->sweep_rows[0].alloc((size_t)n);
+      build_sweep_order(plan->rowptr[0].p, plan->band_off[0].p, plan->sweep_bands, n, plan->sweep_rows[0].p, st);
     }
     check_launch("full plan");
     FLY_HIP(hipStreamSynchronize(st));

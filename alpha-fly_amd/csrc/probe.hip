@@ -154,10 +154,7 @@ extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int
     *swept = sweep_suits(rowptr, prev_rows, nrows, nnz, as_stream(stream)) ? 1 : 0;
     hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
                        static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
-    const int64_t waves = 16 * (int64_t)cu_count();
-    const int64_t per = (nrows + waves - 1) / waves;   // launch_swept's rows_per_wave
-    hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for((nrows + per - 1) / per, 64)), dim3(64), 0, as_stream(stream),
-                       rowptr, nrows, per, order);
+    build_sweep_order(rowptr, band_off, bands, nrows, order, as_stream(stream));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) throw Error{1, std::string("band table launch: ") + hipGetErrorString(e)};
   });

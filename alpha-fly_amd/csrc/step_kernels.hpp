@@ -623,6 +623,85 @@ __global__ void k_sweep_order(const int32_t *__restrict__ rowptr, int64_t nr, in
   }
 }
 
+// Rounds one slot of a swept wave issues for one band: the longest share of its rows' band counts (a slot of
+// r <= 4 rows spreads each row over 2, 4 or 8 groups, as the kernel does), padded to the 4 rounds of a gather block.
+// c(i): the band count of the slot's row i.
+template <typename C>
+__device__ inline int slot_band_rounds(C &&c, int r) {
+  const int lf = r >= 5 ? 0 : (r >= 3 ? 1 : (r == 2 ? 2 : 3));
+  int m = 0;
+  for (int i = 0; i < r; ++i) m = max(m, ((int)c(i) + (1 << lf) - 1) >> lf);
+  return (m + 3) & ~3;
+}
+
+constexpr int kSearchRows = 64;     // wave segments of at most this many rows are searched (longer keep the sort)
+constexpr int kSearchThreads = 64;  // one thread per segment
+constexpr int kSearchIters = 1200;  // proposed swaps per segment (600: 0.933 of the sorted rounds at full scale, 1200: 0.923)
+
+// After k_sweep_order: each wave's rows rearranged between its slots so that a slot's 8 rows have like band
+// counts and fewer of its rounds are padding.  One thread per wave segment runs a seeded local search: it proposes
+// swapping two rows of different slots and keeps the swap when the two slots' rounds (summed over the bands, as
+// slot_band_rounds counts them) do not grow.  The wave keeps its rows, so its share of the work is unchanged.
+// LDS arrays are indexed thread-fastest, so the threads of a wave touch consecutive words.
+__global__ __launch_bounds__(kSearchThreads) void k_sweep_order_search(const int32_t *__restrict__ band_off, int K,
+                                                                       int64_t nr, int64_t per,
+                                                                       int32_t *__restrict__ order) {
+  __shared__ uint16_t cnt[4][kSearchRows][kSearchThreads];
+  __shared__ int32_t row[kSearchRows][kSearchThreads];
+  __shared__ int16_t cost[kSearchRows / 8][kSearchThreads];   // rounds of each slot, summed over the bands
+  const int t = threadIdx.x;
+  const int64_t seg = blockIdx.x * (int64_t)kSearchThreads + t;
+  const int64_t b = seg * per;
+  if (b >= nr || per > kSearchRows) return;
+  const int m = (int)min(per, nr - b);
+  for (int k = 0; k < m; ++k) {
+    const int32_t r = order[b + k];
+    row[k][t] = r;
+    for (int q = 0; q < K; ++q)
+      cnt[q][k][t] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
+  }
+  const int slots = (m + 7) / 8;
+  if (slots < 2) return;
+  auto slot_cost = [&](int j) {
+    const int r = min(8, m - 8 * j);
+    int c = 0;
+    for (int q = 0; q < K; ++q) c += slot_band_rounds([&](int i) { return cnt[q][8 * j + i][t]; }, r);
+    return c;
+  };
+  for (int j = 0; j < slots; ++j) cost[j][t] = (int16_t)slot_cost(j);
+  auto swap_rows = [&](int i, int k) {
+    const int32_t rr = row[i][t];
+    row[i][t] = row[k][t];
+    row[k][t] = rr;
+    for (int q = 0; q < K; ++q) {
+      const uint16_t cc = cnt[q][i][t];
+      cnt[q][i][t] = cnt[q][k][t];
+      cnt[q][k][t] = cc;
+    }
+  };
+  uint32_t state = 2463534242u ^ (uint32_t)(seg * 2654435761u);   // xorshift32, seeded by the segment
+  auto next = [&]() {
+    state ^= state << 13;
+    state ^= state >> 17;
+    state ^= state << 5;
+    return state;
+  };
+  for (int it = 0; it < kSearchIters; ++it) {
+    const int i = (int)(next() % (uint32_t)m), k = (int)(next() % (uint32_t)m);
+    const int si = i >> 3, sk = k >> 3;
+    if (si == sk) continue;
+    swap_rows(i, k);
+    const int ci = slot_cost(si), ck = slot_cost(sk);
+    if (ci + ck > cost[si][t] + cost[sk][t]) {
+      swap_rows(i, k);
+    } else {
+      cost[si][t] = (int16_t)ci;
+      cost[sk][t] = (int16_t)ck;
+    }
+  }
+  for (int k = 0; k < m; ++k) order[b + k] = row[k][t];
+}
+
 __global__ void k_zero_int(int32_t *p) { *p = 0; }
 
 // The longest row of a CSR matrix (rows: nr, into *out, which starts at 0).
@@ -948,6 +1027,20 @@ inline int cu_count() {
     n = cus;
   }
   return n;
+}
+
+// The swept waves' order of a step's rows (nr, into `order`): each wave's own rows_per_wave rows, longest first
+// (k_sweep_order), then rearranged between the wave's slots (k_sweep_order_search) from the band table (nr, K + 1).
+inline void build_sweep_order(const int32_t *rowptr, const int32_t *band_off, int K, int64_t nr, int32_t *order,
+                              hipStream_t st) {
+  FLY_REQUIRE(nr > 0 && nr < (int64_t)INT32_MAX && (K == 3 || K == 4), "rows or bands out of range");
+  const int64_t waves = 16 * (int64_t)cu_count();
+  const int64_t per = (nr + waves - 1) / waves;   // launch_swept's rows_per_wave
+  const int64_t segs = (nr + per - 1) / per;
+  hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, rowptr, nr, per, order);
+  if (per <= kSearchRows)
+    hipLaunchKernelGGL(k_sweep_order_search, dim3(blocks_for(segs, kSearchThreads)), dim3(kSearchThreads), 0, st,
+                       band_off, K, nr, per, order);
 }
 
 template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false, bool PIPE = false>

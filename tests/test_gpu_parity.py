@@ -506,10 +506,26 @@ def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
         net.infer_dtype = torch.float16
 
 
-def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per):
+def _slot_rounds_numpy(c, m, j):
+    """Rounds of slot j (positions 8j .. 8j+7 below m) per segment, summed over the bands: the longest share of its
+    rows' band counts (a slot of r <= 4 rows spreads each row over 2, 4 or 8 lane groups), padded to 4 rounds.
+    c: (segments, bands, positions) counts; m, j: (segments,)."""
+    r = np.clip(m - 8 * j, 0, 8)
+    lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))
+    pos = 8 * j[:, None] + np.arange(8)[None, :]                                   # (segments, 8)
+    valid = np.arange(8)[None, :] < r[:, None]
+    vals = np.take_along_axis(c, np.minimum(pos, c.shape[2] - 1)[:, None, :].repeat(c.shape[1], 1), axis=2)
+    share = (vals + (1 << lf)[:, None, None] - 1) >> lf[:, None, None]
+    mx = np.where(valid[:, None, :], share, 0).max(axis=2)
+    return ((mx + 3) & ~3).sum(axis=1)
+
+
+def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, iters=1200):
     """The swept step's plan tables restated: off[i][b] = row i's start plus its non-zeros with a column in the
-    bands before b (band of column c: c * bands // prev_rows), off[i][bands] = its end; the order lists each
-    consecutive segment of `per` rows longest first, ties by row index."""
+    bands before b (band of column c: c * bands // prev_rows), off[i][bands] = its end.  The order lists each
+    consecutive segment of `per` rows longest first (ties by row index), then, in segments of at most 64 rows, the
+    seeded local search of the plan: xorshift32 per segment, `iters` proposed swaps of two rows in different slots,
+    each kept when the two slots' rounds do not grow."""
     nr = len(rowptr) - 1
     lens = np.diff(rowptr)
     band = cols.astype(np.int64) * bands // prev_rows
@@ -522,14 +538,47 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per):
     for b in range(0, nr, per):
         idx = np.arange(b, min(b + per, nr))
         order[b:b + len(idx)] = idx[np.lexsort((idx, -lens[idx]))]
+    if per > 64:
+        return off, order
+    nseg = -(-nr // per)
+    m = np.minimum(per, nr - np.arange(nseg) * per)
+    pad = np.full(nseg * per, -1, np.int64)
+    pad[:nr] = order
+    rows = pad.reshape(nseg, per)
+    c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)   # (nseg, bands, per)
+    live = (m + 7) // 8 >= 2
+    seg = np.arange(nseg, dtype=np.uint64)
+    state = (np.uint64(2463534242) ^ ((seg * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF))).astype(np.uint32)
+    def nxt():
+        nonlocal state
+        state = state ^ (state << np.uint32(13))
+        state = state ^ (state >> np.uint32(17))
+        state = state ^ (state << np.uint32(5))
+        return state
+    ar = np.arange(nseg)
+    for _ in range(iters):
+        i = (nxt() % m.astype(np.uint32)).astype(np.int64)
+        k = (nxt() % m.astype(np.uint32)).astype(np.int64)
+        si, sk = i >> 3, k >> 3
+        go = live & (si != sk)
+        before = _slot_rounds_numpy(c, m, si) + _slot_rounds_numpy(c, m, sk)
+        c2, rows2 = c.copy(), rows.copy()
+        c2[ar, :, i], c2[ar, :, k] = c[ar, :, k], c[ar, :, i]
+        rows2[ar, i], rows2[ar, k] = rows[ar, k], rows[ar, i]
+        after = _slot_rounds_numpy(c2, m, si) + _slot_rounds_numpy(c2, m, sk)
+        keep = go & (after <= before)
+        c = np.where(keep[:, None, None], c2, c)
+        rows = np.where(keep[:, None], rows2, rows)
+    order = rows.reshape(-1)[:nr]
     return off, order
 
 
 def test_sweep_band_table_order_and_rule_match_numpy():
-    """The plan-time work of a swept step (k_band_off, k_sweep_order and the suitability rule of sweep_suits, shared
-    by the plan and the probe library's flyprobe_band_table) against a numpy restatement, bit for bit, on random
-    CSR matrices of 70,000 rows: a plain one sweeps; one with a hub row (longer than 4 x the mean + 64) and one over
-    32,768 source rows or fewer do not."""
+    """The plan-time work of a swept step (k_band_off, the order of k_sweep_order and k_sweep_order_search, and the
+    suitability rule of sweep_suits, shared by the plan and the probe library's flyprobe_band_table) against a numpy
+    restatement, bit for bit, on random CSR matrices of 70,000 rows (18 rows per wave: slots of 8, 8 and 2): a
+    plain one sweeps; one with a hub row (longer than 4 x the mean + 64) and one over 32,768 source rows or fewer do
+    not.  The search leaves every wave its own rows and never adds rounds."""
     import ctypes
     probe = ctypes.CDLL(os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so"))
     probe.flyprobe_last_error.restype = ctypes.c_char_p
@@ -557,11 +606,30 @@ def test_sweep_band_table_order_and_rule_match_numpy():
                                            d_off.data_ptr(), d_order.data_ptr(), ctypes.byref(swept), None)
             assert rc == 0, probe.flyprobe_last_error()
             torch.cuda.synchronize()
-            off, order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, -(-nr // (16 * cus)))
+            per = -(-nr // (16 * cus))
+            off, order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, iters=1200 if want_swept else 0)
+            got = d_order.cpu().numpy()
             print(f"{label}, {bands} bands: swept {swept.value}", flush=True)
             assert swept.value == want_swept, (label, bands, swept.value)
             assert np.array_equal(d_off.cpu().numpy(), off), (label, bands)
-            assert np.array_equal(d_order.cpu().numpy(), order), (label, bands)
+            if not want_swept:
+                continue
+            assert np.array_equal(got, order), (label, bands)
+            # each wave keeps its rows, and the search issues no more rounds than longest first
+            _, sorted_order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, iters=0)
+            for b0 in range(0, nr, per):
+                assert np.array_equal(np.sort(got[b0:b0 + per]), np.arange(b0, min(b0 + per, nr)))
+            cnt = np.stack([off[:, q + 1] - off[:, q] for q in range(bands)], axis=1)
+            def total(o):
+                nseg = -(-nr // per)
+                m = np.minimum(per, nr - np.arange(nseg) * per)
+                pad = np.full(nseg * per, -1, np.int64)
+                pad[:nr] = o
+                rows = pad.reshape(nseg, per)
+                c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)
+                return sum(int(_slot_rounds_numpy(c, m, np.full(nseg, j)).sum()) for j in range(-(-per // 8)))
+            assert total(got) <= total(sorted_order), (label, bands)
+            print(f"  rounds: longest first {total(sorted_order)}, searched {total(got)}", flush=True)
 
 
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
