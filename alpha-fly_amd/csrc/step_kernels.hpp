@@ -635,71 +635,77 @@ __device__ inline int slot_band_rounds(C &&c, int r) {
 }
 
 constexpr int kSearchRows = 64;     // wave segments of at most this many rows are searched (longer keep the sort)
-constexpr int kSearchThreads = 64;  // one thread per segment
-constexpr int kSearchIters = 1200;  // proposed swaps per segment (600: 0.933 of the sorted rounds at full scale, 1200: 0.923)
+constexpr int kSearchSteps = 200;   // moves tried per segment
 
 // After k_sweep_order: each wave's rows rearranged between its slots so that a slot's 8 rows have like band
-// counts and fewer of its rounds are padding.  One thread per wave segment runs a seeded local search: it proposes
-// swapping two rows of different slots and keeps the swap when the two slots' rounds (summed over the bands, as
-// slot_band_rounds counts them) do not grow.  The wave keeps its rows, so its share of the work is unchanged.
-// LDS arrays are indexed thread-fastest, so the threads of a wave touch consecutive words.
-__global__ __launch_bounds__(kSearchThreads) void k_sweep_order_search(const int32_t *__restrict__ band_off, int K,
-                                                                       int64_t nr, int64_t per,
-                                                                       int32_t *__restrict__ order) {
-  __shared__ uint16_t cnt[4][kSearchRows][kSearchThreads];
-  __shared__ int32_t row[kSearchRows][kSearchThreads];
-  __shared__ int16_t cost[kSearchRows / 8][kSearchThreads];   // rounds of each slot, summed over the bands
-  const int t = threadIdx.x;
-  const int64_t seg = blockIdx.x * (int64_t)kSearchThreads + t;
+// counts and fewer of its rounds are padding.  One wave per segment runs a seeded local search.  At each step every
+// lane draws two rows of the segment (xorshift32, seeded by segment and lane) and, if they sit in different slots,
+// the change in the two slots' rounds (summed over the bands, as slot_band_rounds counts them) that swapping them
+// would make; the lowest change wins (ties: the lowest lane) and is made if it adds no rounds, so the search also
+// walks across plateaus.  The wave keeps its rows, so its share of the work is unchanged.
+__global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__restrict__ band_off, int K, int64_t nr,
+                                                           int64_t per, int32_t *__restrict__ order) {
+  __shared__ uint16_t cnt[4][kSearchRows];
+  __shared__ int32_t row[kSearchRows];
+  __shared__ int32_t cost[kSearchRows / 8];   // rounds of each slot, summed over the bands
+  const int lane = threadIdx.x;
+  const int64_t seg = blockIdx.x;
   const int64_t b = seg * per;
   if (b >= nr || per > kSearchRows) return;
   const int m = (int)min(per, nr - b);
-  for (int k = 0; k < m; ++k) {
+  for (int k = lane; k < m; k += 64) {
     const int32_t r = order[b + k];
-    row[k][t] = r;
+    row[k] = r;
     for (int q = 0; q < K; ++q)
-      cnt[q][k][t] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
+      cnt[q][k] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
   }
+  __syncthreads();
   const int slots = (m + 7) / 8;
   if (slots < 2) return;
-  auto slot_cost = [&](int j) {
+  // rounds of slot j with the row at position `out` replaced by the row at position `in` (out = -1: as it is)
+  auto slot_cost = [&](int j, int out, int in) {
     const int r = min(8, m - 8 * j);
     int c = 0;
-    for (int q = 0; q < K; ++q) c += slot_band_rounds([&](int i) { return cnt[q][8 * j + i][t]; }, r);
+    for (int q = 0; q < K; ++q)
+      c += slot_band_rounds([&](int i) { return cnt[q][8 * j + i == out ? in : 8 * j + i]; }, r);
     return c;
   };
-  for (int j = 0; j < slots; ++j) cost[j][t] = (int16_t)slot_cost(j);
-  auto swap_rows = [&](int i, int k) {
-    const int32_t rr = row[i][t];
-    row[i][t] = row[k][t];
-    row[k][t] = rr;
-    for (int q = 0; q < K; ++q) {
-      const uint16_t cc = cnt[q][i][t];
-      cnt[q][i][t] = cnt[q][k][t];
-      cnt[q][k][t] = cc;
-    }
-  };
-  uint32_t state = 2463534242u ^ (uint32_t)(seg * 2654435761u);   // xorshift32, seeded by the segment
+  if (lane < slots) cost[lane] = slot_cost(lane, -1, 0);
+  __syncthreads();
+  uint32_t state = (2463534242u ^ (uint32_t)(seg * 2654435761u) ^ (uint32_t)((lane + 1) * 2246822507u)) | 1u;
   auto next = [&]() {
     state ^= state << 13;
     state ^= state >> 17;
     state ^= state << 5;
     return state;
   };
-  for (int it = 0; it < kSearchIters; ++it) {
+  for (int step = 0; step < kSearchSteps; ++step) {
     const int i = (int)(next() % (uint32_t)m), k = (int)(next() % (uint32_t)m);
     const int si = i >> 3, sk = k >> 3;
-    if (si == sk) continue;
-    swap_rows(i, k);
-    const int ci = slot_cost(si), ck = slot_cost(sk);
-    if (ci + ck > cost[si][t] + cost[sk][t]) {
-      swap_rows(i, k);
-    } else {
-      cost[si][t] = (int16_t)ci;
-      cost[sk][t] = (int16_t)ck;
+    int ci = 0, ck = 0, d = 1 << 20;
+    if (si != sk) {
+      ci = slot_cost(si, i, k);
+      ck = slot_cost(sk, k, i);
+      d = ci + ck - cost[si] - cost[sk];
     }
+    int key = ((d + (1 << 20)) << 6) | lane;   // the lowest change, then the lowest lane
+    for (int o = 32; o > 0; o >>= 1) key = min(key, __shfl_xor(key, o));
+    __syncthreads();
+    if ((key & 63) == lane && d <= 0) {
+      const int32_t rr = row[i];
+      row[i] = row[k];
+      row[k] = rr;
+      for (int q = 0; q < K; ++q) {
+        const uint16_t cc = cnt[q][i];
+        cnt[q][i] = cnt[q][k];
+        cnt[q][k] = cc;
+      }
+      cost[si] = ci;
+      cost[sk] = ck;
+    }
+    __syncthreads();
   }
-  for (int k = 0; k < m; ++k) order[b + k] = row[k][t];
+  for (int k = lane; k < m; k += 64) order[b + k] = row[k];
 }
 
 __global__ void k_zero_int(int32_t *p) { *p = 0; }
@@ -1039,8 +1045,7 @@ inline void build_sweep_order(const int32_t *rowptr, const int32_t *band_off, in
   const int64_t segs = (nr + per - 1) / per;
   hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, rowptr, nr, per, order);
   if (per <= kSearchRows)
-    hipLaunchKernelGGL(k_sweep_order_search, dim3(blocks_for(segs, kSearchThreads)), dim3(kSearchThreads), 0, st,
-                       band_off, K, nr, per, order);
+    hipLaunchKernelGGL(k_sweep_order_search, dim3((unsigned)segs), dim3(64), 0, st, band_off, K, nr, per, order);
 }
 
 template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false, bool PIPE = false>
