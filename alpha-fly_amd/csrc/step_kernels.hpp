@@ -708,6 +708,135 @@ __global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__rest
   for (int k = lane; k < m; k += 64) order[b + k] = row[k];
 }
 
+constexpr int kBalanceThreads = 256;
+constexpr int kBalanceSteps = 600;
+
+// After k_sweep_order_search: the rows of the 16 waves of one workgroup (one CU, whose waves meet at a barrier after
+// each band) rearranged between those waves and their slots, so that each band's slowest wave is closer to the
+// others.  Cost: for each band, 16 x the largest of the 16 waves' rounds (what the barrier waits for) plus their sum.
+// One workgroup per group of 16 segments; at each step every thread draws two positions (xorshift32 per group and
+// thread), the change in cost that swapping their rows would make is computed from the two slots' new rounds and the
+// three largest wave totals of each band, and the lowest change (ties: the lowest thread) is made if it adds no cost.
+// Every wave keeps its number of rows.
+__global__ __launch_bounds__(kBalanceThreads) void k_sweep_order_balance(const int32_t *__restrict__ band_off, int K,
+                                                                         int64_t nr, int64_t per,
+                                                                         int32_t *__restrict__ order) {
+  constexpr int W = 16;
+  __shared__ uint16_t cnt[4][W * kSearchRows];
+  __shared__ int32_t row[W * kSearchRows];
+  __shared__ int32_t sr[W][kSearchRows / 8][4];   // rounds of each wave's slot in each band
+  __shared__ int32_t tot[W][4];                   // rounds of each wave in each band
+  __shared__ int32_t top[4][3][2];                // per band, the three largest wave totals (value, wave)
+  __shared__ int32_t red[kBalanceThreads / 64];
+  const int t = threadIdx.x;
+  const int64_t grp = blockIdx.x;
+  const int64_t b = grp * W * per;
+  if (b >= nr || per > kSearchRows) return;
+  const int P = (int)per;
+  const int M = (int)min((int64_t)W * per, nr - b);
+  for (int p = t; p < M; p += kBalanceThreads) {
+    const int32_t r = order[b + p];
+    row[p] = r;
+    for (int q = 0; q < K; ++q)
+      cnt[q][p] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
+  }
+  __syncthreads();
+  auto rows_of = [&](int w) { return max(0, min(P, M - w * P)); };
+  // rounds of wave w's slot j in band q with the row at position `out` replaced by the row at `in` (out = -1: none)
+  auto rounds = [&](int w, int j, int q, int out, int in) {
+    const int r = min(8, rows_of(w) - 8 * j);
+    if (r <= 0) return 0;
+    const int base = w * P + 8 * j;
+    return slot_band_rounds([&](int i) { return cnt[q][base + i == out ? in : base + i]; }, r);
+  };
+  for (int x = t; x < W * (kSearchRows / 8) * 4; x += kBalanceThreads) {
+    const int w = x / 32, j = (x / 4) % 8, q = x % 4;
+    sr[w][j][q] = q < K ? rounds(w, j, q, -1, 0) : 0;
+  }
+  __syncthreads();
+  if (t < W * 4) {
+    int sum = 0;
+    for (int j = 0; j < kSearchRows / 8; ++j) sum += sr[t / 4][j][t % 4];
+    tot[t / 4][t % 4] = sum;
+  }
+  __syncthreads();
+  auto refresh_top = [&]() {
+    if (t < K) {
+      int v[3] = {-1, -1, -1}, id[3] = {-1, -1, -1};
+      for (int w = 0; w < W; ++w) {
+        const int x = tot[w][t];
+        if (x > v[0]) { v[2] = v[1]; id[2] = id[1]; v[1] = v[0]; id[1] = id[0]; v[0] = x; id[0] = w; }
+        else if (x > v[1]) { v[2] = v[1]; id[2] = id[1]; v[1] = x; id[1] = w; }
+        else if (x > v[2]) { v[2] = x; id[2] = w; }
+      }
+      for (int e = 0; e < 3; ++e) { top[t][e][0] = v[e]; top[t][e][1] = id[e]; }
+    }
+  };
+  refresh_top();
+  __syncthreads();
+  uint32_t state = (2463534242u ^ (uint32_t)(grp * 2654435761u) ^ (uint32_t)((t + 1) * 2246822507u)) | 1u;
+  auto next = [&]() {
+    state ^= state << 13;
+    state ^= state >> 17;
+    state ^= state << 5;
+    return state;
+  };
+  for (int step = 0; step < kBalanceSteps; ++step) {
+    const int p1 = (int)(next() % (uint32_t)M), p2 = (int)(next() % (uint32_t)M);
+    const int w1 = p1 / P, j1 = (p1 % P) >> 3, w2 = p2 / P, j2 = (p2 % P) >> 3;
+    int a1[4] = {0, 0, 0, 0}, a2[4] = {0, 0, 0, 0};
+    int d = 1 << 20;
+    if (w1 != w2 || j1 != j2) {
+      d = 0;
+      for (int q = 0; q < K; ++q) {
+        a1[q] = rounds(w1, j1, q, p1, p2);
+        a2[q] = rounds(w2, j2, q, p2, p1);
+        int t1, t2;
+        if (w1 == w2) {
+          t1 = t2 = tot[w1][q] - sr[w1][j1][q] - sr[w1][j2][q] + a1[q] + a2[q];
+        } else {
+          t1 = tot[w1][q] - sr[w1][j1][q] + a1[q];
+          t2 = tot[w2][q] - sr[w2][j2][q] + a2[q];
+        }
+        int other = 0;
+        for (int e = 0; e < 3; ++e)
+          if (top[q][e][1] != w1 && top[q][e][1] != w2) { other = max(top[q][e][0], 0); break; }
+        const int newmax = max(other, max(t1, t2));
+        const int dsum = w1 == w2 ? t1 - tot[w1][q] : (t1 - tot[w1][q]) + (t2 - tot[w2][q]);
+        d += W * (newmax - top[q][0][0]) + dsum;
+      }
+    }
+    int key = ((d + (1 << 20)) << 8) | t;   // the lowest change, then the lowest thread
+    for (int o = 32; o > 0; o >>= 1) key = min(key, __shfl_xor(key, o));
+    if ((t & 63) == 0) red[t >> 6] = key;
+    __syncthreads();
+    int best = red[0];
+    for (int x = 1; x < kBalanceThreads / 64; ++x) best = min(best, red[x]);
+    if ((best & 255) == t && d <= 0) {
+      const int32_t rr = row[p1];
+      row[p1] = row[p2];
+      row[p2] = rr;
+      for (int q = 0; q < K; ++q) {
+        const uint16_t cc = cnt[q][p1];
+        cnt[q][p1] = cnt[q][p2];
+        cnt[q][p2] = cc;
+        if (w1 == w2) {
+          tot[w1][q] += a1[q] - sr[w1][j1][q] + a2[q] - sr[w1][j2][q];
+        } else {
+          tot[w1][q] += a1[q] - sr[w1][j1][q];
+          tot[w2][q] += a2[q] - sr[w2][j2][q];
+        }
+        sr[w1][j1][q] = a1[q];
+        sr[w2][j2][q] = a2[q];
+      }
+    }
+    __syncthreads();
+    refresh_top();
+    __syncthreads();
+  }
+  for (int p = t; p < M; p += kBalanceThreads) order[b + p] = row[p];
+}
+
 __global__ void k_zero_int(int32_t *p) { *p = 0; }
 
 // The longest row of a CSR matrix (rows: nr, into *out, which starts at 0).
@@ -1044,8 +1173,11 @@ inline void build_sweep_order(const int32_t *rowptr, const int32_t *band_off, in
   const int64_t per = (nr + waves - 1) / waves;   // launch_swept's rows_per_wave
   const int64_t segs = (nr + per - 1) / per;
   hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, rowptr, nr, per, order);
-  if (per <= kSearchRows)
+  if (per <= kSearchRows) {
     hipLaunchKernelGGL(k_sweep_order_search, dim3((unsigned)segs), dim3(64), 0, st, band_off, K, nr, per, order);
+    hipLaunchKernelGGL(k_sweep_order_balance, dim3((unsigned)((segs + 15) / 16)), dim3(kBalanceThreads), 0, st,
+                       band_off, K, nr, per, order);
+  }
 }
 
 template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false, bool PIPE = false>

@@ -520,14 +520,100 @@ def _slot_rounds_numpy(c, m, j):
     return ((mx + 3) & ~3).sum(axis=1)
 
 
-def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, segments=None):
+def _balance_numpy(order, cnt, per, groups, steps):
+    """The plan's balance search restated for the given groups of 16 segments: cost = per band, 16 x the largest of
+    the group's wave totals plus their sum; at each step each of 256 threads (xorshift32 per group and thread) draws
+    two positions of the group, scores the change a swap of their rows would make (the other waves' largest total
+    from the band's three largest), and the lowest score (ties: lowest thread) is made if it adds no cost."""
+    nr, bands = cnt.shape
+    W, L = 16, 256
+    order = order.copy()
+    G = len(groups)
+    starts = np.asarray(groups) * W * per
+    M = np.minimum(W * per, nr - starts)                                             # rows of each group
+    pos = np.arange(W * per)
+    rows = np.where(pos[None, :] < M[:, None], order[np.minimum(starts[:, None] + pos[None, :], nr - 1)], -1)
+    c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)   # (G, bands, W * per)
+    rows_of = np.clip(M[:, None] - np.arange(W)[None, :] * per, 0, per)             # (G, W)
+    gix = np.arange(G)[:, None, None, None]
+    bix = np.arange(bands)[None, None, :, None]
+    def rounds(w, j, out, inn):   # (G, X) -> (G, X, bands): rounds of wave w's slot j, position out holding inn
+        r = np.clip(np.take_along_axis(rows_of, w, 1) - 8 * j, 0, 8)
+        lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))
+        p = w[..., None] * per + 8 * j[..., None] + np.arange(8)
+        src = np.where(p == out[..., None], inn[..., None], np.minimum(p, W * per - 1))
+        vals = c[gix, bix, src[:, :, None, :]]
+        share = (vals + (1 << lf)[..., None, None] - 1) >> lf[..., None, None]
+        share = np.where((np.arange(8) < r[..., None])[:, :, None, :], share, 0)
+        return np.where(r[..., None] > 0, (share.max(axis=3) + 3) & ~3, 0)
+    ww, jj = np.meshgrid(np.arange(W), np.arange(8), indexing="ij")
+    ww = np.tile(ww.reshape(1, -1), (G, 1)); jj = np.tile(jj.reshape(1, -1), (G, 1))
+    sr = rounds(ww, jj, np.full_like(ww, -1), np.zeros_like(ww)).reshape(G, W, 8, bands)
+    tot = sr.sum(axis=2)                                                             # (G, W, bands)
+    def top3():
+        o = np.lexsort((np.broadcast_to(np.arange(W)[None, :, None], tot.shape), -tot), axis=1)[:, :3, :]
+        return np.take_along_axis(tot, o, 1), o                                      # (G, 3, bands)
+    tv, ti = top3()
+    low = np.uint64(0xFFFFFFFF)
+    gg = np.asarray(groups, dtype=np.uint64)[:, None]
+    tt = np.arange(L, dtype=np.uint64)[None, :]
+    state = ((np.uint64(2463534242) ^ ((gg * np.uint64(2654435761)) & low) ^ (((tt + np.uint64(1)) * np.uint64(2246822507)) & low))
+             | np.uint64(1)).astype(np.uint32)
+    def nxt():
+        nonlocal state
+        state = state ^ (state << np.uint32(13))
+        state = state ^ (state >> np.uint32(17))
+        state = state ^ (state << np.uint32(5))
+        return state
+    ag = np.arange(G)
+    for _ in range(steps):
+        p1 = (nxt() % M[:, None].astype(np.uint32)).astype(np.int64)
+        p2 = (nxt() % M[:, None].astype(np.uint32)).astype(np.int64)
+        w1, j1, w2, j2 = p1 // per, (p1 % per) >> 3, p2 // per, (p2 % per) >> 3
+        a1, a2 = rounds(w1, j1, p1, p2), rounds(w2, j2, p2, p1)                      # (G, L, bands)
+        s1 = sr[ag[:, None], w1, j1]; s2 = sr[ag[:, None], w2, j2]
+        T1, T2 = tot[ag[:, None], w1], tot[ag[:, None], w2]
+        same = (w1 == w2)[..., None]
+        s12 = sr[ag[:, None], w1, j2]
+        t1 = np.where(same, T1 - s1 - s12 + a1 + a2, T1 - s1 + a1)
+        t2 = np.where(same, t1, T2 - s2 + a2)
+        ok = (ti[:, None, :, :] != w1[:, :, None, None]) & (ti[:, None, :, :] != w2[:, :, None, None])   # (G, L, 3, bands)
+        first = np.argmax(ok, axis=2)
+        other = np.maximum(np.take_along_axis(np.broadcast_to(tv[:, None], ok.shape), first[:, :, None, :], 2)[:, :, 0, :], 0)
+        newmax = np.maximum(other, np.maximum(t1, t2))
+        dsum = np.where(same, t1 - T1, (t1 - T1) + (t2 - T2))
+        d = (W * (newmax - tv[:, None, 0, :]) + dsum).sum(axis=2)
+        d = np.where((w1 != w2) | (j1 != j2), d, 1 << 20)
+        win = np.argmin(((d + (1 << 20)) << 8) | np.arange(L)[None, :], axis=1)
+        apply = d[ag, win] <= 0
+        for g in np.nonzero(apply)[0]:
+            x = win[g]
+            q1, q2 = p1[g, x], p2[g, x]
+            rows[g, [q1, q2]] = rows[g, [q2, q1]]
+            c[g][:, [q1, q2]] = c[g][:, [q2, q1]]
+            v1, v2, k1, k2 = w1[g, x], w2[g, x], j1[g, x], j2[g, x]
+            if v1 == v2:
+                tot[g, v1] += a1[g, x] - sr[g, v1, k1] + a2[g, x] - sr[g, v1, k2]
+            else:
+                tot[g, v1] += a1[g, x] - sr[g, v1, k1]
+                tot[g, v2] += a2[g, x] - sr[g, v2, k2]
+            sr[g, v1, k1] = a1[g, x]
+            sr[g, v2, k2] = a2[g, x]
+        tv, ti = top3()
+    for g in range(G):
+        order[starts[g]:starts[g] + M[g]] = rows[g, :M[g]]
+    return order
+
+
+def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_steps=600, groups=None):
     """The swept step's plan tables restated: off[i][b] = row i's start plus its non-zeros with a column in the
     bands before b (band of column c: c * bands // prev_rows), off[i][bands] = its end.  The order lists each
     consecutive segment of `per` rows longest first (ties by row index), then, in segments of at most 64 rows, the
     plan's wave-parallel local search: at each of `steps` steps, each of 64 lanes (xorshift32 per segment and lane)
     draws two positions; a pair in different slots scores the change in the two slots' rounds its swap would make;
-    the lowest score (ties: lowest lane) is applied when it adds no rounds.  Segments are independent: `segments`
-    (indices) limits the search to those, the others keep the sort."""
+    the lowest score (ties: lowest lane) is applied when it adds no rounds.  Then each group of 16 segments (the
+    waves of one workgroup) runs the plan's balance search over `balance_steps` steps (_balance_numpy).  Groups are
+    independent: `groups` (indices) limits both searches to those, the others keep the sort."""
     nr = len(rowptr) - 1
     lens = np.diff(rowptr)
     band = cols.astype(np.int64) * bands // prev_rows
@@ -543,7 +629,9 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, segments
     if per > 64 or steps == 0:
         return off, order
     total_seg = -(-nr // per)
-    segs = np.arange(total_seg) if segments is None else np.asarray(segments)
+    n_groups = -(-total_seg // 16)
+    groups = np.arange(n_groups) if groups is None else np.asarray(groups)
+    segs = np.concatenate([np.arange(16 * g, min(16 * g + 16, total_seg)) for g in groups])
     nseg = len(segs)
     m = np.minimum(per, nr - segs * per)
     pad = np.full(total_seg * per, -1, np.int64)
@@ -594,15 +682,20 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, segments
         cost[a, sk[ar, w][apply]] = ck[ar, w][apply]
     out = pad.reshape(total_seg, per).copy()
     out[segs] = rows
-    return off, out.reshape(-1)[:nr]
+    order = out.reshape(-1)[:nr]
+    if balance_steps:
+        order = _balance_numpy(order, cnt, per, groups, balance_steps)
+    return off, order
 
 
 def test_sweep_band_table_order_and_rule_match_numpy():
-    """The plan-time work of a swept step (k_band_off, the order of k_sweep_order and k_sweep_order_search, and the
+    """The plan-time work of a swept step (k_band_off, the order of k_sweep_order, k_sweep_order_search and
+    k_sweep_order_balance, and the
     suitability rule of sweep_suits, shared by the plan and the probe library's flyprobe_band_table) against a numpy
     restatement, bit for bit, on random CSR matrices of 70,000 rows (18 rows per wave: slots of 8, 8 and 2): a
     plain one sweeps; one with a hub row (longer than 4 x the mean + 64) and one over 32,768 source rows or fewer do
-    not.  The search leaves every wave its own rows and never adds rounds."""
+    not.  The searches (k_sweep_order_search within each wave, k_sweep_order_balance across the 16 waves of a
+    workgroup) leave each workgroup its rows and each wave its number of rows."""
     import ctypes
     probe = ctypes.CDLL(os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so"))
     probe.flyprobe_last_error.restype = ctypes.c_char_p
@@ -632,32 +725,39 @@ def test_sweep_band_table_order_and_rule_match_numpy():
             torch.cuda.synchronize()
             per = -(-nr // (16 * cus))
             nseg = -(-nr // per)
-            check = np.r_[0:160, nseg - 4:nseg]      # the search restated for these segments (they are independent)
+            ngrp = -(-nseg // 16)
+            check = np.r_[0:6, ngrp - 1]      # the searches restated for these groups of 16 waves (independent)
             off, order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200 if want_swept else 0,
-                                             segments=check)
+                                             groups=check)
             got = d_order.cpu().numpy()
             print(f"{label}, {bands} bands: swept {swept.value}", flush=True)
             assert swept.value == want_swept, (label, bands, swept.value)
             assert np.array_equal(d_off.cpu().numpy(), off), (label, bands)
             if not want_swept:
                 continue
-            sel = np.concatenate([np.arange(g * per, min((g + 1) * per, nr)) for g in check])
+            sel = np.concatenate([np.arange(16 * g * per, min(16 * (g + 1) * per, nr)) for g in check])
             assert np.array_equal(got[sel], order[sel]), (label, bands)
-            # each wave keeps its rows, and the search issues no more rounds than longest first
-            _, sorted_order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=0)
-            for b0 in range(0, nr, per):
-                assert np.array_equal(np.sort(got[b0:b0 + per]), np.arange(b0, min(b0 + per, nr)))
+            # each group of 16 waves keeps its rows; on this fixed data the searches lower the workgroups' cost
+            _, sorted_order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=0, balance_steps=0)
+            for g0 in range(0, nr, 16 * per):
+                assert np.array_equal(np.sort(got[g0:g0 + 16 * per]), np.arange(g0, min(g0 + 16 * per, nr)))
             cnt = np.stack([off[:, q + 1] - off[:, q] for q in range(bands)], axis=1)
-            def total(o):
-                nseg = -(-nr // per)
+            def cost(o):   # (rounds, barrier-bound rounds: per workgroup and band the largest wave's)
                 m = np.minimum(per, nr - np.arange(nseg) * per)
                 pad = np.full(nseg * per, -1, np.int64)
                 pad[:nr] = o
                 rows = pad.reshape(nseg, per)
                 c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)
-                return sum(int(_slot_rounds_numpy(c, m, np.full(nseg, j)).sum()) for j in range(-(-per // 8)))
-            assert total(got) <= total(sorted_order), (label, bands)
-            print(f"  rounds: longest first {total(sorted_order)}, searched {total(got)}", flush=True)
+                per_wave = np.zeros((nseg, bands), np.int64)
+                for j in range(-(-per // 8)):
+                    for q in range(bands):
+                        per_wave[:, q] += _slot_rounds_numpy(c[:, q:q + 1, :], m, np.full(nseg, j))
+                padw = np.zeros((ngrp * 16, bands), np.int64)
+                padw[:nseg] = per_wave
+                return int(per_wave.sum()), int(padw.reshape(ngrp, 16, bands).max(axis=1).sum())
+            before, after = cost(sorted_order), cost(got)
+            print(f"  rounds, barrier-bound rounds: longest first {before}, searched {after}", flush=True)
+            assert after[0] < before[0] and after[1] < before[1], (label, bands, before, after)
 
 
 def test_full_scale_b1120_deviation_agrees_with_float32(full_net):
