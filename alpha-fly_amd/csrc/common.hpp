@@ -175,7 +175,7 @@ struct Tuning {
   int download_blocks = 0;  // workgroups of fly_evaluator_download when the call passes 0, 0 = automatic
   int swept = 0;        // long-row steps of half states as a banded sweep: 0 automatic, -1 never
   int sweep_bands = 0;  // source bands of a swept step (3 or 4), read when a plan is created; 0 = automatic
-  int sweep_order = 0;  // swept waves take their rows longest first: 0 yes, -1 in index order
+  int sweep_order = 0;  // swept waves take their rows in the plan's searched order: 0 yes, -1 in index order
   int sweep_paired = 0;  // swept waves walk two rows per pass: 1 always, -1 never, 0 for float32 states
   int sweep_slots = 0;   // swept passes of 3 slots: 3 always, 0 when a wave owns 24 rows or fewer (else 6)
   int sweep_pipe = 0;    // swept gathers of the next four rounds in flight: 0 with 3 slots, 1 also 6, -1 never

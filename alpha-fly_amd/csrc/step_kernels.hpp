@@ -890,15 +890,17 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // A long-row step as a sweep of the source rows in K bands, with each row's sums held in registers across it.
 // One workgroup of 16 waves per CU, all resident at once: wave w owns rows_per_wave consecutive positions of the
 // sweep order (slot j of lane group g: position w * rows_per_wave + 8 j + g, in passes of 8 * SLOTS) for every
-// chunk of columns.  The order (sweep_rows) sorts each wave's own rows longest first, so a slot's 8 rows are of like
-// length while every wave keeps the same share of the work.  For each
+// chunk of columns.  The order (sweep_rows, build_sweep_order) gives a slot rows of like band counts and keeps each
+// band's slowest wave close to the others, while every wave keeps the same number of rows.  For each
 // chunk a wave gathers band 0 of all its rows, then band 1, and so on, and the workgroup's waves meet at a barrier
 // after each band: the CU's waves then draw from one band of the source rows at a time, so one XCD's L2 holds the
 // lines of one band instead of the whole chunk.  (Without the barrier, issue priority lets the oldest waves run
 // ahead and the working set grows.)  band_off (nrows, K + 1): row i's non-zeros of band b are
 // colval[band_off[i][b] .. band_off[i][b+1]).  Lane groups of 8 lanes x 16 bytes gather one 128-byte line each; a
-// slot's rounds run to the longest of the wave's 8 rows in that slot and band, the shorter rows' extra gathers at
-// an offset past the buffer (zeros, no memory access).  REPLAY as for the other step kernels.
+// slot's rounds run to the longest of the wave's 8 rows in that slot and band, the shorter rows' extra gathers from
+// the row past the buffer (zeros, no memory access); a slot of 4 rows or fewer spreads each row over several lane
+// groups.  PIPE keeps the next four rounds' gathers in flight during the sums.  REPLAY as for the other step
+// kernels.
 template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, bool PAIRED = false,
           bool PIPE = false>
 __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, U> a) {

@@ -399,7 +399,7 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * workgroups a CU runs at once (0 = none); "download_blocks": workgroups of fly_evaluator_download when its call
  * passes 0 (0 = 16); "swept": -1 keeps the long-row steps on the grouped kernel instead of the banded sweep (0 =
  * automatic); "sweep_bands": source bands of the sweep, 3 or 4 (0 = 4), read when a plan is created;
- * "sweep_order": -1 lets the swept waves take their rows in index order instead of longest first (0);
+ * "sweep_order": -1 lets the swept waves take their rows in index order instead of the plan's searched order (0);
  * "sweep_paired": 1 makes every swept wave walk two rows per pass, -1 one, 0 two for float32 states only;
  * "sweep_slots": 3 makes swept waves take their rows in passes of 3 slots (0: 6 when a wave owns over 24 rows);
  * "sweep_pipe": the next four rounds' gathers in flight during the sums, 0 in passes of 3 slots, 1 also of 6, -1
