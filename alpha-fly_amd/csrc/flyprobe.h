@@ -37,12 +37,12 @@ int flyprobe_set_tuning(const char *key, int64_t value);
  * pair loads and gathers, chosen by the same rule from nrows, nnz and the layout) with the FMAs replaced by an
  * XOR fold and no row constants, input, carried state, cross-lane sums or stores.  rowptr (nrows+1) and pairs
  * (nnz records) are A_t; xprev (prev_rows, ldx) the previous state, __half if state_f16 else float; batch
- * columns.  band_off, order, bands and positions (from flyprobe_band_table where it reports a sweep, else NULL,
- * NULL, 0, 0): the replay of a swept step is the swept kernel's.  sink: at least 1 KiB, written only if the folded bits hit one value. */
+ * columns.  band_off, order and bands (from flyprobe_band_table where it reports a sweep, else NULL, NULL, 0):
+ * the replay of a swept step is the swept kernel's.  sink: at least 1 KiB, written only if the folded bits hit one value. */
 int flyprobe_replay_step(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
                          const void *xprev_dev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                         const int32_t *band_off_dev, const int32_t *order_dev, int32_t bands, int32_t positions,
-                         void *sink_dev, void *stream);
+                         const int32_t *band_off_dev, const int32_t *order_dev, int32_t bands, void *sink_dev,
+                         void *stream);
 
 /* params (nrows 32-byte row records) with zero constants and the given prev (position in R_{t-1}, -1: not carried)
  * and usrc (input row, -1: none), as fly_cone_step exports them: the row reads of a replay with I/O. */
@@ -55,8 +55,7 @@ int flyprobe_pack_params(const int32_t *prev_dev, const int32_t *usrc_dev, int64
 int flyprobe_replay_step_io(const int32_t *rowptr_dev, const void *pairs_dev, const void *params_dev, int64_t nrows,
                             int64_t nnz, const void *xprev_dev, int64_t prev_rows, int64_t ldx, const float *u_dev,
                             int64_t n_in, int64_t ldu, void *xout_dev, int64_t batch, int32_t state_f16,
-                            const int32_t *band_off_dev, const int32_t *order_dev, int32_t bands, int32_t positions,
-                            void *stream);
+                            const int32_t *band_off_dev, const int32_t *order_dev, int32_t bands, void *stream);
 
 /* Uniform-random row gathers in the state step's lane layout: n reads of read_bytes (128: 8 rows per wave
  * instruction; 64: 16 rows) at byte offset idx[e] * row_bytes (16 bytes per lane) of base (`bytes` long).

@@ -162,11 +162,10 @@ extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int
 
 extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
                                     const void *xprev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                                    const int32_t *band_off, const int32_t *order, int32_t bands, int32_t positions,
-                                    void *sink, void *stream) {
+                                    const int32_t *band_off, const int32_t *order, int32_t bands, void *sink,
+                                    void *stream) {
   return probe_guard([&] {
     FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
-    FLY_REQUIRE(positions >= 0 && positions <= 4096, "positions out of range");
     FLY_REQUIRE(rowptr && pairs && xprev && sink, "null argument");
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
@@ -186,7 +185,6 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
       a.band_off = band_off;
       a.sweep_rows = band_off ? order : nullptr;
-      a.sweep_positions = band_off && order ? positions : 0;
       a.sweep_bands = bands;
       a.sweep_paired = g_sweep.paired;
       a.sweep_slots = g_sweep.slots;
@@ -216,11 +214,9 @@ extern "C" int flyprobe_pack_params(const int32_t *prev, const int32_t *usrc, in
 extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs, const void *params, int64_t nrows,
                                        int64_t nnz, const void *xprev, int64_t prev_rows, int64_t ldx, const float *u,
                                        int64_t n_in, int64_t ldu, void *xout, int64_t batch, int32_t state_f16,
-                                       const int32_t *band_off, const int32_t *order, int32_t bands,
-                                       int32_t positions, void *stream) {
+                                       const int32_t *band_off, const int32_t *order, int32_t bands, void *stream) {
   return probe_guard([&] {
     FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
-    FLY_REQUIRE(positions >= 0 && positions <= 4096, "positions out of range");
     FLY_REQUIRE(rowptr && pairs && params && xprev && xout, "null argument");
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
@@ -243,7 +239,6 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
       a.band_off = band_off;
       a.sweep_rows = band_off ? order : nullptr;
-      a.sweep_positions = band_off && order ? positions : 0;
       a.sweep_bands = bands;
       a.sweep_paired = g_sweep.paired;
       a.sweep_slots = g_sweep.slots;

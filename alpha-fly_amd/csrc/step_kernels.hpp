@@ -90,8 +90,6 @@ struct StepArgs {
   const int32_t *band_off; // swept steps: (nrows, bands + 1) band boundaries in colval, or null
   const int32_t *sweep_rows; // swept steps: the rows in the order the waves take them, or null (index order)
   int32_t rows_per_wave;   // swept steps: consecutive positions of that order each wave owns (set by launch_swept)
-  int32_t sweep_positions; // swept steps: positions of sweep_rows per wave when the order is laid out per wave
-                           // (-1 entries: no row), or 0: the rows split evenly between the waves
   int32_t sweep_bands;     // swept steps: bands of band_off (3 or 4)
   int32_t sweep_paired;    // swept steps: two rows per pass (1), one (-1), by the state type (0)
   int32_t sweep_slots;     // swept steps: 3 forces passes of 3 slots (0: 6 slots when a wave owns over 24 rows)
@@ -916,8 +914,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
   // 2^24, so its 24-bit product with row_bytes is exact)
   const uint32_t past_row = a.xbytes / row_bytes;
   const int R = a.rows_per_wave;
-  // positions of the order: R per wave when it is laid out per wave, else one per row
-  const uint32_t npos = a.sweep_positions > 0 ? (uint32_t)R * 16u * gridDim.x : (uint32_t)a.nrows;
+  const uint32_t npos = (uint32_t)a.nrows;   // positions of the order: one per row
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
   // position p of the sweep order holds row sweep_rows[p] (-1: none; p itself without an order)
   auto row_at = [&](uint32_t p) {
@@ -1204,10 +1201,7 @@ void launch_swept_shape(const StepArgs<S, U> &a, unsigned grid, hipStream_t st) 
 template <typename S, typename U, int REPLAY>
 void launch_swept(StepArgs<S, U> a, hipStream_t st) {
   const unsigned grid = (unsigned)cu_count();
-  FLY_REQUIRE(a.sweep_positions == 0 || (a.sweep_rows && a.sweep_positions > 0),
-              "a per-wave sweep layout needs its order");
-  a.rows_per_wave = a.sweep_positions > 0 ? a.sweep_positions
-                                          : (int32_t)((a.nrows + 16 * (int64_t)grid - 1) / (16 * (int64_t)grid));
+  a.rows_per_wave = (int32_t)((a.nrows + 16 * (int64_t)grid - 1) / (16 * (int64_t)grid));
   const bool few = a.rows_per_wave <= 24 || a.sweep_slots == 3;
   switch (a.sweep_bands) {
     case 3:

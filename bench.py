@@ -261,10 +261,10 @@ def _probe_lib():
     lib.flyprobe_last_error.restype, lib.flyprobe_last_error.argtypes = ctypes.c_char_p, []
     for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
                        ("flyprobe_band_table", [p, p, i64, i64, i64, i32, p, p, p, p]),
-                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p, i32, i32, p, p]),
+                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p, i32, p, p]),
                        ("flyprobe_pack_params", [p, p, i64, p, p]),
                        ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, p,
-                                                    i32, i32, p]),
+                                                    i32, p]),
                        ("flyprobe_random_gather", [p, i64, i64, i64, p, i64, p, p]),
                        ("flyprobe_set_tuning", [ctypes.c_char_p, i64])):
         fn = getattr(lib, name)
@@ -340,12 +340,11 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
                                                       band_off.data_ptr(), order.data_ptr(), ctypes.byref(swept), st),
                      "flyprobe_band_table")
         band_ptr, order_ptr = (band_off.data_ptr(), order.data_ptr()) if swept.value else (None, None)
-        positions = 0
 
         def once():
             _probe_check(probe, probe.flyprobe_replay_step(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz,
                                                            xprev.data_ptr(), prev_rows, ld, batch, int(state_f16),
-                                                           band_ptr, order_ptr, bands, positions, sink.data_ptr(), st),
+                                                           band_ptr, order_ptr, bands, sink.data_ptr(), st),
                          "flyprobe_replay_step")
         row = {"t": t, "rows": nr, "nnz": nnz, "swept": bool(swept.value), "replay_ms": round(_events_ms(once, reps), 4)}
         # with the row I/O: each row's constants, carried state and input drive (float32, as the model forward's
@@ -364,7 +363,7 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
             _probe_check(probe, probe.flyprobe_replay_step_io(rowptr.data_ptr(), pairs.data_ptr(), params.data_ptr(),
                                                               nr, nnz, xprev.data_ptr(), prev_rows, ld, u.data_ptr(),
                                                               n_in, ldu, xout.data_ptr(), batch, int(state_f16),
-                                                              band_ptr, order_ptr, bands, positions, st),
+                                                              band_ptr, order_ptr, bands, st),
                          "flyprobe_replay_step_io")
         row["replay_io_ms"] = round(_events_ms(once_io, reps), 4)
         out.append(row)

@@ -98,7 +98,7 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     i64, p_ = ctypes.c_int64, ctypes.c_void_p
     probe.flyprobe_random_gather.argtypes = [p_, i64, i64, i64, p_, i64, p_, p_]
     i32 = ctypes.c_int32
-    probe.flyprobe_replay_step.argtypes = [p_, p_, i64, i64, p_, i64, i64, i64, i32, p_, p_, i32, i32, p_, p_]
+    probe.flyprobe_replay_step.argtypes = [p_, p_, i64, i64, p_, i64, i64, i64, i32, p_, p_, i32, p_, p_]
     assert probe.flyprobe_random_gather(None, 1024, 128, 128, None, 10, None, None) == 1
     buf = ctypes.create_string_buffer(16)
     p = ctypes.addressof(buf)
@@ -107,20 +107,18 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     assert b"row_bytes" in probe.flyprobe_last_error()
     assert probe.flyprobe_random_gather(p, 1024, 128, 96, p, 10, p, None) == 1
     assert b"read_bytes" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(None, None, 10, 10, None, 10, 64, 64, 1, None, None, 0, 0, None, None) == 1
+    assert probe.flyprobe_replay_step(None, None, 10, 10, None, 10, 64, 64, 1, None, None, 0, None, None) == 1
     assert b"null" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 32, 64, 1, None, None, 0, 0, p, None) == 1
+    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 32, 64, 1, None, None, 0, p, None) == 1
     assert b"layout" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 64, 64, 1, p, p, 5, 0, p, None) == 1
+    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 64, 64, 1, p, p, 5, p, None) == 1
     assert b"bands" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 64, 64, 1, p, p, 4, -8, p, None) == 1
-    assert b"positions" in probe.flyprobe_last_error()
     probe.flyprobe_replay_step_io.argtypes = [p_, p_, p_, i64, i64, p_, i64, i64, p_, i64, i64, p_, i64, i32, p_,
-                                              p_, i32, i32, p_]
-    assert probe.flyprobe_replay_step_io(p, p, None, 10, 10, p, 10, 64, None, 0, 0, p, 64, 1, None, None, 0, 0,
+                                              p_, i32, p_]
+    assert probe.flyprobe_replay_step_io(p, p, None, 10, 10, p, 10, 64, None, 0, 0, p, 64, 1, None, None, 0,
                                          None) == 1
     assert b"null" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step_io(p, p, p, 10, 10, p, 10, 64, p, 5, 32, p, 64, 1, None, None, 0, 0, None) == 1
+    assert probe.flyprobe_replay_step_io(p, p, p, 10, 10, p, 10, 64, p, 5, 32, p, 64, 1, None, None, 0, None) == 1
     assert b"input drive" in probe.flyprobe_last_error()
     probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, p_, p_, p_, p_]
     assert probe.flyprobe_band_table(p, p, 10, 100, 10, 8, p, p, p, None) == 1
