@@ -23,11 +23,12 @@ int flyprobe_pack(const int32_t *col_dev, const float *val_dev, int64_t nnz, voi
 
 /* What the evaluator builds for a step it runs as a banded sweep, from the step matrix (rowptr nrows+1, pairs nnz):
  * per row, where each of `bands` (3 or 4) bands of source rows begins among its non-zeros (band_off, nrows x
- * (bands + 1) int32), and the order in which the swept waves take the rows (order, nrows int32); *swept (host) = 1
- * where the evaluator would sweep this matrix, by the same rule.  Synchronises. */
+ * (bands + 1) int32), and the order in which the swept waves take the rows (order, nrows int32), searched for a
+ * sweep that walks two rows per pass when `paired` (the float32 state's default) or one; *swept (host) = 1 where
+ * the evaluator would sweep this matrix, by the same rule.  Synchronises. */
 int flyprobe_band_table(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
-                        int64_t prev_rows, int32_t bands, int32_t *band_off_dev, int32_t *order_dev, int32_t *swept,
-                        void *stream);
+                        int64_t prev_rows, int32_t bands, int32_t paired, int32_t *band_off_dev, int32_t *order_dev,
+                        int32_t *swept, void *stream);
 
 /* The launch-time choice of the swept kernel that the replays mirror, as fly_set_tuning sets it for the
  * evaluator: "sweep_paired" (1 two rows per pass, -1 one, 0 by the state type).  Other keys are refused. */

@@ -141,6 +141,12 @@ __global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *_
   cbase[j] = (mode == FLY_MODE_F32 && out_src[j] >= 0) ? 0.0f : c;
 }
 
+// Whether a swept step of this state type walks two rows per pass when its waves own over 24 rows (launch_swept's
+// rule, with the sweep_paired tuning as it stands when the plan is created).
+bool sweep_pairs(bool f32_state) {
+  return tuning().sweep_paired > 0 || (tuning().sweep_paired == 0 && f32_state);
+}
+
 }  // namespace
 }  // namespace fly
 
@@ -215,7 +221,8 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
           hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
                              plan->colval[t].p, nr, cone->rows_n[t - 1], plan->sweep_bands, plan->band_off[t].p);
           plan->sweep_rows[t].alloc((size_t)nr);
-          build_sweep_order(plan->rowptr[t].p, plan->band_off[t].p, plan->sweep_bands, nr, plan->sweep_rows[t].p, st);
+          build_sweep_order(plan->rowptr[t].p, plan->band_off[t].p, plan->sweep_bands, nr,
+                            sweep_pairs(mode == FLY_MODE_F32), plan->sweep_rows[t].p, st);
         }
       }
       if (nr) {
@@ -289,7 +296,8 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
       hipLaunchKernelGGL(k_band_off, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
                          plan->colval[0].p, n, n, plan->sweep_bands, plan->band_off[0].p);
       plan->sweep_rows[0].alloc((size_t)n);
-      build_sweep_order(plan->rowptr[0].p, plan->band_off[0].p, plan->sweep_bands, n, plan->sweep_rows[0].p, st);
+      build_sweep_order(plan->rowptr[0].p, plan->band_off[0].p, plan->sweep_bands, n, sweep_pairs(true),
+                        plan->sweep_rows[0].p, st);
     }
     check_launch("full plan");
     FLY_HIP(hipStreamSynchronize(st));

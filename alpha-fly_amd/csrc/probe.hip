@@ -145,8 +145,8 @@ extern "C" int flyprobe_set_tuning(const char *key, int64_t value) {
 }
 
 extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
-                                   int64_t prev_rows, int32_t bands, int32_t *band_off, int32_t *order, int32_t *swept,
-                                   void *stream) {
+                                   int64_t prev_rows, int32_t bands, int32_t paired, int32_t *band_off, int32_t *order,
+                                   int32_t *swept, void *stream) {
   return probe_guard([&] {
     FLY_REQUIRE(rowptr && pairs && band_off && order && swept, "null argument");
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0 && nnz >= 0, "size out of range");
@@ -154,7 +154,7 @@ extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int
     *swept = sweep_suits(rowptr, prev_rows, nrows, nnz, as_stream(stream)) ? 1 : 0;
     hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
                        static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
-    build_sweep_order(rowptr, band_off, bands, nrows, order, as_stream(stream));
+    build_sweep_order(rowptr, band_off, bands, nrows, paired != 0, order, as_stream(stream));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) throw Error{1, std::string("band table launch: ") + hipGetErrorString(e)};
   });

@@ -632,20 +632,32 @@ __device__ inline int slot_band_rounds(C &&c, int r) {
   return (m + 3) & ~3;
 }
 
+// Rounds one unit of a swept wave issues in band q: a slot of 8 positions, or with `paired` two slots walked as one
+// pass, where each lane group walks its two rows (positions g and g + 8) back to back, so the pass runs to the
+// largest pair sum, padded to 4.  c(p): the band count at position p of the unit, of which the first r hold rows.
+template <typename C>
+__device__ inline int unit_band_rounds(C &&c, int r, bool paired) {
+  if (!paired) return slot_band_rounds(c, min(r, 8));
+  int mx = 0;
+  for (int g = 0; g < 8 && g < r; ++g) mx = max(mx, (int)c(g) + (g + 8 < r ? (int)c(g + 8) : 0));
+  return (mx + 3) & ~3;
+}
+
 constexpr int kSearchRows = 64;     // wave segments of at most this many rows are searched (longer keep the sort)
 constexpr int kSearchSteps = 200;   // moves tried per segment
 
 // After k_sweep_order: each wave's rows rearranged between its slots so that a slot's 8 rows have like band
-// counts and fewer of its rounds are padding.  One wave per segment runs a seeded local search.  At each step every
-// lane draws two rows of the segment (xorshift32, seeded by segment and lane) and, if they sit in different slots,
-// the change in the two slots' rounds (summed over the bands, as slot_band_rounds counts them) that swapping them
-// would make; the lowest change wins (ties: the lowest lane) and is made if it adds no rounds, so the search also
-// walks across plateaus.  The wave keeps its rows, so its share of the work is unchanged.
+// counts and fewer of its rounds are padding (with `paired`, units of two slots walked as one pass).  One wave per
+// segment runs a seeded local search.  At each step every lane draws two rows of the segment (xorshift32, seeded by
+// segment and lane) and, if swapping them can change a unit's rounds, the change in the rounds of their units
+// (summed over the bands, as unit_band_rounds counts them); the lowest change wins (ties: the lowest lane) and is
+// made if it adds no rounds, so the search also walks across plateaus.  The wave keeps its rows, so its share of
+// the work is unchanged.
 __global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__restrict__ band_off, int K, int64_t nr,
-                                                           int64_t per, int32_t *__restrict__ order) {
+                                                           int64_t per, int paired, int32_t *__restrict__ order) {
   __shared__ uint16_t cnt[4][kSearchRows];
   __shared__ int32_t row[kSearchRows];
-  __shared__ int32_t cost[kSearchRows / 8];   // rounds of each slot, summed over the bands
+  __shared__ int32_t cost[kSearchRows / 8];   // rounds of each unit, summed over the bands
   const int lane = threadIdx.x;
   const int64_t seg = blockIdx.x;
   const int64_t b = seg * per;
@@ -658,17 +670,21 @@ __global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__rest
       cnt[q][k] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
   }
   __syncthreads();
-  const int slots = (m + 7) / 8;
-  if (slots < 2) return;
-  // rounds of slot j with the row at position `out` replaced by the row at position `in` (out = -1: as it is)
-  auto slot_cost = [&](int j, int out, int in) {
-    const int r = min(8, m - 8 * j);
+  const int U = paired ? 16 : 8;   // positions per unit
+  const int units = (m + U - 1) / U;
+  if (m <= 8) return;              // one slot: nothing to rearrange
+  // rounds of unit u with the rows at positions x and y swapped (x = y = -1: as it is)
+  auto unit_cost = [&](int u, int x, int y) {
+    const int r = min(U, m - U * u);
     int c = 0;
     for (int q = 0; q < K; ++q)
-      c += slot_band_rounds([&](int i) { return cnt[q][8 * j + i == out ? in : 8 * j + i]; }, r);
+      c += unit_band_rounds([&](int i) {
+        const int p = U * u + i;
+        return cnt[q][p == x ? y : (p == y ? x : p)];
+      }, r, paired != 0);
     return c;
   };
-  if (lane < slots) cost[lane] = slot_cost(lane, -1, 0);
+  if (lane < units) cost[lane] = unit_cost(lane, -1, -1);
   __syncthreads();
   uint32_t state = (2463534242u ^ (uint32_t)(seg * 2654435761u) ^ (uint32_t)((lane + 1) * 2246822507u)) | 1u;
   auto next = [&]() {
@@ -679,12 +695,15 @@ __global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__rest
   };
   for (int step = 0; step < kSearchSteps; ++step) {
     const int i = (int)(next() % (uint32_t)m), k = (int)(next() % (uint32_t)m);
-    const int si = i >> 3, sk = k >> 3;
+    const int ui = i / U, uk = k / U;
     int ci = 0, ck = 0, d = 1 << 20;
-    if (si != sk) {
-      ci = slot_cost(si, i, k);
-      ck = slot_cost(sk, k, i);
-      d = ci + ck - cost[si] - cost[sk];
+    if (ui != uk) {
+      ci = unit_cost(ui, i, k);
+      ck = unit_cost(uk, i, k);
+      d = ci + ck - cost[ui] - cost[uk];
+    } else if (paired && (i & 7) != (k & 7)) {   // two lane groups of one pass trade rows
+      ci = ck = unit_cost(ui, i, k);
+      d = ci - cost[ui];
     }
     int key = ((d + (1 << 20)) << 6) | lane;   // the lowest change, then the lowest lane
     for (int o = 32; o > 0; o >>= 1) key = min(key, __shfl_xor(key, o));
@@ -698,8 +717,8 @@ __global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__rest
         cnt[q][i] = cnt[q][k];
         cnt[q][k] = cc;
       }
-      cost[si] = ci;
-      cost[sk] = ck;
+      cost[ui] = ci;
+      cost[uk] = ck;
     }
     __syncthreads();
   }
@@ -717,12 +736,12 @@ constexpr int kBalanceSteps = 600;
 // three largest wave totals of each band, and the lowest change (ties: the lowest thread) is made if it adds no cost.
 // Every wave keeps its number of rows.
 __global__ __launch_bounds__(kBalanceThreads) void k_sweep_order_balance(const int32_t *__restrict__ band_off, int K,
-                                                                         int64_t nr, int64_t per,
+                                                                         int64_t nr, int64_t per, int paired,
                                                                          int32_t *__restrict__ order) {
   constexpr int W = 16;
   __shared__ uint16_t cnt[4][W * kSearchRows];
   __shared__ int32_t row[W * kSearchRows];
-  __shared__ int32_t sr[W][kSearchRows / 8][4];   // rounds of each wave's slot in each band
+  __shared__ int32_t sr[W][kSearchRows / 8][4];   // rounds of each wave's unit (slot, or pair of slots) per band
   __shared__ int32_t tot[W][4];                   // rounds of each wave in each band
   __shared__ int32_t top[4][3][2];                // per band, the three largest wave totals (value, wave)
   __shared__ int32_t red[kBalanceThreads / 64];
@@ -739,17 +758,21 @@ __global__ __launch_bounds__(kBalanceThreads) void k_sweep_order_balance(const i
       cnt[q][p] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
   }
   __syncthreads();
+  const int U = paired ? 16 : 8;   // positions per unit
   auto rows_of = [&](int w) { return max(0, min(P, M - w * P)); };
-  // rounds of wave w's slot j in band q with the row at position `out` replaced by the row at `in` (out = -1: none)
-  auto rounds = [&](int w, int j, int q, int out, int in) {
-    const int r = min(8, rows_of(w) - 8 * j);
+  // rounds of wave w's unit j in band q with the rows at positions x and y swapped (x = y = -1: as it is)
+  auto rounds = [&](int w, int j, int q, int x, int y) {
+    const int r = min(U, rows_of(w) - U * j);
     if (r <= 0) return 0;
-    const int base = w * P + 8 * j;
-    return slot_band_rounds([&](int i) { return cnt[q][base + i == out ? in : base + i]; }, r);
+    const int base = w * P + U * j;
+    return unit_band_rounds([&](int i) {
+      const int p = base + i;
+      return cnt[q][p == x ? y : (p == y ? x : p)];
+    }, r, paired != 0);
   };
   for (int x = t; x < W * (kSearchRows / 8) * 4; x += kBalanceThreads) {
     const int w = x / 32, j = (x / 4) % 8, q = x % 4;
-    sr[w][j][q] = q < K ? rounds(w, j, q, -1, 0) : 0;
+    sr[w][j][q] = q < K ? rounds(w, j, q, -1, -1) : 0;
   }
   __syncthreads();
   if (t < W * 4) {
@@ -781,16 +804,19 @@ __global__ __launch_bounds__(kBalanceThreads) void k_sweep_order_balance(const i
   };
   for (int step = 0; step < kBalanceSteps; ++step) {
     const int p1 = (int)(next() % (uint32_t)M), p2 = (int)(next() % (uint32_t)M);
-    const int w1 = p1 / P, j1 = (p1 % P) >> 3, w2 = p2 / P, j2 = (p2 % P) >> 3;
+    const int w1 = p1 / P, j1 = (p1 % P) / U, w2 = p2 / P, j2 = (p2 % P) / U;
+    const bool same = w1 == w2 && j1 == j2;   // one unit: only two lane groups of a pass trading rows changes it
     int a1[4] = {0, 0, 0, 0}, a2[4] = {0, 0, 0, 0};
     int d = 1 << 20;
-    if (w1 != w2 || j1 != j2) {
+    if (!same || (paired && ((p1 % P) & 7) != ((p2 % P) & 7))) {
       d = 0;
       for (int q = 0; q < K; ++q) {
         a1[q] = rounds(w1, j1, q, p1, p2);
-        a2[q] = rounds(w2, j2, q, p2, p1);
+        a2[q] = same ? a1[q] : rounds(w2, j2, q, p1, p2);
         int t1, t2;
-        if (w1 == w2) {
+        if (same) {
+          t1 = t2 = tot[w1][q] - sr[w1][j1][q] + a1[q];
+        } else if (w1 == w2) {
           t1 = t2 = tot[w1][q] - sr[w1][j1][q] - sr[w1][j2][q] + a1[q] + a2[q];
         } else {
           t1 = tot[w1][q] - sr[w1][j1][q] + a1[q];
@@ -818,7 +844,9 @@ __global__ __launch_bounds__(kBalanceThreads) void k_sweep_order_balance(const i
         const uint16_t cc = cnt[q][p1];
         cnt[q][p1] = cnt[q][p2];
         cnt[q][p2] = cc;
-        if (w1 == w2) {
+        if (same) {
+          tot[w1][q] += a1[q] - sr[w1][j1][q];
+        } else if (w1 == w2) {
           tot[w1][q] += a1[q] - sr[w1][j1][q] + a2[q] - sr[w1][j2][q];
         } else {
           tot[w1][q] += a1[q] - sr[w1][j1][q];
@@ -1164,18 +1192,23 @@ inline int cu_count() {
 }
 
 // The swept waves' order of a step's rows (nr, into `order`): each wave's own rows_per_wave rows, longest first
-// (k_sweep_order), then rearranged between the wave's slots (k_sweep_order_search) from the band table (nr, K + 1).
-inline void build_sweep_order(const int32_t *rowptr, const int32_t *band_off, int K, int64_t nr, int32_t *order,
-                              hipStream_t st) {
+// (k_sweep_order), then rearranged between the wave's slots (k_sweep_order_search) and between the 16 waves of
+// each workgroup (k_sweep_order_balance) from the band table (nr, K + 1).  `paired`: the state is float32 and the
+// sweep walks two rows per pass (sweep_paired), which changes what a slot costs.
+inline void build_sweep_order(const int32_t *rowptr, const int32_t *band_off, int K, int64_t nr, bool paired,
+                              int32_t *order, hipStream_t st) {
   FLY_REQUIRE(nr > 0 && nr < (int64_t)INT32_MAX && (K == 3 || K == 4), "rows or bands out of range");
   const int64_t waves = 16 * (int64_t)cu_count();
   const int64_t per = (nr + waves - 1) / waves;   // launch_swept's rows_per_wave
   const int64_t segs = (nr + per - 1) / per;
   hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, rowptr, nr, per, order);
   if (per <= kSearchRows) {
-    hipLaunchKernelGGL(k_sweep_order_search, dim3((unsigned)segs), dim3(64), 0, st, band_off, K, nr, per, order);
+    // the float32 kernel walks pairs of slots in one pass when a wave owns over 24 rows (launch_swept)
+    const int pair = paired && K == 4 && per > 24 ? 1 : 0;
+    hipLaunchKernelGGL(k_sweep_order_search, dim3((unsigned)segs), dim3(64), 0, st, band_off, K, nr, per, pair,
+                       order);
     hipLaunchKernelGGL(k_sweep_order_balance, dim3((unsigned)((segs + 15) / 16)), dim3(kBalanceThreads), 0, st,
-                       band_off, K, nr, per, order);
+                       band_off, K, nr, per, pair, order);
   }
 }
 

@@ -260,7 +260,7 @@ def _probe_lib():
     p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     lib.flyprobe_last_error.restype, lib.flyprobe_last_error.argtypes = ctypes.c_char_p, []
     for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
-                       ("flyprobe_band_table", [p, p, i64, i64, i64, i32, p, p, p, p]),
+                       ("flyprobe_band_table", [p, p, i64, i64, i64, i32, i32, p, p, p, p]),
                        ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p, i32, p, p]),
                        ("flyprobe_pack_params", [p, p, i64, p, p]),
                        ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, p,
@@ -301,7 +301,7 @@ def _events_ms(fn, reps: int) -> float:
 
 
 def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps: int = 20,
-                   sweep_bands: int = 4) -> list[dict]:
+                   sweep_bands: int = 4, sweep_paired: int = 0) -> list[dict]:
     """Per step with a matrix, the time of the replay of that step's gather stream (flyprobe_replay_step: the
     state step's own kernel, launch shape and wave order over this plan's A_t and a state of this layout, with
     the arithmetic, row inputs and stores taken out), and of the replay that keeps the row reads and stores
@@ -336,8 +336,10 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
         band_off = torch.empty(nr * (bands + 1), dtype=torch.int32, device=dev)
         order = torch.empty(nr, dtype=torch.int32, device=dev)
         swept = ctypes.c_int32(0)
+        paired = int(sweep_paired > 0 or (sweep_paired == 0 and not state_f16))   # the plan's rule for its order
         _probe_check(probe, probe.flyprobe_band_table(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz, prev_rows, bands,
-                                                      band_off.data_ptr(), order.data_ptr(), ctypes.byref(swept), st),
+                                                      paired, band_off.data_ptr(), order.data_ptr(),
+                                                      ctypes.byref(swept), st),
                      "flyprobe_band_table")
         band_ptr, order_ptr = (band_off.data_ptr(), order.data_ptr()) if swept.value else (None, None)
 
@@ -607,7 +609,8 @@ def main() -> int:
         for key in ("sweep_paired", "sweep_slots", "sweep_pipe"):     # the swept kernel's launch-time choices
             if key in tuned:
                 _probe_check(probe, probe.flyprobe_set_tuning(key.encode(), int(tuned[key])), "flyprobe_set_tuning")
-        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev, sweep_bands=bands)
+        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev, sweep_bands=bands,
+                              sweep_paired=int(tuned.get("sweep_paired", 0)))
         for r in rows:
             r["step_ms"] = round(per_step[r["t"]], 4)
             r["replay_over_step"] = round(r["replay_ms"] / r["step_ms"], 4)

@@ -120,8 +120,8 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     assert b"null" in probe.flyprobe_last_error()
     assert probe.flyprobe_replay_step_io(p, p, p, 10, 10, p, 10, 64, p, 5, 32, p, 64, 1, None, None, 0, None) == 1
     assert b"input drive" in probe.flyprobe_last_error()
-    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, p_, p_, p_, p_]
-    assert probe.flyprobe_band_table(p, p, 10, 100, 10, 8, p, p, p, None) == 1
+    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, i32, p_, p_, p_, p_]
+    assert probe.flyprobe_band_table(p, p, 10, 100, 10, 8, 0, p, p, p, None) == 1
     assert b"bands" in probe.flyprobe_last_error()
-    assert probe.flyprobe_band_table(None, p, 10, 100, 10, 4, p, p, p, None) == 1
+    assert probe.flyprobe_band_table(None, p, 10, 100, 10, 4, 0, p, p, p, None) == 1
     assert b"null" in probe.flyprobe_last_error()

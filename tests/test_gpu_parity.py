@@ -506,53 +506,55 @@ def test_full_scale_swept_steps_match_the_grouped_kernel(full_net):
         net.infer_dtype = torch.float16
 
 
-def _slot_rounds_numpy(c, m, j):
-    """Rounds of slot j (positions 8j .. 8j+7 below m) per segment, summed over the bands: the longest share of its
-    rows' band counts (a slot of r <= 4 rows spreads each row over 2, 4 or 8 lane groups), padded to 4 rounds.
-    c: (segments, bands, positions) counts; m, j: (segments,)."""
-    r = np.clip(m - 8 * j, 0, 8)
-    lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))
-    pos = 8 * j[:, None] + np.arange(8)[None, :]                                   # (segments, 8)
-    valid = np.arange(8)[None, :] < r[:, None]
-    vals = np.take_along_axis(c, np.minimum(pos, c.shape[2] - 1)[:, None, :].repeat(c.shape[1], 1), axis=2)
-    share = (vals + (1 << lf)[:, None, None] - 1) >> lf[:, None, None]
-    mx = np.where(valid[:, None, :], share, 0).max(axis=2)
-    return ((mx + 3) & ~3).sum(axis=1)
+def _unit_rounds_numpy(vals, r, paired):
+    """Rounds of swept units summed over the bands, as the plan's searches count them.  vals (..., bands, U): band
+    counts at the unit's positions; r (...): positions holding rows.  A unit is a slot of 8 positions (the longest
+    share of its rows, a slot of r <= 4 rows spreading each over 2, 4 or 8 groups) or, paired, two slots walked as
+    one pass (the largest sum of a lane group's two rows); padded to 4 rounds per band."""
+    U = vals.shape[-1]
+    live = np.arange(U) < r[..., None, None]
+    v = np.where(live, vals, 0)
+    if paired:
+        mx = (v[..., :8] + v[..., 8:]).max(axis=-1)
+    else:
+        lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))[..., None, None]
+        mx = ((v + (1 << lf) - 1) >> lf).max(axis=-1)
+    return ((mx + 3) & ~3).sum(axis=-1)
 
 
-def _balance_numpy(order, cnt, per, groups, steps):
+def _balance_numpy(order, cnt, per, groups, steps, paired=False):
     """The plan's balance search restated for the given groups of 16 segments: cost = per band, 16 x the largest of
     the group's wave totals plus their sum; at each step each of 256 threads (xorshift32 per group and thread) draws
     two positions of the group, scores the change a swap of their rows would make (the other waves' largest total
     from the band's three largest), and the lowest score (ties: lowest thread) is made if it adds no cost."""
     nr, bands = cnt.shape
     W, L = 16, 256
+    U = 16 if paired else 8
     order = order.copy()
     G = len(groups)
     starts = np.asarray(groups) * W * per
-    M = np.minimum(W * per, nr - starts)                                             # rows of each group
+    M = np.minimum(W * per, nr - starts)
     pos = np.arange(W * per)
     rows = np.where(pos[None, :] < M[:, None], order[np.minimum(starts[:, None] + pos[None, :], nr - 1)], -1)
     c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)   # (G, bands, W * per)
-    rows_of = np.clip(M[:, None] - np.arange(W)[None, :] * per, 0, per)             # (G, W)
+    rows_of = np.clip(M[:, None] - np.arange(W)[None, :] * per, 0, per)
     gix = np.arange(G)[:, None, None, None]
     bix = np.arange(bands)[None, None, :, None]
-    def rounds(w, j, out, inn):   # (G, X) -> (G, X, bands): rounds of wave w's slot j, position out holding inn
-        r = np.clip(np.take_along_axis(rows_of, w, 1) - 8 * j, 0, 8)
-        lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))
-        p = w[..., None] * per + 8 * j[..., None] + np.arange(8)
-        src = np.where(p == out[..., None], inn[..., None], np.minimum(p, W * per - 1))
-        vals = c[gix, bix, src[:, :, None, :]]
-        share = (vals + (1 << lf)[..., None, None] - 1) >> lf[..., None, None]
-        share = np.where((np.arange(8) < r[..., None])[:, :, None, :], share, 0)
-        return np.where(r[..., None] > 0, (share.max(axis=3) + 3) & ~3, 0)
-    ww, jj = np.meshgrid(np.arange(W), np.arange(8), indexing="ij")
+    def rounds(w, j, x, y):   # (G, X) -> (G, X, bands) per band rounds of wave w's unit j with rows x, y swapped
+        r = np.clip(np.take_along_axis(rows_of, w, 1) - U * j, 0, U)
+        p = w[..., None] * per + U * j[..., None] + np.arange(U)
+        src = np.where(p == x[..., None], y[..., None], np.where(p == y[..., None], x[..., None], p))
+        vals = c[gix, bix, np.minimum(src, W * per - 1)[:, :, None, :]]                   # (G, X, bands, U)
+        out = np.stack([_unit_rounds_numpy(vals[:, :, q:q + 1, :], r, paired) for q in range(bands)], axis=-1)
+        return np.where(r[..., None] > 0, out, 0)
+    nu = 64 // U
+    ww, jj = np.meshgrid(np.arange(W), np.arange(nu), indexing="ij")
     ww = np.tile(ww.reshape(1, -1), (G, 1)); jj = np.tile(jj.reshape(1, -1), (G, 1))
-    sr = rounds(ww, jj, np.full_like(ww, -1), np.zeros_like(ww)).reshape(G, W, 8, bands)
-    tot = sr.sum(axis=2)                                                             # (G, W, bands)
+    sr = rounds(ww, jj, np.full_like(ww, -1), np.full_like(ww, -1)).reshape(G, W, nu, bands)
+    tot = sr.sum(axis=2)
     def top3():
         o = np.lexsort((np.broadcast_to(np.arange(W)[None, :, None], tot.shape), -tot), axis=1)[:, :3, :]
-        return np.take_along_axis(tot, o, 1), o                                      # (G, 3, bands)
+        return np.take_along_axis(tot, o, 1), o
     tv, ti = top3()
     low = np.uint64(0xFFFFFFFF)
     gg = np.asarray(groups, dtype=np.uint64)[:, None]
@@ -569,30 +571,33 @@ def _balance_numpy(order, cnt, per, groups, steps):
     for _ in range(steps):
         p1 = (nxt() % M[:, None].astype(np.uint32)).astype(np.int64)
         p2 = (nxt() % M[:, None].astype(np.uint32)).astype(np.int64)
-        w1, j1, w2, j2 = p1 // per, (p1 % per) >> 3, p2 // per, (p2 % per) >> 3
-        a1, a2 = rounds(w1, j1, p1, p2), rounds(w2, j2, p2, p1)                      # (G, L, bands)
-        s1 = sr[ag[:, None], w1, j1]; s2 = sr[ag[:, None], w2, j2]
+        w1, j1, w2, j2 = p1 // per, (p1 % per) // U, p2 // per, (p2 % per) // U
+        same = (w1 == w2) & (j1 == j2)
+        valid = ~same | (paired & (((p1 % per) & 7) != ((p2 % per) & 7)))
+        a1 = rounds(w1, j1, p1, p2)
+        a2 = np.where(same[..., None], a1, rounds(w2, j2, p1, p2))
+        s1, s2, s12 = sr[ag[:, None], w1, j1], sr[ag[:, None], w2, j2], sr[ag[:, None], w1, j2]
         T1, T2 = tot[ag[:, None], w1], tot[ag[:, None], w2]
-        same = (w1 == w2)[..., None]
-        s12 = sr[ag[:, None], w1, j2]
-        t1 = np.where(same, T1 - s1 - s12 + a1 + a2, T1 - s1 + a1)
-        t2 = np.where(same, t1, T2 - s2 + a2)
-        ok = (ti[:, None, :, :] != w1[:, :, None, None]) & (ti[:, None, :, :] != w2[:, :, None, None])   # (G, L, 3, bands)
+        sw = ((w1 == w2) & ~same)[..., None]
+        t1 = np.where(same[..., None], T1 - s1 + a1, np.where(sw, T1 - s1 - s12 + a1 + a2, T1 - s1 + a1))
+        t2 = np.where((w1 == w2)[..., None], t1, T2 - s2 + a2)
+        ok = (ti[:, None, :, :] != w1[:, :, None, None]) & (ti[:, None, :, :] != w2[:, :, None, None])
         first = np.argmax(ok, axis=2)
         other = np.maximum(np.take_along_axis(np.broadcast_to(tv[:, None], ok.shape), first[:, :, None, :], 2)[:, :, 0, :], 0)
         newmax = np.maximum(other, np.maximum(t1, t2))
-        dsum = np.where(same, t1 - T1, (t1 - T1) + (t2 - T2))
+        dsum = np.where((w1 == w2)[..., None], t1 - T1, (t1 - T1) + (t2 - T2))
         d = (W * (newmax - tv[:, None, 0, :]) + dsum).sum(axis=2)
-        d = np.where((w1 != w2) | (j1 != j2), d, 1 << 20)
+        d = np.where(valid, d, 1 << 20)
         win = np.argmin(((d + (1 << 20)) << 8) | np.arange(L)[None, :], axis=1)
-        apply = d[ag, win] <= 0
-        for g in np.nonzero(apply)[0]:
+        for g in np.nonzero(d[ag, win] <= 0)[0]:
             x = win[g]
             q1, q2 = p1[g, x], p2[g, x]
             rows[g, [q1, q2]] = rows[g, [q2, q1]]
             c[g][:, [q1, q2]] = c[g][:, [q2, q1]]
             v1, v2, k1, k2 = w1[g, x], w2[g, x], j1[g, x], j2[g, x]
-            if v1 == v2:
+            if same[g, x]:
+                tot[g, v1] += a1[g, x] - sr[g, v1, k1]
+            elif v1 == v2:
                 tot[g, v1] += a1[g, x] - sr[g, v1, k1] + a2[g, x] - sr[g, v1, k2]
             else:
                 tot[g, v1] += a1[g, x] - sr[g, v1, k1]
@@ -605,15 +610,17 @@ def _balance_numpy(order, cnt, per, groups, steps):
     return order
 
 
-def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_steps=600, groups=None):
+def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_steps=600, groups=None, paired=False):
     """The swept step's plan tables restated: off[i][b] = row i's start plus its non-zeros with a column in the
     bands before b (band of column c: c * bands // prev_rows), off[i][bands] = its end.  The order lists each
     consecutive segment of `per` rows longest first (ties by row index), then, in segments of at most 64 rows, the
     plan's wave-parallel local search: at each of `steps` steps, each of 64 lanes (xorshift32 per segment and lane)
-    draws two positions; a pair in different slots scores the change in the two slots' rounds its swap would make;
-    the lowest score (ties: lowest lane) is applied when it adds no rounds.  Then each group of 16 segments (the
-    waves of one workgroup) runs the plan's balance search over `balance_steps` steps (_balance_numpy).  Groups are
-    independent: `groups` (indices) limits both searches to those, the others keep the sort."""
+    draws two positions; a pair whose swap can change a unit's rounds (different units, or with `paired` two lane
+    groups of one pass) scores that change; the lowest score (ties: lowest lane) is applied when it adds no rounds.
+    `paired` counts units of two slots walked as one pass, as for a float32 sweep whose waves own over 24 rows.
+    Then each group of 16 segments (the waves of one workgroup) runs the plan's balance search over `balance_steps`
+    steps (_balance_numpy).  Groups are independent: `groups` (indices) limits both searches to those, the others
+    keep the sort."""
     nr = len(rowptr) - 1
     lens = np.diff(rowptr)
     band = cols.astype(np.int64) * bands // prev_rows
@@ -628,6 +635,8 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_
         order[b:b + len(idx)] = idx[np.lexsort((idx, -lens[idx]))]
     if per > 64 or steps == 0:
         return off, order
+    paired = bool(paired and bands == 4 and per > 24)
+    U = 16 if paired else 8
     total_seg = -(-nr // per)
     n_groups = -(-total_seg // 16)
     groups = np.arange(n_groups) if groups is None else np.asarray(groups)
@@ -638,13 +647,12 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_
     pad[:nr] = order
     rows = pad.reshape(total_seg, per)[segs]
     c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)   # (nseg, bands, per)
-    slots = (m + 7) // 8
-    live = slots >= 2
+    live = m > 8
     sg = segs.astype(np.uint64)[:, None]
     ln = np.arange(64, dtype=np.uint64)[None, :]
     low = np.uint64(0xFFFFFFFF)
     state = ((np.uint64(2463534242) ^ ((sg * np.uint64(2654435761)) & low) ^ (((ln + np.uint64(1)) * np.uint64(2246822507)) & low))
-             | np.uint64(1)).astype(np.uint32)                                                  # (nseg, 64)
+             | np.uint64(1)).astype(np.uint32)
     def nxt():
         nonlocal state
         state = state ^ (state << np.uint32(13))
@@ -653,24 +661,23 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_
         return state
     seg_ix = np.arange(nseg)[:, None, None, None]
     band_ix = np.arange(bands)[None, None, :, None]
-    def slot_cost(j, out, inn):   # j, out, inn: (nseg, L) -> rounds of slot j with position out holding row inn
-        r = np.clip(m[:, None] - 8 * j, 0, 8)
-        lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))
-        pos = 8 * j[..., None] + np.arange(8)
-        src = np.where(pos == out[..., None], inn[..., None], np.minimum(pos, per - 1))
-        vals = c[seg_ix, band_ix, src[:, :, None, :]]                                          # (nseg, L, bands, 8)
-        share = (vals + (1 << lf)[..., None, None] - 1) >> lf[..., None, None]
-        share = np.where((np.arange(8) < r[..., None])[:, :, None, :], share, 0)
-        return ((share.max(axis=3) + 3) & ~3).sum(axis=2)
-    js = np.tile(np.arange(8), (nseg, 1))
-    cost = slot_cost(js, np.full_like(js, -1), np.zeros_like(js))                              # (nseg, 8)
+    def unit_cost(u, x, y):   # (nseg, L) -> rounds of unit u with the rows at positions x and y swapped
+        r = np.clip(m[:, None] - U * u, 0, U)
+        p = U * u[..., None] + np.arange(U)
+        src = np.where(p == x[..., None], y[..., None], np.where(p == y[..., None], x[..., None], p))
+        vals = c[seg_ix, band_ix, np.minimum(src, per - 1)[:, :, None, :]]                   # (nseg, L, bands, U)
+        return np.where(r > 0, _unit_rounds_numpy(vals, r, paired), 0)
+    us = np.tile(np.arange(8), (nseg, 1))
+    cost = unit_cost(us, np.full_like(us, -1), np.full_like(us, -1))                          # (nseg, 8)
     ar = np.arange(nseg)
     for _ in range(steps):
         i = (nxt() % m[:, None].astype(np.uint32)).astype(np.int64)
         k = (nxt() % m[:, None].astype(np.uint32)).astype(np.int64)
-        si, sk = i >> 3, k >> 3
-        ci, ck = slot_cost(si, i, k), slot_cost(sk, k, i)
-        d = np.where(si != sk, ci + ck - np.take_along_axis(cost, si, 1) - np.take_along_axis(cost, sk, 1), 1 << 20)
+        ui, uk = i // U, k // U
+        ci, ck = unit_cost(ui, i, k), unit_cost(uk, i, k)
+        cui, cuk = np.take_along_axis(cost, ui, 1), np.take_along_axis(cost, uk, 1)
+        within = (ui == uk) & paired & ((i & 7) != (k & 7))
+        d = np.where(ui != uk, ci + ck - cui - cuk, np.where(within, ci - cui, 1 << 20))
         w = np.argmin(((d + (1 << 20)) << 6) | np.arange(64)[None, :], axis=1)
         apply = live & (d[ar, w] <= 0)
         iw, kw = i[ar, w], k[ar, w]
@@ -678,57 +685,57 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_
         ia, ka = iw[apply], kw[apply]
         c[a, :, ia], c[a, :, ka] = c[a, :, ka].copy(), c[a, :, ia].copy()
         rows[a, ia], rows[a, ka] = rows[a, ka].copy(), rows[a, ia].copy()
-        cost[a, si[ar, w][apply]] = ci[ar, w][apply]
-        cost[a, sk[ar, w][apply]] = ck[ar, w][apply]
+        cost[a, ui[ar, w][apply]] = ci[ar, w][apply]
+        cost[a, uk[ar, w][apply]] = ck[ar, w][apply]
     out = pad.reshape(total_seg, per).copy()
     out[segs] = rows
     order = out.reshape(-1)[:nr]
     if balance_steps:
-        order = _balance_numpy(order, cnt, per, groups, balance_steps)
+        order = _balance_numpy(order, cnt, per, groups, balance_steps, paired)
     return off, order
 
 
 def test_sweep_band_table_order_and_rule_match_numpy():
     """The plan-time work of a swept step (k_band_off, the order of k_sweep_order, k_sweep_order_search and
-    k_sweep_order_balance, and the
-    suitability rule of sweep_suits, shared by the plan and the probe library's flyprobe_band_table) against a numpy
-    restatement, bit for bit, on random CSR matrices of 70,000 rows (18 rows per wave: slots of 8, 8 and 2): a
-    plain one sweeps; one with a hub row (longer than 4 x the mean + 64) and one over 32,768 source rows or fewer do
-    not.  The searches (k_sweep_order_search within each wave, k_sweep_order_balance across the 16 waves of a
-    workgroup) leave each workgroup its rows and each wave its number of rows."""
+    k_sweep_order_balance, and the suitability rule of sweep_suits, shared by the plan and the probe library's
+    flyprobe_band_table) against a numpy restatement, bit for bit, on random CSR matrices: 70,000 rows (18 rows per
+    wave: slots of 8, 8 and 2) whose plain form sweeps and whose forms with a hub row (longer than 4 x the mean + 64)
+    or with 32,768 source rows do not, and 110,000 rows (27 per wave) searched for a float32 sweep that walks two
+    slots per pass.  The searches leave each workgroup its rows and each wave its number of rows, and lower the
+    rounds and the workgroups' barrier-bound rounds on this fixed data."""
     import ctypes
     probe = ctypes.CDLL(os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so"))
     probe.flyprobe_last_error.restype = ctypes.c_char_p
     i64, i32, p_ = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
-    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, p_, p_, ctypes.POINTER(i32), p_]
+    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, i32, p_, p_, ctypes.POINTER(i32), p_]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     rng = np.random.default_rng(41)
-    nr = 70_000
-    base_lens = rng.poisson(40, nr)
-    cases = [("plain", 40_000, base_lens, 1), ("small source", 32_768, base_lens, 0)]
+    base_lens = rng.poisson(40, 70_000)
     hub = base_lens.copy()
     hub[12_345] = 4 * int(hub.mean()) + 200
-    cases.append(("hub row", 40_000, hub, 0))
-    for label, prev_rows, lens, want_swept in cases:
+    cases = [("plain", 40_000, base_lens, 1, 0, (3, 4)), ("small source", 32_768, base_lens, 0, 0, (3, 4)),
+             ("hub row", 40_000, hub, 0, 0, (3, 4)), ("pairs", 40_000, rng.poisson(40, 110_000), 1, 1, (4,))]
+    for label, prev_rows, lens, want_swept, paired, band_counts in cases:
+        nr = len(lens)
         rowptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
         cols = np.concatenate([np.sort(rng.integers(0, prev_rows, n)) for n in lens]).astype(np.int32)
         pairs = np.stack([cols, rng.standard_normal(len(cols)).astype(np.float32).view(np.int32)], axis=1)
         d_rowptr = torch.as_tensor(rowptr, device=DEV)
         d_pairs = torch.as_tensor(np.ascontiguousarray(pairs), device=DEV)
-        for bands in (3, 4):
+        per = -(-nr // (16 * cus))
+        nseg = -(-nr // per)
+        ngrp = -(-nseg // 16)
+        for bands in band_counts:
             d_off = torch.full((nr, bands + 1), -7, dtype=torch.int32, device=DEV)
             d_order = torch.full((nr,), -7, dtype=torch.int32, device=DEV)
             swept = i32(-1)
             rc = probe.flyprobe_band_table(d_rowptr.data_ptr(), d_pairs.data_ptr(), nr, len(cols), prev_rows, bands,
-                                           d_off.data_ptr(), d_order.data_ptr(), ctypes.byref(swept), None)
+                                           paired, d_off.data_ptr(), d_order.data_ptr(), ctypes.byref(swept), None)
             assert rc == 0, probe.flyprobe_last_error()
             torch.cuda.synchronize()
-            per = -(-nr // (16 * cus))
-            nseg = -(-nr // per)
-            ngrp = -(-nseg // 16)
             check = np.r_[0:6, ngrp - 1]      # the searches restated for these groups of 16 waves (independent)
             off, order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200 if want_swept else 0,
-                                             groups=check)
+                                             groups=check, paired=bool(paired))
             got = d_order.cpu().numpy()
             print(f"{label}, {bands} bands: swept {swept.value}", flush=True)
             assert swept.value == want_swept, (label, bands, swept.value)
@@ -737,21 +744,22 @@ def test_sweep_band_table_order_and_rule_match_numpy():
                 continue
             sel = np.concatenate([np.arange(16 * g * per, min(16 * (g + 1) * per, nr)) for g in check])
             assert np.array_equal(got[sel], order[sel]), (label, bands)
-            # each group of 16 waves keeps its rows; on this fixed data the searches lower the workgroups' cost
             _, sorted_order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=0, balance_steps=0)
             for g0 in range(0, nr, 16 * per):
                 assert np.array_equal(np.sort(got[g0:g0 + 16 * per]), np.arange(g0, min(g0 + 16 * per, nr)))
             cnt = np.stack([off[:, q + 1] - off[:, q] for q in range(bands)], axis=1)
+            U = 16 if paired and per > 24 else 8
             def cost(o):   # (rounds, barrier-bound rounds: per workgroup and band the largest wave's)
                 m = np.minimum(per, nr - np.arange(nseg) * per)
-                pad = np.full(nseg * per, -1, np.int64)
+                pad = np.full(nseg * per + U, -1, np.int64)
                 pad[:nr] = o
-                rows = pad.reshape(nseg, per)
-                c = np.where(rows[:, None, :] >= 0, cnt[np.maximum(rows, 0)].transpose(0, 2, 1), 0)
-                per_wave = np.zeros((nseg, bands), np.int64)
-                for j in range(-(-per // 8)):
-                    for q in range(bands):
-                        per_wave[:, q] += _slot_rounds_numpy(c[:, q:q + 1, :], m, np.full(nseg, j))
+                rows = np.stack([pad[np.arange(nseg) * per + j * U + np.arange(U)[:, None]].T
+                                 for j in range(-(-per // U))], axis=1)               # (nseg, units, U)
+                r = np.clip(m[:, None] - U * np.arange(rows.shape[1])[None, :], 0, U)
+                rows = np.where(np.arange(U) < r[..., None], rows, -1)
+                vals = np.where(rows[..., None] >= 0, cnt[np.maximum(rows, 0)], 0).transpose(0, 1, 3, 2)
+                per_wave = np.stack([np.where(r > 0, _unit_rounds_numpy(vals[:, :, q:q + 1, :], r, U == 16), 0)
+                                     .sum(axis=1) for q in range(bands)], axis=1)     # (nseg, bands)
                 padw = np.zeros((ngrp * 16, bands), np.int64)
                 padw[:nseg] = per_wave
                 return int(per_wave.sum()), int(padw.reshape(ngrp, 16, bands).max(axis=1).sum())
