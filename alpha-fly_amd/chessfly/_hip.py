@@ -69,6 +69,8 @@ SIGNATURES = {
     "fly_evaluator_outputs": (_i32, [_p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p]),
     "fly_evaluator_download": (_i32, [_p, _p, _sz, _i32, _p]),
     "fly_spmm": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p]),
+    "fly_sweep_tables": (_i32, [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "fly_spmm_swept": (_i32, [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p]),
     "fly_transposed_backward": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p,
                                        _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p]),
     "fly_train_step_forward": (_i32, [_i64, _i64, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _f32, _p,

@@ -61,6 +61,39 @@ def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, out: to
     return y
 
 
+def _sweep_tables(holder, crow32, col32, n_rows: int, n_cols: int):
+    """The band starts and row order of the forward product's banded sweep over one structure (fly_sweep_tables),
+    built on first use and kept on `holder` with the row pointer they belong to; None when the structure does not
+    suit a sweep (too few or too short rows, or rows far longer than the mean)."""
+    cached = getattr(holder, "_sweep", None)
+    if cached is not None and cached[0] is crow32:
+        return cached[1]
+    dev = crow32.device
+    band_off = torch.empty(n_rows * 5, dtype=torch.int32, device=dev)
+    order = torch.empty(n_rows, dtype=torch.int32, device=dev)
+    swept = ctypes.c_int32(0)
+    _hip.check(_hip.load().fly_sweep_tables(crow32.data_ptr(), col32.data_ptr(), n_rows, col32.numel(), n_cols,
+                                            band_off.data_ptr(), order.data_ptr(), ctypes.addressof(swept),
+                                            _hip.stream(dev)), "fly_sweep_tables")
+    tables = (band_off, order) if swept.value else None
+    holder._sweep = (crow32, tables)
+    return tables
+
+
+def _spmm_swept(crow32, col32, val, tables, n_rows: int, n_cols: int, x: torch.Tensor) -> torch.Tensor:
+    """y (n_rows, B) = A x as a banded sweep (fly_spmm_swept) from {column, weight} records; x (n_cols, B) float32
+    with B a multiple of 4."""
+    x = x.contiguous()
+    batch = x.shape[1]
+    y = torch.empty(n_rows, batch, dtype=torch.float32, device=x.device)
+    records = torch.stack((col32, val.contiguous().view(torch.int32)), dim=1)
+    band_off, order = tables
+    _hip.check(_hip.load().fly_spmm_swept(crow32.data_ptr(), records.data_ptr(), band_off.data_ptr(),
+                                          order.data_ptr(), n_rows, n_cols, x.data_ptr(), batch, batch,
+                                          y.data_ptr(), batch, _hip.stream(x.device)), "fly_spmm_swept")
+    return y
+
+
 def _spmv_work(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, work,
                out: torch.Tensor | None = None) -> torch.Tensor:
     """y (n_rows, 1) = A x for one column over a work list (fly_spmv_work): rows split into segments of at most
@@ -183,6 +216,11 @@ def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out
             return _spmv_work(crow32, col32, _gathered(op, w, True), n_rows, n_cols, x, op._backward_work(), out=out)
     else:
         crow32, col32, n_rows, n_cols = op._structure()
+        batch = x.shape[1]
+        if out is None and x.dtype == torch.float32 and batch >= 4 and batch % 4 == 0:
+            tables = _sweep_tables(op, crow32, col32, n_rows, n_cols)
+            if tables is not None:
+                return _spmm_swept(crow32, col32, _gathered(op, w, False), tables, n_rows, n_cols, x)
     return _spmm(crow32, col32, _gathered(op, w, transposed), n_rows, n_cols, x, out=out)
 
 

@@ -218,7 +218,7 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
                              cone->edge[t].p, w, cone->nnz[t], plan->colval[t].p);
         if (sweep_suits(plan->rowptr[t].p, cone->rows_n[t - 1], nr, cone->nnz[t], st)) {
           plan->band_off[t].alloc((size_t)nr * (plan->sweep_bands + 1));
-          hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
+          hipLaunchKernelGGL(k_band_off<int2>, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
                              plan->colval[t].p, nr, cone->rows_n[t - 1], plan->sweep_bands, plan->band_off[t].p);
           plan->sweep_rows[t].alloc((size_t)nr);
           build_sweep_order(plan->rowptr[t].p, plan->band_off[t].p, plan->sweep_bands, nr,
@@ -293,7 +293,7 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
     plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
     if (sweep_suits(plan->rowptr[0].p, n, n, n_edges, st)) {
       plan->band_off[0].alloc((size_t)n * (plan->sweep_bands + 1));
-      hipLaunchKernelGGL(k_band_off, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
+      hipLaunchKernelGGL(k_band_off<int2>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
                          plan->colval[0].p, n, n, plan->sweep_bands, plan->band_off[0].p);
       plan->sweep_rows[0].alloc((size_t)n);
       build_sweep_order(plan->rowptr[0].p, plan->band_off[0].p, plan->sweep_bands, n, sweep_pairs(true),

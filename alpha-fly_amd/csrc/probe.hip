@@ -152,7 +152,7 @@ extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0 && nnz >= 0, "size out of range");
     FLY_REQUIRE(bands == 3 || bands == 4, "bands must be 3 or 4");
     *swept = sweep_suits(rowptr, prev_rows, nrows, nnz, as_stream(stream)) ? 1 : 0;
-    hipLaunchKernelGGL(k_band_off, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
+    hipLaunchKernelGGL(k_band_off<int2>, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
                        static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
     build_sweep_order(rowptr, band_off, bands, nrows, paired != 0, order, as_stream(stream));
     const hipError_t e = hipGetLastError();

@@ -582,14 +582,18 @@ namespace {
 // [b * prev_rows / K, (b + 1) * prev_rows / K).  off (nr, K + 1): the row's start plus the count of its columns in
 // the bands before b; off[i][K] is the row's end.  A row's columns rise (CSR order of W[post, pre]), so each range
 // holds exactly its band; in any other order the ranges still split the row's non-zeros between the bands.
-__global__ void k_band_off(const int32_t *__restrict__ rowptr, const int2 *__restrict__ colval, int64_t nr,
+__device__ __forceinline__ int32_t record_col(const int2 &r) { return r.x; }
+__device__ __forceinline__ int32_t record_col(int32_t c) { return c; }
+
+template <typename C>   // C: {column, weight} records (int2) or plain columns (int32_t)
+__global__ void k_band_off(const int32_t *__restrict__ rowptr, const C *__restrict__ colval, int64_t nr,
                            int64_t prev_rows, int32_t K, int32_t *__restrict__ off) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= nr) return;
   const int32_t beg = rowptr[i], end = rowptr[i + 1];
   int32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int32_t q = beg; q < end; ++q) {
-    const int64_t b = (int64_t)colval[q].x * K / prev_rows;
+    const int64_t b = (int64_t)record_col(colval[q]) * K / prev_rows;
 #pragma unroll
     for (int k = 0; k < 8; ++k) cnt[k] += (b == k) ? 1 : 0;
   }
@@ -926,7 +930,7 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // slot's rounds run to the longest of the wave's 8 rows in that slot and band, the shorter rows' extra gathers from
 // the row past the buffer (zeros, no memory access); a slot of 4 rows or fewer spreads each row over several lane
 // groups.  PIPE keeps the next four rounds' gathers in flight during the sums.  REPLAY as for the other step
-// kernels.
+// kernels, and 3: the product alone, each row's sums stored to xout (float32 states; the training forward's A x).
 template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, bool PAIRED = false,
           bool PIPE = false>
 __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, U> a) {
@@ -1012,7 +1016,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                     const uint32_t o = __umul24((uint32_t)cc, row_bytes) + voff;
                     xr[u] = bload<S, V>(r, (int)o, 0);
                   });
-                  if constexpr (REPLAY != 0) {
+                  if constexpr (REPLAY == 1 || REPLAY == 2) {
 #pragma unroll
                     for (int u = 0; u < UNR; ++u) ReplayBits<S, V>::fold(bits, xr[u], wj[u]);
                   } else {
@@ -1067,7 +1071,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
               });
             };
             auto sum4 = [&](const vec (&xr)[4], const int (&wj)[4]) {
-              if constexpr (REPLAY != 0) {
+              if constexpr (REPLAY == 1 || REPLAY == 2) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) ReplayBits<S, V>::fold(bits, xr[u], wj[u]);
               } else {
@@ -1126,7 +1130,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                   const uint32_t o = __umul24((uint32_t)cc, row_bytes) + voff;
                   xr[u] = bload<S, V>(r, (int)o, 0);
                 });
-                if constexpr (REPLAY != 0) {
+                if constexpr (REPLAY == 1 || REPLAY == 2) {
 #pragma unroll
                   for (int u = 0; u < UNR; ++u) ReplayBits<S, V>::fold(bits, xr[u], wj[u]);
                 } else {
@@ -1161,10 +1165,14 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           const int32_t rs = first && i < nrow[j] && in_batch ? row_at(pj) : -1;
           if (rs >= 0) {
             const uint32_t rj = (uint32_t)rs;
-            if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j], bits);
-            RowInputs<S, U, V> in;
-            load_row_inputs(a, rj, col, true, in);
-            finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j], in);
+            if constexpr (REPLAY == 3) {   // the product alone: y[row] = the row's sums, float32
+              Lanes<S, V>::store(a.xout + (int64_t)rj * a.ldo + col, acc[j]);
+            } else {
+              if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j], bits);
+              RowInputs<S, U, V> in;
+              load_row_inputs(a, rj, col, true, in);
+              finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j], in);
+            }
           }
         }
       }

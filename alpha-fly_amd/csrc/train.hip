@@ -6,6 +6,7 @@
 // return zeros, so indices from the caller can never make a kernel read out of bounds.
 #include "common.hpp"
 #include "device.hpp"
+#include "step_kernels.hpp"
 
 namespace fly {
 namespace {
@@ -936,6 +937,53 @@ void launch_spmm(const SpmmArgs &a, hipStream_t st) {
 }  // namespace fly
 
 using namespace fly;
+
+extern "C" int fly_sweep_tables(const int32_t *rowptr, const int32_t *col, int64_t nrows, int64_t nnz,
+                                int64_t ncols, int32_t *band_off, int32_t *order, int32_t *swept, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(rowptr && band_off && order && swept, "null argument");
+    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)1 << 24 && ncols > 0 && ncols < (int64_t)1 << 24 && nnz >= 0,
+                "size out of range");
+    FLY_REQUIRE(nnz == 0 || col, "null columns");
+    hipStream_t st = as_stream(stream);
+    *swept = sweep_suits(rowptr, ncols, nrows, nnz, st) ? 1 : 0;   // synchronises
+    if (!*swept) return;
+    hipLaunchKernelGGL(k_band_off<int32_t>, dim3(blocks_for(nrows, 256)), dim3(256), 0, st, rowptr, col, nrows, ncols,
+                       kSweepBands, band_off);
+    build_sweep_order(rowptr, band_off, kSweepBands, nrows, true, order, st);
+    check_launch("sweep tables");
+  });
+}
+
+extern "C" int fly_spmm_swept(const int32_t *rowptr, const void *records, const int32_t *band_off,
+                              const int32_t *order, int64_t nrows, int64_t ncols, const float *x, int64_t ldx,
+                              int64_t batch, float *y, int64_t ldy, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(rowptr && records && band_off && order && x && y, "null argument");
+    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)1 << 24 && ncols > 0 && ncols < (int64_t)1 << 24, "size out of range");
+    FLY_REQUIRE(batch > 0 && batch % 4 == 0 && batch < (int64_t)INT32_MAX / 2, "the batch must be a multiple of 4");
+    FLY_REQUIRE(ldx >= batch && ldy >= batch && ldx % 4 == 0 && ldy % 4 == 0 && aligned(x, 16) && aligned(y, 16),
+                "x and y rows must be 16-byte aligned and hold the batch");
+    const uint32_t xbytes = buffer_bytes(ncols, ldx, sizeof(float));
+    FLY_REQUIRE(xbytes != 0, "x must be below 2 GiB with rows of 24-bit indices");
+    StepArgs<float, float> a{};
+    a.rowptr = rowptr;
+    a.colval = static_cast<const int2 *>(records);
+    a.xprev = x;
+    a.ldx = ldx;
+    a.xout = y;
+    a.ldo = ldy;
+    a.nrows = (int32_t)nrows;
+    a.batch = (int32_t)batch;
+    a.xbytes = xbytes;
+    a.band_off = band_off;
+    a.sweep_rows = order;
+    a.sweep_bands = kSweepBands;
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    launch_swept<float, float, 3>(a, as_stream(stream));
+    check_launch("swept product");
+  });
+}
 
 extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *val, const int32_t *val_ids,
                         int64_t n_val, int64_t nrows, int64_t ncols, const float *x, int64_t ldx, int64_t batch,

@@ -250,8 +250,19 @@ int fly_evaluator_download(const void *src_dev, void *dst_host, size_t bytes, in
  *              gradient of y = A x with g = dL/dy.  With ids (distinct), out[ids[e]] instead (a sub-matrix's
  *              gradient straight into the whole weight vector); accumulate != 0 adds; out holds n_out entries and slots at
  *              or past it are skipped.  out must not overlap g.
+ *   fly_sweep_tables / fly_spmm_swept: the forward product as a banded sweep of x's rows (the state step's
+ *              swept kernel, storing each row's sums).  fly_sweep_tables builds, once per structure, the band
+ *              starts (band_off, nrows x 5 int32) and the row order (order, nrows int32) from rowptr and col
+ *              (ncols: rows of x); *swept = 1 when the structure suits a sweep (the state step's rule), else
+ *              nothing is built.  It synchronises.  fly_spmm_swept: y = A x from {column, weight bits} records
+ *              (nnz int2, CSR order), for batches that are multiples of 4 with 16-byte aligned rows.
  * Gathered operands must be below 2 GiB; rows and columns below 2^24; column indices are not range-checked
  * (a wrong index reads wrong data, never outside x). */
+int fly_sweep_tables(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t nnz, int64_t ncols,
+                     int32_t *band_off_dev, int32_t *order_dev, int32_t *swept, void *stream);
+int fly_spmm_swept(const int32_t *rowptr_dev, const void *records_dev, const int32_t *band_off_dev,
+                   const int32_t *order_dev, int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx,
+                   int64_t batch, float *y_dev, int64_t ldy, void *stream);
 int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, const int32_t *val_ids_dev,
              int64_t n_val, int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx, int64_t batch,
              float *y_dev, int64_t ldy, int32_t accumulate, void *stream);

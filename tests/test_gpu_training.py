@@ -196,6 +196,47 @@ def test_one_column_product_over_a_work_list_matches_float64(heavy, seg, accumul
     _close(y, torch.as_tensor(want), 1e-5, "spmv over the work list")
 
 
+@pytest.mark.parametrize("batch", [4, 68, 256])
+def test_swept_forward_product_matches_float64(batch):
+    """fly_spmm_swept (the forward product as a banded sweep, training batches that are multiples of 4) against
+    float64 and fly_spmm, on a random CSR matrix that suits the sweep (70,000 rows of ~40 non-zeros over 40,000
+    source rows); fly_sweep_tables refuses one with a hub row."""
+    from chessfly import brain
+    rng = np.random.default_rng(batch)
+    n_rows, n_cols = 70_000, 40_000
+    lens = rng.poisson(40, n_rows)
+    crow = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    col = np.concatenate([np.sort(rng.integers(0, n_cols, n)) for n in lens]).astype(np.int32)
+    val = rng.standard_normal(len(col)).astype(np.float32)
+    x = rng.standard_normal((n_cols, batch)).astype(np.float32)
+    crow32, col32 = torch.as_tensor(crow, device=DEV), torch.as_tensor(col, device=DEV)
+    val_d, x_d = torch.as_tensor(val, device=DEV), torch.as_tensor(x, device=DEV)
+
+    class Holder:
+        pass
+
+    holder = Holder()
+    tables = brain._sweep_tables(holder, crow32, col32, n_rows, n_cols)
+    assert tables is not None
+    assert brain._sweep_tables(holder, crow32, col32, n_rows, n_cols) is tables     # built once per structure
+    y = brain._spmm_swept(crow32, col32, val_d, tables, n_rows, n_cols, x_d)
+    y_ref = brain._spmm(crow32, col32, val_d, n_rows, n_cols, x_d)
+    torch.cuda.synchronize()
+    rows = np.repeat(np.arange(n_rows), lens)
+    exact = np.zeros((n_rows, batch))
+    np.add.at(exact, rows, val[:, None].astype(np.float64) * x[col].astype(np.float64))
+    scale = np.abs(exact).max()
+    err, err_ref = np.abs(y.cpu().numpy() - exact).max() / scale, np.abs(y_ref.cpu().numpy() - exact).max() / scale
+    print(f"B={batch}: swept {err:.2e}, fly_spmm {err_ref:.2e} of the largest |y|", flush=True)
+    assert err < 1e-5 and err_ref < 1e-5
+    hub = lens.copy()
+    hub[123] = 4 * int(lens.mean()) + 200
+    crow_h = torch.as_tensor(np.concatenate([[0], np.cumsum(hub)]).astype(np.int32), device=DEV)
+    col_h = torch.as_tensor(np.concatenate([np.sort(rng.integers(0, n_cols, n)) for n in hub]).astype(np.int32),
+                            device=DEV)
+    assert brain._sweep_tables(Holder(), crow_h, col_h, n_rows, n_cols) is None
+
+
 def test_gather_values_reads_the_weight_vector_at_int32_ids():
     """fly_gather_values: out[i] = w[ids[i]] (a sub-matrix's values in its own or its transpose's order), ids past
     the vector (and negative ones) read 0, bit for bit."""
