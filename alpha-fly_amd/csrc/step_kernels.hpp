@@ -948,10 +948,11 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
   const int R = a.rows_per_wave;
   const uint32_t npos = (uint32_t)a.nrows;   // positions of the order: one per row
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  // position p of the sweep order holds row sweep_rows[p] (-1: none; p itself without an order)
+  // position p of the sweep order holds row sweep_rows[p] (p itself without an order); an entry outside the step's
+  // rows reads as no row
   auto row_at = [&](uint32_t p) {
     const int32_t r = a.sweep_rows ? a.sweep_rows[p] : (int32_t)p;
-    return r < a.nrows ? r : -1;
+    return r >= 0 && r < a.nrows ? r : -1;
   };
   for (int k0 = 0; k0 < R; k0 += 8 * SLOTS) {
     const uint32_t base = wave * (uint32_t)R + (uint32_t)k0;   // slot j, row i of the slot: position base + 8 j + i
