@@ -13,6 +13,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflyeval.so")
 
+ABI_VERSION = 2
 MODE_DEVIATION_F16 = 0
 MODE_F32 = 1
 CONE_UNPRUNED = 1
@@ -44,7 +45,11 @@ SIGNATURES = {
     "fly_cone_outputs": (_i32, [_p, _p, _p]),
     "fly_edge_weights": (_i32, [_p, _p, _p, _i64, _p, _p]),
     "fly_plan_create": (_i32, [_p, _p, _p, _p, _p, _p, _f32, _i32, _p, _pp]),
-    "fly_plan_create_full": (_i32, [_i64, _i64, _p, _p, _p, _p, _f32, _p, _pp]),
+    "fly_plan_create_full": (_i32, [_i64, _i64, _p, _p, _p, _p, _f32, _p, _p, _pp]),
+    "fly_plan_sweep_info": (_i32, [_p, _i32, _p]),
+    "fly_sweep_create": (_i32, [_p, _p, _i64, _i64, _i64, _p, _pp]),
+    "fly_sweep_destroy": (_i32, [_p]),
+    "fly_sweep_info": (_i32, [_p, _p]),
     "fly_plan_destroy": (_i32, [_p]),
     "fly_plan_resting": (_i32, [_p, _p, _p]),
     "fly_plan_matrix": (_i32, [_p, _i32, _p, _p, _p, _p]),
@@ -56,7 +61,8 @@ SIGNATURES = {
     "fly_forward_literal": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
     "fly_forward_literal_f64_workspace": (_sz, [_p, _i64]),
     "fly_forward_literal_f64": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
-    "fly_plan_step": (_i32, [_p, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p]),
+    "fly_plan_step_workspace": (_sz, [_p, _i32, _i64]),
+    "fly_plan_step": (_i32, [_p, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_dense_create": (_i32, [ctypes.POINTER(HeadDesc), _p, _i64, _i64, _p, _i64, _p, _pp]),
     "fly_dense_destroy": (_i32, [_p]),
     "fly_encoder_workspace": (_sz, [_p, _i64]),
@@ -69,8 +75,8 @@ SIGNATURES = {
     "fly_evaluator_outputs": (_i32, [_p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p]),
     "fly_evaluator_download": (_i32, [_p, _p, _sz, _i32, _p]),
     "fly_spmm": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p]),
-    "fly_sweep_tables": (_i32, [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p]),
-    "fly_spmm_swept": (_i32, [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p]),
+    "fly_spmm_swept_workspace": (_sz, [_p, _i64]),
+    "fly_spmm_swept": (_i32, [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_transposed_backward": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p,
                                        _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p]),
     "fly_train_step_forward": (_i32, [_i64, _i64, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _f32, _p,
@@ -88,6 +94,7 @@ SIGNATURES = {
     "fly_profile_read": (_i32, [_p, _p]),
     "fly_profile_launches": (_i64, [_p, _p, _i64]),
     "fly_set_tuning": (_i32, [ctypes.c_char_p, _i64]),
+    "fly_get_tuning": (_i32, [ctypes.c_char_p, _p]),
 }
 
 _lib = None
@@ -104,8 +111,8 @@ def load() -> ctypes.CDLL:
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = res, args
-        if lib.fly_abi_version() != 1:
-            raise RuntimeError(f"{LIB_PATH} has ABI version {lib.fly_abi_version()}, expected 1")
+        if lib.fly_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {lib.fly_abi_version()}, expected {ABI_VERSION}")
         _lib = lib
     return _lib
 
@@ -162,7 +169,7 @@ def profile_launches() -> list[tuple[str, float]]:
 
 
 class Handle:
-    """Owner of a library object (cone, plan or dense plan): destroyed with the matching C call."""
+    """Owner of a library object (cone, plan, dense plan or sweep tables): destroyed with the matching C call."""
 
     def __init__(self, handle: ctypes.c_void_p, destroy: str, key=None):
         self.handle, self._destroy, self.key = handle, destroy, key
@@ -179,3 +186,24 @@ class Handle:
 
 def set_tuning(key: str, value: int) -> None:
     check(load().fly_set_tuning(key.encode(), int(value)), "fly_set_tuning")
+
+
+SWEEP_INFO = ("positions", "pieces", "split_rows", "rows_per_wave", "bands", "workgroups", "tables")
+
+
+def sweep_info(handle, t: int | None = None) -> dict:
+    """How a swept structure runs: from a fly_sweep (t None) or step t of a plan (all zero when it does not sweep)."""
+    info = (ctypes.c_int64 * 7)()
+    if t is None:
+        check(load().fly_sweep_info(handle, info), "fly_sweep_info")
+    else:
+        check(load().fly_plan_sweep_info(handle, int(t), info), "fly_plan_sweep_info")
+    return dict(zip(SWEEP_INFO, (int(v) for v in info)))
+
+
+def sweep_create(crow32: torch.Tensor, col32: torch.Tensor, n_rows: int, n_cols: int):
+    """The banded-sweep tables of one CSR structure (fly_sweep_create) as a Handle, or None when it does not sweep."""
+    h = ctypes.c_void_p()
+    check(load().fly_sweep_create(crow32.data_ptr(), col32.data_ptr(), n_rows, col32.numel(), n_cols,
+                                  stream(crow32.device), ctypes.byref(h)), "fly_sweep_create")
+    return Handle(h, "fly_sweep_destroy") if h.value else None

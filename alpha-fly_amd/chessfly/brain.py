@@ -62,35 +62,28 @@ def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, out: to
 
 
 def _sweep_tables(holder, crow32, col32, n_rows: int, n_cols: int):
-    """The band starts and row order of the forward product's banded sweep over one structure (fly_sweep_tables),
-    built on first use and kept on `holder` with the row pointer they belong to; None when the structure does not
-    suit a sweep (too few or too short rows, or rows far longer than the mean)."""
+    """The banded-sweep tables of the forward product over one structure (fly_sweep_create, float32 operands), built
+    on first use and kept on `holder` with the row pointer they belong to; None when the structure does not sweep
+    (too few or too short rows)."""
     cached = getattr(holder, "_sweep", None)
     if cached is not None and cached[0] is crow32:
         return cached[1]
-    dev = crow32.device
-    band_off = torch.empty(n_rows * 5, dtype=torch.int32, device=dev)
-    order = torch.empty(n_rows, dtype=torch.int32, device=dev)
-    swept = ctypes.c_int32(0)
-    _hip.check(_hip.load().fly_sweep_tables(crow32.data_ptr(), col32.data_ptr(), n_rows, col32.numel(), n_cols,
-                                            band_off.data_ptr(), order.data_ptr(), ctypes.addressof(swept),
-                                            _hip.stream(dev)), "fly_sweep_tables")
-    tables = (band_off, order) if swept.value else None
+    tables = _hip.sweep_create(crow32, col32, n_rows, n_cols)
     holder._sweep = (crow32, tables)
     return tables
 
 
-def _spmm_swept(crow32, col32, val, tables, n_rows: int, n_cols: int, x: torch.Tensor) -> torch.Tensor:
-    """y (n_rows, B) = A x as a banded sweep (fly_spmm_swept) from {column, weight} records; x (n_cols, B) float32
-    with B a multiple of 4."""
-    x = x.contiguous()
+def _spmm_swept(col32, val, tables, n_rows: int, x: torch.Tensor) -> torch.Tensor:
+    """y (n_rows, B) = A x as a banded sweep (fly_spmm_swept) from {column, weight} records; x (n_cols, B) float32,
+    contiguous and 16-byte aligned, with B a multiple of 4."""
     batch = x.shape[1]
     y = torch.empty(n_rows, batch, dtype=torch.float32, device=x.device)
     records = torch.stack((col32, val.contiguous().view(torch.int32)), dim=1)
-    band_off, order = tables
-    _hip.check(_hip.load().fly_spmm_swept(crow32.data_ptr(), records.data_ptr(), band_off.data_ptr(),
-                                          order.data_ptr(), n_rows, n_cols, x.data_ptr(), batch, batch,
-                                          y.data_ptr(), batch, _hip.stream(x.device)), "fly_spmm_swept")
+    lib = _hip.load()
+    ws = _hip.workspace(lib.fly_spmm_swept_workspace(tables.handle, batch), x.device)
+    _hip.check(lib.fly_spmm_swept(tables.handle, records.data_ptr(), col32.numel(), x.data_ptr(), batch, batch,
+                                  y.data_ptr(), batch, ws.data_ptr(), ws.numel(), _hip.stream(x.device)),
+               "fly_spmm_swept")
     return y
 
 
@@ -219,8 +212,9 @@ def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out
         batch = x.shape[1]
         if out is None and x.dtype == torch.float32 and batch >= 4 and batch % 4 == 0:
             tables = _sweep_tables(op, crow32, col32, n_rows, n_cols)
-            if tables is not None:
-                return _spmm_swept(crow32, col32, _gathered(op, w, False), tables, n_rows, n_cols, x)
+            x = x.contiguous()
+            if tables is not None and x.data_ptr() % 16 == 0:
+                return _spmm_swept(col32, _gathered(op, w, False), tables, n_rows, x)
     return _spmm(crow32, col32, _gathered(op, w, transposed), n_rows, n_cols, x, out=out)
 
 
@@ -815,12 +809,22 @@ class ConnectomeRNN(nn.Module):
             self._plans[key_extra] = plan
         return plan
 
+    def _full_sweep(self):
+        """The banded-sweep tables of the whole matrix (float32 states), built once per structure: every literal
+        plan (each weight version) shares them.  None when the matrix does not sweep."""
+        cached = getattr(self, "_full_sweep_tables", None)
+        if cached is None or cached[0] is not self.crow32:
+            self._full_sweep_tables = (self.crow32, _hip.sweep_create(self.crow32, self.pre32, self.n, self.n))
+        return self._full_sweep_tables[1]
+
     def _full_plan(self) -> _Plan:
         def build(handle):
             w = self.edge_weights()
+            sweep = self._full_sweep()
             _hip.check(_hip.load().fly_plan_create_full(self.n, self.n_edges, self.crow32.data_ptr(),
                                                         self.pre32.data_ptr(), w.data_ptr(),
                                                         self.alpha_logit.data_ptr(), self._h_bound,
+                                                        sweep.handle if sweep is not None else None,
                                                         _hip.stream(w.device), ctypes.byref(handle)),
                        "fly_plan_create_full")
         return self._plan(("full",), build)

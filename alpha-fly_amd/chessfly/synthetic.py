@@ -17,6 +17,10 @@ constructors (chessfly/connectome.py:54-95, chessfly/brain.py:176-199, chessfly/
   normaliser keeps its fresh statistics (mean 0, variance 1).
 * Boards: 838 base features in {0, 1} with exactly 40 ones, or a uniform 20..40 ones per board.
 
+`degree_connectome` builds the same kind of graph around a given in-degree sequence and given sensory and
+output sets (the MaleCNS wiring's, whose row pointer and id sets ship as weight data with the reference's
+browser export): a heavy-tailed in-degree, with hub neurons of thousands of partners and neurons with none.
+
 Everything is drawn with numpy's PCG64 generator from explicit seeds, so the same call gives the same
 arrays on every machine with this numpy.
 """
@@ -77,6 +81,44 @@ def synthetic_connectome(spec: GraphSpec = FULL) -> Connectome:
     chosen = rng.permutation(n)
     sensory = np.sort(chosen[:spec.n_sensory])
     output = np.sort(chosen[spec.n_sensory:spec.n_sensory + spec.n_output])
+    return Connectome(_flows(n, sensory, output), torch.from_numpy(pre), torch.from_numpy(post),
+                      torch.from_numpy(syn), torch.from_numpy(nt_sign[pre]))
+
+
+def degree_connectome(in_degree: np.ndarray, sensory: np.ndarray, output: np.ndarray, seed: int = 0,
+                      sigma: float = 1.0, excitatory: float = 0.6, syn_mean: float = 4.0) -> Connectome:
+    """A graph in CSR order of W[post, pre] with the given in-degree per postsynaptic neuron and the given sorted
+    sensory ("afferent") and output ("efferent") sets.  A neuron's presynaptic partners are distinct and never the
+    neuron itself, each drawn with probability proportional to a per-neuron LogNormal(0, sigma) propensity (so
+    out-degrees are heavy-tailed, as in synthetic_connectome); a draw that repeats a partner of the same neuron or
+    hits the neuron itself is drawn again.  syn_count ~ Geometric(1 / syn_mean); the sign belongs to the
+    presynaptic neuron (+1 with probability `excitatory`)."""
+    rng = np.random.default_rng([seed, 0xDE6EE])
+    deg = np.asarray(in_degree, dtype=np.int64)
+    n = deg.size
+    if deg.max(initial=0) >= n:
+        raise ValueError("an in-degree reaches the neuron count: no distinct partners exist")
+    cdf = np.cumsum(rng.lognormal(0.0, sigma, size=n))
+    cdf /= cdf[-1]
+    post = np.repeat(np.arange(n, dtype=np.int64), deg)
+    pre = np.minimum(np.searchsorted(cdf, rng.random(post.size), side="right"), n - 1)
+    for _ in range(1000):
+        key = post * n + pre
+        order = np.argsort(key, kind="stable")
+        ks = key[order]
+        bad = np.zeros(post.size, dtype=bool)
+        bad[order[1:][ks[1:] == ks[:-1]]] = True           # a repeat of an earlier draw for the same neuron
+        bad |= pre == post
+        if not bad.any():
+            break
+        pre[bad] = np.minimum(np.searchsorted(cdf, rng.random(int(bad.sum())), side="right"), n - 1)
+    else:
+        raise RuntimeError("partner draws did not settle")
+    key = np.sort(post * n + pre)                          # (post, pre) order
+    post, pre = key // n, key % n
+    syn = rng.geometric(1.0 / syn_mean, size=key.size).astype(np.float32)
+    nt_sign = np.where(rng.random(n) < excitatory, 1.0, -1.0).astype(np.float32)
+    sensory, output = np.sort(np.asarray(sensory, np.int64)), np.sort(np.asarray(output, np.int64))
     return Connectome(_flows(n, sensory, output), torch.from_numpy(pre), torch.from_numpy(post),
                       torch.from_numpy(syn), torch.from_numpy(nt_sign[pre]))
 
@@ -171,11 +213,12 @@ def _cached_graph(spec: GraphSpec) -> Connectome:
 
 
 def synthetic_net(spec: GraphSpec = FULL, steps: int = 6, seed: int = 0, shuffled: bool = False,
-                  device: str | torch.device = "cpu"):
+                  device: str | torch.device = "cpu", graph: Connectome | None = None):
     """A FlyChessNet on the synthetic graph with every weight drawn from `seed` (returns the net and the
-    Connectome it was built on).  `shuffled` builds the degree-preserving control graph instead."""
+    Connectome it was built on).  `shuffled` builds the degree-preserving control graph instead; `graph` replaces
+    the synthetic graph of `spec` (degree_connectome's, for example)."""
     from .model import FlyChessNet, ModelConfig
-    conn = _cached_graph(spec)
+    conn = _cached_graph(spec) if graph is None else graph
     params = synthetic_params(conn, seed)
     cfg = ModelConfig(steps=steps, shuffled=shuffled, weight_scale=params.global_scale, input_gain=5.0, bias_init=0.1)
     net = FlyChessNet(conn, cfg)
@@ -198,5 +241,5 @@ def synthetic_net(spec: GraphSpec = FULL, steps: int = 6, seed: int = 0, shuffle
     return net.to(device).eval(), used
 
 
-__all__ = ["GraphSpec", "FULL", "synthetic_connectome", "synthetic_params", "synthetic_maps", "synthetic_boards",
+__all__ = ["GraphSpec", "FULL", "synthetic_connectome", "degree_connectome", "synthetic_params", "synthetic_maps", "synthetic_boards",
            "synthetic_net", "spectral_radius", "NeuronParams", "DenseMaps", "N_MOVES"]

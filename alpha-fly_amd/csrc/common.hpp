@@ -99,6 +99,8 @@ inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 inline bool aligned(const void *p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
 // Row stride of a state buffer of `elem`-byte entries: the batch rounded up to 64 columns, plus one 128-byte
 // line when that leaves an even number of lines per row.  A column chunk then sits at a different line offset
 // in every row, so a chunk sweep spreads over all L2 sets and channels; with a power-of-two stride it reaches a
@@ -160,7 +162,8 @@ class NoLaunchEvents {
   NoLaunchEvents &operator=(const NoLaunchEvents &) = delete;
 };
 
-// Tuning knobs set through fly_set_tuning.
+// Tuning knobs set through fly_set_tuning: the defaults that objects created afterwards capture (a plan, a dense
+// plan, a fly_sweep), and that the stateless training and download entry points read at each call.
 struct Tuning {
   int vec = 0;    // elements per lane of the step kernel, 0 = automatic
   int tiles = 0;  // batch tiles swept row-major, 0 = automatic
@@ -173,14 +176,22 @@ struct Tuning {
   int gemm_tile = 0;    // dense-map workgroup tile: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, 10 TM + TN, 0 = auto
   int step_lds = 0;     // bytes of LDS each state-step workgroup reserves (caps waves per SIMD), 0 = none
   int download_blocks = 0;  // workgroups of fly_evaluator_download when the call passes 0, 0 = automatic
-  int swept = 0;        // long-row steps of half states as a banded sweep: 0 automatic, -1 never
-  int sweep_bands = 0;  // source bands of a swept step (3 or 4), read when a plan is created; 0 = automatic
-  int sweep_order = 0;  // swept waves take their rows in the plan's searched order: 0 yes, -1 in index order
-  int sweep_paired = 0;  // swept waves walk two rows per pass: 1 always, -1 never, 0 for float32 states
+  int swept = 0;        // long-row steps as a banded sweep: 0 automatic, -1 never, 1 any step with a matrix whatever
+                        // its size (tests of small graphs)
+  int sweep_bands = 0;  // source bands of a swept step (3 or 4); 0 = automatic
+  int sweep_order = 0;  // swept waves take their rows in the searched order: 0 yes, -1 in the initial order
+  int sweep_grid = 0;   // workgroups of a swept step; 0 = one per CU
+  int sweep_piece = 0;  // split rows longer than this into pieces of at most this many non-zeros; 0 = automatic
+  int sweep_paired = 0;  // swept waves walk two rows per pass: 1 yes, 0 or -1 one row
   int sweep_slots = 0;   // swept passes of 3 slots: 3 always, 0 when a wave owns 24 rows or fewer (else 6)
   int sweep_pipe = 0;    // swept gathers of the next four rounds in flight: 0 with 3 slots, 1 also 6, -1 never
 };
-Tuning &tuning();
+// A copy of the current defaults (taken under a lock: fly_set_tuning may run on another thread).
+Tuning tuning_snapshot();
+
+struct SweepTables;
+// Sweep tables a cone has built for its steps, one entry per (step, configuration); see cone_sweep.
+struct ConeSweepCache;
 
 }  // namespace fly
 
@@ -195,6 +206,10 @@ struct fly_cone {
   std::vector<fly::DevArray<int32_t>> rows, rowptr, col, edge, prev, usrc;
   fly::DevArray<int32_t> out_src;
   fly::DevArray<int32_t> out_idx;
+  // banded-sweep tables of the steps' sub-matrices: they depend on the structure only, so every plan of the cone
+  // (each weight version) shares them; built on the first plan that needs them (guarded: plans of one cone may be
+  // created from several threads)
+  std::shared_ptr<fly::ConeSweepCache> sweep_cache;
 };
 
 struct fly_plan {
@@ -208,12 +223,20 @@ struct fly_plan {
   std::vector<fly::DevArray<int32_t>> rowptr;
   std::vector<fly::DevArray<int2>> colval;  // {local column, float bits of the weight}
   std::vector<fly::DevArray<fly::RowParam>> params;
-  // Long-row steps run as a banded sweep: per row of A_t, where each of the sweep_bands bands of source rows begins
-  // among its non-zeros (|R_t|, sweep_bands + 1); empty for the other steps.
-  std::vector<fly::DevArray<int32_t>> band_off;
-  std::vector<fly::DevArray<int32_t>> sweep_rows;  // the same steps' rows in the order the swept waves take them
-  int32_t sweep_bands = 4;
+  fly::Tuning tune;   // the tuning when the plan was created: its kernels' launch choices
+  // Long-row steps run as a banded sweep over their structure's tables (shared with the cone, or with the
+  // fly_sweep of the whole matrix); null for the other steps.
+  std::vector<std::shared_ptr<const fly::SweepTables>> sweep;
+  int64_t max_pieces = 0;   // the most pieces of split rows in any swept step (their sums take workspace)
   fly::DevArray<int32_t> out_src;  // position of out_idx[j] in R_T or -1
   fly::DevArray<float> cbase;      // value added to the carried state at the outputs
   fly::DevArray<float> c_out;      // c_T[out_idx]
+};
+
+// Banded-sweep tables of one CSR structure (fly_sweep_create), for the literal recurrence's whole matrix and the
+// training's forward products.
+struct fly_sweep {
+  int device = -1;
+  fly::Tuning tune;   // the tuning when it was created: the product's launch choices
+  std::shared_ptr<const fly::SweepTables> t;
 };

@@ -3,6 +3,7 @@
 // deterministic (order-preserving scans, row-parallel fills), so the result is bit-exact with the
 // definition in chessfly/brain.py:126-173 (LightCone) and :102-123 (_SubMatrix).
 #include "common.hpp"
+#include "sweep.hpp"
 
 namespace fly {
 namespace {
@@ -301,6 +302,7 @@ extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, 
     }
 
     auto cone = std::make_unique<fly_cone>();
+    cone->sweep_cache = std::make_shared<ConeSweepCache>();
     cone->device = current_device();
     cone->n = n;
     cone->n_edges = n_edges;

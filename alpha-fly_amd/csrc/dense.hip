@@ -29,9 +29,10 @@ namespace fly {
 
 int64_t io_block(const fly_plan &plan, int64_t batch);
 size_t io_workspace(const fly_plan &plan, int64_t batch);
+size_t plan_pieces_bytes(const fly_plan &plan, int64_t batch);
 template <typename S, typename U>
 const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, bool u_padded, void *ws,
-                        hipStream_t st);
+                        float *pieces, hipStream_t st);
 void check_plan_device(const fly_plan *plan);
 
 }  // namespace fly
@@ -44,6 +45,7 @@ struct fly_dense {
   fly::DevArray<float> enc_b, head_b, norm_mean, norm_var;
   fly::DevArray<int32_t> move_from, move_to;
   float enc_unscale = 1.f, head_unscale = 1.f, eps = 1e-8f, clip = 8.f;
+  int gemm_tile = 0;   // the gemm_tile tuning when the dense plan was created
   int64_t head_rows() const { return n_moves + 131; }
 };
 
@@ -346,10 +348,11 @@ __global__ __launch_bounds__(256) void k_gemm_split(const Split A, const Split B
 // The gemm_tile tuning key forces one: 1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, or 10 TM + TN for a workgroup tile
 // of 32 TM x 32 TN with TM in {2, 3, 4} and TN in {2, 4, 5}.
 template <class EP>
-void gemm_split(const Split &A, const Split &B, int64_t kp, float unscale, const EP &ep, hipStream_t st) {
+void gemm_split(const Split &A, const Split &B, int64_t kp, float unscale, const EP &ep, int tile_key,
+                hipStream_t st) {
   if (A.rows == 0 || B.rows == 0) return;
   auto count = [&](int bm, int bn) { return ((A.rows + bm - 1) / bm) * ((B.rows + bn - 1) / bn); };
-  int shape = tuning().gemm_tile;
+  int shape = tile_key;
   if (shape == 1) shape = 22;
   else if (shape == 2) shape = 42;
   else if (shape == 3) shape = 44;
@@ -465,7 +468,6 @@ void split_into(const T *w, int64_t ld, int64_t rows, int64_t k, float scale, _F
   check_launch("split");
 }
 
-size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 int64_t head_ld(const fly_dense &d) { return round_up(d.head_rows(), 4); }
 
@@ -490,7 +492,7 @@ void run_encoder(const fly_dense &d, const void *x, bool x_f16, int64_t ldx, int
   else
     split_into(static_cast<const float *>(x), ldx, batch, d.k, 1.0f, xh, xl, d.kp_enc, st, exact);
   gemm_split(Split{d.enc_hi.p, d.enc_lo.p, d.n_in, nullptr}, Split{xh, xl, batch, exact}, d.kp_enc, d.enc_unscale,
-             EncoderEpilogue{d.enc_b.p, gain, u, u16, ldu}, st);
+             EncoderEpilogue{d.enc_b.p, gain, u, u16, ldu}, d.gemm_tile, st);
 }
 
 template <typename S>
@@ -509,7 +511,7 @@ void run_head(const fly_dense &d, const S *state, int64_t lds, const int32_t *sr
   const int64_t ldc = head_ld(d);
   gemm_split(Split{d.head_hi.p, d.head_lo.p, d.head_rows(), nullptr}, Split{rh, rl, batch, nullptr}, d.kp_head,
              d.head_unscale,
-             HeadEpilogue{ct, ldc}, st);
+             HeadEpilogue{ct, ldc}, d.gemm_tile, st);
   const bool avec = d.n_moves % 4 == 0 && ldc % 4 == 0 && aligned(logits, 16);
   hipLaunchKernelGGL(k_assemble, dim3((unsigned)std::min<int64_t>(batch, 65535)), dim3(256), 0, st, ct, ldc, d.n_moves,
                      d.head_b.p, d.move_from.p, d.move_to.p, batch, avec, logits, wdl);
@@ -540,6 +542,7 @@ extern "C" int fly_dense_create(const fly_head_desc *h, const float *enc_w, int6
     hipStream_t st = as_stream(stream);
     auto d = std::make_unique<fly_dense>();
     d->device = current_device();
+    d->gemm_tile = tuning_snapshot().gemm_tile;
     d->n_in = n_in;
     d->k = k;
     d->kp_enc = pad_k(k);
@@ -644,7 +647,7 @@ namespace {
 size_t model_ws_block(const fly_plan &plan, const fly_dense &d, int64_t blk) {
   const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float);
   return align256((size_t)plan.n_in * state_ld(blk, sizeof(float)) * sizeof(float)) +
-         align256(2 * (size_t)plan.max_rows * (size_t)state_ld(blk, es) * es + 256) +
+         align256(2 * (size_t)plan.max_rows * (size_t)state_ld(blk, es) * es + 256) + plan_pieces_bytes(plan, blk) +
          std::max(encoder_ws(d, blk), head_ws(d, blk));
 }
 
@@ -668,6 +671,8 @@ void model_forward_blocks(const fly_plan &plan, const fly_dense &d, const void *
   void *states = base;
   const size_t es = plan.mode == FLY_MODE_DEVIATION_F16 ? sizeof(_Float16) : sizeof(float);
   base += align256(2 * (size_t)plan.max_rows * (size_t)state_ld(blk, es) * es + 256);
+  float *pieces = reinterpret_cast<float *>(base);   // the sums of split rows' pieces
+  base += plan_pieces_bytes(plan, blk);
   void *scratch_ops = base;  // the encoder's operand split, then the head's
   const size_t xelem = x_f16 ? sizeof(_Float16) : sizeof(float);
   for (int64_t c0 = 0; c0 < batch; c0 += blk) {
@@ -679,10 +684,10 @@ void model_forward_blocks(const fly_plan &plan, const fly_dense &d, const void *
     // The encoder output stays float32 in both modes: only the deviation state is carried in float16.
     run_encoder(d, xb, x_f16, ldx, nb, input_gain, u, nullptr, ldu, scratch_ops, st);
     if (plan.mode == FLY_MODE_DEVIATION_F16) {
-      const _Float16 *fin = run_cone_steps<_Float16, float>(plan, u, ldu, nb, true, states, st);
+      const _Float16 *fin = run_cone_steps<_Float16, float>(plan, u, ldu, nb, true, states, pieces, st);
       run_head<_Float16>(d, fin, lds, plan.out_src.p, plan.cbase.p, nb, lb, wb, scratch_ops, st);
     } else {
-      const float *fin = run_cone_steps<float, float>(plan, u, ldu, nb, true, states, st);
+      const float *fin = run_cone_steps<float, float>(plan, u, ldu, nb, true, states, pieces, st);
       run_head<float>(d, fin, lds, plan.out_src.p, plan.cbase.p, nb, lb, wb, scratch_ops, st);
     }
   }

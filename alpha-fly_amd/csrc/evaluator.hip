@@ -139,7 +139,8 @@ extern "C" int fly_evaluator_download(const void *src, void *dst_host, size_t by
     if (e != hipSuccess) (void)hipGetLastError();
     FLY_REQUIRE(e == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr,
                 "the destination must be pinned host memory (hipHostMalloc, torch pin_memory=True)");
-    const int wg = workgroups > 0 ? workgroups : (tuning().download_blocks > 0 ? tuning().download_blocks : 16);
+    const int tuned = tuning_snapshot().download_blocks;
+    const int wg = workgroups > 0 ? workgroups : (tuned > 0 ? tuned : 16);
     const int64_t pieces = (int64_t)((bytes + 15) / 16);
     const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(wg, (pieces + kThreads - 1) / kThreads));
     // the device address of dst_host itself, whether the runtime reports the allocation's base or the pointer's own

@@ -21,14 +21,19 @@ const char *flyprobe_last_error(void);
  * the state step streams. */
 int flyprobe_pack(const int32_t *col_dev, const float *val_dev, int64_t nnz, void *pairs_dev, void *stream);
 
-/* What the evaluator builds for a step it runs as a banded sweep, from the step matrix (rowptr nrows+1, pairs nnz):
- * per row, where each of `bands` (3 or 4) bands of source rows begins among its non-zeros (band_off, nrows x
- * (bands + 1) int32), and the order in which the swept waves take the rows (order, nrows int32), searched for a
- * sweep that walks two rows per pass when `paired` (the float32 state's default) or one; *swept (host) = 1 where
- * the evaluator would sweep this matrix, by the same rule.  Synchronises. */
-int flyprobe_band_table(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
-                        int64_t prev_rows, int32_t bands, int32_t paired, int32_t *band_off_dev, int32_t *order_dev,
-                        int32_t *swept, void *stream);
+/* The banded-sweep tables the evaluator builds for a step (its builder, build_sweep), from the step matrix (rowptr
+ * nrows+1, pairs nnz) over prev_rows source rows: cfg[6] = {bands (3 or 4), paired (the order searched for two rows per
+ * pass: the float32 state's default), workgroups (0: one per CU), force (sweep whatever the size), piece (0:
+ * automatic), search (0: the initial order)}, as the evaluator derives them from its tuning.  *sweep = NULL where the
+ * evaluator would not sweep the matrix, by the same rule.  Synchronises.  flyprobe_sweep_destroy frees it. */
+int flyprobe_sweep_create(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
+                          int64_t prev_rows, const int32_t *cfg, void **sweep, void *stream);
+int flyprobe_sweep_destroy(void *sweep);
+/* The tables of a sweep handle, as the swept kernel reads them: info[7] = {positions, pieces, split rows, rows per
+ * wave, bands, workgroups, paired}; range ((rows + pieces) x 2 bands), order (positions), split (split rows) and
+ * split_ptr (split rows + 1) copied to the given device buffers (NULL skips one). */
+int flyprobe_sweep_read(const void *sweep, int64_t *info, int32_t *range_dev, int32_t *order_dev, int32_t *split_dev,
+                        int32_t *split_ptr_dev, void *stream);
 
 /* The launch-time choice of the swept kernel that the replays mirror, as fly_set_tuning sets it for the
  * evaluator: "sweep_paired" (1 two rows per pass, -1 one, 0 by the state type).  Other keys are refused. */
@@ -38,12 +43,11 @@ int flyprobe_set_tuning(const char *key, int64_t value);
  * pair loads and gathers, chosen by the same rule from nrows, nnz and the layout) with the FMAs replaced by an
  * XOR fold and no row constants, input, carried state, cross-lane sums or stores.  rowptr (nrows+1) and pairs
  * (nnz records) are A_t; xprev (prev_rows, ldx) the previous state, __half if state_f16 else float; batch
- * columns.  band_off, order and bands (from flyprobe_band_table where it reports a sweep, else NULL, NULL, 0):
- * the replay of a swept step is the swept kernel's.  sink: at least 1 KiB, written only if the folded bits hit one value. */
+ * columns.  sweep (from flyprobe_sweep_create, or NULL): the replay of a swept step is the swept kernel's.  sink: at
+ * least 1 KiB, written only if the folded bits hit one value. */
 int flyprobe_replay_step(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
                          const void *xprev_dev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                         const int32_t *band_off_dev, const int32_t *order_dev, int32_t bands, void *sink_dev,
-                         void *stream);
+                         const void *sweep, void *sink_dev, void *stream);
 
 /* params (nrows 32-byte row records) with zero constants and the given prev (position in R_{t-1}, -1: not carried)
  * and usrc (input row, -1: none), as fly_cone_step exports them: the row reads of a replay with I/O. */
@@ -52,11 +56,11 @@ int flyprobe_pack_params(const int32_t *prev_dev, const int32_t *usrc_dev, int64
 
 /* The replay with the step's row I/O: as flyprobe_replay_step, plus each row's constants, carried state and input
  * drive u (n_in, ldu float32, padded like the model forward's; NULL: none) read and the new state xout (nrows, ldx)
- * written, without the arithmetic of the sum. */
+ * written, without the arithmetic of the sum.  The pieces of split rows store nothing and are not finished. */
 int flyprobe_replay_step_io(const int32_t *rowptr_dev, const void *pairs_dev, const void *params_dev, int64_t nrows,
                             int64_t nnz, const void *xprev_dev, int64_t prev_rows, int64_t ldx, const float *u_dev,
                             int64_t n_in, int64_t ldu, void *xout_dev, int64_t batch, int32_t state_f16,
-                            const int32_t *band_off_dev, const int32_t *order_dev, int32_t bands, void *stream);
+                            const void *sweep, void *stream);
 
 /* Uniform-random row gathers in the state step's lane layout: n reads of read_bytes (128: 8 rows per wave
  * instruction; 64: 16 rows) at byte offset idx[e] * row_bytes (16 bytes per lane) of base (`bytes` long).

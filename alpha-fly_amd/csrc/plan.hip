@@ -141,13 +141,21 @@ __global__ void k_out_base(const int32_t *__restrict__ out_idx, const int32_t *_
   cbase[j] = (mode == FLY_MODE_F32 && out_src[j] >= 0) ? 0.0f : c;
 }
 
-// Whether a swept step of this state type walks two rows per pass when its waves own over 24 rows (launch_swept's
-// rule, with the sweep_paired tuning as it stands when the plan is created).
-bool sweep_pairs(bool f32_state) {
-  return tuning().sweep_paired > 0 || (tuning().sweep_paired == 0 && f32_state);
+}  // namespace
+
+// The tables of step t of the cone under cfg: built on the first plan that asks and kept on the cone, since they
+// depend on the structure only (null when the step does not sweep).  Guarded by the cache's lock.
+std::shared_ptr<const SweepTables> cone_sweep(const fly_cone &cone, int t, const SweepConfig &cfg, hipStream_t st) {
+  ConeSweepCache &c = *cone.sweep_cache;
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (const auto &e : c.entries)
+    if (e.t == t && e.cfg == cfg) return e.tables;
+  std::shared_ptr<const SweepTables> tables =
+      build_sweep<int32_t>(cone.rowptr[t].p, cone.col[t].p, cone.rows_n[t], cone.nnz[t], cone.rows_n[t - 1], cfg, st);
+  c.entries.push_back({t, cfg, tables});
+  return tables;
 }
 
-}  // namespace
 }  // namespace fly
 
 using namespace fly;
@@ -196,9 +204,9 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
     plan->rowptr.resize(T + 1);
     plan->colval.resize(T + 1);
     plan->params.resize(T + 1);
-    plan->band_off.resize(T + 1);
-    plan->sweep_rows.resize(T + 1);
-    plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
+    plan->sweep.resize(T + 1);
+    plan->tune = tuning_snapshot();
+    const SweepConfig cfg = sweep_config(plan->tune);
 
     DevArray<float> alpha(n), k_full(n), c_a(n), c_b(n);
     hipLaunchKernelGGL(k_sigmoid, dim3(nb), dim3(kThreads), 0, st, alpha_logit, n, alpha.p);
@@ -216,13 +224,9 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
         if (cone->nnz[t])
           hipLaunchKernelGGL(k_pack, dim3(blocks_for(cone->nnz[t], kThreads)), dim3(kThreads), 0, st, cone->col[t].p,
                              cone->edge[t].p, w, cone->nnz[t], plan->colval[t].p);
-        if (sweep_suits(plan->rowptr[t].p, cone->rows_n[t - 1], nr, cone->nnz[t], st)) {
-          plan->band_off[t].alloc((size_t)nr * (plan->sweep_bands + 1));
-          hipLaunchKernelGGL(k_band_off<int2>, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, plan->rowptr[t].p,
-                             plan->colval[t].p, nr, cone->rows_n[t - 1], plan->sweep_bands, plan->band_off[t].p);
-          plan->sweep_rows[t].alloc((size_t)nr);
-          build_sweep_order(plan->rowptr[t].p, plan->band_off[t].p, plan->sweep_bands, nr,
-                            sweep_pairs(mode == FLY_MODE_F32), plan->sweep_rows[t].p, st);
+        if (plan->tune.swept >= 0) {
+          plan->sweep[t] = cone_sweep(*cone, t, cfg, st);
+          if (plan->sweep[t]) plan->max_pieces = std::max(plan->max_pieces, plan->sweep[t]->pieces);
         }
       }
       if (nr) {
@@ -253,7 +257,8 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
 }
 
 extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *crow, const int32_t *pre, const float *w,
-                                    const float *alpha_logit, float h_max, void *stream, fly_plan **out) {
+                                    const float *alpha_logit, float h_max, const fly_sweep *sweep, void *stream,
+                                    fly_plan **out) {
   return guard([&] {
     FLY_REQUIRE(out != nullptr, "out is null");
     *out = nullptr;
@@ -288,16 +293,14 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
     plan->params[0].alloc(n);
     hipLaunchKernelGGL(k_params_full, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, alpha.p, h_max, n,
                        plan->params[0].p);
-    plan->band_off.resize(1);
-    plan->sweep_rows.resize(1);
-    plan->sweep_bands = tuning().sweep_bands == 3 ? 3 : kSweepBands;
-    if (sweep_suits(plan->rowptr[0].p, n, n, n_edges, st)) {
-      plan->band_off[0].alloc((size_t)n * (plan->sweep_bands + 1));
-      hipLaunchKernelGGL(k_band_off<int2>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, st, plan->rowptr[0].p,
-                         plan->colval[0].p, n, n, plan->sweep_bands, plan->band_off[0].p);
-      plan->sweep_rows[0].alloc((size_t)n);
-      build_sweep_order(plan->rowptr[0].p, plan->band_off[0].p, plan->sweep_bands, n, sweep_pairs(true),
-                        plan->sweep_rows[0].p, st);
+    plan->tune = tuning_snapshot();
+    plan->sweep.resize(1);
+    if (sweep && sweep->t && plan->tune.swept >= 0) {
+      FLY_REQUIRE(sweep->device == plan->device, "the sweep tables live on another device");
+      FLY_REQUIRE(sweep->t->nrows == n && sweep->t->ncols == n && sweep->t->nnz == n_edges,
+                  "the sweep tables belong to another structure");
+      plan->sweep[0] = sweep->t;
+      plan->max_pieces = sweep->t->pieces;
     }
     check_launch("full plan");
     FLY_HIP(hipStreamSynchronize(st));
@@ -335,5 +338,56 @@ extern "C" int fly_plan_matrix(const fly_plan *plan, int32_t t, int32_t *rowptr,
                          col, val);
       check_launch("plan matrix");
     }
+  });
+}
+
+extern "C" int fly_sweep_create(const int32_t *rowptr, const int32_t *col, int64_t nrows, int64_t nnz, int64_t ncols,
+                                void *stream, fly_sweep **out) {
+  return guard([&] {
+    FLY_REQUIRE(out != nullptr, "out is null");
+    *out = nullptr;
+    FLY_REQUIRE(nrows >= 0 && nnz >= 0 && ncols >= 0, "negative size");
+    FLY_REQUIRE(rowptr && (nnz == 0 || col), "null argument");
+    auto sw = std::make_unique<fly_sweep>();
+    sw->device = current_device();
+    sw->tune = tuning_snapshot();
+    if (sw->tune.swept < 0) return;   // the sweep is off: nothing to build
+    sw->t = build_sweep<int32_t>(rowptr, col, nrows, nnz, ncols, sweep_config(sw->tune), as_stream(stream));
+    if (sw->t) *out = sw.release();
+  });
+}
+
+extern "C" int fly_sweep_destroy(fly_sweep *sweep) {
+  return guard([&] { delete sweep; });
+}
+
+extern "C" int fly_sweep_info(const fly_sweep *sweep, int64_t *info) {
+  return guard([&] {
+    FLY_REQUIRE(sweep && sweep->t && info, "null argument");
+    const SweepTables &t = *sweep->t;
+    info[0] = t.npos;
+    info[1] = t.pieces;
+    info[2] = t.split_rows;
+    info[3] = t.rows_per_wave;
+    info[4] = t.bands;
+    info[5] = t.grid;
+    info[6] = (int64_t)reinterpret_cast<uintptr_t>(t.order.p);
+  });
+}
+
+extern "C" int fly_plan_sweep_info(const fly_plan *plan, int32_t t, int64_t *info) {
+  return guard([&] {
+    FLY_REQUIRE(plan && info, "null argument");
+    FLY_REQUIRE(plan->full ? t == 1 : (t >= 1 && t <= plan->steps), "step out of range");
+    const SweepTables *s = plan->sweep[plan->full ? 0 : t].get();
+    for (int i = 0; i < 7; ++i) info[i] = 0;
+    if (!s) return;
+    info[0] = s->npos;
+    info[1] = s->pieces;
+    info[2] = s->split_rows;
+    info[3] = s->rows_per_wave;
+    info[4] = s->bands;
+    info[5] = s->grid;
+    info[6] = (int64_t)reinterpret_cast<uintptr_t>(s->order.p);
   });
 }

@@ -2,8 +2,8 @@
 //
 // flyprobe_replay_step runs the state step's own kernels (step_kernels.hpp) built with REPLAY = 1: the same
 // launch shape, wave numbering, per-row pair records and buffer-offset gathers as the evaluator's step on the
-// same matrix and state layout (the banded sweep where the evaluator sweeps, given the band table that
-// flyprobe_band_table builds), without the arithmetic, the row inputs or the stores.  Its time is what the
+// same matrix and state layout (the banded sweep where the evaluator sweeps, over the tables that
+// flyprobe_sweep_create builds with the evaluator's builder), without the arithmetic, the row inputs or the stores.  Its time is what the
 // step's gather stream alone costs, which is the ceiling the fused step is measured against.
 // flyprobe_replay_step_io (REPLAY = 2) adds the step's row reads (carried state, input drive, constants) and its
 // stores: everything but the arithmetic of the sum.
@@ -60,11 +60,10 @@ __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__res
 // passes the band table of flyprobe_band_table then), else lane groups of 16-byte lanes, or row slots of 16- or
 // 32-byte lanes, in groups of 8 lanes with 4 rounds in flight.
 template <int MODE, typename S, typename U>
-void replay(StepArgs<S, U> a, int64_t nnz, int64_t prev_rows, hipStream_t st) {
+void replay(StepArgs<S, U> a, int64_t nnz, const SweepTables *sweep, hipStream_t st) {
   const StepShape sh = shape_step(a, (double)nnz / (double)a.nrows, Tuning{});
-  (void)prev_rows;
-  if (a.band_off && sh.v == 16 / (int)sizeof(S) && sh.groups == 8 && !sh.rows_mode && a.xbytes) {
-    launch_swept<S, U, MODE>(a, st);
+  if (sweep && sh.v == 16 / (int)sizeof(S) && sh.groups == 8 && a.xbytes) {
+    launch_swept<S, U, MODE>(a, *sweep, st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) throw Error{1, std::string("replay launch: ") + hipGetErrorString(e)};
     return;
@@ -144,29 +143,52 @@ extern "C" int flyprobe_set_tuning(const char *key, int64_t value) {
   });
 }
 
-extern "C" int flyprobe_band_table(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
-                                   int64_t prev_rows, int32_t bands, int32_t paired, int32_t *band_off, int32_t *order,
-                                   int32_t *swept, void *stream) {
+extern "C" int flyprobe_sweep_create(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
+                                     int64_t prev_rows, const int32_t *cfg, void **out, void *stream) {
   return probe_guard([&] {
-    FLY_REQUIRE(rowptr && pairs && band_off && order && swept, "null argument");
+    FLY_REQUIRE(rowptr && pairs && cfg && out, "null argument");
+    *out = nullptr;
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX / 8 && prev_rows > 0 && nnz >= 0, "size out of range");
-    FLY_REQUIRE(bands == 3 || bands == 4, "bands must be 3 or 4");
-    *swept = sweep_suits(rowptr, prev_rows, nrows, nnz, as_stream(stream)) ? 1 : 0;
-    hipLaunchKernelGGL(k_band_off<int2>, dim3(blocks_for(nrows, 256)), dim3(256), 0, as_stream(stream), rowptr,
-                       static_cast<const int2 *>(pairs), nrows, prev_rows, bands, band_off);
-    build_sweep_order(rowptr, band_off, bands, nrows, paired != 0, order, as_stream(stream));
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) throw Error{1, std::string("band table launch: ") + hipGetErrorString(e)};
+    SweepConfig c;
+    c.bands = cfg[0];
+    c.paired = cfg[1];
+    c.grid = cfg[2];
+    c.force = cfg[3];
+    c.piece = cfg[4];
+    c.search = cfg[5];
+    auto t = build_sweep<int2>(rowptr, static_cast<const int2 *>(pairs), nrows, nnz, prev_rows, c, as_stream(stream));
+    if (t) *out = new std::shared_ptr<const SweepTables>(std::move(t));
+  });
+}
+
+extern "C" int flyprobe_sweep_destroy(void *sweep) {
+  return probe_guard([&] { delete static_cast<std::shared_ptr<const SweepTables> *>(sweep); });
+}
+
+extern "C" int flyprobe_sweep_read(const void *sweep, int64_t *info, int32_t *range, int32_t *order, int32_t *split,
+                                   int32_t *split_ptr, void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(sweep && info, "null argument");
+    const SweepTables &t = **static_cast<const std::shared_ptr<const SweepTables> *>(sweep);
+    const int64_t v[7] = {t.npos, t.pieces, t.split_rows, t.rows_per_wave, t.bands, t.grid, t.paired};
+    for (int i = 0; i < 7; ++i) info[i] = v[i];
+    hipStream_t st = as_stream(stream);
+    auto copy = [&](int32_t *dst, const DevArray<int32_t> &src) {
+      if (dst && src.n) FLY_HIP(hipMemcpyAsync(dst, src.p, sizeof(int32_t) * src.n, hipMemcpyDeviceToDevice, st));
+    };
+    copy(range, t.range);
+    copy(order, t.order);
+    copy(split, t.split);
+    copy(split_ptr, t.split_ptr);
   });
 }
 
 extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, int64_t nrows, int64_t nnz,
                                     const void *xprev, int64_t prev_rows, int64_t ldx, int64_t batch, int32_t state_f16,
-                                    const int32_t *band_off, const int32_t *order, int32_t bands, void *sink,
-                                    void *stream) {
+                                    const void *sweep, void *sink, void *stream) {
   return probe_guard([&] {
-    FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
     FLY_REQUIRE(rowptr && pairs && xprev && sink, "null argument");
+    const SweepTables *tables = sweep ? static_cast<const std::shared_ptr<const SweepTables> *>(sweep)->get() : nullptr;
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
     FLY_REQUIRE(aligned(sink, 256), "sink must be 256-byte aligned");
@@ -183,13 +205,10 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       a.nrows = (int32_t)nrows;
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
-      a.band_off = band_off;
-      a.sweep_rows = band_off ? order : nullptr;
-      a.sweep_bands = bands;
       a.sweep_paired = g_sweep.paired;
       a.sweep_slots = g_sweep.slots;
       a.sweep_pipe = g_sweep.pipe;
-      replay<1>(a, nnz, prev_rows, as_stream(stream));
+      replay<1>(a, nnz, tables, as_stream(stream));
     };
     if (state_f16)
       run(_Float16(0));
@@ -214,10 +233,10 @@ extern "C" int flyprobe_pack_params(const int32_t *prev, const int32_t *usrc, in
 extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs, const void *params, int64_t nrows,
                                        int64_t nnz, const void *xprev, int64_t prev_rows, int64_t ldx, const float *u,
                                        int64_t n_in, int64_t ldu, void *xout, int64_t batch, int32_t state_f16,
-                                       const int32_t *band_off, const int32_t *order, int32_t bands, void *stream) {
+                                       const void *sweep, void *stream) {
   return probe_guard([&] {
-    FLY_REQUIRE(!band_off || bands == 3 || bands == 4, "bands must be 3 or 4");
     FLY_REQUIRE(rowptr && pairs && params && xprev && xout, "null argument");
+    const SweepTables *tables = sweep ? static_cast<const std::shared_ptr<const SweepTables> *>(sweep)->get() : nullptr;
     FLY_REQUIRE(nrows > 0 && nrows < (int64_t)INT32_MAX && nnz >= 0 && nnz < (int64_t)INT32_MAX, "size out of range");
     FLY_REQUIRE(prev_rows > 0 && batch > 0 && batch < (int64_t)INT32_MAX / 2 && ldx >= batch, "bad state layout");
     FLY_REQUIRE(!u || (n_in > 0 && ldu >= batch), "bad input drive");
@@ -237,13 +256,10 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       a.nrows = (int32_t)nrows;
       a.batch = (int32_t)batch;
       a.xbytes = buffer_bytes(prev_rows, ldx, sizeof(S));
-      a.band_off = band_off;
-      a.sweep_rows = band_off ? order : nullptr;
-      a.sweep_bands = bands;
       a.sweep_paired = g_sweep.paired;
       a.sweep_slots = g_sweep.slots;
       a.sweep_pipe = g_sweep.pipe;
-      replay<2>(a, nnz, prev_rows, as_stream(stream));
+      replay<2>(a, nnz, tables, as_stream(stream));
     };
     if (state_f16)
       run(_Float16(0));

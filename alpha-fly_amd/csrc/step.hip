@@ -2,15 +2,23 @@
 //
 // One pass per step fuses the reference's SpMM, index_add_, gather and jiterator update
 // (chessfly/brain.py:273-277, 310-313, 217-223); the kernels and their launch shapes are in step_kernels.hpp.
+#include <cmath>
+#include <cstring>
+#include <mutex>
 #include <type_traits>
 
 #include "step_kernels.hpp"
 
 namespace fly {
 
-Tuning &tuning() {
-  static Tuning t;
-  return t;
+namespace {
+std::mutex g_tuning_mu;
+Tuning g_tuning;   // the defaults fly_set_tuning sets
+}  // namespace
+
+Tuning tuning_snapshot() {
+  std::lock_guard<std::mutex> lock(g_tuning_mu);
+  return g_tuning;
 }
 
 namespace {
@@ -18,14 +26,14 @@ namespace {
 // Deviation mode (half state) updates with p + a (x - p) like the reference's fused kernel; float32 mode
 // with torch.lerp's formula, like the reference's CPU path.
 template <typename S, typename U, int V>
-void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, hipStream_t st) {
+void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, int step_lds, hipStream_t st) {
   const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
   constexpr bool kTL = sizeof(S) == 4;
   // the kernels use no LDS: a reservation only caps the workgroups (waves per SIMD) a CU runs at once
-  const unsigned lds = (unsigned)std::max(0, tuning().step_lds);
+  const unsigned lds = (unsigned)std::max(0, step_lds);
   if constexpr (V * sizeof(S) == 32) {
     // 32-byte lanes exist for the row slots of half states only (state_step picks them for nothing else)
     hipLaunchKernelGGL((k_state_step_rows<S, U, V, 8, 4, kTL>), grid, block, lds, st, a);
@@ -65,34 +73,38 @@ void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, h
     hipLaunchKernelGGL((k_state_step<S, U, V, 8, kTL>), grid, block, lds, st, a);
 }
 
+// One state step.  `sweep`: the step matrix's banded-sweep tables (null: the step does not sweep); a.pieces must then
+// hold sweep_pieces_bytes(sweep, batch) bytes.
 template <typename S, typename U>
-void state_step(StepArgs<S, U> a, double avg_nnz, hipStream_t st) {
+void state_step(StepArgs<S, U> a, double avg_nnz, const Tuning &tune, const SweepTables *sweep, hipStream_t st) {
   if (a.nrows == 0 || a.batch == 0) return;
-  const StepShape sh = shape_step(a, avg_nnz, tuning());
+  Tuning tu = tune;
+  if (sweep && tune.swept > 0) tu.rows_mode = -1;   // a forced sweep takes steps of short rows too
+  const StepShape sh = shape_step(a, avg_nnz, tu);
   const int v = sh.v, groups = sh.groups, unroll = sh.unroll;
   const bool rows_mode = sh.rows_mode;
-  // long-row steps with a band table: the banded sweep, on the grouped kernel's lane layout
-  if (a.band_off && tuning().swept >= 0 && v == 16 / (int)sizeof(S) && groups == 8 && !rows_mode && a.rowptr &&
-      a.xprev && a.xbytes && !(a.out_exact && a.batch % v)) {
+  // long-row steps with sweep tables: the banded sweep, on the grouped kernel's lane layout
+  if (sweep && tune.swept >= 0 && v == 16 / (int)sizeof(S) && groups == 8 && !rows_mode && a.rowptr && a.xprev &&
+      a.xbytes && !(a.out_exact && a.batch % v)) {
     LaunchTimer timer(FLY_K_STATE_STEP, st);
-    a.sweep_paired = tuning().sweep_paired;
-    a.sweep_slots = tuning().sweep_slots;
-    a.sweep_pipe = tuning().sweep_pipe;
-    launch_swept<S, U, 0>(a, st);
+    a.sweep_paired = tune.sweep_paired;
+    a.sweep_slots = tune.sweep_slots;
+    a.sweep_pipe = tune.sweep_pipe;
+    launch_swept<S, U, 0>(a, *sweep, st);
     check_launch("swept state step");
     return;
   }
   switch (v) {
     // only 16-byte lanes (V = 16 / sizeof(S)) have grouped and row-slot kernels, and 32-byte lanes of half
     // states a row-slot kernel; pick_shape sets groups to 1 for every other V, so rows_mode is false there too
-    case 1: launch_v<S, U, 1>(a, 1, unroll, false, st); break;
-    case 2: launch_v<S, U, 2>(a, 1, unroll, false, st); break;
-    case 4: launch_v<S, U, 4>(a, groups, unroll, rows_mode, st); break;
+    case 1: launch_v<S, U, 1>(a, 1, unroll, false, tune.step_lds, st); break;
+    case 2: launch_v<S, U, 2>(a, 1, unroll, false, tune.step_lds, st); break;
+    case 4: launch_v<S, U, 4>(a, groups, unroll, rows_mode, tune.step_lds, st); break;
     case 8:
-      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, groups, unroll, rows_mode, st);
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 8>(a, groups, unroll, rows_mode, tune.step_lds, st);
       break;
     default:
-      if constexpr (sizeof(S) == 2) launch_v<S, U, 16>(a, groups, unroll, rows_mode, st);
+      if constexpr (sizeof(S) == 2) launch_v<S, U, 16>(a, groups, unroll, rows_mode, tune.step_lds, st);
       break;
   }
   check_launch("state step");
@@ -221,17 +233,27 @@ size_t state_bytes(const fly_plan &plan) { return plan.mode == FLY_MODE_DEVIATIO
 
 int64_t io_block(const fly_plan &plan, int64_t batch) { return block_cols(plan.max_rows, state_bytes(plan), batch); }
 
-size_t io_workspace(const fly_plan &plan, int64_t batch) {
+size_t plan_pieces_bytes(const fly_plan &plan, int64_t batch) {
+  return plan.max_pieces ? align256((size_t)plan.max_pieces * (size_t)round_up(batch, 64) * sizeof(float)) : 0;
+}
+
+size_t io_states_bytes(const fly_plan &plan, int64_t blk) {
   const size_t es = state_bytes(plan);
-  return 2 * (size_t)plan.max_rows * (size_t)state_ld(io_block(plan, batch), es) * es + 256;
+  return align256(2 * (size_t)plan.max_rows * (size_t)state_ld(blk, es) * es + 256);
+}
+
+size_t io_workspace(const fly_plan &plan, int64_t batch) {
+  const int64_t blk = io_block(plan, batch);
+  return io_states_bytes(plan, blk) + plan_pieces_bytes(plan, blk);
 }
 
 // Runs steps 1..T of a light-cone plan.  Returns the final state (null if R_T is empty) in one of the two
 // workspace buffers, whose row stride is state_ld(batch, sizeof(S)).  u_padded: the drive u is the library's own
-// workspace, whose rows may be read up to the batch rounded up to 64 columns.
+// workspace, whose rows may be read up to the batch rounded up to 64 columns.  pieces: plan_pieces_bytes(plan,
+// batch) bytes for the sums of split rows.
 template <typename S, typename U>
 const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t batch, bool u_padded, void *ws,
-                        hipStream_t st) {
+                        float *pieces, hipStream_t st) {
   const int64_t lds = state_ld(batch, sizeof(S));
   S *buf[2] = {reinterpret_cast<S *>(ws), reinterpret_cast<S *>(ws) + (size_t)plan.max_rows * lds};
   const S *prev = nullptr;
@@ -256,12 +278,9 @@ const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t b
     a.nrows = (int32_t)nr;
     a.batch = (int32_t)batch;
     a.xbytes = prev ? buffer_bytes(plan.rows_n[t - 1], lds, sizeof(S)) : 0;
-    if ((size_t)t < plan.band_off.size()) {
-      a.band_off = plan.band_off[t].p;
-      a.sweep_rows = tuning().sweep_order >= 0 ? plan.sweep_rows[t].p : nullptr;
-      a.sweep_bands = plan.sweep_bands;
-    }
-    state_step(a, nr ? (double)plan.nnz[t] / (double)nr : 0.0, st);
+    a.pieces = pieces;
+    a.sweep_exact = std::isfinite(plan.h_max) ? 0 : 1;   // no upper clamp: a state may overflow to inf
+    state_step(a, nr ? (double)plan.nnz[t] / (double)nr : 0.0, plan.tune, plan.sweep[t].get(), st);
     prev = buf[cur];
     cur ^= 1;
   }
@@ -279,11 +298,11 @@ void write_outputs(const fly_plan &plan, const S *state, int64_t batch, float *o
 }
 
 template const _Float16 *run_cone_steps<_Float16, _Float16>(const fly_plan &, const _Float16 *, int64_t, int64_t, bool,
-                                                            void *, hipStream_t);
+                                                            void *, float *, hipStream_t);
 template const _Float16 *run_cone_steps<_Float16, float>(const fly_plan &, const float *, int64_t, int64_t, bool, void *,
-                                                         hipStream_t);
+                                                         float *, hipStream_t);
 template const float *run_cone_steps<float, float>(const fly_plan &, const float *, int64_t, int64_t, bool, void *,
-                                                   hipStream_t);
+                                                   float *, hipStream_t);
 
 void check_plan_device(const fly_plan *plan) {
   FLY_REQUIRE(plan != nullptr, "plan is null");
@@ -311,15 +330,16 @@ extern "C" int fly_forward_io(const fly_plan *plan, const void *u_in, int64_t ld
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     hipStream_t st = as_stream(stream);
     const int64_t blk = io_block(*plan, batch);
+    float *pieces = reinterpret_cast<float *>(static_cast<char *>(ws) + io_states_bytes(*plan, blk));
     for (int64_t c0 = 0; c0 < batch; c0 += blk) {
       const int64_t nb = std::min(blk, batch - c0);
       if (plan->mode == FLY_MODE_DEVIATION_F16) {
         const _Float16 *u = plan->n_in ? static_cast<const _Float16 *>(u_in) + c0 : nullptr;
-        const _Float16 *fin = run_cone_steps<_Float16, _Float16>(*plan, u, ldu, nb, false, ws, st);
+        const _Float16 *fin = run_cone_steps<_Float16, _Float16>(*plan, u, ldu, nb, false, ws, pieces, st);
         write_outputs<_Float16>(*plan, fin, nb, out + c0, ldo, st);
       } else {
         const float *u = plan->n_in ? static_cast<const float *>(u_in) + c0 : nullptr;
-        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, false, ws, st);
+        const float *fin = run_cone_steps<float, float>(*plan, u, ldu, nb, false, ws, pieces, st);
         write_outputs<float>(*plan, fin, nb, out + c0, ldo, st);
       }
     }
@@ -373,7 +393,8 @@ extern "C" int fly_forward_io_f64(const fly_plan *plan, const double *u_in, int6
 extern "C" size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch) {
   if (!plan) return 0;
   const int64_t blk = block_cols(plan->n, sizeof(float), batch);
-  return 2 * (size_t)plan->n * (size_t)state_ld(blk, sizeof(float)) * sizeof(float) + 256;
+  return align256(2 * (size_t)plan->n * (size_t)state_ld(blk, sizeof(float)) * sizeof(float) + 256) +
+         plan_pieces_bytes(*plan, blk);
 }
 
 extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, const float *bias, int64_t batch,
@@ -401,6 +422,8 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
     FLY_REQUIRE(ws && ws_bytes >= fly_forward_literal_workspace(plan, batch), "workspace too small");
     FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
     const int64_t blk = block_cols(n, sizeof(float), batch);
+    float *pieces = reinterpret_cast<float *>(
+        static_cast<char *>(ws) + align256(2 * (size_t)n * (size_t)state_ld(blk, sizeof(float)) * sizeof(float) + 256));
     for (int64_t c0 = 0; c0 < batch; c0 += blk) {
       const int64_t nb = std::min(blk, batch - c0);
       const int64_t lds = state_ld(nb, sizeof(float));
@@ -423,12 +446,9 @@ extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, 
         a.nrows = (int32_t)n;
         a.batch = (int32_t)nb;
         a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
-        if (!plan->band_off.empty()) {
-          a.band_off = plan->band_off[0].p;
-          a.sweep_rows = tuning().sweep_order >= 0 ? plan->sweep_rows[0].p : nullptr;
-          a.sweep_bands = plan->sweep_bands;
-        }
-        state_step(a, (double)plan->nnz[0] / (double)n, st);
+        a.pieces = pieces;
+        a.sweep_exact = std::isfinite(plan->h_max) ? 0 : 1;
+        state_step(a, (double)plan->nnz[0] / (double)n, plan->tune, plan->sweep[0].get(), st);
         prev = buf[cur];
         cur ^= 1;
       }
@@ -481,8 +501,14 @@ extern "C" int fly_forward_literal_f64(const fly_plan *plan, double *u, int64_t 
   });
 }
 
+extern "C" size_t fly_plan_step_workspace(const fly_plan *plan, int32_t t, int64_t batch) {
+  if (!plan || (plan->full ? t != 1 : (t < 1 || t > plan->steps))) return 0;
+  return sweep_pieces_bytes(plan->sweep[plan->full ? 0 : t].get(), batch);
+}
+
 extern "C" int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev, int64_t ldx, const void *u_in,
-                             int64_t ldu, int64_t batch, void *xout, int64_t ldo, void *stream) {
+                             int64_t ldu, int64_t batch, void *xout, int64_t ldo, void *ws, size_t ws_bytes,
+                             void *stream) {
   return guard([&] {
     check_plan_device(plan);
     FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
@@ -496,6 +522,9 @@ extern "C" int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev,
     FLY_REQUIRE(plan->full || np > 0 || !xprev, "R_{t-1} is empty: the previous state must be NULL");
     FLY_REQUIRE(plan->full || np == 0 || t == 1 || xprev, "the previous state is missing");
     FLY_REQUIRE(!u_in || ldu >= batch, "bad input drive");
+    const SweepTables *sweep = plan->sweep[ti].get();
+    const size_t need = sweep_pieces_bytes(sweep, batch);
+    FLY_REQUIRE(need == 0 || (ws && ws_bytes >= need && aligned(ws, 256)), "workspace too small or misaligned");
     // the states are caller buffers: out_exact keeps every read and write inside columns [0, batch) of a row
     hipStream_t st = as_stream(stream);
     auto run = [&](auto *xo, const auto *xp, const auto *u) {
@@ -516,7 +545,9 @@ extern "C" int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev,
       a.nrows = (int32_t)nr;
       a.batch = (int32_t)batch;
       a.xbytes = xp ? buffer_bytes(np, ldx, sizeof(S)) : 0;
-      state_step(a, nr ? (double)plan->nnz[ti] / (double)nr : 0.0, st);
+      a.pieces = static_cast<float *>(ws);
+      a.sweep_exact = 1;   // caller states may hold anything
+      state_step(a, nr ? (double)plan->nnz[ti] / (double)nr : 0.0, plan->tune, sweep, st);
     };
     if (plan->mode == FLY_MODE_DEVIATION_F16)
       run(static_cast<_Float16 *>(xout), static_cast<const _Float16 *>(xprev), static_cast<const _Float16 *>(u_in));
@@ -525,27 +556,61 @@ extern "C" int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev,
   });
 }
 
+namespace fly {
+namespace {
+
+// The tuning keys: name, field and the range a value is clamped to.
+struct TuningKey {
+  const char *name;
+  int Tuning::*field;
+  int64_t lo, hi;
+};
+constexpr int64_t kAny = (int64_t)1 << 30;
+const TuningKey kTuningKeys[] = {
+    {"vec", &Tuning::vec, -kAny, kAny},
+    {"unroll", &Tuning::unroll, -kAny, kAny},
+    {"groups", &Tuning::groups, -kAny, kAny},
+    {"rows_mode", &Tuning::rows_mode, -kAny, kAny},
+    {"rows_vec", &Tuning::rows_vec, -kAny, kAny},
+    {"nt_store", &Tuning::nt_store, -kAny, kAny},
+    {"tiles", &Tuning::tiles, -kAny, kAny},
+    {"spmm_groups", &Tuning::spmm_groups, -kAny, kAny},
+    {"gemm_tile", &Tuning::gemm_tile, -kAny, kAny},
+    {"download_blocks", &Tuning::download_blocks, -kAny, kAny},
+    {"swept", &Tuning::swept, -1, 1},
+    {"sweep_bands", &Tuning::sweep_bands, -kAny, kAny},
+    {"sweep_order", &Tuning::sweep_order, -kAny, kAny},
+    {"sweep_grid", &Tuning::sweep_grid, 0, 65535},
+    {"sweep_piece", &Tuning::sweep_piece, 0, 1 << 20},
+    {"sweep_paired", &Tuning::sweep_paired, -kAny, kAny},
+    {"sweep_slots", &Tuning::sweep_slots, -kAny, kAny},
+    {"sweep_pipe", &Tuning::sweep_pipe, -kAny, kAny},
+    {"step_lds", &Tuning::step_lds, 0, 65536},
+};
+
+const TuningKey &tuning_key(const char *key) {
+  FLY_REQUIRE(key != nullptr, "key is null");
+  for (const TuningKey &k : kTuningKeys)
+    if (std::strcmp(k.name, key) == 0) return k;
+  throw Error{FLY_ERR_INVALID, std::string("unknown tuning key ") + key};
+}
+
+}  // namespace
+}  // namespace fly
+
 extern "C" int fly_set_tuning(const char *key, int64_t value) {
   return guard([&] {
-    FLY_REQUIRE(key != nullptr, "key is null");
-    const std::string k(key);
-    if (k == "vec") tuning().vec = (int)value;
-    else if (k == "unroll") tuning().unroll = (int)value;
-    else if (k == "groups") tuning().groups = (int)value;
-    else if (k == "rows_mode") tuning().rows_mode = (int)value;
-    else if (k == "rows_vec") tuning().rows_vec = (int)value;
-    else if (k == "nt_store") tuning().nt_store = (int)value;
-    else if (k == "tiles") tuning().tiles = (int)value;
-    else if (k == "spmm_groups") tuning().spmm_groups = (int)value;
-    else if (k == "gemm_tile") tuning().gemm_tile = (int)value;
-    else if (k == "download_blocks") tuning().download_blocks = (int)value;
-    else if (k == "swept") tuning().swept = (int)value;
-    else if (k == "sweep_bands") tuning().sweep_bands = (int)value;
-    else if (k == "sweep_order") tuning().sweep_order = (int)value;
-    else if (k == "sweep_paired") tuning().sweep_paired = (int)value;
-    else if (k == "sweep_slots") tuning().sweep_slots = (int)value;
-    else if (k == "sweep_pipe") tuning().sweep_pipe = (int)value;
-    else if (k == "step_lds") tuning().step_lds = (int)std::min<int64_t>(std::max<int64_t>(value, 0), 65536);
-    else FLY_REQUIRE(false, "unknown tuning key " + k);
+    const TuningKey &k = tuning_key(key);
+    std::lock_guard<std::mutex> lock(g_tuning_mu);
+    g_tuning.*k.field = (int)std::min(std::max(value, k.lo), k.hi);
+  });
+}
+
+extern "C" int fly_get_tuning(const char *key, int64_t *value) {
+  return guard([&] {
+    const TuningKey &k = tuning_key(key);
+    FLY_REQUIRE(value != nullptr, "value is null");
+    std::lock_guard<std::mutex> lock(g_tuning_mu);
+    *value = g_tuning.*k.field;
   });
 }

@@ -15,8 +15,11 @@
 // builds; the evaluator library instantiates only REPLAY = 0).
 #pragma once
 
+#include <atomic>
+
 #include "common.hpp"
 #include "device.hpp"
+#include "sweep.hpp"
 
 namespace fly {
 
@@ -87,14 +90,19 @@ struct StepArgs {
   int32_t out_exact;       // caller buffers: nothing past column batch - 1 of a row may be read or written
   int32_t nt_store;        // write the new state with non-temporal stores
   uint32_t xbytes;         // bytes of X_{t-1} (rows of X_{t-1} * ldx * sizeof(S)) when below 2^31, else 0
-  const int32_t *band_off; // swept steps: (nrows, bands + 1) band boundaries in colval, or null
-  const int32_t *sweep_rows; // swept steps: the rows in the order the waves take them, or null (index order)
-  int32_t rows_per_wave;   // swept steps: consecutive positions of that order each wave owns (set by launch_swept)
-  int32_t sweep_bands;     // swept steps: bands of band_off (3 or 4)
-  int32_t sweep_paired;    // swept steps: two rows per pass (1), one (-1), by the state type (0)
-  int32_t sweep_slots;     // swept steps: 3 forces passes of 3 slots (0: 6 slots when a wave owns over 24 rows)
-  int32_t sweep_pipe;      // swept steps: the next four rounds' gathers in flight during the sums: 0 with 3 slots,
-                           // 1 also with 6, -1 never
+  // swept steps (set by launch_swept from the structure's SweepTables)
+  const int32_t *sweep_range;  // (rows + pieces, 2 * bands) band ranges in colval
+  const int32_t *sweep_order;  // (npos) the rows and pieces in the order the waves take them
+  int32_t sweep_npos;          // positions of that order
+  int32_t sweep_vrows;         // rows + pieces: order entries at or past it read as no row
+  int32_t rows_per_wave;       // consecutive positions of the order each wave owns
+  float *pieces;               // raw sums of the pieces of split rows (pieces, ldp), float32
+  int64_t ldp;
+  // launch-time choices of a swept step (the plan's tuning)
+  int32_t sweep_paired;    // two rows per pass (1), one (-1), by the state type (0)
+  int32_t sweep_slots;     // 3 forces passes of 3 slots (0: 6 slots when a wave owns over 24 rows)
+  int32_t sweep_pipe;      // the next four rounds' gathers in flight during the sums: 0 with 3 slots, 1 also 6, -1 never
+  int32_t sweep_exact;     // paired passes change only the owning row's sums (states that may hold inf or NaN)
 };
 
 // Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
@@ -134,11 +142,9 @@ struct RowInputs {
   bool has_u, carried;
 };
 
-// The constants of each lane group's row for groups of 8 lanes: lane s reads word s of the 32-byte record and the
-// group's lanes exchange them, one 4-byte load per lane instead of eight lanes each reading all 32 bytes.
-template <typename S, typename U>
-__device__ __forceinline__ RowParam row_param_shared8(const StepArgs<S, U> &a, uint32_t row, bool has_row, int s) {
-  const int word = has_row ? reinterpret_cast<const int *>(a.params + row)[s] : 0;
+// The constants of each lane group's row from word s of the record, held by lane s of the group: the group's lanes
+// exchange the 8 words (every lane of the group must execute this).
+__device__ __forceinline__ RowParam row_param_from_word(int word) {
   int w[8];
   static_for<8>([&](auto J) { w[decltype(J)::value] = group_bcast<8, decltype(J)::value>(word); });
   RowParam p;
@@ -151,6 +157,13 @@ __device__ __forceinline__ RowParam row_param_shared8(const StepArgs<S, U> &a, u
   p.prev = w[6];
   p.usrc = w[7];
   return p;
+}
+
+// The constants of each lane group's row for groups of 8 lanes: lane s reads word s of the 32-byte record and the
+// group's lanes exchange them, one 4-byte load per lane instead of eight lanes each reading all 32 bytes.
+template <typename S, typename U>
+__device__ __forceinline__ RowParam row_param_shared8(const StepArgs<S, U> &a, uint32_t row, bool has_row, int s) {
+  return row_param_from_word(has_row ? reinterpret_cast<const int *>(a.params + row)[s] : 0);
 }
 
 // The drive and carried state of a row whose constants in.p are already loaded.
@@ -567,335 +580,6 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
 
 // ---- banded sweep of the long-row steps ---------------------------------------------------------------
 
-constexpr int kSweepBands = 4;   // source bands of a swept step: 3 and 4 measured best (5: +3%, 6: +6% per step)
-
-// Whether a step runs as a banded sweep: its sources overflow one XCD's 4 MB L2 at one 128-byte line per row and
-// chunk (more than 32,768 rows of X_{t-1}), it has rows enough to give each of the GPU's waves several, and its
-// rows are long enough for every band to hold several non-zeros.
-inline bool sweep_eligible(int64_t prev_rows, int64_t rows, int64_t nnz) {
-  return prev_rows > 32768 && rows >= 65536 && nnz >= 32 * rows;
-}
-
-namespace {
-
-// Per row of A_t, where each of K bands of source rows begins among its non-zeros: band b holds the columns
-// [b * prev_rows / K, (b + 1) * prev_rows / K).  off (nr, K + 1): the row's start plus the count of its columns in
-// the bands before b; off[i][K] is the row's end.  A row's columns rise (CSR order of W[post, pre]), so each range
-// holds exactly its band; in any other order the ranges still split the row's non-zeros between the bands.
-__device__ __forceinline__ int32_t record_col(const int2 &r) { return r.x; }
-__device__ __forceinline__ int32_t record_col(int32_t c) { return c; }
-
-template <typename C>   // C: {column, weight} records (int2) or plain columns (int32_t)
-__global__ void k_band_off(const int32_t *__restrict__ rowptr, const C *__restrict__ colval, int64_t nr,
-                           int64_t prev_rows, int32_t K, int32_t *__restrict__ off) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= nr) return;
-  const int32_t beg = rowptr[i], end = rowptr[i + 1];
-  int32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int32_t q = beg; q < end; ++q) {
-    const int64_t b = (int64_t)record_col(colval[q]) * K / prev_rows;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) cnt[k] += (b == k) ? 1 : 0;
-  }
-  int32_t o = beg;
-  for (int k = 0; k < K; ++k) {
-    off[i * (K + 1) + k] = o;
-    o += cnt[k];
-  }
-  off[i * (K + 1) + K] = end;
-}
-
-// The order in which the swept kernel's waves take a step's rows: each wave's own `per` consecutive rows, longest
-// first (ties in index order), so the 8 rows of a slot are of like length and its rounds, which run to the longest
-// of them, waste fewer gathers, while every wave keeps the same rows and share of the work.  One thread per wave's
-// segment ranks each of its rows by counting the rows that go before it.
-__global__ void k_sweep_order(const int32_t *__restrict__ rowptr, int64_t nr, int64_t per, int32_t *__restrict__ order) {
-  const int64_t seg = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t b = seg * per;
-  if (b >= nr) return;
-  const int64_t e = min(b + per, nr);
-  for (int64_t i = b; i < e; ++i) {
-    const int32_t li = rowptr[i + 1] - rowptr[i];
-    int64_t rank = 0;
-    for (int64_t j = b; j < e; ++j) {
-      const int32_t lj = rowptr[j + 1] - rowptr[j];
-      rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
-    }
-    order[b + rank] = (int32_t)i;
-  }
-}
-
-// Rounds one slot of a swept wave issues for one band: the longest share of its rows' band counts (a slot of
-// r <= 4 rows spreads each row over 2, 4 or 8 groups, as the kernel does), padded to the 4 rounds of a gather block.
-// c(i): the band count of the slot's row i.
-template <typename C>
-__device__ inline int slot_band_rounds(C &&c, int r) {
-  const int lf = r >= 5 ? 0 : (r >= 3 ? 1 : (r == 2 ? 2 : 3));
-  int m = 0;
-  for (int i = 0; i < r; ++i) m = max(m, ((int)c(i) + (1 << lf) - 1) >> lf);
-  return (m + 3) & ~3;
-}
-
-// Rounds one unit of a swept wave issues in band q: a slot of 8 positions, or with `paired` two slots walked as one
-// pass, where each lane group walks its two rows (positions g and g + 8) back to back, so the pass runs to the
-// largest pair sum, padded to 4.  c(p): the band count at position p of the unit, of which the first r hold rows.
-template <typename C>
-__device__ inline int unit_band_rounds(C &&c, int r, bool paired) {
-  if (!paired) return slot_band_rounds(c, min(r, 8));
-  int mx = 0;
-  for (int g = 0; g < 8 && g < r; ++g) mx = max(mx, (int)c(g) + (g + 8 < r ? (int)c(g + 8) : 0));
-  return (mx + 3) & ~3;
-}
-
-constexpr int kSearchRows = 64;     // wave segments of at most this many rows are searched (longer keep the sort)
-constexpr int kSearchSteps = 200;   // moves tried per segment
-
-// After k_sweep_order: each wave's rows rearranged between its slots so that a slot's 8 rows have like band
-// counts and fewer of its rounds are padding (with `paired`, units of two slots walked as one pass).  One wave per
-// segment runs a seeded local search.  At each step every lane draws two rows of the segment (xorshift32, seeded by
-// segment and lane) and, if swapping them can change a unit's rounds, the change in the rounds of their units
-// (summed over the bands, as unit_band_rounds counts them); the lowest change wins (ties: the lowest lane) and is
-// made if it adds no rounds, so the search also walks across plateaus.  The wave keeps its rows, so its share of
-// the work is unchanged.
-__global__ __launch_bounds__(64) void k_sweep_order_search(const int32_t *__restrict__ band_off, int K, int64_t nr,
-                                                           int64_t per, int paired, int32_t *__restrict__ order) {
-  __shared__ uint16_t cnt[4][kSearchRows];
-  __shared__ int32_t row[kSearchRows];
-  __shared__ int32_t cost[kSearchRows / 8];   // rounds of each unit, summed over the bands
-  const int lane = threadIdx.x;
-  const int64_t seg = blockIdx.x;
-  const int64_t b = seg * per;
-  if (b >= nr || per > kSearchRows) return;
-  const int m = (int)min(per, nr - b);
-  for (int k = lane; k < m; k += 64) {
-    const int32_t r = order[b + k];
-    row[k] = r;
-    for (int q = 0; q < K; ++q)
-      cnt[q][k] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
-  }
-  __syncthreads();
-  const int U = paired ? 16 : 8;   // positions per unit
-  const int units = (m + U - 1) / U;
-  if (m <= 8) return;              // one slot: nothing to rearrange
-  // rounds of unit u with the rows at positions x and y swapped (x = y = -1: as it is)
-  auto unit_cost = [&](int u, int x, int y) {
-    const int r = min(U, m - U * u);
-    int c = 0;
-    for (int q = 0; q < K; ++q)
-      c += unit_band_rounds([&](int i) {
-        const int p = U * u + i;
-        return cnt[q][p == x ? y : (p == y ? x : p)];
-      }, r, paired != 0);
-    return c;
-  };
-  if (lane < units) cost[lane] = unit_cost(lane, -1, -1);
-  __syncthreads();
-  uint32_t state = (2463534242u ^ (uint32_t)(seg * 2654435761u) ^ (uint32_t)((lane + 1) * 2246822507u)) | 1u;
-  auto next = [&]() {
-    state ^= state << 13;
-    state ^= state >> 17;
-    state ^= state << 5;
-    return state;
-  };
-  for (int step = 0; step < kSearchSteps; ++step) {
-    const int i = (int)(next() % (uint32_t)m), k = (int)(next() % (uint32_t)m);
-    const int ui = i / U, uk = k / U;
-    int ci = 0, ck = 0, d = 1 << 20;
-    if (ui != uk) {
-      ci = unit_cost(ui, i, k);
-      ck = unit_cost(uk, i, k);
-      d = ci + ck - cost[ui] - cost[uk];
-    } else if (paired && (i & 7) != (k & 7)) {   // two lane groups of one pass trade rows
-      ci = ck = unit_cost(ui, i, k);
-      d = ci - cost[ui];
-    }
-    int key = ((d + (1 << 20)) << 6) | lane;   // the lowest change, then the lowest lane
-    for (int o = 32; o > 0; o >>= 1) key = min(key, __shfl_xor(key, o));
-    __syncthreads();
-    if ((key & 63) == lane && d <= 0) {
-      const int32_t rr = row[i];
-      row[i] = row[k];
-      row[k] = rr;
-      for (int q = 0; q < K; ++q) {
-        const uint16_t cc = cnt[q][i];
-        cnt[q][i] = cnt[q][k];
-        cnt[q][k] = cc;
-      }
-      cost[ui] = ci;
-      cost[uk] = ck;
-    }
-    __syncthreads();
-  }
-  for (int k = lane; k < m; k += 64) order[b + k] = row[k];
-}
-
-constexpr int kBalanceThreads = 256;
-constexpr int kBalanceSteps = 600;
-
-// After k_sweep_order_search: the rows of the 16 waves of one workgroup (one CU, whose waves meet at a barrier after
-// each band) rearranged between those waves and their slots, so that each band's slowest wave is closer to the
-// others.  Cost: for each band, 16 x the largest of the 16 waves' rounds (what the barrier waits for) plus their sum.
-// One workgroup per group of 16 segments; at each step every thread draws two positions (xorshift32 per group and
-// thread), the change in cost that swapping their rows would make is computed from the two slots' new rounds and the
-// three largest wave totals of each band, and the lowest change (ties: the lowest thread) is made if it adds no cost.
-// Every wave keeps its number of rows.
-__global__ __launch_bounds__(kBalanceThreads) void k_sweep_order_balance(const int32_t *__restrict__ band_off, int K,
-                                                                         int64_t nr, int64_t per, int paired,
-                                                                         int32_t *__restrict__ order) {
-  constexpr int W = 16;
-  __shared__ uint16_t cnt[4][W * kSearchRows];
-  __shared__ int32_t row[W * kSearchRows];
-  __shared__ int32_t sr[W][kSearchRows / 8][4];   // rounds of each wave's unit (slot, or pair of slots) per band
-  __shared__ int32_t tot[W][4];                   // rounds of each wave in each band
-  __shared__ int32_t top[4][3][2];                // per band, the three largest wave totals (value, wave)
-  __shared__ int32_t red[kBalanceThreads / 64];
-  const int t = threadIdx.x;
-  const int64_t grp = blockIdx.x;
-  const int64_t b = grp * W * per;
-  if (b >= nr || per > kSearchRows) return;
-  const int P = (int)per;
-  const int M = (int)min((int64_t)W * per, nr - b);
-  for (int p = t; p < M; p += kBalanceThreads) {
-    const int32_t r = order[b + p];
-    row[p] = r;
-    for (int q = 0; q < K; ++q)
-      cnt[q][p] = (uint16_t)min(band_off[(int64_t)r * (K + 1) + q + 1] - band_off[(int64_t)r * (K + 1) + q], 65535);
-  }
-  __syncthreads();
-  const int U = paired ? 16 : 8;   // positions per unit
-  auto rows_of = [&](int w) { return max(0, min(P, M - w * P)); };
-  // rounds of wave w's unit j in band q with the rows at positions x and y swapped (x = y = -1: as it is)
-  auto rounds = [&](int w, int j, int q, int x, int y) {
-    const int r = min(U, rows_of(w) - U * j);
-    if (r <= 0) return 0;
-    const int base = w * P + U * j;
-    return unit_band_rounds([&](int i) {
-      const int p = base + i;
-      return cnt[q][p == x ? y : (p == y ? x : p)];
-    }, r, paired != 0);
-  };
-  for (int x = t; x < W * (kSearchRows / 8) * 4; x += kBalanceThreads) {
-    const int w = x / 32, j = (x / 4) % 8, q = x % 4;
-    sr[w][j][q] = q < K ? rounds(w, j, q, -1, -1) : 0;
-  }
-  __syncthreads();
-  if (t < W * 4) {
-    int sum = 0;
-    for (int j = 0; j < kSearchRows / 8; ++j) sum += sr[t / 4][j][t % 4];
-    tot[t / 4][t % 4] = sum;
-  }
-  __syncthreads();
-  auto refresh_top = [&]() {
-    if (t < K) {
-      int v[3] = {-1, -1, -1}, id[3] = {-1, -1, -1};
-      for (int w = 0; w < W; ++w) {
-        const int x = tot[w][t];
-        if (x > v[0]) { v[2] = v[1]; id[2] = id[1]; v[1] = v[0]; id[1] = id[0]; v[0] = x; id[0] = w; }
-        else if (x > v[1]) { v[2] = v[1]; id[2] = id[1]; v[1] = x; id[1] = w; }
-        else if (x > v[2]) { v[2] = x; id[2] = w; }
-      }
-      for (int e = 0; e < 3; ++e) { top[t][e][0] = v[e]; top[t][e][1] = id[e]; }
-    }
-  };
-  refresh_top();
-  __syncthreads();
-  uint32_t state = (2463534242u ^ (uint32_t)(grp * 2654435761u) ^ (uint32_t)((t + 1) * 2246822507u)) | 1u;
-  auto next = [&]() {
-    state ^= state << 13;
-    state ^= state >> 17;
-    state ^= state << 5;
-    return state;
-  };
-  for (int step = 0; step < kBalanceSteps; ++step) {
-    const int p1 = (int)(next() % (uint32_t)M), p2 = (int)(next() % (uint32_t)M);
-    const int w1 = p1 / P, j1 = (p1 % P) / U, w2 = p2 / P, j2 = (p2 % P) / U;
-    const bool same = w1 == w2 && j1 == j2;   // one unit: only two lane groups of a pass trading rows changes it
-    int a1[4] = {0, 0, 0, 0}, a2[4] = {0, 0, 0, 0};
-    int d = 1 << 20;
-    if (!same || (paired && ((p1 % P) & 7) != ((p2 % P) & 7))) {
-      d = 0;
-      for (int q = 0; q < K; ++q) {
-        a1[q] = rounds(w1, j1, q, p1, p2);
-        a2[q] = same ? a1[q] : rounds(w2, j2, q, p1, p2);
-        int t1, t2;
-        if (same) {
-          t1 = t2 = tot[w1][q] - sr[w1][j1][q] + a1[q];
-        } else if (w1 == w2) {
-          t1 = t2 = tot[w1][q] - sr[w1][j1][q] - sr[w1][j2][q] + a1[q] + a2[q];
-        } else {
-          t1 = tot[w1][q] - sr[w1][j1][q] + a1[q];
-          t2 = tot[w2][q] - sr[w2][j2][q] + a2[q];
-        }
-        int other = 0;
-        for (int e = 0; e < 3; ++e)
-          if (top[q][e][1] != w1 && top[q][e][1] != w2) { other = max(top[q][e][0], 0); break; }
-        const int newmax = max(other, max(t1, t2));
-        const int dsum = w1 == w2 ? t1 - tot[w1][q] : (t1 - tot[w1][q]) + (t2 - tot[w2][q]);
-        d += W * (newmax - top[q][0][0]) + dsum;
-      }
-    }
-    int key = ((d + (1 << 20)) << 8) | t;   // the lowest change, then the lowest thread
-    for (int o = 32; o > 0; o >>= 1) key = min(key, __shfl_xor(key, o));
-    if ((t & 63) == 0) red[t >> 6] = key;
-    __syncthreads();
-    int best = red[0];
-    for (int x = 1; x < kBalanceThreads / 64; ++x) best = min(best, red[x]);
-    if ((best & 255) == t && d <= 0) {
-      const int32_t rr = row[p1];
-      row[p1] = row[p2];
-      row[p2] = rr;
-      for (int q = 0; q < K; ++q) {
-        const uint16_t cc = cnt[q][p1];
-        cnt[q][p1] = cnt[q][p2];
-        cnt[q][p2] = cc;
-        if (same) {
-          tot[w1][q] += a1[q] - sr[w1][j1][q];
-        } else if (w1 == w2) {
-          tot[w1][q] += a1[q] - sr[w1][j1][q] + a2[q] - sr[w1][j2][q];
-        } else {
-          tot[w1][q] += a1[q] - sr[w1][j1][q];
-          tot[w2][q] += a2[q] - sr[w2][j2][q];
-        }
-        sr[w1][j1][q] = a1[q];
-        sr[w2][j2][q] = a2[q];
-      }
-    }
-    __syncthreads();
-    refresh_top();
-    __syncthreads();
-  }
-  for (int p = t; p < M; p += kBalanceThreads) order[b + p] = row[p];
-}
-
-__global__ void k_zero_int(int32_t *p) { *p = 0; }
-
-// The longest row of a CSR matrix (rows: nr, into *out, which starts at 0).
-__global__ void k_max_row_length(const int32_t *__restrict__ rowptr, int64_t nr, int32_t *__restrict__ out) {
-  int32_t m = 0;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nr; i += (int64_t)gridDim.x * blockDim.x)
-    m = max(m, rowptr[i + 1] - rowptr[i]);
-  for (int off = 32; off > 0; off >>= 1) m = max(m, __shfl_xor(m, off));
-  if ((threadIdx.x & 63) == 0) atomicMax(out, m);
-}
-
-}  // namespace
-
-// Whether a step's matrix runs as a banded sweep: eligible by size, and no row much longer than the mean.  A slot's
-// rounds run to the longest of its 8 rows and a workgroup's waves wait for each other after every band, so a row
-// far above the mean (a hub of a graph with heavy-tailed in-degrees) would hold its whole workgroup; such a matrix
-// stays on the grouped kernel.  Synchronises the stream (a plan-time decision).
-inline bool sweep_suits(const int32_t *rowptr, int64_t prev_rows, int64_t nr, int64_t nnz, hipStream_t st) {
-  if (!sweep_eligible(prev_rows, nr, nnz)) return false;
-  DevArray<int32_t> mx(1);
-  hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(1), 0, st, mx.p);
-  hipLaunchKernelGGL(k_max_row_length, dim3((unsigned)std::min<int64_t>(blocks_for(nr, 256), 1024)), dim3(256), 0, st,
-                     rowptr, nr, mx.p);
-  int32_t longest = 0;
-  FLY_HIP(hipMemcpyAsync(&longest, mx.p, sizeof(longest), hipMemcpyDeviceToHost, st));
-  FLY_HIP(hipStreamSynchronize(st));
-  return (double)longest <= 4.0 * (double)nnz / (double)nr + 64.0;
-}
-
 // The sum over each aligned block of 2^lf lane groups of 8 lanes (lf = 0..3, wave-uniform), in every lane of the
 // block: the first lf levels of group_sum's butterfly.
 __device__ __forceinline__ float groups_sum(float v, int lf) {
@@ -920,22 +604,26 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // A long-row step as a sweep of the source rows in K bands, with each row's sums held in registers across it.
 // One workgroup of 16 waves per CU, all resident at once: wave w owns rows_per_wave consecutive positions of the
 // sweep order (slot j of lane group g: position w * rows_per_wave + 8 j + g, in passes of 8 * SLOTS) for every
-// chunk of columns.  The order (sweep_rows, build_sweep_order) gives a slot rows of like band counts and keeps each
-// band's slowest wave close to the others, while every wave keeps the same number of rows.  For each
+// chunk of columns.  The order (SweepTables, build_sweep) gives a slot rows of like band counts and keeps each
+// band's slowest wave close to the others, while every wave keeps the same number of rows.  A position holds a row
+// of the step, or a piece of a row the tables split (rows far longer than the mean): a piece stores its raw sums to
+// `pieces`, and k_sweep_finish adds a split row's pieces and runs its epilogue.  For each
 // chunk a wave gathers band 0 of all its rows, then band 1, and so on, and the workgroup's waves meet at a barrier
 // after each band: the CU's waves then draw from one band of the source rows at a time, so one XCD's L2 holds the
 // lines of one band instead of the whole chunk.  (Without the barrier, issue priority lets the oldest waves run
-// ahead and the working set grows.)  band_off (nrows, K + 1): row i's non-zeros of band b are
-// colval[band_off[i][b] .. band_off[i][b+1]).  Lane groups of 8 lanes x 16 bytes gather one 128-byte line each; a
+// ahead and the working set grows.)  sweep_range (rows + pieces, 2K): row or piece v's non-zeros of band b are
+// colval[range[v][2b] .. range[v][2b+1]).  Lane groups of 8 lanes x 16 bytes gather one 128-byte line each; a
 // slot's rounds run to the longest of the wave's 8 rows in that slot and band, the shorter rows' extra gathers from
 // the row past the buffer (zeros, no memory access); a slot of 4 rows or fewer spreads each row over several lane
-// groups.  PIPE keeps the next four rounds' gathers in flight during the sums.  REPLAY as for the other step
-// kernels, and 3: the product alone, each row's sums stored to xout (float32 states; the training forward's A x).
-template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, bool PAIRED = false,
+// groups.  PAIRED walks two slots' rows per pass (1: the other row's weight is zero, for states that hold no inf
+// or NaN; 2: only the owning row's sums change).  PIPE keeps the next four rounds' gathers in flight during the
+// sums.  REPLAY as for the other step kernels, and 3: the product alone, each row's sums stored to xout (float32
+// states; the training forward's A x).
+template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, int PAIRED = 0,
           bool PIPE = false>
 __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, U> a) {
   constexpr int UNR = 4;
-  static_assert(K + 1 <= 8 && V * sizeof(S) == 16, "band starts in the lanes of a group, 16-byte lanes");
+  static_assert(2 * K <= 8 && V * sizeof(S) == 16, "band ranges in the lanes of a group, 16-byte lanes");
   const int lane = threadIdx.x & 63, g = lane >> 3, s = lane & 7;
   const uint32_t wave = blockIdx.x * 16u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t row_bytes = (uint32_t)a.ldx * (uint32_t)sizeof(S);
@@ -946,13 +634,19 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
   // 2^24, so its 24-bit product with row_bytes is exact)
   const uint32_t past_row = a.xbytes / row_bytes;
   const int R = a.rows_per_wave;
-  const uint32_t npos = (uint32_t)a.nrows;   // positions of the order: one per row
+  const uint32_t npos = (uint32_t)a.sweep_npos;   // positions of the order
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
-  // position p of the sweep order holds row sweep_rows[p] (p itself without an order); an entry outside the step's
-  // rows reads as no row
+  // Per wave, slot and lane: the row the lane's group finishes in the epilogue (-1: none) and word s of that row's
+  // 32-byte constants, written once per pass and read by the same lane after every chunk, so the epilogue issues
+  // the loads of several rows' carried state and drive at once instead of three dependent loads per row.
+  const int wv = threadIdx.x >> 6;
+  __shared__ int ep_row[REPLAY != 1 ? 16 * SLOTS * 64 : 1];
+  __shared__ int ep_par[REPLAY == 0 || REPLAY == 2 ? 16 * SLOTS * 64 : 1];
+  // position p of the sweep order holds row (or nrows + piece) sweep_order[p]; an entry outside the step's rows and
+  // pieces reads as no row
   auto row_at = [&](uint32_t p) {
-    const int32_t r = a.sweep_rows ? a.sweep_rows[p] : (int32_t)p;
-    return r >= 0 && r < a.nrows ? r : -1;
+    const int32_t r = a.sweep_order[p];
+    return r >= 0 && r < a.sweep_vrows ? r : -1;
   };
   for (int k0 = 0; k0 < R; k0 += 8 * SLOTS) {
     const uint32_t base = wave * (uint32_t)R + (uint32_t)k0;   // slot j, row i of the slot: position base + 8 j + i
@@ -965,15 +659,23 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
     for (int j = 0; j < SLOTS; ++j) {
       const int64_t left = min((int64_t)R - k0 - 8 * j, (int64_t)npos - (int64_t)base - 8 * j);
       nrow[j] = (int)max<int64_t>(0, min<int64_t>(8, left));
-      lf[j] = PAIRED || nrow[j] >= 5 || nrow[j] == 0 ? 0
+      lf[j] = PAIRED != 0 || nrow[j] >= 5 || nrow[j] == 0 ? 0
               : (nrow[j] >= 3 ? 1 : (nrow[j] == 2 ? 2 : 3));
     }
-    int off[SLOTS];   // lane s <= K: band_off[row][s]
+    int off[SLOTS];   // lane s < 2K: sweep_range[row][s]
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
       const int i = g >> lf[j];
       const int32_t rj = i < nrow[j] ? row_at(base + 8u * j + (uint32_t)i) : -1;
-      off[j] = rj >= 0 && s <= K ? a.band_off[(int64_t)rj * (K + 1) + s] : 0;
+      off[j] = rj >= 0 && s < 2 * K ? a.sweep_range[(int64_t)rj * (2 * K) + s] : 0;
+      if constexpr (REPLAY != 1) {
+        // the epilogue's row (first group of a spread row only) and word s of its constants, for every chunk
+        const bool first = (g & ((1 << lf[j]) - 1)) == 0;
+        const int e = (wv * SLOTS + j) * 64 + lane;
+        ep_row[e] = first ? rj : -1;
+        if constexpr (REPLAY != 3)
+          ep_par[e] = first && rj >= 0 && rj < a.nrows ? reinterpret_cast<const int *>(a.params + rj)[s] : 0;
+      }
     }
     for (int c = 0; c < chunks; ++c) {
       const int64_t col = (int64_t)c * (8 * V) + (int64_t)s * V;
@@ -992,8 +694,8 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           // sums of the row it belongs to (the other row's weight is zero).
 #pragma unroll
           for (int j = 0; j < SLOTS; j += 2) {
-            const int bA = group_bcast<8, b>(off[j]), eA = group_bcast<8, b + 1>(off[j]);
-            const int bB = group_bcast<8, b>(off[j + 1]), eB = group_bcast<8, b + 1>(off[j + 1]);
+            const int bA = group_bcast<8, 2 * b>(off[j]), eA = group_bcast<8, 2 * b + 1>(off[j]);
+            const int bB = group_bcast<8, 2 * b>(off[j + 1]), eB = group_bcast<8, 2 * b + 1>(off[j + 1]);
             const int nA = eA - bA, n = nA + (eB - bB);
             const int rounds = wave_max_of_groups(n);
             auto block = [&](int q0) {
@@ -1025,12 +727,25 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                     for (int u = 0; u < UNR; ++u) {
                       const float wt = __int_as_float(wj[u]);
                       const bool in_a = q0 + h0 + u < nA;
-                      const float wa = in_a ? wt : 0.0f, wb = in_a ? 0.0f : wt;
+                      if constexpr (PAIRED == 2) {
+                        // only the row that owns the gathered record changes: a zero weight times an inf or NaN
+                        // source would otherwise reach the partner row, which never reads that source
 #pragma unroll
-                      for (int i = 0; i < V; ++i) {
-                        const float x = Lanes<S, V>::at(xr[u], i);
-                        acc[j][i] = fmaf(wa, x, acc[j][i]);
-                        acc[j + 1][i] = fmaf(wb, x, acc[j + 1][i]);
+                        for (int i = 0; i < V; ++i) {
+                          const float x = Lanes<S, V>::at(xr[u], i);
+                          const float ta = fmaf(wt, x, acc[j][i]), tb = fmaf(wt, x, acc[j + 1][i]);
+                          acc[j][i] = in_a ? ta : acc[j][i];
+                          acc[j + 1][i] = in_a ? acc[j + 1][i] : tb;
+                        }
+                      } else {
+                        // the other row's weight is zero: exact for the finite states of a bounded clamp
+                        const float wa = in_a ? wt : 0.0f, wb = in_a ? 0.0f : wt;
+#pragma unroll
+                        for (int i = 0; i < V; ++i) {
+                          const float x = Lanes<S, V>::at(xr[u], i);
+                          acc[j][i] = fmaf(wa, x, acc[j][i]);
+                          acc[j + 1][i] = fmaf(wb, x, acc[j + 1][i]);
+                        }
                       }
                     }
                   }
@@ -1042,7 +757,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
         } else {
 #pragma unroll
         for (int j = 0; j < SLOTS; ++j) {
-          int beg = group_bcast<8, b>(off[j]), end = group_bcast<8, b + 1>(off[j]);
+          int beg = group_bcast<8, 2 * b>(off[j]), end = group_bcast<8, 2 * b + 1>(off[j]);
           if (lf[j]) {   // this group's share of the row's band
             const int n = end - beg, p = g & ((1 << lf[j]) - 1), b0 = beg;
             beg = b0 + ((n * p) >> lf[j]);
@@ -1158,24 +873,42 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[j][i] = groups_sum(acc[j][i], lf[j]);
           }
-          const int i = g >> lf[j];
-          const bool first = (g & ((1 << lf[j]) - 1)) == 0;
-          // the position is recomputed for every chunk rather than its address kept live across the bands
-          uint32_t pj = base + 8u * j + (uint32_t)i;
-          asm volatile("" : "+v"(pj));
-          const int32_t rs = first && i < nrow[j] && in_batch ? row_at(pj) : -1;
-          if (rs >= 0) {
-            const uint32_t rj = (uint32_t)rs;
-            if constexpr (REPLAY == 3) {   // the product alone: y[row] = the row's sums, float32
-              Lanes<S, V>::store(a.xout + (int64_t)rj * a.ldo + col, acc[j]);
-            } else {
-              if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j], bits);
-              RowInputs<S, U, V> in;
-              load_row_inputs(a, rj, col, true, in);
-              finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j], in);
-            }
-          }
         }
+        // Slots in batches: the carried state and drive of a batch's rows load together, then the batch finishes.
+        // Batches of 3, or of 2 when 6 slots' sums share the registers with 32-byte drive vectors (float32 drive
+        // of a half state), which would otherwise spill.
+        constexpr int EB = (SLOTS == 6 && V * sizeof(U) > 16) ? 2 : (SLOTS % 3 == 0 ? 3 : 1);
+        static_for<SLOTS / EB>([&](auto H) {
+          constexpr int j0 = decltype(H)::value * EB;
+          int rs[EB];
+          RowInputs<S, U, V> in[EB];
+          static_for<EB>([&](auto J) {
+            constexpr int u = decltype(J)::value;
+            const int e = (wv * SLOTS + j0 + u) * 64 + lane;
+            rs[u] = in_batch ? ep_row[e] : -1;
+            if constexpr (REPLAY != 3) {
+              in[u].p = row_param_from_word(ep_par[e]);   // every lane takes part in the group broadcasts
+              load_row_drive(a, col, rs[u] >= 0 && rs[u] < a.nrows, in[u]);
+            }
+          });
+          static_for<EB>([&](auto J) {
+            constexpr int u = decltype(J)::value;
+            if (rs[u] >= a.nrows) {   // a piece of a split row: its raw sums
+              if constexpr (REPLAY != 2) {
+                float *dst = a.pieces + (int64_t)(rs[u] - a.nrows) * a.ldp + col;
+                Lanes<float, V>::store(dst, acc[j0 + u]);
+              }
+            } else if (rs[u] >= 0) {
+              const uint32_t rj = (uint32_t)rs[u];
+              if constexpr (REPLAY == 3) {   // the product alone: y[row] = the row's sums, float32
+                Lanes<S, V>::store(a.xout + (int64_t)rj * a.ldo + col, acc[j0 + u]);
+              } else {
+                if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j0 + u], bits);
+                finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j0 + u], in[u]);
+              }
+            }
+          });
+        });
       }
     }
   }
@@ -1187,65 +920,76 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
   }
 }
 
-// The GPU's CU count (the swept kernel runs one workgroup per CU).
-inline int cu_count() {
-  static int n = -1;
-  if (n < 0) {
-    int dev = 0, cus = 0;
-    FLY_HIP(hipGetDevice(&dev));
-    FLY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    FLY_REQUIRE(cus > 0, "no compute units");
-    n = cus;
-  }
-  return n;
-}
-
-// The swept waves' order of a step's rows (nr, into `order`): each wave's own rows_per_wave rows, longest first
-// (k_sweep_order), then rearranged between the wave's slots (k_sweep_order_search) and between the 16 waves of
-// each workgroup (k_sweep_order_balance) from the band table (nr, K + 1).  `paired`: the state is float32 and the
-// sweep walks two rows per pass (sweep_paired), which changes what a slot costs.
-inline void build_sweep_order(const int32_t *rowptr, const int32_t *band_off, int K, int64_t nr, bool paired,
-                              int32_t *order, hipStream_t st) {
-  FLY_REQUIRE(nr > 0 && nr < (int64_t)INT32_MAX && (K == 3 || K == 4), "rows or bands out of range");
-  const int64_t waves = 16 * (int64_t)cu_count();
-  const int64_t per = (nr + waves - 1) / waves;   // launch_swept's rows_per_wave
-  const int64_t segs = (nr + per - 1) / per;
-  hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, rowptr, nr, per, order);
-  if (per <= kSearchRows) {
-    // the float32 kernel walks pairs of slots in one pass when a wave owns over 24 rows (launch_swept)
-    const int pair = paired && K == 4 && per > 24 ? 1 : 0;
-    hipLaunchKernelGGL(k_sweep_order_search, dim3((unsigned)segs), dim3(64), 0, st, band_off, K, nr, per, pair,
-                       order);
-    hipLaunchKernelGGL(k_sweep_order_balance, dim3((unsigned)((segs + 15) / 16)), dim3(kBalanceThreads), 0, st,
-                       band_off, K, nr, per, pair, order);
+// The rows a swept step split into pieces (k_state_step_swept stored each piece's raw sums): per split row, the
+// pieces' sums added in piece order, then the row's epilogue as the swept kernel runs it (REPLAY == 3: the sums
+// stored).  One thread per V columns of a row, blockIdx.y over the split rows.
+template <typename S, typename U, int V, bool TORCH_LERP, int REPLAY>
+__global__ __launch_bounds__(256) void k_sweep_finish(const StepArgs<S, U> a, const int32_t *__restrict__ split,
+                                                     const int32_t *__restrict__ split_ptr, int32_t nsplit) {
+  const int64_t col = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) * V;
+  if (col >= a.batch) return;
+  for (int32_t h = blockIdx.y; h < nsplit; h += gridDim.y) {
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    const int32_t q1 = split_ptr[h + 1];
+    for (int32_t q = split_ptr[h]; q < q1; ++q) {
+      float v[V];
+      Lanes<float, V>::load(a.pieces + (int64_t)q * a.ldp + col, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += v[i];
+    }
+    const uint32_t row = (uint32_t)split[h];
+    if constexpr (REPLAY == 3) {
+      Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, acc);
+    } else {
+      RowInputs<S, U, V> in;
+      load_row_inputs(a, row, col, true, in);
+      finish_row<S, U, V, TORCH_LERP>(a, row, col, acc, in);
+    }
   }
 }
 
-template <typename S, typename U, int K, int SLOTS, int REPLAY, bool PAIRED = false, bool PIPE = false>
+template <typename S, typename U, int K, int SLOTS, int REPLAY, int PAIRED = 0, bool PIPE = false>
 void launch_swept_shape(const StepArgs<S, U> &a, unsigned grid, hipStream_t st) {
   constexpr int V = 16 / (int)sizeof(S);
-  static bool fits = false;
-  if (!fits) {   // the kernel's registers allow one 16-wave workgroup on every CU
+  static std::atomic<bool> fits{false};
+  if (!fits.load(std::memory_order_relaxed)) {   // the kernel's registers allow one 16-wave workgroup on a CU
     int nb = 0;
     FLY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
         &nb,
         reinterpret_cast<const void *>(&k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED, PIPE>),
         1024, 0));
     FLY_REQUIRE(nb >= 1, "the swept state step does not fit a CU");
-    fits = true;
+    fits.store(true, std::memory_order_relaxed);
   }
   hipLaunchKernelGGL((k_state_step_swept<S, U, V, K, SLOTS, sizeof(S) == 4, REPLAY, PAIRED, PIPE>), dim3(grid),
                      dim3(1024), 0, st, a);
 }
 
-// One swept step: one workgroup per CU, the rows split evenly between the waves (one pass of up to 24 or 48 rows
-// per wave; a larger step takes several passes).
+// Bytes of the pieces buffer a swept step of `batch` columns over these tables needs (0 without split rows).
+inline size_t sweep_pieces_bytes(const SweepTables *t, int64_t batch) {
+  return t && t->pieces ? (size_t)t->pieces * (size_t)round_up(batch, 64) * sizeof(float) : 0;
+}
+
+// One swept step over the tables of its structure: one workgroup per CU (or the tables' grid), the rows split evenly
+// between the waves (one pass of up to 24 or 48 rows per wave; a larger step takes several passes), then the split
+// rows' pieces added and finished.  a.pieces: sweep_pieces_bytes(t, batch) bytes, 16-byte aligned (unused without
+// split rows).
 template <typename S, typename U, int REPLAY>
-void launch_swept(StepArgs<S, U> a, hipStream_t st) {
-  const unsigned grid = (unsigned)cu_count();
-  a.rows_per_wave = (int32_t)((a.nrows + 16 * (int64_t)grid - 1) / (16 * (int64_t)grid));
+void launch_swept(StepArgs<S, U> a, const SweepTables &t, hipStream_t st) {
+  FLY_REQUIRE(t.nrows == a.nrows, "sweep tables of another structure");
+  FLY_REQUIRE(!t.pieces || REPLAY == 1 || REPLAY == 2 || (a.pieces && aligned(a.pieces, 32)),
+              "a swept step with split rows needs its pieces buffer");
+  const unsigned grid = (unsigned)t.grid;
+  a.sweep_range = t.range.p;
+  a.sweep_order = t.order.p;
+  a.sweep_npos = (int32_t)t.npos;
+  a.sweep_vrows = (int32_t)(t.nrows + t.pieces);
+  a.rows_per_wave = t.rows_per_wave;
+  a.ldp = round_up(a.batch, 64);
   const bool few = a.rows_per_wave <= 24 || a.sweep_slots == 3;
-  switch (a.sweep_bands) {
+  switch (t.bands) {
     case 3:
       if (few) launch_swept_shape<S, U, 3, 3, REPLAY>(a, grid, st);
       else launch_swept_shape<S, U, 3, 6, REPLAY>(a, grid, st);
@@ -1253,17 +997,27 @@ void launch_swept(StepArgs<S, U> a, hipStream_t st) {
     case 4:
       // passes of 3 slots keep the next four rounds' gathers in flight during the sums (step 5 at B = 1120:
       // 1.006 -> 0.959 ms); at 6 slots the second set of gathers costs spills and gains nothing
-      if (few && a.sweep_pipe >= 0) launch_swept_shape<S, U, 4, 3, REPLAY, false, true>(a, grid, st);
+      if (few && a.sweep_pipe >= 0) launch_swept_shape<S, U, 4, 3, REPLAY, 0, true>(a, grid, st);
       else if (few) launch_swept_shape<S, U, 4, 3, REPLAY>(a, grid, st);
-      else if (a.sweep_pipe > 0) launch_swept_shape<S, U, 4, 6, REPLAY, false, true>(a, grid, st);
-      // float32 states walk two rows per pass (measured +1.6% at B = 1120); half states not (-5%: 16 FMAs per
-      // gathered line of 8 halves cost more than the rounds they save)
-      else if (a.sweep_paired > 0 || (a.sweep_paired == 0 && sizeof(S) == 4))
-        launch_swept_shape<S, U, 4, 6, REPLAY, true>(a, grid, st);
-      else launch_swept_shape<S, U, 4, 6, REPLAY>(a, grid, st);
+      else if (a.sweep_pipe > 0) launch_swept_shape<S, U, 4, 6, REPLAY, 0, true>(a, grid, st);
+      // two rows per pass only when the tuning asks: with the epilogue's batched loads one row per pass measured
+      // faster for float32 states too (126,100 against 124,500 evals/s, float32 light cone at B = 1120), and half
+      // states lose 5% (16 FMAs per gathered line of 8 halves cost more than the rounds they save)
+      else if (a.sweep_paired > 0) {
+        if (a.sweep_exact) launch_swept_shape<S, U, 4, 6, REPLAY, 2>(a, grid, st);
+        else launch_swept_shape<S, U, 4, 6, REPLAY, 1>(a, grid, st);
+      } else {
+        launch_swept_shape<S, U, 4, 6, REPLAY>(a, grid, st);
+      }
       break;
     default:
       FLY_REQUIRE(false, "swept steps take 3 or 4 bands");
+  }
+  if (t.pieces && (REPLAY == 0 || REPLAY == 3)) {
+    constexpr int V = 16 / (int)sizeof(S);
+    const dim3 fgrid(blocks_for((a.batch + V - 1) / V, 256), (unsigned)std::min<int64_t>(t.split_rows, 65535));
+    hipLaunchKernelGGL((k_sweep_finish<S, U, V, sizeof(S) == 4, REPLAY>), fgrid, dim3(256), 0, st, a, t.split.p,
+                       t.split_ptr.p, (int32_t)t.split_rows);
   }
 }
 

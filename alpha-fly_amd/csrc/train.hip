@@ -938,49 +938,41 @@ void launch_spmm(const SpmmArgs &a, hipStream_t st) {
 
 using namespace fly;
 
-extern "C" int fly_sweep_tables(const int32_t *rowptr, const int32_t *col, int64_t nrows, int64_t nnz,
-                                int64_t ncols, int32_t *band_off, int32_t *order, int32_t *swept, void *stream) {
-  return guard([&] {
-    FLY_REQUIRE(rowptr && band_off && order && swept, "null argument");
-    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)1 << 24 && ncols > 0 && ncols < (int64_t)1 << 24 && nnz >= 0,
-                "size out of range");
-    FLY_REQUIRE(nnz == 0 || col, "null columns");
-    hipStream_t st = as_stream(stream);
-    *swept = sweep_suits(rowptr, ncols, nrows, nnz, st) ? 1 : 0;   // synchronises
-    if (!*swept) return;
-    hipLaunchKernelGGL(k_band_off<int32_t>, dim3(blocks_for(nrows, 256)), dim3(256), 0, st, rowptr, col, nrows, ncols,
-                       kSweepBands, band_off);
-    build_sweep_order(rowptr, band_off, kSweepBands, nrows, true, order, st);
-    check_launch("sweep tables");
-  });
+extern "C" size_t fly_spmm_swept_workspace(const fly_sweep *sweep, int64_t batch) {
+  return sweep ? sweep_pieces_bytes(sweep->t.get(), batch) : 0;
 }
 
-extern "C" int fly_spmm_swept(const int32_t *rowptr, const void *records, const int32_t *band_off,
-                              const int32_t *order, int64_t nrows, int64_t ncols, const float *x, int64_t ldx,
-                              int64_t batch, float *y, int64_t ldy, void *stream) {
+extern "C" int fly_spmm_swept(const fly_sweep *sweep, const void *records, int64_t nnz, const float *x, int64_t ldx,
+                              int64_t batch, float *y, int64_t ldy, void *ws, size_t ws_bytes, void *stream) {
   return guard([&] {
-    FLY_REQUIRE(rowptr && records && band_off && order && x && y, "null argument");
-    FLY_REQUIRE(nrows > 0 && nrows < (int64_t)1 << 24 && ncols > 0 && ncols < (int64_t)1 << 24, "size out of range");
+    FLY_REQUIRE(sweep && sweep->t && records && x && y, "null argument");
+    FLY_REQUIRE(current_device() == sweep->device, "the sweep tables live on another device");
+    const SweepTables &t = *sweep->t;
+    // the tables index the records: they must be the structure's nnz records, in its CSR order
+    FLY_REQUIRE(nnz == t.nnz, "the records do not match the structure's non-zeros");
     FLY_REQUIRE(batch > 0 && batch % 4 == 0 && batch < (int64_t)INT32_MAX / 2, "the batch must be a multiple of 4");
     FLY_REQUIRE(ldx >= batch && ldy >= batch && ldx % 4 == 0 && ldy % 4 == 0 && aligned(x, 16) && aligned(y, 16),
                 "x and y rows must be 16-byte aligned and hold the batch");
-    const uint32_t xbytes = buffer_bytes(ncols, ldx, sizeof(float));
+    const size_t need = sweep_pieces_bytes(&t, batch);
+    FLY_REQUIRE(need == 0 || (ws && ws_bytes >= need && aligned(ws, 256)), "workspace too small or misaligned");
+    const uint32_t xbytes = buffer_bytes(t.ncols, ldx, sizeof(float));
     FLY_REQUIRE(xbytes != 0, "x must be below 2 GiB with rows of 24-bit indices");
     StepArgs<float, float> a{};
-    a.rowptr = rowptr;
     a.colval = static_cast<const int2 *>(records);
     a.xprev = x;
     a.ldx = ldx;
     a.xout = y;
     a.ldo = ldy;
-    a.nrows = (int32_t)nrows;
+    a.nrows = (int32_t)t.nrows;
     a.batch = (int32_t)batch;
     a.xbytes = xbytes;
-    a.band_off = band_off;
-    a.sweep_rows = order;
-    a.sweep_bands = kSweepBands;
+    a.pieces = static_cast<float *>(ws);
+    a.sweep_paired = sweep->tune.sweep_paired;
+    a.sweep_slots = sweep->tune.sweep_slots;
+    a.sweep_pipe = sweep->tune.sweep_pipe;
+    a.sweep_exact = 1;   // x is the caller's: it may hold inf or NaN
     LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
-    launch_swept<float, float, 3>(a, as_stream(stream));
+    launch_swept<float, float, 3>(a, t, as_stream(stream));
     check_launch("swept product");
   });
 }
@@ -1006,7 +998,8 @@ extern "C" int fly_spmm(const int32_t *rowptr, const int32_t *col, const float *
                   accumulate != 0, nullptr, 0, 0, nullptr};
       hipLaunchKernelGGL(k_spmv, dim3(blocks_for(nrows, 16)), dim3(256), 0, as_stream(stream), b);
     } else if (batch >= 4 && vec4_ok(x, ldx) && vec4_ok(y, ldy)) {
-      const int g = tuning().spmm_groups == 2 || tuning().spmm_groups == 8 ? tuning().spmm_groups : 4;
+      const int tg = tuning_snapshot().spmm_groups;
+      const int g = tg == 2 || tg == 8 ? tg : 4;
       const int width = 64 / g * 4;   // columns per chunk
       a.chunks = (int32_t)((batch + width - 1) / width);
       if (g == 2)

@@ -12,7 +12,11 @@ value = B * steps / wall time; `roofline` rates the fused state-step kernel by i
 its launch time measured with HIP events on its stream; `cpu_baseline` times the reference's CPU path
 (restated in oracle/, the float32 light cone with cached constants) on a bounded sample of the same boards.
 
-    python bench.py [--steps K] [--warmup W] [--batch B] [--dtype f16|f32] [--graph synthetic|shuffled]
+    python bench.py [--steps K] [--warmup W] [--batch B] [--dtype f16|f32] [--graph synthetic|shuffled|realdeg]
+
+`--graph realdeg` runs the same network on a graph with the MaleCNS wiring's in-degree sequence and sensory /
+output sets (tests/golden/realdeg_fixture.npz, from the reference's shipped weight data) and seeded partners:
+heavy-tailed in-degrees, hub rows of up to 9,193 partners, 2,190 neurons with none.
 """
 
 from __future__ import annotations
@@ -187,7 +191,7 @@ def train_bench(args, dev) -> dict:
     from chessfly import _hip
     from chessfly.synthetic import synthetic_boards, synthetic_net
 
-    net, conn = synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev)
+    net, conn = bench_net(args, dev)
     net.train()
     opt = torch.optim.AdamW(net.parameters(), lr=1e-4, weight_decay=0.0)
     x_np = synthetic_boards(args.batch, seed=1)
@@ -248,6 +252,28 @@ def train_bench(args, dev) -> dict:
     }
 
 
+REALDEG_FIXTURE = os.path.join(REPO, "tests", "golden", "realdeg_fixture.npz")
+
+
+def realdeg_graph(seed: int = 0):
+    """The graph with the MaleCNS wiring's in-degrees and sensory / output sets (the committed fixture) and
+    partners drawn from `seed` (chessfly.synthetic.degree_connectome)."""
+    import numpy as np
+    from chessfly.synthetic import degree_connectome
+    f = np.load(REALDEG_FIXTURE)
+    ids = lambda gaps: np.cumsum(gaps.astype(np.int64))
+    return degree_connectome(f["in_degree"], ids(f["in_idx_gaps"]), ids(f["out_idx_gaps"]), seed=seed)
+
+
+def bench_net(args, dev):
+    """The network of the benchmark's --graph on `dev`: the synthetic graph, its shuffled control, or the graph with
+    the real in-degrees; the same seeded weights and maps either way."""
+    from chessfly.synthetic import synthetic_net
+    graph = realdeg_graph() if args.graph == "realdeg" else None
+    return synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev,
+                         graph=graph)
+
+
 PROBE_LIB = os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so")
 
 
@@ -260,16 +286,25 @@ def _probe_lib():
     p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     lib.flyprobe_last_error.restype, lib.flyprobe_last_error.argtypes = ctypes.c_char_p, []
     for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
-                       ("flyprobe_band_table", [p, p, i64, i64, i64, i32, i32, p, p, p, p]),
-                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p, i32, p, p]),
+                       ("flyprobe_sweep_create", [p, p, i64, i64, i64, p, ctypes.POINTER(p), p]),
+                       ("flyprobe_sweep_destroy", [p]),
+                       ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p, p]),
                        ("flyprobe_pack_params", [p, p, i64, p, p]),
-                       ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, p,
-                                                    i32, p]),
+                       ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, p]),
                        ("flyprobe_random_gather", [p, i64, i64, i64, p, i64, p, p]),
                        ("flyprobe_set_tuning", [ctypes.c_char_p, i64])):
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = i32, args
     return lib
+
+
+def sweep_config(tuned: dict, state_f16: bool) -> list[int]:
+    """The sweep tables' configuration a plan derives from its tuning (sweep_config in csrc/sweep.hpp): bands,
+    paired, workgroups, force, piece, search."""
+    get = lambda k: int(tuned.get(k, 0))
+    paired = get("sweep_paired") > 0
+    return [3 if get("sweep_bands") == 3 else 4, int(paired), max(get("sweep_grid"), 0), int(get("swept") > 0),
+            max(get("sweep_piece"), 0), int(get("sweep_order") >= 0)]
 
 
 def _probe_check(lib, status: int, what: str) -> None:
@@ -301,7 +336,7 @@ def _events_ms(fn, reps: int) -> float:
 
 
 def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps: int = 20,
-                   sweep_bands: int = 4, sweep_paired: int = 0) -> list[dict]:
+                   tuned: dict | None = None) -> list[dict]:
     """Per step with a matrix, the time of the replay of that step's gather stream (flyprobe_replay_step: the
     state step's own kernel, launch shape and wave order over this plan's A_t and a state of this layout, with
     the arithmetic, row inputs and stores taken out), and of the replay that keeps the row reads and stores
@@ -329,26 +364,24 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
                      "flyprobe_pack")
         del col, val
         xprev = (torch.randn(prev_rows, ld, device=dev) * 0.01).to(dtype)
-        # the band table of the evaluator's banded sweep: where the evaluator sweeps this step (same rule), the
-        # probe replays the swept kernel
+        # where the evaluator sweeps this step, the probe replays the swept kernel over tables from the same builder
+        # and configuration (the plan's tuning), which are then the plan's own
         import ctypes
-        bands = sweep_bands
-        band_off = torch.empty(nr * (bands + 1), dtype=torch.int32, device=dev)
-        order = torch.empty(nr, dtype=torch.int32, device=dev)
-        swept = ctypes.c_int32(0)
-        paired = int(sweep_paired > 0 or (sweep_paired == 0 and not state_f16))   # the plan's rule for its order
-        _probe_check(probe, probe.flyprobe_band_table(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz, prev_rows, bands,
-                                                      paired, band_off.data_ptr(), order.data_ptr(),
-                                                      ctypes.byref(swept), st),
-                     "flyprobe_band_table")
-        band_ptr, order_ptr = (band_off.data_ptr(), order.data_ptr()) if swept.value else (None, None)
+        info = _hip.sweep_info(plan.handle, t)
+        sweep = ctypes.c_void_p()
+        if info["positions"]:
+            cfg = (ctypes.c_int32 * 6)(*sweep_config(tuned or {}, state_f16))
+            _probe_check(probe, probe.flyprobe_sweep_create(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz, prev_rows,
+                                                            cfg, ctypes.byref(sweep), st), "flyprobe_sweep_create")
 
         def once():
             _probe_check(probe, probe.flyprobe_replay_step(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz,
                                                            xprev.data_ptr(), prev_rows, ld, batch, int(state_f16),
-                                                           band_ptr, order_ptr, bands, sink.data_ptr(), st),
+                                                           sweep, sink.data_ptr(), st),
                          "flyprobe_replay_step")
-        row = {"t": t, "rows": nr, "nnz": nnz, "swept": bool(swept.value), "replay_ms": round(_events_ms(once, reps), 4)}
+        row = {"t": t, "rows": nr, "nnz": nnz, "swept": bool(sweep.value), "replay_ms": round(_events_ms(once, reps), 4)}
+        if info["pieces"]:
+            row["split_rows"], row["pieces"] = info["split_rows"], info["pieces"]
         # with the row I/O: each row's constants, carried state and input drive (float32, as the model forward's
         # encoder writes it) read, and the new state written
         prev32 = torch.empty(nr, dtype=torch.int32, device=dev)
@@ -365,11 +398,13 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
             _probe_check(probe, probe.flyprobe_replay_step_io(rowptr.data_ptr(), pairs.data_ptr(), params.data_ptr(),
                                                               nr, nnz, xprev.data_ptr(), prev_rows, ld, u.data_ptr(),
                                                               n_in, ldu, xout.data_ptr(), batch, int(state_f16),
-                                                              band_ptr, order_ptr, bands, st),
+                                                              sweep, st),
                          "flyprobe_replay_step_io")
         row["replay_io_ms"] = round(_events_ms(once_io, reps), 4)
         out.append(row)
-        del rowptr, pairs, xprev, prev32, usrc32, params, u, xout, band_off, order
+        if sweep.value:
+            probe.flyprobe_sweep_destroy(sweep)
+        del rowptr, pairs, xprev, prev32, usrc32, params, u, xout
     return out
 
 
@@ -452,7 +487,7 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1120)
     ap.add_argument("--recurrent-steps", type=int, default=6)
     ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
-    ap.add_argument("--graph", choices=["synthetic", "shuffled"], default="synthetic")
+    ap.add_argument("--graph", choices=["synthetic", "shuffled", "realdeg"], default="synthetic")
     ap.add_argument("--ones", default="40", help="ones per board: N or LO-HI")
     ap.add_argument("--no-prune", action="store_true",
                     help="compute every neuron at every step (the same function without the light cone)")
@@ -499,7 +534,7 @@ def main() -> int:
         print(json.dumps(train_bench(args, dev)), flush=True)
         return 0
     t0 = time.perf_counter()
-    net, conn = synthetic_net(steps=args.recurrent_steps, seed=0, shuffled=args.graph == "shuffled", device=dev)
+    net, conn = bench_net(args, dev)
     net.infer_dtype = torch.float16 if args.dtype == "f16" else torch.float32
     net.light_cone_pruning = not args.no_prune
     ones = tuple(int(v) for v in args.ones.split("-")) if "-" in args.ones else int(args.ones)
@@ -604,13 +639,11 @@ def main() -> int:
         # the ceiling: each step's own gather stream replayed alone (same kernel, shape and order, no arithmetic)
         plan = brain._cone_plan(cone, mode)
         tuned = dict(kv.split("=") for kv in args.tune)
-        bands = 3 if tuned.get("sweep_bands") == "3" else 4      # the plan's band count (sweep_bands tuning)
         probe = _probe_lib()
         for key in ("sweep_paired", "sweep_slots", "sweep_pipe"):     # the swept kernel's launch-time choices
             if key in tuned:
                 _probe_check(probe, probe.flyprobe_set_tuning(key.encode(), int(tuned[key])), "flyprobe_set_tuning")
-        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev, sweep_bands=bands,
-                              sweep_paired=int(tuned.get("sweep_paired", 0)))
+        rows = replay_ceiling(plan, cone, len(net.in_idx), args.batch, args.dtype == "f16", dev, tuned=tuned)
         for r in rows:
             r["step_ms"] = round(per_step[r["t"]], 4)
             r["replay_over_step"] = round(r["replay_ms"] / r["step_ms"], 4)
@@ -635,6 +668,30 @@ def main() -> int:
         roofline["random_gather_GBps"] = rates
         roofline["random_gather_rows_per_s_21MB_G"] = rows_per_s
         log(f"uniform random-row gathers {rates} GB/s; state step gathers at {roofline['gather_GBps']} GB/s")
+        # The line rate: the state step moves one 128-byte line of the previous state per non-zero and chunk of
+        # columns (64 of the float16 state, 32 of float32); against the rate of uniformly random 128-byte reads
+        # from an L2-resident set in the same lane layout, the fastest such reads run on this chip.
+        per_line = 128 // state_bytes
+        chunks = -(-args.batch // per_line)
+        lines = sum(cone.nnz) * chunks
+        step_fwd_ms = avg_launch_ms * launches_per_fwd
+        probe = rates["l2_2MB"] * 1e9 / 128
+        line_rate = {"lines_per_forward": int(lines), "achieved_G_lines_per_s": round(lines / (step_fwd_ms * 1e-3) / 1e9, 2),
+                     "l2_probe_G_lines_per_s": round(probe / 1e9, 2),
+                     "frac": round(lines / (step_fwd_ms * 1e-3) / probe, 4), "per_step": []}
+        for t, ms in per_step.items():
+            n_t = cone.nnz[t] * chunks
+            if n_t:
+                line_rate["per_step"].append({"t": t, "lines": int(n_t), "ms": round(ms, 4),
+                                              "G_lines_per_s": round(n_t / (ms * 1e-3) / 1e9, 2),
+                                              "frac": round(n_t / (ms * 1e-3) / probe, 4)})
+        line_rate["note"] = ("gathered 128-byte lines (non-zeros x column chunks) per second of state step, against "
+                             "uniformly random 128-byte reads over a 2 MB (L2-resident) set in the same lane layout "
+                             "(flyprobe_random_gather); frac stays on lines, roofline.frac on algorithmic bytes")
+        roofline["line_rate"] = line_rate
+        log(f"line rate: {line_rate['achieved_G_lines_per_s']} G lines/s of state step against "
+            f"{line_rate['l2_probe_G_lines_per_s']} for L2-resident random reads ({line_rate['frac']:.3f}); "
+            f"per step {[(r['t'], r['G_lines_per_s'], r['frac']) for r in line_rate['per_step']]}")
 
     evaluator = None
     if args.evaluator_steps > 0:

@@ -8,7 +8,9 @@
  * matching destroy.  `stream` is a hipStream_t passed as void* (torch's current stream); every
  * launch goes on it.  Only the create functions synchronise (they read sizes back to the host);
  * the forward entry points are asynchronous.  Index arrays are int32, the graph is CSR of
- * W[post, pre] (row = postsynaptic neuron).  Objects are not thread-safe.
+ * W[post, pre] (row = postsynaptic neuron).  A created object is immutable apart from the cone's cache of sweep
+ * tables, which takes a lock: plans may be created and forwards run from several threads, each with its own
+ * workspace and stream.  fly_set_tuning changes the defaults of objects created afterwards.
  *
  * Reference interfaces replaced (paths relative to the alpha-fly repository):
  *   fly_cone_*            chessfly/brain.py:126-173 LightCone, :102-123 _SubMatrix, :232-236 light_cone
@@ -46,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FLY_ABI_VERSION 1
+#define FLY_ABI_VERSION 2
 
 enum fly_status {
     FLY_OK = 0,
@@ -63,6 +65,7 @@ enum fly_mode {
 
 typedef struct fly_cone fly_cone;
 typedef struct fly_plan fly_plan;
+typedef struct fly_sweep fly_sweep;
 
 int fly_abi_version(void);
 const char *fly_last_error(void);
@@ -97,25 +100,48 @@ int fly_edge_weights(const float *sign_dev, const float *w0_dev, const float *lo
 
 /* Weight-set plan for forward_io: per-step sub-matrices with float32 values, per-row constants and the
  * resting trajectory, from the cone and the graph (crow/pre as given to fly_cone_create), edge weights w
- * (n_edges), bias and alpha_logit (n).  The plan is self-contained: the inputs may be freed afterwards.
+ * (n_edges), bias and alpha_logit (n).  The plan keeps no pointer to its inputs: they may be freed afterwards.
  * Activity is clamped to [0, h_max]; h_max = +INFINITY clamps only below (the reference's h_max=None,
- * chessfly/brain.py:178-182, 221).  A negative or NaN h_max is FLY_ERR_INVALID. */
+ * chessfly/brain.py:178-182, 221).  A negative or NaN h_max is FLY_ERR_INVALID.
+ * The plan captures the tuning (fly_set_tuning) current at its creation.  Long-row steps run as a banded sweep
+ * over tables that depend only on the cone's structure: the cone builds them on the first plan that needs them
+ * and every later plan of the cone (each new weight version) shares them, so only that first plan pays for them.
+ * A plan holds a reference to them, so it outlives fly_cone_destroy. */
 int fly_plan_create(const fly_cone *cone, const int32_t *crow_dev, const int32_t *pre_dev, const float *w_dev,
                     const float *bias_dev, const float *alpha_logit_dev, float h_max, int32_t mode,
                     void *stream, fly_plan **out);
-/* Plan for the literal recurrence over the whole matrix (mode FLY_MODE_F32, every row carried). */
+/* Plan for the literal recurrence over the whole matrix (mode FLY_MODE_F32, every row carried).  sweep: the banded-
+ * sweep tables of the matrix's structure (fly_sweep_create over crow/pre), shared by every plan of
+ * the structure; NULL runs every step on the grouped kernel. */
 int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *crow_dev, const int32_t *pre_dev,
-                         const float *w_dev, const float *alpha_logit_dev, float h_max, void *stream,
-                         fly_plan **out);
+                         const float *w_dev, const float *alpha_logit_dev, float h_max, const fly_sweep *sweep,
+                         void *stream, fly_plan **out);
 int fly_plan_destroy(fly_plan *plan);
 /* c_T[out_idx] (n_out floats): the outputs of a network that sees no position. */
 int fly_plan_resting(const fly_plan *plan, float *c_out_dev, void *stream);
+/* How step t runs (t = 1 for a literal plan): info[7] = {positions of the sweep order, pieces of split rows, rows
+ * split, rows per wave, bands, workgroups, an identity of the tables (equal for plans that share them)}, all 0 when
+ * the step does not sweep. */
+int fly_plan_sweep_info(const fly_plan *plan, int32_t t, int64_t *info);
 /* The plan's sub-matrix A_t as the step kernels read it, the cached per-step matrix of chessfly/brain.py:267-268
  * (fp16 path) and :303 (float32 path): row pointer (|R_t|+1), local column and float32 value (nnz_t each), in
  * W's edge order.  Nothing is written where A_t does not exist; NULL skips an array.  A literal plan has one
  * matrix, t = 1 (W itself). */
 int fly_plan_matrix(const fly_plan *plan, int32_t t, int32_t *rowptr_dev, int32_t *col_dev, float *val_dev,
                     void *stream);
+
+/* ---- banded-sweep tables of one structure ----------------------------------------------------- */
+/* No counterpart in the reference (cuSPARSE keeps its own analysis).  The tables a swept product or literal step
+ * reads for a CSR structure: rowptr (nrows+1) and col (nnz) over ncols columns (rows of the operand).  Rows far
+ * longer than the mean (4 x the mean + 64 non-zeros) are split into pieces that each take a share of every band;
+ * the step adds a split row's pieces in piece order.  Captures the tuning current at creation (sweep_paired > 0:
+ * the order is searched for waves that walk two rows per pass).  *out = NULL (FLY_OK) when the structure is too small to
+ * sweep (by size: over 32,768 columns, at least 65,536 rows and 32 non-zeros per row).  Synchronises.
+ * fly_sweep_info: info[7] as fly_plan_sweep_info's. */
+int fly_sweep_create(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t nnz, int64_t ncols,
+                     void *stream, fly_sweep **out);
+int fly_sweep_destroy(fly_sweep *sweep);
+int fly_sweep_info(const fly_sweep *sweep, int64_t *info);
 
 /* ---- forward ----------------------------------------------------------------------------------- */
 /* Bytes of scratch the forward entry points need for `batch` columns (pass at least this many).  A batch whose
@@ -152,9 +178,12 @@ int fly_forward_literal_f64(const fly_plan *plan, double *u_dev, int64_t ldu, co
  * NULL when R_{t-1} is empty (t = 1) and required otherwise; u_in NULL adds no input.  For a plan from
  * fly_plan_create_full, t is 1 and the step is one literal update of every row, x = clamp(W h + u, 0, h_max),
  * h' = lerp(h, x, alpha), with u_in (n, ldu) holding u + bias and xprev NULL for h = 0.  Only columns
- * [0, batch) of the caller's rows are read or written. */
+ * [0, batch) of the caller's rows are read or written.  workspace: fly_plan_step_workspace bytes, 256-byte aligned
+ * (the sums of a swept step's split rows; 0 bytes and NULL for other steps). */
+size_t fly_plan_step_workspace(const fly_plan *plan, int32_t t, int64_t batch);
 int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev_dev, int64_t ldx, const void *u_in_dev,
-                  int64_t ldu, int64_t batch, void *xout_dev, int64_t ldo, void *stream);
+                  int64_t ldu, int64_t batch, void *xout_dev, int64_t ldo, void *workspace_dev,
+                  size_t workspace_bytes, void *stream);
 
 /* ---- dense maps -------------------------------------------------------------------------------- */
 /* Weights of the read-out: RunningNorm statistics and the four linear maps over the n_out outputs. */
@@ -250,19 +279,17 @@ int fly_evaluator_download(const void *src_dev, void *dst_host, size_t bytes, in
  *              gradient of y = A x with g = dL/dy.  With ids (distinct), out[ids[e]] instead (a sub-matrix's
  *              gradient straight into the whole weight vector); accumulate != 0 adds; out holds n_out entries and slots at
  *              or past it are skipped.  out must not overlap g.
- *   fly_sweep_tables / fly_spmm_swept: the forward product as a banded sweep of x's rows (the state step's
- *              swept kernel, storing each row's sums).  fly_sweep_tables builds, once per structure, the band
- *              starts (band_off, nrows x 5 int32) and the row order (order, nrows int32) from rowptr and col
- *              (ncols: rows of x); *swept = 1 when the structure suits a sweep (the state step's rule), else
- *              nothing is built.  It synchronises.  fly_spmm_swept: y = A x from {column, weight bits} records
- *              (nnz int2, CSR order), for batches that are multiples of 4 with 16-byte aligned rows.
+ *   fly_spmm_swept: the forward product as a banded sweep of x's rows (the state step's swept kernel, storing
+ *              each row's sums) over the tables of fly_sweep_create: y = A x from the
+ *              structure's nnz {column, weight bits} records (int2, CSR order), for batches that are multiples of
+ *              4 with 16-byte aligned rows; workspace: fly_spmm_swept_workspace bytes, 256-byte aligned (the sums
+ *              of split rows' pieces; 0 without).  nnz must be the structure's.
  * Gathered operands must be below 2 GiB; rows and columns below 2^24; column indices are not range-checked
  * (a wrong index reads wrong data, never outside x). */
-int fly_sweep_tables(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t nnz, int64_t ncols,
-                     int32_t *band_off_dev, int32_t *order_dev, int32_t *swept, void *stream);
-int fly_spmm_swept(const int32_t *rowptr_dev, const void *records_dev, const int32_t *band_off_dev,
-                   const int32_t *order_dev, int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx,
-                   int64_t batch, float *y_dev, int64_t ldy, void *stream);
+size_t fly_spmm_swept_workspace(const fly_sweep *sweep, int64_t batch);
+int fly_spmm_swept(const fly_sweep *sweep, const void *records_dev, int64_t nnz, const float *x_dev, int64_t ldx,
+                   int64_t batch, float *y_dev, int64_t ldy, void *workspace_dev, size_t workspace_bytes,
+                   void *stream);
 int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val_dev, const int32_t *val_ids_dev,
              int64_t n_val, int64_t nrows, int64_t ncols, const float *x_dev, int64_t ldx, int64_t batch,
              float *y_dev, int64_t ldy, int32_t accumulate, void *stream);
@@ -398,7 +425,10 @@ int fly_profile_read(double *ms, int64_t *launches);
 int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
 
 /* ---- tuning (for sweeps; defaults are the measured best) --------------------------------------- */
-/* key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept
+/* Defaults for objects created afterwards: a plan, dense plan or fly_sweep captures the tuning current at its
+ * creation, so plans built under different tuning each keep their own; the training products and
+ * fly_evaluator_download read it at each call.  Set and read under a lock.
+ * key "vec": elements per lane of the state step kernel (0 = automatic); "tiles": batch tiles swept
  * row-major (0 = automatic, 1 = all column chunks of a row back to back); "unroll": non-zeros each wave
  * gathers per iteration (8, 16 or 32; 0 = automatic); "nt_store": 1 writes the new state with non-temporal
  * stores; "groups": lane groups per wave that gather different non-zeros (1, 2, 4, 8; 0 = automatic);
@@ -408,14 +438,19 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * maps (1 = 64 x 64, 2 = 128 x 64, 3 = 128 x 128, or 10 TM + TN for 32 TM x 32 TN with TM in {2, 3, 4} and TN in
  * {2, 4, 5}; 0 = automatic); "step_lds": bytes of LDS each state-step workgroup reserves, which caps the
  * workgroups a CU runs at once (0 = none); "download_blocks": workgroups of fly_evaluator_download when its call
- * passes 0 (0 = 16); "swept": -1 keeps the long-row steps on the grouped kernel instead of the banded sweep (0 =
- * automatic); "sweep_bands": source bands of the sweep, 3 or 4 (0 = 4), read when a plan is created;
- * "sweep_order": -1 lets the swept waves take their rows in index order instead of the plan's searched order (0);
- * "sweep_paired": 1 makes every swept wave walk two rows per pass, -1 one, 0 two for float32 states only;
- * "sweep_slots": 3 makes swept waves take their rows in passes of 3 slots (0: 6 when a wave owns over 24 rows);
- * "sweep_pipe": the next four rounds' gathers in flight during the sums, 0 in passes of 3 slots, 1 also of 6, -1
- * never.  Every selectable shape computes the same function. */
+ * passes 0 (0 = 16); "swept": -1 keeps the long-row steps on the grouped kernel instead of the banded sweep, 1
+ * sweeps every step with a matrix whatever its size (small graphs in tests), 0 = the size rule; "sweep_bands":
+ * source bands of the sweep, 3 or 4 (0 = 4); "sweep_order": -1 lets the swept waves take their rows in the initial
+ * order instead of the searched one (0); "sweep_grid": workgroups of a swept step (0: one per CU), which sets the rows
+ * each wave owns; "sweep_piece": split rows longer than this many non-zeros into pieces of at most this many (0: rows
+ * longer than 4 x the mean + 64 into pieces of at most 2 x the mean + 32); "sweep_paired": 1 makes every swept wave
+ * that owns over 24 rows walk two rows per pass (0, -1: one); "sweep_slots": 3 makes swept waves take their
+ * rows in passes of 3 slots (0: 6 when a wave owns over 24 rows); "sweep_pipe": the next four rounds' gathers in
+ * flight during the sums, 0 in passes of 3 slots, 1 also of 6, -1 never.  Every selectable shape computes the same
+ * function. */
 int fly_set_tuning(const char *key, int64_t value);
+/* The current default of a tuning key (as fly_set_tuning left it). */
+int fly_get_tuning(const char *key, int64_t *value);
 
 #ifdef __cplusplus
 }

@@ -55,3 +55,15 @@ def random_params(conn: Connectome, seed: int, gain_sd: float = 0.3, bias_mean: 
     return (rng.normal(0, gain_sd, conn.n_edges).astype(np.float32),
             rng.normal(bias_mean, bias_sd, conn.n_neurons).astype(np.float32),
             rng.normal(0, alpha_sd, conn.n_neurons).astype(np.float32))
+
+
+REALDEG_FIXTURE = os.path.join(REPO, "tests", "golden", "realdeg_fixture.npz")
+
+
+def realdeg_connectome(seed: int = 0) -> Connectome:
+    """The full-scale graph with the MaleCNS wiring's in-degree sequence and sensory / output sets (the committed
+    fixture made by tests/golden/make_realdeg_fixture.py) and partners drawn from `seed`."""
+    from chessfly.synthetic import degree_connectome
+    f = np.load(REALDEG_FIXTURE)
+    ids = lambda gaps: np.cumsum(gaps.astype(np.int64))
+    return degree_connectome(f["in_degree"], ids(f["in_idx_gaps"]), ids(f["out_idx_gaps"]), seed=seed)

@@ -47,7 +47,7 @@ def test_binding_covers_the_header_exactly():
 
 
 def test_version_and_error_reporting_on_host(lib):
-    assert lib.fly_abi_version() == 1
+    assert lib.fly_abi_version() == 2
     assert lib.fly_set_tuning(b"no-such-knob", 1) == 1          # FLY_ERR_INVALID
     assert b"no-such-knob" in lib.fly_last_error()
     out = ctypes.c_void_p()
@@ -98,7 +98,7 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     i64, p_ = ctypes.c_int64, ctypes.c_void_p
     probe.flyprobe_random_gather.argtypes = [p_, i64, i64, i64, p_, i64, p_, p_]
     i32 = ctypes.c_int32
-    probe.flyprobe_replay_step.argtypes = [p_, p_, i64, i64, p_, i64, i64, i64, i32, p_, p_, i32, p_, p_]
+    probe.flyprobe_replay_step.argtypes = [p_, p_, i64, i64, p_, i64, i64, i64, i32, p_, p_, p_]
     assert probe.flyprobe_random_gather(None, 1024, 128, 128, None, 10, None, None) == 1
     buf = ctypes.create_string_buffer(16)
     p = ctypes.addressof(buf)
@@ -107,21 +107,52 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     assert b"row_bytes" in probe.flyprobe_last_error()
     assert probe.flyprobe_random_gather(p, 1024, 128, 96, p, 10, p, None) == 1
     assert b"read_bytes" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(None, None, 10, 10, None, 10, 64, 64, 1, None, None, 0, None, None) == 1
+    assert probe.flyprobe_replay_step(None, None, 10, 10, None, 10, 64, 64, 1, None, None, None) == 1
     assert b"null" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 32, 64, 1, None, None, 0, p, None) == 1
+    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 32, 64, 1, None, p, None) == 1
     assert b"layout" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step(p, p, 10, 10, p, 10, 64, 64, 1, p, p, 5, p, None) == 1
-    assert b"bands" in probe.flyprobe_last_error()
     probe.flyprobe_replay_step_io.argtypes = [p_, p_, p_, i64, i64, p_, i64, i64, p_, i64, i64, p_, i64, i32, p_,
-                                              p_, i32, p_]
-    assert probe.flyprobe_replay_step_io(p, p, None, 10, 10, p, 10, 64, None, 0, 0, p, 64, 1, None, None, 0,
-                                         None) == 1
+                                              p_]
+    assert probe.flyprobe_replay_step_io(p, p, None, 10, 10, p, 10, 64, None, 0, 0, p, 64, 1, None, None) == 1
     assert b"null" in probe.flyprobe_last_error()
-    assert probe.flyprobe_replay_step_io(p, p, p, 10, 10, p, 10, 64, p, 5, 32, p, 64, 1, None, None, 0, None) == 1
+    assert probe.flyprobe_replay_step_io(p, p, p, 10, 10, p, 10, 64, p, 5, 32, p, 64, 1, None, None) == 1
     assert b"input drive" in probe.flyprobe_last_error()
-    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, i32, p_, p_, p_, p_]
-    assert probe.flyprobe_band_table(p, p, 10, 100, 10, 8, 0, p, p, p, None) == 1
-    assert b"bands" in probe.flyprobe_last_error()
-    assert probe.flyprobe_band_table(None, p, 10, 100, 10, 4, 0, p, p, p, None) == 1
+    probe.flyprobe_sweep_create.argtypes = [p_, p_, i64, i64, i64, p_, ctypes.POINTER(p_), p_]
+    out = p_(12345)
+    cfg = (ctypes.c_int32 * 6)(8, 0, 0, 0, 0, 1)
+    assert probe.flyprobe_sweep_create(p, p, 10, 100, 10, cfg, ctypes.byref(out), None) == 1
+    assert b"bands" in probe.flyprobe_last_error() and out.value is None
+    cfg[0] = 4
+    assert probe.flyprobe_sweep_create(None, p, 10, 100, 10, cfg, ctypes.byref(out), None) == 1
     assert b"null" in probe.flyprobe_last_error()
+
+
+def test_tuning_is_read_and_written_under_a_lock(lib):
+    """fly_set_tuning from several threads at once while others read the values back (fly_get_tuning): every read
+    sees a value some writer set, unknown keys are refused, and the defaults come back when set."""
+    import threading
+    keys = [b"sweep_grid", b"sweep_piece", b"unroll", b"gemm_tile"]
+    errors = []
+
+    def writer(k, base):
+        for i in range(2000):
+            if lib.fly_set_tuning(k, base + i % 7) != 0:
+                errors.append(("set", k))
+
+    def reader(k, base):
+        v = ctypes.c_int64(-1)
+        for _ in range(2000):
+            if lib.fly_get_tuning(k, ctypes.byref(v)) != 0 or not (v.value == 0 or base <= v.value < base + 7):
+                errors.append(("get", k, v.value))
+
+    threads = [threading.Thread(target=f, args=(k, 10 * (j + 1))) for j, k in enumerate(keys) for f in (writer, reader)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:5]
+    v = ctypes.c_int64(-1)
+    assert lib.fly_get_tuning(b"no-such-knob", ctypes.byref(v)) == 1
+    for k in keys:
+        assert lib.fly_set_tuning(k, 0) == 0
+        assert lib.fly_get_tuning(k, ctypes.byref(v)) == 0 and v.value == 0

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 import torch
 
+from conftest import swept_steps
 from helpers import brain_arrays, head_arrays, random_params, tiny_connectome
 
 from oracle import brute, lightcone as L, forward as F
@@ -78,6 +79,36 @@ def _check_model(net, x, ref, boards, label, dtypes=(torch.float32, torch.float1
     return outs
 
 
+def _run(net, x, dtypes=(torch.float32, torch.float16)):
+    """net(x) in each dtype: {dtype: (logits, wdl)} on the device."""
+    outs = {}
+    try:
+        for dtype in dtypes:
+            net.infer_dtype = dtype
+            with torch.no_grad():
+                outs[dtype] = net(x.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        net.infer_dtype = torch.float16
+    return outs
+
+
+def _check_boards(outs, ref, label, rows=None):
+    """Boards `rows` (all: None) of each dtype's output against the oracle's float32 forward of those boards (ref):
+    max |logit diff| and max |wdl diff| below 1e-3 and the policy argmax equal on at least 99.9% of the boards (the
+    north star's bar, at the reference's fp32 path); prints the figures."""
+    ref_logits, ref_wdl = ref
+    for dtype, (logits, wdl) in outs.items():
+        lg, wd = logits.cpu(), wdl.cpu()
+        if rows is not None:
+            lg, wd = lg[rows], wd[rows]
+        dl, dw = float((lg - ref_logits).abs().max()), float((wd - ref_wdl).abs().max())
+        agree = (lg.argmax(1) == ref_logits.argmax(1)).float()
+        print(f"{label} {dtype}: {lg.shape[0]} boards, max |logit - oracle| {dl:.3e}, max |wdl - oracle| {dw:.3e}, "
+              f"argmax agrees on {int(agree.sum())}/{lg.shape[0]} ({float(agree.mean()):.4%})", flush=True)
+        assert dl < 1e-3 and dw < 1e-3 and float(agree.mean()) >= 0.999, (label, dtype, dl, dw)
+
+
 def _agree(outs, label):
     """float16 deviation vs float32 on every board: within 1e-3, argmax on >= 99.9% of the boards."""
     (l32, w32), (l16, w16) = outs[torch.float32], outs[torch.float16]
@@ -127,8 +158,8 @@ def test_shuffled_small_graph_sums_repeats_and_self_loops():
 
 def test_full_scale_shuffled_control_forward_matches_oracle():
     """The degree-preserving control graph at full scale (166,700 neurons, seed 0), B = 1120 boards through
-    FlyChessNet in both dtypes: the first 32 boards against the oracle's float32 forward on the shuffled arrays,
-    and the float16 deviation path against float32 on all 1120."""
+    FlyChessNet in both dtypes: every board against the oracle's float32 forward on the shuffled arrays, and the
+    float16 deviation path against float32 on all 1120."""
     from chessfly.synthetic import FULL, _cached_graph, synthetic_boards, synthetic_net
     net, conn_s = synthetic_net(steps=6, seed=0, shuffled=True, device=DEV)
     orig = _cached_graph(FULL)
@@ -139,8 +170,8 @@ def test_full_scale_shuffled_control_forward_matches_oracle():
     assert repeats > 0 and loops > 0
     ba, hp, cone = _full_oracle(conn_s, orig)
     x = torch.as_tensor(synthetic_boards(1120, seed=17))
-    ref = F.model_forward(ba, hp, cone, x[:32], "f32")
-    outs = _check_model(net, x, ref, 32, "shuffled B=1120")
+    outs = _run(net, x)
+    _check_boards(outs, F.model_forward(ba, hp, cone, x, "f32"), "shuffled B=1120")
     _agree(outs, "shuffled B=1120")
     del net
     torch.cuda.empty_cache()
@@ -190,15 +221,71 @@ def test_full_scale_float32_unpruned_b64_matches_literal_recurrence(full_net):
 # ---- boards with 20-40 ones at B = 256 ----------------------------------------------------------------------
 
 def test_full_scale_b256_boards_with_20_to_40_ones(full_net):
+    """All 256 boards of the B = 256 workload (20-40 ones per board) against the oracle's float32 forward."""
     from chessfly.synthetic import synthetic_boards
     net, conn = full_net
     ba, hp, cone = _full_oracle(conn, conn)
     x = torch.as_tensor(synthetic_boards(256, seed=31, ones=(20, 40)))
     ones = x[:, :838].sum(1)
     assert int(ones.min()) >= 20 and int(ones.max()) <= 40 and int(ones.max()) > int(ones.min())
-    ref = F.model_forward(ba, hp, cone, x[:32], "f32")
-    outs = _check_model(net, x, ref, 32, "B=256 20-40 ones")
+    outs = _run(net, x)
+    _check_boards(outs, F.model_forward(ba, hp, cone, x, "f32"), "B=256 20-40 ones")
     _agree(outs, "B=256 20-40 ones")
+
+
+def test_full_scale_b1120_every_board_matches_oracle(full_net):
+    """The headline workload (light cone, B = 1120, 40 ones per board): every board, both dtypes, against the
+    oracle's float32 forward, and the plan's long-row steps (3-5) on the banded sweep."""
+    from chessfly import _hip
+    from chessfly.synthetic import synthetic_boards
+    net, conn = full_net
+    ba, hp, cone = _full_oracle(conn, conn)
+    x = torch.as_tensor(synthetic_boards(1120, seed=43))
+    outs = _run(net, x)
+    _check_boards(outs, F.model_forward(ba, hp, cone, x, "f32"), "B=1120")
+    dcone = net.brain.light_cone(net.in_idx, net.out_idx, 6)
+    for mode in (_hip.MODE_DEVIATION_F16, _hip.MODE_F32):
+        assert [t for t, *_ in swept_steps(net.brain._cone_plan(dcone, mode).handle, 6)] == [3, 4, 5]
+
+
+@pytest.mark.parametrize("batch,rows", [(4096, np.r_[0:32, 4064:4096]), (8192, np.r_[4096:4128, 8160:8192])])
+def test_full_scale_large_batches_far_boards_match_oracle(full_net, batch, rows):
+    """B = 4096 (its first and last 32 boards) and B = 8192, which runs as two column blocks of 4,096 boards in
+    float16 and three in float32 (the state stays below 2 GiB): the second block's first and last 32 boards, both
+    dtypes, against the oracle's float32 forward."""
+    from chessfly.synthetic import synthetic_boards
+    net, conn = full_net
+    ba, hp, cone = _full_oracle(conn, conn)
+    x = torch.as_tensor(synthetic_boards(batch, seed=47, ones=(20, 40)))
+    outs = _run(net, x)
+    _check_boards(outs, F.model_forward(ba, hp, cone, x[rows], "f32"), f"B={batch}", rows=rows)
+    del outs
+    torch.cuda.empty_cache()
+
+
+def test_full_scale_real_in_degrees_forward_matches_oracle():
+    """The network on the graph with the MaleCNS wiring's in-degrees (hub rows of up to 9,193 partners, 2,190 rows
+    with none; partners seeded): its long-row steps sweep with the hub rows split into pieces, and B = 64 (every
+    board) and B = 1120 (the first and last 64-board chunks) in both dtypes match the oracle's float32 forward."""
+    from chessfly import _hip
+    from chessfly.synthetic import synthetic_boards, synthetic_net
+    from helpers import realdeg_connectome
+    conn = realdeg_connectome()
+    net, _ = synthetic_net(steps=6, seed=0, device=DEV, graph=conn)
+    ba, hp, cone = _full_oracle(conn, conn)
+    dcone = net.brain.light_cone(net.in_idx, net.out_idx, 6)
+    x = torch.as_tensor(synthetic_boards(1120, seed=53))
+    rows = np.r_[0:64, 1056:1120]
+    outs = _run(net, x)
+    _check_boards(outs, F.model_forward(ba, hp, cone, x[rows], "f32"), "real in-degrees B=1120", rows=rows)
+    for mode in (_hip.MODE_DEVIATION_F16, _hip.MODE_F32):
+        swept = swept_steps(net.brain._cone_plan(dcone, mode).handle, 6)
+        print(f"real in-degrees, mode {mode}: swept steps (t, positions, pieces, workgroups) {swept}", flush=True)
+        assert {3, 4} <= {t for t, *_ in swept} and all(p > 0 for t, _, p, _ in swept if t in (3, 4))
+    x64 = x[:64]
+    _check_boards(_run(net, x64), F.model_forward(ba, hp, cone, x64, "f32"), "real in-degrees B=64")
+    del net
+    torch.cuda.empty_cache()
 
 
 # ---- attack planes: the encoder over all 967 feature columns -------------------------------------------------
@@ -281,7 +368,7 @@ def _medium(seed):
     return synthetic_connectome(GraphSpec(n=3000, edges=120_000, n_sensory=300, n_output=80, seed=seed))
 
 
-def test_unbounded_activity_literal_and_light_cone():
+def test_unbounded_activity_literal_and_light_cone(sweep_core):
     """ConnectomeRNN(h_max=None) (brain.py:178-182, 221) with biases that drive activity past 10: the literal
     recurrence and forward_io in float32 against the float64 oracle, and the float16 deviation path against the
     exact function."""
@@ -313,7 +400,7 @@ def test_unbounded_activity_literal_and_light_cone():
     assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
 
 
-def test_other_activity_bounds_literal_and_light_cone():
+def test_other_activity_bounds_literal_and_light_cone(sweep_core):
     """A bound other than 10 (the reference's fused kernel applies only at h_max == 10, brain.py:310; its general
     path clamps to any h_max, brain.py:321): activity pushed past h_max = 3.5 by the biases, the literal recurrence
     and forward_io in float32 against the float64 oracle, and the float16 deviation path against the exact
@@ -348,17 +435,21 @@ def test_other_activity_bounds_literal_and_light_cone():
 # ---- fly_plan_step: one step at a time ---------------------------------------------------------------------------
 
 def _plan_step(lib, _hip, plan, t, xprev, u, batch, xout):
+    ws = _hip.workspace(lib.fly_plan_step_workspace(plan.handle, t, batch), torch.device(DEV))
     _hip.check(lib.fly_plan_step(plan.handle, t, _hip.ptr(xprev), xprev.stride(0) if xprev is not None else 0,
                                  _hip.ptr(u), u.stride(0) if u is not None else 0, batch, xout.data_ptr(),
-                                 xout.stride(0), _hip.stream(torch.device(DEV))), "fly_plan_step")
+                                 xout.stride(0), ws.data_ptr(), ws.numel(), _hip.stream(torch.device(DEV))),
+               "fly_plan_step")
 
 
-@pytest.mark.parametrize("batch", [5, 64, 100])
-def test_plan_step_matches_the_oracle_step_by_step(batch):
+@pytest.mark.parametrize("batch", [5, 64, 100, 136])
+def test_plan_step_matches_the_oracle_step_by_step(batch, sweep_core):
     """fly_plan_step (the per-step op of brain.py:273-277 / 310-313) fed the oracle's own state of R_{t-1}:
     float32 mode against f32_step in float64 (2e-5), deviation mode against deviation_step in float64 on the same
     float16-rounded inputs (one float16 rounding of the result), every step of a 6-step cone.  Batches of 5 and
-    100 end inside a lane's columns, so no lane may read or write past the caller's columns."""
+    100 end inside a lane's columns, so no lane may read or write past the caller's columns (the banded sweep takes
+    the float16 state only at batches in whole 8-column lanes, the float32 state at batches in whole 4-column
+    lanes, under the forced sweep modes)."""
     from chessfly import _hip
     lib = _hip.load()
     conn = _medium(5)
@@ -378,6 +469,8 @@ def test_plan_step_matches_the_oracle_step_by_step(batch):
     with torch.no_grad():
         p32 = rnn._cone_plan(dcone, _hip.MODE_F32)
         p16 = rnn._cone_plan(dcone, _hip.MODE_DEVIATION_F16)
+    if sweep_core != "auto":
+        assert swept_steps(p32.handle, steps) and swept_steps(p16.handle, steps), "the forced sweep has no tables"
     u32, u16 = u_in.to(DEV), u_in.half().to(DEV)
     for t in range(1, steps + 1):
         rows = len(cone.rows[t])
@@ -510,7 +603,7 @@ def test_literal_recurrence_in_float64(h_max):
 # ---- forward_io in float64 ---------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("h_max", [10.0, None])
-def test_forward_io_in_float64(h_max):
+def test_forward_io_in_float64(h_max, sweep_core):
     """forward_io with float64 u_in (brain.py:295-329 in u_in's dtype): the float32 cache widens, the state and
     every sum and update are float64, and the outputs come back float64.  With log_gain, bias and alpha_logit zero
     the cache is exact (resting trajectory 0, weights sign * w0, alpha 1/2), so the device matches the float64

@@ -527,7 +527,8 @@ def _balance_numpy(order, cnt, per, groups, steps, paired=False):
     the group's wave totals plus their sum; at each step each of 256 threads (xorshift32 per group and thread) draws
     two positions of the group, scores the change a swap of their rows would make (the other waves' largest total
     from the band's three largest), and the lowest score (ties: lowest thread) is made if it adds no cost."""
-    nr, bands = cnt.shape
+    bands = cnt.shape[1]
+    nr = len(order)      # positions of the order
     W, L = 16, 256
     U = 16 if paired else 8
     order = order.copy()
@@ -610,17 +611,31 @@ def _balance_numpy(order, cnt, per, groups, steps, paired=False):
     return order
 
 
-def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_steps=600, groups=None, paired=False):
-    """The swept step's plan tables restated: off[i][b] = row i's start plus its non-zeros with a column in the
-    bands before b (band of column c: c * bands // prev_rows), off[i][bands] = its end.  The order lists each
-    consecutive segment of `per` rows longest first (ties by row index), then, in segments of at most 64 rows, the
-    plan's wave-parallel local search: at each of `steps` steps, each of 64 lanes (xorshift32 per segment and lane)
-    draws two positions; a pair whose swap can change a unit's rounds (different units, or with `paired` two lane
-    groups of one pass) scores that change; the lowest score (ties: lowest lane) is applied when it adds no rounds.
-    `paired` counts units of two slots walked as one pass, as for a float32 sweep whose waves own over 24 rows.
-    Then each group of 16 segments (the waves of one workgroup) runs the plan's balance search over `balance_steps`
-    steps (_balance_numpy).  Groups are independent: `groups` (indices) limits both searches to those, the others
-    keep the sort."""
+def _deal_numpy(items, vlen, caps):
+    """Items (longest first) each to the bin with the least work that has room (ties: the lower bin)."""
+    import heapq
+    heap = [(0, b) for b in range(len(caps)) if caps[b] > 0]
+    heapq.heapify(heap)
+    bins = [[] for _ in caps]
+    for v in items:
+        work, b = heapq.heappop(heap)
+        bins[b].append(v)
+        if len(bins[b]) < caps[b]:
+            heapq.heappush(heap, (work + int(vlen[v]), b))
+    return bins
+
+
+def _sweep_split_numpy(rowptr, cols, prev_rows, bands, piece=0, grid=None):
+    """The sweep tables' rows restated: off[i][b] = row i's start plus its non-zeros with a column in the bands
+    before b (band of column c: c * bands // prev_rows), off[i][bands] = its end.  Rows longer than the limit
+    (piece, or 4 x the mean + 64) are split into m = ceil(len / p) pieces (p: piece, or max(8, 2 x the mean + 32));
+    piece i of m of row h takes [off[h][b] + n_b i // m, off[h][b] + n_b (i + 1) // m) of each band b.  range
+    ((rows + pieces), 2 bands) holds each row's and then each piece's begin and end per band.  The initial order puts
+    piece j at position (2 j + 1) npos // (2 pieces) and the unsplit rows in index order between; where that leaves
+    some workgroup of 16 waves (grid workgroups, per = ceil(npos / (16 grid)) positions per wave) over 1.05 x the
+    mean work (a piece's work: its row's length share len (i + 1) // m - len i // m), the rows and pieces are dealt
+    longest first (stable) to workgroups, then within each to its waves, by _deal_numpy.  Returns range, the initial
+    order, the split rows and split_ptr."""
     nr = len(rowptr) - 1
     lens = np.diff(rowptr)
     band = cols.astype(np.int64) * bands // prev_rows
@@ -629,12 +644,67 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_
     off[:, 0] = rowptr[:-1]
     off[:, 1:bands] = rowptr[:-1, None] + np.cumsum(cnt, axis=1)[:, :bands - 1]
     off[:, bands] = rowptr[1:]
+    mean = int(rowptr[-1]) / nr
+    limit = piece if piece > 0 else int(4.0 * mean + 64.0)
+    psize = piece if piece > 0 else max(8, int(2.0 * mean + 32.0))
+    split = np.nonzero(lens > limit)[0]
+    m = -(-lens[split] // psize)
+    prow = np.repeat(split, m)
+    pidx = np.concatenate([np.arange(k) for k in m]) if len(m) else np.zeros(0, np.int64)
+    pcnt = np.repeat(m, m)
+    npieces = len(prow)
+    rng = np.empty((nr + npieces, 2 * bands), np.int64)
+    rng[:nr, 0::2] = off[:, :bands]
+    rng[:nr, 1::2] = off[:, 1:]
+    o = off[prow, :bands]
+    n = off[prow, 1:] - o
+    rng[nr:, 0::2] = o + n * pidx[:, None] // pcnt[:, None]
+    rng[nr:, 1::2] = o + n * (pidx + 1)[:, None] // pcnt[:, None]
+    npos = nr - len(split) + npieces
+    init = np.empty(npos, np.int64)
+    at = (2 * np.arange(npieces) + 1) * npos // (2 * npieces) if npieces else np.zeros(0, np.int64)
+    mask = np.zeros(npos, bool)
+    mask[at] = True
+    init[mask] = nr + np.arange(npieces)
+    init[~mask] = np.setdiff1d(np.arange(nr), split)
+    split_ptr = np.concatenate([[0], np.cumsum(m)])
+    if grid is not None:
+        vlen = np.concatenate([lens, lens[prow] * (pidx + 1) // pcnt - lens[prow] * pidx // pcnt]).astype(np.int64)
+        per = -(-npos // (16 * grid))
+        wg_pos = 16 * per
+        n_wg = -(-npos // wg_pos)
+        tot = np.add.reduceat(vlen[init], np.arange(0, npos, wg_pos))
+        if int(tot.max()) * 20 * n_wg > int(tot.sum()) * 21:
+            items = init[np.argsort(-vlen[init], kind="stable")]
+            caps = [min(wg_pos, npos - g * wg_pos) for g in range(n_wg)]
+            for g, its in enumerate(_deal_numpy(items, vlen, caps)):
+                wcap = [max(0, min(per, npos - g * wg_pos - w * per)) for w in range(16)]
+                for w, vs in enumerate(_deal_numpy(its, vlen, wcap)):
+                    init[g * wg_pos + w * per: g * wg_pos + w * per + len(vs)] = vs
+    return rng, init, split, split_ptr
+
+
+def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_steps=600, groups=None, paired=False,
+                        piece=0, grid=None):
+    """The swept step's tables restated (_sweep_split_numpy), then the order: each consecutive segment of `per`
+    positions of the initial order longest first (the sum of its band ranges; ties by initial position), then, in
+    segments of at most 64 positions, the plan's wave-parallel local search: at each of `steps` steps, each of 64
+    lanes (xorshift32 per segment and lane) draws two positions; a pair whose swap can change a unit's rounds
+    (different units, or with `paired` two lane groups of one pass) scores that change; the lowest score (ties:
+    lowest lane) is applied when it adds no rounds.  `paired` counts units of two slots walked as one pass, as for a
+    float32 sweep whose waves own over 24 rows.  Then each group of 16 segments (the waves of one workgroup) runs
+    the plan's balance search over `balance_steps` steps (_balance_numpy).  Groups are independent: `groups`
+    (indices) limits both searches to those, the others keep the sort.  Returns range, order, split, split_ptr."""
+    rng, init, split, split_ptr = _sweep_split_numpy(rowptr, cols, prev_rows, bands, piece, grid)
+    cnt = rng[:, 1::2] - rng[:, 0::2]                  # band counts of the rows and pieces
+    lens = cnt.sum(axis=1)
+    nr = len(init)                                     # positions
     order = np.empty(nr, np.int64)
     for b in range(0, nr, per):
         idx = np.arange(b, min(b + per, nr))
-        order[b:b + len(idx)] = idx[np.lexsort((idx, -lens[idx]))]
+        order[b:b + len(idx)] = init[idx[np.lexsort((idx, -lens[init[idx]]))]]
     if per > 64 or steps == 0:
-        return off, order
+        return rng, order, split, split_ptr
     paired = bool(paired and bands == 4 and per > 24)
     U = 16 if paired else 8
     total_seg = -(-nr // per)
@@ -692,67 +762,91 @@ def _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200, balance_
     order = out.reshape(-1)[:nr]
     if balance_steps:
         order = _balance_numpy(order, cnt, per, groups, balance_steps, paired)
-    return off, order
+    return rng, order, split, split_ptr
 
 
 def test_sweep_band_table_order_and_rule_match_numpy():
-    """The plan-time work of a swept step (k_band_off, the order of k_sweep_order, k_sweep_order_search and
-    k_sweep_order_balance, and the suitability rule of sweep_suits, shared by the plan and the probe library's
-    flyprobe_band_table) against a numpy restatement, bit for bit, on random CSR matrices: 70,000 rows (18 rows per
-    wave: slots of 8, 8 and 2) whose plain form sweeps and whose forms with a hub row (longer than 4 x the mean + 64)
-    or with 32,768 source rows do not, and 110,000 rows (27 per wave) searched for a float32 sweep that walks two
-    slots per pass.  The searches leave each workgroup its rows and each wave its number of rows, and lower the
-    rounds and the workgroups' barrier-bound rounds on this fixed data."""
+    """The tables of a swept step (build_sweep, shared by the plan and the probe library's flyprobe_sweep_create):
+    the range table of rows and split rows' pieces, the split rows, the initial order, the order of k_sweep_order,
+    k_sweep_order_search and k_sweep_order_balance, and the size rule, against a numpy restatement, bit for bit, on
+    random CSR matrices: 70,000 rows (18 rows per wave: slots of 8, 8 and 2) whose plain form sweeps and whose form
+    with 32,768 source rows does not; the same with hub rows (longer than 4 x the mean + 64), which are split into
+    pieces; 110,000 rows (27 per wave) searched for a float32 sweep that walks two slots per pass; and a forced
+    piece size that splits a third of the rows.  The searches leave each workgroup its rows and pieces and each wave
+    its number of positions, and lower the rounds and the workgroups' barrier-bound rounds on this fixed data."""
     import ctypes
     probe = ctypes.CDLL(os.path.join(REPO, "alpha-fly_amd", "csrc", "libflyprobe.so"))
     probe.flyprobe_last_error.restype = ctypes.c_char_p
     i64, i32, p_ = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
-    probe.flyprobe_band_table.argtypes = [p_, p_, i64, i64, i64, i32, i32, p_, p_, ctypes.POINTER(i32), p_]
+    probe.flyprobe_sweep_create.argtypes = [p_, p_, i64, i64, i64, p_, ctypes.POINTER(p_), p_]
+    probe.flyprobe_sweep_read.argtypes = [p_, p_, p_, p_, p_, p_, p_]
+    probe.flyprobe_sweep_destroy.argtypes = [p_]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     rng = np.random.default_rng(41)
     base_lens = rng.poisson(40, 70_000)
     hub = base_lens.copy()
     hub[12_345] = 4 * int(hub.mean()) + 200
-    cases = [("plain", 40_000, base_lens, 1, 0, (3, 4)), ("small source", 32_768, base_lens, 0, 0, (3, 4)),
-             ("hub row", 40_000, hub, 0, 0, (3, 4)), ("pairs", 40_000, rng.poisson(40, 110_000), 1, 1, (4,))]
-    for label, prev_rows, lens, want_swept, paired, band_counts in cases:
+    hub[70] = 3000
+    hub[69_999] = 700
+    clustered = np.sort(rng.poisson(40, 70_000) + rng.integers(0, 60, 70_000))[::-1].copy()   # long rows first
+    cases = [("plain", 40_000, base_lens, 1, 0, (3, 4), 0), ("small source", 32_768, base_lens, 0, 0, (3, 4), 0),
+             ("hub rows", 40_000, hub, 1, 0, (3, 4), 0), ("pairs", 40_000, rng.poisson(40, 110_000), 1, 1, (4,), 0),
+             ("forced pieces", 40_000, base_lens, 1, 0, (4,), 44), ("clustered lengths", 40_000, clustered, 1, 0, (4,), 0)]
+    for label, prev_rows, lens, want_swept, paired, band_counts, piece in cases:
         nr = len(lens)
         rowptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
         cols = np.concatenate([np.sort(rng.integers(0, prev_rows, n)) for n in lens]).astype(np.int32)
         pairs = np.stack([cols, rng.standard_normal(len(cols)).astype(np.float32).view(np.int32)], axis=1)
         d_rowptr = torch.as_tensor(rowptr, device=DEV)
         d_pairs = torch.as_tensor(np.ascontiguousarray(pairs), device=DEV)
-        per = -(-nr // (16 * cus))
-        nseg = -(-nr // per)
-        ngrp = -(-nseg // 16)
         for bands in band_counts:
-            d_off = torch.full((nr, bands + 1), -7, dtype=torch.int32, device=DEV)
-            d_order = torch.full((nr,), -7, dtype=torch.int32, device=DEV)
-            swept = i32(-1)
-            rc = probe.flyprobe_band_table(d_rowptr.data_ptr(), d_pairs.data_ptr(), nr, len(cols), prev_rows, bands,
-                                           paired, d_off.data_ptr(), d_order.data_ptr(), ctypes.byref(swept), None)
+            cfg = (ctypes.c_int32 * 6)(bands, paired, 0, 0, piece, 1)
+            handle = p_()
+            rc = probe.flyprobe_sweep_create(d_rowptr.data_ptr(), d_pairs.data_ptr(), nr, len(cols), prev_rows, cfg,
+                                             ctypes.byref(handle), None)
             assert rc == 0, probe.flyprobe_last_error()
-            torch.cuda.synchronize()
-            check = np.r_[0:6, ngrp - 1]      # the searches restated for these groups of 16 waves (independent)
-            off, order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=200 if want_swept else 0,
-                                             groups=check, paired=bool(paired))
-            got = d_order.cpu().numpy()
-            print(f"{label}, {bands} bands: swept {swept.value}", flush=True)
-            assert swept.value == want_swept, (label, bands, swept.value)
-            assert np.array_equal(d_off.cpu().numpy(), off), (label, bands)
+            print(f"{label}, {bands} bands: swept {bool(handle.value)}", flush=True)
+            assert bool(handle.value) == bool(want_swept), (label, bands)
             if not want_swept:
                 continue
-            sel = np.concatenate([np.arange(16 * g * per, min(16 * (g + 1) * per, nr)) for g in check])
+            want_rng, init, want_split, want_ptr = _sweep_split_numpy(rowptr, cols, prev_rows, bands, piece, cus)
+            npos, nv = len(init), len(want_rng)
+            per = -(-npos // (16 * cus))
+            nseg = -(-npos // per)
+            ngrp = -(-nseg // 16)
+            info = (ctypes.c_int64 * 7)()
+            d_rng = torch.full((nv, 2 * bands), -7, dtype=torch.int32, device=DEV)
+            d_order = torch.full((npos,), -7, dtype=torch.int32, device=DEV)
+            d_split = torch.full((max(len(want_split), 1),), -7, dtype=torch.int32, device=DEV)
+            d_ptr = torch.full((len(want_ptr),), -7, dtype=torch.int32, device=DEV)
+            rc = probe.flyprobe_sweep_read(handle, info, d_rng.data_ptr(), d_order.data_ptr(), d_split.data_ptr(),
+                                           d_ptr.data_ptr(), None)
+            assert rc == 0, probe.flyprobe_last_error()
+            probe.flyprobe_sweep_destroy(handle)
+            torch.cuda.synchronize()
+            assert list(info)[:6] == [npos, nv - nr, len(want_split), per, bands, cus], (label, list(info))
+            assert np.array_equal(d_rng.cpu().numpy(), want_rng), (label, bands)
+            if len(want_split):
+                assert np.array_equal(d_split.cpu().numpy(), want_split) and np.array_equal(d_ptr.cpu().numpy(),
+                                                                                            want_ptr), label
+            print(f"  {len(want_split)} rows split into {nv - nr} pieces, {npos} positions, {per} per wave",
+                  flush=True)
+            check = np.r_[0:6, ngrp - 1]      # the searches restated for these groups of 16 waves (independent)
+            _, order, _, _ = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, groups=check,
+                                                 paired=bool(paired), piece=piece, grid=cus)
+            got = d_order.cpu().numpy()
+            sel = np.concatenate([np.arange(16 * g * per, min(16 * (g + 1) * per, npos)) for g in check])
             assert np.array_equal(got[sel], order[sel]), (label, bands)
-            _, sorted_order = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=0, balance_steps=0)
-            for g0 in range(0, nr, 16 * per):
-                assert np.array_equal(np.sort(got[g0:g0 + 16 * per]), np.arange(g0, min(g0 + 16 * per, nr)))
-            cnt = np.stack([off[:, q + 1] - off[:, q] for q in range(bands)], axis=1)
+            _, sorted_order, _, _ = _sweep_tables_numpy(rowptr, cols, prev_rows, bands, per, steps=0,
+                                                        balance_steps=0, piece=piece, grid=cus)
+            for g0 in range(0, npos, 16 * per):
+                assert np.array_equal(np.sort(got[g0:g0 + 16 * per]), np.sort(init[g0:g0 + 16 * per]))
+            cnt = want_rng[:, 1::2] - want_rng[:, 0::2]
             U = 16 if paired and per > 24 else 8
             def cost(o):   # (rounds, barrier-bound rounds: per workgroup and band the largest wave's)
-                m = np.minimum(per, nr - np.arange(nseg) * per)
+                m = np.minimum(per, npos - np.arange(nseg) * per)
                 pad = np.full(nseg * per + U, -1, np.int64)
-                pad[:nr] = o
+                pad[:npos] = o
                 rows = np.stack([pad[np.arange(nseg) * per + j * U + np.arange(U)[:, None]].T
                                  for j in range(-(-per // U))], axis=1)               # (nseg, units, U)
                 r = np.clip(m[:, None] - U * np.arange(rows.shape[1])[None, :], 0, U)

@@ -197,14 +197,18 @@ def test_one_column_product_over_a_work_list_matches_float64(heavy, seg, accumul
 
 
 @pytest.mark.parametrize("batch", [4, 68, 256])
-def test_swept_forward_product_matches_float64(batch):
+@pytest.mark.parametrize("hubs", [False, True])
+def test_swept_forward_product_matches_float64(batch, hubs):
     """fly_spmm_swept (the forward product as a banded sweep, training batches that are multiples of 4) against
     float64 and fly_spmm, on a random CSR matrix that suits the sweep (70,000 rows of ~40 non-zeros over 40,000
-    source rows); fly_sweep_tables refuses one with a hub row."""
-    from chessfly import brain
+    source rows), plain and with hub rows (longer than 4 x the mean + 64), which the tables split into pieces whose
+    sums meet in k_sweep_finish; an inf in a source row reaches only the rows that read it."""
+    from chessfly import _hip, brain
     rng = np.random.default_rng(batch)
     n_rows, n_cols = 70_000, 40_000
     lens = rng.poisson(40, n_rows)
+    if hubs:
+        lens[[5, 123, 69_999]] = [4 * int(lens.mean()) + 200, 2500, 900]
     crow = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     col = np.concatenate([np.sort(rng.integers(0, n_cols, n)) for n in lens]).astype(np.int32)
     val = rng.standard_normal(len(col)).astype(np.float32)
@@ -219,7 +223,9 @@ def test_swept_forward_product_matches_float64(batch):
     tables = brain._sweep_tables(holder, crow32, col32, n_rows, n_cols)
     assert tables is not None
     assert brain._sweep_tables(holder, crow32, col32, n_rows, n_cols) is tables     # built once per structure
-    y = brain._spmm_swept(crow32, col32, val_d, tables, n_rows, n_cols, x_d)
+    info = _hip.sweep_info(tables.handle)
+    assert (info["split_rows"] == 3) == hubs and (info["pieces"] > 0) == hubs, info
+    y = brain._spmm_swept(col32, val_d, tables, n_rows, x_d)
     y_ref = brain._spmm(crow32, col32, val_d, n_rows, n_cols, x_d)
     torch.cuda.synchronize()
     rows = np.repeat(np.arange(n_rows), lens)
@@ -227,14 +233,30 @@ def test_swept_forward_product_matches_float64(batch):
     np.add.at(exact, rows, val[:, None].astype(np.float64) * x[col].astype(np.float64))
     scale = np.abs(exact).max()
     err, err_ref = np.abs(y.cpu().numpy() - exact).max() / scale, np.abs(y_ref.cpu().numpy() - exact).max() / scale
-    print(f"B={batch}: swept {err:.2e}, fly_spmm {err_ref:.2e} of the largest |y|", flush=True)
+    print(f"B={batch}, hubs {hubs} ({info}): swept {err:.2e}, fly_spmm {err_ref:.2e} of the largest |y|", flush=True)
     assert err < 1e-5 and err_ref < 1e-5
-    hub = lens.copy()
-    hub[123] = 4 * int(lens.mean()) + 200
-    crow_h = torch.as_tensor(np.concatenate([[0], np.cumsum(hub)]).astype(np.int32), device=DEV)
-    col_h = torch.as_tensor(np.concatenate([np.sort(rng.integers(0, n_cols, n)) for n in hub]).astype(np.int32),
-                            device=DEV)
-    assert brain._sweep_tables(Holder(), crow_h, col_h, n_rows, n_cols) is None
+    # Tables for 128 workgroups with paired passes: each wave owns over 24 rows and walks two slots per pass.
+    _hip.set_tuning("sweep_grid", 128)
+    _hip.set_tuning("sweep_paired", 1)
+    try:
+        paired = _hip.sweep_create(crow32, col32, n_rows, n_cols)
+    finally:
+        _hip.set_tuning("sweep_grid", 0)
+        _hip.set_tuning("sweep_paired", 0)
+    assert _hip.sweep_info(paired.handle)["rows_per_wave"] > 24
+    y2 = brain._spmm_swept(col32, val_d, paired, n_rows, x_d).cpu().numpy()
+    assert np.abs(y2 - exact).max() / scale < 1e-5
+    # an inf in one source row: the rows that read it are inf or NaN, every other row stays finite (a paired pass
+    # changes only the owning row's sums when the operand is the caller's)
+    src = int(col[crow[123]]) if hubs else int(col[0])
+    x_inf = x_d.clone()
+    x_inf[src] = float("inf")
+    reads = np.zeros(n_rows, bool)
+    reads[rows[col == src]] = True
+    for tb in (tables, paired):
+        y_inf = brain._spmm_swept(col32, val_d, tb, n_rows, x_inf).cpu().numpy()
+        assert np.isfinite(y_inf[~reads]).all(), "a row that never reads the inf source is not finite"
+        assert not np.isfinite(y_inf[reads]).any()
 
 
 def test_gather_values_reads_the_weight_vector_at_int32_ids():

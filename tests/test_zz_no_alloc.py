@@ -83,3 +83,50 @@ def test_static_scratch_refuses_what_does_not_fit_and_bad_arguments():
     ref = _forward(lib, _hip, p16, dense, x, static=False)
     got = _forward(lib, _hip, p16, dense, x, static=True)
     assert float((got[0] - ref[0]).abs().max()) < 1e-3 and float((got[1] - ref[1]).abs().max()) < 1e-3
+
+
+def test_static_forward_allocates_nothing_and_runs_under_graph_capture(full_net):
+    """The property the entry point exists for.  A warm call leaves the device's free memory unchanged, and one call
+    captured into a HIP graph (capture fails if the call allocates, frees or synchronises) replays correctly: three
+    replays with new boards copied in and the workspace forward run eagerly between them, each replay's outputs
+    within 1e-3 of that forward's (float16 state, 300 boards: two blocks of the static array)."""
+    from chessfly import _hip
+    from chessfly.encoding import N_BASE
+    from chessfly.synthetic import synthetic_boards
+    lib = _hip.load()
+    net, _ = full_net
+    cone = net.brain.light_cone(net.in_idx, net.out_idx, net.cfg.steps)
+    dense = net._dense(N_BASE)
+    with torch.no_grad():
+        plan = net.brain._cone_plan(cone, _hip.MODE_DEVIATION_F16)
+    batch = 300
+    x = torch.as_tensor(synthetic_boards(batch, seed=60)).to(DEV)
+    logits = torch.zeros(batch, 4168, device=DEV)
+    wdl = torch.zeros(batch, 3, device=DEV)
+
+    def call():
+        _hip.check(lib.fly_model_forward_static(plan.handle, dense.handle, x.data_ptr(), 0, x.stride(0), batch, 5.0,
+                                                logits.data_ptr(), wdl.data_ptr(), _hip.stream(torch.device(DEV))),
+                   "fly_model_forward_static")
+
+    call()                                   # first call on the device: looks up the static array's address
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    call()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    torch.cuda.synchronize()
+    for i in range(3):
+        x.copy_(torch.as_tensor(synthetic_boards(batch, seed=61 + i)).to(DEV))
+        logits.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (logits.clone(), wdl.clone())
+        ref = _forward(lib, _hip, plan, dense, x, static=False)
+        for a, b in zip(got, ref):
+            d = float((a - b).abs().max())
+            print(f"replay {i}: max |graph replay - workspace forward| {d:.3e}", flush=True)
+            assert bool(torch.isfinite(a).all()) and d < 1e-3, (i, d)
