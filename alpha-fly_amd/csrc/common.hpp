@@ -185,6 +185,8 @@ struct Tuning {
   int sweep_paired = 0;  // swept waves walk two rows per pass: 1 yes, 0 or -1 one row
   int sweep_slots = 0;   // swept passes of 3 slots: 3 always, 0 when a wave owns 24 rows or fewer (else 6)
   int sweep_pipe = 0;    // swept gathers of the next four rounds in flight: 0 with 3 slots, 1 also 6, -1 never
+  int nt_load = 0;       // read the carried state with non-temporal loads
+  int sweep_last_sync = 0;  // 1: a swept workgroup also meets after the last band of a chunk
 };
 // A copy of the current defaults (taken under a lock: fly_set_tuning may run on another thread).
 Tuning tuning_snapshot();

@@ -90,6 +90,7 @@ void state_step(StepArgs<S, U> a, double avg_nnz, const Tuning &tune, const Swee
     a.sweep_paired = tune.sweep_paired;
     a.sweep_slots = tune.sweep_slots;
     a.sweep_pipe = tune.sweep_pipe;
+    a.sweep_last_sync = tune.sweep_last_sync;
     launch_swept<S, U, 0>(a, *sweep, st);
     check_launch("swept state step");
     return;
@@ -586,6 +587,8 @@ const TuningKey kTuningKeys[] = {
     {"sweep_slots", &Tuning::sweep_slots, -kAny, kAny},
     {"sweep_pipe", &Tuning::sweep_pipe, -kAny, kAny},
     {"step_lds", &Tuning::step_lds, 0, 65536},
+    {"nt_load", &Tuning::nt_load, -kAny, kAny},
+    {"sweep_last_sync", &Tuning::sweep_last_sync, 0, 1},
 };
 
 const TuningKey &tuning_key(const char *key) {

@@ -446,8 +446,9 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * longer than 4 x the mean + 64 into pieces of at most 2 x the mean + 32); "sweep_paired": 1 makes every swept wave
  * that owns over 24 rows walk two rows per pass (0, -1: one); "sweep_slots": 3 makes swept waves take their
  * rows in passes of 3 slots (0: 6 when a wave owns over 24 rows); "sweep_pipe": the next four rounds' gathers in
- * flight during the sums, 0 in passes of 3 slots, 1 also of 6, -1 never.  Every selectable shape computes the same
- * function. */
+ * flight during the sums, 0 in passes of 3 slots, 1 also of 6, -1 never; "sweep_last_sync": 1 makes a swept
+ * workgroup's waves also meet after a chunk's last band (0: they go on to the epilogue at once); "nt_load": 1 reads
+ * the carried state with non-temporal loads.  Every selectable shape computes the same function. */
 int fly_set_tuning(const char *key, int64_t value);
 /* The current default of a tuning key (as fly_set_tuning left it). */
 int fly_get_tuning(const char *key, int64_t *value);
