@@ -181,7 +181,8 @@ struct Tuning {
   int sweep_bands = 0;  // source bands of a swept step (3 or 4); 0 = automatic
   int sweep_order = 0;  // swept waves take their rows in the searched order: 0 yes, -1 in the initial order
   int sweep_grid = 0;   // workgroups of a swept step; 0 = one per CU
-  int sweep_piece = 0;  // split rows longer than this into pieces of at most this many non-zeros; 0 = automatic
+  int sweep_piece = 0;  // split rows longer than this into pieces of at most this many non-zeros; 0 = 3 x the mean + 10
+  int sweep_deal = 0;   // swept rows dealt to the waves by work: 0 where index order is unbalanced, 1 always, -1 never
   int sweep_paired = 0;  // swept waves walk two rows per pass: 1 yes, 0 or -1 one row
   int sweep_slots = 0;   // swept passes of 3 slots: 3 always, 0 when a wave owns 24 rows or fewer (else 6)
   int sweep_pipe = 0;    // swept gathers of the next four rounds in flight: 0 with 3 slots, 1 also 6, -1 never

@@ -22,10 +22,11 @@ const char *flyprobe_last_error(void);
 int flyprobe_pack(const int32_t *col_dev, const float *val_dev, int64_t nnz, void *pairs_dev, void *stream);
 
 /* The banded-sweep tables the evaluator builds for a step (its builder, build_sweep), from the step matrix (rowptr
- * nrows+1, pairs nnz) over prev_rows source rows: cfg[6] = {bands (3 or 4), paired (the order searched for two rows per
- * pass: the float32 state's default), workgroups (0: one per CU), force (sweep whatever the size), piece (0:
- * automatic), search (0: the initial order)}, as the evaluator derives them from its tuning.  *sweep = NULL where the
- * evaluator would not sweep the matrix, by the same rule.  Synchronises.  flyprobe_sweep_destroy frees it. */
+ * nrows+1, pairs nnz) over prev_rows source rows: cfg[7] = {bands (3 or 4), paired (the order searched for two rows per
+ * pass), workgroups (0: one per CU), force (sweep whatever the size), piece (0: automatic), search (0: the initial
+ * order), deal (0: where the index order is unbalanced, 1 always, -1 never)}, as the evaluator derives them from its
+ * tuning.  *sweep = NULL where the evaluator would not sweep the matrix, by the same rule.  Synchronises.
+ * flyprobe_sweep_destroy frees it. */
 int flyprobe_sweep_create(const int32_t *rowptr_dev, const void *pairs_dev, int64_t nrows, int64_t nnz,
                           int64_t prev_rows, const int32_t *cfg, void **sweep, void *stream);
 int flyprobe_sweep_destroy(void *sweep);

@@ -156,6 +156,7 @@ extern "C" int flyprobe_sweep_create(const int32_t *rowptr, const void *pairs, i
     c.force = cfg[3];
     c.piece = cfg[4];
     c.search = cfg[5];
+    c.deal = cfg[6];
     auto t = build_sweep<int2>(rowptr, static_cast<const int2 *>(pairs), nrows, nnz, prev_rows, c, as_stream(stream));
     if (t) *out = new std::shared_ptr<const SweepTables>(std::move(t));
   });

@@ -583,6 +583,7 @@ const TuningKey kTuningKeys[] = {
     {"sweep_order", &Tuning::sweep_order, -kAny, kAny},
     {"sweep_grid", &Tuning::sweep_grid, 0, 65535},
     {"sweep_piece", &Tuning::sweep_piece, 0, 1 << 20},
+    {"sweep_deal", &Tuning::sweep_deal, -1, 1},
     {"sweep_paired", &Tuning::sweep_paired, -kAny, kAny},
     {"sweep_slots", &Tuning::sweep_slots, -kAny, kAny},
     {"sweep_pipe", &Tuning::sweep_pipe, -kAny, kAny},

@@ -38,9 +38,11 @@ struct SweepConfig {
   int32_t paired = 0;            // the order is searched for waves that walk two slots per pass (float32 states)
   int32_t grid = 0;              // workgroups of the swept launch; 0: one per CU of the current device
   int32_t force = 0;             // sweep any matrix with rows and non-zeros, whatever its size
-  int32_t piece = 0;             // split rows longer than this into pieces of at most this many non-zeros; 0: rows
-                                 // longer than 4 x the mean + 64 into pieces of at most 2 x the mean + 32
+  int32_t piece = 0;             // split rows longer than this into pieces of at most this many non-zeros; 0: 3 x the
+                                 // mean + 10
   int32_t search = 1;            // 0: the initial order, unsorted and unsearched
+  int32_t deal = 0;              // the initial order dealt out by work: 0 where index order is unbalanced, 1 always,
+                                 // -1 never
   bool operator==(const SweepConfig &o) const { return std::memcmp(this, &o, sizeof(*this)) == 0; }
 };
 
@@ -423,9 +425,12 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
   FLY_HIP(hipStreamSynchronize(st));
   FLY_REQUIRE(rp[0] == 0 && rp[nrows] == nnz, "the row pointer does not span the non-zeros");
   // 1. split rows
+  //    Rows over 3 x the mean + 10 non-zeros run to several times their slot's other rows (measured on the real
+  //    connectome's in-degrees at B = 1120: limits of 120, 150, 180, 200 (3 x the mean + 10), 230 and 260 gave state
+  //    steps of 5.77, 5.58, 5.55, 5.49, 5.62 and 6.32 ms per forward).
   const double mean = (double)nnz / (double)nrows;
-  const int64_t limit = cfg.piece > 0 ? cfg.piece : (int64_t)(4.0 * mean + 64.0);
-  const int64_t piece = cfg.piece > 0 ? cfg.piece : std::max<int64_t>(8, (int64_t)(2.0 * mean + 32.0));
+  const int64_t limit = cfg.piece > 0 ? cfg.piece : std::max<int64_t>(8, (int64_t)(3.0 * mean + 10.0));
+  const int64_t piece = limit;
   std::vector<PieceDesc> pieces;
   std::vector<int32_t> split, split_ptr{0};
   std::vector<uint8_t> is_split((size_t)nrows, 0);
@@ -487,9 +492,13 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
   const int64_t segs = (t->npos + per - 1) / per;
   //    A workgroup waits for its slowest wave and the step for its slowest workgroup.  Where rows of like length sit
   //    together in index order (a real connectome's neurons are numbered by type), consecutive positions give some
-  //    workgroups several times the mean work; then the rows and pieces are dealt out instead, longest first, each
-  //    to the workgroup with the least work that has a free position, and within each workgroup to its 16 waves the
-  //    same way (ties: the lower index).  A layout within 5% of the mean is kept.
+  //    workgroups several times the mean work; then the rows and pieces are dealt out instead.  Sorted longest first
+  //    (stable), they are cut into units of 8 consecutive ones, a slot's worth of like length; each unit goes to the
+  //    wave with the least work that has room for a whole unit, and the rows left over once no unit fits go one by
+  //    one to the wave with the least work that has a free position (ties: the lower wave).  Every wave's work is
+  //    then close to the mean whatever its number of positions, and its slots hold rows of like length (dealt one
+  //    row at a time, every wave would get one row from each length and its slots would run to their longest).  A
+  //    layout within 5% of the mean is kept (cfg.deal: 1 deals always, -1 never).
   {
     std::vector<int64_t> vlen((size_t)(nrows + t->pieces));
     for (int64_t r = 0; r < nrows; ++r) vlen[r] = rp[r + 1] - rp[r];
@@ -506,34 +515,49 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
       all += vlen[ord[p]];
     }
     const int64_t mx = *std::max_element(tot.begin(), tot.end());
-    if (mx * 20 * n_wg > all * 21) {
+    if (cfg.deal > 0 || (cfg.deal == 0 && mx * 20 * n_wg > all * 21)) {
       std::vector<int32_t> items(ord);
       std::stable_sort(items.begin(), items.end(), [&](int32_t a, int32_t b) { return vlen[a] > vlen[b]; });
-      // deal `its` (longest first) to `k` bins of the given capacities, least work first (ties: the lower bin)
-      auto deal = [&](const std::vector<int32_t> &its, const std::vector<int64_t> &cap) {
-        typedef std::pair<int64_t, int64_t> Bin;   // (work, bin)
+      typedef std::pair<int64_t, int64_t> Bin;   // (work, wave)
+      std::vector<std::vector<int32_t>> bins((size_t)segs);
+      std::vector<int64_t> cap((size_t)segs), work((size_t)segs, 0);
+      int64_t units = 0;
+      for (int64_t w = 0; w < segs; ++w) {
+        cap[w] = std::min(per, t->npos - w * per);
+        units += cap[w] / 8;
+      }
+      {  // whole units
         std::priority_queue<Bin, std::vector<Bin>, std::greater<Bin>> heap;
-        for (int64_t b = 0; b < (int64_t)cap.size(); ++b)
-          if (cap[b] > 0) heap.push({0, b});
-        std::vector<std::vector<int32_t>> bins(cap.size());
-        for (int32_t v : its) {
+        for (int64_t w = 0; w < segs; ++w)
+          if (cap[w] >= 8) heap.push({0, w});
+        for (int64_t u = 0; u < units; ++u) {
           const Bin top = heap.top();
           heap.pop();
-          bins[top.second].push_back(v);
-          if ((int64_t)bins[top.second].size() < cap[top.second]) heap.push({top.first + vlen[v], top.second});
+          const int64_t w = top.second;
+          int64_t sum = 0;
+          for (int64_t k = 8 * u; k < 8 * u + 8; ++k) {
+            bins[w].push_back(items[k]);
+            sum += vlen[items[k]];
+          }
+          work[w] = top.first + sum;
+          if ((int64_t)bins[w].size() + 8 <= cap[w]) heap.push({work[w], w});
         }
-        return bins;
-      };
-      std::vector<int64_t> wg_cap((size_t)n_wg), wave_cap(16);
-      for (int64_t g = 0; g < n_wg; ++g) wg_cap[g] = std::min(wg_pos, t->npos - g * wg_pos);
-      const auto by_wg = deal(items, wg_cap);
-      for (int64_t g = 0; g < n_wg; ++g) {
-        for (int64_t w = 0; w < 16; ++w)
-          wave_cap[w] = std::max<int64_t>(0, std::min(per, t->npos - g * wg_pos - w * per));
-        const auto by_wave = deal(by_wg[g], wave_cap);
-        for (int64_t w = 0; w < 16; ++w)
-          for (size_t k = 0; k < by_wave[w].size(); ++k) ord[g * wg_pos + w * per + (int64_t)k] = by_wave[w][k];
       }
+      {  // the rest, one by one
+        std::priority_queue<Bin, std::vector<Bin>, std::greater<Bin>> heap;
+        for (int64_t w = 0; w < segs; ++w)
+          if ((int64_t)bins[w].size() < cap[w]) heap.push({work[w], w});
+        for (size_t k = (size_t)(8 * units); k < items.size(); ++k) {
+          const Bin top = heap.top();
+          heap.pop();
+          const int64_t w = top.second;
+          bins[w].push_back(items[k]);
+          work[w] = top.first + vlen[items[k]];
+          if ((int64_t)bins[w].size() < cap[w]) heap.push({work[w], w});
+        }
+      }
+      for (int64_t w = 0; w < segs; ++w)
+        for (size_t k = 0; k < bins[w].size(); ++k) ord[w * per + (int64_t)k] = bins[w][k];
       t->dealt = 1;
     }
   }
@@ -571,6 +595,7 @@ inline SweepConfig sweep_config(const Tuning &tu) {
   c.force = tu.swept > 0 ? 1 : 0;
   c.piece = tu.sweep_piece > 0 ? tu.sweep_piece : 0;
   c.search = tu.sweep_order >= 0 ? 1 : 0;
+  c.deal = tu.sweep_deal > 0 ? 1 : (tu.sweep_deal < 0 ? -1 : 0);
   return c;
 }
 

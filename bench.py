@@ -300,11 +300,11 @@ def _probe_lib():
 
 def sweep_config(tuned: dict, state_f16: bool) -> list[int]:
     """The sweep tables' configuration a plan derives from its tuning (sweep_config in csrc/sweep.hpp): bands,
-    paired, workgroups, force, piece, search."""
+    paired, workgroups, force, piece, search, deal."""
     get = lambda k: int(tuned.get(k, 0))
     paired = get("sweep_paired") > 0
     return [3 if get("sweep_bands") == 3 else 4, int(paired), max(get("sweep_grid"), 0), int(get("swept") > 0),
-            max(get("sweep_piece"), 0), int(get("sweep_order") >= 0)]
+            max(get("sweep_piece"), 0), int(get("sweep_order") >= 0), max(min(get("sweep_deal"), 1), -1)]
 
 
 def _probe_check(lib, status: int, what: str) -> None:
@@ -370,7 +370,7 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
         info = _hip.sweep_info(plan.handle, t)
         sweep = ctypes.c_void_p()
         if info["positions"]:
-            cfg = (ctypes.c_int32 * 6)(*sweep_config(tuned or {}, state_f16))
+            cfg = (ctypes.c_int32 * 7)(*sweep_config(tuned or {}, state_f16))
             _probe_check(probe, probe.flyprobe_sweep_create(rowptr.data_ptr(), pairs.data_ptr(), nr, nnz, prev_rows,
                                                             cfg, ctypes.byref(sweep), st), "flyprobe_sweep_create")
 

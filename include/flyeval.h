@@ -132,8 +132,8 @@ int fly_plan_matrix(const fly_plan *plan, int32_t t, int32_t *rowptr_dev, int32_
 
 /* ---- banded-sweep tables of one structure ----------------------------------------------------- */
 /* No counterpart in the reference (cuSPARSE keeps its own analysis).  The tables a swept product or literal step
- * reads for a CSR structure: rowptr (nrows+1) and col (nnz) over ncols columns (rows of the operand).  Rows far
- * longer than the mean (4 x the mean + 64 non-zeros) are split into pieces that each take a share of every band;
+ * reads for a CSR structure: rowptr (nrows+1) and col (nnz) over ncols columns (rows of the operand).  Rows longer
+ * than 3 x the mean + 10 non-zeros are split into pieces of at most that many, each a share of every band;
  * the step adds a split row's pieces in piece order.  Captures the tuning current at creation (sweep_paired > 0:
  * the order is searched for waves that walk two rows per pass).  *out = NULL (FLY_OK) when the structure is too small to
  * sweep (by size: over 32,768 columns, at least 65,536 rows and 32 non-zeros per row).  Synchronises.
@@ -442,8 +442,9 @@ int64_t fly_profile_launches(int32_t *cls, double *ms, int64_t cap);
  * sweeps every step with a matrix whatever its size (small graphs in tests), 0 = the size rule; "sweep_bands":
  * source bands of the sweep, 3 or 4 (0 = 4); "sweep_order": -1 lets the swept waves take their rows in the initial
  * order instead of the searched one (0); "sweep_grid": workgroups of a swept step (0: one per CU), which sets the rows
- * each wave owns; "sweep_piece": split rows longer than this many non-zeros into pieces of at most this many (0: rows
- * longer than 4 x the mean + 64 into pieces of at most 2 x the mean + 32); "sweep_paired": 1 makes every swept wave
+ * each wave owns; "sweep_piece": split rows longer than this many non-zeros into pieces of at most this many (0: 3 x
+ * the mean + 10); "sweep_deal": 1 deals the rows out to the waves by work always, -1 never (0: where the index order
+ * leaves a workgroup over 5% above the mean work); "sweep_paired": 1 makes every swept wave
  * that owns over 24 rows walk two rows per pass (0, -1: one); "sweep_slots": 3 makes swept waves take their
  * rows in passes of 3 slots (0: 6 when a wave owns over 24 rows); "sweep_pipe": the next four rounds' gathers in
  * flight during the sums, 0 in passes of 3 slots, 1 also of 6, -1 never; "sweep_last_sync": 1 makes a swept

@@ -119,7 +119,7 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     assert b"input drive" in probe.flyprobe_last_error()
     probe.flyprobe_sweep_create.argtypes = [p_, p_, i64, i64, i64, p_, ctypes.POINTER(p_), p_]
     out = p_(12345)
-    cfg = (ctypes.c_int32 * 6)(8, 0, 0, 0, 0, 1)
+    cfg = (ctypes.c_int32 * 7)(8, 0, 0, 0, 0, 1, 0)
     assert probe.flyprobe_sweep_create(p, p, 10, 100, 10, cfg, ctypes.byref(out), None) == 1
     assert b"bands" in probe.flyprobe_last_error() and out.value is None
     cfg[0] = 4

@@ -612,30 +612,44 @@ def _balance_numpy(order, cnt, per, groups, steps, paired=False):
 
 
 def _deal_numpy(items, vlen, caps):
-    """Items (longest first) each to the bin with the least work that has room (ties: the lower bin)."""
+    """Items (longest first) dealt to waves of the given capacities: cut into units of 8 consecutive items, as many
+    as whole units fit the waves; each unit to the wave with the least work that has room for a whole unit, then the
+    items left each to the wave with the least work that has a free position (ties: the lower wave)."""
     import heapq
-    heap = [(0, b) for b in range(len(caps)) if caps[b] > 0]
-    heapq.heapify(heap)
+    units = sum(c // 8 for c in caps)
     bins = [[] for _ in caps]
-    for v in items:
-        work, b = heapq.heappop(heap)
-        bins[b].append(v)
-        if len(bins[b]) < caps[b]:
-            heapq.heappush(heap, (work + int(vlen[v]), b))
+    work = [0] * len(caps)
+    heap = [(0, w) for w in range(len(caps)) if caps[w] >= 8]
+    heapq.heapify(heap)
+    for u in range(units):
+        wk, w = heapq.heappop(heap)
+        unit = items[8 * u: 8 * u + 8]
+        bins[w].extend(unit)
+        work[w] = wk + int(vlen[unit].sum())
+        if len(bins[w]) + 8 <= caps[w]:
+            heapq.heappush(heap, (work[w], w))
+    heap = [(work[w], w) for w in range(len(caps)) if len(bins[w]) < caps[w]]
+    heapq.heapify(heap)
+    for v in items[8 * units:]:
+        wk, w = heapq.heappop(heap)
+        bins[w].append(v)
+        work[w] = wk + int(vlen[v])
+        if len(bins[w]) < caps[w]:
+            heapq.heappush(heap, (work[w], w))
     return bins
 
 
 def _sweep_split_numpy(rowptr, cols, prev_rows, bands, piece=0, grid=None):
     """The sweep tables' rows restated: off[i][b] = row i's start plus its non-zeros with a column in the bands
     before b (band of column c: c * bands // prev_rows), off[i][bands] = its end.  Rows longer than the limit
-    (piece, or 4 x the mean + 64) are split into m = ceil(len / p) pieces (p: piece, or max(8, 2 x the mean + 32));
+    p (piece, or max(8, 3 x the mean + 10)) are split into m = ceil(len / p) pieces;
     piece i of m of row h takes [off[h][b] + n_b i // m, off[h][b] + n_b (i + 1) // m) of each band b.  range
     ((rows + pieces), 2 bands) holds each row's and then each piece's begin and end per band.  The initial order puts
     piece j at position (2 j + 1) npos // (2 pieces) and the unsplit rows in index order between; where that leaves
     some workgroup of 16 waves (grid workgroups, per = ceil(npos / (16 grid)) positions per wave) over 1.05 x the
     mean work (a piece's work: its row's length share len (i + 1) // m - len i // m), the rows and pieces are dealt
-    longest first (stable) to workgroups, then within each to its waves, by _deal_numpy.  Returns range, the initial
-    order, the split rows and split_ptr."""
+    to the waves, each of per positions (the last fewer), by _deal_numpy.  Returns range, the initial order, the
+    split rows and split_ptr."""
     nr = len(rowptr) - 1
     lens = np.diff(rowptr)
     band = cols.astype(np.int64) * bands // prev_rows
@@ -645,8 +659,8 @@ def _sweep_split_numpy(rowptr, cols, prev_rows, bands, piece=0, grid=None):
     off[:, 1:bands] = rowptr[:-1, None] + np.cumsum(cnt, axis=1)[:, :bands - 1]
     off[:, bands] = rowptr[1:]
     mean = int(rowptr[-1]) / nr
-    limit = piece if piece > 0 else int(4.0 * mean + 64.0)
-    psize = piece if piece > 0 else max(8, int(2.0 * mean + 32.0))
+    limit = piece if piece > 0 else max(8, int(3.0 * mean + 10.0))
+    psize = limit
     split = np.nonzero(lens > limit)[0]
     m = -(-lens[split] // psize)
     prow = np.repeat(split, m)
@@ -676,11 +690,9 @@ def _sweep_split_numpy(rowptr, cols, prev_rows, bands, piece=0, grid=None):
         tot = np.add.reduceat(vlen[init], np.arange(0, npos, wg_pos))
         if int(tot.max()) * 20 * n_wg > int(tot.sum()) * 21:
             items = init[np.argsort(-vlen[init], kind="stable")]
-            caps = [min(wg_pos, npos - g * wg_pos) for g in range(n_wg)]
-            for g, its in enumerate(_deal_numpy(items, vlen, caps)):
-                wcap = [max(0, min(per, npos - g * wg_pos - w * per)) for w in range(16)]
-                for w, vs in enumerate(_deal_numpy(its, vlen, wcap)):
-                    init[g * wg_pos + w * per: g * wg_pos + w * per + len(vs)] = vs
+            caps = [min(per, npos - w * per) for w in range(-(-npos // per))]
+            for w, vs in enumerate(_deal_numpy(items, vlen, caps)):
+                init[w * per: w * per + len(vs)] = vs
     return rng, init, split, split_ptr
 
 
@@ -770,7 +782,7 @@ def test_sweep_band_table_order_and_rule_match_numpy():
     the range table of rows and split rows' pieces, the split rows, the initial order, the order of k_sweep_order,
     k_sweep_order_search and k_sweep_order_balance, and the size rule, against a numpy restatement, bit for bit, on
     random CSR matrices: 70,000 rows (18 rows per wave: slots of 8, 8 and 2) whose plain form sweeps and whose form
-    with 32,768 source rows does not; the same with hub rows (longer than 4 x the mean + 64), which are split into
+    with 32,768 source rows does not; the same with hub rows (longer than 3 x the mean + 10), which are split into
     pieces; 110,000 rows (27 per wave) searched for a float32 sweep that walks two slots per pass; and a forced
     piece size that splits a third of the rows.  The searches leave each workgroup its rows and pieces and each wave
     its number of positions, and lower the rounds and the workgroups' barrier-bound rounds on this fixed data."""
@@ -800,7 +812,7 @@ def test_sweep_band_table_order_and_rule_match_numpy():
         d_rowptr = torch.as_tensor(rowptr, device=DEV)
         d_pairs = torch.as_tensor(np.ascontiguousarray(pairs), device=DEV)
         for bands in band_counts:
-            cfg = (ctypes.c_int32 * 6)(bands, paired, 0, 0, piece, 1)
+            cfg = (ctypes.c_int32 * 7)(bands, paired, 0, 0, piece, 1, 0)
             handle = p_()
             rc = probe.flyprobe_sweep_create(d_rowptr.data_ptr(), d_pairs.data_ptr(), nr, len(cols), prev_rows, cfg,
                                              ctypes.byref(handle), None)

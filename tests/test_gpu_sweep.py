@@ -49,7 +49,7 @@ def _medium(seed):
 
 def _heavy_tailed(seed):
     """3,000 neurons with in-degrees like the MaleCNS wiring's: LogNormal around 25, a tenth of the neurons with no
-    partner at all, and hubs of 1,500, 900 and 400 partners (far past 4 x the mean + 64, so the tables split them)."""
+    partner at all, and hubs of 1,500, 900 and 400 partners (far past 3 x the mean + 10, so the tables split them)."""
     from chessfly.synthetic import degree_connectome
     rng = np.random.default_rng([seed, 77])
     n = 3000

@@ -201,7 +201,7 @@ def test_one_column_product_over_a_work_list_matches_float64(heavy, seg, accumul
 def test_swept_forward_product_matches_float64(batch, hubs):
     """fly_spmm_swept (the forward product as a banded sweep, training batches that are multiples of 4) against
     float64 and fly_spmm, on a random CSR matrix that suits the sweep (70,000 rows of ~40 non-zeros over 40,000
-    source rows), plain and with hub rows (longer than 4 x the mean + 64), which the tables split into pieces whose
+    source rows), plain and with hub rows (longer than 3 x the mean + 10), which the tables split into pieces whose
     sums meet in k_sweep_finish; an inf in a source row reaches only the rows that read it."""
     from chessfly import _hip, brain
     rng = np.random.default_rng(batch)
