@@ -59,6 +59,8 @@ SIGNATURES = {
     "fly_forward_io_f64": (_i32, [_p, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_forward_literal_workspace": (_sz, [_p, _i64]),
     "fly_forward_literal": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
+    "fly_forward_literal_f16_workspace": (_sz, [_p, _i64]),
+    "fly_forward_literal_f16": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
     "fly_forward_literal_f64_workspace": (_sz, [_p, _i64]),
     "fly_forward_literal_f64": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p, _i64, _p, _sz, _p]),
     "fly_plan_step_workspace": (_sz, [_p, _i32, _i64]),

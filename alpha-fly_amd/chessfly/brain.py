@@ -817,9 +817,13 @@ class ConnectomeRNN(nn.Module):
             self._full_sweep_tables = (self.crow32, _hip.sweep_create(self.crow32, self.pre32, self.n, self.n))
         return self._full_sweep_tables[1]
 
-    def _full_plan(self) -> _Plan:
+    def _full_plan(self, half: bool = False) -> _Plan:
+        """The literal recurrence's plan for this weight version; `half`: its weights rounded to float16, as the
+        reference's float16 forward rounds them (w.to(u.dtype), brain.py:215)."""
         def build(handle):
             w = self.edge_weights()
+            if half:
+                w = w.half().float()
             sweep = self._full_sweep()
             _hip.check(_hip.load().fly_plan_create_full(self.n, self.n_edges, self.crow32.data_ptr(),
                                                         self.pre32.data_ptr(), w.data_ptr(),
@@ -827,7 +831,7 @@ class ConnectomeRNN(nn.Module):
                                                         sweep.handle if sweep is not None else None,
                                                         _hip.stream(w.device), ctypes.byref(handle)),
                        "fly_plan_create_full")
-        return self._plan(("full",), build)
+        return self._plan(("full16",) if half else ("full",), build)
 
     def _cone_plan(self, cone: LightCone, mode: int) -> _Plan:
         def build(handle):
@@ -841,27 +845,28 @@ class ConnectomeRNN(nn.Module):
     # ---- the literal recurrence ----------------------------------------------------------------------
     def forward(self, u: torch.Tensor, steps: int) -> torch.Tensor:
         """u: (N, B) contiguous constant external drive.  Returns the state after `steps` updates, (N, B).
-        As in the reference's inference path, u is updated in place to u + bias (brain.py:218)."""
+        As in the reference's inference path, u is updated in place to u + bias (brain.py:218).  The recurrence
+        runs in u's dtype (brain.py:215-216): float32; float64 (the float32 weights widen exactly); float16 (the
+        weights and bias rounded to float16, a float16 state, its sums in float32)."""
         assert u.is_contiguous()
         _hip.require_device(u, "ConnectomeRNN.forward")
         self._check_params("ConnectomeRNN.forward")
         if torch.is_grad_enabled():
             return self._forward_autograd(u, steps)
-        if u.dtype not in (torch.float32, torch.float64) or u.dim() != 2 or u.shape[0] != self.n:
-            raise RuntimeError(f"ConnectomeRNN.forward: u must be float32 or float64 ({self.n}, B), got {u.dtype} "
-                               f"{tuple(u.shape)}")
+        if u.dtype not in (torch.float16, torch.float32, torch.float64) or u.dim() != 2 or u.shape[0] != self.n:
+            raise RuntimeError(f"ConnectomeRNN.forward: u must be float16, float32 or float64 ({self.n}, B), got "
+                               f"{u.dtype} {tuple(u.shape)}")
         lib = _hip.load()
-        plan = self._full_plan()
         batch = u.shape[1]
         h = torch.empty_like(u)
-        # the recurrence runs in u's dtype (brain.py:215-216): float64 widens the float32 weights exactly
-        f64 = u.dtype == torch.float64
-        size = lib.fly_forward_literal_f64_workspace if f64 else lib.fly_forward_literal_workspace
-        run = lib.fly_forward_literal_f64 if f64 else lib.fly_forward_literal
-        ws = _hip.workspace(size(plan.handle, batch), u.device)
-        _hip.check(run(plan.handle, u.data_ptr(), batch, self.bias.data_ptr(), batch, int(steps), h.data_ptr(), batch,
-                       ws.data_ptr(), ws.numel(), _hip.stream(u.device)),
-                   "fly_forward_literal_f64" if f64 else "fly_forward_literal")
+        # the recurrence runs in u's dtype (brain.py:215-216): float64 widens the float32 weights exactly; float16
+        # rounds them to float16 and carries a float16 state, summed in float32
+        name = {torch.float16: "fly_forward_literal_f16", torch.float32: "fly_forward_literal",
+                torch.float64: "fly_forward_literal_f64"}[u.dtype]
+        plan = self._full_plan(half=u.dtype == torch.float16)
+        ws = _hip.workspace(getattr(lib, name + "_workspace")(plan.handle, batch), u.device)
+        _hip.check(getattr(lib, name)(plan.handle, u.data_ptr(), batch, self.bias.data_ptr(), batch, int(steps),
+                                      h.data_ptr(), batch, ws.data_ptr(), ws.numel(), _hip.stream(u.device)), name)
         return h
 
     def _forward_autograd(self, u: torch.Tensor, steps: int) -> torch.Tensor:
@@ -901,7 +906,7 @@ class ConnectomeRNN(nn.Module):
         key = (steps, in_idx.data_ptr(), out_idx.data_ptr(), str(self.pre.device), bool(prune))
         if self._cone is None or self._cone[0] != key:
             self._cone = None                         # release the old cone (and its plans) first
-            self._plans = {k: v for k, v in self._plans.items() if k[0] == "full"}
+            self._plans = {k: v for k, v in self._plans.items() if k[0] in ("full", "full16")}
             self._cone = (key, LightCone(self, in_idx, out_idx, steps, prune))
         return self._cone[1]
 

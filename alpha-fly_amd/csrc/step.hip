@@ -391,69 +391,97 @@ extern "C" int fly_forward_io_f64(const fly_plan *plan, const double *u_in, int6
   });
 }
 
+namespace fly {
+namespace {
+
+// Scratch of the literal recurrence in state type S: two (n, ld) state buffers, then the sums of split rows' pieces.
+template <typename S>
+size_t literal_workspace(const fly_plan &plan, int64_t batch) {
+  const int64_t blk = block_cols(plan.n, sizeof(S), batch);
+  return align256(2 * (size_t)plan.n * (size_t)state_ld(blk, sizeof(S)) * sizeof(S) + 256) +
+         plan_pieces_bytes(plan, blk);
+}
+
+// The literal recurrence (brain.py:211-223, no-grad branch) in state type S (float32, or float16 as the reference runs
+// it for float16 u): u += bias in place, then `steps` fused steps over the whole matrix, the last into h.
+template <typename S>
+void run_literal(const fly_plan *plan, S *u, int64_t ldu, const float *bias, int64_t batch, int32_t steps, S *h,
+                 int64_t ldh, void *ws, size_t ws_bytes, hipStream_t st) {
+  check_plan_device(plan);
+  FLY_REQUIRE(plan->full, "the literal recurrence needs a plan from fly_plan_create_full");
+  FLY_REQUIRE(steps >= 0, "negative steps");
+  FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
+  if (batch == 0) return;
+  FLY_REQUIRE(u && bias && h && ldu >= batch && ldh >= batch, "bad argument");
+  const int64_t n = plan->n;
+  {
+    LaunchTimer timer(FLY_K_OTHER, st);
+    hipLaunchKernelGGL(k_add_bias<S>, rows_grid(n, batch), dim3(256), 0, st, u, ldu, bias, n, batch);
+  }
+  check_launch("bias add");
+  if (steps == 0) {
+    LaunchTimer timer(FLY_K_OTHER, st);
+    hipLaunchKernelGGL(k_zero_rows<S>, rows_grid(n, batch), dim3(256), 0, st, h, ldh, n, batch);
+    check_launch("zero state");
+    return;
+  }
+  FLY_REQUIRE(ws && ws_bytes >= literal_workspace<S>(*plan, batch), "workspace too small");
+  FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
+  const int64_t blk = block_cols(n, sizeof(S), batch);
+  float *pieces = reinterpret_cast<float *>(
+      static_cast<char *>(ws) + align256(2 * (size_t)n * (size_t)state_ld(blk, sizeof(S)) * sizeof(S) + 256));
+  for (int64_t c0 = 0; c0 < batch; c0 += blk) {
+    const int64_t nb = std::min(blk, batch - c0);
+    const int64_t lds = state_ld(nb, sizeof(S));
+    S *buf[2] = {static_cast<S *>(ws), static_cast<S *>(ws) + (size_t)n * lds};
+    const S *prev = nullptr;
+    int cur = 0;
+    for (int t = 1; t <= steps; ++t) {
+      const bool last = t == steps;
+      StepArgs<S, S> a{};
+      a.rowptr = plan->rowptr[0].p;
+      a.colval = plan->colval[0].p;
+      a.params = plan->params[0].p;
+      a.xprev = prev;
+      a.ldx = lds;
+      a.u = u + c0;
+      a.ldu = ldu;
+      a.xout = last ? h + c0 : buf[cur];
+      a.ldo = last ? ldh : lds;
+      a.out_exact = last ? 1 : 0;   // the caller's h: no store past the block's last column
+      a.nrows = (int32_t)n;
+      a.batch = (int32_t)nb;
+      a.xbytes = prev ? buffer_bytes(n, lds, sizeof(S)) : 0;
+      a.pieces = pieces;
+      a.sweep_exact = std::isfinite(plan->h_max) ? 0 : 1;
+      state_step(a, (double)plan->nnz[0] / (double)n, plan->tune, plan->sweep[0].get(), st);
+      prev = buf[cur];
+      cur ^= 1;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace fly
+
 extern "C" size_t fly_forward_literal_workspace(const fly_plan *plan, int64_t batch) {
-  if (!plan) return 0;
-  const int64_t blk = block_cols(plan->n, sizeof(float), batch);
-  return align256(2 * (size_t)plan->n * (size_t)state_ld(blk, sizeof(float)) * sizeof(float) + 256) +
-         plan_pieces_bytes(*plan, blk);
+  return plan ? literal_workspace<float>(*plan, batch) : 0;
 }
 
 extern "C" int fly_forward_literal(const fly_plan *plan, float *u, int64_t ldu, const float *bias, int64_t batch,
                                    int32_t steps, float *h, int64_t ldh, void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] { run_literal<float>(plan, u, ldu, bias, batch, steps, h, ldh, ws, ws_bytes, as_stream(stream)); });
+}
+
+extern "C" size_t fly_forward_literal_f16_workspace(const fly_plan *plan, int64_t batch) {
+  return plan ? literal_workspace<_Float16>(*plan, batch) : 0;
+}
+
+extern "C" int fly_forward_literal_f16(const fly_plan *plan, void *u, int64_t ldu, const float *bias, int64_t batch,
+                                       int32_t steps, void *h, int64_t ldh, void *ws, size_t ws_bytes, void *stream) {
   return guard([&] {
-    check_plan_device(plan);
-    FLY_REQUIRE(plan->full, "the literal recurrence needs a plan from fly_plan_create_full");
-    FLY_REQUIRE(steps >= 0, "negative steps");
-    FLY_REQUIRE(batch >= 0 && batch < (int64_t)INT32_MAX / 2, "batch out of range");
-    if (batch == 0) return;
-    FLY_REQUIRE(u && bias && h && ldu >= batch && ldh >= batch, "bad argument");
-    const int64_t n = plan->n;
-    hipStream_t st = as_stream(stream);
-    {
-      LaunchTimer timer(FLY_K_OTHER, st);
-      hipLaunchKernelGGL(k_add_bias<float>, rows_grid(n, batch), dim3(256), 0, st, u, ldu, bias, n, batch);
-    }
-    check_launch("bias add");
-    if (steps == 0) {
-      LaunchTimer timer(FLY_K_OTHER, st);
-      hipLaunchKernelGGL(k_zero_rows<float>, rows_grid(n, batch), dim3(256), 0, st, h, ldh, n, batch);
-      check_launch("zero state");
-      return;
-    }
-    FLY_REQUIRE(ws && ws_bytes >= fly_forward_literal_workspace(plan, batch), "workspace too small");
-    FLY_REQUIRE(aligned(ws, 256), "workspace must be 256-byte aligned");
-    const int64_t blk = block_cols(n, sizeof(float), batch);
-    float *pieces = reinterpret_cast<float *>(
-        static_cast<char *>(ws) + align256(2 * (size_t)n * (size_t)state_ld(blk, sizeof(float)) * sizeof(float) + 256));
-    for (int64_t c0 = 0; c0 < batch; c0 += blk) {
-      const int64_t nb = std::min(blk, batch - c0);
-      const int64_t lds = state_ld(nb, sizeof(float));
-      float *buf[2] = {static_cast<float *>(ws), static_cast<float *>(ws) + (size_t)n * lds};
-      const float *prev = nullptr;
-      int cur = 0;
-      for (int t = 1; t <= steps; ++t) {
-        const bool last = t == steps;
-        StepArgs<float, float> a{};
-        a.rowptr = plan->rowptr[0].p;
-        a.colval = plan->colval[0].p;
-        a.params = plan->params[0].p;
-        a.xprev = prev;
-        a.ldx = lds;
-        a.u = u + c0;
-        a.ldu = ldu;
-        a.xout = last ? h + c0 : buf[cur];
-        a.ldo = last ? ldh : lds;
-        a.out_exact = last ? 1 : 0;   // the caller's h: no store past the block's last column
-        a.nrows = (int32_t)n;
-        a.batch = (int32_t)nb;
-        a.xbytes = prev ? buffer_bytes(n, lds, sizeof(float)) : 0;
-        a.pieces = pieces;
-        a.sweep_exact = std::isfinite(plan->h_max) ? 0 : 1;
-        state_step(a, (double)plan->nnz[0] / (double)n, plan->tune, plan->sweep[0].get(), st);
-        prev = buf[cur];
-        cur ^= 1;
-      }
-    }
+    run_literal<_Float16>(plan, static_cast<_Float16 *>(u), ldu, bias, batch, steps, static_cast<_Float16 *>(h), ldh,
+                          ws, ws_bytes, as_stream(stream));
   });
 }
 

@@ -19,7 +19,8 @@
  *                         :238-252 _constants
  *   fly_plan_create_full  chessfly/brain.py:215-216 (per-call weights of the literal recurrence)
  *   fly_forward_io        chessfly/brain.py:282-329 ConnectomeRNN.forward_io (and :254-280); _f64 in float64
- *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch); _f64 in float64
+ *   fly_forward_literal   chessfly/brain.py:211-223 ConnectomeRNN.forward (no-grad branch); _f64 and _f16 in those
+ *                         dtypes
  *   fly_plan_step         chessfly/brain.py:273-277 and :310-313 (one step of forward_io; :219-220 one literal step)
  *   fly_dense_create      chessfly/model.py:79-93 (the encoder and head weights, as the matrix cores read them)
  *   fly_encoder           chessfly/model.py:99-102 (encoder linear map, input gain, cast, transpose)
@@ -166,6 +167,13 @@ int fly_forward_literal(const fly_plan *plan, float *u_dev, int64_t ldu, const f
 /* The same recurrence in float64 (chessfly/brain.py:215-223 with u float64: the float32 weights, alphas and bias
  * widen exactly, and every sum, clamp and lerp is float64; the reference's tests run it this way).  u (n, ldu) is
  * updated in place to u + bias; h (n, ldh) float64. */
+/* The same in float16 (chessfly/brain.py:213-223 with u float16): u and h are __half, u += bias rounded to float16 in
+ * place, the state is float16 with float32 sums.  The reference rounds the weights to u's dtype: pass a plan built from
+ * float16-rounded weights for that. */
+size_t fly_forward_literal_f16_workspace(const fly_plan *plan, int64_t batch);
+int fly_forward_literal_f16(const fly_plan *plan, void *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
+                            int32_t steps, void *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
+                            void *stream);
 size_t fly_forward_literal_f64_workspace(const fly_plan *plan, int64_t batch);
 int fly_forward_literal_f64(const fly_plan *plan, double *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
                             int32_t steps, double *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,

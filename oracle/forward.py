@@ -109,6 +109,15 @@ def literal_operands(b: BrainArrays, dtype):
     return full_matrix(b, edge_weights(b, pdt).to(dtype)), alpha
 
 
+def literal_f16_operands(b: BrainArrays):
+    """The operands of the reference's float16 literal recurrence (brain.py:213-216 with u float16): the weights and
+    alpha computed in the parameters' dtype and rounded to float16, widened exactly to float64, so a float64
+    recurrence over them is the exact function of what the float16 path computes with."""
+    pdt = b.alpha_logit.dtype
+    alpha = torch.sigmoid(b.alpha_logit).half().double().unsqueeze(1)
+    return full_matrix(b, edge_weights(b, pdt).half().double()), alpha
+
+
 def literal(b: BrainArrays, u: torch.Tensor, steps: int) -> torch.Tensor:
     """Literal recurrence h <- lerp(h, clamp(W h + b + u, 0, H), alpha) from h = 0; u (N, B)."""
     dtype = u.dtype

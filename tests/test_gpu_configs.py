@@ -600,6 +600,44 @@ def test_literal_recurrence_in_float64(h_max):
     np.testing.assert_allclose(h.cpu().numpy(), dense, rtol=1e-12, atol=1e-12)
 
 
+# ---- the literal recurrence in float16 ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("h_max", [10.0, None])
+def test_literal_recurrence_in_float16(h_max, sweep_core):
+    """ConnectomeRNN.forward with float16 u runs the reference's float16 path (brain.py:213-223): u += bias rounded to
+    float16 in place (bit for bit), weights and alpha rounded to float16, a float16 state.  Against the float64
+    recurrence over those float16 operands (oracle.forward.literal_f16_operands, the exact function of the path's
+    inputs), which the device follows up to its float16 roundings of the state: within 4e-3 of the largest |h| (six
+    roundings of 2^-11 of the state and of the sum per step bound it by 6e-3); and against the float32 forward
+    within 1e-2 of the largest |h| (the operands' own float16 rounding on top)."""
+    conn = _medium(8)
+    lg, b, al = random_params(conn, 28, gain_sd=0.1, bias_mean=2.0 if h_max is None else 0.1)
+    rnn = _rnn(conn, 4.0, lg, b, al, h_max=h_max)
+    ba = brain_arrays(conn, 4.0, lg, b, al, h_max=h_max)               # float32 parameters, as the product's
+    ba.w0 = rnn.w0.cpu()
+    mat, alpha = F.literal_f16_operands(ba)
+    g = torch.Generator().manual_seed(13)
+    for batch, steps in ((1, 1), (70, 3), (130, 6)):
+        u = torch.randn(conn.n_neurons, batch, generator=g)
+        u16 = u.half().to(DEV)
+        drive16 = (u.half().float() + torch.as_tensor(b).half().float()[:, None]).half()   # u.add_(bias.half())
+        with torch.no_grad():
+            h16 = rnn(u16, steps)
+            h32 = rnn(u.clone().to(DEV), steps)
+        assert h16.dtype == torch.float16
+        assert torch.equal(u16.cpu(), drive16), "u + bias in float16, in place"
+        h = torch.zeros(conn.n_neurons, batch, dtype=torch.float64)
+        for _ in range(steps):
+            h = F.literal_step(ba, mat, alpha, h, drive16.double())
+        ref = h.numpy()
+        scale = max(np.abs(ref).max(), 1e-3)
+        err = np.abs(h16.double().cpu().numpy() - ref).max()
+        d32 = np.abs(h16.double().cpu().numpy() - h32.double().cpu().numpy()).max()
+        print(f"float16 literal {sweep_core} h_max={h_max} B={batch} T={steps}: max |h16 - exact| {err:.2e}, "
+              f"|h16 - h32| {d32:.2e} of max |h| {scale:.2e}", flush=True)
+        assert err < 4e-3 * scale and d32 < 1e-2 * scale, (batch, steps, err, d32, scale)
+
+
 # ---- forward_io in float64 ---------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("h_max", [10.0, None])

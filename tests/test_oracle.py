@@ -87,6 +87,32 @@ def test_literal_matches_dense_closed_form_with_repeated_pairs():
         assert np.abs(ref).sum() > 0
 
 
+def test_float16_literal_operands_are_the_rounded_weights():
+    """literal_f16_operands (the reference's float16 literal recurrence, brain.py:213-216 with u float16): every weight
+    and alpha is the float32 value rounded to nearest float16 (checked against numpy's float16 cast, and within half an
+    ulp of float16), and the float64 recurrence over them is the dense closed form over those rounded values; with
+    weights that are already float16 values it is the float32 operands' recurrence itself."""
+    conn = tiny_connectome(40, 500, 2).shuffled(1)
+    lg, b, al = random_params(conn, 11, bias_sd=0.5)
+    ba = brain_arrays(conn, 3.0, lg, b, al)                       # float32 parameters, as the product's
+    mat, alpha = F.literal_f16_operands(ba)
+    w32 = F.edge_weights(ba, torch.float32).numpy()
+    w16 = mat.values().numpy()
+    np.testing.assert_array_equal(w16, w32.astype(np.float16).astype(np.float64))
+    assert np.all(np.abs(w16 - w32) <= np.abs(w32) * 2.0 ** -11)
+    a32 = (1 / (1 + np.exp(-al.astype(np.float64)))).astype(np.float32)
+    np.testing.assert_allclose(alpha.numpy()[:, 0], a32.astype(np.float16).astype(np.float64), rtol=0, atol=1e-3)
+    assert np.all(alpha.numpy()[:, 0] == alpha.numpy()[:, 0].astype(np.float16).astype(np.float64))
+    W = brute.dense_matrix(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), w16)
+    u = torch.randn(conn.n_neurons, 5, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    drive = u + torch.as_tensor(b, dtype=torch.float64)[:, None]
+    h = torch.zeros_like(drive)
+    for steps in range(1, 5):
+        h = F.literal_step(ba, mat, alpha, h, drive)
+        ref = brute.dense_recurrence(W, b.astype(np.float64), alpha.numpy()[:, 0], u.numpy(), steps)
+        np.testing.assert_allclose(h.numpy(), ref, rtol=1e-12, atol=1e-13)
+
+
 def test_unbounded_activity_matches_dense_closed_form():
     """h_max=None (brain.py:178-182, 221): the clamp keeps only its lower bound.  Biases large enough that
     activity passes 10, so a bound left in place would show; the light cone with h_max None is the same
