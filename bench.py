@@ -288,6 +288,7 @@ def _probe_lib():
     for name, args in (("flyprobe_pack", [p, p, i64, p, p]),
                        ("flyprobe_sweep_create", [p, p, i64, i64, i64, p, ctypes.POINTER(p), p]),
                        ("flyprobe_sweep_destroy", [p]),
+                       ("flyprobe_sweep_read", [p, p, p, p, p, p, p]),
                        ("flyprobe_replay_step", [p, p, i64, i64, p, i64, i64, i64, i32, p, p, p]),
                        ("flyprobe_pack_params", [p, p, i64, p, p]),
                        ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, p]),
@@ -333,6 +334,39 @@ def _events_ms(fn, reps: int) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def issued_lines_per_nnz(rng, order, per: int, bands: int, paired: bool = False) -> float:
+    """Lines a swept step's gathers issue per chunk of columns, per non-zero, from its tables (range (rows + pieces,
+    2 bands), order (positions), rows_per_wave `per`): wave w takes positions [w per, (w + 1) per) in slots of 8;
+    each slot issues, per band, 8 lane groups x its rounds: the longest of its rows' band counts (a slot of 3-4 rows
+    spreads each row over 2 groups, of 2 rows over 4, of 1 row over 8, and the rounds run to the longest share),
+    padded to a block of 4 rounds; a float32 sweep over pairs of slots runs each pass to the largest sum of a lane
+    group's two rows (k_state_step_swept).  1.0: no padding gathers."""
+    import numpy as np
+    npos = len(order)
+    cnt = (rng[:, 1::2] - rng[:, 0::2])[order].astype(np.int64)      # (npos, bands)
+    nnz = int(cnt.sum())
+    waves = -(-npos // per)
+    unit = 16 if paired else 8
+    units = -(-per // unit)
+    full = np.zeros((waves, units * unit, bands), dtype=np.int64)
+    have = np.zeros((waves, units * unit), dtype=bool)
+    for w in range(waves):
+        n = min(per, npos - w * per)
+        full[w, :n] = cnt[w * per:w * per + n]
+        have[w, :n] = True
+    full = full.reshape(waves, units, unit, bands)
+    have = have.reshape(waves, units, unit)
+    if paired:
+        rounds = (full[:, :, :8] + full[:, :, 8:]).max(axis=2)
+    else:
+        r = have.sum(axis=2)                                            # rows of each slot
+        lf = np.where(r >= 5, 0, np.where(r >= 3, 1, np.where(r == 2, 2, 3)))
+        share = (full + (1 << lf)[..., None, None] - 1) >> lf[..., None, None]
+        rounds = share.max(axis=2)
+    rounds = (rounds + 3) & ~3
+    return float(8 * rounds.sum()) / max(nnz, 1)
 
 
 def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps: int = 20,
@@ -382,6 +416,18 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
         row = {"t": t, "rows": nr, "nnz": nnz, "swept": bool(sweep.value), "replay_ms": round(_events_ms(once, reps), 4)}
         if info["pieces"]:
             row["split_rows"], row["pieces"] = info["split_rows"], info["pieces"]
+        if sweep.value:
+            sinfo = (ctypes.c_int64 * 7)()
+            npos = info["positions"]
+            d_rng = torch.empty((nr + info["pieces"], 2 * info["bands"]), dtype=torch.int32, device=dev)
+            d_order = torch.empty(npos, dtype=torch.int32, device=dev)
+            _probe_check(probe, probe.flyprobe_sweep_read(sweep, sinfo, d_rng.data_ptr(), d_order.data_ptr(), None,
+                                                          None, st), "flyprobe_sweep_read")
+            torch.cuda.synchronize()
+            paired = bool(sinfo[6]) and not state_f16 and int((tuned or {}).get("sweep_paired", 0)) > 0
+            row["issued_lines_per_nnz"] = round(issued_lines_per_nnz(d_rng.cpu().numpy(), d_order.cpu().numpy(),
+                                                                     int(sinfo[3]), int(sinfo[4]), paired), 4)
+            del d_rng, d_order
         # with the row I/O: each row's constants, carried state and input drive (float32, as the model forward's
         # encoder writes it) read, and the new state written
         prev32 = torch.empty(nr, dtype=torch.int32, device=dev)
@@ -437,7 +483,7 @@ def random_gather_rates(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dic
     return gbps, rows_per_s
 
 
-def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> dict:
+def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32, download_workgroups: int = 0) -> dict:
     """The search's view (chessfly/model.py:113-135): fp16 boards from host numpy through Evaluator.submit
     and result, so the pinned H2D copy of the boards, the forward, the output kernel and the D2H copy of the
     answers are all inside the clock.  Lazy returns the whole fp16 policy; eager returns `legal_per_board`
@@ -447,8 +493,11 @@ def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> d
     import numpy as np
     import torch
     from chessfly.encoding import N_MOVES
+    import chessfly.model as model_mod
     from chessfly.model import Evaluator
 
+    if download_workgroups > 0:
+        model_mod.DOWNLOAD_SHARED = download_workgroups
     ev = Evaluator(net, dev)
     x16 = x_np.astype(np.float16)
     rng = np.random.default_rng(3)
@@ -475,7 +524,8 @@ def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32) -> d
         out[name + "_pipelined"] = {"evals_per_s": round(len(x16) / dt, 1), "ms_per_batch": round(dt * 1e3, 3)}
     out["note"] = (f"B={len(x16)} fp16 boards from host numpy, pinned staging; lazy: fp16 (B, {N_MOVES}) policy "
                    f"back; eager: {legal_per_board} legal logits per board back; plus values; pipelined: two "
-                   f"batches in flight")
+                   f"batches in flight; the answers' download runs on {model_mod.DOWNLOAD_SHARED} workgroups while "
+                   f"another batch computes, {model_mod.DOWNLOAD_ALONE} alone")
     return out
 
 
@@ -504,6 +554,9 @@ def main() -> int:
     ap.add_argument("--evaluator-steps", type=int, default=10,
                     help="batches through Evaluator.submit/result from host numpy, PCIe included (0: skip)")
     ap.add_argument("--tune", action="append", default=[], help="key=value for fly_set_tuning")
+    ap.add_argument("--download-workgroups", type=int, default=0, metavar="N",
+                    help="workgroups of the evaluator's answer download while another batch computes (0: the "
+                         "evaluator's own choice, chessfly.model.DOWNLOAD_SHARED)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed loop, run a plain float32 streaming copy of MIB MiB three times (a kernel "
                          "of known HBM traffic, to scale rocprof FETCH_SIZE / WRITE_SIZE readings)")
@@ -707,7 +760,8 @@ def main() -> int:
 
     evaluator = None
     if args.evaluator_steps > 0:
-        evaluator = evaluator_figure(net, dev, x_np, args.evaluator_steps)
+        evaluator = evaluator_figure(net, dev, x_np, args.evaluator_steps,
+                                     download_workgroups=args.download_workgroups)
         log(f"Evaluator from host numpy: {evaluator}")
 
     cpu = None

@@ -167,16 +167,16 @@ int fly_forward_literal(const fly_plan *plan, float *u_dev, int64_t ldu, const f
 /* The same recurrence in float64 (chessfly/brain.py:215-223 with u float64: the float32 weights, alphas and bias
  * widen exactly, and every sum, clamp and lerp is float64; the reference's tests run it this way).  u (n, ldu) is
  * updated in place to u + bias; h (n, ldh) float64. */
-/* The same in float16 (chessfly/brain.py:213-223 with u float16): u and h are __half, u += bias rounded to float16 in
- * place, the state is float16 with float32 sums.  The reference rounds the weights to u's dtype: pass a plan built from
- * float16-rounded weights for that. */
-size_t fly_forward_literal_f16_workspace(const fly_plan *plan, int64_t batch);
-int fly_forward_literal_f16(const fly_plan *plan, void *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
-                            int32_t steps, void *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
-                            void *stream);
 size_t fly_forward_literal_f64_workspace(const fly_plan *plan, int64_t batch);
 int fly_forward_literal_f64(const fly_plan *plan, double *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
                             int32_t steps, double *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
+                            void *stream);
+/* The same recurrence in float16 (chessfly/brain.py:213-223 with u float16): u and h are __half, u += bias rounded to
+ * float16 in place, the state is float16 with float32 sums.  The reference rounds the weights to u's dtype: pass a
+ * plan built from float16-rounded weights for that. */
+size_t fly_forward_literal_f16_workspace(const fly_plan *plan, int64_t batch);
+int fly_forward_literal_f16(const fly_plan *plan, void *u_dev, int64_t ldu, const float *bias_dev, int64_t batch,
+                            int32_t steps, void *h_dev, int64_t ldh, void *workspace_dev, size_t workspace_bytes,
                             void *stream);
 
 /* One state step of a plan, the per-step op of chessfly/brain.py:273-277 (float16 deviation: s = A_t d_{t-1},
