@@ -65,13 +65,16 @@ __global__ void k_grow_forward(const int32_t *__restrict__ crow, const int32_t *
 }
 
 // D_t |= presynaptic partners of D_{t+1} rows.  dout already holds a copy of din; concurrent stores all
-// write 1, so the result does not depend on their order.
-__global__ void k_grow_backward(const int32_t *__restrict__ crow, const int32_t *__restrict__ pre,
-                                const uint8_t *__restrict__ din, uint8_t *__restrict__ dout, int64_t n) {
-  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+// write 1, so the result does not depend on their order.  16 lanes per row, lane s marking the partners s, s + 16,
+// ..., so a hub row's thousands of partners do not fall to one lane.
+__global__ __launch_bounds__(256) void k_grow_backward(const int32_t *__restrict__ crow, const int32_t *__restrict__ pre,
+                                                       const uint8_t *__restrict__ din, uint8_t *__restrict__ dout,
+                                                       int64_t n) {
+  const int s = threadIdx.x & 15;
+  const int64_t r = blockIdx.x * 16 + (threadIdx.x >> 4);
   if (r >= n || !din[r]) return;
   const int32_t end = crow[r + 1];
-  for (int32_t e = crow[r]; e < end; ++e) dout[pre[e]] = 1;
+  for (int32_t e = crow[r] + s; e < end; e += 16) dout[pre[e]] = 1;
 }
 
 // Block-wide inclusive scan of one value per thread (kScanThreads threads).
@@ -330,7 +333,7 @@ extern "C" int fly_cone_create(int64_t n, int64_t n_edges, const int32_t *crow, 
       if (n_out) hipLaunchKernelGGL(k_mark, dim3(blocks_for(n_out, kThreads)), dim3(kThreads), 0, st, D(T), out_idx, n_out);
       for (int t = T - 1; t >= 0; --t) {
         copy_d2d(D(t), D(t + 1), (size_t)n, st);
-        hipLaunchKernelGGL(k_grow_backward, dim3(nb), dim3(kThreads), 0, st, crow, pre, D(t + 1), D(t), n);
+        hipLaunchKernelGGL(k_grow_backward, dim3(blocks_for(n, 16)), dim3(256), 0, st, crow, pre, D(t + 1), D(t), n);
       }
     }
     check_launch("reach masks");

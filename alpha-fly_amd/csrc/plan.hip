@@ -30,17 +30,42 @@ __global__ void k_sigmoid(const float *__restrict__ x, int64_t n, float *__restr
   if (i < n) y[i] = 1.0f / (1.0f + expf(-x[i]));
 }
 
-// k_full[r] = (c ? sum_e w_e c[pre_e] : 0) + bias[r], edges summed in CSR order
-__global__ void k_drive(const int32_t *__restrict__ crow, const int32_t *__restrict__ pre, const float *__restrict__ w,
-                        const float *__restrict__ c, const float *__restrict__ bias, int64_t n, float *__restrict__ k_full) {
-  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (r >= n) return;
-  float s = 0.0f;
-  if (c) {
-    const int32_t end = crow[r + 1];
-    for (int32_t e = crow[r]; e < end; ++e) s = fmaf(w[e], c[pre[e]], s);
+// Sum over row r's edges of w_e c[pre_e]: 16 lanes per row (a unit), four units per wave.  Lane s of the unit takes
+// the edges s, s + 16, ... in rounds of 64 (four loads in flight), and the 16 partial sums meet through xor
+// shuffles: the summation order of the training side's one-column products (k_spmv), so the resting trajectory
+// has the same bits in both.  A hub row of thousands of partners takes a few hundred rounds instead of thousands
+// of dependent loads in one lane.  Every lane of the unit returns the sum.
+__device__ __forceinline__ float unit_row_dot(const int32_t *__restrict__ pre, const float *__restrict__ w,
+                                              const float *__restrict__ c, int32_t beg, int32_t end, int s) {
+  float acc = 0.0f;
+  for (int32_t e0 = beg + s; e0 < end; e0 += 64) {
+    float v[4], xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t e = e0 + 16 * j;
+      const bool live = e < end;
+      v[j] = live ? w[e] : 0.0f;
+      xv[j] = live ? c[pre[e]] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(v[j], xv[j], acc);
   }
-  k_full[r] = s + bias[r];
+  acc += __shfl_xor(acc, 8);
+  acc += __shfl_xor(acc, 4);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 1);
+  return acc;
+}
+
+// k_full[r] = (c ? sum_e w_e c[pre_e] : 0) + bias[r]: one 16-lane unit per row (unit_row_dot)
+__global__ __launch_bounds__(256) void k_drive(const int32_t *__restrict__ crow, const int32_t *__restrict__ pre,
+                                               const float *__restrict__ w, const float *__restrict__ c,
+                                               const float *__restrict__ bias, int64_t n, float *__restrict__ k_full) {
+  const int s = threadIdx.x & 15;
+  const int64_t r = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool has = r < n;
+  const float sum = has && c ? unit_row_dot(pre, w, c, crow[r], crow[r + 1], s) : 0.0f;
+  if (has && s == 0) k_full[r] = sum + bias[r];
 }
 
 __global__ void k_rest_update(const float *__restrict__ c, const float *__restrict__ k_full,
@@ -68,24 +93,40 @@ __global__ void k_params_deviation(const int32_t *__restrict__ rows, int64_t nr,
   rp[i] = p;
 }
 
-// k_t = k_full[R_t[i]] - sum over the kept edges of w_e c_{t-1}[pre_e]
-__global__ void k_params_f32(const int32_t *__restrict__ rows, int64_t nr, const float *__restrict__ k_full,
-                             const float *__restrict__ alpha, float h_max, const float *__restrict__ c_prev,
-                             const int32_t *__restrict__ rowptr, const int32_t *__restrict__ edge,
-                             const int32_t *__restrict__ pre, const float *__restrict__ w,
-                             const int32_t *__restrict__ prev, const int32_t *__restrict__ usrc,
-                             RowParam *__restrict__ rp) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= nr) return;
-  const int32_t r = rows[i];
+// k_t = k_full[R_t[i]] - sum over the kept edges of w_e c_{t-1}[pre_e]: one 16-lane unit per row of R_t, lane s
+// taking the kept edges s, s + 16, ... (as unit_row_dot, through the edge ids)
+__global__ __launch_bounds__(256) void k_params_f32(const int32_t *__restrict__ rows, int64_t nr,
+                                                    const float *__restrict__ k_full, const float *__restrict__ alpha,
+                                                    float h_max, const float *__restrict__ c_prev,
+                                                    const int32_t *__restrict__ rowptr,
+                                                    const int32_t *__restrict__ edge, const int32_t *__restrict__ pre,
+                                                    const float *__restrict__ w, const int32_t *__restrict__ prev,
+                                                    const int32_t *__restrict__ usrc, RowParam *__restrict__ rp) {
+  const int s = threadIdx.x & 15;
+  const int64_t i = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool has = i < nr;
   float sub = 0.0f;
-  if (rowptr) {
+  if (has && rowptr) {
     const int32_t end = rowptr[i + 1];
-    for (int32_t q = rowptr[i]; q < end; ++q) {
-      const int32_t e = edge[q];
-      sub = fmaf(w[e], c_prev[pre[e]], sub);
+    for (int32_t q0 = rowptr[i] + s; q0 < end; q0 += 64) {
+      float v[4], xv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t q = q0 + 16 * j;
+        const int32_t e = q < end ? edge[q] : -1;
+        v[j] = e >= 0 ? w[e] : 0.0f;
+        xv[j] = e >= 0 ? c_prev[pre[e]] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sub = fmaf(v[j], xv[j], sub);
     }
   }
+  sub += __shfl_xor(sub, 8);
+  sub += __shfl_xor(sub, 4);
+  sub += __shfl_xor(sub, 2);
+  sub += __shfl_xor(sub, 1);
+  if (!has || s != 0) return;
+  const int32_t r = rows[i];
   RowParam p;
   p.k = k_full[r] - sub;
   p.lo = 0.0f;
@@ -213,8 +254,8 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
     float *c_prev = nullptr;  // c_0 = 0
     float *c_next = c_a.p;
     for (int t = 1; t <= T; ++t) {
-      hipLaunchKernelGGL(k_drive, dim3(nb), dim3(kThreads), 0, st, crow, pre, w, t > 1 ? c_prev : nullptr, bias, n,
-                         k_full.p);
+      hipLaunchKernelGGL(k_drive, dim3(blocks_for(n, 16)), dim3(256), 0, st, crow, pre, w, t > 1 ? c_prev : nullptr,
+                         bias, n, k_full.p);
       const int64_t nr = cone->rows_n[t];
       plan->params[t].alloc(nr);
       if (cone->has_op[t]) {
@@ -234,7 +275,7 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
           hipLaunchKernelGGL(k_params_deviation, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, cone->rows[t].p,
                              nr, k_full.p, alpha.p, h_max, cone->prev[t].p, cone->usrc[t].p, plan->params[t].p);
         else
-          hipLaunchKernelGGL(k_params_f32, dim3(blocks_for(nr, kThreads)), dim3(kThreads), 0, st, cone->rows[t].p, nr,
+          hipLaunchKernelGGL(k_params_f32, dim3(blocks_for(nr, 16)), dim3(256), 0, st, cone->rows[t].p, nr,
                              k_full.p, alpha.p, h_max, c_prev, cone->has_op[t] && c_prev ? cone->rowptr[t].p : nullptr,
                              cone->edge[t].p, pre, w, cone->prev[t].p, cone->usrc[t].p, plan->params[t].p);
       }

@@ -85,17 +85,28 @@ __device__ __forceinline__ int32_t record_col(const int2 &r) { return r.x; }
 __device__ __forceinline__ int32_t record_col(int32_t c) { return c; }
 
 template <typename C>   // C: {column, weight} records (int2) or plain columns (int32_t)
-__global__ void k_band_off(const int32_t *__restrict__ rowptr, const C *__restrict__ colval, int64_t nr,
-                           int64_t prev_rows, int32_t K, int32_t *__restrict__ off) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= nr) return;
-  const int32_t beg = rowptr[i], end = rowptr[i + 1];
+__global__ __launch_bounds__(256) void k_band_off(const int32_t *__restrict__ rowptr, const C *__restrict__ colval,
+                                                  int64_t nr, int64_t prev_rows, int32_t K, int32_t *__restrict__ off) {
+  // 16 lanes per row, lane s counting the records s, s + 16, ..., their counts added through xor shuffles (a hub
+  // row's thousands of records do not fall to one lane)
+  const int s = threadIdx.x & 15;
+  const int64_t i = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool has = i < nr;
+  const int32_t beg = has ? rowptr[i] : 0, end = has ? rowptr[i + 1] : 0;
   int32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int32_t q = beg; q < end; ++q) {
+  for (int32_t q = beg + s; q < end; q += 16) {
     const int64_t b = (int64_t)record_col(colval[q]) * K / prev_rows;
 #pragma unroll
     for (int k = 0; k < 8; ++k) cnt[k] += (b == k) ? 1 : 0;
   }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    cnt[k] += __shfl_xor(cnt[k], 8);
+    cnt[k] += __shfl_xor(cnt[k], 4);
+    cnt[k] += __shfl_xor(cnt[k], 2);
+    cnt[k] += __shfl_xor(cnt[k], 1);
+  }
+  if (!has || s != 0) return;
   int32_t o = beg;
   for (int k = 0; k < K; ++k) {
     off[i * (K + 1) + k] = o;
@@ -129,6 +140,34 @@ __global__ void k_sweep_order(const int32_t *__restrict__ range, int K, const in
       rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
     }
     out[b + rank] = in[i];
+  }
+}
+
+// k_sweep_order with one 64-lane workgroup per wave's segment and the segment's lengths in LDS (per ints of dynamic
+// LDS): the same ranks, each lane ranking positions i, i + 64, ... against the lengths in LDS instead of summing
+// every other position's band ranges again from memory.
+__global__ __launch_bounds__(64) void k_sweep_order_lds(const int32_t *__restrict__ range, int K,
+                                                        const int32_t *__restrict__ in, int64_t npos, int64_t per,
+                                                        int32_t *__restrict__ out) {
+  extern __shared__ int32_t seg_len[];
+  const int64_t b = (int64_t)blockIdx.x * per;
+  if (b >= npos) return;
+  const int m = (int)min(per, npos - b);
+  for (int k = threadIdx.x; k < m; k += 64) {
+    const int32_t *r = range + (int64_t)in[b + k] * (2 * K);
+    int32_t n = 0;
+    for (int q = 0; q < K; ++q) n += r[2 * q + 1] - r[2 * q];
+    seg_len[k] = n;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < m; i += 64) {
+    const int32_t li = seg_len[i];
+    int rank = 0;
+    for (int j = 0; j < m; ++j) {
+      const int32_t lj = seg_len[j];
+      rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
+    }
+    out[b + rank] = in[b + i];
   }
 }
 
@@ -456,7 +495,7 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
   // 2. ranges
   {
     DevArray<int32_t> off((size_t)nrows * (K + 1));
-    hipLaunchKernelGGL(k_band_off<C>, dim3(blocks_for(nrows, 256)), dim3(256), 0, st, rowptr, cols, nrows, ncols, K,
+    hipLaunchKernelGGL(k_band_off<C>, dim3(blocks_for(nrows, 16)), dim3(256), 0, st, rowptr, cols, nrows, ncols, K,
                        off.p);
     DevArray<PieceDesc> pd(pieces.size());
     if (!pieces.empty())
@@ -570,8 +609,12 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
   } else {
     DevArray<int32_t> init((size_t)t->npos);
     FLY_HIP(hipMemcpyAsync(init.p, ord.data(), sizeof(int32_t) * ord.size(), hipMemcpyHostToDevice, st));
-    hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, t->range.p, K, init.p, t->npos,
-                       per, t->order.p);
+    if (per <= 4096)
+      hipLaunchKernelGGL(k_sweep_order_lds, dim3((unsigned)segs), dim3(64), (unsigned)(per * sizeof(int32_t)), st,
+                         t->range.p, K, init.p, t->npos, per, t->order.p);
+    else
+      hipLaunchKernelGGL(k_sweep_order, dim3(blocks_for(segs, 64)), dim3(64), 0, st, t->range.p, K, init.p, t->npos,
+                         per, t->order.p);
     if (per <= kSearchRows) {
       hipLaunchKernelGGL(k_sweep_order_search, dim3((unsigned)segs), dim3(64), 0, st, t->range.p, K, t->npos, per,
                          (int)t->paired, t->order.p);
