@@ -81,6 +81,10 @@ SIGNATURES = {
     "fly_spmm_swept": (_i32, [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _sz, _p]),
     "fly_transposed_backward": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p,
                                        _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p]),
+    "fly_gather_records": (_i32, [_p, _p, _i64, _p, _i64, _p, _p]),
+    "fly_transposed_backward_swept_workspace": (_sz, [_p, _i64]),
+    "fly_transposed_backward_swept": (_i32, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _i64, _p,
+                                             _sz, _p]),
     "fly_train_step_forward": (_i32, [_i64, _i64, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _f32, _p,
                                       _i64, _p]),
     "fly_train_step_backward": (_i32, [_i64, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _f32, _p, _i64, _p,

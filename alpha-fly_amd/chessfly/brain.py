@@ -61,24 +61,25 @@ def _spmm(crow32, col32, val, n_rows: int, n_cols: int, x: torch.Tensor, out: to
     return y
 
 
-def _sweep_tables(holder, crow32, col32, n_rows: int, n_cols: int):
-    """The banded-sweep tables of the forward product over one structure (fly_sweep_create, float32 operands), built
-    on first use and kept on `holder` with the row pointer they belong to; None when the structure does not sweep
+def _sweep_tables(holder, crow32, col32, n_rows: int, n_cols: int, attr: str = "_sweep"):
+    """The banded-sweep tables of a product over one structure (fly_sweep_create, float32 operands), built on first
+    use and kept on `holder` (as `attr`) with the row pointer they belong to; None when the structure does not sweep
     (too few or too short rows)."""
-    cached = getattr(holder, "_sweep", None)
+    cached = getattr(holder, attr, None)
     if cached is not None and cached[0] is crow32:
         return cached[1]
     tables = _hip.sweep_create(crow32, col32, n_rows, n_cols)
-    holder._sweep = (crow32, tables)
+    setattr(holder, attr, (crow32, tables))
     return tables
 
 
-def _spmm_swept(col32, val, tables, n_rows: int, x: torch.Tensor) -> torch.Tensor:
-    """y (n_rows, B) = A x as a banded sweep (fly_spmm_swept) from {column, weight} records; x (n_cols, B) float32,
-    contiguous and 16-byte aligned, with B a multiple of 4."""
+def _spmm_swept(col32, val, tables, n_rows: int, x: torch.Tensor, records: torch.Tensor | None = None) -> torch.Tensor:
+    """y (n_rows, B) = A x as a banded sweep (fly_spmm_swept) from {column, weight} records (`records`, or built from
+    col32 and val); x (n_cols, B) float32, contiguous and 16-byte aligned, with B a multiple of 4."""
     batch = x.shape[1]
     y = torch.empty(n_rows, batch, dtype=torch.float32, device=x.device)
-    records = torch.stack((col32, val.contiguous().view(torch.int32)), dim=1)
+    if records is None:
+        records = torch.stack((col32, val.contiguous().view(torch.int32)), dim=1)
     lib = _hip.load()
     ws = _hip.workspace(lib.fly_spmm_swept_workspace(tables.handle, batch), x.device)
     _hip.check(lib.fly_spmm_swept(tables.handle, records.data_ptr(), col32.numel(), x.data_ptr(), batch, batch,
@@ -171,6 +172,31 @@ def _gathered(op, w: torch.Tensor, transposed: bool, via: tuple | None = None) -
     return vals
 
 
+def _records(op, w: torch.Tensor, transposed: bool, via: tuple | None = None) -> torch.Tensor:
+    """op's {column, value bits} records (nnz, 2) int32 in CSR order or in the transposed structure's order, the
+    swept products' operand, with the values taken from the whole weight vector w in one pass
+    (fly_gather_records) and kept once per weight tensor, as _gathered keeps the values alone.  `via` = (src,
+    ids32) as in _gathered."""
+    slot = "_rec_t" if transposed else "_rec"
+    cached = getattr(op, slot, None)
+    if cached is not None and cached[0]() is w:
+        return cached[1]
+    if transposed:
+        _, col32, t_ids32 = op._transposed()
+        src, ids32 = via if via is not None else (w, t_ids32)
+    else:
+        col32 = op._structure()[1]
+        ids = op._edge_ids()
+        src, ids32 = w, (None if ids is None else ids[0])
+    src = src.contiguous()
+    rec = torch.empty(col32.numel(), 2, dtype=torch.int32, device=w.device)
+    _hip.check(_hip.load().fly_gather_records(col32.data_ptr(), src.data_ptr(), src.numel(), _hip.ptr(ids32),
+                                              col32.numel(), rec.data_ptr(), _hip.stream(w.device)),
+               "fly_gather_records")
+    setattr(op, slot, (weakref.ref(w), rec))
+    return rec
+
+
 def backward_work(t_crow: torch.Tensor, seg: int = 256):
     """The work list of fly_transposed_backward over the rows of A^T with row pointer t_crow: each row in
     segments of at most `seg` non-zeros (a multiple of 64), longest first, so the heavy-tailed rows of A^T
@@ -214,7 +240,7 @@ def _product(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False, out
             tables = _sweep_tables(op, crow32, col32, n_rows, n_cols)
             x = x.contiguous()
             if tables is not None and x.data_ptr() % 16 == 0:
-                return _spmm_swept(col32, _gathered(op, w, False), tables, n_rows, x)
+                return _spmm_swept(col32, None, tables, n_rows, x, records=_records(op, w, False))
     return _spmm(crow32, col32, _gathered(op, w, transposed), n_rows, n_cols, x, out=out)
 
 
@@ -310,21 +336,32 @@ class _ConeRecurrence(torch.autograd.Function):
                         w_pos32 = ctx.rnn._transposed_positions()
                         w_t = _gathered(ctx.rnn, w, True)     # shared with the resting trajectory's backward
                     wt_ids32 = op._whole_transposed_ids(w_pos32)
-                    vals_t = _gathered(op, w, True, via=(w_t, wt_ids32))
-                    items, splits, n_slots = op._backward_work()
-                    partials = torch.empty(n_slots, ld, dtype=torch.float32, device=dev) if n_slots else None
-                    # more than one 64-column chunk: chunk-major, each chunk's dot products kept in a workspace
-                    chunks = (batch + 63) // 64
-                    dots = torch.empty(chunks * wt_ids32.numel(), dtype=torch.float32, device=dev) \
-                        if chunks > 1 else None
                     if gw_t is None:
                         gw_t = torch.zeros_like(w)
-                    _hip.check(lib.fly_transposed_backward(
-                        t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(), wt_ids32.data_ptr(),
-                        wt_ids32.numel(), n_cols, n_rows, gy.data_ptr(), ld, h_prev.data_ptr(), ld, batch,
-                        gh_prev.data_ptr(), ld, 1, gw_t.data_ptr(), gw_t.numel(), items.data_ptr(), items.shape[0],
-                        splits.data_ptr(), splits.shape[0], _hip.ptr(partials), n_slots, _hip.ptr(dots),
-                        dots.numel() if dots is not None else 0, st), "fly_transposed_backward")
+                    # A^T's structure as a banded sweep of gy's rows where it suits the sweep (tables built once per
+                    # sub-matrix), else the chunk-major pass over the longest-first work list
+                    tables_t = _sweep_tables(op, t_crow32, t_col32, n_cols, n_rows, attr="_sweep_t")
+                    if tables_t is not None:
+                        records = _records(op, w, True, via=(w_t, wt_ids32))
+                        ws = _hip.workspace(lib.fly_transposed_backward_swept_workspace(tables_t.handle, batch), dev)
+                        _hip.check(lib.fly_transposed_backward_swept(
+                            tables_t.handle, records.data_ptr(), t_col32.numel(), wt_ids32.data_ptr(), gy.data_ptr(),
+                            ld, h_prev.data_ptr(), ld, batch, gh_prev.data_ptr(), ld, 1, gw_t.data_ptr(), gw_t.numel(),
+                            ws.data_ptr(), ws.numel(), st), "fly_transposed_backward_swept")
+                    else:
+                        vals_t = _gathered(op, w, True, via=(w_t, wt_ids32))
+                        items, splits, n_slots = op._backward_work()
+                        partials = torch.empty(n_slots, ld, dtype=torch.float32, device=dev) if n_slots else None
+                        # more than one 64-column chunk: chunk-major, each chunk's dot products kept in a workspace
+                        chunks = (batch + 63) // 64
+                        dots = torch.empty(chunks * wt_ids32.numel(), dtype=torch.float32, device=dev) \
+                            if chunks > 1 else None
+                        _hip.check(lib.fly_transposed_backward(
+                            t_crow32.data_ptr(), t_col32.data_ptr(), vals_t.data_ptr(), wt_ids32.data_ptr(),
+                            wt_ids32.numel(), n_cols, n_rows, gy.data_ptr(), ld, h_prev.data_ptr(), ld, batch,
+                            gh_prev.data_ptr(), ld, 1, gw_t.data_ptr(), gw_t.numel(), items.data_ptr(),
+                            items.shape[0], splits.data_ptr(), splits.shape[0], _hip.ptr(partials), n_slots,
+                            _hip.ptr(dots), dots.numel() if dots is not None else 0, st), "fly_transposed_backward")
                 else:
                     _product(op, w, gy, transposed=True, out=gh_prev)
                     ids32, ids = op._edge_ids()

@@ -49,4 +49,25 @@ __device__ __forceinline__ int group_bcast(int v) {
   return __builtin_amdgcn_ds_swizzle(v, (0x1F & ~(N - 1)) | (J << 5));
 }
 
+// v from the lane (l ^ X) of lane l's group of 32 (X < 8 stays inside groups of 8): ds_swizzle in bit mode.
+template <int X>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(X > 0 && X < 32, "xor mask of 5 bits");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (X << 10)));
+}
+
+// Reduce-scatter inside each group of 8 lanes: d[r] holds a lane's share of value r (r = 0..7); lane s of the group
+// returns the sum of value s over the group's 8 lanes.  Three halving exchanges (lanes 4 apart, 2, 1), 7 swizzles in
+// all, summed in a fixed tree order.
+__device__ __forceinline__ float group_reduce_scatter8(const float (&d)[8], int s) {
+  const bool h4 = s & 4, h2 = s & 2, h1 = s & 1;
+  float e[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) e[k] = (h4 ? d[k + 4] : d[k]) + lane_xor<4>(h4 ? d[k] : d[k + 4]);
+  float f[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) f[k] = (h2 ? e[k + 2] : e[k]) + lane_xor<2>(h2 ? e[k] : e[k + 2]);
+  return (h1 ? f[1] : f[0]) + lane_xor<1>(h1 ? f[0] : f[1]);
+}
+
 }  // namespace fly

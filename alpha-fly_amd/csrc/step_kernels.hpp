@@ -109,6 +109,13 @@ struct StepArgs {
   int32_t sweep_pipe;      // the next four rounds' gathers in flight during the sums: 0 with 3 slots, 1 also 6, -1 never
   int32_t sweep_exact;     // paired passes change only the owning row's sums (states that may hold inf or NaN)
   int32_t sweep_last_sync; // 1: the workgroup also meets after a chunk's last band
+  // the transposed backward (swept, REPLAY == 4): each gathered line of grad_y dotted with the row's own h_{t-1}
+  const float *hdot;           // (rows, ldh): h_{t-1} by row of A^T
+  int64_t ldh;
+  float *dots;                 // (chunks of 8 V columns, ndots): each record's dot in each chunk
+  int64_t ndots;
+  const int32_t *piece_row;    // (pieces): the row each piece of a split row belongs to
+  int32_t accumulate;          // REPLAY 3 and 4: add the sums to xout instead of storing them
 };
 
 // Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
@@ -627,7 +634,9 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // groups.  PAIRED walks two slots' rows per pass (1: the other row's weight is zero, for states that hold no inf
 // or NaN; 2: only the owning row's sums change).  PIPE keeps the next four rounds' gathers in flight during the
 // sums.  REPLAY as for the other step kernels, and 3: the product alone, each row's sums stored to xout (float32
-// states; the training forward's A x).
+// states; the training forward's A x); 4: the training backward's pass over A^T, the product grad_h = A^T grad_y
+// added to xout and, per record and chunk, the dot of the gathered line of grad_y with the row's own h_{t-1}
+// (hdot) stored to dots (dL/dw's share of the chunk).
 template <typename S, typename U, int V, int K, int SLOTS, bool TORCH_LERP, int REPLAY = 0, int PAIRED = 0,
           bool PIPE = false>
 __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, U> a) {
@@ -672,24 +681,41 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
               : (nrow[j] >= 3 ? 1 : (nrow[j] == 2 ? 2 : 3));
     }
     int off[SLOTS];   // lane s < 2K: sweep_range[row][s]
+    int hrow[SLOTS];  // REPLAY 4: the row of A^T (a piece's own row) whose h_{t-1} the group's dots read, or -1
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
       const int i = g >> lf[j];
       const int32_t rj = i < nrow[j] ? row_at(base + 8u * j + (uint32_t)i) : -1;
       off[j] = rj >= 0 && s < 2 * K ? a.sweep_range[(int64_t)rj * (2 * K) + s] : 0;
+      if constexpr (REPLAY == 4) hrow[j] = rj < 0 ? -1 : (rj < a.nrows ? rj : a.piece_row[rj - a.nrows]);
       if constexpr (REPLAY != 1) {
         // the epilogue's row (first group of a spread row only) and word s of its constants, for every chunk
         const bool first = (g & ((1 << lf[j]) - 1)) == 0;
         const int e = (wv * SLOTS + j) * 64 + lane;
         ep_row[e] = first ? rj : -1;
-        if constexpr (REPLAY != 3)
+        if constexpr (REPLAY != 3 && REPLAY != 4)
           ep_par[e] = first && rj >= 0 && rj < a.nrows ? reinterpret_cast<const int *>(a.params + rj)[s] : 0;
       }
     }
     for (int c = 0; c < chunks; ++c) {
       const int64_t col = (int64_t)c * (8 * V) + (int64_t)s * V;
       const bool in_batch = col < a.batch;
-      const uint32_t voff = (uint32_t)(in_batch ? col : (int64_t)c * (8 * V)) * (uint32_t)sizeof(S);
+      // lanes past the batch gather their chunk's first columns (no sum reads them), or zeros where a record's
+      // dot sums the group's columns (an offset past any buffer below 2^31 bytes)
+      const uint32_t voff = REPLAY == 4 ? (in_batch ? (uint32_t)col * (uint32_t)sizeof(S) : 0x80000000u)
+                                        : (uint32_t)(in_batch ? col : (int64_t)c * (8 * V)) * (uint32_t)sizeof(S);
+      float hv[REPLAY == 4 ? SLOTS : 1][V];   // REPLAY 4: the group's row of h_{t-1}, this lane's columns
+      if constexpr (REPLAY == 4) {
+#pragma unroll
+        for (int j = 0; j < SLOTS; ++j) {
+          if (hrow[j] >= 0 && in_batch) {
+            Lanes<float, V>::load(a.hdot + (int64_t)hrow[j] * a.ldh + col, hv[j]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i) hv[j][i] = 0.0f;
+          }
+        }
+      }
       float acc[SLOTS][V];
 #pragma unroll
       for (int j = 0; j < SLOTS; ++j)
@@ -843,6 +869,9 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           int2 rec = rounds > 0 ? block(0) : make_int2(0, 0);
           for (int q0 = 0; q0 < rounds; q0 += 8) {
             const int2 nxt = block(q0 + 8);
+            float dl[REPLAY == 4 ? 8 : 1];   // REPLAY 4: this lane's share of each round's dot
+#pragma unroll
+            for (int u = 0; u < (REPLAY == 4 ? 8 : 1); ++u) dl[u] = 0.0f;
             static_for<8 / UNR>([&](auto H) {
               constexpr int h0 = decltype(H)::value * UNR;
               if (q0 + h0 < rounds) {
@@ -864,10 +893,22 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                     const float wt = __int_as_float(wj[u]);
 #pragma unroll
                     for (int i = 0; i < V; ++i) acc[j][i] = fmaf(wt, Lanes<S, V>::at(xr[u], i), acc[j][i]);
+                    if constexpr (REPLAY == 4) {
+                      float d = 0.0f;
+#pragma unroll
+                      for (int i = 0; i < V; ++i) d = fmaf(Lanes<S, V>::at(xr[u], i), hv[j][i], d);
+                      dl[h0 + u] = d;
+                    }
                   }
                 }
               }
             });
+            if constexpr (REPLAY == 4) {
+              // lane s ends with the group's dot of round s: the record it loaded for this block
+              const float dot = group_reduce_scatter8(dl, s);
+              const int q = beg + q0 + s;
+              if (q < end) __builtin_nontemporal_store(dot, a.dots + (int64_t)c * a.ndots + q);
+            }
             rec = nxt;
           }
           }
@@ -898,7 +939,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
             constexpr int u = decltype(J)::value;
             const int e = (wv * SLOTS + j0 + u) * 64 + lane;
             rs[u] = in_batch ? ep_row[e] : -1;
-            if constexpr (REPLAY != 3) {
+            if constexpr (REPLAY != 3 && REPLAY != 4) {
               in[u].p = row_param_from_word(ep_par[e]);   // every lane takes part in the group broadcasts
               load_row_drive(a, col, rs[u] >= 0 && rs[u] < a.nrows, in[u]);
             }
@@ -912,8 +953,15 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
               }
             } else if (rs[u] >= 0) {
               const uint32_t rj = (uint32_t)rs[u];
-              if constexpr (REPLAY == 3) {   // the product alone: y[row] = the row's sums, float32
-                Lanes<S, V>::store(a.xout + (int64_t)rj * a.ldo + col, acc[j0 + u]);
+              if constexpr (REPLAY == 3 || REPLAY == 4) {   // the product alone: y[row] (+)= the row's sums, float32
+                S *dst = a.xout + (int64_t)rj * a.ldo + col;
+                if (a.accumulate) {
+                  float o[V];
+                  Lanes<float, V>::load(dst, o);
+#pragma unroll
+                  for (int i = 0; i < V; ++i) acc[j0 + u][i] += o[i];
+                }
+                Lanes<S, V>::store(dst, acc[j0 + u]);
               } else {
                 if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j0 + u], bits);
                 finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j0 + u], in[u]);
@@ -933,8 +981,8 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
 }
 
 // The rows a swept step split into pieces (k_state_step_swept stored each piece's raw sums): per split row, the
-// pieces' sums added in piece order, then the row's epilogue as the swept kernel runs it (REPLAY == 3: the sums
-// stored).  One thread per V columns of a row, blockIdx.y over the split rows.
+// pieces' sums added in piece order, then the row's epilogue as the swept kernel runs it (REPLAY == 3 and 4: the
+// sums stored, or added with a.accumulate).  One thread per V columns of a row, blockIdx.y over the split rows.
 template <typename S, typename U, int V, bool TORCH_LERP, int REPLAY>
 __global__ __launch_bounds__(256) void k_sweep_finish(const StepArgs<S, U> a, const int32_t *__restrict__ split,
                                                      const int32_t *__restrict__ split_ptr, int32_t nsplit) {
@@ -952,8 +1000,15 @@ __global__ __launch_bounds__(256) void k_sweep_finish(const StepArgs<S, U> a, co
       for (int i = 0; i < V; ++i) acc[i] += v[i];
     }
     const uint32_t row = (uint32_t)split[h];
-    if constexpr (REPLAY == 3) {
-      Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, acc);
+    if constexpr (REPLAY == 3 || REPLAY == 4) {
+      S *dst = a.xout + (int64_t)row * a.ldo + col;
+      if (a.accumulate) {
+        float o[V];
+        Lanes<float, V>::load(dst, o);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] += o[i];
+      }
+      Lanes<S, V>::store(dst, acc);
     } else {
       RowInputs<S, U, V> in;
       load_row_inputs(a, row, col, true, in);
@@ -1001,6 +1056,17 @@ void launch_swept(StepArgs<S, U> a, const SweepTables &t, hipStream_t st) {
   a.rows_per_wave = t.rows_per_wave;
   a.ldp = round_up(a.batch, 64);
   const bool few = a.rows_per_wave <= 24 || a.sweep_slots == 3;
+  if constexpr (REPLAY == 4) {
+    // the transposed backward keeps each slot's row of h_{t-1} beside its sums
+    static_assert(sizeof(S) == 4, "the transposed backward is float32");
+    if (t.bands == 3) {
+      if (few) launch_swept_shape<S, U, 3, 3, 4>(a, grid, st);
+      else launch_swept_shape<S, U, 3, 6, 4>(a, grid, st);
+    } else {
+      if (few) launch_swept_shape<S, U, 4, 3, 4>(a, grid, st);
+      else launch_swept_shape<S, U, 4, 6, 4>(a, grid, st);
+    }
+  } else {
   switch (t.bands) {
     case 3:
       if (few) launch_swept_shape<S, U, 3, 3, REPLAY>(a, grid, st);
@@ -1025,7 +1091,8 @@ void launch_swept(StepArgs<S, U> a, const SweepTables &t, hipStream_t st) {
     default:
       FLY_REQUIRE(false, "swept steps take 3 or 4 bands");
   }
-  if (t.pieces && (REPLAY == 0 || REPLAY == 3)) {
+  }
+  if (t.pieces && (REPLAY == 0 || REPLAY == 3 || REPLAY == 4)) {
     constexpr int V = 16 / (int)sizeof(S);
     const dim3 fgrid(blocks_for((a.batch + V - 1) / V, 256), (unsigned)std::min<int64_t>(t.split_rows, 65535));
     hipLaunchKernelGGL((k_sweep_finish<S, U, V, sizeof(S) == 4, REPLAY>), fgrid, dim3(256), 0, st, a, t.split.p,

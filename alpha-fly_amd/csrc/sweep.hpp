@@ -56,6 +56,7 @@ struct SweepTables {
   DevArray<int32_t> order;          // (npos): a row (< nrows) or nrows + a piece
   DevArray<int32_t> split;          // (split_rows): the rows split into pieces
   DevArray<int32_t> split_ptr;      // (split_rows + 1): the pieces of split[h] are split_ptr[h] .. split_ptr[h + 1] - 1
+  DevArray<int32_t> piece_row;      // (pieces): the row each piece belongs to
 };
 
 // The GPU's CU count (the swept kernel runs one workgroup per CU), per device, cached; safe to call from several
@@ -493,6 +494,7 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
   t->npos = nrows - t->split_rows + t->pieces;
   FLY_REQUIRE(nrows + t->pieces < (int64_t)1 << 24, "too many pieces");
   // 2. ranges
+  std::vector<int32_t> prow;   // each piece's row (copied until the synchronisation below)
   {
     DevArray<int32_t> off((size_t)nrows * (K + 1));
     hipLaunchKernelGGL(k_band_off<C>, dim3(blocks_for(nrows, 16)), dim3(256), 0, st, rowptr, cols, nrows, ncols, K,
@@ -510,6 +512,10 @@ std::shared_ptr<SweepTables> build_sweep(const int32_t *rowptr, const C *cols, i
       FLY_HIP(hipMemcpyAsync(t->split.p, split.data(), sizeof(int32_t) * split.size(), hipMemcpyHostToDevice, st));
       FLY_HIP(hipMemcpyAsync(t->split_ptr.p, split_ptr.data(), sizeof(int32_t) * split_ptr.size(),
                              hipMemcpyHostToDevice, st));
+      prow.resize(pieces.size());
+      for (size_t q = 0; q < pieces.size(); ++q) prow[q] = pieces[q].row;
+      t->piece_row.alloc(prow.size());
+      FLY_HIP(hipMemcpyAsync(t->piece_row.p, prow.data(), sizeof(int32_t) * prow.size(), hipMemcpyHostToDevice, st));
     }
     FLY_HIP(hipStreamSynchronize(st));   // the host vectors and temporaries end here
   }

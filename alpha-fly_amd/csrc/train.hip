@@ -918,6 +918,19 @@ __global__ __launch_bounds__(256) void k_gather_values(const float *__restrict__
   }
 }
 
+// records[i] = {col[i], the bits of w[ids[i]]} (w[i] without ids; ids past n_w give 0): a structure's {column,
+// value} records for the swept products in one pass, from the columns and the whole weight vector
+__global__ __launch_bounds__(256) void k_gather_records(const int32_t *__restrict__ col, const float *__restrict__ w,
+                                                        uint32_t wbytes, const int32_t *__restrict__ ids, int64_t n,
+                                                        int2 *__restrict__ records) {
+  const __amdgpu_buffer_rsrc_t rw = buffer_of(w, wbytes);
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const uint32_t id = ids ? (uint32_t)ids[i] : (uint32_t)i;
+    const uint32_t v = id < wbytes / 4u ? __builtin_amdgcn_raw_buffer_load_b32(rw, (int)(id * 4u), 0, 0) : 0u;
+    records[i] = make_int2(col[i], (int)v);
+  }
+}
+
 bool vec4_ok(const void *p, int64_t ld) { return ld % 4 == 0 && aligned(p, 16); }
 
 uint32_t checked_bytes(int64_t rows, int64_t ld) {
@@ -974,6 +987,63 @@ extern "C" int fly_spmm_swept(const fly_sweep *sweep, const void *records, int64
     LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
     launch_swept<float, float, 3>(a, t, as_stream(stream));
     check_launch("swept product");
+  });
+}
+
+namespace {
+// dL/dw's dots of a swept transposed backward: one float per record and chunk of 32 columns, after the pieces' sums
+size_t swept_backward_dots_bytes(const SweepTables &t, int64_t batch) {
+  return (size_t)((batch + 31) / 32) * (size_t)t.nnz * sizeof(float);
+}
+}  // namespace
+
+extern "C" size_t fly_transposed_backward_swept_workspace(const fly_sweep *sweep, int64_t batch) {
+  if (!sweep || !sweep->t || batch <= 0) return 0;
+  return align256(sweep_pieces_bytes(sweep->t.get(), batch)) + swept_backward_dots_bytes(*sweep->t, batch);
+}
+
+extern "C" int fly_transposed_backward_swept(const fly_sweep *sweep, const void *records, int64_t nnz,
+                                             const int32_t *ids, const float *gy, int64_t ldgy, const float *h,
+                                             int64_t ldh, int64_t batch, float *gh, int64_t ldgh, int32_t accumulate,
+                                             float *gw, int64_t n_w, void *ws, size_t ws_bytes, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(sweep && sweep->t && records && ids && gy && h && gh && gw, "null argument");
+    FLY_REQUIRE(current_device() == sweep->device, "the sweep tables live on another device");
+    const SweepTables &t = *sweep->t;
+    // the tables index the records: they must be the structure's nnz records, in its CSR order
+    FLY_REQUIRE(nnz == t.nnz, "the records do not match the structure's non-zeros");
+    FLY_REQUIRE(batch > 0 && batch % 4 == 0 && batch < (int64_t)INT32_MAX / 2, "the batch must be a multiple of 4");
+    FLY_REQUIRE(vec4_ok(gy, ldgy) && vec4_ok(h, ldh) && vec4_ok(gh, ldgh) && ldgy >= batch && ldh >= batch &&
+                    ldgh >= batch,
+                "gy, h and gh rows must be 16-byte aligned and hold the batch");
+    FLY_REQUIRE(n_w >= 0 && n_w < (int64_t)1 << 32, "n_w out of range");
+    const size_t pieces = align256(sweep_pieces_bytes(&t, batch));
+    FLY_REQUIRE(ws && aligned(ws, 256) && ws_bytes >= pieces + swept_backward_dots_bytes(t, batch),
+                "workspace too small or misaligned");
+    const uint32_t xbytes = buffer_bytes(t.ncols, ldgy, sizeof(float));
+    FLY_REQUIRE(xbytes != 0, "gy must be below 2 GiB with rows of 24-bit indices");
+    StepArgs<float, float> a{};
+    a.colval = static_cast<const int2 *>(records);
+    a.xprev = gy;
+    a.ldx = ldgy;
+    a.xout = gh;
+    a.ldo = ldgh;
+    a.nrows = (int32_t)t.nrows;
+    a.batch = (int32_t)batch;
+    a.xbytes = xbytes;
+    a.pieces = static_cast<float *>(ws);
+    a.hdot = h;
+    a.ldh = ldh;
+    a.dots = reinterpret_cast<float *>(static_cast<char *>(ws) + pieces);
+    a.ndots = nnz;
+    a.piece_row = t.piece_row.p;
+    a.accumulate = accumulate != 0;
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    launch_swept<float, float, 4>(a, t, as_stream(stream));
+    check_launch("swept transposed backward");
+    hipLaunchKernelGGL(k_dots_to_gw, dim3(blocks_for(nnz, 256)), dim3(256), 0, as_stream(stream), a.dots,
+                       (int32_t)nnz, (int32_t)((batch + 31) / 32), ids, (uint32_t)n_w, gw);
+    check_launch("dots to gw");
   });
 }
 
@@ -1144,6 +1214,20 @@ extern "C" int fly_gather_values(const float *w, int64_t n_w, const int32_t *ids
     hipLaunchKernelGGL(k_gather_values, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), w,
                        (uint32_t)(n_w * 4), ids, n, out);
     check_launch("gather values");
+  });
+}
+
+extern "C" int fly_gather_records(const int32_t *col, const float *w, int64_t n_w, const int32_t *ids, int64_t n,
+                                  void *records, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(n_w >= 0 && n_w < (int64_t)1 << 29 && n >= 0 && n < (int64_t)1 << 40, "size out of range");
+    if (!n) return;
+    FLY_REQUIRE(col && records && aligned(records, 8) && (n_w == 0 || w), "bad argument");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    const int64_t blocks = std::min<int64_t>(blocks_for(n, 256), 65536);
+    hipLaunchKernelGGL(k_gather_records, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), col, w,
+                       (uint32_t)(n_w * 4), ids, n, static_cast<int2 *>(records));
+    check_launch("gather records");
   });
 }
 

@@ -30,12 +30,14 @@
  *                         expected_value)
  *   fly_evaluator_download chessfly/model.py:130-131 (Evaluator.result's copies of the answers to the host)
  *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
- *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass)
+ *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass;
+ *                         _swept as a banded sweep)
  *   fly_spmv_work         chessfly/brain.py:79-99 and :238-252 (grad_h = A^T grad_y of the resting trajectory's
  *                         one-column products, under autograd)
  *   fly_rest_*            chessfly/brain.py:238-252 (_constants under autograd: the resting trajectory and the
  *                         constant drives k_t, forward and backward)
  *   fly_gather_values     chessfly/brain.py:123, 208, 248, 293 (w[op.edges], w[t_order]: a sub-matrix's values)
+ *   fly_gather_records    the same, beside the structure's columns (the swept products' records)
  *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
  *                         gradients)
  */
@@ -309,6 +311,11 @@ int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, 
  * read 0.  n_w below 2^29. */
 int fly_gather_values(const float *w_dev, int64_t n_w, const int32_t *ids_dev, int64_t n, float *out_dev,
                       void *stream);
+/* The same gather into a structure's {column, value bits} records, as fly_spmm_swept and
+ * fly_transposed_backward_swept read them: records[i] = {col[i], w[ids[i]]} (w[i] with ids NULL; ids at or past n_w
+ * give 0), records 8-byte aligned (chessfly/brain.py:123, 208: w[op.edges] beside the structure's columns). */
+int fly_gather_records(const int32_t *col_dev, const float *w_dev, int64_t n_w, const int32_t *ids_dev, int64_t n,
+                       void *records_dev, void *stream);
 
 /* The resting trajectory of training (chessfly/brain.py:238-252: the network with no position, one column) and
  * the drive the rows of each light-cone step get from outside the cone, k_t = (W c_{t-1} + b -
@@ -390,6 +397,19 @@ int fly_transposed_backward(const int32_t *t_rowptr_dev, const int32_t *t_col_de
                             int64_t ldgh, int32_t accumulate, float *gw_dev, int64_t n_w, const int32_t *items_dev,
                             int64_t n_items, const int32_t *splits_dev, int64_t n_splits, float *partials_dev,
                             int64_t n_slots, float *dots_dev, int64_t n_dots, void *stream);
+
+/* The same backward as a banded sweep of gy's rows: sweep = the tables of A^T's structure (fly_sweep_create over
+ * t_rowptr / t_col, rows = columns of A), records_dev = A^T's nnz {column, value bits} pairs in its CSR order,
+ * ids_dev = each non-zero's slot in gw (ids at or past n_w skipped).  gh (rows of A^T, ldgh) (+)= A^T gy, split
+ * rows' pieces added in piece order; each record's dot with the row's own h over each 32-column chunk is kept in
+ * the workspace and the chunks are added in order into gw[ids[e]], so results are deterministic.  The batch must be
+ * a multiple of 4 and the rows of gy, h and gh 16-byte aligned.  workspace: fly_transposed_backward_swept_workspace
+ * bytes, 256-byte aligned. */
+size_t fly_transposed_backward_swept_workspace(const fly_sweep *sweep, int64_t batch);
+int fly_transposed_backward_swept(const fly_sweep *sweep, const void *records_dev, int64_t nnz, const int32_t *ids_dev,
+                                  const float *gy_dev, int64_t ldgy, const float *h_dev, int64_t ldh, int64_t batch,
+                                  float *gh_dev, int64_t ldgh, int32_t accumulate, float *gw_dev, int64_t n_w,
+                                  void *workspace_dev, size_t workspace_bytes, void *stream);
 
 /* One recurrent step of training, the elementwise parts fused (brain.py:313-327 under autograd), float32,
  * one row of R_t per wave; rows are (rows, batch) with leading dimensions ld*:

@@ -259,6 +259,76 @@ def test_swept_forward_product_matches_float64(batch, hubs):
         assert not np.isfinite(y_inf[reads]).any()
 
 
+@pytest.mark.parametrize("batch", [4, 68, 200, 256])
+@pytest.mark.parametrize("shape", ["by size", "by size with hubs", "forced, small and heavy-tailed"])
+def test_swept_transposed_backward_matches_float64(batch, shape):
+    """fly_transposed_backward_swept (the backward over A^T as a banded sweep of gy's rows): gh (+)= A^T gy and
+    gw[ids[e]] += sum_b gy[i_e, b] h[j_e, b], against float64.  A^T with 70,000 rows of ~40 non-zeros over 40,000
+    rows of gy (the size rule sweeps it), plain and with hub rows split into pieces; and a 300-row A^T with rows of
+    up to 1,500 non-zeros and empty ones, swept by force on 4 workgroups (spread slots, several passes per wave).
+    Batches end inside a 32-column chunk (68, 200); the workspace starts as NaN, so a dot left unwritten would show;
+    a second call gives the same bits."""
+    from chessfly import _hip
+    lib = _hip.load()
+    rng = np.random.default_rng([batch, len(shape)])
+    if shape == "forced, small and heavy-tailed":
+        n_t, n_g = 300, 400                                     # rows of A^T (= rows of h), rows of gy
+        t_crow_h, rt, ct, val = _heavy_csr(n_t, n_g, batch + 11)
+        t_crow = np.asarray(t_crow_h, np.int64)
+        t_col = np.asarray(ct, np.int64)
+        val = np.asarray(val, np.float32)
+        keys = {"swept": 1, "sweep_grid": 4}
+    else:
+        n_t, n_g = 70_000, 40_000
+        lens = rng.poisson(40, n_t)
+        if shape == "by size with hubs":
+            lens[[3, 4_321, 69_999]] = [3000, 900, 4 * int(lens.mean()) + 200]
+        t_crow = np.concatenate([[0], np.cumsum(lens)])
+        t_col = np.concatenate([np.sort(rng.integers(0, n_g, n)) for n in lens])
+        val = rng.standard_normal(len(t_col)).astype(np.float32)
+        keys = {}
+    nnz = len(t_col)
+    rows_t = np.repeat(np.arange(n_t), np.diff(t_crow))          # each non-zero's row of A^T
+    gy = rng.standard_normal((n_g, batch)).astype(np.float32)
+    h = rng.standard_normal((n_t, batch)).astype(np.float32)
+    gh0 = rng.standard_normal((n_t, batch)).astype(np.float32)
+    ids = rng.permutation(2 * nnz)[:nnz].astype(np.int32)        # each non-zero's slot in a longer vector
+    gw0 = rng.standard_normal(2 * nnz).astype(np.float32)
+    d = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=DEV)
+    t_crow_d, t_col_d, val_d, ids_d = d(t_crow.astype(np.int32)), d(t_col.astype(np.int32)), d(val), d(ids)
+    gy_d, h_d = d(gy), d(h)
+    for k, v in keys.items():
+        _hip.set_tuning(k, v)
+    try:
+        tables = _hip.sweep_create(t_crow_d, t_col_d, n_t, n_g)
+    finally:
+        for k in keys:
+            _hip.set_tuning(k, 0)
+    assert tables is not None, "the structure did not sweep"
+    info = _hip.sweep_info(tables.handle)
+    records = torch.stack((t_col_d, val_d.view(torch.int32)), dim=1)
+    st = _hip.stream(torch.device(DEV))
+    outs = []
+    for _ in range(2):
+        gh, gw = d(gh0), d(gw0)
+        ws = _hip.workspace(lib.fly_transposed_backward_swept_workspace(tables.handle, batch), torch.device(DEV))
+        ws.fill_(255)                                            # NaN floats
+        _hip.check(lib.fly_transposed_backward_swept(tables.handle, records.data_ptr(), nnz, ids_d.data_ptr(),
+                                                     gy_d.data_ptr(), batch, h_d.data_ptr(), batch, batch,
+                                                     gh.data_ptr(), batch, 1, gw.data_ptr(), gw.numel(),
+                                                     ws.data_ptr(), ws.numel(), st), "fly_transposed_backward_swept")
+        torch.cuda.synchronize()
+        outs.append((gh.cpu(), gw.cpu()))
+    want_gh = gh0.astype(np.float64).copy()
+    np.add.at(want_gh, rows_t, val[:, None].astype(np.float64) * gy[t_col].astype(np.float64))
+    want_gw = gw0.astype(np.float64).copy()
+    want_gw[ids] += (gy[t_col].astype(np.float64) * h[rows_t].astype(np.float64)).sum(1)
+    print(f"{shape} B={batch}: {info}", flush=True)
+    _close(outs[0][0], torch.as_tensor(want_gh), 1e-5, "grad_h")
+    _close(outs[0][1], torch.as_tensor(want_gw), 1e-5, "dL/dw")
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), "not deterministic"
+
+
 def test_gather_values_reads_the_weight_vector_at_int32_ids():
     """fly_gather_values: out[i] = w[ids[i]] (a sub-matrix's values in its own or its transpose's order), ids past
     the vector (and negative ones) read 0, bit for bit."""
@@ -355,12 +425,16 @@ def test_forward_io_gradients_match_the_oracle_and_the_full_recurrence(steps):
 
 
 @pytest.mark.parametrize("batch", [8, 200])
-def test_cone_gradients_over_the_transposed_pass_match_the_oracle_and_repeat_exactly(batch):
+@pytest.mark.parametrize("swept", [False, True])
+def test_cone_gradients_over_the_transposed_pass_match_the_oracle_and_repeat_exactly(batch, swept):
     """forward_io under autograd at batches that take the one pass over A^T (multiples of 4): one chunk (8
     boards) and chunk-major with a ragged last chunk (200), on a 3,000-neuron synthetic graph whose longest rows
     of A^T (out-degrees up to 870) run as several work-list segments.  Gradients against the oracle in float64
     (chessfly/brain.py:289-329), and a second run from the same state gives the same bits: partial rows meet
-    in slot order, the chunks' dots add in order, and dL/dw returns from W^T's order by a gather."""
+    in slot order, the chunks' dots add in order, and dL/dw returns from W^T's order by a gather.  `swept`: the
+    sweep forced onto the graph's structures (4 workgroups), so the forward products and the passes over A^T run
+    as banded sweeps, with the long rows of A^T split into pieces."""
+    from chessfly import _hip
     from chessfly.synthetic import GraphSpec, synthetic_connectome
     from oracle import training as T
     from oracle.lightcone import light_cone
@@ -371,12 +445,23 @@ def test_cone_gradients_over_the_transposed_pass_match_the_oracle_and_repeat_exa
     u_in = rng.normal(0, 1, (300, batch))
     target = torch.as_tensor(rng.normal(0, 1, (100, batch)))
     runs = []
-    for _ in range(2):
-        rnn.zero_grad()
-        u_d = torch.tensor(u_in, dtype=torch.float32, device=DEV, requires_grad=True)
-        out = rnn.forward_io(u_d, in_idx, out_idx, 6)
-        ((out - target.float().to(DEV)) ** 2).sum().backward()
-        runs.append([out.detach().clone()] + [g.clone() for g in _device_grads(rnn, u_d)])
+    keys = {"swept": 1, "sweep_grid": 4} if swept else {}
+    for k, v in keys.items():
+        _hip.set_tuning(k, v)
+    try:
+        for _ in range(2):
+            rnn.zero_grad()
+            u_d = torch.tensor(u_in, dtype=torch.float32, device=DEV, requires_grad=True)
+            out = rnn.forward_io(u_d, in_idx, out_idx, 6)
+            ((out - target.float().to(DEV)) ** 2).sum().backward()
+            runs.append([out.detach().clone()] + [g.clone() for g in _device_grads(rnn, u_d)])
+    finally:
+        for k in keys:
+            _hip.set_tuning(k, 0)
+    if swept:
+        dcone = rnn.light_cone(in_idx, out_idx, 6)
+        ops = [op for op in dcone.ops if op is not None]
+        assert any(getattr(op, "_sweep_t", (None, None))[1] is not None for op in ops), "no pass over A^T swept"
     names = ("out", "u_in", "log_gain", "bias", "alpha_logit")
     for first, second, name in zip(runs[0], runs[1], names):
         assert torch.equal(first, second), f"{name} differs between two identical runs"
