@@ -286,6 +286,35 @@ def test_heads_and_norm_closed_form():
     np.testing.assert_allclose(F.expected_value(wdl).numpy(), p[:, 0] - p[:, 2], rtol=1e-12)
 
 
+def test_encode_input_closed_form():
+    """encode_input (model.py:101-102: ((x[:, :n_base] W[:, :n_base]^T + b) * input_gain), cast, transposed) against a
+    loop over the sensory rows: only the first n_base feature columns count (a change past them changes nothing), the
+    gain multiplies the biased sum, the output is (n_in, B) contiguous in the requested dtype, and a float64 x is
+    computed in float64."""
+    rng = np.random.default_rng(5)
+    from oracle.forward import HeadArrays
+    n_in, k_all, n_base, batch = 7, 12, 9, 5
+    t = lambda a: torch.as_tensor(np.asarray(a, dtype=np.float64))
+    z = lambda *shape: t(np.zeros(shape))
+    hp = HeadArrays(t(rng.normal(size=(n_in, k_all))), t(rng.normal(size=n_in)), 5.0, n_base, z(3, 2), z(3), z(64, 2),
+                    z(64), z(64, 2), z(64), z(3, 2), z(3), torch.zeros(3, dtype=torch.long),
+                    torch.zeros(3, dtype=torch.long), z(2), t(np.ones(2)))
+    x = t(rng.integers(0, 2, size=(batch, k_all)))
+    u = F.encode_input(hp, x, torch.float64)
+    assert u.shape == (n_in, batch) and u.is_contiguous() and u.dtype == torch.float64
+    W, b = hp.enc_w.numpy(), hp.enc_b.numpy()
+    for i in range(n_in):
+        for bi in range(batch):
+            want = (sum(x[bi, f].item() * W[i, f] for f in range(n_base)) + b[i]) * 5.0
+            assert u[i, bi].item() == pytest.approx(want, rel=1e-13, abs=1e-13)
+    x2 = x.clone()
+    x2[:, n_base:] = 1.0 - x2[:, n_base:]
+    assert torch.equal(F.encode_input(hp, x2, torch.float64), u), "columns past n_base must not count"
+    u16 = F.encode_input(hp, x.float(), torch.float16)   # float32 arithmetic, then one float16 rounding
+    assert u16.dtype == torch.float16 and u16.shape == (n_in, batch)
+    assert float((u16.double() - u).abs().max()) <= float(u.abs().max()) * 2.0 ** -10
+
+
 def test_move_squares_matches_the_move_index_of_every_move():
     """move_squares against the policy-index definition (chessfly/encoding.py:70-77) for every normal move
     and every legal underpromotion (the check of tests/test_core.py:394-405, without python-chess)."""
