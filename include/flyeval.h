@@ -29,7 +29,10 @@
  *   fly_evaluator_outputs chessfly/model.py:120-128 and :107-110 (Evaluator.submit's half cast or legal gather,
  *                         expected_value)
  *   fly_evaluator_download chessfly/model.py:130-131 (Evaluator.result's copies of the answers to the host)
- *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w)
+ *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w); fly_spmm_swept the
+ *                         forward product as a banded sweep
+ *   fly_sweep_*, fly_plan_sweep_info  no counterpart (cuSPARSE keeps its own analysis of a structure): the banded
+ *                         sweep's tables of one CSR structure
  *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass;
  *                         _swept as a banded sweep)
  *   fly_spmv_work         chessfly/brain.py:79-99 and :238-252 (grad_h = A^T grad_y of the resting trajectory's
@@ -40,6 +43,8 @@
  *   fly_gather_records    the same, beside the structure's columns (the swept products' records)
  *   fly_train_step_*      chessfly/brain.py:313-327 under autograd (clamp, index_add, index_copy, lerp and their
  *                         gradients)
+ *   fly_model_forward_static  no counterpart: the model forward for callers that cannot allocate
+ *   fly_profile_*, fly_set_tuning, fly_get_tuning  measurement and launch-shape choices (timing scripts)
  */
 #ifndef FLYEVAL_H
 #define FLYEVAL_H
