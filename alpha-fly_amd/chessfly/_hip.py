@@ -82,6 +82,8 @@ SIGNATURES = {
     "fly_transposed_backward": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p,
                                        _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p]),
     "fly_gather_records": (_i32, [_p, _p, _i64, _p, _i64, _p, _p]),
+    "fly_spmm_f64": (_i32, [_p, _p, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p]),
+    "fly_sddmm_f64": (_i32, [_p, _p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _i32, _p]),
     "fly_transposed_backward_swept_workspace": (_sz, [_p, _i64]),
     "fly_transposed_backward_swept": (_i32, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _i64, _p,
                                              _sz, _p]),

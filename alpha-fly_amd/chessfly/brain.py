@@ -485,6 +485,58 @@ class _SparseRecurrent(torch.autograd.Function):
         return grad_h, grad_w, None
 
 
+def _spmm64(op, w: torch.Tensor, x: torch.Tensor, transposed: bool = False) -> torch.Tensor:
+    """A x (or A^T x) in float64 (fly_spmm_f64), A's values read from the whole weight vector w at A's edge ids."""
+    if transposed:
+        crow32, col32, ids32 = op._transposed()          # A^T's structure, its non-zeros' edge ids
+        _, _, n_rows, n_cols = op._structure()
+        n_rows, n_cols = n_cols, n_rows
+    else:
+        crow32, col32, n_rows, n_cols = op._structure()
+        ids = op._edge_ids()
+        ids32 = None if ids is None else ids[0]
+    x = x.contiguous()
+    batch = x.shape[1]
+    y = torch.empty(n_rows, batch, dtype=torch.float64, device=x.device)
+    _hip.check(_hip.load().fly_spmm_f64(crow32.data_ptr(), col32.data_ptr(), col32.numel(), w.data_ptr(),
+                                        _hip.ptr(ids32), w.numel(), n_rows, n_cols, x.data_ptr(), max(batch, 1),
+                                        batch, y.data_ptr(), max(batch, 1), 0, _hip.stream(x.device)), "fly_spmm_f64")
+    return y
+
+
+class _SparseRecurrent64(torch.autograd.Function):
+    """y = A h in float64 for networks converted to float64 (brain.py:66-99 in float64): the product over A's
+    structure, the state gradient over its transposed structure (fly_spmm_f64) and dL/dw at A's edge ids
+    (fly_sddmm_f64), every sum in CSR order."""
+
+    @staticmethod
+    def forward(ctx, h, w, op):
+        h = h.contiguous()
+        ctx.save_for_backward(h, w)
+        ctx.op = op
+        return _spmm64(op, w, h)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        h, w = ctx.saved_tensors
+        op = ctx.op
+        g = grad_y.contiguous()
+        grad_h = grad_w = None
+        if ctx.needs_input_grad[0]:
+            grad_h = _spmm64(op, w, g, transposed=True)
+        if ctx.needs_input_grad[1]:
+            crow32, col32, n_rows, n_cols = op._structure()
+            ids = op._edge_ids()
+            batch = h.shape[1]
+            grad_w = torch.zeros_like(w)
+            _hip.check(_hip.load().fly_sddmm_f64(crow32.data_ptr(), col32.data_ptr(), col32.numel(), n_rows, n_cols,
+                                                 g.data_ptr(), max(batch, 1), h.data_ptr(), max(batch, 1), batch,
+                                                 grad_w.data_ptr(), grad_w.numel(),
+                                                 _hip.ptr(None if ids is None else ids[0]), 0,
+                                                 _hip.stream(h.device)), "fly_sddmm_f64")
+        return grad_h, grad_w, None
+
+
 class _SubMatrix:
     """Rows x columns of W as its own CSR (brain.py:102-123), read back from the device cone on first use:
     `edges` (global edge ids in W's order), `post` / `pre` (local row / column), `crow`, `shape`."""
@@ -778,6 +830,68 @@ class ConnectomeRNN(nn.Module):
     def _param_key(self):
         return tuple((p._version, p.data_ptr()) for p in (self.log_gain, self.bias, self.alpha_logit))
 
+    def _is_f64(self) -> bool:
+        """A network converted to float64 (the reference's .double() test modules): it runs through the float64
+        products, in float64, under autograd or not."""
+        return self.log_gain.dtype == torch.float64
+
+    def _check_params_f64(self, what: str) -> None:
+        for name in ("log_gain", "bias", "alpha_logit", "sign", "w0"):
+            t = getattr(self, name)
+            _hip.require_device(t, what)
+            if t.dtype != torch.float64:
+                raise RuntimeError(f"{what}: a float64 network needs every parameter in float64; {name} is {t.dtype}")
+
+    def _forward64(self, u: torch.Tensor, steps: int) -> torch.Tensor:
+        """The literal recurrence of a float64 network (brain.py:211-229 in float64).  Under autograd u stays as it
+        is; without, u becomes u + bias in place, as the reference's inference path leaves it."""
+        self._check_params_f64("ConnectomeRNN.forward")
+        if u.dtype != torch.float64 or u.dim() != 2 or u.shape[0] != self.n:
+            raise RuntimeError(f"ConnectomeRNN.forward: a float64 network takes float64 u ({self.n}, B), got "
+                               f"{u.dtype} {tuple(u.shape)}")
+        alpha = torch.sigmoid(self.alpha_logit).unsqueeze(1)
+        w = self.edge_weights()
+        drive = self.bias.unsqueeze(1) + u if torch.is_grad_enabled() else u.add_(self.bias.unsqueeze(1))
+        h = torch.zeros_like(drive)
+        for _ in range(steps):
+            x = (_SparseRecurrent64.apply(h, w, self) + drive).clamp(0, self.h_max)
+            h = torch.lerp(h, x, alpha)
+        return h
+
+    def _forward_io64(self, u_in: torch.Tensor, cone: "LightCone", out_idx: torch.Tensor, steps: int) -> torch.Tensor:
+        """forward_io of a float64 network (brain.py:238-252 and 289-329 in float64), under autograd or not: the
+        resting trajectory c_t and the constant drives k_t of the light cone's rows, then per step the sub-matrix
+        product plus k_t and the input, clamped, from the resting state or the carried row."""
+        self._check_params_f64("ConnectomeRNN.forward_io")
+        if u_in.dtype != torch.float64:
+            raise RuntimeError(f"forward_io: a float64 network takes float64 u_in, got {u_in.dtype}")
+        batch = u_in.shape[1]
+        w = self.edge_weights()
+        alpha = torch.sigmoid(self.alpha_logit).unsqueeze(1)
+        bias = self.bias.unsqueeze(1)
+        c = torch.zeros(self.n, 1, dtype=torch.float64, device=u_in.device)
+        cs, ks = [c], [None]
+        for t in range(1, steps + 1):
+            full = (_SparseRecurrent64.apply(c, w, self) if t > 1 else torch.zeros_like(c)) + bias
+            k = full.index_select(0, cone.rows[t])
+            op = cone.ops[t]
+            if op is not None:     # the drive from outside R_{t-1}: the full sum less the sub-matrix's share
+                k = k - _SparseRecurrent64.apply(c.index_select(0, cone.rows[t - 1]), w, op)
+            ks.append(k)
+            c = torch.lerp(c, full.clamp(0, self.h_max), alpha)
+            cs.append(c)
+        h = None
+        for t in range(1, steps + 1):
+            rows, op = cone.rows[t], cone.ops[t]
+            x = ks[t].expand(-1, batch) if op is None else _SparseRecurrent64.apply(h, w, op) + ks[t]
+            x = x.index_add(0, cone.u_pos[t], u_in.index_select(0, cone.u_src[t])).clamp(0, self.h_max)
+            p = cs[t - 1].index_select(0, rows).expand(-1, batch)
+            if cone.keep_next[t].numel():
+                p = p.index_copy(0, cone.keep_next[t], h.index_select(0, cone.keep_prev[t]))
+            h = torch.lerp(p, x, alpha.index_select(0, rows))
+        out = cs[steps].index_select(0, out_idx.to(u_in.device)).expand(-1, batch)
+        return out.index_copy(0, cone.out_pos, h.index_select(0, cone.out_src))
+
     def _check_params(self, what: str) -> None:
         for name in ("log_gain", "bias", "alpha_logit", "sign", "w0"):
             t = getattr(self, name)
@@ -788,7 +902,7 @@ class ConnectomeRNN(nn.Module):
     def edge_weights(self) -> torch.Tensor:
         """sign * w0 * exp(log_gain) per edge, in CSR order (brain.py:201-202).  Under autograd, the
         differentiable expression; otherwise one device kernel."""
-        if torch.is_grad_enabled() and self.log_gain.requires_grad:
+        if (torch.is_grad_enabled() and self.log_gain.requires_grad) or self._is_f64():
             return self.sign * self.w0 * torch.exp(self.log_gain)
         self._check_params("edge_weights")
         w = torch.empty_like(self.w0)
@@ -884,9 +998,12 @@ class ConnectomeRNN(nn.Module):
         """u: (N, B) contiguous constant external drive.  Returns the state after `steps` updates, (N, B).
         As in the reference's inference path, u is updated in place to u + bias (brain.py:218).  The recurrence
         runs in u's dtype (brain.py:215-216): float32; float64 (the float32 weights widen exactly); float16 (the
-        weights and bias rounded to float16, a float16 state, its sums in float32)."""
+        weights and bias rounded to float16, a float16 state, its sums in float32).  A network converted to float64
+        (.double()) runs in float64 through its float64 products, with or without autograd."""
         assert u.is_contiguous()
         _hip.require_device(u, "ConnectomeRNN.forward")
+        if self._is_f64():
+            return self._forward64(u, steps)
         self._check_params("ConnectomeRNN.forward")
         if torch.is_grad_enabled():
             return self._forward_autograd(u, steps)
@@ -952,8 +1069,13 @@ class ConnectomeRNN(nn.Module):
         updates, (len(out_idx), B): forward(u, steps)[out_idx] with u zero outside in_idx.  float16 u_in
         takes the deviation path and returns float32; float32 u_in takes the float32 path; float64 u_in runs the
         light cone in float64 over the float32 cache (brain.py:295-329 in u_in's dtype) and returns float64.
-        Under autograd the float32 light cone runs differentiably (training)."""
+        Under autograd the float32 light cone runs differentiably (training).  A network converted to float64 runs
+        the light cone in float64, with or without autograd."""
         _hip.require_device(u_in, "ConnectomeRNN.forward_io")
+        if self._is_f64():
+            if u_in.dim() != 2 or u_in.shape[0] != len(in_idx):
+                raise RuntimeError(f"forward_io: u_in must be (len(in_idx), B), got {tuple(u_in.shape)}")
+            return self._forward_io64(u_in, self.light_cone(in_idx, out_idx, steps), out_idx, steps)
         self._check_params("ConnectomeRNN.forward_io")
         if torch.is_grad_enabled():
             if u_in.dim() != 2 or u_in.shape[0] != len(in_idx):

@@ -1217,6 +1217,86 @@ extern "C" int fly_gather_values(const float *w, int64_t n_w, const int32_t *ids
   });
 }
 
+namespace {
+// float64 products for modules converted to float64 (the reference's .double() tests): plain and exact, one wave per
+// row with the lanes over the batch columns, each sum in CSR order.  Row pointers are clamped into [0, nnz], values
+// read at e or val_ids[e] only below n_val and columns only below ncols, so a malformed structure gives wrong
+// results, never an access outside the arrays.
+__global__ __launch_bounds__(256) void k_spmm_f64(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col,
+                                                  int64_t nnz, const double *__restrict__ val,
+                                                  const int32_t *__restrict__ val_ids, int64_t n_val, int64_t nrows,
+                                                  int64_t ncols, const double *__restrict__ x, int64_t ldx,
+                                                  int64_t batch, double *__restrict__ y, int64_t ldy, int accumulate) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= nrows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t beg = min(max((int64_t)rowptr[r], (int64_t)0), nnz);
+  const int64_t end = min(max((int64_t)rowptr[r + 1], beg), nnz);
+  for (int64_t b = lane; b < batch; b += 64) {
+    double acc = 0.0;
+    for (int64_t e = beg; e < end; ++e) {
+      const int64_t v = val_ids ? (int64_t)val_ids[e] : e;
+      const int64_t c = col[e];
+      if (v >= 0 && v < n_val && c >= 0 && c < ncols) acc = fma(val[v], x[c * ldx + b], acc);
+    }
+    double *dst = y + r * ldy + b;
+    *dst = accumulate ? *dst + acc : acc;
+  }
+}
+
+// out[ids ? ids[e] : e] (+)= sum_b g[row_e, b] x[col_e, b]: one wave per row, a lane per non-zero (ids distinct; ids
+// at or past n_out skipped)
+__global__ __launch_bounds__(256) void k_sddmm_f64(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col,
+                                                   int64_t nnz, int64_t nrows, int64_t ncols,
+                                                   const double *__restrict__ g, int64_t ldg,
+                                                   const double *__restrict__ x, int64_t ldx, int64_t batch,
+                                                   double *__restrict__ out, int64_t n_out,
+                                                   const int32_t *__restrict__ ids, int accumulate) {
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= nrows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t beg = min(max((int64_t)rowptr[r], (int64_t)0), nnz);
+  const int64_t end = min(max((int64_t)rowptr[r + 1], beg), nnz);
+  for (int64_t e = beg + lane; e < end; e += 64) {
+    const int64_t c = col[e];
+    const int64_t slot = ids ? (int64_t)ids[e] : e;
+    if (c < 0 || c >= ncols || slot < 0 || slot >= n_out) continue;
+    double acc = 0.0;
+    for (int64_t b = 0; b < batch; ++b) acc = fma(g[r * ldg + b], x[c * ldx + b], acc);
+    out[slot] = accumulate ? out[slot] + acc : acc;
+  }
+}
+}  // namespace
+
+extern "C" int fly_spmm_f64(const int32_t *rowptr, const int32_t *col, int64_t nnz, const double *val,
+                            const int32_t *val_ids, int64_t n_val, int64_t nrows, int64_t ncols, const double *x,
+                            int64_t ldx, int64_t batch, double *y, int64_t ldy, int32_t accumulate, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0 && nnz >= 0 && n_val >= 0, "negative size");
+    if (!nrows || !batch) return;
+    FLY_REQUIRE(rowptr && y && ldy >= batch, "bad argument");
+    FLY_REQUIRE(nnz == 0 || (col && val && x && ldx >= batch), "bad argument");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    hipLaunchKernelGGL(k_spmm_f64, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), rowptr, col, nnz, val,
+                       val_ids, n_val, nrows, ncols, x, ldx, batch, y, ldy, (int)(accumulate != 0));
+    check_launch("spmm f64");
+  });
+}
+
+extern "C" int fly_sddmm_f64(const int32_t *rowptr, const int32_t *col, int64_t nnz, int64_t nrows, int64_t ncols,
+                             const double *g, int64_t ldg, const double *x, int64_t ldx, int64_t batch, double *out,
+                             int64_t n_out, const int32_t *ids, int32_t accumulate, void *stream) {
+  return guard([&] {
+    FLY_REQUIRE(nrows >= 0 && ncols >= 0 && batch >= 0 && nnz >= 0 && n_out >= 0, "negative size");
+    if (!nrows || !nnz) return;
+    FLY_REQUIRE(rowptr && col && out && (batch == 0 || (g && x && ldg >= batch && ldx >= batch)), "bad argument");
+    LaunchTimer timer(FLY_K_OTHER, as_stream(stream));
+    hipLaunchKernelGGL(k_sddmm_f64, dim3(blocks_for(nrows, 4)), dim3(256), 0, as_stream(stream), rowptr, col, nnz,
+                       nrows, ncols, g, ldg, x, ldx, batch, out, n_out, ids, (int)(accumulate != 0));
+    check_launch("sddmm f64");
+  });
+}
+
 extern "C" int fly_gather_records(const int32_t *col, const float *w, int64_t n_w, const int32_t *ids, int64_t n,
                                   void *records, void *stream) {
   return guard([&] {

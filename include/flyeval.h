@@ -30,7 +30,7 @@
  *                         expected_value)
  *   fly_evaluator_download chessfly/model.py:130-131 (Evaluator.result's copies of the answers to the host)
  *   fly_spmm, fly_sddmm   chessfly/brain.py:66-99 (_SparseRecurrent forward, grad_h and grad_w); fly_spmm_swept the
- *                         forward product as a banded sweep
+ *                         forward product as a banded sweep; _f64 in float64
  *   fly_sweep_*, fly_plan_sweep_info  no counterpart (cuSPARSE keeps its own analysis of a structure): the banded
  *                         sweep's tables of one CSR structure
  *   fly_transposed_backward  chessfly/brain.py:79-99 (_SparseRecurrent.backward: grad_h and grad_w in one pass;
@@ -311,6 +311,18 @@ int fly_spmm(const int32_t *rowptr_dev, const int32_t *col_dev, const float *val
 int fly_sddmm(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nrows, int64_t ncols, const float *g_dev,
               int64_t ldg, const float *x_dev, int64_t ldx, int64_t batch, float *out_dev, int64_t n_out,
               const int32_t *ids_dev, int32_t accumulate, void *stream);
+
+/* The same products in float64, for networks converted to float64 (the reference's .double() test modules,
+ * tests/test_core.py:28-44 and :309-338, which run ConnectomeRNN under autograd in float64): y (nrows, ldy) (+)= A x with
+ * A's values val[e] or val[val_ids[e]], and out[ids ? ids[e] : e] (+)= sum_b g[row_e, b] x[col_e, b].  nnz bounds
+ * the row pointer; values past n_val, columns past ncols and ids past n_out are skipped.  Each sum runs in CSR
+ * order. */
+int fly_spmm_f64(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nnz, const double *val_dev,
+                 const int32_t *val_ids_dev, int64_t n_val, int64_t nrows, int64_t ncols, const double *x_dev,
+                 int64_t ldx, int64_t batch, double *y_dev, int64_t ldy, int32_t accumulate, void *stream);
+int fly_sddmm_f64(const int32_t *rowptr_dev, const int32_t *col_dev, int64_t nnz, int64_t nrows, int64_t ncols,
+                  const double *g_dev, int64_t ldg, const double *x_dev, int64_t ldx, int64_t batch, double *out_dev,
+                  int64_t n_out, const int32_t *ids_dev, int32_t accumulate, void *stream);
 
 /* out[i] = w[ids[i]] for i < n (a sub-matrix's values in its own or its transpose's order); ids at or past n_w
  * read 0.  n_w below 2^29. */

@@ -329,6 +329,100 @@ def test_swept_transposed_backward_matches_float64(batch, shape):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), "not deterministic"
 
 
+def _rnn64_pair(conn, seed: int, h_max=10.0, scale: float = 3.0):
+    """A network converted to float64 (as the reference's tests convert theirs, tests/test_core.py:29, 312) with
+    parameters that float32 cannot hold, and the oracle's arrays of the same float64 values."""
+    from chessfly.brain import ConnectomeRNN
+    lg, bias, al = random_params(conn, seed)
+    rng = np.random.default_rng(seed + 1000)
+    lg, bias, al = (a.astype(np.float64) + rng.normal(0, 1e-3, a.shape) for a in (lg, bias, al))
+    rnn = ConnectomeRNN(conn, global_scale=scale, h_max=h_max).double().to(DEV)
+    with torch.no_grad():
+        rnn.log_gain.copy_(torch.as_tensor(lg))
+        rnn.bias.copy_(torch.as_tensor(bias))
+        rnn.alpha_logit.copy_(torch.as_tensor(al))
+    b = brain_arrays(conn, scale, lg, bias, al, h_max=h_max, dtype=torch.double)
+    b.w0 = rnn.w0.cpu()                                        # the network's own float64 weights
+    for name in ("log_gain", "bias", "alpha_logit"):
+        setattr(b, name, getattr(b, name).clone().requires_grad_(True))
+    return rnn, b
+
+
+@pytest.mark.parametrize("h_max", [10.0, None])
+def test_float64_network_literal_recurrence_and_gradients(h_max):
+    """A float64 network (ConnectomeRNN(...).double(), tests/test_core.py:28-44): the literal recurrence under
+    autograd runs in float64 on the device (fly_spmm_f64, fly_sddmm_f64), state and gradients of u, log_gain, bias and
+    alpha_logit against the oracle's float64 recurrence to 1e-10; without autograd the same state, with u left as
+    u + bias (brain.py:218)."""
+    from oracle import training as T
+    conn = tiny_connectome(200, 3000, seed=1)
+    rnn, b = _rnn64_pair(conn, 4, h_max=h_max)
+    assert rnn.log_gain.dtype == torch.float64
+    rng = np.random.default_rng(5)
+    u = rng.random((conn.n_neurons, 6)) * (3.0 if h_max is None else 1.0)
+    target = rng.random((conn.n_neurons, 6))
+    u_d = torch.tensor(u, device=DEV, requires_grad=True)
+    out = rnn(u_d, 5)
+    assert out.dtype == torch.float64
+    ((out - torch.as_tensor(target, device=DEV)) ** 2).sum().backward()
+    u_r = torch.tensor(u, requires_grad=True)
+    ref = T.literal_grad(b, u_r, 5)
+    ((ref - torch.as_tensor(target)) ** 2).sum().backward()
+    _close(out, ref, 1e-10, "state")
+    for got, want, name in zip(_device_grads(rnn, u_d), (u_r.grad, b.log_gain.grad, b.bias.grad, b.alpha_logit.grad),
+                               ("u", "log_gain", "bias", "alpha_logit")):
+        assert float(want.abs().max()) > 0, name
+        _close(got, want, 1e-10, name)
+    u2 = torch.tensor(u, device=DEV)
+    with torch.no_grad():
+        h = rnn(u2, 5)
+    _close(h, ref, 1e-10, "state without autograd")
+    assert torch.equal(u2.cpu(), torch.as_tensor(u) + b.bias.detach()[:, None]), "u + bias in place"
+
+
+@pytest.mark.parametrize("steps", [1, 2, 4, 6])
+def test_float64_network_light_cone_equals_the_literal_recurrence(steps):
+    """A float64 network's forward_io (tests/test_core.py:309-338): outputs and the gradients of u_in, log_gain, bias
+    and alpha_logit equal the literal recurrence's at the output rows (to 1e-9) and the oracle's float64 light cone
+    (oracle.training.cone_grad); without autograd the same outputs."""
+    from oracle import training as T
+    from oracle.lightcone import light_cone
+    conn = tiny_connectome(120, 700, seed=3)
+    rnn, b = _rnn64_pair(conn, 6)
+    in_idx, out_idx = torch.arange(0, 9, device=DEV), torch.arange(100, 120, device=DEV)
+    rng = np.random.default_rng(steps)
+    u_in = rng.normal(0, 1, (9, 5))
+    target = torch.as_tensor(rng.normal(0, 1, (20, 5)), device=DEV)
+    results = []
+    for mode in ("literal", "cone"):
+        rnn.zero_grad()
+        u_d = torch.tensor(u_in, device=DEV, requires_grad=True)
+        if mode == "literal":
+            u = torch.zeros(conn.n_neurons, 5, dtype=torch.float64, device=DEV).index_add(0, in_idx, u_d)
+            out = rnn(u.contiguous(), steps)[out_idx]
+        else:
+            out = rnn.forward_io(u_d, in_idx, out_idx, steps)
+        ((out - target) ** 2).sum().backward()
+        results.append([out.detach()] + [g if g is not None else torch.zeros_like(p)
+                                         for g, p in zip(_device_grads(rnn, u_d), (u_d, rnn.log_gain, rnn.bias,
+                                                                                    rnn.alpha_logit))])
+    names = ("out", "u_in", "log_gain", "bias", "alpha_logit")
+    for lit, cone_r, name in zip(results[0], results[1], names):
+        _close(cone_r, lit, 1e-9, f"{name}: light cone against the literal recurrence")
+    assert steps == 1 or float(results[1][2].abs().max()) > 0
+    cone = light_cone(conn.n_neurons, conn.pre.numpy(), conn.post.numpy(), np.arange(9), np.arange(100, 120), steps)
+    u_r = torch.tensor(u_in, requires_grad=True)
+    ref = T.cone_grad(b, cone, u_r)
+    ((ref - target.cpu()) ** 2).sum().backward()
+    wants = (ref.detach(), u_r.grad, b.log_gain.grad, b.bias.grad, b.alpha_logit.grad)
+    for got, want, name in zip(results[1], wants, names):
+        want = torch.zeros_like(got.cpu()) if want is None else want     # one step never reaches W
+        _close(got, want, 1e-10, f"{name}: against the oracle")
+    with torch.no_grad():
+        _close(rnn.forward_io(torch.tensor(u_in, device=DEV), in_idx, out_idx, steps), results[1][0], 1e-12,
+               "forward_io without autograd")
+
+
 def test_gather_values_reads_the_weight_vector_at_int32_ids():
     """fly_gather_values: out[i] = w[ids[i]] (a sub-matrix's values in its own or its transpose's order), ids past
     the vector (and negative ones) read 0, bit for bit."""
