@@ -866,9 +866,8 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
               }
             }
           } else {
-          int2 rec = rounds > 0 ? block(0) : make_int2(0, 0);
-          for (int q0 = 0; q0 < rounds; q0 += 8) {
-            const int2 nxt = block(q0 + 8);
+          // one block of 8 rounds: the gathers and sums of records rec (lane s: record q0 + s of its group's row)
+          auto run_block = [&](const int2 rec, int q0) {
             float dl[REPLAY == 4 ? 8 : 1];   // REPLAY 4: this lane's share of each round's dot
 #pragma unroll
             for (int u = 0; u < (REPLAY == 4 ? 8 : 1); ++u) dl[u] = 0.0f;
@@ -909,7 +908,27 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
               const int q = beg + q0 + s;
               if (q < end) __builtin_nontemporal_store(dot, a.dots + (int64_t)c * a.ndots + q);
             }
-            rec = nxt;
+          };
+          // The first blocks' records load together (PRE blocks, 6 VGPRs): vector memory counters retire in order,
+          // so a record load issued during a block's gathers holds up that block's sums, and one shared wait per
+          // slot and band replaces one per block.  Longer bands go on block by block, the next one's load in flight.
+          constexpr int PRE = 3;
+          int2 pre[PRE];
+          static_for<PRE>([&](auto KB) {
+            constexpr int kb = decltype(KB)::value;
+            pre[kb] = kb * 8 < rounds ? block(kb * 8) : make_int2(0, 0);
+          });
+          static_for<PRE>([&](auto KB) {
+            constexpr int kb = decltype(KB)::value;
+            if (kb * 8 < rounds) run_block(pre[kb], kb * 8);
+          });
+          if (rounds > PRE * 8) {
+            int2 rec = block(PRE * 8);
+            for (int q0 = PRE * 8; q0 < rounds; q0 += 8) {
+              const int2 nxt = block(q0 + 8);
+              run_block(rec, q0);
+              rec = nxt;
+            }
           }
           }
         }
