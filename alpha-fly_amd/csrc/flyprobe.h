@@ -69,6 +69,13 @@ int flyprobe_replay_step_io(const int32_t *rowptr_dev, const void *pairs_dev, co
 int flyprobe_random_gather(const void *base_dev, int64_t bytes, int64_t row_bytes, int64_t read_bytes,
                            const int32_t *idx_dev, int64_t n, float *sink_dev, void *stream);
 
+/* The same reads with no index stream: read e of lane group g picks row h < rows by a hash of (g, e, seed), so the
+ * rate is that of the reads alone.  (The index-streamed probe above waits for each index load from memory before
+ * the reads issued after it can be used: vector memory counters retire in order.)  n rounded up to whole waves of
+ * 1,024 reads per lane group. */
+int flyprobe_hashed_gather(const void *base_dev, int64_t bytes, int64_t rows, int64_t row_bytes, int64_t read_bytes,
+                           int64_t n, int64_t seed, float *sink_dev, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,8 +9,11 @@
 // stores: everything but the arithmetic of the sum.
 //
 // flyprobe_random_gather reads rows picked uniformly at random in the same lane layout (8 rows of 128 bytes
-// per wave load, or 16 of 64 bytes): the gather rate of a working set of a given size with no reuse beyond
-// chance, for context.
+// per wave load, or 16 of 64 bytes), their indices streamed from memory one per read: the gather rate of a working
+// set of a given size with no reuse beyond chance.  flyprobe_hashed_gather picks the rows by a hash instead, with no
+// index stream: the chip's own rate of random line reads.  (Vector memory counters retire in order, so an index
+// load from HBM holds up every read issued after it: the index-streamed probe measures that latency, not the
+// reads.)
 #include <string>
 
 #include "flyprobe.h"
@@ -111,6 +114,34 @@ __global__ __launch_bounds__(256) void k_random_gather(const char *base, uint32_
     acc += __uint_as_float(v.x) + __uint_as_float(v.y) + __uint_as_float(v.z) + __uint_as_float(v.w);
   }
   if (acc == 1234.5f) sink[threadIdx.x] = acc;  // keeps the loads alive; a probe over zeros never stores
+}
+
+// Rows picked by a hash of the lane group and round, no index stream: each lane group of 64 / G lanes reads
+// 128 / (G / 8) bytes of row h (16 bytes per lane), 8 reads per group in flight.  h < rows by construction, so every
+// offset lies below rows * row_bytes <= bytes; the buffer resource bounds it again.
+template <int G>
+__global__ __launch_bounds__(256) void k_hashed_gather(const char *base, uint32_t bytes, uint32_t rows,
+                                                       uint32_t row_bytes, uint32_t seed, int rounds,
+                                                       float *__restrict__ sink) {
+  constexpr int LPG = 64 / G;
+  const int lane = threadIdx.x & 63, g = lane / LPG, s = lane % LPG;
+  const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const __amdgpu_buffer_rsrc_t r = buffer_of(base, bytes);
+  uint32_t h = (wave * (uint32_t)G + (uint32_t)g) * 2654435761u + seed;
+  uint32_t fold = 0;
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  for (int k = 0; k < rounds; k += 8) {
+    u4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      h = h * 1664525u + 1013904223u;   // a linear congruential step per read, the same in the group's lanes
+      const uint32_t row = __umulhi(h, rows);
+      v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(row * row_bytes + (uint32_t)s * 16u), 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fold ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  if (fold == 0x9E3779B9u) sink[threadIdx.x] = 1.0f;   // keeps the loads alive
 }
 
 }  // namespace
@@ -266,6 +297,33 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       run(_Float16(0));
     else
       run(0.0f);
+  });
+}
+
+extern "C" int flyprobe_hashed_gather(const void *base, int64_t bytes, int64_t rows, int64_t row_bytes,
+                                      int64_t read_bytes, int64_t n, int64_t seed, float *sink, void *stream) {
+  return probe_guard([&] {
+    FLY_REQUIRE(base && sink, "null argument");
+    FLY_REQUIRE(bytes > 0 && bytes <= INT32_MAX, "the probed buffer must hold 1 .. 2^31-1 bytes");
+    FLY_REQUIRE(read_bytes == 64 || read_bytes == 128, "read_bytes must be 64 or 128");
+    FLY_REQUIRE(row_bytes >= read_bytes && row_bytes < (1 << 24), "row_bytes must be read_bytes .. 2^24-1");
+    FLY_REQUIRE(rows > 0 && rows * row_bytes <= bytes, "rows x row_bytes must fit the buffer");
+    FLY_REQUIRE(n > 0 && n <= (int64_t)1 << 34, "n out of range");
+    const int G = read_bytes == 128 ? 8 : 16;
+    constexpr int kRounds = 1024;   // long-lived waves: 8,192 of them for 2^26 reads
+    const int64_t waves = (n + kRounds * G - 1) / (kRounds * G);
+    FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 64, "probe grid too large");
+    hipStream_t st = as_stream(stream);
+    if (G == 8)
+      hipLaunchKernelGGL(k_hashed_gather<8>, dim3(blocks_for(waves, 4)), dim3(256), 0, st,
+                         static_cast<const char *>(base), (uint32_t)bytes, (uint32_t)rows, (uint32_t)row_bytes,
+                         (uint32_t)seed, kRounds, sink);
+    else
+      hipLaunchKernelGGL(k_hashed_gather<16>, dim3(blocks_for(waves, 4)), dim3(256), 0, st,
+                         static_cast<const char *>(base), (uint32_t)bytes, (uint32_t)rows, (uint32_t)row_bytes,
+                         (uint32_t)seed, kRounds, sink);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error{1, std::string("gather launch: ") + hipGetErrorString(e)};
   });
 }
 

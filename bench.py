@@ -293,6 +293,7 @@ def _probe_lib():
                        ("flyprobe_pack_params", [p, p, i64, p, p]),
                        ("flyprobe_replay_step_io", [p, p, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i32, p, p]),
                        ("flyprobe_random_gather", [p, i64, i64, i64, p, i64, p, p]),
+                       ("flyprobe_hashed_gather", [p, i64, i64, i64, i64, i64, i64, p, p]),
                        ("flyprobe_set_tuning", [ctypes.c_char_p, i64])):
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = i32, args
@@ -454,33 +455,45 @@ def replay_ceiling(plan, cone, n_in: int, batch: int, state_f16: bool, dev, reps
     return out
 
 
-def random_gather_rates(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dict]:
-    """Context for the replay: GB/s of uniformly random 128-byte row reads in the state step's lane layout
-    (flyprobe_random_gather: 8 rows per wave load, 16 bytes per lane) over working sets that fit one XCD's L2
-    (2 MB), the Infinity Cache (21 MB: one 64-column chunk of 166,700 rows) and neither (373 MB), and rows per
-    second over the 21 MB set for 128- and 64-byte reads.  The state step's rows are not uniform (a source row
-    is picked in proportion to its out-degree), so this is no ceiling for it: the replay is."""
+def random_gather_rates(dev, n: int = 1 << 26, reps: int = 5) -> tuple[dict, dict, dict]:
+    """Context for the state step's gathers: GB/s of uniformly random 128-byte row reads in the state step's lane
+    layout (8 rows per wave load, 16 bytes per lane) over working sets that fit one XCD's L2 (2 MB), that are one
+    band of a swept step (41,600 rows: 5.3 MB), one 64-column chunk of 166,700 rows (21 MB, Infinity Cache) and
+    neither (373 MB); rows per second over the 21 MB set for 128- and 64-byte reads.  The rows come from a hash with
+    no index stream (flyprobe_hashed_gather): the chip's rate of random line reads.  The third dict repeats the sets
+    with the row indices streamed from memory, one 4-byte load per read (flyprobe_random_gather): vector memory
+    counters retire in order, so each index load from HBM holds up the reads issued after it, and that probe
+    measures the latency of its own index stream."""
     import torch
     from chessfly import _hip
     probe = _probe_lib()
     sink = torch.zeros(256, device=dev)
     st = _hip.stream(dev)
-    gbps, rows_per_s = {}, {}
-    for name, rows, read in (("l2_2MB", 16384, 128), ("infinity_cache_21MB", 166700, 128),
-                             ("hbm_373MB", 166700 * 35 // 2, 128), ("infinity_cache_21MB_64B", 166700, 64)):
+    gbps, rows_per_s, indexed = {}, {}, {}
+    sets = (("l2_2MB", 16384, 128), ("band_5MB", 41600, 128), ("infinity_cache_21MB", 166700, 128),
+            ("hbm_373MB", 166700 * 35 // 2, 128), ("infinity_cache_21MB_64B", 166700, 64))
+    for name, rows, read in sets:
         base = torch.randint(0, 256, (rows * 128,), dtype=torch.uint8, device=dev)
-        idx = torch.randint(0, rows, (n,), dtype=torch.int32, device=dev)
 
-        def once():
-            _probe_check(probe, probe.flyprobe_random_gather(base.data_ptr(), base.numel(), 128, read, idx.data_ptr(),
-                                                             n, sink.data_ptr(), st), "flyprobe_random_gather")
-        sec = _events_ms(once, reps) * 1e-3
+        def hashed():
+            _probe_check(probe, probe.flyprobe_hashed_gather(base.data_ptr(), base.numel(), rows, 128, read, n, 12345,
+                                                             sink.data_ptr(), st), "flyprobe_hashed_gather")
+        sec = _events_ms(hashed, reps) * 1e-3
         if read == 128:
             gbps[name] = round(n * 128 / sec / 1e9, 1)
         if rows == 166700:
             rows_per_s[f"{read}B"] = round(n / sec / 1e9, 1)
-        del base, idx
-    return gbps, rows_per_s
+        if read == 128:
+            idx = torch.randint(0, rows, (n,), dtype=torch.int32, device=dev)
+
+            def streamed():
+                _probe_check(probe, probe.flyprobe_random_gather(base.data_ptr(), base.numel(), 128, read,
+                                                                 idx.data_ptr(), n, sink.data_ptr(), st),
+                             "flyprobe_random_gather")
+            indexed[name] = round(n * 128 / (_events_ms(streamed, reps) * 1e-3) / 1e9, 1)
+            del idx
+        del base
+    return gbps, rows_per_s, indexed
 
 
 def evaluator_figure(net, dev, x_np, steps: int, legal_per_board: int = 32, download_workgroups: int = 0) -> dict:
@@ -729,30 +742,38 @@ def main() -> int:
             f"{tot_step:.3f} ms of state steps (per step t, replay, replay_io, step: "
             f"{[(r['t'], r['replay_ms'], r['replay_io_ms'], r['step_ms']) for r in rows]})")
     if not args.no_gather_ceiling:
-        rates, rows_per_s = random_gather_rates(dev)
+        rates, rows_per_s, indexed = random_gather_rates(dev)
         roofline["random_gather_GBps"] = rates
         roofline["random_gather_rows_per_s_21MB_G"] = rows_per_s
-        log(f"uniform random-row gathers {rates} GB/s; state step gathers at {roofline['gather_GBps']} GB/s")
+        roofline["random_gather_indexed_GBps"] = indexed
+        log(f"uniform random-row gathers {rates} GB/s (index stream from memory: {indexed}); state step gathers at "
+            f"{roofline['gather_GBps']} GB/s")
         # The line rate: the state step moves one 128-byte line of the previous state per non-zero and chunk of
         # columns (64 of the float16 state, 32 of float32); against the rate of uniformly random 128-byte reads
-        # from an L2-resident set in the same lane layout, the fastest such reads run on this chip.
+        # from an L2-resident set in the same lane layout with no index stream, the fastest such reads run on this
+        # chip, and against the same reads over a set the size of one band of a swept step.
         per_line = 128 // state_bytes
         chunks = -(-args.batch // per_line)
         lines = sum(cone.nnz) * chunks
         step_fwd_ms = avg_launch_ms * launches_per_fwd
         probe = rates["l2_2MB"] * 1e9 / 128
+        band = rates["band_5MB"] * 1e9 / 128
         line_rate = {"lines_per_forward": int(lines), "achieved_G_lines_per_s": round(lines / (step_fwd_ms * 1e-3) / 1e9, 2),
-                     "l2_probe_G_lines_per_s": round(probe / 1e9, 2),
-                     "frac": round(lines / (step_fwd_ms * 1e-3) / probe, 4), "per_step": []}
+                     "l2_probe_G_lines_per_s": round(probe / 1e9, 2), "band_probe_G_lines_per_s": round(band / 1e9, 2),
+                     "frac": round(lines / (step_fwd_ms * 1e-3) / probe, 4),
+                     "frac_of_band_probe": round(lines / (step_fwd_ms * 1e-3) / band, 4), "per_step": []}
         for t, ms in per_step.items():
             n_t = cone.nnz[t] * chunks
             if n_t:
                 line_rate["per_step"].append({"t": t, "lines": int(n_t), "ms": round(ms, 4),
                                               "G_lines_per_s": round(n_t / (ms * 1e-3) / 1e9, 2),
-                                              "frac": round(n_t / (ms * 1e-3) / probe, 4)})
+                                              "frac": round(n_t / (ms * 1e-3) / probe, 4),
+                                              "frac_of_band_probe": round(n_t / (ms * 1e-3) / band, 4)})
         line_rate["note"] = ("gathered 128-byte lines (non-zeros x column chunks) per second of state step, against "
-                             "uniformly random 128-byte reads over a 2 MB (L2-resident) set in the same lane layout "
-                             "(flyprobe_random_gather); frac stays on lines, roofline.frac on algorithmic bytes")
+                             "uniformly random 128-byte reads in the same lane layout with no index stream "
+                             "(flyprobe_hashed_gather) over a 2 MB (L2-resident) set (frac) and over a set the size of "
+                             "one band of a swept step, 5.3 MB (frac_of_band_probe); frac stays on lines, roofline.frac "
+                             "on algorithmic bytes")
         roofline["line_rate"] = line_rate
         log(f"line rate: {line_rate['achieved_G_lines_per_s']} G lines/s of state step against "
             f"{line_rate['l2_probe_G_lines_per_s']} for L2-resident random reads ({line_rate['frac']:.3f}); "

@@ -97,6 +97,7 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     probe.flyprobe_last_error.restype = ctypes.c_char_p
     i64, p_ = ctypes.c_int64, ctypes.c_void_p
     probe.flyprobe_random_gather.argtypes = [p_, i64, i64, i64, p_, i64, p_, p_]
+    probe.flyprobe_hashed_gather.argtypes = [p_, i64, i64, i64, i64, i64, i64, p_, p_]
     i32 = ctypes.c_int32
     probe.flyprobe_replay_step.argtypes = [p_, p_, i64, i64, p_, i64, i64, i64, i32, p_, p_, p_]
     assert probe.flyprobe_random_gather(None, 1024, 128, 128, None, 10, None, None) == 1
@@ -106,6 +107,12 @@ def test_probe_library_is_apart_and_checks_arguments_on_host():
     assert probe.flyprobe_random_gather(p, 1024, 64, 128, p, 10, p, None) == 1
     assert b"row_bytes" in probe.flyprobe_last_error()
     assert probe.flyprobe_random_gather(p, 1024, 128, 96, p, 10, p, None) == 1
+    assert b"read_bytes" in probe.flyprobe_last_error()
+    assert probe.flyprobe_hashed_gather(None, 1024, 8, 128, 128, 10, 1, p, None) == 1
+    assert b"null" in probe.flyprobe_last_error()
+    assert probe.flyprobe_hashed_gather(p, 1024, 9, 128, 128, 10, 1, p, None) == 1
+    assert b"fit" in probe.flyprobe_last_error()
+    assert probe.flyprobe_hashed_gather(p, 1024, 8, 128, 96, 10, 1, p, None) == 1
     assert b"read_bytes" in probe.flyprobe_last_error()
     assert probe.flyprobe_replay_step(None, None, 10, 10, None, 10, 64, 64, 1, None, None, None) == 1
     assert b"null" in probe.flyprobe_last_error()
