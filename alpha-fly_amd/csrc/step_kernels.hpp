@@ -912,8 +912,10 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           // The first blocks' records load together (PRE blocks, 6 VGPRs): vector memory counters retire in order,
           // so a record load issued during a block's gathers holds up that block's sums, and one shared wait per
           // slot and band replaces one per block.  Longer bands go on block by block, the next one's load in flight.
-          constexpr int PRE = 3;
-          int2 pre[PRE];
+          // (The training backward's pass, whose dots hold more registers, keeps the next block's load in flight
+          // from the start instead: 3 blocks spill there.)
+          constexpr int PRE = REPLAY == 4 ? 0 : 3;
+          int2 pre[PRE > 0 ? PRE : 1];
           static_for<PRE>([&](auto KB) {
             constexpr int kb = decltype(KB)::value;
             pre[kb] = kb * 8 < rounds ? block(kb * 8) : make_int2(0, 0);
