@@ -520,11 +520,8 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
           const int32_t e = max(min(beg + k + s, end - 1), 0);
           return a.colval[e];
         };
-        // (the next block loads unconditionally, clamped, so no branch makes the wave drain its loads; slots past
-        // a row's end gather at an offset past the buffer, which reads zeros without touching memory)
-        int2 rec = len > 0 ? block(0) : make_int2(0, 0);
-        for (int32_t k = 0; k < len; k += 8) {
-          const int2 nxt = block(k + 8);
+        // one block of 8 rounds: the gathers and sums of records rec (lane s: record k + s of its group's row)
+        auto run = [&](const int2 rec, int32_t k) {
           static_for<8 / UNROLL>([&](auto H) {
             constexpr int h0 = decltype(H)::value * UNROLL;
             typename Lanes<S, V>::vec xr[UNROLL];
@@ -548,7 +545,23 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
               }
             }
           });
-          rec = nxt;
+        };
+        // The first two blocks' records load together (a row slot's rows average a few non-zeros, so most waves
+        // need one or two blocks): vector memory counters retire in order, and a record load issued among a
+        // block's gathers would hold up their sums.  Longer rows go on block by block, the next one's load in
+        // flight (it loads unconditionally, clamped, so no branch makes the wave drain its loads; slots past a
+        // row's end gather at an offset past the buffer, which reads zeros without touching memory).
+        const int2 r0 = len > 0 ? block(0) : make_int2(0, 0);
+        const int2 r1 = len > 8 ? block(8) : r0;
+        if (len > 0) run(r0, 0);
+        if (len > 8) run(r1, 8);
+        if (len > 16) {
+          int2 rec = block(16);
+          for (int32_t k = 16; k < len; k += 8) {
+            const int2 nxt = block(k + 8);
+            run(rec, k);
+            rec = nxt;
+          }
         }
       }
     }
