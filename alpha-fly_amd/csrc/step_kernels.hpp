@@ -49,14 +49,20 @@ struct Lanes {
 #pragma unroll
     for (int i = 0; i < V; ++i) f[i] = static_cast<float>(v[i]);
   }
-  static __device__ __forceinline__ void store(S *p, const float (&f)[V], bool nt = false) {
+  static __device__ __forceinline__ vec pack(const float (&f)[V]) {
     vec v;
 #pragma unroll
     for (int i = 0; i < V; ++i) v[i] = static_cast<S>(f[i]);
+    return v;
+  }
+  static __device__ __forceinline__ void store_raw(S *p, const vec &v, bool nt = false) {
     if (nt)
       __builtin_nontemporal_store(v, reinterpret_cast<vec *>(p));
     else
       *reinterpret_cast<vec *>(p) = v;
+  }
+  static __device__ __forceinline__ void store(S *p, const float (&f)[V], bool nt = false) {
+    store_raw(p, pack(f), nt);
   }
 };
 
@@ -68,11 +74,15 @@ struct Lanes<S, 1> {
   static __device__ __forceinline__ vec zero() { return static_cast<S>(0.0f); }
   static __device__ __forceinline__ float at(const vec &v, int) { return static_cast<float>(v); }
   static __device__ __forceinline__ void load(const S *p, float (&f)[1]) { f[0] = static_cast<float>(*p); }
-  static __device__ __forceinline__ void store(S *p, const float (&f)[1], bool nt = false) {
+  static __device__ __forceinline__ vec pack(const float (&f)[1]) { return static_cast<S>(f[0]); }
+  static __device__ __forceinline__ void store_raw(S *p, const vec &v, bool nt = false) {
     if (nt)
-      __builtin_nontemporal_store(static_cast<S>(f[0]), p);
+      __builtin_nontemporal_store(v, p);
     else
-      *p = static_cast<S>(f[0]);
+      *p = v;
+  }
+  static __device__ __forceinline__ void store(S *p, const float (&f)[1], bool nt = false) {
+    store_raw(p, pack(f), nt);
   }
 };
 
@@ -228,12 +238,11 @@ __device__ __forceinline__ void load_row_inputs(const StepArgs<S, U> &a, uint32_
 
 // Input drive, clamp and leaky update of V columns of one row, then the store.
 template <typename S, typename U, int V, bool TORCH_LERP>
-__device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V],
-                                           RowInputs<S, U, V> &in) {
+__device__ __forceinline__ void finish_value(const StepArgs<S, U> &a, int64_t col, const float (&acc)[V],
+                                             RowInputs<S, U, V> &in, float (&out)[V]) {
   keep_opaque(in.u);
   keep_opaque(in.pv);
   const RowParam &p = in.p;
-  float out[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const float pv = in.carried ? Lanes<S, V>::at(in.pv, i) : p.pdef;
@@ -241,6 +250,13 @@ __device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row
     const float x = fminf(fmaxf((acc[i] + u) + p.k, p.lo), p.hi) + p.e;
     out[i] = TORCH_LERP ? lerp_torch(pv, x, p.a) : fmaf(p.a, x - pv, pv);
   }
+}
+
+template <typename S, typename U, int V, bool TORCH_LERP>
+__device__ __forceinline__ void finish_row(const StepArgs<S, U> &a, uint32_t row, int64_t col, const float (&acc)[V],
+                                           RowInputs<S, U, V> &in) {
+  float out[V];
+  finish_value<S, U, V, TORCH_LERP>(a, col, acc, in, out);
   Lanes<S, V>::store(a.xout + (int64_t)row * a.ldo + col, out, a.nt_store != 0);
 }
 
@@ -965,6 +981,22 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
         // Batches of 3, or of 2 when 6 slots' sums share the registers with 32-byte drive vectors (float32 drive
         // of a half state), which would otherwise spill.
         constexpr int EB = (SLOTS == 6 && V * sizeof(U) > 16) ? 2 : (SLOTS % 3 == 0 ? 3 : 1);
+        // A batch's new states are stored after the next batch's loads are issued: vector memory counters retire
+        // in order, so the next batch's epilogue then waits for its own loads and not for these stores.  (Not
+        // with 6 slots of a half state and half drive, whose batches of 3 rows would spill the held states.)
+        constexpr bool DEFER = (REPLAY == 0 || REPLAY == 2) && !(sizeof(S) == 2 && sizeof(U) == 2 && SLOTS == 6);
+        constexpr int NP = DEFER ? EB : 1;
+        typename Lanes<S, V>::vec pend[NP];
+        int prow[NP];
+#pragma unroll
+        for (int u = 0; u < NP; ++u) prow[u] = -1;
+        auto flush = [&]() {
+#pragma unroll
+          for (int u = 0; u < NP; ++u) {
+            if (prow[u] >= 0) Lanes<S, V>::store_raw(a.xout + (int64_t)prow[u] * a.ldo + col, pend[u], a.nt_store != 0);
+            prow[u] = -1;
+          }
+        };
         static_for<SLOTS / EB>([&](auto H) {
           constexpr int j0 = decltype(H)::value * EB;
           int rs[EB];
@@ -978,6 +1010,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
               load_row_drive(a, col, rs[u] >= 0 && rs[u] < a.nrows, in[u]);
             }
           });
+          if constexpr (DEFER) flush();
           static_for<EB>([&](auto J) {
             constexpr int u = decltype(J)::value;
             if (rs[u] >= a.nrows) {   // a piece of a split row: its raw sums
@@ -998,11 +1031,19 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
                 Lanes<S, V>::store(dst, acc[j0 + u]);
               } else {
                 if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc[j0 + u], bits);
-                finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j0 + u], in[u]);
+                if constexpr (DEFER) {
+                  float out[V];
+                  finish_value<S, U, V, TORCH_LERP>(a, col, acc[j0 + u], in[u], out);
+                  pend[u % NP] = Lanes<S, V>::pack(out);
+                  prow[u % NP] = (int)rj;
+                } else {
+                  finish_row<S, U, V, TORCH_LERP>(a, rj, col, acc[j0 + u], in[u]);
+                }
               }
             }
           });
         });
+        if constexpr (DEFER) flush();
       }
     }
   }
