@@ -231,6 +231,11 @@ struct fly_plan {
   // fly_sweep of the whole matrix); null for the other steps.
   std::vector<std::shared_ptr<const fly::SweepTables>> sweep;
   int64_t max_pieces = 0;   // the most pieces of split rows in any swept step (their sums take workspace)
+  // Steps of short rows (row slots of 8 rows): the slots holding a row far longer than the mean run first
+  // (fly::build_lead_slots); empty where there are none.
+  std::vector<fly::DevArray<int32_t>> lead;
+  std::vector<fly::DevArray<uint8_t>> lead_flag;
+  std::vector<int32_t> nlead;
   fly::DevArray<int32_t> out_src;  // position of out_idx[j] in R_T or -1
   fly::DevArray<float> cbase;      // value added to the carried state at the outputs
   fly::DevArray<float> c_out;      // c_T[out_idx]

@@ -246,6 +246,9 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
     plan->colval.resize(T + 1);
     plan->params.resize(T + 1);
     plan->sweep.resize(T + 1);
+    plan->lead.resize(T + 1);
+    plan->lead_flag.resize(T + 1);
+    plan->nlead.assign(T + 1, 0);
     plan->tune = tuning_snapshot();
     const SweepConfig cfg = sweep_config(plan->tune);
 
@@ -268,6 +271,12 @@ extern "C" int fly_plan_create(const fly_cone *cone, const int32_t *crow, const 
         if (plan->tune.swept >= 0) {
           plan->sweep[t] = cone_sweep(*cone, t, cfg, st);
           if (plan->sweep[t]) plan->max_pieces = std::max(plan->max_pieces, plan->sweep[t]->pieces);
+        }
+        if (cone->nnz[t] < 16 * nr) {   // short rows on average: the step runs as row slots
+          LeadSlots ls = build_lead_slots(plan->rowptr[t].p, nr, cone->nnz[t], st);
+          plan->lead[t] = std::move(ls.lead);
+          plan->lead_flag[t] = std::move(ls.flag);
+          plan->nlead[t] = ls.n;
         }
       }
       if (nr) {
@@ -336,6 +345,9 @@ extern "C" int fly_plan_create_full(int64_t n, int64_t n_edges, const int32_t *c
                        plan->params[0].p);
     plan->tune = tuning_snapshot();
     plan->sweep.resize(1);
+    plan->lead.resize(1);
+    plan->lead_flag.resize(1);
+    plan->nlead.assign(1, 0);
     if (sweep && sweep->t && plan->tune.swept >= 0) {
       FLY_REQUIRE(sweep->device == plan->device, "the sweep tables live on another device");
       FLY_REQUIRE(sweep->t->nrows == n && sweep->t->ncols == n && sweep->t->nnz == n_edges,

@@ -14,7 +14,10 @@
 // index stream: the chip's own rate of random line reads.  (Vector memory counters retire in order, so an index
 // load from HBM holds up every read issued after it: the index-streamed probe measures that latency, not the
 // reads.)
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 
 #include "flyprobe.h"
 #include "step_kernels.hpp"
@@ -59,6 +62,22 @@ __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__res
   if (q < nnz) out[q] = make_int2(col[q], __float_as_int(val[q]));
 }
 
+// The lead slots the evaluator's plan builds for a step matrix (build_lead_slots), kept per matrix so that repeated
+// replays of one step launch without a host synchronisation after the first.
+const LeadSlots &lead_slots_of(const int32_t *rowptr, int64_t nrows, int64_t nnz, hipStream_t st) {
+  static std::mutex mu;
+  static std::map<std::tuple<const int32_t *, int64_t, int64_t>, LeadSlots> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(rowptr, nrows, nnz);
+  auto it = cache.find(key);
+  if (it == cache.end()) {
+    LeadSlots ls;
+    if (nnz < 16 * nrows) ls = build_lead_slots(rowptr, nrows, nnz, st);   // the plan's rule: short rows on average
+    it = cache.emplace(key, std::move(ls)).first;
+  }
+  return it->second;
+}
+
 // The evaluator's default shapes only (no tuning knobs): the banded sweep where the evaluator runs one (the caller
 // passes the band table of flyprobe_band_table then), else lane groups of 16-byte lanes, or row slots of 16- or
 // 32-byte lanes, in groups of 8 lanes with 4 rounds in flight.
@@ -71,7 +90,12 @@ void replay(StepArgs<S, U> a, int64_t nnz, const SweepTables *sweep, hipStream_t
     if (e != hipSuccess) throw Error{1, std::string("replay launch: ") + hipGetErrorString(e)};
     return;
   }
-  const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
+  if (!(sh.rows_mode && sh.groups == 8 && a.wpt == 1 && a.lead && a.lead_flag && a.slots == (a.nrows + 7) / 8)) {
+    a.lead = nullptr;   // lead slots exist for row slots of 8 rows, one chunk per tile (as the evaluator runs them)
+    a.lead_flag = nullptr;
+    a.nlead = 0;
+  }
+  const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles + (int64_t)a.nlead * a.ntiles;
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "replay grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   constexpr int kV16 = 16 / (int)sizeof(S);
@@ -228,6 +252,12 @@ extern "C" int flyprobe_replay_step(const int32_t *rowptr, const void *pairs, in
       using S = decltype(zero);
       StepArgs<S, S> a{};
       a.rowptr = rowptr;
+      {
+        const LeadSlots &ls = lead_slots_of(rowptr, nrows, nnz, as_stream(stream));
+        a.lead = ls.lead.p;
+        a.lead_flag = ls.flag.p;
+        a.nlead = ls.n;
+      }
       a.colval = static_cast<const int2 *>(pairs);
       a.params = nullptr;
       a.xprev = static_cast<const S *>(xprev);
@@ -276,6 +306,12 @@ extern "C" int flyprobe_replay_step_io(const int32_t *rowptr, const void *pairs,
       using S = decltype(zero);
       StepArgs<S, float> a{};
       a.rowptr = rowptr;
+      {
+        const LeadSlots &ls = lead_slots_of(rowptr, nrows, nnz, as_stream(stream));
+        a.lead = ls.lead.p;
+        a.lead_flag = ls.flag.p;
+        a.nlead = ls.n;
+      }
       a.colval = static_cast<const int2 *>(pairs);
       a.params = static_cast<const RowParam *>(params);
       a.xprev = static_cast<const S *>(xprev);

@@ -27,7 +27,7 @@ namespace {
 // with torch.lerp's formula, like the reference's CPU path.
 template <typename S, typename U, int V>
 void launch_v(const StepArgs<S, U> &a, int groups, int unroll, bool rows_mode, int step_lds, hipStream_t st) {
-  const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles;
+  const int64_t waves = (int64_t)a.slots * a.wpt * a.ntiles + (int64_t)a.nlead * a.ntiles;   // lead slots first
   FLY_REQUIRE(waves < (int64_t)UINT32_MAX / 2, "state step grid too large");
   const dim3 grid(blocks_for(waves, 4)), block(256);
   LaunchTimer timer(FLY_K_STATE_STEP, st);
@@ -83,6 +83,12 @@ void state_step(StepArgs<S, U> a, double avg_nnz, const Tuning &tune, const Swee
   const StepShape sh = shape_step(a, avg_nnz, tu);
   const int v = sh.v, groups = sh.groups, unroll = sh.unroll;
   const bool rows_mode = sh.rows_mode;
+  // lead slots are tables of slots of 8 rows, taken one chunk per tile
+  if (!(rows_mode && groups == 8 && a.wpt == 1 && a.lead && a.lead_flag && a.slots == (a.nrows + 7) / 8)) {
+    a.lead = nullptr;
+    a.lead_flag = nullptr;
+    a.nlead = 0;
+  }
   // long-row steps with sweep tables: the banded sweep, on the grouped kernel's lane layout
   if (sweep && tune.swept >= 0 && v == 16 / (int)sizeof(S) && groups == 8 && !rows_mode && a.rowptr && a.xprev &&
       a.xbytes && !(a.out_exact && a.batch % v)) {
@@ -269,6 +275,9 @@ const S *run_cone_steps(const fly_plan &plan, const U *u, int64_t ldu, int64_t b
     a.rowptr = plan.rowptr[t].p;  // null where A_t does not exist
     a.colval = plan.colval[t].p;
     a.params = plan.params[t].p;
+    a.lead = plan.lead[t].p;
+    a.lead_flag = plan.lead_flag[t].p;
+    a.nlead = plan.nlead[t];
     a.xprev = prev;
     a.ldx = lds;
     a.u = u;
@@ -563,6 +572,9 @@ extern "C" int fly_plan_step(const fly_plan *plan, int32_t t, const void *xprev,
       a.rowptr = plan->rowptr[ti].p;
       a.colval = plan->colval[ti].p;
       a.params = plan->params[ti].p;
+      a.lead = plan->lead[ti].p;
+      a.lead_flag = plan->lead_flag[ti].p;
+      a.nlead = plan->nlead[ti];
       a.xprev = xp;
       a.ldx = ldx;
       a.u = u;

@@ -126,6 +126,10 @@ struct StepArgs {
   int64_t ndots;
   const int32_t *piece_row;    // (pieces): the row each piece of a split row belongs to
   int32_t accumulate;          // REPLAY 3 and 4: add the sums to xout instead of storing them
+  // row slots of 8 rows: the lead slots (holding a row far longer than the mean) run first, for every chunk
+  const int32_t *lead;         // (nlead) the lead slots, rising
+  const uint8_t *lead_flag;    // (slots) 1 for a lead slot
+  int32_t nlead;               // 0: none (and whenever the launch is not row slots of 8 rows, one chunk per tile)
 };
 
 // Wave -> (row, chunk of TW batch columns).  Waves are numbered (tile, row, chunk-in-tile) so a tile of
@@ -143,6 +147,23 @@ __device__ __forceinline__ WaveSlot wave_slot(const StepArgs<S, U> &a) {
   const uint32_t in_tile = wave - tile * per_tile;
   const uint32_t row = in_tile / (uint32_t)a.wpt;
   return {row, tile * (uint32_t)a.wpt + (in_tile - row * (uint32_t)a.wpt), tile < (uint32_t)a.ntiles};
+}
+
+// The row-slot kernel's waves: with lead slots, the first nlead x chunks waves take the lead slots for every chunk,
+// so a slot of one very long row (a hub of a heavy-tailed in-degree) starts with the launch instead of running on
+// as a tail after the rest; the chunk-major waves after them skip the lead slots.  (Needs one chunk per tile.)
+template <typename S, typename U>
+__device__ __forceinline__ WaveSlot rows_wave_slot(const StepArgs<S, U> &a) {
+  if (a.nlead <= 0) return wave_slot(a);
+  const uint32_t wave = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t chunks = (uint32_t)a.ntiles, nl = (uint32_t)a.nlead * chunks;
+  if (wave < nl) {
+    const uint32_t i = wave / chunks;
+    return {(uint32_t)a.lead[i], wave - i * chunks, true};
+  }
+  const uint32_t w2 = wave - nl, tile = w2 / (uint32_t)a.slots, slot = w2 - tile * (uint32_t)a.slots;
+  const bool valid = tile < (uint32_t)a.ntiles && a.lead_flag[slot] == 0;
+  return {slot, tile, valid};
 }
 
 // An empty asm that takes v in and out of vector registers: the compiler cannot move v's uses (a conversion, a
@@ -480,7 +501,7 @@ __global__ __launch_bounds__(256) void k_state_step_grouped(const StepArgs<S, U>
 template <typename S, typename U, int V, int G, int UNROLL, bool TORCH_LERP, int REPLAY = 0, bool SHARED = true>
 __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a) {
   constexpr int LPG = 64 / G;
-  const WaveSlot w = wave_slot(a);                // w.row counts slots of G rows
+  const WaveSlot w = rows_wave_slot(a);           // w.row counts slots of G rows
   if (!w.valid) return;
   const int lane = threadIdx.x & 63;
   const int g = lane / LPG, s = lane % LPG;
@@ -1173,6 +1194,56 @@ void launch_swept(StepArgs<S, U> a, const SweepTables &t, hipStream_t st) {
     hipLaunchKernelGGL((k_sweep_finish<S, U, V, sizeof(S) == 4, REPLAY>), fgrid, dim3(256), 0, st, a, t.split.p,
                        t.split_ptr.p, (int32_t)t.split_rows);
   }
+}
+
+// ---- lead row slots --------------------------------------------------------------------------------------
+
+namespace {
+// flag[s] = 1 where a slot of 8 consecutive rows holds a row of more than len non-zeros
+__global__ __launch_bounds__(256) void k_lead_flags(const int32_t *__restrict__ rowptr, int64_t nrows, int64_t slots,
+                                                    int32_t len, uint8_t *__restrict__ flag) {
+  const int64_t sl = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (sl >= slots) return;
+  int32_t longest = 0;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int64_t row = sl * 8 + r;
+    if (row < nrows) longest = max(longest, rowptr[row + 1] - rowptr[row]);
+  }
+  flag[sl] = longest > len ? 1 : 0;
+}
+}  // namespace
+
+struct LeadSlots {
+  DevArray<int32_t> lead;    // the lead slots, rising
+  DevArray<uint8_t> flag;    // (slots of 8 rows) 1 for a lead slot
+  int32_t n = 0;
+};
+
+// The lead slots of a step matrix (rowptr, nrows + 1) whose rows run as slots of 8 rows: those holding a row of more
+// than max(64, 8 x the mean) non-zeros (on the real connectome's in-degrees, step 2's rows average 7.6 non-zeros
+// and reach 1,008).  Synchronises the stream: the count sizes the launch.  None (n = 0) for an empty matrix.
+inline LeadSlots build_lead_slots(const int32_t *rowptr, int64_t nrows, int64_t nnz, hipStream_t st) {
+  LeadSlots out;
+  if (!rowptr || nrows <= 0 || nnz <= 0) return out;
+  const int64_t slots = (nrows + 7) / 8;
+  const int32_t len = (int32_t)std::min<int64_t>(INT32_MAX, std::max<int64_t>(64, 8 * nnz / nrows));
+  DevArray<uint8_t> flag(slots);
+  hipLaunchKernelGGL(k_lead_flags, dim3(blocks_for(slots, 256)), dim3(256), 0, st, rowptr, nrows, slots, len, flag.p);
+  FLY_HIP(hipGetLastError());
+  std::vector<uint8_t> hf(slots);
+  FLY_HIP(hipMemcpyAsync(hf.data(), flag.p, (size_t)slots, hipMemcpyDeviceToHost, st));
+  FLY_HIP(hipStreamSynchronize(st));
+  std::vector<int32_t> list;
+  for (int64_t i = 0; i < slots; ++i)
+    if (hf[i]) list.push_back((int32_t)i);
+  if (list.empty()) return out;
+  out.lead.alloc(list.size());
+  FLY_HIP(hipMemcpyAsync(out.lead.p, list.data(), sizeof(int32_t) * list.size(), hipMemcpyHostToDevice, st));
+  FLY_HIP(hipStreamSynchronize(st));   // the host list is a temporary
+  out.flag = std::move(flag);
+  out.n = (int32_t)list.size();
+  return out;
 }
 
 template <typename S>
