@@ -771,6 +771,8 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
       for (int j = 0; j < SLOTS; ++j)
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[j][i] = 0.0f;
+      // slot 0's first records of the next band, loaded with the band's last slot (see below)
+      int2 pre_next[3];
       static_for<K>([&](auto B) {
         constexpr int b = decltype(B)::value;
         if constexpr (PAIRED) {
@@ -966,10 +968,38 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           // from the start instead: 3 blocks spill there.)
           constexpr int PRE = REPLAY == 4 ? 0 : 3;
           int2 pre[PRE > 0 ? PRE : 1];
-          static_for<PRE>([&](auto KB) {
-            constexpr int kb = decltype(KB)::value;
-            pre[kb] = kb * 8 < rounds ? block(kb * 8) : make_int2(0, 0);
-          });
+          if (PRE > 0 && b > 0 && j == 0) {
+            // loaded with the previous band's last slot, so the wait for them is not the first thing after the
+            // workgroup's barrier
+#pragma unroll
+            for (int kb = 0; kb < (PRE > 0 ? PRE : 1); ++kb) pre[kb] = pre_next[kb];
+          } else {
+            static_for<PRE>([&](auto KB) {
+              constexpr int kb = decltype(KB)::value;
+              pre[kb] = kb * 8 < rounds ? block(kb * 8) : make_int2(0, 0);
+            });
+          }
+          if constexpr (PRE == 3 && b + 1 < K) {
+            if (j == SLOTS - 1) {   // slot 0's first records of the next band, issued with this slot's own
+              int nb = group_bcast<8, 2 * (b + 1)>(off[0]), ne = group_bcast<8, 2 * (b + 1) + 1>(off[0]);
+              if (lf[0]) {
+                const int n = ne - nb, p = g & ((1 << lf[0]) - 1), b0 = nb;
+                nb = b0 + ((n * p) >> lf[0]);
+                ne = b0 + ((n * (p + 1)) >> lf[0]);
+              }
+              const int r1 = wave_max_of_groups(ne - nb);
+              static_for<3>([&](auto KB) {
+                constexpr int kb = decltype(KB)::value;
+                if (kb * 8 < r1) {
+                  const int q = nb + kb * 8 + s;
+                  const int2 rc = a.colval[max(min(q, ne - 1), 0)];
+                  pre_next[kb] = q < ne ? rc : make_int2((int)past_row, 0);
+                } else {
+                  pre_next[kb] = make_int2(0, 0);
+                }
+              });
+            }
+          }
           static_for<PRE>([&](auto KB) {
             constexpr int kb = decltype(KB)::value;
             if (kb * 8 < rounds) run_block(pre[kb], kb * 8);
