@@ -683,7 +683,9 @@ __device__ __forceinline__ int wave_max_of_groups(int v) {
 // the row past the buffer (zeros, no memory access); a slot of 4 rows or fewer spreads each row over several lane
 // groups.  PAIRED walks two slots' rows per pass (1: the other row's weight is zero, for states that hold no inf
 // or NaN; 2: only the owning row's sums change).  PIPE keeps the next four rounds' gathers in flight during the
-// sums.  REPLAY as for the other step kernels, and 3: the product alone, each row's sums stored to xout (float32
+// sums.  Vector memory counters retire in order, so every load is placed where waiting for it costs nothing extra:
+// a slot's first record blocks load together, the next band's first records load with a band's last slot, and the
+// epilogue stores a batch's new states after the next batch's row reads.  REPLAY as for the other step kernels, and 3: the product alone, each row's sums stored to xout (float32
 // states; the training forward's A x); 4: the training backward's pass over A^T, the product grad_h = A^T grad_y
 // added to xout and, per record and chunk, the dot of the gathered line of grad_y with the row's own h_{t-1}
 // (hdot) stored to dots (dL/dw's share of the chunk).
@@ -852,7 +854,7 @@ __global__ __launch_bounds__(1024, 1) void k_state_step_swept(const StepArgs<S, 
           }
           const int rounds = wave_max_of_groups(end - beg);
           // lane s brings record q0 + s of its row's band (clamped into the row), and round q reaches the group's
-          // lanes by a broadcast of lane q; the next block of 8 loads while this one's gathers are in flight
+          // lanes by a broadcast of lane q (the first blocks of a slot load together, below)
           auto block = [&](int q0) {
             const int q = beg + q0 + s;
             const int2 rc = a.colval[max(min(q, end - 1), 0)];
