@@ -1,8 +1,8 @@
 """GPU parity for the benchmark workloads and call paths beyond the headline forward: the shuffled control graph
 (repeated pairs and self-loops summed), the unpruned float16-deviation and float32 forwards, 20-40-ones boards at
-B = 256, the attack-plane encoder, the factorised policy head, unbounded activity (h_max=None) and the per-step
-export fly_plan_step, each against the CPU oracle (or, for the policy head, the layer-by-layer path) through the
-C ABI.
+B = 256, the attack-plane encoder, the factorised policy head, unbounded activity (h_max=None), hub rows in a step
+of short rows and the per-step export fly_plan_step, each against the CPU oracle (or, for the policy head, the
+layer-by-layer path) through the C ABI.
 
 Tolerances: float32 paths within float32 round-off of the float64 oracle (2e-5); full models within 1e-3 max-abs
 of the oracle's float32 forward with the argmax equal; the float16 deviation path against the exact function
@@ -433,6 +433,53 @@ def test_other_activity_bounds_literal_and_light_cone(sweep_core):
 
 
 # ---- fly_plan_step: one step at a time ---------------------------------------------------------------------------
+
+def _with_hubs(conn, n_hubs=3):
+    """conn plus, into each of n_hubs intrinsic neurons, an edge from every sensory neuron it does not already hear
+    (4 synapses, the presynaptic neuron's sign): rows of step 2 far longer than the mean."""
+    from chessfly.connectome import Connectome
+    n = conn.n_neurons
+    pre, post = conn.pre.numpy(), conn.post.numpy()
+    sens, hubs = conn.nodes("afferent").numpy(), conn.nodes("intrinsic").numpy()[:n_hubs]
+    have = set(zip(post.tolist(), pre.tolist()))
+    extra = np.array([(h, s_) for h in hubs for s_ in sens if (h, s_) not in have and h != s_], dtype=np.int64)
+    sign_of = np.ones(n, dtype=np.float32)
+    sign_of[pre] = conn.sign.numpy()
+    new_post = np.concatenate([post, extra[:, 0]])
+    new_pre = np.concatenate([pre, extra[:, 1]])
+    syn = np.concatenate([conn.syn_count.numpy(), np.full(len(extra), 4.0, dtype=np.float32)])
+    order = np.lexsort((new_pre, new_post))
+    return Connectome(conn.neurons, torch.as_tensor(new_pre[order]), torch.as_tensor(new_post[order]),
+                      torch.as_tensor(syn[order]), torch.as_tensor(sign_of[new_pre[order]]))
+
+
+@pytest.mark.parametrize("batch", [100, 1120])
+def test_hub_rows_in_a_step_of_short_rows_match_the_oracle(batch):
+    """A step of short rows (row slots of 8 rows) holding a few rows far longer than the mean: three neurons hear
+    every sensory neuron, so step 2's rows average a few non-zeros and theirs about 300, past the rule by which the
+    plan runs their slots first for every chunk (more than max(64, 8 x the mean) non-zeros).  forward_io in
+    float32 against the float64 oracle (2e-5) and the float16 deviation path against the exact function (the
+    float16 bound of the other tests), at one chunk of columns and at several."""
+    conn = _with_hubs(_medium(7))
+    lg, b, al = random_params(conn, 23, gain_sd=0.1)
+    rnn = _rnn(conn, 4.0, lg, b, al)
+    ba = brain_arrays(conn, 4.0, lg, b, al, dtype=torch.float64)
+    in_idx, out_idx = conn.nodes("afferent"), conn.nodes("efferent")
+    cone = _cone(conn, in_idx, out_idx, 6)
+    lens = np.diff(cone.ops[2].crow)
+    assert lens.mean() < 16 and lens.max() > max(64, 8 * lens.sum() // len(lens)), (lens.mean(), lens.max())
+    u_in = torch.randn(len(in_idx), batch, generator=torch.Generator().manual_seed(batch)) * 0.5
+    exact = F.cone_f32(ba, cone, u_in.double(), 6).numpy()
+    ind, outd = in_idx.to(DEV), out_idx.to(DEV)
+    with torch.no_grad():
+        out32 = rnn.forward_io(u_in.to(DEV), ind, outd, 6)
+        out16 = rnn.forward_io(u_in.half().to(DEV), ind, outd, 6)
+    np.testing.assert_allclose(out32.cpu().numpy(), exact, rtol=2e-5, atol=2e-5 * np.abs(exact).max())
+    exact16 = F.cone_f32(ba, cone, u_in.half().double(), 6).numpy()
+    dev_scale = np.abs(exact16 - F.cone_f32(ba, cone, torch.zeros_like(u_in).double(), 6).numpy()).max()
+    err = np.abs(out16.cpu().numpy() - exact16).max()
+    assert err < 2e-3 * max(dev_scale, 1e-3), (err, dev_scale)
+
 
 def _plan_step(lib, _hip, plan, t, xprev, u, batch, xout):
     ws = _hip.workspace(lib.fly_plan_step_workspace(plan.handle, t, batch), torch.device(DEV))
