@@ -633,20 +633,25 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
     float dot[R], acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < R; ++r) dot[r] = 0.0f;
-#pragma unroll
-    for (int r0 = 0; r0 < R; r0 += 4) {
-      // wave-uniform: a group of 16 non-zeros wholly past the segment's end is not loaded; inside the last
-      // group the slots past the end read column 0 with weight 0
-      if (blk + 4 * r0 >= n) break;
-      int32_t c[4];
-      float w[4];
-      float4 x[4];
+    // Each round's records load right after the previous round's gathers: vector memory counters retire in order,
+    // so the previous round's sums wait only for its gathers, and the records have those sums to arrive.
+    // Wave-uniform: a group of 16 non-zeros wholly past the segment's end is not loaded; inside the last group the
+    // slots past the end read column 0 with weight 0.
+    auto records = [&](int r0, int32_t (&c)[4], float (&w)[4]) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int off = (blk + 4 * (r0 + q) + g) * 4;
         c[q] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
         w[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
       }
+    };
+    int32_t c[4] = {0, 0, 0, 0};
+    float w[4] = {0.f, 0.f, 0.f, 0.f};
+    if (blk < n) records(0, c, w);
+#pragma unroll
+    for (int r0 = 0; r0 < R; r0 += 4) {
+      if (blk + 4 * r0 >= n) break;
+      float4 x[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -654,6 +659,9 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
             rgy, (int)(__umul24((uint32_t)c[q], gy_row) + coff), 0, 0);
         x[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
       }
+      int32_t cn[4] = {0, 0, 0, 0};
+      float wn[4] = {0.f, 0.f, 0.f, 0.f};
+      if (r0 + 4 < R && blk + 4 * (r0 + 4) < n) records(r0 + 4, cn, wn);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         acc[0] = fmaf(w[q], x[q].x, acc[0]);
@@ -661,6 +669,11 @@ __global__ __launch_bounds__(256) void k_transposed_backward_chunks(const Transp
         acc[2] = fmaf(w[q], x[q].z, acc[2]);
         acc[3] = fmaf(w[q], x[q].w, acc[3]);
         dot[r0 + q] = fmaf(x[q].x, hv.x, fmaf(x[q].y, hv.y, fmaf(x[q].z, hv.z, x[q].w * hv.w)));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        c[q] = cn[q];
+        w[q] = wn[q];
       }
     }
 #pragma unroll
