@@ -66,14 +66,15 @@ __global__ void k_pack_pairs(const int32_t *__restrict__ col, const float *__res
 // replays of one step launch without a host synchronisation after the first.
 const LeadSlots &lead_slots_of(const int32_t *rowptr, int64_t nrows, int64_t nnz, hipStream_t st) {
   static std::mutex mu;
-  static std::map<std::tuple<const int32_t *, int64_t, int64_t>, LeadSlots> cache;
+  // never destroyed: device memory is not freed from a static destructor, which may run after the HIP runtime's
+  static auto *cache = new std::map<std::tuple<const int32_t *, int64_t, int64_t>, LeadSlots>();
   std::lock_guard<std::mutex> lock(mu);
   const auto key = std::make_tuple(rowptr, nrows, nnz);
-  auto it = cache.find(key);
-  if (it == cache.end()) {
+  auto it = cache->find(key);
+  if (it == cache->end()) {
     LeadSlots ls;
     if (nnz < 16 * nrows) ls = build_lead_slots(rowptr, nrows, nnz, st);   // the plan's rule: short rows on average
-    it = cache.emplace(key, std::move(ls)).first;
+    it = cache->emplace(key, std::move(ls)).first;
   }
   return it->second;
 }
