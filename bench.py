@@ -9,8 +9,10 @@ FlyChessNet.forward exactly as the search's Evaluator calls it, with the boards 
 One "step" of this benchmark is one forward of the whole batch.  Prints one JSON line on stdout:
 value = B * steps / wall time; `roofline` rates the fused state-step kernel by its compulsory HBM bytes
 (CSR columns and values, per-row constants, previous/new state and input rows, read or written once) over
-its launch time measured with HIP events on its stream; `cpu_baseline` times the reference's CPU path
-(restated in oracle/, the float32 light cone with cached constants) on a bounded sample of the same boards.
+its launch time measured with HIP events on its stream; `roofline.replay` and `roofline.line_rate` set the
+state step beside the replay of its own memory stream and beside the chip's rate of random 128-byte line reads
+(libflyprobe.so); `cpu_baseline` times the reference's CPU path (restated in oracle/, the float32 light cone with
+cached constants) on a bounded sample of the same boards.
 
     python bench.py [--steps K] [--warmup W] [--batch B] [--dtype f16|f32] [--graph synthetic|shuffled|realdeg]
 
