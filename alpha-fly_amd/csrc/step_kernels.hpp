@@ -203,11 +203,14 @@ __device__ __forceinline__ RowParam row_param_from_word(int word) {
   return p;
 }
 
-// The constants of each lane group's row for groups of 8 lanes: lane s reads word s of the 32-byte record and the
-// group's lanes exchange them, one 4-byte load per lane instead of eight lanes each reading all 32 bytes.
+// Word s of the 32-byte constants of each lane group's row, for groups of 8 lanes: lane s reads word s and the
+// group's lanes exchange them (row_param_from_word), one 4-byte load per lane instead of eight lanes each reading
+// all 32 bytes.  Lanes past the step's rows read row crow's word (crow: a row of the step) and drop it, so the
+// load needs no branch.
 template <typename S, typename U>
-__device__ __forceinline__ RowParam row_param_shared8(const StepArgs<S, U> &a, uint32_t row, bool has_row, int s) {
-  return row_param_from_word(has_row ? reinterpret_cast<const int *>(a.params + row)[s] : 0);
+__device__ __forceinline__ int row_param_word(const StepArgs<S, U> &a, uint32_t crow, bool has_row, int s) {
+  const int word = reinterpret_cast<const int *>(a.params + crow)[s];
+  return has_row ? word : 0;
 }
 
 // The drive and carried state of a row whose constants in.p are already loaded.
@@ -516,21 +519,61 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   typename ReplayBits<S, V>::vec bits = ReplayBits<S, V>::zero();
+  // Vector memory counters retire in order, and a load that waits on an earlier load's value costs a round trip of
+  // its own: the row pointers and constants load first, together (each needs only the row; lanes past the step's
+  // rows read the last row's and drop them, so neither load sits behind a branch), then the first record blocks,
+  // then the drive and carried state (behind branches of their own, which may wait for them: the records are
+  // already in flight then), then the gathers.
+  constexpr bool kShared = G == 8 && SHARED;
+  const bool mat = a.xprev != nullptr && a.rowptr != nullptr;
+  const uint32_t crow = has_row ? row : (uint32_t)a.nrows - 1;
+  int32_t beg = 0, end = 0;
+  if (mat) {
+    beg = a.rowptr[crow];
+    end = a.rowptr[crow + 1];
+  }
+  // Shared path: the gathers need only the drive's and carried state's rows (words 7 and 6) of the constants, so
+  // the other six words are passed between the group's lanes in the epilogue and hold no registers meanwhile.
   RowInputs<S, U, V> in;
+  int pword = 0;
   if constexpr (REPLAY != 1) {
-    if constexpr (G == 8 && SHARED) {
-      in.p = row_param_shared8(a, row, has_row, s);
-      load_row_drive(a, col, active, in);
+    if constexpr (kShared) {
+      pword = row_param_word(a, crow, has_row, s);
+      in.p.prev = group_bcast<8, 6>(pword);
+      in.p.usrc = group_bcast<8, 7>(pword);
     } else if (has_row) {
       load_row_inputs(a, row, col, active, in);
     }
   }
-
-  if (a.xprev != nullptr && a.rowptr != nullptr) {
-    const int32_t beg = has_row ? a.rowptr[row] : 0, end = has_row ? a.rowptr[row + 1] : 0;
-    int32_t len = end - beg;
+  beg = has_row ? beg : 0;
+  end = has_row ? end : 0;
+  int32_t len = 0;
+  if (mat) {
+    len = end - beg;
 #pragma unroll
     for (int off = LPG; off < 64; off <<= 1) len = max(len, __shfl_xor(len, off));
+    len = __builtin_amdgcn_readfirstlane(len);   // the wave's longest row: equal in every lane
+  }
+  const bool buf = a.xbytes != 0;   // 24-bit multiply-add buffer offsets, as in the grouped kernel
+  const bool shared = kShared && mat && buf;   // the records come through the shared path below
+  // The shared path: one 8-byte load per lane brings the group's next 8 records (lane s: record k + s of its row,
+  // the index clamped into the row so every load is in bounds), and slot j of the block reaches the group's lanes
+  // by a broadcast of lane j: one record load per 8 gathers instead of one per gather.  Records past a row's end
+  // only feed gathers that are skipped.
+  auto block = [&](int32_t k) {
+    const int32_t e = max(min(beg + k + s, end - 1), 0);
+    return a.colval[e];
+  };
+  // The first two blocks' records load together (a row slot's rows average a few non-zeros, so most waves need one
+  // or two blocks), neither behind the other's value.  Longer rows go on block by block below.
+  int2 r0 = make_int2(0, 0), r1 = make_int2(0, 0);
+  if (shared) {
+    if (len > 0) r0 = block(0);
+    if (len > 8) r1 = block(8);
+  }
+  if constexpr (REPLAY != 1 && kShared) load_row_drive(a, col, active, in);
+
+  if (mat) {
     const S *base = a.xprev + lcol;
     // pairs past a row's end read as {column 0, weight 0} and their gathers are skipped; the next round's
     // pairs load while this round's gathers are in flight
@@ -541,26 +584,17 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
         cv[j] = e < end ? a.colval[e] : make_int2(0, 0);
       }
     };
-    const bool buf = a.xbytes != 0;   // 24-bit multiply-add buffer offsets, as in the grouped kernel
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<S *>(a.xprev), (short)0, (int)a.xbytes, kBufferWord3);
     const uint32_t row_bytes = (uint32_t)a.ldx * (uint32_t)sizeof(S), voff = (uint32_t)lcol * (uint32_t)sizeof(S);
-    bool shared = false;   // the records came through the shared path below
-    if constexpr (G == 8 && SHARED) {
-      if (buf) {
-        shared = true;
-        // One 8-byte load per lane brings the group's next 8 records (lane s: record k + s of its row, the index
-        // clamped into the row so every load is in bounds), and slot j of the block reaches the group's lanes by
-        // a broadcast of lane j: one record load per 8 gathers instead of one per gather.  Records past a row's
-        // end only feed gathers that are skipped.
-        auto block = [&](int32_t k) {
-          const int32_t e = max(min(beg + k + s, end - 1), 0);
-          return a.colval[e];
-        };
-        // one block of 8 rounds: the gathers and sums of records rec (lane s: record k + s of its group's row)
+    if constexpr (kShared) {
+      if (shared) {
+        // one block of 8 rounds: the gathers and sums of records rec (lane s: record k + s of its group's row), in
+        // steps of UNROLL rounds up to the wave's longest row (len is wave-uniform)
         auto run = [&](const int2 rec, int32_t k) {
           static_for<8 / UNROLL>([&](auto H) {
             constexpr int h0 = decltype(H)::value * UNROLL;
+            if (h0 > 0 && k + h0 >= len) return;
             typename Lanes<S, V>::vec xr[UNROLL];
             int wj[UNROLL];
             static_for<UNROLL>([&](auto J) {
@@ -583,13 +617,9 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
             }
           });
         };
-        // The first two blocks' records load together (a row slot's rows average a few non-zeros, so most waves
-        // need one or two blocks): vector memory counters retire in order, and a record load issued among a
-        // block's gathers would hold up their sums.  Longer rows go on block by block, the next one's load in
-        // flight (it loads unconditionally, clamped, so no branch makes the wave drain its loads; slots past a
-        // row's end gather at an offset past the buffer, which reads zeros without touching memory).
-        const int2 r0 = len > 0 ? block(0) : make_int2(0, 0);
-        const int2 r1 = len > 8 ? block(8) : r0;
+        // Rows past two blocks go on block by block, the next one's load in flight (it loads unconditionally,
+        // clamped, so no branch makes the wave drain its loads; slots past a row's end gather at an offset past
+        // the buffer, which reads zeros without touching memory).
         if (len > 0) run(r0, 0);
         if (len > 8) run(r1, 8);
         if (len > 16) {
@@ -640,6 +670,10 @@ __global__ __launch_bounds__(256) void k_state_step_rows(const StepArgs<S, U> a)
     return;
   }
   if constexpr (REPLAY == 2) ReplayBits<S, V>::seed(acc, bits);
+  if constexpr (kShared) {   // every lane of the group takes part in the exchange
+    keep_opaque(pword);
+    in.p = row_param_from_word(pword);
+  }
   if (!active) return;
   finish_row<S, U, V, TORCH_LERP>(a, row, col, acc, in);
 }
